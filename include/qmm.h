@@ -1,0 +1,151 @@
+/*
+ * qmm.h — C ABI of libqmm.so, the MI355X (gfx950) quantized-weight matmul library.
+ *
+ * Each entry point replaces one family of the reference's Loom kernels, keeping its argument order and buffer
+ * layouts (paths relative to the reference root, S/ = skills/loom-port-llm/starter/). The reference boundary is
+ * the `kernel.launch @name[grid](args)` contract its generators emit; here the kernel-name parameters (format, K,
+ * mode, token group) become explicit arguments and every call takes the HIP stream it is enqueued on.
+ *
+ * Conventions
+ *   - Pointers are caller-owned device pointers (no allocation happens inside any entry point except where a
+ *     workspace size function says so); weights are the raw GGUF block bytes.
+ *   - Calls are asynchronous on `stream` (a hipStream_t, NULL = the default stream) and return QMM_OK (0) or a
+ *     negative qmm_status after host-side validation; a nonzero return means nothing was launched.
+ *   - Outputs are written in full; with `accumulate` / QMM_GEMM_ACC the kernel reads and adds to them.
+ */
+#ifndef QMM_H
+#define QMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *qmm_stream_t; /* hipStream_t */
+
+enum qmm_status {
+  QMM_OK = 0,
+  QMM_ERR_FORMAT = -1,    /* unsupported weight format for this entry point */
+  QMM_ERR_SHAPE = -2,     /* a size violates a divisibility / range precondition */
+  QMM_ERR_ALIGN = -3,     /* a pointer is not aligned as the kernel requires */
+  QMM_ERR_NULL = -4,      /* a required pointer is NULL */
+  QMM_ERR_RANGE = -5,     /* an enum or small integer argument is out of range (E, top-k, gating, ...) */
+  QMM_ERR_DTYPE = -6,     /* unsupported activation / output dtype */
+  QMM_ERR_LAUNCH = -7,    /* the HIP launch itself failed */
+  QMM_ERR_WORKSPACE = -8  /* workspace too small */
+};
+
+enum qmm_format { QMM_Q4_0 = 0, QMM_Q4_K = 1, QMM_MXFP4 = 2, QMM_MXFP4S = 3 };
+enum qmm_dtype { QMM_F32 = 0, QMM_F16 = 1, QMM_BF16 = 2 };
+enum qmm_gemm_mode { QMM_GEMM_STORE = 0, QMM_GEMM_ACC = 1, QMM_GEMM_SWIGLU = 2 };
+enum qmm_act { QMM_ACT_SILU = 0, QMM_ACT_SWIGLU_OAI = 1 };
+
+/* Library version (major*10000 + minor*100 + patch) and the text of a status code. */
+int qmm_version(void);
+const char *qmm_strerror(int status);
+
+/* Bytes of one weight row of K values: K / values_per_block * bytes_per_block
+ * (replaces S/gen_llm.py:182-183 row_bytes; S/formats.py:5-19 FMT/SB). Returns 0 for an invalid (fmt, k). */
+int64_t qmm_row_bytes(int fmt, int64_t k);
+
+/* Bit-exact dequantization of `rows` rows of K values to f32 [rows, K]
+ * (the values @g_q4_0_values S/quant_values.loom:386-408, @g_q4_k_values S/gen_llm.py:288-326,
+ *  @g_mxfp4_values S/gen_llm.py:786-841 and @g_mxfp4s_values S/gen_llm.py:844-895 produce).
+ * w: weight bytes; ws: the E8M0 scale plane for QMM_MXFP4S, else NULL. */
+int qmm_dequant(int fmt, const void *w, const void *ws, int64_t rows, int64_t k, float *out, qmm_stream_t stream);
+
+/* Decode matrix-vector product, the g_mv_{fmt}_k{K}[_t{TG}][_r{R}] family
+ * (S/gen_llm.py:1159-1378 `_mv`, launch args S/gen_llm.py:1187-1197):
+ *   y[t, r] = (accumulate ? y[t, r] : 0) + sum_k x[t, k] * W[r, k]   for t < tokens, r < n, fp32 accumulation.
+ * x: [tokens, k] of x_dtype (QMM_F32 as the reference, or QMM_BF16); w: n rows of qmm_row_bytes(fmt, k) bytes;
+ * ws: scale plane for QMM_MXFP4S else NULL; y: f32 [tokens, n]. Every token is computed with the same arithmetic
+ * whatever `tokens` is, so a multi-token call equals one-token calls bit for bit. */
+int qmm_mv(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
+           const void *w, const void *ws, float *y, qmm_stream_t stream);
+
+/* Prefill GEMM, the g_gemm_{fmt}_{store|acc|swiglu}[_m128|_m256] family
+ * (S/gen_gemm.py:535-703, :706, :1224; launch args S/gen_gemm.py:549-556):
+ *   store:  Y = (X W^T) * inv[row]        acc: Y += (X W^T) * inv[row]
+ *   swiglu: Y = silu((X W^T) inv) * ((X W2^T) inv)
+ * x: [rows, k] of x_dtype (QMM_F16 = the reference's row-scaled x16, or QMM_BF16); scales: f32 [rows, 2] with
+ * inv = scales[row, 1] (the reference's (2^-e, 2^e) pairs), or NULL for inv = 1; y: [rows, n] of y_dtype
+ * (QMM_F32 as the reference, or QMM_BF16, rounded to nearest even). fp32 accumulation. */
+int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, const void *x, int x_dtype, const float *scales,
+             const void *w, const void *w2, void *y, int y_dtype, qmm_stream_t stream);
+
+/* MoE router top-k from logits, g_moe_route / g_moe_route_tr after the router matvec
+ * (S/gen_moe.py:116-252, :255-500; llama.cpp gating: 1 softmax, 2 sigmoid, 3 softmax over the picked logits):
+ *   ids i32 [tokens, KU] = the top-KU experts by score (ties to the lower id), wts f32 [tokens, KU].
+ * logits f32 [tokens, E]; bias f32 [E] or NULL (gating 2: selection bias; gating 3: added to the logits);
+ * norm != 0 divides the weights by max(sum, 6.103515625e-05); scale multiplies them. E <= 256, KU <= 8. */
+int qmm_moe_topk(const float *logits, int64_t tokens, int E, int KU, int gating, int norm, float scale,
+                 const float *bias, int32_t *ids, float *wts, qmm_stream_t stream);
+
+/* MoE bucket / permute, g_moe_bucket (S/gen_moe.py:829-955; scratch sizes S/gen_llm.py:5388-5432):
+ * assignments a = t*KU + k of live tokens (info[t, 2] != 0; info i32 [tokens, 4] or NULL = all live) grouped by
+ * expert into 64-row tiles in expert-id order, assignments in ascending a inside each expert's segment.
+ *   tile_info i32 [max_tiles, 2] = (expert, rows) or (-1, 0); rowmap i32 [max_tiles*64] = assignment or -1;
+ *   pos i32 [tokens*KU] = row or -1.   max_tiles >= tokens*KU/64 + E. */
+int qmm_moe_bucket(int64_t tokens, int KU, int E, int64_t max_tiles, const int32_t *info, const int32_t *ids,
+                   int32_t *tile_info, int32_t *rowmap, int32_t *pos, qmm_stream_t stream);
+
+/* Decode expert matvecs, g_moe_gu_{fmt}[_fused]_k{H}_r{R} / g_moe_dn_{fmt}_k{FE}_r{R}
+ * (S/gen_moe.py:535-727; launch args :564):
+ *   gu (mode 0): act[a] = act_fn(Wg[e] x[a/KU], Wu[e] x[a/KU])      e = ids[a], a < assignments
+ *   dn (mode 1): ys[a]  = Wd[e] x[a]
+ * n: output width (FE for gu, H for dn); k: input width. w: expert tensor [E, n, k] (gu: gate; fused != 0: one
+ * [E, 2n, k] tensor, each expert's n gate rows then its n up rows, w2 ignored); w2: up tensor [E, n, k] for gu.
+ * bias: for gu f32 [E, n] gate bias and bias2 up bias; for dn bias [E, n]; NULL = none. x: [rows, k] of x_dtype
+ * (gu: rows = assignments/KU tokens; dn: rows = assignments). y: f32 [assignments, n]. */
+int qmm_moe_expert_mv(int fmt, int mode, int fused, int act, int64_t k, int64_t n, int E, int KU,
+                      int64_t assignments, const int32_t *ids, const void *x, int x_dtype, const void *w,
+                      const void *w2, const float *bias, const float *bias2, float *y, qmm_stream_t stream);
+
+/* Grouped expert GEMM over bucketed rows, g_moe_ggu_{fmt}[_fused]_k{H} / g_moe_gdn_{fmt}_k{FE}
+ * (S/gen_moe.py:1126-1228; launch args S/gen_llm.py:5376-5378):
+ *   gu (mode 0): act_sorted[r] = act_fn(Wg[e] x[rowmap[r]/KU], Wu[e] x[rowmap[r]/KU])   (x rows gathered)
+ *   dn (mode 1): ys_sorted[r]  = Wd[e] x[r]                                              (x rows sorted)
+ * for every row r of every tile whose expert e = tile_info[tile, 0] >= 0; rows of rowmap -1 produce zeros.
+ * Weights as qmm_moe_expert_mv (QMM_Q4_K; QMM_MXFP4S split planes via ws/ws2 with the scaled-MFMA path).
+ * x: QMM_BF16 / QMM_F16 rows, or for the MXFP4S path E4M3 codes u8 [rows, k] + E8M0 scales u8 [rows, k/32]
+ *   (x_scales, from qmm_quant_mxfp8); x_rows is the number of rows of x.
+ * y: gu: f32 [max_tiles*64, n] (or the MXFP8 act via qmm_quant_mxfp8 afterwards); dn: f32 [max_tiles*64, n].
+ * y_scales: optional f32 [max_tiles*64] per-row output multipliers (the reference's inverse row scales) or NULL. */
+int qmm_moe_grouped(int fmt, int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
+                    const int32_t *tile_info, const int32_t *rowmap, const void *x, int x_dtype, const void *x_scales,
+                    int64_t x_rows, const void *w, const void *ws, const void *w2, const void *ws2,
+                    const float *y_scales, float *y, qmm_stream_t stream);
+
+/* Row-scaled f16 producer, g_row_scale_f16[_tiles] (S/gen_llm.py:1843-1915, S/gen_moe.py:503-527):
+ * per row e = clamp(exponent(max|x|) - 13, 0, 100), x16 = f16(x * 2^-e), scales = (2^-e, 2^e).
+ * tile_info (i32 [rows/64, 2]) or NULL: rows of tiles with expert -1 are skipped. x: f32 [rows, k]. */
+int qmm_row_scale_f16(int64_t rows, int64_t k, const float *x, float *scales, void *x16, const int32_t *tile_info,
+                      qmm_stream_t stream);
+
+/* Per-32 MXFP8 activation quantizer, the A operand of the gfx950 scaled MFMA (no reference counterpart: the
+ * reference's fp8 producers, S/gen_mxfp4s.py:852-969, quantize with a per-row scale for gfx12 WMMA):
+ *   s = clamp(floor(log2(amax_32)) - 7, -127, 127), codes = E4M3_RNE(x * 2^-s), scales = s + 127.
+ * x: [rows, k] of x_dtype (QMM_F32 / QMM_BF16). tile_info (i32 [rows/64, 2]) or NULL: rows of unused tiles
+ * are skipped. codes u8 [rows, k], scales u8 [rows, k/32]. */
+int qmm_quant_mxfp8(int64_t rows, int64_t k, const void *x, int x_dtype, const int32_t *tile_info, uint8_t *codes,
+                    uint8_t *scales, qmm_stream_t stream);
+
+/* One-time weight preparation: GGUF MXFP4 17-byte blocks -> split planes (the reference's mxfp4s layout,
+ * S/formats.py:12-15): nibbles u8 [rows, k/2] (byte j = elements 2j low nibble, 2j+1 high nibble) and
+ * E8M0 scales u8 [rows, k/32]. Bit-exact: every code and exponent is kept. */
+int qmm_repack_mxfp4(const void *w, int64_t rows, int64_t k, uint8_t *nibbles, uint8_t *scales, qmm_stream_t stream);
+
+/* MoE combine, g_moe_combine / g_moe_combine_sorted (S/gen_moe.py:730-762, :1231-1280):
+ *   y[t, c] = fma(w[t,KU-1], v[KU-1], ... fma(w[t,0], v[0], accumulate ? y[t, c] : 0))
+ * with v[k] = ys[row(t,k), c], row = pos[t*KU+k] (pos != NULL; -1 gives 0) or t*KU+k (pos == NULL).
+ * ys f32 [rows, H]; wts f32 [tokens, KU]; y f32 [tokens, H]. */
+int qmm_moe_combine(int64_t tokens, int64_t rows, int64_t H, int KU, const float *ys, const int32_t *pos,
+                    const float *wts, int accumulate, float *y, qmm_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QMM_H */

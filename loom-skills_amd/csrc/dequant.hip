@@ -1,0 +1,125 @@
+// Bit-exact dequantization kernels (parity / debug path) and the library's small host entry points.
+//
+// Each thread decodes one 32-value group into f32, with the single rounding of the reference's value helpers:
+//   Q4_0   w = f32(d) * (q - 8)                       S/quant_values.loom:386-408
+//   Q4_K   w = (f32(d) * sc) * q - f32(dmin) * m      S/gen_llm.py:269-326
+//   MXFP4  w = kvalues[code] * 2^(e - 128)            S/gen_llm.py:786-841 (code 8 -> +0)
+//   MXFP4S w = E2M1(code) * 2^(e - 127)               S/st_tensors.py:26-33 (code 8 -> -0)
+#include "common.hpp"
+
+using namespace qmm;
+
+namespace {
+
+__constant__ float kE2M1[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+__constant__ signed char kKvalues[16] = {0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12};
+
+__global__ void dequant_q4_0_kernel(const u8 *__restrict__ w, int64_t groups, float *__restrict__ out) {
+  const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gi >= groups) return;
+  const u8 *b = w + gi * 18;
+  const float d = f16_to_f32((u32)b[0] | ((u32)b[1] << 8));
+  float *o = out + gi * 32;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const u32 q = b[2 + j];
+    o[j] = d * (float)((int)(q & 15u) - 8);
+    o[j + 16] = d * (float)((int)(q >> 4) - 8);
+  }
+}
+
+__global__ void dequant_q4_k_kernel(const u8 *__restrict__ w, int64_t groups, float *__restrict__ out) {
+  const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // one 32-value sub-block
+  if (gi >= groups) return;
+  const int64_t blk = gi >> 3;
+  const int g = (int)(gi & 7);
+  const u32 *h = reinterpret_cast<const u32 *>(w + blk * 144);
+  const u32 h0 = h[0], s0 = h[1], s1 = h[2], s2 = h[3];
+  u32 sc, mn;
+  q4k_scale_min(s0, s1, s2, g, sc, mn);
+  const float scale = f16_to_f32(h0) * (float)sc;
+  const float minimum = f16_to_f32(h0 >> 16) * (float)mn;
+  const u8 *qs = w + blk * 144 + 16 + 32 * (g >> 1);
+  const int shift = 4 * (g & 1);
+  float *o = out + gi * 32;
+#pragma unroll
+  for (int l = 0; l < 32; ++l) {
+    const float q = (float)((qs[l] >> shift) & 15u);
+    o[l] = __fsub_rn(__fmul_rn(scale, q), minimum);
+  }
+}
+
+__global__ void dequant_mxfp4_kernel(const u8 *__restrict__ w, int64_t groups, float *__restrict__ out) {
+  const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gi >= groups) return;
+  const u8 *b = w + gi * 17;
+  const float half = e8m0_half(b[0]);
+  float *o = out + gi * 32;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const u32 q = b[1 + j];
+    o[j] = (float)kKvalues[q & 15u] * half;
+    o[j + 16] = (float)kKvalues[q >> 4] * half;
+  }
+}
+
+__global__ void dequant_mxfp4s_kernel(const u8 *__restrict__ nib, const u8 *__restrict__ sc, int64_t groups,
+                                      float *__restrict__ out) {
+  const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gi >= groups) return;
+  const float s = e8m0_scale(sc[gi]);
+  const u8 *b = nib + gi * 16;
+  float *o = out + gi * 32;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const u32 q = b[j];
+    const u32 lo = q & 15u, hi = q >> 4;
+    const float vlo = kE2M1[lo & 7u] * s, vhi = kE2M1[hi & 7u] * s;
+    o[2 * j] = (lo & 8u) ? -vlo : vlo;
+    o[2 * j + 1] = (hi & 8u) ? -vhi : vhi;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int qmm_version(void) { return 100; }
+
+const char *qmm_strerror(int status) {
+  switch (status) {
+    case QMM_OK: return "ok";
+    case QMM_ERR_FORMAT: return "unsupported weight format";
+    case QMM_ERR_SHAPE: return "invalid shape";
+    case QMM_ERR_ALIGN: return "misaligned pointer";
+    case QMM_ERR_NULL: return "null pointer";
+    case QMM_ERR_RANGE: return "argument out of range";
+    case QMM_ERR_DTYPE: return "unsupported dtype";
+    case QMM_ERR_LAUNCH: return "kernel launch failed";
+    case QMM_ERR_WORKSPACE: return "workspace too small";
+    default: return "unknown status";
+  }
+}
+
+int64_t qmm_row_bytes(int fmt, int64_t k) { return row_bytes(fmt, k); }
+
+int qmm_dequant(int fmt, const void *w, const void *ws, int64_t rows, int64_t k, float *out, qmm_stream_t stream) {
+  if (fmt < QMM_Q4_0 || fmt > QMM_MXFP4S) return QMM_ERR_FORMAT;
+  if (!w || !out || (fmt == QMM_MXFP4S && !ws)) return QMM_ERR_NULL;
+  if (rows <= 0 || row_bytes(fmt, k) == 0) return QMM_ERR_SHAPE;
+  if (fmt == QMM_Q4_K && !aligned(w, 4)) return QMM_ERR_ALIGN;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t groups = rows * (k / 32);
+  const int threads = 256;
+  const unsigned grid = (unsigned)((groups + threads - 1) / threads);
+  const u8 *wb = static_cast<const u8 *>(w);
+  switch (fmt) {
+    case QMM_Q4_0: dequant_q4_0_kernel<<<grid, threads, 0, s>>>(wb, groups, out); break;
+    case QMM_Q4_K: dequant_q4_k_kernel<<<grid, threads, 0, s>>>(wb, groups, out); break;
+    case QMM_MXFP4: dequant_mxfp4_kernel<<<grid, threads, 0, s>>>(wb, groups, out); break;
+    default: dequant_mxfp4s_kernel<<<grid, threads, 0, s>>>(wb, static_cast<const u8 *>(ws), groups, out); break;
+  }
+  return launch_status();
+}
+
+}  // extern "C"

@@ -1,0 +1,294 @@
+// Decode matvecs with fused weight dequantization:
+//   qmm_mv             y[t, r] (+)= sum_k x[t, k] W[r, k]        g_mv_{fmt}_k{K}[_t{TG}][_r{R}], S/gen_llm.py:1159-1378
+//   qmm_moe_expert_mv  gu: act[a] = act(Wg[e] x[a/KU], Wu[e] x[a/KU]); dn: ys[a] = Wd[e] x[a]
+//                                                                 g_moe_gu_* / g_moe_dn_*, S/gen_moe.py:535-727
+//
+// Launch shape (wave64): a workgroup is 4 waves, each wave owns RW consecutive weight rows. A wave walks the row
+// in passes of 64 items (rowdot.hpp), keeps the lane's activation fragments of its TG tokens in registers for all
+// RW rows, issues every row's 128-bit loads before the math, and folds each row's 64 lane partials with a
+// butterfly. Every token runs the same per-lane arithmetic and the same butterfly, so a call's result for one
+// token does not depend on how many tokens the call carries (multi-token == one-token, bit for bit).
+#include <type_traits>
+
+#include "rowdot.hpp"
+
+using namespace qmm;
+
+namespace {
+
+constexpr int kWavesPerBlock = 4;
+constexpr int kRW = 4;
+
+template <int RW, int TG>
+__device__ __forceinline__ void reduce_all(float (&acc)[RW][TG]) {
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int t = 0; t < TG; ++t) acc[r][t] = wave_sum(acc[r][t]);
+}
+
+template <class P, int TG, int RW>
+__global__ __launch_bounds__(256) void mv_kernel(int64_t n, int64_t tokens, int64_t k, int accumulate,
+                                                 const u8 *__restrict__ x, int64_t x_row_bytes,
+                                                 const u8 *__restrict__ w, const u8 *__restrict__ ws, int64_t rb,
+                                                 int64_t srb, float *__restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t t0 = (int64_t)blockIdx.x * TG;
+  const int64_t row0 = ((int64_t)blockIdx.y * kWavesPerBlock + wave) * RW;
+  if (row0 >= n) return;
+  const int nitems = P::items(k);
+  float acc[RW][TG];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int t = 0; t < TG; ++t) acc[r][t] = 0.f;
+
+  for (int it0 = 0; it0 < nitems; it0 += 64) {
+    const int item = it0 + lane;
+    const bool live = item < nitems;
+    typename P::X xs[TG];
+#pragma unroll
+    for (int t = 0; t < TG; ++t) P::load_x(x + (t0 + t) * x_row_bytes, item, live && (t0 + t) < tokens, xs[t]);
+    typename P::W wv[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+      P::load_w(w + (row0 + r) * rb, ws + (row0 + r) * srb, item, live && (row0 + r) < n, wv[r]);
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+      for (int t = 0; t < TG; ++t) acc[r][t] += P::dot(wv[r], xs[t], item);
+  }
+  reduce_all<RW, TG>(acc);
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int t = 0; t < TG; ++t) {
+      const int64_t row = row0 + r, tok = t0 + t;
+      if (lane == r * TG + t && row < n && tok < tokens) {
+        float *p = y + tok * n + row;
+        *p = accumulate ? *p + acc[r][t] : acc[r][t];
+      }
+    }
+}
+
+__device__ __forceinline__ float act_fn(int act, float g, float u) {
+  if (act == QMM_ACT_SWIGLU_OAI) {
+    const float xg = fminf(g, 7.0f);
+    const float yu = fminf(fmaxf(u, -7.0f), 7.0f);
+    return xg / (1.0f + expf(-1.702f * xg)) * (yu + 1.0f);
+  }
+  return g / (1.0f + expf(-g)) * u;
+}
+
+// One assignment per workgroup row (blockIdx.x), RW output rows per wave.
+template <class P, int RW, bool GU>
+__global__ __launch_bounds__(256) void expert_mv_kernel(int64_t n, int64_t assignments, int KU, int E, int64_t k,
+                                                        const int32_t *__restrict__ ids, const u8 *__restrict__ x,
+                                                        int64_t x_row_bytes, const u8 *__restrict__ w,
+                                                        const u8 *__restrict__ ws, const u8 *__restrict__ w2,
+                                                        const u8 *__restrict__ ws2, int64_t rb, int64_t srb,
+                                                        int64_t ebytes, int64_t esbytes, const float *__restrict__ bias,
+                                                        const float *__restrict__ bias2, int act,
+                                                        float *__restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t a = blockIdx.x;
+  const int64_t row0 = ((int64_t)blockIdx.y * kWavesPerBlock + wave) * RW;
+  if (row0 >= n || a >= assignments) return;
+  int e = ids[a];
+  e = e < 0 ? 0 : (e >= E ? E - 1 : e);   // ids are clamped into range as the reference does (S/gen_moe.py:592-596)
+  const u8 *xr = x + (GU ? a / KU : a) * x_row_bytes;
+  const u8 *we = w + e * ebytes, *wse = ws + e * esbytes;
+  const u8 *w2e = w2 + e * ebytes, *ws2e = ws2 + e * esbytes;
+  const int nitems = P::items(k);
+  float ag[RW], au[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) ag[r] = au[r] = 0.f;
+  for (int it0 = 0; it0 < nitems; it0 += 64) {
+    const int item = it0 + lane;
+    const bool live = item < nitems;
+    typename P::X xs;
+    P::load_x(xr, item, live, xs);
+    typename P::W wg[RW], wu[GU ? RW : 1];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const bool rl = live && (row0 + r) < n;
+      P::load_w(we + (row0 + r) * rb, wse + (row0 + r) * srb, item, rl, wg[r]);
+      if constexpr (GU) P::load_w(w2e + (row0 + r) * rb, ws2e + (row0 + r) * srb, item, rl, wu[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      ag[r] += P::dot(wg[r], xs, item);
+      if constexpr (GU) au[r] += P::dot(wu[r], xs, item);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    ag[r] = wave_sum(ag[r]);
+    if constexpr (GU) au[r] = wave_sum(au[r]);
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int64_t row = row0 + r;
+    if (lane == r && row < n) {
+      float g = ag[r];
+      if (bias) g += bias[e * n + row];
+      float v = g;
+      if constexpr (GU) {
+        float u = au[r];
+        if (bias2) u += bias2[e * n + row];
+        v = act_fn(act, g, u);
+      }
+      y[a * n + row] = v;
+    }
+  }
+}
+
+template <class P, int TG>
+int launch_mv(int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int64_t x_row_bytes,
+              const void *w, const void *ws, int64_t rb, int64_t srb, float *y, hipStream_t s) {
+  const dim3 grid((unsigned)((tokens + TG - 1) / TG), (unsigned)((n + kWavesPerBlock * kRW - 1) / (kWavesPerBlock * kRW)));
+  mv_kernel<P, TG, kRW><<<grid, 256, 0, s>>>(n, tokens, k, accumulate, static_cast<const u8 *>(x), x_row_bytes,
+                                            static_cast<const u8 *>(w), static_cast<const u8 *>(ws), rb, srb, y);
+  return launch_status();
+}
+
+// token group: 4 (bf16 activations) or 2 (f32 activations) tokens share every weight load
+template <template <bool> class P>
+int dispatch_mv(bool bf, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, const void *w,
+                const void *ws, int64_t rb, int64_t srb, float *y, hipStream_t s) {
+  if (bf) {
+    const int64_t xb = k * 2;
+    if (tokens >= 4) return launch_mv<P<true>, 4>(k, n, tokens, accumulate, x, xb, w, ws, rb, srb, y, s);
+    if (tokens >= 2) return launch_mv<P<true>, 2>(k, n, tokens, accumulate, x, xb, w, ws, rb, srb, y, s);
+    return launch_mv<P<true>, 1>(k, n, tokens, accumulate, x, xb, w, ws, rb, srb, y, s);
+  }
+  const int64_t xb = k * 4;
+  if (tokens >= 2) return launch_mv<P<false>, 2>(k, n, tokens, accumulate, x, xb, w, ws, rb, srb, y, s);
+  return launch_mv<P<false>, 1>(k, n, tokens, accumulate, x, xb, w, ws, rb, srb, y, s);
+}
+
+template <bool B> using MXG = MXFP4<B, false>;
+template <bool B> using MXS = MXFP4<B, true>;
+
+bool valid_fmt(int fmt) { return fmt >= QMM_Q4_0 && fmt <= QMM_MXFP4S; }
+
+// Alignment the row engine needs: 16-byte rows for Q4_K / MXFP4S, 4-byte rows for Q4_0 pairs.
+int check_weights(int fmt, int64_t k, const void *w, const void *ws) {
+  if (!w || (fmt == QMM_MXFP4S && !ws)) return QMM_ERR_NULL;
+  if (fmt == QMM_Q4_0 && k % 64) return QMM_ERR_SHAPE;
+  if ((fmt == QMM_Q4_K || fmt == QMM_MXFP4S) && !aligned(w, 16)) return QMM_ERR_ALIGN;
+  if (fmt == QMM_Q4_0 && !aligned(w, 4)) return QMM_ERR_ALIGN;
+  return QMM_OK;
+}
+
+}  // namespace
+
+extern "C" int qmm_mv(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
+                      const void *w, const void *ws, float *y, qmm_stream_t stream) {
+  if (!valid_fmt(fmt)) return QMM_ERR_FORMAT;
+  if (!x || !y) return QMM_ERR_NULL;
+  if (n <= 0 || tokens <= 0 || row_bytes(fmt, k) == 0) return QMM_ERR_SHAPE;
+  if (n > (1ll << 30) || tokens > (1ll << 20) || k > (1ll << 24)) return QMM_ERR_SHAPE;
+  if (x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
+  if (int st = check_weights(fmt, k, w, ws)) return st;
+  if (!aligned(x, 16) || !aligned(y, 4)) return QMM_ERR_ALIGN;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool bf = x_dtype == QMM_BF16;
+  const int64_t rb = row_bytes(fmt, k), srb = fmt == QMM_MXFP4S ? k / 32 : 0;
+  switch (fmt) {
+    case QMM_Q4_K: return dispatch_mv<Q4K>(bf, k, n, tokens, accumulate, x, w, w, rb, 0, y, s);
+    case QMM_Q4_0: return dispatch_mv<Q40>(bf, k, n, tokens, accumulate, x, w, w, rb, 0, y, s);
+    case QMM_MXFP4: return dispatch_mv<MXG>(bf, k, n, tokens, accumulate, x, w, w, rb, 0, y, s);
+    default: return dispatch_mv<MXS>(bf, k, n, tokens, accumulate, x, w, ws, rb, srb, y, s);
+  }
+}
+
+namespace {
+template <class P, bool GU>
+int launch_expert(int64_t k, int64_t n, int E, int KU, int64_t assignments, const int32_t *ids, const void *x,
+                  int64_t x_row_bytes, const void *w, const void *ws, const void *w2, const void *ws2, int64_t rb,
+                  int64_t srb, int64_t ebytes, int64_t esbytes, const float *bias, const float *bias2, int act,
+                  float *y, hipStream_t s) {
+  const dim3 grid((unsigned)assignments, (unsigned)((n + kWavesPerBlock * kRW - 1) / (kWavesPerBlock * kRW)));
+  expert_mv_kernel<P, kRW, GU><<<grid, 256, 0, s>>>(
+      n, assignments, KU, E, k, ids, static_cast<const u8 *>(x), x_row_bytes, static_cast<const u8 *>(w),
+      static_cast<const u8 *>(ws), static_cast<const u8 *>(w2), static_cast<const u8 *>(ws2), rb, srb, ebytes, esbytes,
+      bias, bias2, act, y);
+  return launch_status();
+}
+
+template <template <bool> class P>
+int dispatch_expert(bool gu, bool bf, int64_t k, int64_t n, int E, int KU, int64_t assignments, const int32_t *ids,
+                    const void *x, const void *w, const void *ws, const void *w2, const void *ws2, int64_t rb,
+                    int64_t srb, int64_t ebytes, int64_t esbytes, const float *bias, const float *bias2, int act,
+                    float *y, hipStream_t s) {
+  const int64_t xb = k * (bf ? 2 : 4);
+  if (gu) {
+    return bf ? launch_expert<P<true>, true>(k, n, E, KU, assignments, ids, x, xb, w, ws, w2, ws2, rb, srb, ebytes, esbytes, bias, bias2, act, y, s)
+              : launch_expert<P<false>, true>(k, n, E, KU, assignments, ids, x, xb, w, ws, w2, ws2, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
+  }
+  return bf ? launch_expert<P<true>, false>(k, n, E, KU, assignments, ids, x, xb, w, ws, w2, ws2, rb, srb, ebytes, esbytes, bias, bias2, act, y, s)
+            : launch_expert<P<false>, false>(k, n, E, KU, assignments, ids, x, xb, w, ws, w2, ws2, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
+}
+}  // namespace
+
+// ws / ws2: for QMM_MXFP4S the scale planes come through `w2`-style pairing: w = nibble plane, bias slots unchanged.
+// The split-plane expert tensors are passed as w (nibbles [E, rows, k/2]) with their scale planes in ws.
+extern "C" int qmm_moe_expert_mv_split(int mode, int fused, int act, int64_t k, int64_t n, int E, int KU,
+                                       int64_t assignments, const int32_t *ids, const void *x, int x_dtype,
+                                       const void *w, const void *ws, const void *w2, const void *ws2,
+                                       const float *bias, const float *bias2, float *y, qmm_stream_t stream);
+
+static int expert_mv_impl(int fmt, int mode, int fused, int act, int64_t k, int64_t n, int E, int KU,
+                          int64_t assignments, const int32_t *ids, const void *x, int x_dtype, const void *w,
+                          const void *ws, const void *w2, const void *ws2, const float *bias, const float *bias2,
+                          float *y, qmm_stream_t stream) {
+  if (!valid_fmt(fmt)) return QMM_ERR_FORMAT;
+  if (mode != 0 && mode != 1) return QMM_ERR_RANGE;
+  if (act != QMM_ACT_SILU && act != QMM_ACT_SWIGLU_OAI) return QMM_ERR_RANGE;
+  if (E <= 0 || E > 1024 || KU <= 0 || KU > 8) return QMM_ERR_RANGE;
+  if (!ids || !x || !y) return QMM_ERR_NULL;
+  if (n <= 0 || assignments <= 0 || assignments > (1 << 24) || row_bytes(fmt, k) == 0) return QMM_ERR_SHAPE;
+  if (mode == 0 && assignments % KU) return QMM_ERR_SHAPE;
+  if (x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
+  if (int st = check_weights(fmt, k, w, ws)) return st;
+  const bool gu = mode == 0;
+  if (gu && !fused && (check_weights(fmt, k, w2, ws2) != QMM_OK)) return check_weights(fmt, k, w2, ws2);
+  if (!aligned(x, 16) || !aligned(y, 4)) return QMM_ERR_ALIGN;
+  const int64_t rb = row_bytes(fmt, k), srb = fmt == QMM_MXFP4S ? k / 32 : 0;
+  const int64_t ebytes = rb * n * (fused && gu ? 2 : 1), esbytes = srb * n * (fused && gu ? 2 : 1);
+  const void *wu = w2, *wsu = ws2;
+  if (gu && fused) {   // one [E, 2n, k] tensor: expert e's n gate rows, then its n up rows (S/gen_moe.py:538)
+    wu = static_cast<const u8 *>(w) + rb * n;
+    wsu = fmt == QMM_MXFP4S ? static_cast<const u8 *>(ws) + srb * n : nullptr;
+  }
+  if (!gu) { wu = w; wsu = ws; }
+  if (!wsu) wsu = wu;
+  const void *wsg = ws ? ws : w;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool bf = x_dtype == QMM_BF16;
+  switch (fmt) {
+    case QMM_Q4_K: return dispatch_expert<Q4K>(gu, bf, k, n, E, KU, assignments, ids, x, w, wsg, wu, wsu, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
+    case QMM_Q4_0: return dispatch_expert<Q40>(gu, bf, k, n, E, KU, assignments, ids, x, w, wsg, wu, wsu, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
+    case QMM_MXFP4: return dispatch_expert<MXG>(gu, bf, k, n, E, KU, assignments, ids, x, w, wsg, wu, wsu, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
+    default: return dispatch_expert<MXS>(gu, bf, k, n, E, KU, assignments, ids, x, w, wsg, wu, wsu, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
+  }
+}
+
+extern "C" int qmm_moe_expert_mv(int fmt, int mode, int fused, int act, int64_t k, int64_t n, int E, int KU,
+                                 int64_t assignments, const int32_t *ids, const void *x, int x_dtype, const void *w,
+                                 const void *w2, const float *bias, const float *bias2, float *y, qmm_stream_t stream) {
+  if (fmt == QMM_MXFP4S) return QMM_ERR_FORMAT;   // split planes go through qmm_moe_expert_mv_split
+  return expert_mv_impl(fmt, mode, fused, act, k, n, E, KU, assignments, ids, x, x_dtype, w, nullptr, w2, nullptr,
+                        bias, bias2, y, stream);
+}
+
+extern "C" int qmm_moe_expert_mv_split(int mode, int fused, int act, int64_t k, int64_t n, int E, int KU,
+                                       int64_t assignments, const int32_t *ids, const void *x, int x_dtype,
+                                       const void *w, const void *ws, const void *w2, const void *ws2,
+                                       const float *bias, const float *bias2, float *y, qmm_stream_t stream) {
+  return expert_mv_impl(QMM_MXFP4S, mode, fused, act, k, n, E, KU, assignments, ids, x, x_dtype, w, ws, w2, ws2,
+                        bias, bias2, y, stream);
+}

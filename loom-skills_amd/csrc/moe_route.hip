@@ -1,0 +1,421 @@
+// MoE routing, permutation and combine, plus the activation producers of the grouped GEMMs.
+//
+//   qmm_moe_topk       top-k of router logits + gating weights      g_moe_route[_tr], S/gen_moe.py:116-500
+//   qmm_moe_bucket     canonical bucket of assignments into 64-row expert tiles
+//                                                                    g_moe_bucket, S/gen_moe.py:829-955
+//   qmm_moe_combine    y[t] (+)= sum_k w[t,k] ys[row(t,k)]           g_moe_combine[_sorted], S/gen_moe.py:730-762, :1231-1280
+//   qmm_row_scale_f16  per-row power-of-two scale + f16 copy         g_row_scale_f16[_tiles], S/gen_llm.py:1843-1915
+//   qmm_quant_mxfp8    per-32 E4M3 + E8M0 operand of the scaled MFMA
+//   qmm_repack_mxfp4   GGUF 17-byte MXFP4 blocks -> split planes
+#include "common.hpp"
+
+using namespace qmm;
+
+namespace {
+
+constexpr int kTile = 64;
+constexpr float kNormFloor = 6.103515625e-05f;
+
+// ------------------------------------------------------------------------------------------------- top-k
+// One wave per token; lane l holds experts l, l+64, l+128, l+192. KU rounds of a wave argmax on the selection
+// score, ties to the lower expert id (the reference's workgroup max then min-index, S/gen_moe.py:219-235).
+// The score is the logit (+ bias) for gating 1 and 3 and for gating 2 without a bias: those selections are
+// monotone in the logit, so choosing on the exact f32 logit reproduces the float64 oracle's choice.
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+
+__global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ logits, int64_t tokens, int E, int KU,
+                                                   int gating, int norm, float scale, const float *__restrict__ bias,
+                                                   int32_t *__restrict__ ids, float *__restrict__ wts) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= tokens) return;
+  const float *lg = logits + t * E;
+  float l[4], sel[4];
+  const float NEG = -3.0e38f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + 64 * i;
+    const bool in = e < E;
+    l[i] = in ? lg[e] : NEG;
+    const float b = (in && bias) ? bias[e] : 0.f;
+    if (gating == 3) l[i] = in ? l[i] + b : NEG;   // the router bias is part of the logit (gating 3)
+    float s = l[i];
+    if (gating == 2 && bias) s = in ? 1.f / (1.f + expf(-l[i])) + b : NEG;
+    sel[i] = in ? s : NEG;
+  }
+  // probabilities the weights come from
+  float prob_den = 1.f, lmax = 0.f;
+  if (gating == 1) {
+    float m = fmaxf(fmaxf(l[0], l[1]), fmaxf(l[2], l[3]));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    lmax = m;
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s += (lane + 64 * i < E) ? expf(l[i] - lmax) : 0.f;
+    prob_den = wave_sum(s);
+  }
+  float wk[8];
+  int ik[8];
+  for (int r = 0; r < KU; ++r) {
+    float bv = NEG;
+    int bi = 1 << 30;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (better(sel[i], lane + 64 * i, bv, bi)) { bv = sel[i]; bi = lane + 64 * i; }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    // every lane now agrees on the winner bi; its owner removes it and everybody learns its logit
+    float lw = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (lane + 64 * i == bi) { lw = l[i]; sel[i] = NEG; }
+    lw = __shfl(lw, bi & 63, 64);
+    ik[r] = bi;
+    wk[r] = lw;
+  }
+  if (lane == 0) {
+    float w[8];
+    float sum = 0.f;
+    if (gating == 3) {   // softmax over the picked (round 0 holds the largest)
+      for (int r = 0; r < KU; ++r) { w[r] = expf(wk[r] - wk[0]); sum += w[r]; }
+      for (int r = 0; r < KU; ++r) w[r] = w[r] / sum;
+      sum = 0.f;
+      for (int r = 0; r < KU; ++r) sum += w[r];
+    } else {
+      for (int r = 0; r < KU; ++r) {
+        w[r] = gating == 1 ? expf(wk[r] - lmax) / prob_den : 1.f / (1.f + expf(-wk[r]));
+        sum += w[r];
+      }
+    }
+    const float den = norm ? fmaxf(sum, kNormFloor) : 1.f;
+    for (int r = 0; r < KU; ++r) {
+      ids[t * KU + r] = ik[r];
+      wts[t * KU + r] = (norm ? w[r] / den : w[r]) * scale;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ bucket
+// One workgroup of 1024 threads. Counts per expert, 64-row tiles per expert in id order, then a stable scatter:
+// assignments are taken in chunks of 1024 in ascending order; inside a wave the lanes with the same expert are
+// found with 8 ballots (one per bit of the id) and ranked by popcount, waves are ranked through a per-wave count
+// table, chunks through a running offset per expert. The row of an assignment is therefore its rank among the
+// live assignments of its expert in ascending a (the canonical order), independent of thread timing.
+constexpr int kBucketThreads = 1024;
+constexpr int kBucketWaves = kBucketThreads / 64;
+constexpr int kMaxE = 256;
+
+__global__ __launch_bounds__(kBucketThreads) void bucket_kernel(int64_t tokens, int KU, int E, int64_t max_tiles,
+                                                                const int32_t *__restrict__ info,
+                                                                const int32_t *__restrict__ ids,
+                                                                int32_t *__restrict__ tile_info,
+                                                                int32_t *__restrict__ rowmap, int32_t *__restrict__ pos) {
+  __shared__ int count[kMaxE];
+  __shared__ int base[kMaxE];
+  __shared__ int running[kMaxE];
+  __shared__ int wcount[kBucketWaves][kMaxE];
+  __shared__ int total_tiles;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int64_t A = tokens * KU;
+  for (int e = tid; e < kMaxE; e += kBucketThreads) { count[e] = 0; running[e] = 0; }
+  for (int i = tid; i < kBucketWaves * kMaxE; i += kBucketThreads) (&wcount[0][0])[i] = 0;
+  __syncthreads();
+  for (int64_t a = tid; a < A; a += kBucketThreads) {
+    const int64_t t = a / KU;
+    if (info && info[t * 4 + 2] == 0) continue;
+    int e = ids[a];
+    e = e < 0 ? 0 : (e >= E ? E - 1 : e);
+    atomicAdd(&count[e], 1);
+  }
+  __syncthreads();
+  if (wave == 0) {   // exclusive scan of tiles per expert over <= 256 experts, 4 per lane
+    int tl[4], s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = lane * 4 + i;
+      tl[i] = e < E ? (count[e] + kTile - 1) / kTile : 0;
+      s += tl[i];
+    }
+    int incl = s;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int o = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += o;
+    }
+    int b = incl - s;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = lane * 4 + i;
+      if (e < kMaxE) base[e] = b;
+      b += tl[i];
+    }
+    if (lane == 63) total_tiles = incl;
+  }
+  __syncthreads();
+  // tile table
+  for (int e = tid; e < E; e += kBucketThreads) {
+    const int tiles = (count[e] + kTile - 1) / kTile;
+    for (int j = 0; j < tiles; ++j) {
+      tile_info[2 * (base[e] + j)] = e;
+      tile_info[2 * (base[e] + j) + 1] = min(kTile, count[e] - kTile * j);
+    }
+  }
+  for (int64_t i = total_tiles + tid; i < max_tiles; i += kBucketThreads) {
+    tile_info[2 * i] = -1;
+    tile_info[2 * i + 1] = 0;
+  }
+  for (int64_t r = tid; r < max_tiles * kTile; r += kBucketThreads) rowmap[r] = -1;
+  __syncthreads();
+  // stable scatter
+  for (int64_t c0 = 0; c0 < A; c0 += kBucketThreads) {
+    const int64_t a = c0 + tid;
+    bool live = a < A;
+    int e = 0;
+    if (live) {
+      const int64_t t = a / KU;
+      live = !(info && info[t * 4 + 2] == 0);
+      e = ids[a];
+      e = e < 0 ? 0 : (e >= E ? E - 1 : e);
+    }
+    uint64_t peers = __ballot(live);
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit) {
+      const uint64_t ones = __ballot(live && ((e >> bit) & 1));
+      peers &= ((e >> bit) & 1) ? ones : ~ones;
+    }
+    const uint64_t lt = (1ull << lane) - 1ull;
+    const int rank_w = __popcll(peers & lt);
+    if (live && rank_w == 0) wcount[wave][e] = __popcll(peers);
+    __syncthreads();
+    for (int ex = tid; ex < E; ex += kBucketThreads) {   // per expert: exclusive offsets over waves
+      int run = running[ex];
+      for (int w = 0; w < kBucketWaves; ++w) {
+        const int c = wcount[w][ex];
+        wcount[w][ex] = run;
+        run += c;
+      }
+      running[ex] = run;
+    }
+    __syncthreads();
+    if (a < A) {
+      if (live) {
+        const int row = base[e] * kTile + wcount[wave][e] + rank_w;
+        rowmap[row] = (int32_t)a;
+        pos[a] = row;
+      } else {
+        pos[a] = -1;
+      }
+    }
+    __syncthreads();
+    for (int i = tid; i < kBucketWaves * kMaxE; i += kBucketThreads) (&wcount[0][0])[i] = 0;
+    __syncthreads();
+  }
+}
+
+// ----------------------------------------------------------------------------------------------- combine
+// One workgroup per token, 256-channel blocks; the fma chain runs in k order (S/gen_moe.py:1231-1280).
+__global__ __launch_bounds__(256) void combine_kernel(int64_t tokens, int64_t rows, int64_t H, int KU,
+                                                      const float *__restrict__ ys, const int32_t *__restrict__ pos,
+                                                      const float *__restrict__ wts, int accumulate,
+                                                      float *__restrict__ y) {
+  const int64_t t = blockIdx.x;
+  int64_t row[8];
+  float w[8];
+  for (int k = 0; k < KU; ++k) {
+    row[k] = pos ? pos[t * KU + k] : t * KU + k;
+    w[k] = wts[t * KU + k];
+  }
+  for (int64_t c = threadIdx.x; c < H; c += blockDim.x) {
+    float acc = accumulate ? y[t * H + c] : 0.f;
+    for (int k = 0; k < KU; ++k) {
+      const float v = (row[k] >= 0 && row[k] < rows) ? ys[row[k] * H + c] : 0.f;
+      acc = __builtin_fmaf(w[k], v, acc);
+    }
+    y[t * H + c] = acc;
+  }
+}
+
+// ------------------------------------------------------------------------------------------ row scale f16
+__global__ __launch_bounds__(256) void row_scale_kernel(int64_t rows, int64_t k, const float *__restrict__ x,
+                                                        float *__restrict__ scales, _Float16 *__restrict__ x16,
+                                                        const int32_t *__restrict__ tile_info) {
+  const int64_t r = blockIdx.x;
+  if (tile_info && tile_info[2 * (r / kTile)] < 0) return;
+  __shared__ float wmax[4];
+  const float *xr = x + r * k;
+  float m = 0.f;
+  for (int64_t c = threadIdx.x; c < k; c += 256) m = fmaxf(m, fabsf(xr[c]));
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const int biased = (int)((f32_as_u32(m) >> 23) & 255u);
+  const int e = min(max(biased - 127 - 13, 0), 100);
+  const float sc = u32_as_f32((u32)(127 - e) << 23), inv = u32_as_f32((u32)(127 + e) << 23);
+  for (int64_t c = threadIdx.x; c < k; c += 256) x16[r * k + c] = (_Float16)(xr[c] * sc);
+  if (threadIdx.x == 0) {
+    scales[2 * r] = sc;
+    scales[2 * r + 1] = inv;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- MXFP8 quant
+// One thread per 32 values. s = clamp(floor(log2(amax)) - 7, -127, 127) keeps every |x| 2^-s below 256, under the
+// E4M3 maximum 448; the conversion is v_cvt_pk_fp8_f32 (round to nearest even, OCP E4M3FN on gfx950).
+__global__ __launch_bounds__(256) void quant_mxfp8_kernel(int64_t rows, int64_t k, const void *__restrict__ xv,
+                                                          int bf, const int32_t *__restrict__ tile_info,
+                                                          u8 *__restrict__ codes, u8 *__restrict__ scales) {
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t groups = rows * (k / 32);
+  if (g >= groups) return;
+  const int64_t r = g / (k / 32);
+  if (tile_info && tile_info[2 * (r / kTile)] < 0) return;
+  float v[32];
+  if (bf) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(static_cast<const u16 *>(xv) + g * 32);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 q = p[i];
+      const u32 d[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[8 * i + 2 * j] = bf16_to_f32(d[j] & 0xFFFFu);
+        v[8 * i + 2 * j + 1] = bf16_to_f32(d[j] >> 16);
+      }
+    }
+  } else {
+    const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(xv) + g * 32);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 q = p[i];
+      v[4 * i] = q.x; v[4 * i + 1] = q.y; v[4 * i + 2] = q.z; v[4 * i + 3] = q.w;
+    }
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  int s = -127;
+  if (amax > 0.f) {
+    int ex;
+    frexpf(amax, &ex);        // amax = f 2^ex, f in [0.5, 1)
+    s = min(max(ex - 1 - 7, -127), 127);
+  }
+  u32 out[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    int w = 0;
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * i], -s), ldexpf(v[4 * i + 1], -s), w, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * i + 2], -s), ldexpf(v[4 * i + 3], -s), w, true);
+    out[i] = (u32)w;
+  }
+  uint4 *o = reinterpret_cast<uint4 *>(codes + g * 32);
+  o[0] = make_uint4(out[0], out[1], out[2], out[3]);
+  o[1] = make_uint4(out[4], out[5], out[6], out[7]);
+  scales[g] = (u8)(s + 127);
+}
+
+// -------------------------------------------------------------------------------------------- MXFP4 repack
+__global__ __launch_bounds__(256) void repack_mxfp4_kernel(int64_t groups, const u8 *__restrict__ w,
+                                                           u8 *__restrict__ nib, u8 *__restrict__ sc) {
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= groups) return;
+  const u8 *b = w + g * 17;
+  u32 code[32];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const u32 q = b[1 + j];
+    code[j] = q & 15u;
+    code[j + 16] = q >> 4;
+  }
+  u32 out[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    u32 v = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v |= (code[8 * i + 2 * j] | (code[8 * i + 2 * j + 1] << 4)) << (8 * j);
+    out[i] = v;
+  }
+  reinterpret_cast<uint4 *>(nib)[g] = make_uint4(out[0], out[1], out[2], out[3]);
+  sc[g] = b[0];
+}
+
+}  // namespace
+
+extern "C" {
+
+int qmm_moe_topk(const float *logits, int64_t tokens, int E, int KU, int gating, int norm, float scale,
+                 const float *bias, int32_t *ids, float *wts, qmm_stream_t stream) {
+  if (!logits || !ids || !wts) return QMM_ERR_NULL;
+  if (E <= 0 || E > 256 || KU <= 0 || KU > 8 || KU > E) return QMM_ERR_RANGE;
+  if (gating < 1 || gating > 3 || (gating == 1 && bias)) return QMM_ERR_RANGE;
+  if (tokens <= 0 || tokens > (1ll << 24)) return QMM_ERR_SHAPE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  topk_kernel<<<(unsigned)((tokens + 3) / 4), 256, 0, s>>>(logits, tokens, E, KU, gating, norm, scale, bias, ids, wts);
+  return launch_status();
+}
+
+int qmm_moe_bucket(int64_t tokens, int KU, int E, int64_t max_tiles, const int32_t *info, const int32_t *ids,
+                   int32_t *tile_info, int32_t *rowmap, int32_t *pos, qmm_stream_t stream) {
+  if (!ids || !tile_info || !rowmap || !pos) return QMM_ERR_NULL;
+  if (E <= 0 || E > kMaxE || KU <= 0 || KU > 8) return QMM_ERR_RANGE;
+  if (tokens <= 0 || tokens > 65536) return QMM_ERR_SHAPE;
+  if (max_tiles < tokens * KU / kTile + E || max_tiles > (1 << 24)) return QMM_ERR_SHAPE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  bucket_kernel<<<1, kBucketThreads, 0, s>>>(tokens, KU, E, max_tiles, info, ids, tile_info, rowmap, pos);
+  return launch_status();
+}
+
+int qmm_moe_combine(int64_t tokens, int64_t rows, int64_t H, int KU, const float *ys, const int32_t *pos,
+                    const float *wts, int accumulate, float *y, qmm_stream_t stream) {
+  if (!ys || !wts || !y) return QMM_ERR_NULL;
+  if (KU <= 0 || KU > 8) return QMM_ERR_RANGE;
+  if (tokens <= 0 || H <= 0 || rows <= 0 || tokens > (1ll << 24)) return QMM_ERR_SHAPE;
+  if (!pos && rows < tokens * KU) return QMM_ERR_SHAPE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  combine_kernel<<<(unsigned)tokens, 256, 0, s>>>(tokens, rows, H, KU, ys, pos, wts, accumulate, y);
+  return launch_status();
+}
+
+int qmm_row_scale_f16(int64_t rows, int64_t k, const float *x, float *scales, void *x16, const int32_t *tile_info,
+                      qmm_stream_t stream) {
+  if (!x || !scales || !x16) return QMM_ERR_NULL;
+  if (rows <= 0 || k <= 0 || rows > (1ll << 24)) return QMM_ERR_SHAPE;
+  if (tile_info && rows % kTile) return QMM_ERR_SHAPE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  row_scale_kernel<<<(unsigned)rows, 256, 0, s>>>(rows, k, x, scales, static_cast<_Float16 *>(x16), tile_info);
+  return launch_status();
+}
+
+int qmm_quant_mxfp8(int64_t rows, int64_t k, const void *x, int x_dtype, const int32_t *tile_info, uint8_t *codes,
+                    uint8_t *scales, qmm_stream_t stream) {
+  if (!x || !codes || !scales) return QMM_ERR_NULL;
+  if (x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
+  if (rows <= 0 || k <= 0 || k % 32 || rows > (1ll << 24)) return QMM_ERR_SHAPE;
+  if (tile_info && rows % kTile) return QMM_ERR_SHAPE;
+  if (!aligned(x, 16) || !aligned(codes, 16)) return QMM_ERR_ALIGN;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t groups = rows * (k / 32);
+  quant_mxfp8_kernel<<<(unsigned)((groups + 255) / 256), 256, 0, s>>>(rows, k, x, x_dtype == QMM_BF16, tile_info,
+                                                                      codes, scales);
+  return launch_status();
+}
+
+int qmm_repack_mxfp4(const void *w, int64_t rows, int64_t k, uint8_t *nibbles, uint8_t *scales, qmm_stream_t stream) {
+  if (!w || !nibbles || !scales) return QMM_ERR_NULL;
+  if (rows <= 0 || k <= 0 || k % 32) return QMM_ERR_SHAPE;
+  if (!aligned(nibbles, 16)) return QMM_ERR_ALIGN;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t groups = rows * (k / 32);
+  repack_mxfp4_kernel<<<(unsigned)((groups + 255) / 256), 256, 0, s>>>(groups, static_cast<const u8 *>(w), nibbles,
+                                                                       scales);
+  return launch_status();
+}
+
+}  // extern "C"

@@ -1,0 +1,28 @@
+"""Weight formats of the quantized matmul path: bytes per block, values per block and the C-ABI format codes.
+
+Mirrors the reference's format table (skills/loom-port-llm/starter/formats.py:5-19, FMT / SB / SPLIT / SCALE_DIV)
+for the formats this library decodes. The integer codes are this library's own (include/qmm.h, enum qmm_format).
+"""
+
+FMT = {"q4_0": 18, "q4_k": 144, "mxfp4": 17, "mxfp4s": 16}     # bytes per block (mxfp4s: the nibble plane only)
+SB = {"q4_0": 32, "q4_k": 256, "mxfp4": 32, "mxfp4s": 32}      # values per block
+SPLIT = frozenset({"mxfp4s"})                                   # weight plane + scale plane (two operands)
+SCALE_DIV = {"mxfp4s": 16}                                      # nibble-plane bytes per scale-plane byte
+
+CODE = {"q4_0": 0, "q4_k": 1, "mxfp4": 2, "mxfp4s": 3}          # enum qmm_format
+DTYPE = {"f32": 0, "f16": 1, "bf16": 2}                         # enum qmm_dtype
+GEMM_MODE = {"store": 0, "acc": 1, "swiglu": 2}                 # enum qmm_gemm_mode
+ACT = {"silu": 0, "swiglu_oai": 1}                              # enum qmm_act
+GATING = {"softmax": 1, "sigmoid": 2, "softmax_weight": 3}      # llama.cpp expert_gating_func values
+
+
+def row_bytes(fmt, k):
+    """Bytes of one row of K values (S/gen_llm.py:182-183); for mxfp4s the nibble plane's bytes."""
+    if k % SB[fmt]:
+        raise ValueError(f"{fmt}: K={k} is not a multiple of {SB[fmt]}")
+    return k // SB[fmt] * FMT[fmt]
+
+
+def scale_row_bytes(fmt, k):
+    """Bytes of one row of a split format's scale plane (K/32 E8M0 bytes)."""
+    return row_bytes(fmt, k) // SCALE_DIV[fmt] if fmt in SPLIT else 0

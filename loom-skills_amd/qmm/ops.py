@@ -1,0 +1,187 @@
+"""Op surface of the quantized matmul path: torch device tensors in, HIP kernels of libqmm.so underneath.
+
+The functions mirror the reference's kernel families (paths relative to the reference root,
+S/ = skills/loom-port-llm/starter/):
+
+    mv                g_mv_{fmt}_k{K}[_t{TG}][_r{R}]          S/gen_llm.py:1159-1378, launch args :1187-1197
+    gemm              g_gemm_{fmt}_{store|acc|swiglu}[_m*]    S/gen_gemm.py:535-703, launch args :549-556
+    moe_topk          g_moe_route / g_moe_route_tr            S/gen_moe.py:116-500
+    moe_bucket        g_moe_bucket                            S/gen_moe.py:829-955
+    moe_expert_mv     g_moe_gu_* / g_moe_dn_*                 S/gen_moe.py:535-727
+    moe_grouped       g_moe_ggu_* / g_moe_gdn_*               S/gen_moe.py:1126-1228
+    moe_combine       g_moe_combine[_sorted]                  S/gen_moe.py:730-762, :1231-1280
+    row_scale_f16     g_row_scale_f16[_tiles]                 S/gen_llm.py:1843-1915, S/gen_moe.py:503-527
+    dequant           the @g_<fmt>_values helpers (bit-exact f32 values)
+
+plus the gfx950-specific producers ``quant_mxfp8`` (A operand of the scaled MFMA) and ``repack_mxfp4`` (GGUF
+MXFP4 blocks to split planes, a one-time weight preparation).
+
+Every function validates its arguments on the host (the C ABI returns a status that becomes ``QmmError``) and
+launches asynchronously on torch's current stream. Weights are uint8 tensors holding the raw GGUF block bytes.
+"""
+import torch
+
+from . import _lib
+from .formats import ACT, CODE, DTYPE, GEMM_MODE, SPLIT, row_bytes
+
+TILE = 64
+
+
+def _dt(t):
+    if t.dtype == torch.float32:
+        return DTYPE["f32"]
+    if t.dtype == torch.bfloat16:
+        return DTYPE["bf16"]
+    if t.dtype == torch.float16:
+        return DTYPE["f16"]
+    raise TypeError(f"unsupported activation dtype {t.dtype}")
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _dev(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("qmm ops take device tensors")
+        if t is not None and not t.is_contiguous():
+            raise ValueError("qmm ops take contiguous tensors")
+
+
+def dequant(fmt, w, rows, k, ws=None, out=None):
+    """f32 [rows, k] values of the weight bytes, bit-exact to the reference's value helpers."""
+    _dev(w, ws)
+    out = torch.empty((rows, k), dtype=torch.float32, device=w.device) if out is None else out
+    _lib.call("qmm_dequant", CODE[fmt], _ptr(w), _ptr(ws), rows, k, _ptr(out), _stream())
+    return out
+
+
+def mv(fmt, w, x, n, k, y=None, accumulate=False, ws=None):
+    """y[t, r] (+)= sum_k x[t, k] W[r, k]; x f32 or bf16 [tokens, k]; returns y f32 [tokens, n]."""
+    _dev(w, x, y, ws)
+    tokens = x.shape[0]
+    if x.shape[-1] != k:
+        raise ValueError(f"x has {x.shape[-1]} columns, K is {k}")
+    y = torch.empty((tokens, n), dtype=torch.float32, device=x.device) if y is None else y
+    _lib.call("qmm_mv", CODE[fmt], k, n, tokens, int(bool(accumulate)), _ptr(x), _dt(x), _ptr(w), _ptr(ws),
+              _ptr(y), _stream())
+    return y
+
+
+def gemm(fmt, mode, x, w, n, k, w2=None, scales=None, out_dtype=torch.float32, y=None):
+    """Y = (X W^T) inv (store), Y += ... (acc), silu(X W^T inv) (X W2^T inv) (swiglu); x bf16 / f16 [rows, k]."""
+    _dev(x, w, w2, scales, y)
+    rows = x.shape[0]
+    if y is None:
+        y = torch.empty((rows, n), dtype=out_dtype, device=x.device)
+    _lib.call("qmm_gemm", CODE[fmt], GEMM_MODE[mode], rows, k, n, _ptr(x), _dt(x), _ptr(scales), _ptr(w), _ptr(w2),
+              _ptr(y), _dt(y), _stream())
+    return y
+
+
+def moe_topk(logits, KU, gating, norm, scale=1.0, bias=None):
+    """(ids i32 [T, KU], wts f32 [T, KU]) from router logits f32 [T, E]."""
+    _dev(logits, bias)
+    T, E = logits.shape
+    ids = torch.empty((T, KU), dtype=torch.int32, device=logits.device)
+    wts = torch.empty((T, KU), dtype=torch.float32, device=logits.device)
+    _lib.call("qmm_moe_topk", _ptr(logits), T, E, KU, gating, int(bool(norm)), float(scale), _ptr(bias), _ptr(ids),
+              _ptr(wts), _stream())
+    return ids, wts
+
+
+def max_tiles(tokens, KU, E):
+    """Worst-case bucketed tiles: T*KU/64 + E (S/gen_llm.py:5407-5411)."""
+    return tokens * KU // TILE + E
+
+
+def moe_bucket(ids, E, n_tiles=None, info=None):
+    """(tile_info i32 [max_tiles, 2], rowmap i32 [max_tiles*64], pos i32 [T*KU]) of the assignments."""
+    _dev(ids, info)
+    T, KU = ids.shape
+    n_tiles = max_tiles(T, KU, E) if n_tiles is None else n_tiles
+    dev = ids.device
+    tile_info = torch.empty((n_tiles, 2), dtype=torch.int32, device=dev)
+    rowmap = torch.empty(n_tiles * TILE, dtype=torch.int32, device=dev)
+    pos = torch.empty(T * KU, dtype=torch.int32, device=dev)
+    _lib.call("qmm_moe_bucket", T, KU, E, n_tiles, _ptr(info), _ptr(ids), _ptr(tile_info), _ptr(rowmap), _ptr(pos),
+              _stream())
+    return tile_info, rowmap, pos
+
+
+def moe_expert_mv(fmt, mode, ids, x, w, n, k, E, KU, w2=None, ws=None, ws2=None, fused=False, act="silu",
+                  bias=None, bias2=None, y=None):
+    """Decode expert matvecs: mode 'gu' act[a] = act(Wg[e] x[a/KU], Wu[e] x[a/KU]) or 'dn' ys[a] = Wd[e] x[a]."""
+    _dev(ids, x, w, w2, ws, ws2, bias, bias2, y)
+    A = ids.numel()
+    y = torch.empty((A, n), dtype=torch.float32, device=x.device) if y is None else y
+    m = {"gu": 0, "dn": 1}[mode]
+    if fmt in SPLIT:
+        _lib.call("qmm_moe_expert_mv_split", m, int(fused), ACT[act], k, n, E, KU, A, _ptr(ids), _ptr(x), _dt(x),
+                  _ptr(w), _ptr(ws), _ptr(w2), _ptr(ws2), _ptr(bias), _ptr(bias2), _ptr(y), _stream())
+    else:
+        _lib.call("qmm_moe_expert_mv", CODE[fmt], m, int(fused), ACT[act], k, n, E, KU, A, _ptr(ids), _ptr(x), _dt(x),
+                  _ptr(w), _ptr(w2), _ptr(bias), _ptr(bias2), _ptr(y), _stream())
+    return y
+
+
+def moe_grouped(fmt, mode, tile_info, rowmap, x, w, n, k, E, KU, w2=None, ws=None, ws2=None, x_scales=None,
+                fused=False, act="silu", y_scales=None, y=None, x_dtype=None):
+    """Grouped expert GEMM over bucketed 64-row tiles (see include/qmm.h, qmm_moe_grouped)."""
+    _dev(tile_info, rowmap, x, w, w2, ws, ws2, x_scales, y_scales, y)
+    n_tiles = tile_info.shape[0]
+    y = torch.empty((n_tiles * TILE, n), dtype=torch.float32, device=x.device) if y is None else y
+    xd = _dt(x) if x_dtype is None else x_dtype
+    _lib.call("qmm_moe_grouped", CODE[fmt], {"gu": 0, "dn": 1}[mode], int(fused), ACT[act], n_tiles, k, n, E, KU,
+              _ptr(tile_info), _ptr(rowmap), _ptr(x), xd, _ptr(x_scales), x.shape[0], _ptr(w), _ptr(ws), _ptr(w2),
+              _ptr(ws2), _ptr(y_scales), _ptr(y), _stream())
+    return y
+
+
+def moe_combine(ys, wts, pos=None, y=None, accumulate=False):
+    """y[t] (+)= sum_k w[t, k] ys[row(t, k)], row = pos[t*KU + k] (sorted rows) or t*KU + k."""
+    _dev(ys, wts, pos, y)
+    T, KU = wts.shape
+    H = ys.shape[1]
+    y = torch.empty((T, H), dtype=torch.float32, device=ys.device) if y is None else y
+    _lib.call("qmm_moe_combine", T, ys.shape[0], H, KU, _ptr(ys), _ptr(pos), _ptr(wts), int(bool(accumulate)),
+              _ptr(y), _stream())
+    return y
+
+
+def row_scale_f16(x, tile_info=None):
+    """(x16 f16 [rows, k], scales f32 [rows, 2]) with the per-row power-of-two scale."""
+    _dev(x, tile_info)
+    rows, k = x.shape
+    x16 = torch.empty((rows, k), dtype=torch.float16, device=x.device)
+    scales = torch.empty((rows, 2), dtype=torch.float32, device=x.device)
+    _lib.call("qmm_row_scale_f16", rows, k, _ptr(x), _ptr(scales), _ptr(x16), _ptr(tile_info), _stream())
+    return x16, scales
+
+
+def quant_mxfp8(x, tile_info=None, codes=None, scales=None):
+    """(E4M3 codes u8 [rows, k], E8M0 scales u8 [rows, k/32]) of x f32 / bf16 [rows, k]."""
+    _dev(x, tile_info, codes, scales)
+    rows, k = x.shape
+    codes = torch.empty((rows, k), dtype=torch.uint8, device=x.device) if codes is None else codes
+    scales = torch.empty((rows, k // 32), dtype=torch.uint8, device=x.device) if scales is None else scales
+    _lib.call("qmm_quant_mxfp8", rows, k, _ptr(x), _dt(x), _ptr(tile_info), _ptr(codes), _ptr(scales), _stream())
+    return codes, scales
+
+
+def repack_mxfp4(w, rows, k):
+    """GGUF MXFP4 bytes -> (nibbles u8 [rows, k/2] pairs order, scales u8 [rows, k/32])."""
+    _dev(w)
+    nib = torch.empty((rows, k // 2), dtype=torch.uint8, device=w.device)
+    sc = torch.empty((rows, k // 32), dtype=torch.uint8, device=w.device)
+    _lib.call("qmm_repack_mxfp4", _ptr(w), rows, k, _ptr(nib), _ptr(sc), _stream())
+    return nib, sc
+
+
+def weight_bytes(fmt, rows, k):
+    return rows * row_bytes(fmt, k)

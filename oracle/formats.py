@@ -1,0 +1,149 @@
+"""Bit-exact CPU decoders of the weight formats on the quantized matmul path (oracle; test infrastructure only).
+
+All byte orders are little endian. Every decoder returns float32 values produced with at most one rounding, exactly
+as the reference's decoders do, so any correct implementation reproduces them bit for bit:
+
+* Q4_0  (18 B / 32 values)   S/quant_values.loom:386-408, S/moe_q4_0.py:1-38,
+                             .github/devlab/kbench/moe_q4_0/gen_bench.py:19-25
+* Q4_K  (144 B / 256 values) S/gen_llm.py:234-326 (@g_k_scale_minimum, @g_k_metadata, @g_q4_k_values)
+* MXFP4 GGUF (17 B / 32)     S/gen_llm.py:786-841 (@g_mxfp4_values)
+* MXFP4 split planes         S/gen_llm.py:844-895 (@g_mxfp4s_values), S/st_tensors.py:17-33 (dequant_mxfp4)
+"""
+import numpy as np
+
+# bytes per block and values per block (S/formats.py:5-19)
+BLOCK_BYTES = {"q4_0": 18, "q4_k": 144, "mxfp4": 17, "mxfp4s": 16}
+BLOCK_VALUES = {"q4_0": 32, "q4_k": 256, "mxfp4": 32, "mxfp4s": 32}
+
+# E2M1 magnitudes; bit 3 of a code is the sign (S/st_tensors.py:17-22)
+E2M1 = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], np.float64)
+# ggml's kvalues_mxfp4: twice the E2M1 values, code 8 is +0 (S/gen_llm.py:821-829)
+KVALUES_MXFP4 = np.array([0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12], np.int8)
+
+
+def row_bytes(fmt, k):
+    """Bytes of one weight row of K values (S/gen_llm.py:182-183)."""
+    assert k % BLOCK_VALUES[fmt] == 0, (fmt, k)
+    return k // BLOCK_VALUES[fmt] * BLOCK_BYTES[fmt]
+
+
+def _blocks(raw, fmt):
+    b = np.ascontiguousarray(np.asarray(raw).view(np.uint8).reshape(-1))
+    assert b.size % BLOCK_BYTES[fmt] == 0, (fmt, b.size)
+    return b.reshape(-1, BLOCK_BYTES[fmt])
+
+
+def _f16(two_bytes):
+    return np.ascontiguousarray(two_bytes).view("<f2").reshape(-1).astype(np.float32)
+
+
+def dequant_q4_0(raw, rows, k):
+    """Q4_0: d = f16 bytes 0..1, qs = bytes 2..17; value j = f32(d) * (q_j - 8), q_j the low nibble of qs[j] for
+    j < 16 and the high nibble of qs[j-16] otherwise (S/quant_values.loom:386-408). The product is exact in f32."""
+    b = _blocks(raw, "q4_0")
+    d = _f16(b[:, 0:2])
+    qs = b[:, 2:18]
+    q = np.concatenate([qs & 15, qs >> 4], axis=1).astype(np.int32) - 8
+    return (d[:, None] * q.astype(np.float32)).astype(np.float32).reshape(rows, k)
+
+
+def q4_k_scale_min(S):
+    """The 6-bit (scale, minimum) of the 8 sub-blocks from the 12 packed scale bytes S [..., 12] (ggml
+    get_scale_min_k4, restated from S/gen_llm.py:234-267): g < 4: sc = S[g] & 63, m = S[g+4] & 63; g >= 4:
+    sc = (S[g+4] & 15) | (S[g-4] >> 6) << 4, m = (S[g+4] >> 4) | (S[g] >> 6) << 4."""
+    S = np.asarray(S).astype(np.int32)
+    sc = np.empty(S.shape[:-1] + (8,), np.int32)
+    m = np.empty_like(sc)
+    sc[..., :4] = S[..., 0:4] & 63
+    m[..., :4] = S[..., 4:8] & 63
+    sc[..., 4:] = (S[..., 8:12] & 15) | ((S[..., 0:4] >> 6) << 4)
+    m[..., 4:] = (S[..., 8:12] >> 4) | ((S[..., 4:8] >> 6) << 4)
+    return sc, m
+
+
+def q4_k_pack_scale_min(sc, m):
+    """Inverse of q4_k_scale_min: 8 six-bit scales and minima -> the 12 packed bytes (used to build synthetic and
+    known-answer blocks; the round trip over all 64 x 64 values is a test)."""
+    sc = np.asarray(sc).astype(np.int32)
+    m = np.asarray(m).astype(np.int32)
+    S = np.empty(sc.shape[:-1] + (12,), np.int32)
+    S[..., 0:4] = (sc[..., 0:4] & 63) | ((sc[..., 4:8] >> 4) << 6)
+    S[..., 4:8] = (m[..., 0:4] & 63) | ((m[..., 4:8] >> 4) << 6)
+    S[..., 8:12] = (sc[..., 4:8] & 15) | ((m[..., 4:8] & 15) << 4)
+    return S.astype(np.uint8)
+
+
+def q4_k_fields(raw):
+    """(d f32 [nb], dmin f32 [nb], sc i32 [nb,8], m i32 [nb,8], q u8 [nb,8,32]) of Q4_K super-blocks: sub-block
+    g = 2p + h holds the nibble h (0 low, 1 high) of qs[32p .. 32p+31] (S/gen_llm.py:288-326)."""
+    b = _blocks(raw, "q4_k")
+    d, dmin = _f16(b[:, 0:2]), _f16(b[:, 2:4])
+    sc, m = q4_k_scale_min(b[:, 4:16])
+    qs = b[:, 16:144].reshape(-1, 4, 32)
+    q = np.stack([qs & 15, qs >> 4], axis=2).reshape(-1, 8, 32)
+    return d, dmin, sc, m, q
+
+
+def dequant_q4_k(raw, rows, k):
+    """Q4_K: value = (f32(d) * sc_g) * q - f32(dmin) * m_g. Both products are exact in f32 (at most 21 significant
+    bits), so the single rounding is the subtraction (S/gen_llm.py:269-326)."""
+    d, dmin, sc, m, q = q4_k_fields(raw)
+    scale = (d[:, None] * sc.astype(np.float32)).astype(np.float32)
+    minimum = (dmin[:, None] * m.astype(np.float32)).astype(np.float32)
+    v = scale[:, :, None] * q.astype(np.float32) - minimum[:, :, None]
+    return v.astype(np.float32).reshape(rows, k)
+
+
+def e8m0_half_scale(e):
+    """ggml GGML_E8M0_TO_FP32_HALF: 2^(e - 128) as f32 bits, (0x00200000 << e) for e < 2 (S/gen_llm.py:797-806)."""
+    e = np.asarray(e).astype(np.uint32)
+    bits = np.where(e < 2, np.uint32(0x00200000) << e, (e - np.uint32(1)) << np.uint32(23)).astype(np.uint32)
+    return bits.view(np.float32)
+
+
+def dequant_mxfp4(raw, rows, k):
+    """MXFP4 GGUF block (17 B): e = byte 0, codes = bytes 1..16 in split16 order (value j < 16: low nibble of
+    qs[j], j >= 16: high nibble of qs[j-16]); value = kvalues_mxfp4[code] * 2^(e-128) (S/gen_llm.py:786-841).
+    Code 8 decodes to +0."""
+    b = _blocks(raw, "mxfp4")
+    half = e8m0_half_scale(b[:, 0])
+    qs = b[:, 1:17]
+    codes = np.concatenate([qs & 15, qs >> 4], axis=1)
+    v = KVALUES_MXFP4[codes].astype(np.float32) * half[:, None]
+    return v.astype(np.float32).reshape(rows, k)
+
+
+def dequant_mxfp4s(nibbles, scales, rows, k):
+    """MXFP4 split planes: nibbles [rows, K/2] in pairs order (byte j = element 2j low nibble, 2j+1 high nibble),
+    scales [rows, K/32] E8M0; value = E2M1(code) * 2^(e - 127) (S/st_tensors.py:26-33). Code 8 decodes to -0, as the
+    reference's numpy decoder does."""
+    nib = np.asarray(nibbles).view(np.uint8).reshape(rows, k // 2)
+    sc = np.asarray(scales).view(np.uint8).reshape(rows, k // 32)
+    lut = np.concatenate([E2M1, -E2M1])
+    v = np.stack([lut[nib & 15], lut[nib >> 4]], axis=-1).reshape(rows, k)
+    s = np.exp2(sc.astype(np.float64) - 127.0)
+    return (v.reshape(rows, -1, 32) * s[:, :, None]).reshape(rows, k).astype(np.float32)
+
+
+def mxfp4_to_split(raw, rows, k):
+    """GGUF MXFP4 blocks -> (nibbles [rows, K/2] pairs order, scales [rows, K/32]): the same codes and exponents in
+    the split-plane layout (S/formats.py:12-15). Values are preserved except that code 8 reads as -0 in the split
+    convention and +0 in the GGUF one."""
+    b = _blocks(raw, "mxfp4").reshape(rows, k // 32, 17)
+    e = b[:, :, 0].copy()
+    qs = b[:, :, 1:17]
+    codes = np.concatenate([qs & 15, qs >> 4], axis=2)          # [rows, nb, 32] in element order
+    pairs = (codes[:, :, 0::2] | (codes[:, :, 1::2] << 4)).astype(np.uint8)
+    return pairs.reshape(rows, k // 2), e
+
+
+def dequantize(fmt, raw, rows, k, scales=None):
+    if fmt == "q4_0":
+        return dequant_q4_0(raw, rows, k)
+    if fmt == "q4_k":
+        return dequant_q4_k(raw, rows, k)
+    if fmt == "mxfp4":
+        return dequant_mxfp4(raw, rows, k)
+    if fmt == "mxfp4s":
+        return dequant_mxfp4s(raw, scales, rows, k)
+    raise ValueError(fmt)

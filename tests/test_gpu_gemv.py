@@ -1,0 +1,158 @@
+"""GPU parity of the dequant kernels (bit-exact) and of the decode GEMV (rel-L2 <= 1e-3 against the float64 oracle,
+plus the reference's own GEMV tolerance atol = rtol = 2e-3, make_kernel_tests.py:241).
+
+Inputs follow the workload generators (loom-skills_amd/qmm/synth.py) with their seeds; shapes include the
+benchmark shapes (Q4_0 4096x4096, Q4_K 12288x4096 at M = 1, 4, 8) and edge shapes: row counts that do not fill a
+wave's rows, K of 3 and 32 super-blocks, one token group partly empty.
+"""
+import numpy as np
+import pytest
+
+from helpers import (assert_bits_equal, assert_close_rel_l2, bf16_values, dev_bf16, dev_f32, dev_u8, host)
+from oracle import formats as of
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _qmm():
+    import qmm.ops as ops
+    return ops
+
+
+def _weights(fmt, rng, n, k):
+    from qmm import synth
+    return synth.weights(fmt, rng, n, k)
+
+
+@pytest.mark.parametrize("fmt,n,k", [("q4_0", 64, 4096), ("q4_k", 48, 4096), ("q4_k", 7, 768), ("mxfp4", 33, 2880)])
+def test_dequant_bit_exact(dev, fmt, n, k):
+    rng = np.random.default_rng(7)
+    w = _weights(fmt, rng, n, k)
+    got = host(_qmm().dequant(fmt, dev_u8(w, dev), n, k))
+    assert_bits_equal(got, of.dequantize(fmt, w, n, k), fmt)
+
+
+def test_dequant_mxfp4s_bit_exact(dev):
+    rng = np.random.default_rng(8)
+    n, k = 19, 2880
+    w = _weights("mxfp4", rng, n, k)
+    nib, sc = of.mxfp4_to_split(w, n, k)
+    got = host(_qmm().dequant("mxfp4s", dev_u8(nib, dev), n, k, ws=dev_u8(sc, dev)))
+    assert_bits_equal(got, of.dequant_mxfp4s(nib, sc, n, k), "mxfp4s")
+
+
+def test_dequant_q4_0_every_finite_f16_scale(dev):
+    """The reference's bit-proof input (kbench moe_q4_0/gen_bench.py:51-63): every finite f16 scale with all 16
+    codes; expected f32 values are exact products."""
+    bits = np.arange(65536, dtype=np.uint16)
+    bits = bits[(bits & 0x7C00) != 0x7C00]
+    raw = np.empty((bits.size, 18), np.uint8)
+    raw[:, :2] = bits.astype("<u2").view(np.uint8).reshape(-1, 2)
+    codes = np.arange(16, dtype=np.uint8)
+    raw[:, 2:] = codes | ((15 - codes) << 4)
+    got = host(_qmm().dequant("q4_0", dev_u8(raw, dev), bits.size, 32))
+    assert_bits_equal(got, of.dequant_q4_0(raw, bits.size, 32), "q4_0 all scales")
+
+
+def _mv_case(dev, fmt, n, k, m, x_dtype, seed=11):
+    import torch
+    rng = np.random.default_rng(seed)
+    w = _weights(fmt, rng, n, k)
+    x32 = rng.standard_normal((m, k)).astype(np.float32)
+    if x_dtype == "bf16":
+        from qmm.synth import to_bf16_bits
+        xb = to_bf16_bits(x32)
+        xv = bf16_values(xb)
+        xt = dev_bf16(xb, dev)
+    else:
+        xv = x32
+        xt = dev_f32(x32, dev)
+    W = of.dequantize(fmt, w, n, k)
+    expected = ref.gemv(xv, W)
+    y = host(_qmm().mv(fmt, dev_u8(w, dev), xt, n, k))
+    torch.cuda.synchronize()
+    return y, expected, w, xv, xt
+
+
+@pytest.mark.parametrize("fmt,n,k,m,xd", [
+    ("q4_k", 12288, 4096, 1, "bf16"),     # the Q4_K GEMV workload
+    ("q4_k", 12288, 4096, 4, "bf16"),
+    ("q4_k", 12288, 4096, 8, "bf16"),
+    ("q4_0", 4096, 4096, 1, "f32"),       # the Q4_0 GEMV workload
+    ("q4_k", 37, 768, 3, "f32"),          # 3 super-blocks, rows that do not fill a wave, partial token group
+    ("q4_k", 50, 8192, 5, "bf16"),        # 32 super-blocks: two passes per row
+    ("q4_0", 21, 4096, 2, "bf16"),
+    ("mxfp4", 45, 2880, 1, "bf16"),       # GGUF 17-byte blocks, 90 per row
+    ("mxfp4", 16, 2880, 3, "f32"),
+])
+def test_mv_matches_oracle(dev, fmt, n, k, m, xd):
+    y, e, *_ = _mv_case(dev, fmt, n, k, m, xd)
+    assert_close_rel_l2(y, e, 1e-3, f"{fmt} mv n={n} k={k} m={m} x={xd}")
+    np.testing.assert_allclose(y, e, atol=2e-3, rtol=2e-3)
+
+
+def test_mv_mxfp4s_split_planes(dev):
+    import torch
+    rng = np.random.default_rng(5)
+    n, k, m = 40, 2880, 2
+    w = _weights("mxfp4", rng, n, k)
+    nib, sc = of.mxfp4_to_split(w, n, k)
+    from qmm.synth import to_bf16_bits
+    xb = to_bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    y = host(_qmm().mv("mxfp4s", dev_u8(nib, dev), dev_bf16(xb, dev), n, k, ws=dev_u8(sc, dev)))
+    e = ref.gemv(bf16_values(xb), of.dequant_mxfp4s(nib, sc, n, k))
+    assert_close_rel_l2(y, e, 1e-3, "mxfp4s mv")
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("fmt,xd", [("q4_k", "bf16"), ("q4_k", "f32"), ("q4_0", "bf16"), ("mxfp4", "bf16")])
+def test_mv_multi_token_equals_single_token(dev, fmt, xd):
+    """A token's result does not depend on the token count of the call (make_kernel_tests.py:264-268)."""
+    import torch
+    n, k, m = 96, 2048 if fmt != "mxfp4" else 2880, 8
+    y, _, w, _, xt = _mv_case(dev, fmt, n, k, m, xd, seed=3)
+    wt = dev_u8(w, dev)
+    ops = _qmm()
+    for t in range(m):
+        y1 = host(ops.mv(fmt, wt, xt[t:t + 1].contiguous(), n, k))
+        assert_bits_equal(y1[0], y[t], f"{fmt} token {t}")
+    torch.cuda.synchronize()
+
+
+def test_mv_accumulate(dev):
+    import torch
+    rng = np.random.default_rng(9)
+    n, k = 64, 4096
+    w = _weights("q4_k", rng, n, k)
+    x = rng.standard_normal((2, k)).astype(np.float32)
+    y0 = rng.standard_normal((2, n)).astype(np.float32)
+    yt = dev_f32(y0, dev)
+    _qmm().mv("q4_k", dev_u8(w, dev), dev_f32(x, dev), n, k, y=yt, accumulate=True)
+    e = y0 + ref.gemv(x, of.dequant_q4_k(w, n, k))
+    assert_close_rel_l2(host(yt), e, 1e-6 + 1e-3, "accumulate")
+    torch.cuda.synchronize()
+
+
+def test_mv_negative_control_nibble_swap(dev):
+    """The GEMV must not match an oracle fed nibble-swapped weight bytes (a plausible layout mistake)."""
+    y, e, w, xv, _ = _mv_case(dev, "q4_k", 256, 4096, 1, "bf16", seed=21)
+    raw = w.reshape(-1, 144).copy()
+    raw[:, 16:] = (raw[:, 16:] << 4) | (raw[:, 16:] >> 4)
+    wrong = ref.gemv(xv, of.dequant_q4_k(raw.reshape(-1), 256, 4096))
+    assert ref.rel_l2(y, wrong) > 1e-1
+    assert ref.rel_l2(y, e) <= 1e-3
+
+
+def test_mv_rejects_bad_arguments(dev):
+    import torch
+    from qmm._lib import QmmError
+    ops = _qmm()
+    w = torch.zeros(144 * 4, dtype=torch.uint8, device=dev)
+    x = torch.zeros((1, 256), dtype=torch.float32, device=dev)
+    with pytest.raises(QmmError):
+        ops.mv("q4_k", w, torch.zeros((1, 100), dtype=torch.float32, device=dev), 4, 100)   # K % 256
+    with pytest.raises(QmmError):
+        ops.mv("q4_k", w, x.to(torch.float16), 4, 256)                                      # dtype
+    with pytest.raises(QmmError):
+        ops.mv("q4_0", w, torch.zeros((1, 32), dtype=torch.float32, device=dev), 4, 32)     # K % 64 for Q4_0
