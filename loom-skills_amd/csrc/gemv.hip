@@ -185,6 +185,9 @@ int check_weights(int fmt, int64_t k, const void *w, const void *ws) {
 
 }  // namespace
 
+int qmm_mv_q4k_fast(int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, const void *w, float *y,
+                    hipStream_t s);
+
 extern "C" int qmm_mv(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
                       const void *w, const void *ws, float *y, qmm_stream_t stream) {
   if (!valid_fmt(fmt)) return QMM_ERR_FORMAT;
@@ -198,7 +201,12 @@ extern "C" int qmm_mv(int fmt, int64_t k, int64_t n, int64_t tokens, int accumul
   const bool bf = x_dtype == QMM_BF16;
   const int64_t rb = row_bytes(fmt, k), srb = fmt == QMM_MXFP4S ? k / 32 : 0;
   switch (fmt) {
-    case QMM_Q4_K: return dispatch_mv<Q4K>(bf, k, n, tokens, accumulate, x, w, w, rb, 0, y, s);
+    case QMM_Q4_K:
+      if (bf) {
+        const int st = qmm_mv_q4k_fast(k, n, tokens, accumulate, x, w, y, s);
+        if (st != 1) return st;
+      }
+      return dispatch_mv<Q4K>(bf, k, n, tokens, accumulate, x, w, w, rb, 0, y, s);
     case QMM_Q4_0: return dispatch_mv<Q40>(bf, k, n, tokens, accumulate, x, w, w, rb, 0, y, s);
     case QMM_MXFP4: return dispatch_mv<MXG>(bf, k, n, tokens, accumulate, x, w, w, rb, 0, y, s);
     default: return dispatch_mv<MXS>(bf, k, n, tokens, accumulate, x, w, ws, rb, srb, y, s);
