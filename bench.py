@@ -1,0 +1,200 @@
+#!/usr/bin/env python3
+"""Throughput of the quantized-weight matmul path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--workload NAME] [--m M] [--no-cpu]
+
+A step is one launch of the hot path over one batch of synthetic input:
+
+    q4_k_gemv   (default) Q4_K decode GEMV, W [12288, 4096] (Qwen3-8B FFN gate/up), x bf16 [M, 4096], y f32
+    q4_0_gemv   Q4_0 decode GEMV, W [4096, 4096], x f32 [1, 4096], y f32
+
+Consecutive steps read different copies of the weight (more than 300 MB in rotation), so the 256 MB MALL cannot
+serve them and the figure is an HBM figure. The K timed steps are captured in one HIP graph and replayed on the
+launching stream between two HIP events; value = algorithmic bytes x K / elapsed. The JSON line also carries the
+roofline of the kernel (achieved = algorithmic bytes per launch / average launch time from the same events) and
+a CPU baseline: the numpy oracle timed on this host's cores on a bounded sample of the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "loom-skills_amd"))
+
+import numpy as np  # noqa: E402
+
+METRIC = "Q4_K GEMV GB/s (% HBM peak); MXFP4 MoE prefill TFLOP/s (% MFMA peak)"
+HBM_PEAK_GBS = 8000.0
+ROTATE_BYTES = 300 * 2 ** 20
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=2000)
+    p.add_argument("--warmup", type=int, default=200)
+    p.add_argument("--workload", default="q4_k_gemv", choices=sorted(WORKLOADS))
+    p.add_argument("--m", type=int, default=None, help="tokens per GEMV (q4_k_gemv: 1, 4 or 8)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
+    p.add_argument("--no-graph", action="store_true", help="launch steps one by one instead of a HIP graph")
+    return p.parse_args()
+
+
+def traffic_from_profile(name):
+    """HBM bytes per launch recorded by the rocprofv3 --pmc runs summarised in profiles/<name>.txt
+    (a line 'traffic_bytes_per_launch: <int>'), or None."""
+    path = os.path.join(ROOT, "profiles", name + ".txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    return None
+
+
+# ------------------------------------------------------------------------------------------------ workloads
+class GemvWorkload:
+    """Decode GEMV y = x W^T over rotated weight copies; one step = one qmm_mv launch."""
+
+    def __init__(self, name, index, fmt, n, k, m, x_dtype, traffic_name):
+        self.name, self.index, self.fmt, self.n, self.k, self.m = name, index, fmt, n, k, m
+        self.x_dtype, self.traffic_name = x_dtype, traffic_name
+
+    def setup(self, dev):
+        import torch
+        from qmm import ops, synth
+        d = synth.workload(self.index, m=self.m)
+        self.raw = d["w"]
+        if self.x_dtype == "bf16":
+            self.x_host = synth.bf16_bits_to_f32(d["x_bf16"])
+            x = torch.from_numpy(d["x_bf16"].view(np.int16)).to(dev).view(torch.bfloat16)
+        else:
+            self.x_host = d["x"]
+            x = torch.from_numpy(d["x"]).to(dev)
+        w0 = torch.from_numpy(self.raw).to(dev)
+        self.wbytes = w0.numel()
+        copies = max(2, -(-ROTATE_BYTES // self.wbytes))
+        self.ws = [w0] + [w0.clone() for _ in range(copies - 1)]
+        self.x = x
+        self.y = torch.empty((self.m, self.n), dtype=torch.float32, device=dev)
+        self.ops = ops
+        self.copies = copies
+
+    def step(self, i):
+        self.ops.mv(self.fmt, self.ws[i % self.copies], self.x, self.n, self.k, y=self.y)
+
+    def alg_bytes(self):
+        xb = 2 if self.x_dtype == "bf16" else 4
+        return self.wbytes + self.m * self.k * xb + self.m * self.n * 4
+
+    def alg_flops(self):
+        return 2 * self.m * self.n * self.k
+
+    def cpu_baseline(self, budget):
+        from oracle import cpu_baseline
+        sec, runs, threads = cpu_baseline.time_gemv(self.fmt, self.raw, self.n, self.k, self.x_host, budget_s=budget)
+        return {"value": round(self.alg_bytes() / sec / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+                "sample": f"{runs} full {self.fmt} GEMVs (N={self.n}, K={self.k}, M={self.m}): numpy oracle dequant "
+                          f"in 256-row chunks + f32 matmul on {threads} threads, median {sec * 1e3:.1f} ms per GEMV"}
+
+    def config(self):
+        return {"workload": self.name, "format": self.fmt, "N": self.n, "K": self.k, "M": self.m,
+                "x_dtype": self.x_dtype, "y_dtype": "f32", "weight_copies_rotated": self.copies,
+                "rotated_bytes": self.copies * self.wbytes}
+
+
+def _q4k_gemv(m):
+    return GemvWorkload("q4_k_gemv", 1, "q4_k", 12288, 4096, m or 1, "bf16", f"q4k_gemv_m{m or 1}_traffic")
+
+
+def _q40_gemv(m):
+    return GemvWorkload("q4_0_gemv", 0, "q4_0", 4096, 4096, m or 1, "f32", f"q40_gemv_m{m or 1}_traffic")
+
+
+WORKLOADS = {"q4_k_gemv": _q4k_gemv, "q4_0_gemv": _q40_gemv}
+
+
+# ---------------------------------------------------------------------------------------------------- main
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: this path has no multi-GPU code (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE {world})", file=sys.stderr)
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (torch.cuda.is_available() is False)", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    wl = WORKLOADS[args.workload](args.m)
+    wl.setup(dev)
+    stream = torch.cuda.current_stream()
+
+    def run(count, start):
+        for i in range(count):
+            wl.step(start + i)
+
+    torch.cuda.synchronize()
+    if args.no_graph:
+        run(args.warmup, 0)
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        wall0 = time.perf_counter()
+        t0.record(stream)
+        run(args.steps, args.warmup)
+        t1.record(stream)
+    else:
+        # capture: warm-up graph and timed graph (steps continue the weight rotation)
+        gw, gt = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gw):
+            run(max(args.warmup, 1), 0)
+        with torch.cuda.graph(gt):
+            run(args.steps, args.warmup)
+        torch.cuda.synchronize()
+        if args.warmup:
+            gw.replay()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        wall0 = time.perf_counter()
+        t0.record(stream)
+        gt.replay()
+        t1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms = t0.elapsed_time(t1)
+    per_launch_s = ms / 1e3 / args.steps
+    gbs = wl.alg_bytes() / per_launch_s / 1e9
+    traffic = traffic_from_profile(wl.traffic_name)
+    out = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k x bf16 -> f32" if wl.fmt == "q4_k" else "q4_0 x f32 -> f32",
+        "data": "synthetic (seeded generators of the workload's distributions)",
+        "config": wl.config(),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "alg_bytes_per_launch": wl.alg_bytes(), "avg_launch_us": round(per_launch_s * 1e6, 3)},
+        "tflops": round(wl.alg_flops() / per_launch_s / 1e12, 3),
+        "wall_s_timed_region": round(wall, 4),
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = wl.cpu_baseline(args.cpu_budget)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
