@@ -103,6 +103,14 @@ int qmm_moe_expert_mv(int fmt, int mode, int fused, int act, int64_t k, int64_t 
                       int64_t assignments, const int32_t *ids, const void *x, int x_dtype, const void *w,
                       const void *w2, const float *bias, const float *bias2, float *y, qmm_stream_t stream);
 
+/* qmm_moe_expert_mv for MXFP4 split planes (the reference's mxfp4s expert tensors, S/gen_llm.py:844-895):
+ * w / w2 are nibble planes [E, rows, k/2] and ws / ws2 their E8M0 scale planes [E, rows, k/32]; with fused != 0
+ * w and ws hold each expert's n gate rows then its n up rows and w2 / ws2 are ignored. */
+int qmm_moe_expert_mv_split(int mode, int fused, int act, int64_t k, int64_t n, int E, int KU, int64_t assignments,
+                            const int32_t *ids, const void *x, int x_dtype, const void *w, const void *ws,
+                            const void *w2, const void *ws2, const float *bias, const float *bias2, float *y,
+                            qmm_stream_t stream);
+
 /* Grouped expert GEMM over bucketed rows, g_moe_ggu_{fmt}[_fused]_k{H} / g_moe_gdn_{fmt}_k{FE}
  * (S/gen_moe.py:1126-1228; launch args S/gen_llm.py:5376-5378):
  *   gu (mode 0): act_sorted[r] = act_fn(Wg[e] x[rowmap[r]/KU], Wu[e] x[rowmap[r]/KU])   (x rows gathered)

@@ -1,0 +1,117 @@
+"""The C-ABI boundary without a GPU: libqmm.so loads, exports every entry point include/qmm.h declares with the
+argument count the ctypes binding uses, and its host-side validation turns bad arguments into the documented
+negative status before anything reaches the device (the reference's generators assert the same preconditions at
+generation time, S/gen_llm.py:4573, S/gen_moe.py:121). No compute call is made here.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "qmm.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"^(?:int|int64_t|const char \*)\s*(qmm_\w+)\(([^)]*)\);", text, flags=re.M):
+        args = [a.strip() for a in m.group(2).split(",") if a.strip() and a.strip() != "void"]
+        out[m.group(1)] = len(args)
+    return out
+
+
+def header_enum(name):
+    text = open(HEADER).read()
+    body = re.search(r"enum %s \{(.*?)\};" % name, text, flags=re.S).group(1)
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    return {k.strip(): int(v) for k, v in re.findall(r"(\w+)\s*=\s*(-?\d+)", body)}
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from qmm import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        from qmm import build
+        build.build()
+    return _lib.load()
+
+
+def test_binding_covers_the_header():
+    from qmm import _lib
+    decl = header_functions()
+    assert len(decl) >= 15
+    assert set(decl) == set(_lib.SIGNATURES), set(decl) ^ set(_lib.SIGNATURES)
+    for name, n in decl.items():
+        assert len(_lib.SIGNATURES[name]) == n, name
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in header_functions():
+        assert hasattr(lib, name), name
+
+
+def test_enums_match_python_tables():
+    from qmm import formats
+    fmt = header_enum("qmm_format")
+    assert {k.lower()[4:]: v for k, v in fmt.items()} == formats.CODE
+    dt = header_enum("qmm_dtype")
+    assert {k.lower()[4:]: v for k, v in dt.items()} == formats.DTYPE
+    st = header_enum("qmm_status")
+    assert st["QMM_OK"] == 0 and all(v < 0 for k, v in st.items() if k != "QMM_OK")
+
+
+def test_host_only_entry_points(lib):
+    assert lib.qmm_version() >= 100
+    assert lib.qmm_row_bytes(1, 4096) == 2304
+    assert lib.qmm_row_bytes(0, 2816) == 1584
+    assert lib.qmm_row_bytes(2, 2880) == 1530
+    assert lib.qmm_row_bytes(3, 2880) == 1440
+    assert lib.qmm_row_bytes(1, 100) == 0
+    assert lib.qmm_row_bytes(7, 256) == 0
+    assert lib.qmm_strerror(-2) == b"invalid shape"
+
+
+def test_argument_validation_without_a_device(lib):
+    """Each call fails host-side validation, so nothing is launched (the pointers are never dereferenced)."""
+    st = header_enum("qmm_status")
+    fake = ctypes.c_void_p(0x1000)      # a non-null, 4 KiB-aligned address that is never touched
+    odd = ctypes.c_void_p(0x1002)
+    n = None
+    # qmm_mv: unsupported format, null x, K not a multiple of the block, bad dtype, misaligned Q4_K weights
+    assert lib.qmm_mv(9, 256, 4, 1, 0, fake, 0, fake, n, fake, n) == st["QMM_ERR_FORMAT"]
+    assert lib.qmm_mv(1, 256, 4, 1, 0, n, 0, fake, n, fake, n) == st["QMM_ERR_NULL"]
+    assert lib.qmm_mv(1, 100, 4, 1, 0, fake, 0, fake, n, fake, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_mv(1, 256, 4, 1, 0, fake, 1, fake, n, fake, n) == st["QMM_ERR_DTYPE"]
+    assert lib.qmm_mv(1, 256, 4, 1, 0, fake, 0, odd, n, fake, n) == st["QMM_ERR_ALIGN"]
+    assert lib.qmm_mv(0, 32, 4, 1, 0, fake, 0, fake, n, fake, n) == st["QMM_ERR_SHAPE"]     # Q4_0 needs K % 64
+    assert lib.qmm_mv(3, 64, 4, 1, 0, fake, 0, fake, n, fake, n) == st["QMM_ERR_NULL"]      # split planes need ws
+    # dequant
+    assert lib.qmm_dequant(1, n, n, 4, 256, fake, n) == st["QMM_ERR_NULL"]
+    assert lib.qmm_dequant(1, fake, n, 0, 256, fake, n) == st["QMM_ERR_SHAPE"]
+    # top-k: E, KU and gating ranges
+    assert lib.qmm_moe_topk(fake, 4, 300, 4, 1, 1, ctypes.c_float(1), n, fake, fake, n) == st["QMM_ERR_RANGE"]
+    assert lib.qmm_moe_topk(fake, 4, 32, 9, 1, 1, ctypes.c_float(1), n, fake, fake, n) == st["QMM_ERR_RANGE"]
+    assert lib.qmm_moe_topk(fake, 4, 32, 4, 4, 1, ctypes.c_float(1), n, fake, fake, n) == st["QMM_ERR_RANGE"]
+    assert lib.qmm_moe_topk(fake, 4, 32, 4, 1, 1, ctypes.c_float(1), fake, fake, fake, n) == st["QMM_ERR_RANGE"]
+    # bucket: too few tiles for the worst case T*KU/64 + E
+    assert lib.qmm_moe_bucket(256, 4, 32, 47, n, fake, fake, fake, fake, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_moe_bucket(256, 4, 300, 500, n, fake, fake, fake, fake, n) == st["QMM_ERR_RANGE"]
+    # combine and expert matvecs
+    assert lib.qmm_moe_combine(4, 2, 8, 4, fake, n, fake, 0, fake, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_moe_expert_mv(1, 2, 0, 0, 256, 8, 4, 2, 4, fake, fake, 0, fake, fake, n, n, fake, n) \
+        == st["QMM_ERR_RANGE"]
+    assert lib.qmm_moe_expert_mv(3, 0, 0, 0, 64, 8, 4, 2, 4, fake, fake, 0, fake, fake, n, n, fake, n) \
+        == st["QMM_ERR_FORMAT"]
+    # quantizer / repack shapes
+    assert lib.qmm_quant_mxfp8(4, 48, fake, 0, n, fake, fake, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_repack_mxfp4(fake, 4, 48, fake, fake, n) == st["QMM_ERR_SHAPE"]
+
+
+def test_python_surface_refuses_host_tensors():
+    torch = pytest.importorskip("torch")
+    from qmm import ops
+    with pytest.raises(ValueError):
+        ops.mv("q4_k", torch.zeros(144, dtype=torch.uint8), torch.zeros((1, 256)), 1, 256)
