@@ -7,6 +7,8 @@ A step is one launch of the hot path over one batch of synthetic input:
 
     q4_k_gemv   (default) Q4_K decode GEMV, W [12288, 4096] (Qwen3-8B FFN gate/up), x bf16 [M, 4096], y f32
     q4_0_gemv   Q4_0 decode GEMV, W [4096, 4096], x f32 [1, 4096], y f32
+    q4_k_gemm   Q4_K prefill GEMM, x bf16 [512, 4096] (row scale to f16, then the MFMA GEMM), W [4096, 4096],
+                y bf16 [512, 4096] (Qwen3-8B attn o_proj)
 
 Consecutive steps read different copies of the weight (more than 300 MB in rotation), so the 256 MB MALL cannot
 serve them and the figure is an HBM figure. The K timed steps are captured in one HIP graph and replayed on the
@@ -27,6 +29,7 @@ import numpy as np  # noqa: E402
 
 METRIC = "Q4_K GEMV GB/s (% HBM peak); MXFP4 MoE prefill TFLOP/s (% MFMA peak)"
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "fp16": 2500.0, "fp8": 5000.0, "fp4": 10100.0}
 ROTATE_BYTES = 300 * 2 ** 20
 
 
@@ -59,6 +62,7 @@ def traffic_from_profile(name):
 # ------------------------------------------------------------------------------------------------ workloads
 class GemvWorkload:
     """Decode GEMV y = x W^T over rotated weight copies; one step = one qmm_mv launch."""
+    metric, unit, bound = METRIC, "GB/s", "hbm"
 
     def __init__(self, name, index, fmt, n, k, m, x_dtype, traffic_name):
         self.name, self.index, self.fmt, self.n, self.k, self.m = name, index, fmt, n, k, m
@@ -87,6 +91,14 @@ class GemvWorkload:
     def step(self, i):
         self.ops.mv(self.fmt, self.ws[i % self.copies], self.x, self.n, self.k, y=self.y)
 
+    kernel_step = None
+
+    def value(self, sec):
+        return self.alg_bytes() / sec / 1e9
+
+    def dtype(self):
+        return "q4_k x bf16 -> f32" if self.fmt == "q4_k" else "q4_0 x f32 -> f32"
+
     def alg_bytes(self):
         xb = 2 if self.x_dtype == "bf16" else 4
         return self.wbytes + self.m * self.k * xb + self.m * self.n * 4
@@ -107,6 +119,66 @@ class GemvWorkload:
                 "rotated_bytes": self.copies * self.wbytes}
 
 
+class GemmWorkload:
+    """Q4_K prefill GEMM: one step = row-scale bf16 x to f16 + the GEMM (bf16 out) on the next weight copy."""
+    metric, unit, bound = "Q4_K prefill GEMM TFLOP/s (Qwen3-8B o_proj, 512 x 4096 x 4096)", "TFLOP/s", "mfma"
+    peak_key = "fp16"
+    name, traffic_name = "q4_k_gemm", "q4k_gemm_traffic"
+
+    def __init__(self, m):
+        self.m, self.n, self.k = m or 512, 4096, 4096
+
+    def setup(self, dev):
+        import torch
+        from qmm import ops, synth
+        d = synth.workload(2, m=self.m)
+        self.raw, self.x_bits = d["w"], d["x_bf16"]
+        w0 = torch.from_numpy(self.raw).to(dev)
+        self.wbytes = w0.numel()
+        self.copies = max(2, -(-ROTATE_BYTES // self.wbytes))
+        self.ws = [w0] + [w0.clone() for _ in range(self.copies - 1)]
+        self.x = torch.from_numpy(self.x_bits.view(np.int16)).to(dev).view(torch.bfloat16)
+        self.x16 = torch.empty((self.m, self.k), dtype=torch.float16, device=dev)
+        self.scales = torch.empty((self.m, 2), dtype=torch.float32, device=dev)
+        self.y = torch.empty((self.m, self.n), dtype=torch.bfloat16, device=dev)
+        self.ops = ops
+        self.ops.row_scale_f16(self.x, x16=self.x16, scales=self.scales)
+
+    def step(self, i):
+        self.ops.row_scale_f16(self.x, x16=self.x16, scales=self.scales)
+        self.kernel_step(i)
+
+    def kernel_step(self, i):
+        self.ops.gemm("q4_k", "store", self.x16, self.ws[i % self.copies], self.n, self.k, scales=self.scales,
+                      y=self.y)
+
+    def alg_bytes(self):
+        return self.wbytes + self.m * self.k * 2 + self.m * self.n * 2
+
+    def alg_flops(self):
+        return 2 * self.m * self.n * self.k
+
+    def value(self, sec):
+        return self.alg_flops() / sec / 1e12
+
+    def dtype(self):
+        return "q4_k x f16 (row-scaled bf16) -> bf16, fp32 accumulate"
+
+    def cpu_baseline(self, budget):
+        from oracle import cpu_baseline
+        from qmm import synth
+        x = synth.bf16_bits_to_f32(self.x_bits)
+        sec, runs, threads = cpu_baseline.time_gemv("q4_k", self.raw, self.n, self.k, x, budget_s=budget)
+        return {"value": round(self.alg_flops() / sec / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+                "kind": "port",
+                "sample": f"{runs} full GEMMs (M={self.m}, N={self.n}, K={self.k}): numpy oracle dequant in 256-row "
+                          f"chunks + f32 matmul on {threads} threads, median {sec * 1e3:.1f} ms per GEMM"}
+
+    def config(self):
+        return {"workload": self.name, "format": "q4_k", "M": self.m, "N": self.n, "K": self.k, "x_dtype": "bf16",
+                "y_dtype": "bf16", "weight_copies_rotated": self.copies, "rotated_bytes": self.copies * self.wbytes}
+
+
 def _q4k_gemv(m):
     return GemvWorkload("q4_k_gemv", 1, "q4_k", 12288, 4096, m or 1, "bf16", f"q4k_gemv_m{m or 1}_traffic")
 
@@ -115,7 +187,7 @@ def _q40_gemv(m):
     return GemvWorkload("q4_0_gemv", 0, "q4_0", 4096, 4096, m or 1, "f32", f"q40_gemv_m{m or 1}_traffic")
 
 
-WORKLOADS = {"q4_k_gemv": _q4k_gemv, "q4_0_gemv": _q40_gemv}
+WORKLOADS = {"q4_k_gemv": _q4k_gemv, "q4_0_gemv": _q40_gemv, "q4_k_gemm": GemmWorkload}
 
 
 # ---------------------------------------------------------------------------------------------------- main
@@ -135,45 +207,52 @@ def main():
     wl.setup(dev)
     stream = torch.cuda.current_stream()
 
-    def run(count, start):
-        for i in range(count):
-            wl.step(start + i)
-
-    torch.cuda.synchronize()
-    if args.no_graph:
-        run(args.warmup, 0)
+    def timed(step_fn):
+        """ms for args.steps steps (HIP-graph replay between two events on the launching stream) and the wall time"""
+        def run(count, start):
+            for i in range(count):
+                step_fn(start + i)
         torch.cuda.synchronize()
-        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        wall0 = time.perf_counter()
-        t0.record(stream)
-        run(args.steps, args.warmup)
-        t1.record(stream)
-    else:
-        # capture: warm-up graph and timed graph (steps continue the weight rotation)
-        gw, gt = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gw):
-            run(max(args.warmup, 1), 0)
-        with torch.cuda.graph(gt):
+        if args.no_graph:
+            run(args.warmup, 0)
+            torch.cuda.synchronize()
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            wall0 = time.perf_counter()
+            t0.record(stream)
             run(args.steps, args.warmup)
+            t1.record(stream)
+        else:
+            gw, gt = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gw):
+                run(max(args.warmup, 1), 0)
+            with torch.cuda.graph(gt):
+                run(args.steps, args.warmup)
+            torch.cuda.synchronize()
+            if args.warmup:
+                gw.replay()
+            torch.cuda.synchronize()
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            wall0 = time.perf_counter()
+            t0.record(stream)
+            gt.replay()
+            t1.record(stream)
         torch.cuda.synchronize()
-        if args.warmup:
-            gw.replay()
-        torch.cuda.synchronize()
-        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        wall0 = time.perf_counter()
-        t0.record(stream)
-        gt.replay()
-        t1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    ms = t0.elapsed_time(t1)
-    per_launch_s = ms / 1e3 / args.steps
-    gbs = wl.alg_bytes() / per_launch_s / 1e9
+        return t0.elapsed_time(t1), time.perf_counter() - wall0
+
+    ms, wall = timed(wl.step)
+    per_step_s = ms / 1e3 / args.steps
+    value = wl.value(per_step_s)
+    kms = timed(wl.kernel_step)[0] if wl.kernel_step is not None else ms
+    per_launch_s = kms / 1e3 / args.steps
+    if wl.bound == "hbm":
+        achieved, peak, unit = wl.alg_bytes() / per_launch_s / 1e9, HBM_PEAK_GBS, "GB/s"
+    else:
+        achieved, peak, unit = wl.alg_flops() / per_launch_s / 1e12, MFMA_PEAK_TFLOPS[wl.peak_key], "TFLOP/s"
     traffic = traffic_from_profile(wl.traffic_name)
     out = {
-        "metric": METRIC,
-        "value": round(gbs, 2),
-        "unit": "GB/s",
+        "metric": wl.metric,
+        "value": round(value, 3),
+        "unit": wl.unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -181,13 +260,15 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_k x bf16 -> f32" if wl.fmt == "q4_k" else "q4_0 x f32 -> f32",
+        "dtype": wl.dtype(),
         "data": "synthetic (seeded generators of the workload's distributions)",
         "config": wl.config(),
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "alg_bytes_per_launch": wl.alg_bytes(), "avg_launch_us": round(per_launch_s * 1e6, 3)},
-        "tflops": round(wl.alg_flops() / per_launch_s / 1e12, 3),
+        "roofline": {"bound": wl.bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
+                     "frac": round(achieved / peak, 4), "traffic": traffic,
+                     "alg_bytes_per_launch": wl.alg_bytes(), "alg_flops_per_launch": wl.alg_flops(),
+                     "avg_launch_us": round(per_launch_s * 1e6, 3)},
+        "gbs": round(wl.alg_bytes() / per_step_s / 1e9, 2),
+        "tflops": round(wl.alg_flops() / per_step_s / 1e12, 3),
         "wall_s_timed_region": round(wall, 4),
     }
     if not args.no_cpu:

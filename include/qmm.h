@@ -69,9 +69,10 @@ int qmm_mv(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const 
  * (S/gen_gemm.py:535-703, :706, :1224; launch args S/gen_gemm.py:549-556):
  *   store:  Y = (X W^T) * inv[row]        acc: Y += (X W^T) * inv[row]
  *   swiglu: Y = silu((X W^T) inv) * ((X W2^T) inv)
- * x: [rows, k] of x_dtype (QMM_F16 = the reference's row-scaled x16, or QMM_BF16); scales: f32 [rows, 2] with
- * inv = scales[row, 1] (the reference's (2^-e, 2^e) pairs), or NULL for inv = 1; y: [rows, n] of y_dtype
- * (QMM_F32 as the reference, or QMM_BF16, rounded to nearest even). fp32 accumulation. */
+ * x: f16 [rows, k] (x_dtype QMM_F16), the reference's row-scaled x16 from qmm_row_scale_f16; scales: f32 [rows, 2]
+ * with inv = scales[row, 1] (the reference's (2^-e, 2^e) pairs), or NULL for inv = 1; y: [rows, n] of y_dtype
+ * (QMM_F32 as the reference, or QMM_BF16, rounded to nearest even). fp32 accumulation. Q4_K weights, K % 256 == 0;
+ * the weights are dequantized to f16 as the reference stages them: fma_f16(f16(q), f16(d sc), f16(-dmin m)). */
 int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, const void *x, int x_dtype, const float *scales,
              const void *w, const void *w2, void *y, int y_dtype, qmm_stream_t stream);
 
@@ -128,9 +129,10 @@ int qmm_moe_grouped(int fmt, int mode, int fused, int act, int64_t max_tiles, in
 
 /* Row-scaled f16 producer, g_row_scale_f16[_tiles] (S/gen_llm.py:1843-1915, S/gen_moe.py:503-527):
  * per row e = clamp(exponent(max|x|) - 13, 0, 100), x16 = f16(x * 2^-e), scales = (2^-e, 2^e).
- * tile_info (i32 [rows/64, 2]) or NULL: rows of tiles with expert -1 are skipped. x: f32 [rows, k]. */
-int qmm_row_scale_f16(int64_t rows, int64_t k, const float *x, float *scales, void *x16, const int32_t *tile_info,
-                      qmm_stream_t stream);
+ * tile_info (i32 [rows/64, 2]) or NULL: rows of tiles with expert -1 are skipped. x: [rows, k] of x_dtype
+ * (QMM_F32 as the reference, or QMM_BF16). This is the A operand qmm_gemm takes. */
+int qmm_row_scale_f16(int64_t rows, int64_t k, const void *x, int x_dtype, float *scales, void *x16,
+                      const int32_t *tile_info, qmm_stream_t stream);
 
 /* Per-32 MXFP8 activation quantizer, the A operand of the gfx950 scaled MFMA (no reference counterpart: the
  * reference's fp8 producers, S/gen_mxfp4s.py:852-969, quantize with a per-row scale for gfx12 WMMA):

@@ -242,15 +242,20 @@ __global__ __launch_bounds__(256) void combine_kernel(int64_t tokens, int64_t ro
 }
 
 // ------------------------------------------------------------------------------------------ row scale f16
-__global__ __launch_bounds__(256) void row_scale_kernel(int64_t rows, int64_t k, const float *__restrict__ x,
+// One workgroup per row: e = clamp(exponent(max |x|) - 13, 0, 100), x16 = f16(x 2^-e) (round to nearest even),
+// scales = (2^-e, 2^e). x is f32 or bf16.
+__device__ __forceinline__ float load_act(const void *x, int bf, int64_t i) {
+  return bf ? bf16_to_f32(static_cast<const u16 *>(x)[i]) : static_cast<const float *>(x)[i];
+}
+
+__global__ __launch_bounds__(256) void row_scale_kernel(int64_t rows, int64_t k, const void *__restrict__ x, int bf,
                                                         float *__restrict__ scales, _Float16 *__restrict__ x16,
                                                         const int32_t *__restrict__ tile_info) {
   const int64_t r = blockIdx.x;
   if (tile_info && tile_info[2 * (r / kTile)] < 0) return;
   __shared__ float wmax[4];
-  const float *xr = x + r * k;
   float m = 0.f;
-  for (int64_t c = threadIdx.x; c < k; c += 256) m = fmaxf(m, fabsf(xr[c]));
+  for (int64_t c = threadIdx.x; c < k; c += 256) m = fmaxf(m, fabsf(load_act(x, bf, r * k + c)));
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
   if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
@@ -259,7 +264,7 @@ __global__ __launch_bounds__(256) void row_scale_kernel(int64_t rows, int64_t k,
   const int biased = (int)((f32_as_u32(m) >> 23) & 255u);
   const int e = min(max(biased - 127 - 13, 0), 100);
   const float sc = u32_as_f32((u32)(127 - e) << 23), inv = u32_as_f32((u32)(127 + e) << 23);
-  for (int64_t c = threadIdx.x; c < k; c += 256) x16[r * k + c] = (_Float16)(xr[c] * sc);
+  for (int64_t c = threadIdx.x; c < k; c += 256) x16[r * k + c] = (_Float16)(load_act(x, bf, r * k + c) * sc);
   if (threadIdx.x == 0) {
     scales[2 * r] = sc;
     scales[2 * r + 1] = inv;
@@ -383,13 +388,15 @@ int qmm_moe_combine(int64_t tokens, int64_t rows, int64_t H, int KU, const float
   return launch_status();
 }
 
-int qmm_row_scale_f16(int64_t rows, int64_t k, const float *x, float *scales, void *x16, const int32_t *tile_info,
-                      qmm_stream_t stream) {
+int qmm_row_scale_f16(int64_t rows, int64_t k, const void *x, int x_dtype, float *scales, void *x16,
+                      const int32_t *tile_info, qmm_stream_t stream) {
   if (!x || !scales || !x16) return QMM_ERR_NULL;
+  if (x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
   if (rows <= 0 || k <= 0 || rows > (1ll << 24)) return QMM_ERR_SHAPE;
   if (tile_info && rows % kTile) return QMM_ERR_SHAPE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  row_scale_kernel<<<(unsigned)rows, 256, 0, s>>>(rows, k, x, scales, static_cast<_Float16 *>(x16), tile_info);
+  row_scale_kernel<<<(unsigned)rows, 256, 0, s>>>(rows, k, x, x_dtype == QMM_BF16, scales,
+                                                  static_cast<_Float16 *>(x16), tile_info);
   return launch_status();
 }
 

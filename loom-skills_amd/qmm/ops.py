@@ -74,9 +74,14 @@ def mv(fmt, w, x, n, k, y=None, accumulate=False, ws=None):
 
 
 def gemm(fmt, mode, x, w, n, k, w2=None, scales=None, out_dtype=torch.float32, y=None):
-    """Y = (X W^T) inv (store), Y += ... (acc), silu(X W^T inv) (X W2^T inv) (swiglu); x bf16 / f16 [rows, k]."""
+    """Y = (X16 W^T) inv (store) or Y += ... (acc). x is the row-scaled f16 operand with its scales (the reference's
+    g_row_scale_f16 output), or bf16 / f32 rows, which are row-scaled here first (qmm_row_scale_f16)."""
     _dev(x, w, w2, scales, y)
     rows = x.shape[0]
+    if x.dtype != torch.float16:
+        if scales is not None:
+            raise ValueError("scales come with an f16 operand; pass bf16 / f32 rows without them")
+        x, scales = row_scale_f16(x)
     if y is None:
         y = torch.empty((rows, n), dtype=out_dtype, device=x.device)
     _lib.call("qmm_gemm", CODE[fmt], GEMM_MODE[mode], rows, k, n, _ptr(x), _dt(x), _ptr(scales), _ptr(w), _ptr(w2),
@@ -154,13 +159,13 @@ def moe_combine(ys, wts, pos=None, y=None, accumulate=False):
     return y
 
 
-def row_scale_f16(x, tile_info=None):
-    """(x16 f16 [rows, k], scales f32 [rows, 2]) with the per-row power-of-two scale."""
-    _dev(x, tile_info)
+def row_scale_f16(x, tile_info=None, x16=None, scales=None):
+    """(x16 f16 [rows, k], scales f32 [rows, 2]) with the per-row power-of-two scale; x f32 or bf16 [rows, k]."""
+    _dev(x, tile_info, x16, scales)
     rows, k = x.shape
-    x16 = torch.empty((rows, k), dtype=torch.float16, device=x.device)
-    scales = torch.empty((rows, 2), dtype=torch.float32, device=x.device)
-    _lib.call("qmm_row_scale_f16", rows, k, _ptr(x), _ptr(scales), _ptr(x16), _ptr(tile_info), _stream())
+    x16 = torch.empty((rows, k), dtype=torch.float16, device=x.device) if x16 is None else x16
+    scales = torch.empty((rows, 2), dtype=torch.float32, device=x.device) if scales is None else scales
+    _lib.call("qmm_row_scale_f16", rows, k, _ptr(x), _dt(x), _ptr(scales), _ptr(x16), _ptr(tile_info), _stream())
     return x16, scales
 
 

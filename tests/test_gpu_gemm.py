@@ -1,0 +1,113 @@
+"""GPU parity of the Q4_K prefill GEMM (g_gemm_q4_k_*, S/gen_gemm.py:535-703) and its row-scale producer
+(g_row_scale_f16, S/gen_llm.py:1843-1915).
+
+The oracle is the reference's own GEMM check (make_kernel_tests.py:1858-1900): float64 (X16 W^T) inv with W exactly
+dequantized and X16 the row-scaled f16 operand (oracle.ref.f16_rows). Bars: rel-L2 <= 1e-3 for the fp32 accumulation (f32
+store); a bf16 store must equal that result rounded to nearest even, bit for bit; the reference's own tolerance
+(atol 3e-2 std(y), rtol 1e-2, make_kernel_tests.py:1889) holds for both. Shapes: the Qwen3-8B o_proj
+workload (512 x 4096 x 4096) and edge shapes with partial row / column tiles and few super-blocks.
+"""
+import numpy as np
+import pytest
+
+from helpers import assert_close_rel_l2, dev_bf16, dev_f32, dev_u8, host
+from oracle import formats as of
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(dev, M, N, K, seed, x_kind="bf16"):
+    from qmm import synth
+    rng = np.random.default_rng(seed)
+    w = synth.q4_k_weights(rng, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    if x_kind == "bf16":
+        xb = synth.to_bf16_bits(x)
+        xv = synth.bf16_bits_to_f32(xb)
+        xt = dev_bf16(xb, dev)
+    else:                                   # f32 rows with a wide spread of magnitudes: the row scale matters
+        x *= np.exp2(rng.integers(-10, 24, (M, 1))).astype(np.float32)
+        xv = x
+        xt = dev_f32(x, dev)
+    W = of.dequant_q4_k(w, N, K)
+    want = ref.gemv(ref.f16_rows(xv), W)
+    return dev_u8(w, dev), xt, want, xv, w
+
+
+def _check(y, want, what):
+    assert_close_rel_l2(y, want, 1e-3, what)
+    np.testing.assert_allclose(y, want, atol=3e-2 * float(np.std(want)), rtol=1e-2)
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 4096, 4096), (70, 200, 768), (64, 128, 256), (130, 384, 1280)])
+def test_gemm_f32_out(dev, M, N, K):
+    import qmm.ops as ops
+    wt, xt, want, _, _ = _case(dev, M, N, K, seed=M + N + K)
+    y = host(ops.gemm("q4_k", "store", xt, wt, N, K))
+    _check(y, want, f"gemm {M}x{N}x{K}")
+
+
+def test_gemm_bf16_out_workload_shape(dev):
+    """The Q4_K prefill workload: bf16 x [512, 4096], W [4096, 4096], bf16 out. The fp32 accumulation meets the
+    rel-L2 bar (f32 store); the bf16 store is exactly that result rounded to nearest even, so its distance to the
+    oracle is the accumulation error plus bf16's own rounding (about 1.1e-3 rel-L2 on its own)."""
+    import torch
+    import qmm.ops as ops
+    M, N, K = 512, 4096, 4096
+    wt, xt, want, _, _ = _case(dev, M, N, K, seed=20261202)
+    y32 = host(ops.gemm("q4_k", "store", xt, wt, N, K))
+    y16 = host(ops.gemm("q4_k", "store", xt, wt, N, K, out_dtype=torch.bfloat16))
+    assert_close_rel_l2(y32, want, 1e-3, "fp32 accumulation")
+    assert np.array_equal(ref.bf16_round(y32).view(np.uint32), y16.view(np.uint32)), "bf16 store is not RNE(f32)"
+    np.testing.assert_allclose(y16, want, atol=3e-2 * float(np.std(want)), rtol=1e-2)
+
+
+def test_gemm_row_scaled_f32_rows_and_accumulate(dev):
+    """f32 rows spanning 2^-10 .. 2^24 go through the row-scale producer; acc mode adds to y."""
+    import qmm.ops as ops
+    M, N, K = 96, 256, 1024
+    wt, xt, want, _, _ = _case(dev, M, N, K, seed=5, x_kind="f32")
+    rng = np.random.default_rng(6)
+    y0 = (rng.standard_normal((M, N)) * np.std(want)).astype(np.float32)
+    yt = dev_f32(y0, dev)
+    ops.gemm("q4_k", "acc", xt, wt, N, K, y=yt)
+    _check(host(yt), want + y0, "acc with row scale")
+
+
+def test_gemm_deterministic_and_negative_control(dev):
+    import qmm.ops as ops
+    M, N, K = 128, 256, 2048
+    wt, xt, want, xv, w = _case(dev, M, N, K, seed=9)
+    a = host(ops.gemm("q4_k", "store", xt, wt, N, K))
+    b = host(ops.gemm("q4_k", "store", xt, wt, N, K))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    raw = w.reshape(-1, 144).copy()
+    raw[:, 16:] = (raw[:, 16:] << 4) | (raw[:, 16:] >> 4)
+    wrong = ref.gemv(xv, of.dequant_q4_k(raw.reshape(-1), N, K))
+    assert ref.rel_l2(a, wrong) > 0.1 and ref.rel_l2(a, want) <= 1e-3
+
+
+def test_row_scale_bf16_input(dev):
+    import qmm.ops as ops
+    from qmm import synth
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((64, 512)) * np.exp2(rng.integers(-4, 30, (64, 1)))).astype(np.float32)
+    xb = synth.to_bf16_bits(x)
+    x16, sc = ops.row_scale_f16(dev_bf16(xb, dev))
+    xv = synth.bf16_bits_to_f32(xb)
+    e = ref.row_scale_exponent(xv)
+    np.testing.assert_array_equal(host(sc)[:, 1], 2.0 ** e)
+    want = (xv.astype(np.float64) * 2.0 ** -e[:, None]).astype(np.float16)
+    np.testing.assert_array_equal(host(x16).view(np.uint16), want.view(np.uint16))
+
+
+def test_gemm_rejects_bad_arguments(dev):
+    import torch
+    from qmm._lib import QmmError
+    import qmm.ops as ops
+    w = torch.zeros(144 * 4, dtype=torch.uint8, device=dev)
+    with pytest.raises(QmmError):
+        ops.gemm("q4_0", "store", torch.zeros((4, 256), dtype=torch.float16, device=dev), w, 4, 256)
+    with pytest.raises(QmmError):
+        ops.gemm("q4_k", "store", torch.zeros((4, 128), dtype=torch.float16, device=dev), w, 4, 128)
