@@ -27,6 +27,11 @@ using namespace qmm;
 namespace {
 
 constexpr int BM = 64, BN = 128, KSTEP = 64;
+#ifndef QMM_GEMM_DEPTH
+#define QMM_GEMM_DEPTH 4
+#endif
+constexpr int kDepth = QMM_GEMM_DEPTH;   // steps of loads in flight per wave (even)
+static_assert(kDepth % 2 == 0, "the LDS double buffer follows the step parity");
 constexpr int APITCH = KSTEP + 8;   // f16 per LDS row: 144 bytes, rows 16-byte aligned, reads 2-way at most
 typedef __attribute__((ext_vector_type(2))) _Float16 h2;
 
@@ -63,7 +68,7 @@ __device__ __forceinline__ void sub_scale(const uint4 &hd, int g, h2 &dsc, h2 &n
 
 __device__ __forceinline__ uint4 ld16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
 
-template <bool ACC, bool BF16OUT>
+template <bool ACC, bool BF16OUT, int DEPTH>
 __global__ __launch_bounds__(256, 1) void gemm_q4k_kernel(int M, int N, int K, const _Float16 *__restrict__ x16,
                                                           const float *__restrict__ scales,
                                                           const u8 *__restrict__ w, void *__restrict__ yv,
@@ -79,13 +84,13 @@ __global__ __launch_bounds__(256, 1) void gemm_q4k_kernel(int M, int N, int K, c
   const int S = K / KSTEP, S0 = (S + 1) / 2, S1 = S - S0;
   const int my_steps = kh ? S1 : S0;
 
-  // ---- A staging map: chunk c = i * 256 + tid of 16 bytes; K-half, row, 16-byte column
-  auto a_src = [&](int i, int s, bool &ok) -> const uint4 * {
+  // ---- A staging map: chunk c = i * 256 + tid of 16 bytes; K-half, row, 16-byte column. Loads are unconditional
+  // with clamped addresses, so no branch or select splits the load stream: rows past M load row M - 1 (their
+  // outputs are never stored) and steps past S0 load step S0 - 1 (their weights are zeroed in the compute).
+  auto a_load = [&](int i, int s) -> uint4 {
     const int c = i * 256 + tid, ckh = c >> 9, row = (c >> 3) & 63, col = c & 7;
-    const int gs = ckh * S0 + s;
-    ok = (m0 + row < M) && (s < (ckh ? S1 : S0));
-    return reinterpret_cast<const uint4 *>(x16 + (int64_t)(ok ? m0 + row : 0) * K + (int64_t)(ok ? gs : 0) * KSTEP +
-                                           col * 8);
+    const int r = m0 + row < M ? m0 + row : M - 1, gs = ckh * S0 + (s < S0 ? s : S0 - 1);
+    return *reinterpret_cast<const uint4 *>(x16 + (int64_t)r * K + (int64_t)gs * KSTEP + col * 8);
   };
   auto a_dst = [&](int i, int buf) -> uint4 * {
     const int c = i * 256 + tid, ckh = c >> 9, row = (c >> 3) & 63, col = c & 7;
@@ -102,10 +107,12 @@ __global__ __launch_bounds__(256, 1) void gemm_q4k_kernel(int M, int N, int K, c
     wcol[j] = w + (int64_t)c * RB;
   }
   auto b_code = [&](int j, int s) -> uint4 {
-    const int gs = kh * S0 + s;
+    const int gs = kh * S0 + (s < S0 ? s : S0 - 1);
     return ld16(wcol[j] + (int64_t)(gs >> 2) * 144 + 16 + 32 * (gs & 3) + 16 * h);
   };
-  auto b_head = [&](int j, int s) -> uint4 { return ld16(wcol[j] + (int64_t)((kh * S0 + s) >> 2) * 144); };
+  auto b_head = [&](int j, int s) -> uint4 {
+    return ld16(wcol[j] + (int64_t)((kh * S0 + (s < S0 ? s : S0 - 1)) >> 2) * 144);
+  };
 
   f32x16 acc[2][2];
 #pragma unroll
@@ -115,60 +122,51 @@ __global__ __launch_bounds__(256, 1) void gemm_q4k_kernel(int M, int N, int K, c
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  // prologue: stage step 0, load B of step 0
-  {
-    uint4 a[4];
+  // Register rings, DEPTH steps deep: A chunks of steps s+1 .. s+DEPTH, B code/header of steps s .. s+DEPTH-1.
+  // Step t lives in slot t % DEPTH; the step loop is unrolled DEPTH times so every slot index is static.
+  uint4 aring[DEPTH][4], cring[DEPTH][2], hring[DEPTH][2];
+  auto load_a = [&](int slot, int st) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      bool ok;
-      const uint4 *p = a_src(i, 0, ok);
-      a[i] = ok ? *p : make_uint4(0, 0, 0, 0);
-    }
+    for (int i = 0; i < 4; ++i) aring[slot][i] = a_load(i, st);
+  };
+  auto load_b = [&](int slot, int st) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *a_dst(i, 0) = a[i];
-  }
-  uint4 code[2], head[2];
-  if (my_steps > 0) {
+    for (int j = 0; j < 2; ++j) { cring[slot][j] = b_code(j, st); hring[slot][j] = b_head(j, st); }
+  };
+  // prologue: A of step 0 into LDS buffer 0, A of steps 1..DEPTH and B of steps 0..DEPTH-1 in flight
+  load_a(0, 0);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) { code[j] = b_code(j, 0); head[j] = b_head(j, 0); }
-  }
+  for (int i = 0; i < 4; ++i) *a_dst(i, 0) = aring[0][i];
+#pragma unroll
+  for (int u = 1; u <= DEPTH; ++u) load_a(u % DEPTH, u);
+#pragma unroll
+  for (int u = 0; u < DEPTH; ++u) load_b(u, u);
   __syncthreads();
 
-  for (int s = 0; s < S0; ++s) {
-    const int buf = s & 1;
-    // issue the next step's loads first
-    uint4 an[4];
-    const bool more = s + 1 < S0;
-    if (more) {
+  // The step count is rounded up to a multiple of DEPTH; steps past S0 get zero weights (no contribution), so
+  // the loop body has no data-dependent branch and every wave runs the same barriers. Both K-halves have S0 steps
+  // (K is a multiple of 256, so K / 64 is even).
+  const int SP = (S0 + DEPTH - 1) / DEPTH * DEPTH;
+  for (int s0 = 0; s0 < SP; s0 += DEPTH) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        bool ok;
-        const uint4 *p = a_src(i, s + 1, ok);
-        an[i] = ok ? *p : make_uint4(0, 0, 0, 0);
-      }
-    }
-    uint4 coden[2], headn[2];
-    const bool bmore = s + 1 < my_steps;
-    if (bmore) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        coden[j] = b_code(j, s + 1);
-        headn[j] = ((kh * S0 + s + 1) & 3) == 0 ? b_head(j, s + 1) : head[j];
-      }
-    }
-    if (s < my_steps) {
-      const int page = (kh * S0 + s) & 3;
+    for (int u = 0; u < DEPTH; ++u) {
+      const int s = s0 + u;
+      const int buf = u & 1;   // DEPTH is even, so s & 1 == u & 1
+      const int page = (kh * S0 + (s < S0 ? s : S0 - 1)) & 3;
 #pragma unroll
       for (int gl = 0; gl < 2; ++gl) {
         h2 dsc[2], nmn[2];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) sub_scale(head[j], 2 * page + gl, dsc[j], nmn[j]);
+        for (int j = 0; j < 2; ++j) {
+          sub_scale(hring[u][j], 2 * page + gl, dsc[j], nmn[j]);
+          if (s >= S0) dsc[j] = nmn[j] = h2{0, 0};   // a padding step: zero weights
+        }
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
           f16x8 bf[2], af[2];
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
-            const u32 q0 = s2 ? code[j].z : code[j].x, q1 = s2 ? code[j].w : code[j].y;
+            const u32 q0 = s2 ? cring[u][j].z : cring[u][j].x, q1 = s2 ? cring[u][j].w : cring[u][j].y;
             bf[j] = gl ? deq8<true>(q0, q1, dsc[j], nmn[j]) : deq8<false>(q0, q1, dsc[j], nmn[j]);
           }
 #pragma unroll
@@ -177,19 +175,17 @@ __global__ __launch_bounds__(256, 1) void gemm_q4k_kernel(int M, int N, int K, c
 #pragma unroll
           for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < 2; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
       }
-    }
-    if (more) {
+      load_b(u, s + DEPTH);
+      const int nx = (u + 1) % DEPTH;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) *a_dst(i, buf ^ 1) = an[i];
+      for (int i = 0; i < 4; ++i) *a_dst(i, buf ^ 1) = aring[nx][i];
+      load_a(nx, s + 1 + DEPTH);
+      __syncthreads();
     }
-    if (bmore) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j) { code[j] = coden[j]; head[j] = headn[j]; }
-    }
-    __syncthreads();
   }
 
   // ---- sum the K-halves through LDS (K-half 1 hands its partial to K-half 0), then the epilogue
@@ -250,9 +246,9 @@ extern "C" int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, c
   const _Float16 *xp = static_cast<const _Float16 *>(x);
   const u8 *wp = static_cast<const u8 *>(w);
   const bool acc = mode == QMM_GEMM_ACC, bf = y_dtype == QMM_BF16;
-  if (acc && bf) gemm_q4k_kernel<true, true><<<grid, 256, 0, s>>>((int)rows, (int)n, (int)k, xp, scales, wp, y, tiles_m, total);
-  else if (acc) gemm_q4k_kernel<true, false><<<grid, 256, 0, s>>>((int)rows, (int)n, (int)k, xp, scales, wp, y, tiles_m, total);
-  else if (bf) gemm_q4k_kernel<false, true><<<grid, 256, 0, s>>>((int)rows, (int)n, (int)k, xp, scales, wp, y, tiles_m, total);
-  else gemm_q4k_kernel<false, false><<<grid, 256, 0, s>>>((int)rows, (int)n, (int)k, xp, scales, wp, y, tiles_m, total);
+  if (acc && bf) gemm_q4k_kernel<true, true, kDepth><<<grid, 256, 0, s>>>((int)rows, (int)n, (int)k, xp, scales, wp, y, tiles_m, total);
+  else if (acc) gemm_q4k_kernel<true, false, kDepth><<<grid, 256, 0, s>>>((int)rows, (int)n, (int)k, xp, scales, wp, y, tiles_m, total);
+  else if (bf) gemm_q4k_kernel<false, true, kDepth><<<grid, 256, 0, s>>>((int)rows, (int)n, (int)k, xp, scales, wp, y, tiles_m, total);
+  else gemm_q4k_kernel<false, false, kDepth><<<grid, 256, 0, s>>>((int)rows, (int)n, (int)k, xp, scales, wp, y, tiles_m, total);
   return launch_status();
 }
