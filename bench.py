@@ -9,6 +9,10 @@ A step is one launch of the hot path over one batch of synthetic input:
     q4_0_gemv   Q4_0 decode GEMV, W [4096, 4096], x f32 [1, 4096], y f32
     q4_k_gemm   Q4_K prefill GEMM, x bf16 [512, 4096] (row scale to f16, then the MFMA GEMM), W [4096, 4096],
                 y bf16 [512, 4096] (Qwen3-8B attn o_proj)
+    mxfp4_moe   MXFP4 MoE prefill chain at the gpt-oss-20b shape (32 experts, top-4, H = FE = 2880), T tokens
+                (--m, default 256): top-k, bucket, MXFP8 quantize, grouped gate_up (scaled MFMA) + swiglu_oai,
+                quantize, grouped down, combine
+    q4_k_moe    Q4_K MoE prefill chain at the Qwen3-30B-A3B shape (128 experts, top-8, H = 2048, FE = 768), T = 64
 
 Consecutive steps read different copies of the weight (more than 300 MB in rotation), so the 256 MB MALL cannot
 serve them and the figure is an HBM figure. The K timed steps are captured in one HIP graph and replayed on the
@@ -179,6 +183,138 @@ class GemmWorkload:
                 "y_dtype": "bf16", "weight_copies_rotated": self.copies, "rotated_bytes": self.copies * self.wbytes}
 
 
+class MoeWorkload:
+    """MoE prefill chain; one step = the whole chain over one batch of T tokens. The expert weights (423 MB MXFP4,
+    340 MB Q4_K) exceed the 256 MB MALL, so no rotation is needed."""
+    unit, higher = "TFLOP/s", True
+
+    def __init__(self, name, index, m):
+        self.name, self.index = name, index
+        if index == 3:
+            self.T = m or 256
+            self.metric = METRIC
+            self.traffic_name = f"mxfp4_moe_t{self.T}_traffic"
+        else:
+            self.T = m or 64
+            self.metric = "Q4_K MoE prefill TFLOP/s (Qwen3-30B-A3B, 128 experts, top-8, T = 64)"
+            self.traffic_name = f"q4k_moe_t{self.T}_traffic"
+
+    def setup(self, dev):
+        import torch
+        from qmm import ops, synth
+        d = synth.workload(self.index, T=self.T)
+        self.d = d
+        self.E, self.KU, self.H, self.FE = d["E"], d["KU"], d["H"], d["FE"]
+        u8 = lambda a: torch.from_numpy(a).to(dev)
+        self.x = torch.from_numpy(d["x_bf16"].view(np.int16)).to(dev).view(torch.bfloat16)
+        self.logits = torch.from_numpy(d["logits"]).to(dev)
+        if d["fmt"] == "mxfp4":
+            E, H, FE = self.E, self.H, self.FE
+            gn, gs = ops.repack_mxfp4(u8(d["gate_up"]), E * 2 * FE, H)
+            dn, ds = ops.repack_mxfp4(u8(d["down"]), E * H, FE)
+            self.fmt = "mxfp4s"
+            self.kw = dict(w_gate=gn, ws_gate=gs, w_down=dn, ws_down=ds, fused=True, act=d["act"])
+            self.wbytes_expert = (2 * FE * H + H * FE) // 2 + (2 * FE * H + H * FE) // 32
+            self.peak_key = "fp8"
+        else:
+            self.fmt = "q4_k"
+            self.kw = dict(w_gate=u8(d["gate"]), w_up=u8(d["up"]), w_down=u8(d["down"]), fused=False, act=d["act"])
+            self.wbytes_expert = (2 * self.FE * self.H + self.H * self.FE) // 256 * 144
+            self.peak_key = "fp16"
+        self.ops = ops
+        y, mid = self.run_chain()
+        torch.cuda.synchronize()
+        self.experts_hit = int(torch.unique(mid["ids"]).numel())
+        # inputs of the dominant kernel (the grouped gate/up GEMM) for its own timing
+        self.mid = mid
+        if self.fmt == "mxfp4s":
+            self.gu_x, self.gu_xs = ops.quant_mxfp8(self.x)
+        else:
+            self.gu_x, self.gu_xs = ops.row_scale_f16(self.x)
+        self.gu_y = torch.empty_like(mid["act"])
+
+    def run_chain(self):
+        return self.ops.moe_prefill(self.fmt, self.x, self.logits, self.E, self.KU, self.H, self.FE, self.d["gating"],
+                                    self.d["norm"], **self.kw)
+
+    def step(self, i):
+        self.run_chain()
+
+    def kernel_step(self, i):
+        kw = self.kw
+        self.ops.moe_grouped(self.fmt, "gu", self.mid["tile_info"], self.mid["rowmap"], self.gu_x, kw["w_gate"],
+                             self.FE, self.H, self.E, self.KU, w2=kw.get("w_up"), ws=kw.get("ws_gate"),
+                             x_scales=self.gu_xs, fused=kw["fused"], act=kw["act"], y=self.gu_y)
+
+    @property
+    def bound(self):
+        # arithmetic intensity of the whole chain against the MFMA / HBM balance point
+        ai = self.alg_flops() / self.alg_bytes()
+        return "mfma" if ai > MFMA_PEAK_TFLOPS[self.peak_key] * 1e12 / (HBM_PEAK_GBS * 1e9) else "hbm"
+
+    def alg_bytes(self):
+        T, H, E = self.T, self.H, self.E
+        return self.experts_hit * self.wbytes_expert + T * H * 2 + T * H * 4 + T * E * 4
+
+    def alg_flops(self):
+        return 2 * self.T * self.KU * (self.H * 2 * self.FE + self.FE * self.H)
+
+    def gu_bytes(self):
+        T, H = self.T, self.H
+        per = self.wbytes_expert * 2 // 3 if self.fmt == "mxfp4s" else (2 * self.FE * H) // 256 * 144
+        return self.experts_hit * per + T * H + T * self.KU * self.FE * 4
+
+    def gu_flops(self):
+        return 2 * self.T * self.KU * self.H * 2 * self.FE
+
+    def value(self, sec):
+        return self.alg_flops() / sec / 1e12
+
+    def dtype(self):
+        return ("mxfp4 x mxfp8 (E4M3, E8M0 per 32) -> f32" if self.fmt == "mxfp4s"
+                else "q4_k x f16 (row-scaled) -> f32")
+
+    def cpu_baseline(self, budget):
+        from oracle import formats as of
+        from oracle import ref
+        from qmm import synth
+        import time as _t
+        d = self.d
+        gfmt = "mxfp4" if self.fmt == "mxfp4s" else "q4_k"
+        E, KU, H, FE = self.E, self.KU, self.H, self.FE
+        rb_h, rb_f = of.row_bytes(gfmt, H), of.row_bytes(gfmt, FE)
+        def gate_up(e):
+            if self.fmt == "mxfp4s":
+                g = of.dequantize(gfmt, d["gate_up"][2 * FE * e * rb_h:(2 * FE * e + FE) * rb_h], FE, H)
+                u = of.dequantize(gfmt, d["gate_up"][(2 * FE * e + FE) * rb_h:2 * FE * (e + 1) * rb_h], FE, H)
+                return g, u
+            return (of.dequantize(gfmt, d["gate"][FE * e * rb_h:FE * (e + 1) * rb_h], FE, H),
+                    of.dequantize(gfmt, d["up"][FE * e * rb_h:FE * (e + 1) * rb_h], FE, H))
+        def down(e):
+            return of.dequantize(gfmt, d["down"][H * e * rb_f:H * (e + 1) * rb_f], H, FE)
+        x = synth.bf16_bits_to_f32(d["x_bf16"])
+        ids, wts = ref.route(d["logits"], KU, d["gating"], d["norm"])
+        rnd = ref.mxfp8_values if self.fmt == "mxfp4s" else ref.f16_rows
+        # bounded sample: the first tokens whose experts fit the time budget (the whole chain on them)
+        tokens = 0
+        t0 = _t.perf_counter()
+        while tokens < self.T and _t.perf_counter() - t0 < budget:
+            n = min(self.T - tokens, max(1, self.T // 16))
+            ref.moe(x[tokens:tokens + n], ids[tokens:tokens + n], wts[tokens:tokens + n], gate_up, down,
+                    act=d["act"], x_round=rnd, act_round=rnd)
+            tokens += n
+        sec = _t.perf_counter() - t0
+        flops = 2 * tokens * KU * (H * 2 * FE + FE * H)
+        return {"value": round(flops / sec / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+                "sample": f"{tokens} of {self.T} tokens through the numpy oracle's MoE chain (per-expert exact "
+                          f"dequant + float64 matmuls, single-threaded numpy), {sec:.1f} s"}
+
+    def config(self):
+        return {"workload": self.name, "format": self.fmt, "E": self.E, "top_k": self.KU, "H": self.H,
+                "FE": self.FE, "T": self.T, "gating": self.d["gating"], "act": self.d["act"],
+                "experts_hit": self.experts_hit}
+
+
 def _q4k_gemv(m):
     return GemvWorkload("q4_k_gemv", 1, "q4_k", 12288, 4096, m or 1, "bf16", f"q4k_gemv_m{m or 1}_traffic")
 
@@ -187,7 +323,8 @@ def _q40_gemv(m):
     return GemvWorkload("q4_0_gemv", 0, "q4_0", 4096, 4096, m or 1, "f32", f"q40_gemv_m{m or 1}_traffic")
 
 
-WORKLOADS = {"q4_k_gemv": _q4k_gemv, "q4_0_gemv": _q40_gemv, "q4_k_gemm": GemmWorkload}
+WORKLOADS = {"q4_k_gemv": _q4k_gemv, "q4_0_gemv": _q40_gemv, "q4_k_gemm": GemmWorkload,
+             "mxfp4_moe": lambda m: MoeWorkload("mxfp4_moe", 3, m), "q4_k_moe": lambda m: MoeWorkload("q4_k_moe", 4, m)}
 
 
 # ---------------------------------------------------------------------------------------------------- main
@@ -244,10 +381,12 @@ def main():
     value = wl.value(per_step_s)
     kms = timed(wl.kernel_step)[0] if wl.kernel_step is not None else ms
     per_launch_s = kms / 1e3 / args.steps
+    kb = wl.gu_bytes() if hasattr(wl, "gu_bytes") else wl.alg_bytes()
+    kf = wl.gu_flops() if hasattr(wl, "gu_flops") else wl.alg_flops()
     if wl.bound == "hbm":
-        achieved, peak, unit = wl.alg_bytes() / per_launch_s / 1e9, HBM_PEAK_GBS, "GB/s"
+        achieved, peak, unit = kb / per_launch_s / 1e9, HBM_PEAK_GBS, "GB/s"
     else:
-        achieved, peak, unit = wl.alg_flops() / per_launch_s / 1e12, MFMA_PEAK_TFLOPS[wl.peak_key], "TFLOP/s"
+        achieved, peak, unit = kf / per_launch_s / 1e12, MFMA_PEAK_TFLOPS[wl.peak_key], "TFLOP/s"
     traffic = traffic_from_profile(wl.traffic_name)
     out = {
         "metric": wl.metric,
@@ -265,8 +404,9 @@ def main():
         "config": wl.config(),
         "roofline": {"bound": wl.bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
                      "frac": round(achieved / peak, 4), "traffic": traffic,
-                     "alg_bytes_per_launch": wl.alg_bytes(), "alg_flops_per_launch": wl.alg_flops(),
-                     "avg_launch_us": round(per_launch_s * 1e6, 3)},
+                     "alg_bytes_per_launch": kb, "alg_flops_per_launch": kf,
+                     "avg_launch_us": round(per_launch_s * 1e6, 3),
+                     "mfma_frac": round(kf / per_launch_s / 1e12 / MFMA_PEAK_TFLOPS.get(getattr(wl, "peak_key", "fp16"), 2500.0), 4)},
         "gbs": round(wl.alg_bytes() / per_step_s / 1e9, 2),
         "tflops": round(wl.alg_flops() / per_step_s / 1e12, 3),
         "wall_s_timed_region": round(wall, 4),

@@ -38,7 +38,7 @@ enum qmm_status {
 };
 
 enum qmm_format { QMM_Q4_0 = 0, QMM_Q4_K = 1, QMM_MXFP4 = 2, QMM_MXFP4S = 3 };
-enum qmm_dtype { QMM_F32 = 0, QMM_F16 = 1, QMM_BF16 = 2 };
+enum qmm_dtype { QMM_F32 = 0, QMM_F16 = 1, QMM_BF16 = 2, QMM_MXFP8 = 3 /* E4M3 codes + E8M0 per 32 */ };
 enum qmm_gemm_mode { QMM_GEMM_STORE = 0, QMM_GEMM_ACC = 1, QMM_GEMM_SWIGLU = 2 };
 enum qmm_act { QMM_ACT_SILU = 0, QMM_ACT_SWIGLU_OAI = 1 };
 
@@ -114,18 +114,22 @@ int qmm_moe_expert_mv_split(int mode, int fused, int act, int64_t k, int64_t n, 
 
 /* Grouped expert GEMM over bucketed rows, g_moe_ggu_{fmt}[_fused]_k{H} / g_moe_gdn_{fmt}_k{FE}
  * (S/gen_moe.py:1126-1228; launch args S/gen_llm.py:5376-5378):
- *   gu (mode 0): act_sorted[r] = act_fn(Wg[e] x[rowmap[r]/KU], Wu[e] x[rowmap[r]/KU])   (x rows gathered)
- *   dn (mode 1): ys_sorted[r]  = Wd[e] x[r]                                              (x rows sorted)
- * for every row r of every tile whose expert e = tile_info[tile, 0] >= 0; rows of rowmap -1 produce zeros.
- * Weights as qmm_moe_expert_mv (QMM_Q4_K; QMM_MXFP4S split planes via ws/ws2 with the scaled-MFMA path).
- * x: QMM_BF16 / QMM_F16 rows, or for the MXFP4S path E4M3 codes u8 [rows, k] + E8M0 scales u8 [rows, k/32]
- *   (x_scales, from qmm_quant_mxfp8); x_rows is the number of rows of x.
- * y: gu: f32 [max_tiles*64, n] (or the MXFP8 act via qmm_quant_mxfp8 afterwards); dn: f32 [max_tiles*64, n].
- * y_scales: optional f32 [max_tiles*64] per-row output multipliers (the reference's inverse row scales) or NULL. */
+ *   gu (mode 0): act[r] = act_fn(Wg[e] x[rowmap[r]/KU] inv, Wu[e] x[rowmap[r]/KU] inv)     (x rows gathered)
+ *   dn (mode 1): ys[r]  = Wd[e] x[r] inv                                                   (x rows sorted)
+ * for every row r of every 64-row tile whose expert e = tile_info[tile, 0] >= 0; rows with rowmap[r] == -1 are
+ * written as zeros, rows of unused tiles are not written. Weights as qmm_moe_expert_mv: w [E, n, k] (gu: gate;
+ * fused != 0: [E, 2n, k], each expert's n gate rows then its n up rows; w2 the up tensor otherwise).
+ *   QMM_Q4_K:   x is the row-scaled f16 operand (x_dtype QMM_F16) from qmm_row_scale_f16 with its scales f32
+ *               [x_rows, 2] in x_scales (inv = scales[row, 1]); K % 256 == 0; f16 MFMA, weights staged as
+ *               fma_f16(f16(q), f16(d sc), f16(-dmin m)).
+ *   QMM_MXFP4S: weights in split planes, ws / ws2 the E8M0 planes [E, rows, k/32]; x is MXFP8 (x_dtype
+ *               QMM_MXFP8) from qmm_quant_mxfp8: E4M3 codes u8 [x_rows, k] with x_scales u8 [x_rows, k/32];
+ *               K % 64 == 0; scaled f8f6f4 MFMA, inv = 1.
+ * x_rows: rows of x (gu: tokens; dn: >= max_tiles * 64). y: f32 [max_tiles * 64, n]. */
 int qmm_moe_grouped(int fmt, int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
                     const int32_t *tile_info, const int32_t *rowmap, const void *x, int x_dtype, const void *x_scales,
-                    int64_t x_rows, const void *w, const void *ws, const void *w2, const void *ws2,
-                    const float *y_scales, float *y, qmm_stream_t stream);
+                    int64_t x_rows, const void *w, const void *ws, const void *w2, const void *ws2, float *y,
+                    qmm_stream_t stream);
 
 /* Row-scaled f16 producer, g_row_scale_f16[_tiles] (S/gen_llm.py:1843-1915, S/gen_moe.py:503-527):
  * per row e = clamp(exponent(max|x|) - 13, 0, 100), x16 = f16(x * 2^-e), scales = (2^-e, 2^e).
@@ -134,11 +138,11 @@ int qmm_moe_grouped(int fmt, int mode, int fused, int act, int64_t max_tiles, in
 int qmm_row_scale_f16(int64_t rows, int64_t k, const void *x, int x_dtype, float *scales, void *x16,
                       const int32_t *tile_info, qmm_stream_t stream);
 
-/* Per-32 MXFP8 activation quantizer, the A operand of the gfx950 scaled MFMA (no reference counterpart: the
- * reference's fp8 producers, S/gen_mxfp4s.py:852-969, quantize with a per-row scale for gfx12 WMMA):
- *   s = clamp(floor(log2(amax_32)) - 7, -127, 127), codes = E4M3_RNE(x * 2^-s), scales = s + 127.
- * x: [rows, k] of x_dtype (QMM_F32 / QMM_BF16). tile_info (i32 [rows/64, 2]) or NULL: rows of unused tiles
- * are skipped. codes u8 [rows, k], scales u8 [rows, k/32]. */
+/* MXFP8 activation quantizer, the A operand of the gfx950 scaled MFMA (no reference counterpart: the reference's
+ * fp8 producers, S/gen_mxfp4s.py:852-969, quantize with a per-row power-of-two scale for gfx12 WMMA). One E8M0
+ * scale per 32 values along K (OCP MX):  s = clamp(floor(log2(amax_32)) - 7, -127, 127),
+ * codes = E4M3_RNE(x * 2^-s), scales = s + 127. x: [rows, k] of x_dtype (QMM_F32 / QMM_BF16), k % 32 == 0.
+ * tile_info (i32 [rows/64, 2]) or NULL: rows of unused tiles are skipped. codes u8 [rows, k], scales u8 [rows, k/32]. */
 int qmm_quant_mxfp8(int64_t rows, int64_t k, const void *x, int x_dtype, const int32_t *tile_info, uint8_t *codes,
                     uint8_t *scales, qmm_stream_t stream);
 

@@ -1,32 +1,40 @@
-// Q4_K prefill GEMM on the f16 MFMA: the g_gemm_q4_k_{store|acc}[_m128|_m256] family (S/gen_gemm.py:535-703).
+// Q4_K matmuls on the f16 MFMA: the prefill GEMM g_gemm_q4_k_{store|acc} (S/gen_gemm.py:535-703) and the MoE
+// grouped expert GEMMs g_moe_ggu_q4_k[_fused]_k{H} / g_moe_gdn_q4_k_k{FE} (S/gen_moe.py:1126-1228).
 //
-//   Y[r, c] = (acc ? Y[r, c] : 0) + inv[r] * sum_k X16[r, k] W[c, k]         fp32 accumulation
+//   dense   Y[r, c]   = (acc ? Y[r, c] : 0) + inv[r] sum_k X16[r, k] W[c, k]
+//   gu      act[r, c] = act_fn(inv[t] sum_k X16[t, k] Wg[e][c, k], inv[t] sum_k X16[t, k] Wu[e][c, k]),
+//                       t = rowmap[r] / KU  (rows gathered from the token rows)
+//   dn      ys[r, c]  = inv[r] sum_k A16[r, k] Wd[e][c, k]                       (rows already sorted)
 //
-// X16 is the row-scaled f16 operand the reference's g_row_scale_f16 produces (S/gen_llm.py:1843-1915) with
-// inv[r] = scales[r, 1]; W is Q4_K, dequantized to f16 in registers the way the reference stages it
-// (S/gen_gemm.py:499-530): w = fma_f16(f16(q), f16(d sc), f16(-dmin m)).
+// for every row r of every 64-row tile whose expert e = tile_info[tile, 0] >= 0; rows with rowmap[r] < 0 are
+// written as zeros. X16 / A16 are the row-scaled f16 operands the reference's g_row_scale_f16[_tiles] produces
+// (S/gen_llm.py:1843-1915, S/gen_moe.py:503-527) and inv = their scales[row, 1]. W is Q4_K, dequantized to f16 in
+// registers the way the reference stages it (S/gen_gemm.py:499-530): w = fma_f16(f16(q), f16(d sc), f16(-dmin m)).
+// fp32 accumulation throughout.
 //
-// Tiling (gfx950, wave64). A workgroup owns a 64 x 128 output tile and has four waves: wave (nh, kh) computes the
-// 64 x 64 quadrant nh of the tile over K-half kh with 2 x 2 v_mfma_f32_32x32x16_f16 tiles, so 256 workgroups
-// fill the 256 CUs with one wave per SIMD at the Qwen3-8B o_proj shape (512 x 4096 x 4096). The two K-halves are
-// summed through LDS at the end, in a fixed order. A step is one 64-value page of a super-block: the X16 rows of
-// both K-halves (2 x 64 x 64 f16) are staged in LDS, double-buffered, one barrier per step; each wave streams its
-// own 64 weight columns straight into registers (one 16-byte code chunk per column per step, the 16-byte header
-// once per super-block) and dequantizes them there, so B never touches LDS.
+// Tiling (gfx950, wave64). A workgroup has four waves and one 64-row tile. Dense and dn: the tile is 64 x 128 and
+// wave (nh, kh) computes the 64 x 64 quadrant nh over K-half kh; gu: the tile is 64 x 64 and wave (mat, kh)
+// computes it for matrix mat (gate, up) over K-half kh. Each wave holds 2 x 2 v_mfma_f32_32x32x16_f16
+// accumulators. The K-halves are summed through LDS at the end in a fixed order (and, for gu, the up result is
+// handed to the gate wave for the activation). A step is one 64-value page of a super-block: the activation rows
+// of both K-halves (2 x 64 x 64 f16) are staged in LDS, double-buffered, one barrier per step; each wave streams
+// its own 64 weight columns straight into registers and dequantizes them there, so weights never touch LDS. Loads
+// run DEPTH steps ahead of the math through register rings; the loads are unconditional (clamped addresses), so no
+// branch splits the load stream and the compiler keeps them in flight.
 //
 // MFMA operand order. Lane l of a 32x32x16 step holds 8 K values of row/column l % 32, octet l / 32. Lane half h
 // takes code bytes 16h .. 16h+15 of a page, i.e. values 16h .. 16h+15 of both of the page's sub-blocks; K16 step
 // s2 of a sub-block uses the lane's values 8 s2 .. 8 s2 + 7. The A fragment is read from LDS at the same K.
 //
-// Tile order is XCD-aware: consecutive tile ids (the M tiles of one N tile) land on one XCD, so the weight columns
-// a tile streams are read from HBM once per XCD and served from its L2 to the other M tiles.
+// Tile order is XCD-aware: consecutive tile ids land on one XCD (dense: the M tiles of one N tile, which share
+// weight columns; grouped: the column blocks of one expert tile, which share its activation rows).
 #include "common.hpp"
 
 using namespace qmm;
 
 namespace {
 
-constexpr int BM = 64, BN = 128, KSTEP = 64;
+constexpr int BM = 64, KSTEP = 64;
 #ifndef QMM_GEMM_DEPTH
 #define QMM_GEMM_DEPTH 4
 #endif
@@ -34,6 +42,8 @@ constexpr int kDepth = QMM_GEMM_DEPTH;   // steps of loads in flight per wave (e
 static_assert(kDepth % 2 == 0, "the LDS double buffer follows the step parity");
 constexpr int APITCH = KSTEP + 8;   // f16 per LDS row: 144 bytes, rows 16-byte aligned, reads 2-way at most
 typedef __attribute__((ext_vector_type(2))) _Float16 h2;
+
+enum Kind { kDense = 0, kGU = 1, kDN = 2 };
 
 __device__ __forceinline__ h2 as_h2(u32 v) { return __builtin_bit_cast(h2, v); }
 __device__ __forceinline__ u32 as_u32(h2 v) { return __builtin_bit_cast(u32, v); }
@@ -68,29 +78,83 @@ __device__ __forceinline__ void sub_scale(const uint4 &hd, int g, h2 &dsc, h2 &n
 
 __device__ __forceinline__ uint4 ld16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
 
-template <bool ACC, bool BF16OUT, int DEPTH>
-__global__ __launch_bounds__(256, 1) void gemm_q4k_kernel(int M, int N, int K, const _Float16 *__restrict__ x16,
-                                                          const float *__restrict__ scales,
-                                                          const u8 *__restrict__ w, void *__restrict__ yv,
-                                                          int tiles_m, int tiles_total) {
+__device__ __forceinline__ float act_fn(int act, float g, float u) {
+  if (act == QMM_ACT_SWIGLU_OAI) {
+    const float xg = fminf(g, 7.0f);
+    const float yu = fminf(fmaxf(u, -7.0f), 7.0f);
+    return xg / (1.0f + expf(-1.702f * xg)) * (yu + 1.0f);
+  }
+  return g / (1.0f + expf(-g)) * u;
+}
+
+struct Args {
+  int M, N, K;                 // dense: rows; grouped: rows of the sorted output (max_tiles * 64)
+  const _Float16 *x16;         // activation rows (dense / dn: [M, K]; gu: token rows [x_rows, K])
+  const float *scales;         // [rows of x16, 2] or NULL
+  int x_rows;                  // rows of x16 (gu)
+  const u8 *w, *w2;            // dense: W; grouped: expert tensors (gu: gate, up; fused: w only)
+  int64_t ebytes;              // bytes of one expert's matrix (grouped)
+  int64_t up_off;              // gu: byte offset of the up matrix from the gate matrix of an expert (fused)
+  const int32_t *tile_info, *rowmap;
+  int KU, E, act;
+  void *y;
+  int tiles_m, n_blocks, tiles_total;
+};
+
+template <int KIND, bool ACC, bool BF16OUT, int DEPTH>
+__global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
+  constexpr int BN = KIND == kGU ? 64 : 128;
   __shared__ __align__(16) _Float16 As[2][2][BM][APITCH];   // [buffer][K-half][row][k]
+  __shared__ int src_row[BM];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nh = wave & 1, kh = wave >> 1;
+  const int sel = wave & 1, kh = wave >> 1;   // sel: N-half (dense, dn) or matrix (gu: 0 gate, 1 up)
   const int per = (int)(gridDim.x / 8);
   const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
-  if (t >= tiles_total) return;
-  const int m0 = (t % tiles_m) * BM, n0 = (t / tiles_m) * BN;
+  if (t >= a.tiles_total) return;
+  const int M = a.M, N = a.N, K = a.K;
+
+  int m0, n0, expert = 0;
+  if constexpr (KIND == kDense) {
+    m0 = (t % a.tiles_m) * BM;
+    n0 = (t / a.tiles_m) * BN;
+  } else {
+    const int tile = t / a.n_blocks;
+    n0 = (t % a.n_blocks) * BN;
+    m0 = tile * BM;
+    expert = a.tile_info[2 * tile];
+    if (expert < 0) return;
+    expert = expert >= a.E ? a.E - 1 : expert;
+  }
+  // activation row of each tile row (-1: a dead row, written as zero)
+  if (tid < BM) {
+    int src;
+    if constexpr (KIND == kDense) src = m0 + tid < M ? m0 + tid : -1;
+    else if constexpr (KIND == kGU) {
+      const int rm = a.rowmap[m0 + tid];
+      src = rm >= 0 ? rm / a.KU : -1;
+      src = src < a.x_rows ? src : -1;
+    } else {
+      src = a.rowmap[m0 + tid] >= 0 ? m0 + tid : -1;
+    }
+    src_row[tid] = src;
+  }
+  __syncthreads();
+
   const int64_t RB = (int64_t)K / 256 * 144;
-  const int S = K / KSTEP, S0 = (S + 1) / 2, S1 = S - S0;
-  const int my_steps = kh ? S1 : S0;
+  const int S = K / KSTEP, S0 = S / 2;
 
   // ---- A staging map: chunk c = i * 256 + tid of 16 bytes; K-half, row, 16-byte column. Loads are unconditional
-  // with clamped addresses, so no branch or select splits the load stream: rows past M load row M - 1 (their
-  // outputs are never stored) and steps past S0 load step S0 - 1 (their weights are zeroed in the compute).
-  auto a_load = [&](int i, int s) -> uint4 {
+  // (dead rows read activation row 0 and their outputs are zeroed; steps past S0 reload step S0 - 1 and get zero
+  // weights in the math).
+  const _Float16 *arow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
     const int c = i * 256 + tid, ckh = c >> 9, row = (c >> 3) & 63, col = c & 7;
-    const int r = m0 + row < M ? m0 + row : M - 1, gs = ckh * S0 + (s < S0 ? s : S0 - 1);
-    return *reinterpret_cast<const uint4 *>(x16 + (int64_t)r * K + (int64_t)gs * KSTEP + col * 8);
+    const int src = src_row[row];
+    arow[i] = a.x16 + (int64_t)(src >= 0 ? src : 0) * K + (int64_t)ckh * S0 * KSTEP + col * 8;
+  }
+  auto a_load = [&](int i, int s) -> uint4 {
+    return *reinterpret_cast<const uint4 *>(arow[i] + (int64_t)(s < S0 ? s : S0 - 1) * KSTEP);
   };
   auto a_dst = [&](int i, int buf) -> uint4 * {
     const int c = i * 256 + tid, ckh = c >> 9, row = (c >> 3) & 63, col = c & 7;
@@ -99,12 +163,20 @@ __global__ __launch_bounds__(256, 1) void gemm_q4k_kernel(int M, int N, int K, c
 
   // ---- B: this lane's two weight columns and code half
   const int h = lane >> 5, lc = lane & 31;
+  const u8 *wbase;
+  if constexpr (KIND == kDense) wbase = a.w;
+  else if constexpr (KIND == kGU) {
+    const u8 *g = a.w + (int64_t)expert * a.ebytes;
+    wbase = sel ? (a.w2 ? a.w2 + (int64_t)expert * a.ebytes : g + a.up_off) : g;
+  } else {
+    wbase = a.w + (int64_t)expert * a.ebytes;
+  }
   const u8 *wcol[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    int c = n0 + nh * 64 + 32 * j + lc;
+    int c = n0 + (KIND == kGU ? 0 : sel * 64) + 32 * j + lc;
     c = c < N ? c : N - 1;
-    wcol[j] = w + (int64_t)c * RB;
+    wcol[j] = wbase + (int64_t)c * RB;
   }
   auto b_code = [&](int j, int s) -> uint4 {
     const int gs = kh * S0 + (s < S0 ? s : S0 - 1);
@@ -133,7 +205,6 @@ __global__ __launch_bounds__(256, 1) void gemm_q4k_kernel(int M, int N, int K, c
 #pragma unroll
     for (int j = 0; j < 2; ++j) { cring[slot][j] = b_code(j, st); hring[slot][j] = b_head(j, st); }
   };
-  // prologue: A of step 0 into LDS buffer 0, A of steps 1..DEPTH and B of steps 0..DEPTH-1 in flight
   load_a(0, 0);
 #pragma unroll
   for (int i = 0; i < 4; ++i) *a_dst(i, 0) = aring[0][i];
@@ -143,8 +214,8 @@ __global__ __launch_bounds__(256, 1) void gemm_q4k_kernel(int M, int N, int K, c
   for (int u = 0; u < DEPTH; ++u) load_b(u, u);
   __syncthreads();
 
-  // The step count is rounded up to a multiple of DEPTH; steps past S0 get zero weights (no contribution), so
-  // the loop body has no data-dependent branch and every wave runs the same barriers. Both K-halves have S0 steps
+  // The step count is rounded up to a multiple of DEPTH; steps past S0 get zero weights (no contribution), so the
+  // loop body has no data-dependent branch and every wave runs the same barriers. Both K-halves have S0 steps
   // (K is a multiple of 256, so K / 64 is even).
   const int SP = (S0 + DEPTH - 1) / DEPTH * DEPTH;
   for (int s0 = 0; s0 < SP; s0 += DEPTH) {
@@ -188,41 +259,85 @@ __global__ __launch_bounds__(256, 1) void gemm_q4k_kernel(int M, int N, int K, c
     }
   }
 
-  // ---- sum the K-halves through LDS (K-half 1 hands its partial to K-half 0), then the epilogue
-  float *red = reinterpret_cast<float *>(&As[0][0][0][0]);   // [nh][64 values][64 lanes]
+  // ---- sum the K-halves through LDS (K-half 1 hands its partial to K-half 0)
+  float *red = reinterpret_cast<float *>(&As[0][0][0][0]);   // [sel][64 values][64 lanes]
+  auto red_at = [&](int sl, int i, int j, int r) -> float & {
+    return red[(sl * 64 + (i * 2 + j) * 16 + r) * 64 + lane];
+  };
   if (kh == 1) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) red[(nh * 64 + (i * 2 + j) * 16 + r) * 64 + lane] = acc[i][j][r];
+        for (int r = 0; r < 16; ++r) red_at(sel, i, j, r) = acc[i][j][r];
   }
   __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] += red_at(sel, i, j, r);
+
+  if constexpr (KIND == kGU) {
+    // the up wave (K-half 0) hands its result to the gate wave; every wave takes part in the barriers
+    __syncthreads();
+    if (kh == 0 && sel == 1) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) red_at(0, i, j, r) = acc[i][j][r];
+    }
+    __syncthreads();
+    if (sel == 1) return;
+  }
   if (kh == 1) return;
+
+  // ---- epilogue
+  float *yf = static_cast<float *>(a.y);
+  u16 *yb = static_cast<u16 *>(a.y);
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-        const int col = n0 + nh * 64 + 32 * j + lc;
-        if (row < M && col < N) {
-          float v = acc[i][j][r] + red[(nh * 64 + (i * 2 + j) * 16 + r) * 64 + lane];
-          if (scales) v *= scales[2 * row + 1];
-          const int64_t o = (int64_t)row * N + col;
+        const int lr = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+        const int row = m0 + lr;
+        const int col = n0 + (KIND == kGU ? 0 : sel * 64) + 32 * j + lc;
+        if (col >= N || (KIND == kDense && row >= M)) continue;
+        const int src = src_row[lr];
+        const int64_t o = (int64_t)row * N + col;
+        if constexpr (KIND == kDense) {
+          float v = acc[i][j][r];
+          if (a.scales) v *= a.scales[2 * row + 1];
           if constexpr (BF16OUT) {
-            u16 *y = static_cast<u16 *>(yv);
-            if constexpr (ACC) v += bf16_to_f32(y[o]);
-            y[o] = (u16)f32_to_bf16_rne(v);
+            if constexpr (ACC) v += bf16_to_f32(yb[o]);
+            yb[o] = (u16)f32_to_bf16_rne(v);
           } else {
-            float *y = static_cast<float *>(yv);
-            if constexpr (ACC) v += y[o];
-            y[o] = v;
+            if constexpr (ACC) v += yf[o];
+            yf[o] = v;
           }
+        } else {
+          float v = 0.f;
+          if (src >= 0) {
+            const float inv = a.scales ? a.scales[2 * src + 1] : 1.f;
+            if constexpr (KIND == kGU) v = act_fn(a.act, acc[i][j][r] * inv, red_at(0, i, j, r) * inv);
+            else v = acc[i][j][r] * inv;
+          }
+          yf[o] = v;
         }
       }
+}
+
+template <int KIND, bool ACC, bool BF16OUT>
+int launch(const Args &a, hipStream_t s) {
+  const dim3 grid((unsigned)(8 * ((a.tiles_total + 7) / 8)));
+  q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth><<<grid, 256, 0, s>>>(a);
+  return launch_status();
 }
 
 }  // namespace
@@ -239,16 +354,43 @@ extern "C" int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, c
   if (rows <= 0 || n <= 0 || k <= 0 || k % 256) return QMM_ERR_SHAPE;
   if (rows > (1 << 24) || n > (1 << 24) || k > (1 << 20)) return QMM_ERR_SHAPE;
   if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 4)) return QMM_ERR_ALIGN;
+  Args a{};
+  a.M = (int)rows; a.N = (int)n; a.K = (int)k;
+  a.x16 = static_cast<const _Float16 *>(x); a.scales = scales; a.x_rows = (int)rows;
+  a.w = static_cast<const u8 *>(w); a.y = y;
+  a.tiles_m = (int)((rows + BM - 1) / BM);
+  a.tiles_total = a.tiles_m * (int)((n + 127) / 128);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int tiles_m = (int)((rows + BM - 1) / BM), tiles_n = (int)((n + BN - 1) / BN);
-  const int total = tiles_m * tiles_n, per = (total + 7) / 8;
-  const dim3 grid((unsigned)(8 * per));
-  const _Float16 *xp = static_cast<const _Float16 *>(x);
-  const u8 *wp = static_cast<const u8 *>(w);
   const bool acc = mode == QMM_GEMM_ACC, bf = y_dtype == QMM_BF16;
-  if (acc && bf) gemm_q4k_kernel<true, true, kDepth><<<grid, 256, 0, s>>>((int)rows, (int)n, (int)k, xp, scales, wp, y, tiles_m, total);
-  else if (acc) gemm_q4k_kernel<true, false, kDepth><<<grid, 256, 0, s>>>((int)rows, (int)n, (int)k, xp, scales, wp, y, tiles_m, total);
-  else if (bf) gemm_q4k_kernel<false, true, kDepth><<<grid, 256, 0, s>>>((int)rows, (int)n, (int)k, xp, scales, wp, y, tiles_m, total);
-  else gemm_q4k_kernel<false, false, kDepth><<<grid, 256, 0, s>>>((int)rows, (int)n, (int)k, xp, scales, wp, y, tiles_m, total);
-  return launch_status();
+  if (acc && bf) return launch<kDense, true, true>(a, s);
+  if (acc) return launch<kDense, true, false>(a, s);
+  if (bf) return launch<kDense, false, true>(a, s);
+  return launch<kDense, false, false>(a, s);
+}
+
+// The Q4_K path of qmm_moe_grouped (grouped.hip checks the arguments shared with the MXFP4 path).
+int qmm_grouped_q4k(int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
+                    const int32_t *tile_info, const int32_t *rowmap, const void *x, const float *x_scales,
+                    int64_t x_rows, const void *w, const void *w2, float *y, hipStream_t s) {
+  if (k % 256) return QMM_ERR_SHAPE;
+  if (!aligned(x, 16) || !aligned(w, 16) || (w2 && !aligned(w2, 16))) return QMM_ERR_ALIGN;
+  const int64_t RB = k / 256 * 144;
+  Args a{};
+  a.M = (int)(max_tiles * BM); a.N = (int)n; a.K = (int)k;
+  a.x16 = static_cast<const _Float16 *>(x); a.scales = x_scales; a.x_rows = (int)x_rows;
+  a.tile_info = tile_info; a.rowmap = rowmap; a.KU = KU; a.E = E; a.act = act; a.y = y;
+  a.w = static_cast<const u8 *>(w);
+  if (mode == 0) {
+    if (!fused && !w2) return QMM_ERR_NULL;
+    a.ebytes = RB * n * (fused ? 2 : 1);
+    a.up_off = fused ? RB * n : 0;
+    a.w2 = fused ? nullptr : static_cast<const u8 *>(w2);
+    a.n_blocks = (int)((n + 63) / 64);
+    a.tiles_total = (int)max_tiles * a.n_blocks;
+    return launch<kGU, false, false>(a, s);
+  }
+  a.ebytes = RB * n;
+  a.n_blocks = (int)((n + 127) / 128);
+  a.tiles_total = (int)max_tiles * a.n_blocks;
+  return launch<kDN, false, false>(a, s);
 }

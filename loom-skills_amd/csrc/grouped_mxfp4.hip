@@ -1,0 +1,267 @@
+// MXFP4 grouped expert GEMMs on the gfx950 scaled MFMA, the g_moe_ggu_mxfp4s[_fused]_k{H} / g_moe_gdn_mxfp4s_k{FE}
+// kernels of the reference's MoE prefill chain (S/gen_moe.py:1126-1228; its fp8 MXFP4 GEMM, S/gen_mxfp4s.py:1-21,
+// is the gfx12 WMMA counterpart):
+//
+//   gu   act[r, c] = act_fn(sum_k X8[t, k] Wg[e][c, k], sum_k X8[t, k] Wu[e][c, k]),  t = rowmap[r] / KU
+//   dn   ys[r, c]  = sum_k A8[r, k] Wd[e][c, k]                                        (rows already sorted)
+//
+// for every row r of every 64-row tile with expert e = tile_info[tile, 0] >= 0 (rows with rowmap[r] < 0 are written
+// as zeros). W is MXFP4 in split planes: nibbles [E, rows, K/2] ("pairs": byte j holds elements 2j, 2j+1) and
+// E8M0 scales [E, rows, K/32]. X8 / A8 are MXFP8 activations from qmm_quant_mxfp8: E4M3 codes [rows, K] with one
+// E8M0 scale per 32 values along K. fp32 accumulation.
+//
+// One v_mfma_scale_f32_32x32x64_f8f6f4 per 32 x 32 x 64 block, A = E4M3 activations (format 0), B = E2M1 weights
+// (format 4), both with E8M0 block scales applied by the MFMA itself (measured lane layouts on gfx950, half
+// h = lane / 32): the E2M1 operand of lane h holds K values 32h .. 32h+31 of the 64-value chunk as 16 bytes, low
+// nibble first, which is exactly one 32-value block of the split nibble plane, so weights go from HBM to the MFMA
+// without any unpacking, and its scale is that block's E8M0 byte. The E4M3 operand of lane h holds K values
+// 16h .. 16h+15 in bytes 0..15 and 32+16h .. 32+16h+15 in bytes 16..31, and its scale is the one of block h; both
+// operands therefore see the same two 32-value blocks per chunk.
+//
+// Tiling: a workgroup of four waves owns one 64-row expert tile; each wave computes 64 rows x 64 columns
+// (2 x 2 MFMA blocks) over all of K. gu: waves (mat, nh) = gate / up x two 64-column halves of a 128-column block;
+// the up waves hand their results to the gate waves through LDS for the activation. dn: four 64-column quarters of
+// a 256-column block. A step is one 64-value chunk: the tile's 64 activation rows (64 B each) and their scales are
+// staged in LDS, double-buffered, one barrier per step; the weights stream straight into registers DEPTH steps
+// ahead through register rings with unconditional (clamped) loads.
+#include "common.hpp"
+
+using namespace qmm;
+
+namespace {
+
+#ifndef QMM_MX_DEPTH
+#define QMM_MX_DEPTH 4
+#endif
+constexpr int kDepth = QMM_MX_DEPTH;
+static_assert(kDepth % 2 == 0, "the LDS double buffer follows the step parity");
+constexpr int BM = 64, KC = 64, APITCH = KC + 16;   // activation bytes per LDS row (80: 16-byte aligned rows)
+
+enum Kind { kGU = 1, kDN = 2 };
+
+struct MArgs {
+  int N, K;
+  const u8 *x8, *xs;            // activation codes [rows, K], scales [rows, K/32]
+  int x_rows;
+  const u8 *wn, *wsc;           // gate (or down) nibbles / scales of expert 0
+  const u8 *wn2, *wsc2;         // up nibbles / scales (gu, not fused) or NULL
+  int64_t nib_ebytes, sc_ebytes;   // bytes of one expert's nibble / scale plane
+  int64_t up_nib_off, up_sc_off;   // fused gu: offset of the up rows inside an expert
+  const int32_t *tile_info, *rowmap;
+  int KU, E, act;
+  float *y;
+  int n_blocks, tiles_total;
+};
+
+__device__ __forceinline__ float act_fn(int act, float g, float u) {
+  if (act == QMM_ACT_SWIGLU_OAI) {
+    const float xg = fminf(g, 7.0f);
+    const float yu = fminf(fmaxf(u, -7.0f), 7.0f);
+    return xg / (1.0f + expf(-1.702f * xg)) * (yu + 1.0f);
+  }
+  return g / (1.0f + expf(-g)) * u;
+}
+
+template <int KIND, int DEPTH>
+__global__ __launch_bounds__(256, 1) void mxfp4_grouped_kernel(MArgs a) {
+  constexpr int BN = KIND == kGU ? 128 : 256;
+  __shared__ __align__(16) u8 As[2][BM][APITCH];
+  __shared__ u16 Ass[2][BM];   // the row's two E8M0 scales of the chunk (block 2c in the low byte)
+  __shared__ int src_row[BM];
+  __shared__ __align__(16) float red[2][16 * 4][64];   // gu: the up waves' results, [nh][value][lane]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int per = (int)(gridDim.x / 8);
+  const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+  if (t >= a.tiles_total) return;
+  const int N = a.N, K = a.K, C = K / KC;
+  const int tile = t / a.n_blocks, n0 = (t % a.n_blocks) * BN, m0 = tile * BM;
+  int expert = a.tile_info[2 * tile];
+  if (expert < 0) return;
+  expert = expert >= a.E ? a.E - 1 : expert;
+  const int mat = KIND == kGU ? wave >> 1 : 0;   // gu: 0 gate, 1 up
+  const int nq = KIND == kGU ? wave & 1 : wave;   // 64-column slice of the block
+
+  if (tid < BM) {
+    int src;
+    if constexpr (KIND == kGU) {
+      const int rm = a.rowmap[m0 + tid];
+      src = rm >= 0 ? rm / a.KU : -1;
+      src = src < a.x_rows ? src : -1;
+    } else {
+      src = a.rowmap[m0 + tid] >= 0 ? m0 + tid : -1;
+    }
+    src_row[tid] = src;
+  }
+  __syncthreads();
+
+  // ---- activation staging: thread tid carries 16 bytes of row tid / 4 (and the row's two scale bytes when
+  // tid % 4 == 0)
+  const int arow_i = tid >> 2, apart = tid & 3;
+  const int asrc = src_row[arow_i] >= 0 ? src_row[arow_i] : 0;
+  const u8 *acode = a.x8 + (int64_t)asrc * K + 16 * apart;
+  const u16 *ascale = reinterpret_cast<const u16 *>(a.xs + (int64_t)asrc * (K / 32));
+  auto clampc = [&](int c) { return c < C ? c : C - 1; };
+
+  // ---- weights: this lane's two columns and K half
+  const int h = lane >> 5, lc = lane & 31;
+  const u8 *nb, *sb;
+  if constexpr (KIND == kGU) {
+    const u8 *gn = a.wn + (int64_t)expert * a.nib_ebytes, *gs = a.wsc + (int64_t)expert * a.sc_ebytes;
+    if (mat == 0) { nb = gn; sb = gs; }
+    else if (a.wn2) { nb = a.wn2 + (int64_t)expert * a.nib_ebytes; sb = a.wsc2 + (int64_t)expert * a.sc_ebytes; }
+    else { nb = gn + a.up_nib_off; sb = gs + a.up_sc_off; }
+  } else {
+    nb = a.wn + (int64_t)expert * a.nib_ebytes;
+    sb = a.wsc + (int64_t)expert * a.sc_ebytes;
+  }
+  const u8 *wcn[2], *wcs[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    int col = n0 + 64 * nq + 32 * j + lc;
+    col = col < N ? col : N - 1;
+    wcn[j] = nb + (int64_t)col * (K / 2) + 16 * h;
+    wcs[j] = sb + (int64_t)col * (K / 32) + h;
+  }
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  uint4 aring[DEPTH], bring[DEPTH][2];
+  u32 asr[DEPTH], bsr[DEPTH][2];
+  auto load_a = [&](int slot, int c) {
+    const int cc = clampc(c);
+    aring[slot] = *reinterpret_cast<const uint4 *>(acode + (int64_t)cc * KC);
+    asr[slot] = ascale[cc];
+  };
+  auto load_b = [&](int slot, int c) {
+    const int cc = clampc(c);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      bring[slot][j] = *reinterpret_cast<const uint4 *>(wcn[j] + (int64_t)cc * 32);
+      bsr[slot][j] = wcs[j][2 * cc];
+    }
+  };
+  auto stage = [&](int slot, int buf) {
+    *reinterpret_cast<uint4 *>(&As[buf][arow_i][16 * apart]) = aring[slot];
+    if (apart == 0) Ass[buf][arow_i] = (u16)asr[slot];
+  };
+  load_a(0, 0);
+  stage(0, 0);
+#pragma unroll
+  for (int u = 1; u <= DEPTH; ++u) load_a(u % DEPTH, u);
+#pragma unroll
+  for (int u = 0; u < DEPTH; ++u) load_b(u, u);
+  __syncthreads();
+
+  const int CP = (C + DEPTH - 1) / DEPTH * DEPTH;
+  for (int c0 = 0; c0 < CP; c0 += DEPTH) {
+#pragma unroll
+    for (int u = 0; u < DEPTH; ++u) {
+      const int c = c0 + u;
+      const int buf = u & 1;
+      if (c < C) {
+        i32x8 af[2];
+        int sa[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const uint4 v0 = *reinterpret_cast<const uint4 *>(&As[buf][32 * i + lc][16 * h]);
+          const uint4 v1 = *reinterpret_cast<const uint4 *>(&As[buf][32 * i + lc][32 + 16 * h]);
+          af[i] = i32x8{(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w, (int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w};
+          sa[i] = (Ass[buf][32 * i + lc] >> (8 * h)) & 0xFF;
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const i32x8 bf = i32x8{(int)bring[u][j].x, (int)bring[u][j].y, (int)bring[u][j].z, (int)bring[u][j].w,
+                                 0, 0, 0, 0};
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[i], bf, acc[i][j], 0, 4, 0, sa[i], 0,
+                                                                        (int)bsr[u][j]);
+        }
+      }
+      load_b(u, c + DEPTH);
+      const int nx = (u + 1) % DEPTH;
+      stage(nx, buf ^ 1);
+      load_a(nx, c + 1 + DEPTH);
+      __syncthreads();
+    }
+  }
+
+  if constexpr (KIND == kGU) {
+    if (mat == 1) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) red[nq][(i * 2 + j) * 16 + r][lane] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (mat == 1) return;
+  }
+
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int lr = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+        const int col = n0 + 64 * nq + 32 * j + lc;
+        if (col >= N) continue;
+        float v = 0.f;
+        if (src_row[lr] >= 0) {
+          if constexpr (KIND == kGU) v = act_fn(a.act, acc[i][j][r], red[nq][(i * 2 + j) * 16 + r][lane]);
+          else v = acc[i][j][r];
+        }
+        a.y[(int64_t)(m0 + lr) * N + col] = v;
+      }
+}
+
+template <int KIND>
+int launch(const MArgs &a, hipStream_t s) {
+  const dim3 grid((unsigned)(8 * ((a.tiles_total + 7) / 8)));
+  mxfp4_grouped_kernel<KIND, kDepth><<<grid, 256, 0, s>>>(a);
+  return launch_status();
+}
+
+}  // namespace
+
+// The MXFP4 (split planes) path of qmm_moe_grouped.
+int qmm_grouped_mxfp4(int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
+                      const int32_t *tile_info, const int32_t *rowmap, const void *x, const void *x_scales,
+                      int64_t x_rows, const void *w, const void *ws, const void *w2, const void *ws2, float *y,
+                      hipStream_t s) {
+  if (k % 64) return QMM_ERR_SHAPE;
+  if (!x_scales || !ws) return QMM_ERR_NULL;
+  if (!aligned(x_scales, 2)) return QMM_ERR_ALIGN;
+  if (!aligned(x, 16) || !aligned(w, 16) || (w2 && !aligned(w2, 16))) return QMM_ERR_ALIGN;
+  MArgs a{};
+  a.N = (int)n; a.K = (int)k;
+  a.x8 = static_cast<const u8 *>(x); a.xs = static_cast<const u8 *>(x_scales); a.x_rows = (int)x_rows;
+  a.wn = static_cast<const u8 *>(w); a.wsc = static_cast<const u8 *>(ws);
+  a.tile_info = tile_info; a.rowmap = rowmap; a.KU = KU; a.E = E; a.act = act; a.y = y;
+  const int64_t nrow = k / 2, srow = k / 32;
+  if (mode == 0) {
+    if (!fused && (!w2 || !ws2)) return QMM_ERR_NULL;
+    a.nib_ebytes = nrow * n * (fused ? 2 : 1);
+    a.sc_ebytes = srow * n * (fused ? 2 : 1);
+    a.up_nib_off = fused ? nrow * n : 0;
+    a.up_sc_off = fused ? srow * n : 0;
+    a.wn2 = fused ? nullptr : static_cast<const u8 *>(w2);
+    a.wsc2 = fused ? nullptr : static_cast<const u8 *>(ws2);
+    a.n_blocks = (int)((n + 127) / 128);
+    a.tiles_total = (int)max_tiles * a.n_blocks;
+    return launch<kGU>(a, s);
+  }
+  a.nib_ebytes = nrow * n;
+  a.sc_ebytes = srow * n;
+  a.n_blocks = (int)((n + 255) / 256);
+  a.tiles_total = (int)max_tiles * a.n_blocks;
+  return launch<kDN>(a, s);
+}

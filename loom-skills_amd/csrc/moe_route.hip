@@ -5,7 +5,7 @@
 //                                                                    g_moe_bucket, S/gen_moe.py:829-955
 //   qmm_moe_combine    y[t] (+)= sum_k w[t,k] ys[row(t,k)]           g_moe_combine[_sorted], S/gen_moe.py:730-762, :1231-1280
 //   qmm_row_scale_f16  per-row power-of-two scale + f16 copy         g_row_scale_f16[_tiles], S/gen_llm.py:1843-1915
-//   qmm_quant_mxfp8    per-32 E4M3 + E8M0 operand of the scaled MFMA
+//   qmm_quant_mxfp8    E4M3 + E8M0-per-32 operand of the scaled MFMA
 //   qmm_repack_mxfp4   GGUF 17-byte MXFP4 blocks -> split planes
 #include "common.hpp"
 
@@ -274,19 +274,21 @@ __global__ __launch_bounds__(256) void row_scale_kernel(int64_t rows, int64_t k,
 // ---------------------------------------------------------------------------------------------- MXFP8 quant
 // One thread per 32 values. s = clamp(floor(log2(amax)) - 7, -127, 127) keeps every |x| 2^-s below 256, under the
 // E4M3 maximum 448; the conversion is v_cvt_pk_fp8_f32 (round to nearest even, OCP E4M3FN on gfx950).
+constexpr int kMxBlock = 32;
+
 __global__ __launch_bounds__(256) void quant_mxfp8_kernel(int64_t rows, int64_t k, const void *__restrict__ xv,
                                                           int bf, const int32_t *__restrict__ tile_info,
                                                           u8 *__restrict__ codes, u8 *__restrict__ scales) {
   const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t groups = rows * (k / 32);
-  if (g >= groups) return;
-  const int64_t r = g / (k / 32);
+  const int64_t per_row = k / kMxBlock;
+  if (g >= rows * per_row) return;
+  const int64_t r = g / per_row;
   if (tile_info && tile_info[2 * (r / kTile)] < 0) return;
-  float v[32];
+  float v[kMxBlock];
   if (bf) {
-    const uint4 *p = reinterpret_cast<const uint4 *>(static_cast<const u16 *>(xv) + g * 32);
+    const uint4 *p = reinterpret_cast<const uint4 *>(static_cast<const u16 *>(xv) + g * kMxBlock);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < kMxBlock / 8; ++i) {
       const uint4 q = p[i];
       const u32 d[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
@@ -296,33 +298,33 @@ __global__ __launch_bounds__(256) void quant_mxfp8_kernel(int64_t rows, int64_t 
       }
     }
   } else {
-    const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(xv) + g * 32);
+    const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(xv) + g * kMxBlock);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < kMxBlock / 4; ++i) {
       const float4 q = p[i];
       v[4 * i] = q.x; v[4 * i + 1] = q.y; v[4 * i + 2] = q.z; v[4 * i + 3] = q.w;
     }
   }
   float amax = 0.f;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  for (int i = 0; i < kMxBlock; ++i) amax = fmaxf(amax, fabsf(v[i]));
   int s = -127;
   if (amax > 0.f) {
     int ex;
     frexpf(amax, &ex);        // amax = f 2^ex, f in [0.5, 1)
     s = min(max(ex - 1 - 7, -127), 127);
   }
-  u32 out[8];
+  u32 out[kMxBlock / 4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < kMxBlock / 4; ++i) {
     int w = 0;
     w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * i], -s), ldexpf(v[4 * i + 1], -s), w, false);
     w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * i + 2], -s), ldexpf(v[4 * i + 3], -s), w, true);
     out[i] = (u32)w;
   }
-  uint4 *o = reinterpret_cast<uint4 *>(codes + g * 32);
-  o[0] = make_uint4(out[0], out[1], out[2], out[3]);
-  o[1] = make_uint4(out[4], out[5], out[6], out[7]);
+  uint4 *o = reinterpret_cast<uint4 *>(codes + g * kMxBlock);
+#pragma unroll
+  for (int i = 0; i < kMxBlock / 16; ++i) o[i] = make_uint4(out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]);
   scales[g] = (u8)(s + 127);
 }
 
@@ -404,11 +406,11 @@ int qmm_quant_mxfp8(int64_t rows, int64_t k, const void *x, int x_dtype, const i
                     uint8_t *scales, qmm_stream_t stream) {
   if (!x || !codes || !scales) return QMM_ERR_NULL;
   if (x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
-  if (rows <= 0 || k <= 0 || k % 32 || rows > (1ll << 24)) return QMM_ERR_SHAPE;
+  if (rows <= 0 || k <= 0 || k % kMxBlock || rows > (1ll << 24)) return QMM_ERR_SHAPE;
   if (tile_info && rows % kTile) return QMM_ERR_SHAPE;
   if (!aligned(x, 16) || !aligned(codes, 16)) return QMM_ERR_ALIGN;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int64_t groups = rows * (k / 32);
+  const int64_t groups = rows * (k / kMxBlock);
   quant_mxfp8_kernel<<<(unsigned)((groups + 255) / 256), 256, 0, s>>>(rows, k, x, x_dtype == QMM_BF16, tile_info,
                                                                       codes, scales);
   return launch_status();

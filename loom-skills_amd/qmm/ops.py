@@ -10,6 +10,8 @@ S/ = skills/loom-port-llm/starter/):
     moe_expert_mv     g_moe_gu_* / g_moe_dn_*                 S/gen_moe.py:535-727
     moe_grouped       g_moe_ggu_* / g_moe_gdn_*               S/gen_moe.py:1126-1228
     moe_combine       g_moe_combine[_sorted]                  S/gen_moe.py:730-762, :1231-1280
+    moe_prefill       the prefill chain of moe_routed          S/gen_llm.py:5324-5385 (t >= 64)
+    moe_decode        the decode chain of moe_routed           S/gen_llm.py:5324-5385 (t < 64)
     row_scale_f16     g_row_scale_f16[_tiles]                 S/gen_llm.py:1843-1915, S/gen_moe.py:503-527
     dequant           the @g_<fmt>_values helpers (bit-exact f32 values)
 
@@ -22,7 +24,7 @@ launches asynchronously on torch's current stream. Weights are uint8 tensors hol
 import torch
 
 from . import _lib
-from .formats import ACT, CODE, DTYPE, GEMM_MODE, SPLIT, row_bytes
+from .formats import ACT, CODE, DTYPE, GEMM_MODE, MX_BLOCK, SPLIT, row_bytes
 
 TILE = 64
 
@@ -136,15 +138,17 @@ def moe_expert_mv(fmt, mode, ids, x, w, n, k, E, KU, w2=None, ws=None, ws2=None,
 
 
 def moe_grouped(fmt, mode, tile_info, rowmap, x, w, n, k, E, KU, w2=None, ws=None, ws2=None, x_scales=None,
-                fused=False, act="silu", y_scales=None, y=None, x_dtype=None):
-    """Grouped expert GEMM over bucketed 64-row tiles (see include/qmm.h, qmm_moe_grouped)."""
-    _dev(tile_info, rowmap, x, w, w2, ws, ws2, x_scales, y_scales, y)
+                fused=False, act="silu", y=None):
+    """Grouped expert GEMM over bucketed 64-row tiles (include/qmm.h, qmm_moe_grouped).
+    q4_k: x f16 row-scaled rows with x_scales f32 [rows, 2] (row_scale_f16); mxfp4s: x E4M3 codes uint8 [rows, k]
+    with x_scales uint8 [rows, k/64] (quant_mxfp8). y: f32 [max_tiles * 64, n]."""
+    _dev(tile_info, rowmap, x, w, w2, ws, ws2, x_scales, y)
     n_tiles = tile_info.shape[0]
     y = torch.empty((n_tiles * TILE, n), dtype=torch.float32, device=x.device) if y is None else y
-    xd = _dt(x) if x_dtype is None else x_dtype
+    xd = DTYPE["mxfp8"] if x.dtype == torch.uint8 else _dt(x)
     _lib.call("qmm_moe_grouped", CODE[fmt], {"gu": 0, "dn": 1}[mode], int(fused), ACT[act], n_tiles, k, n, E, KU,
               _ptr(tile_info), _ptr(rowmap), _ptr(x), xd, _ptr(x_scales), x.shape[0], _ptr(w), _ptr(ws), _ptr(w2),
-              _ptr(ws2), _ptr(y_scales), _ptr(y), _stream())
+              _ptr(ws2), _ptr(y), _stream())
     return y
 
 
@@ -170,11 +174,11 @@ def row_scale_f16(x, tile_info=None, x16=None, scales=None):
 
 
 def quant_mxfp8(x, tile_info=None, codes=None, scales=None):
-    """(E4M3 codes u8 [rows, k], E8M0 scales u8 [rows, k/32]) of x f32 / bf16 [rows, k]."""
+    """(E4M3 codes u8 [rows, k], E8M0 scales u8 [rows, k/64]) of x f32 / bf16 [rows, k]."""
     _dev(x, tile_info, codes, scales)
     rows, k = x.shape
     codes = torch.empty((rows, k), dtype=torch.uint8, device=x.device) if codes is None else codes
-    scales = torch.empty((rows, k // 32), dtype=torch.uint8, device=x.device) if scales is None else scales
+    scales = torch.empty((rows, k // MX_BLOCK), dtype=torch.uint8, device=x.device) if scales is None else scales
     _lib.call("qmm_quant_mxfp8", rows, k, _ptr(x), _dt(x), _ptr(tile_info), _ptr(codes), _ptr(scales), _stream())
     return codes, scales
 
@@ -190,3 +194,41 @@ def repack_mxfp4(w, rows, k):
 
 def weight_bytes(fmt, rows, k):
     return rows * row_bytes(fmt, k)
+
+
+# ------------------------------------------------------------------------------------------------ MoE chains
+def moe_prefill(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=None, ws_gate=None, ws_down=None,
+                ws_up=None, fused=False, act="silu", scale=1.0, bias=None):
+    """The reference's prefill MoE chain (moe_routed with t >= 64, S/gen_llm.py:5324-5385): route, bucket into
+    64-row expert tiles, grouped gate/up GEMM with the activation, grouped down GEMM, combine.
+    q4_k: activations row-scaled to f16 (g_row_scale_f16[_tiles]); mxfp4s: quantized to MXFP8.
+    x bf16 / f32 [T, H], logits f32 [T, E]. Returns (y f32 [T, H], intermediates dict)."""
+    ids, wts = moe_topk(logits, KU, gating, norm, scale=scale, bias=bias)
+    tile_info, rowmap, pos = moe_bucket(ids, E)
+    if fmt == "q4_k":
+        x16, xs = row_scale_f16(x)
+        a = moe_grouped("q4_k", "gu", tile_info, rowmap, x16, w_gate, FE, H, E, KU, w2=w_up, x_scales=xs,
+                        fused=fused, act=act)
+        a16, as_ = row_scale_f16(a, tile_info=tile_info)
+        ys = moe_grouped("q4_k", "dn", tile_info, rowmap, a16, w_down, H, FE, E, KU, x_scales=as_)
+    elif fmt == "mxfp4s":
+        x8, xs = quant_mxfp8(x)
+        a = moe_grouped("mxfp4s", "gu", tile_info, rowmap, x8, w_gate, FE, H, E, KU, w2=w_up, ws=ws_gate,
+                        ws2=ws_up, x_scales=xs, fused=fused, act=act)
+        a8, as8 = quant_mxfp8(a, tile_info=tile_info)
+        ys = moe_grouped("mxfp4s", "dn", tile_info, rowmap, a8, w_down, H, FE, E, KU, ws=ws_down, x_scales=as8)
+    else:
+        raise ValueError(f"no grouped path for {fmt}")
+    y = moe_combine(ys, wts, pos=pos)
+    return y, {"ids": ids, "wts": wts, "tile_info": tile_info, "rowmap": rowmap, "pos": pos, "act": a, "ys": ys}
+
+
+def moe_decode(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=None, ws_gate=None, ws_down=None,
+               ws_up=None, fused=False, act="silu", scale=1.0, bias=None):
+    """The reference's decode MoE chain (moe_routed with t < 64): route, per-assignment expert matvecs
+    (g_moe_gu_* then g_moe_dn_*), combine in assignment order. Returns (y f32 [T, H], intermediates dict)."""
+    ids, wts = moe_topk(logits, KU, gating, norm, scale=scale, bias=bias)
+    a = moe_expert_mv(fmt, "gu", ids, x, w_gate, FE, H, E, KU, w2=w_up, ws=ws_gate, ws2=ws_up, fused=fused, act=act)
+    ys = moe_expert_mv(fmt, "dn", ids, a, w_down, H, FE, E, KU, ws=ws_down)
+    y = moe_combine(ys, wts)
+    return y, {"ids": ids, "wts": wts, "act": a, "ys": ys}

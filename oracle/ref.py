@@ -98,15 +98,16 @@ def f16_rows(x):
 MX_BLOCK = 32
 
 
-def mxfp8_quantize(x):
-    """Per-32 MXFP8 (E4M3 elements, one E8M0 scale per 32 values along the last axis), the operand format of the
-    gfx950 scaled MFMA. Shared exponent s = clamp(floor(log2(amax)) - 7, -127, 127) so that every scaled element
-    lies below 256 and never saturates; elements are E4M3 round-to-nearest-even of x * 2^-s.
-    Returns (codes u8 [..., K], scale bytes u8 [..., K/32] = s + 127, values f64 [..., K])."""
+def mxfp8_quantize(x, block=MX_BLOCK):
+    """MXFP8 (E4M3 elements, one E8M0 scale per `block` values along the last axis, OCP MX: 32), the activation
+    operand format of the gfx950 scaled-MFMA path. Shared exponent s = clamp(floor(log2(amax)) - 7, -127, 127) so that every scaled element lies below 256
+    and never saturates; elements are E4M3 round-to-nearest-even of x * 2^-s (e4m3_round, restated from
+    make_kernel_tests.py:2006-2012). Returns (codes u8 [..., K], scale bytes u8 [..., K/block] = s + 127,
+    values f64 [..., K])."""
     x = np.asarray(x, np.float64)
     k = x.shape[-1]
-    assert k % MX_BLOCK == 0
-    g = x.reshape(x.shape[:-1] + (k // MX_BLOCK, MX_BLOCK))
+    assert k % block == 0
+    g = x.reshape(x.shape[:-1] + (k // block, block))
     amax = np.abs(g).max(-1)
     fl = np.frexp(amax)[1] - 1                    # floor(log2(amax)) for amax > 0
     s = np.where(amax > 0, np.clip(fl - 7, -127, 127), -127).astype(np.int64)

@@ -1,0 +1,174 @@
+"""GPU parity of the MoE chains (S/gen_llm.py:5324-5385 moe_routed): the prefill chain (top-k, bucket, grouped
+gate/up GEMM with the activation, grouped down GEMM, combine) in Q4_K (f16 MFMA) and MXFP4 (scaled f8f6f4 MFMA),
+and the decode chain (per-assignment expert matvecs).
+
+The oracle is the reference's experts_ref (make_kernel_tests.py:3197-3221) in float64 on exactly dequantized expert
+weights, with the activation rounding of the path under test applied to its inputs: the Q4_K prefill chain rounds
+the hidden rows and the expert activations with the f16 row scale (f16_rows, as the reference's own prefill case
+does, make_kernel_tests.py:3194-3196), the MXFP4 chain quantizes them to MXFP8 (E4M3 with one E8M0 per 32 values).
+Expert ids must match exactly, and the MoE output within rel-L2 1e-3. Shapes: the Qwen3-30B-A3B (128 experts, top-8,
+T = 64) and gpt-oss-20b (32 experts, top-4, T = 1 and 256) workloads, plus small shapes with an expert holding more
+than 64 rows, dead tokens and swiglu_oai; and the reference's grouped-GEMM-alone case (make_kernel_tests.py:
+3423-3500): hand-made tiles of 64, 37, 0 (expert -1) and 5 rows with inputs scaled by 0.05, 1 and 20.
+"""
+import numpy as np
+import pytest
+
+from helpers import assert_close_rel_l2, dev_bf16, dev_f32, dev_u8, host
+from oracle import formats as of
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    import qmm.ops as ops
+    return ops
+
+
+class Experts:
+    """Expert weights of one MoE layer: host bytes (GGUF blocks), device tensors and exact oracle dequantization."""
+
+    def __init__(self, dev, fmt, rng, E, H, FE, fused):
+        from qmm import synth
+        self.fmt, self.E, self.H, self.FE, self.fused = fmt, E, H, FE, fused
+        gen = synth.q4_k_weights if fmt == "q4_k" else synth.mxfp4_weights
+        if fused:
+            self.gu = gen(rng, E * 2 * FE, H)
+        else:
+            self.g, self.u = gen(rng, E * FE, H), gen(rng, E * FE, H)
+        self.d = gen(rng, E * H, FE)
+        self.dev = dev
+        self.gfmt = "q4_k" if fmt == "q4_k" else "mxfp4"
+
+    def rows(self, raw, r0, r1, k):
+        rb = of.row_bytes(self.gfmt, k)
+        return of.dequantize(self.gfmt, raw[r0 * rb:r1 * rb], r1 - r0, k)
+
+    def gate_up(self, e):
+        FE, H = self.FE, self.H
+        if self.fused:
+            return self.rows(self.gu, 2 * FE * e, 2 * FE * e + FE, H), self.rows(self.gu, 2 * FE * e + FE, 2 * FE * (e + 1), H)
+        return self.rows(self.g, FE * e, FE * (e + 1), H), self.rows(self.u, FE * e, FE * (e + 1), H)
+
+    def down(self, e):
+        return self.rows(self.d, self.H * e, self.H * (e + 1), self.FE)
+
+    def device(self, split):
+        """kwargs of ops.moe_prefill / moe_decode; split: MXFP4 as split planes (repacked on the device)."""
+        ops = _ops()
+        dv = lambda a: dev_u8(a, self.dev)
+        if self.fmt == "q4_k" or not split:
+            fmt = self.fmt if self.fmt == "q4_k" else "mxfp4"
+            kw = dict(w_gate=dv(self.gu if self.fused else self.g), w_down=dv(self.d))
+            if not self.fused:
+                kw["w_up"] = dv(self.u)
+            return fmt, kw
+        E, H, FE = self.E, self.H, self.FE
+        if self.fused:
+            gn, gs = ops.repack_mxfp4(dv(self.gu), E * 2 * FE, H)
+            kw = dict(w_gate=gn, ws_gate=gs)
+        else:
+            gn, gs = ops.repack_mxfp4(dv(self.g), E * FE, H)
+            un, us = ops.repack_mxfp4(dv(self.u), E * FE, H)
+            kw = dict(w_gate=gn, ws_gate=gs, w_up=un, ws_up=us)
+        dn, ds = ops.repack_mxfp4(dv(self.d), E * H, FE)
+        kw.update(w_down=dn, ws_down=ds)
+        return "mxfp4s", kw
+
+
+def _run_chain(dev, fmt, E, KU, H, FE, T, gating, norm, act, fused, prefill, seed, live_logits=None):
+    import torch
+    from qmm import synth
+    rng = np.random.default_rng(seed)
+    ex = Experts(dev, fmt, rng, E, H, FE, fused)
+    xb = synth.to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32))
+    logits = rng.standard_normal((T, E)).astype(np.float32) if live_logits is None else live_logits
+    wfmt, kw = ex.device(split=prefill)
+    chain = _ops().moe_prefill if prefill else _ops().moe_decode
+    y, mid = chain(wfmt, dev_bf16(xb, dev), dev_f32(logits, dev), E, KU, H, FE, gating, norm, fused=fused, act=act,
+                   **kw)
+    torch.cuda.synchronize()
+    ids = host(mid["ids"])
+    eids, ewts = ref.route(logits, KU, gating, norm)
+    np.testing.assert_array_equal(ids, eids)
+    np.testing.assert_allclose(host(mid["wts"]), ewts, atol=1e-5, rtol=1e-4)
+    x = synth.bf16_bits_to_f32(xb)
+    if not prefill:
+        rnd = None
+    elif fmt == "q4_k":
+        rnd = ref.f16_rows
+    else:
+        rnd = ref.mxfp8_values
+    want, _ = ref.moe(x, eids, ewts, ex.gate_up, ex.down, act=act, x_round=rnd, act_round=rnd)
+    return host(y), want, mid
+
+
+@pytest.mark.parametrize("prefill", [True, False])
+def test_q4_k_moe_qwen3_30b_a3b_shape(dev, prefill):
+    """128 experts, top-8 of softmax + normalize (gating 1), H = 2048, FE = 768, T = 64, SwiGLU."""
+    y, want, _ = _run_chain(dev, "q4_k", 128, 8, 2048, 768, 64, 1, True, "silu", False, prefill, seed=20261204)
+    assert_close_rel_l2(y, want, 1e-3, f"q4_k moe prefill={prefill}")
+
+
+@pytest.mark.parametrize("T,prefill", [(256, True), (1, False)])
+def test_mxfp4_moe_gpt_oss_20b_shape(dev, T, prefill):
+    """32 experts, top-4 with softmax over the picked logits (gating 3), H = FE = 2880, fused gate_up,
+    swiglu_oai; prefill quantizes activations to MXFP8 for the scaled MFMA, decode multiplies bf16 directly."""
+    y, want, _ = _run_chain(dev, "mxfp4", 32, 4, 2880, 2880, T, 3, False, "swiglu_oai", True, prefill,
+                            seed=20261203 + T)
+    assert_close_rel_l2(y, want, 1e-3, f"mxfp4 moe T={T}")
+
+
+@pytest.mark.parametrize("fmt,fused,act", [("q4_k", True, "swiglu_oai"), ("q4_k", False, "silu"),
+                                           ("mxfp4", False, "silu"), ("mxfp4", True, "swiglu_oai")])
+def test_moe_prefill_small_shapes_heavy_expert(dev, fmt, fused, act):
+    E, KU, H, FE, T = 8, 2, 512, 256 if fmt == "q4_k" else 320, 100
+    rng = np.random.default_rng(5)
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    logits[:80, 3] += 6.0                      # expert 3 gets more than 64 rows: two tiles
+    y, want, mid = _run_chain(dev, fmt, E, KU, H, FE, T, 1, True, act, fused, True, seed=11, live_logits=logits)
+    ti = host(mid["tile_info"])
+    assert (ti[:, 0] == 3).sum() == 2
+    assert_close_rel_l2(y, want, 1e-3, f"{fmt} small moe")
+
+
+def test_grouped_gemm_alone_hand_made_tiles(dev):
+    """dn mode on a hand-made tile table (make_kernel_tests.py:3423-3500): tiles of 64, 37, 0 (expert -1) and 5
+    rows on experts 0, E/2, -1, E-1; row groups scaled by 0.05, 1 and 20; dead rows must come out as zeros."""
+    import torch
+    from qmm import synth
+    ops = _ops()
+    rng = np.random.default_rng(17)
+    E, H, FE = 8, 512, 768
+    wd = synth.q4_k_weights(rng, E * H, FE)
+    tiles = [(0, 64), (E // 2, 37), (-1, 0), (E - 1, 5)]
+    n_tiles = len(tiles)
+    tile_info = np.array(tiles, np.int32)
+    rowmap = np.full(n_tiles * 64, -1, np.int32)
+    for t, (e, rows) in enumerate(tiles):
+        rowmap[64 * t: 64 * t + rows] = np.arange(rows) + 64 * t
+    a = rng.standard_normal((n_tiles * 64, FE)).astype(np.float32)
+    a *= np.repeat([0.05, 1.0, 20.0, 1.0], 64)[:, None].astype(np.float32)
+    a16, sc = ops.row_scale_f16(dev_f32(a, dev))
+    ys = host(ops.moe_grouped("q4_k", "dn", torch.from_numpy(tile_info).to(dev), torch.from_numpy(rowmap).to(dev),
+                              a16, dev_u8(wd, dev), H, FE, E, 1, x_scales=sc))
+    ar = ref.f16_rows(a)
+    for t, (e, rows) in enumerate(tiles):
+        blk = ys[64 * t: 64 * t + 64]
+        if e < 0:
+            continue                            # unused tiles are not written
+        Wd = of.dequant_q4_k(wd[e * H * (FE // 256 * 144):(e + 1) * H * (FE // 256 * 144)], H, FE)
+        want = ar[64 * t: 64 * t + rows] @ Wd.T
+        assert_close_rel_l2(blk[:rows], want, 1e-3, f"tile {t}")
+        assert np.all(blk[rows:] == 0), f"dead rows of tile {t} are not zero"
+
+
+def test_quant_mxfp8_matches_oracle(dev):
+    rng = np.random.default_rng(2)
+    x = (rng.standard_normal((64, 2880)) * np.exp(rng.uniform(-8, 8, (64, 1)))).astype(np.float32)
+    codes, scales = _ops().quant_mxfp8(dev_f32(x, dev))
+    ec, es, _ = ref.mxfp8_quantize(x)
+    np.testing.assert_array_equal(host(scales), es)
+    c = host(codes)
+    assert np.all(ref.e4m3_decode(c) == ref.e4m3_decode(ec))

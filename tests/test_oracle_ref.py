@@ -100,6 +100,9 @@ def test_mxfp8_exponent_choice():
     assert sc[0, 0] == 0 and np.all(codes[0, :32] == 0)
     assert np.array_equal(ref.e4m3_decode(codes).reshape(16, 8, 32) * 2.0 ** s[..., None], vals.reshape(16, 8, 32))
     assert ref.rel_l2(vals, x) < 0.04
+    c64, s64, v64 = ref.mxfp8_quantize(x, block=64)  # a coarser block shares the larger exponent
+    assert s64.shape == (16, 4) and np.all(s64 == np.maximum(sc[:, 0::2], sc[:, 1::2]))
+    assert ref.rel_l2(v64, x) < 0.04
 
 
 def test_row_scale_exponent():
