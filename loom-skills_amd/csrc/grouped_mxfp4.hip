@@ -24,6 +24,8 @@
 // a 256-column block. A step is one 64-value chunk: the tile's 64 activation rows (64 B each) and their scales are
 // staged in LDS, double-buffered, one barrier per step; the weights stream straight into registers DEPTH steps
 // ahead through register rings with unconditional (clamped) loads.
+#include <type_traits>
+
 #include "common.hpp"
 
 using namespace qmm;
@@ -38,6 +40,7 @@ static_assert(kDepth % 2 == 0, "the LDS double buffer follows the step parity");
 constexpr int BM = 64, KC = 64, APITCH = KC + 16;   // activation bytes per LDS row (80: 16-byte aligned rows)
 
 enum Kind { kGU = 1, kDN = 2 };
+typedef __attribute__((ext_vector_type(4))) u32 v4u;   // a native vector: the register rings stay in VGPRs
 
 struct MArgs {
   int N, K;
@@ -60,6 +63,16 @@ __device__ __forceinline__ float act_fn(int act, float g, float u) {
     return xg / (1.0f + expf(-1.702f * xg)) * (yu + 1.0f);
   }
   return g / (1.0f + expf(-g)) * u;
+}
+
+// f(integral_constant<I>) for I = 0 .. N-1, in order: ring slots as compile-time constants
+template <class F, int... I>
+__device__ __forceinline__ void for_slots(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <class F, int... I>
+__device__ __forceinline__ void for_steps(F &&f, int c0, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}, c0), ...);
 }
 
 template <int KIND, int DEPTH>
@@ -94,13 +107,12 @@ __global__ __launch_bounds__(256, 1) void mxfp4_grouped_kernel(MArgs a) {
   }
   __syncthreads();
 
-  // ---- activation staging: thread tid carries 16 bytes of row tid / 4 (and the row's two scale bytes when
-  // tid % 4 == 0)
+  // ---- activation staging: thread tid carries 16 bytes of row tid / 4 and the row's two scale bytes
   const int arow_i = tid >> 2, apart = tid & 3;
   const int asrc = src_row[arow_i] >= 0 ? src_row[arow_i] : 0;
   const u8 *acode = a.x8 + (int64_t)asrc * K + 16 * apart;
   const u16 *ascale = reinterpret_cast<const u16 *>(a.xs + (int64_t)asrc * (K / 32));
-  auto clampc = [&](int c) { return c < C ? c : C - 1; };
+  auto clampc = [&](int c) __attribute__((always_inline)) { return c < C ? c : C - 1; };
 
   // ---- weights: this lane's two columns and K half
   const int h = lane >> 5, lc = lane & 31;
@@ -131,66 +143,69 @@ __global__ __launch_bounds__(256, 1) void mxfp4_grouped_kernel(MArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  uint4 aring[DEPTH], bring[DEPTH][2];
+  v4u aring[DEPTH], bring[DEPTH][2];
   u32 asr[DEPTH], bsr[DEPTH][2];
-  auto load_a = [&](int slot, int c) {
+  auto load_a = [&](int slot, int c) __attribute__((always_inline)) {
     const int cc = clampc(c);
-    aring[slot] = *reinterpret_cast<const uint4 *>(acode + (int64_t)cc * KC);
+    aring[slot] = *reinterpret_cast<const v4u *>(acode + (int64_t)cc * KC);
     asr[slot] = ascale[cc];
   };
-  auto load_b = [&](int slot, int c) {
+  auto load_b = [&](int slot, int c) __attribute__((always_inline)) {
     const int cc = clampc(c);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      bring[slot][j] = *reinterpret_cast<const uint4 *>(wcn[j] + (int64_t)cc * 32);
+      bring[slot][j] = *reinterpret_cast<const v4u *>(wcn[j] + (int64_t)cc * 32);
       bsr[slot][j] = wcs[j][2 * cc];
     }
   };
-  auto stage = [&](int slot, int buf) {
-    *reinterpret_cast<uint4 *>(&As[buf][arow_i][16 * apart]) = aring[slot];
-    if (apart == 0) Ass[buf][arow_i] = (u16)asr[slot];
+  auto stage = [&](int slot, int buf) __attribute__((always_inline)) {
+    *reinterpret_cast<v4u *>(&As[buf][arow_i][16 * apart]) = aring[slot];
+    Ass[buf][arow_i] = (u16)asr[slot];   // the row's four threads write the same value: no branch
   };
   load_a(0, 0);
   stage(0, 0);
-#pragma unroll
-  for (int u = 1; u <= DEPTH; ++u) load_a(u % DEPTH, u);
-#pragma unroll
-  for (int u = 0; u < DEPTH; ++u) load_b(u, u);
+  for_slots([&](auto uc) { constexpr int u = decltype(uc)::value; load_a((u + 1) % DEPTH, u + 1); },
+            std::make_integer_sequence<int, DEPTH>{});
+  for_slots([&](auto uc) { constexpr int u = decltype(uc)::value; load_b(u, u); },
+            std::make_integer_sequence<int, DEPTH>{});
   __syncthreads();
 
-  const int CP = (C + DEPTH - 1) / DEPTH * DEPTH;
-  for (int c0 = 0; c0 < CP; c0 += DEPTH) {
+  // The chunk count is rounded up to a multiple of DEPTH. A padding chunk (c >= C) runs with both E8M0 scales 0:
+  // its products are at most 448 * 6 * 2^-254, far below the smallest f32 subnormal, so they add exactly zero.
+  // The loop body thus has no data-dependent branch; each step is instantiated with its ring slot as a constant
+  // (integral_constant), so the rings stay in registers.
+  auto step = [&](auto uc, int c0) __attribute__((always_inline)) {
+    constexpr int u = decltype(uc)::value;
+    constexpr int nx = (u + 1) % DEPTH;
+    constexpr int buf = u & 1;
+    const int c = c0 + u;
+    const bool live = c < C;
+    i32x8 af[2];
+    int sa[2];
 #pragma unroll
-    for (int u = 0; u < DEPTH; ++u) {
-      const int c = c0 + u;
-      const int buf = u & 1;
-      if (c < C) {
-        i32x8 af[2];
-        int sa[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const uint4 v0 = *reinterpret_cast<const uint4 *>(&As[buf][32 * i + lc][16 * h]);
-          const uint4 v1 = *reinterpret_cast<const uint4 *>(&As[buf][32 * i + lc][32 + 16 * h]);
-          af[i] = i32x8{(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w, (int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w};
-          sa[i] = (Ass[buf][32 * i + lc] >> (8 * h)) & 0xFF;
-        }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const i32x8 bf = i32x8{(int)bring[u][j].x, (int)bring[u][j].y, (int)bring[u][j].z, (int)bring[u][j].w,
-                                 0, 0, 0, 0};
-#pragma unroll
-          for (int i = 0; i < 2; ++i)
-            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[i], bf, acc[i][j], 0, 4, 0, sa[i], 0,
-                                                                        (int)bsr[u][j]);
-        }
-      }
-      load_b(u, c + DEPTH);
-      const int nx = (u + 1) % DEPTH;
-      stage(nx, buf ^ 1);
-      load_a(nx, c + 1 + DEPTH);
-      __syncthreads();
+    for (int i = 0; i < 2; ++i) {
+      const v4u v0 = *reinterpret_cast<const v4u *>(&As[buf][32 * i + lc][16 * h]);
+      const v4u v1 = *reinterpret_cast<const v4u *>(&As[buf][32 * i + lc][32 + 16 * h]);
+      af[i] = i32x8{(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w, (int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w};
+      sa[i] = live ? (Ass[buf][32 * i + lc] >> (8 * h)) & 0xFF : 0;
     }
-  }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const i32x8 bf = i32x8{(int)bring[u][j].x, (int)bring[u][j].y, (int)bring[u][j].z, (int)bring[u][j].w,
+                             0, 0, 0, 0};
+      const int sb = live ? (int)bsr[u][j] : 0;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[i], bf, acc[i][j], 0, 4, 0, sa[i], 0, sb);
+    }
+    load_b(u, c + DEPTH);
+    stage(nx, buf ^ 1);
+    load_a(nx, c + 1 + DEPTH);
+    __syncthreads();
+  };
+  const int CP = (C + DEPTH - 1) / DEPTH * DEPTH;
+  for (int c0 = 0; c0 < CP; c0 += DEPTH)
+    for_steps(step, c0, std::make_integer_sequence<int, DEPTH>{});
 
   if constexpr (KIND == kGU) {
     if (mat == 1) {

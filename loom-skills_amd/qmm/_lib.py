@@ -4,7 +4,7 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libqmm.so")
+LIB_PATH = os.environ.get("QMM_LIB", os.path.join(HERE, "libqmm.so"))   # QMM_LIB: another build of the library
 
 c_i64, c_int, c_float, c_vp = ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_void_p
 

@@ -27,30 +27,33 @@ def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
-def _compile(src):
-    obj = os.path.join(OBJ, os.path.basename(src)[:-4] + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+def _compile(src, obj_dir=OBJ, defines=()):
+    obj = os.path.join(obj_dir, os.path.basename(src)[:-4] + ".o")
+    cmd = [HIPCC, *FLAGS, *[f"-D{d}" for d in defines], "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stderr}")
     return obj
 
 
-def build(verbose=False):
-    """Compiles every HIP source (in parallel) and links libqmm.so; returns the library path."""
-    os.makedirs(OBJ, exist_ok=True)
+def build(verbose=False, lib=LIB, defines=()):
+    """Compiles every HIP source (in parallel) and links the library (libqmm.so next to this file unless `lib`
+    names another path; `defines` are extra -D macros, e.g. a kernel's tuning knob); returns the library path."""
+    obj_dir = OBJ if lib == LIB else lib + ".objs"
+    os.makedirs(obj_dir, exist_ok=True)
     srcs = sources()
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = LIB + ".tmp"
+        objs = list(ex.map(lambda s: _compile(s, obj_dir, defines), srcs))
+    LIB_ = lib
+    tmp = LIB_ + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode:
         raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, LIB_)
     if verbose:
-        print(f"built {LIB} from {len(srcs)} sources")
-    return LIB
+        print(f"built {LIB_} from {len(srcs)} sources")
+    return LIB_
 
 
 if __name__ == "__main__":
