@@ -232,3 +232,26 @@ def moe_decode(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=
     ys = moe_expert_mv(fmt, "dn", ids, a, w_down, H, FE, E, KU, ws=ws_down)
     y = moe_combine(ys, wts)
     return y, {"ids": ids, "wts": wts, "act": a, "ys": ys}
+
+
+# ---------------------------------------------------------------------------------------------------- dispatch
+GEMM_MIN_TOKENS = 64   # %gemm: epochs of 64+ tokens take the GEMM / grouped chain (S/gen_llm.py:6107-6126)
+
+
+def linear(fmt, x, w, n, k, y=None, mode="store", ws=None):
+    """Projection y (+)= x W^T with the reference's per-epoch choice (linear, S/gen_llm.py:4568-4625): the prefill
+    GEMM for 64+ tokens (Q4_K; the activation is row-scaled to f16 first), else the decode GEMV. y is f32."""
+    if mode not in ("store", "acc"):
+        raise ValueError(f"linear mode {mode}")
+    if x.shape[0] >= GEMM_MIN_TOKENS and fmt == "q4_k":
+        return gemm(fmt, mode, x, w, n, k, y=y)
+    return mv(fmt, w, x, n, k, y=y, accumulate=mode == "acc", ws=ws)
+
+
+def moe_routed(fmt, x, logits, E, KU, H, FE, gating, norm, **kw):
+    """The routed experts of one MoE layer (moe_routed, S/gen_llm.py:5324-5385): the grouped prefill chain for 64+
+    tokens, the per-assignment decode chain below. Returns (y f32 [T, H], intermediates dict)."""
+    chain = moe_prefill if x.shape[0] >= GEMM_MIN_TOKENS else moe_decode
+    if chain is moe_decode and fmt == "mxfp4s" and "w_gate" in kw and kw.get("ws_gate") is None:
+        raise ValueError("mxfp4s weights need their scale planes")
+    return chain(fmt, x, logits, E, KU, H, FE, gating, norm, **kw)
