@@ -13,6 +13,7 @@ A step is one launch of the hot path over one batch of synthetic input:
                 (--m, default 256): top-k, bucket, MXFP8 quantize, grouped gate_up (scaled MFMA) + swiglu_oai,
                 quantize, grouped down, combine
     q4_k_moe    Q4_K MoE prefill chain at the Qwen3-30B-A3B shape (128 experts, top-8, H = 2048, FE = 768), T = 64
+    hbm_copy    calibration: a 256 MiB device copy, whose counter readings scale FETCH_SIZE / WRITE_SIZE to bytes
 
 Consecutive steps read different copies of the weight (more than 300 MB in rotation), so the 256 MB MALL cannot
 serve them and the figure is an HBM figure. The K timed steps are captured in one HIP graph and replayed on the
@@ -127,7 +128,7 @@ class GemmWorkload:
     """Q4_K prefill GEMM: one step = row-scale bf16 x to f16 + the GEMM (bf16 out) on the next weight copy."""
     metric, unit, bound = "Q4_K prefill GEMM TFLOP/s (Qwen3-8B o_proj, 512 x 4096 x 4096)", "TFLOP/s", "mfma"
     peak_key = "fp16"
-    name, traffic_name = "q4_k_gemm", "q4k_gemm_traffic"
+    name, traffic_name = "q4_k_gemm", "q4k_mfma_kernel_dense.q4_k_gemm_m512_n4096_k4096"
 
     def __init__(self, m):
         self.m, self.n, self.k = m or 512, 4096, 4096
@@ -193,11 +194,11 @@ class MoeWorkload:
         if index == 3:
             self.T = m or 256
             self.metric = METRIC
-            self.traffic_name = f"mxfp4_moe_t{self.T}_traffic"
+            self.traffic_name = f"mxfp4_grouped_kernel_gu.mxfp4_moe_gpt_oss_20b_t{self.T}"
         else:
             self.T = m or 64
             self.metric = "Q4_K MoE prefill TFLOP/s (Qwen3-30B-A3B, 128 experts, top-8, T = 64)"
-            self.traffic_name = f"q4k_moe_t{self.T}_traffic"
+            self.traffic_name = f"q4k_mfma_kernel_gu.q4_k_moe_qwen3_30b_a3b_t{self.T}"
 
     def setup(self, dev):
         import torch
@@ -315,16 +316,64 @@ class MoeWorkload:
                 "experts_hit": self.experts_hit}
 
 
+class CopyWorkload:
+    """Calibration: a plain device-to-device copy of a known size (256 MiB, torch's copy kernel). Its FETCH_SIZE and
+    WRITE_SIZE counter readings against the bytes it must move give the factors that turn those counters into HBM
+    bytes for the other kernels."""
+    metric, unit, bound = "HBM copy GB/s (counter calibration)", "GB/s", "hbm"
+    name, traffic_name, kernel_step = "hbm_copy", "copy.hbm_copy_256mib", None
+
+    def __init__(self, m):
+        self.nbytes = (m or 256) * 2 ** 20
+
+    def setup(self, dev):
+        import torch
+        self.src = [torch.randint(0, 255, (self.nbytes,), dtype=torch.uint8, device=dev) for _ in range(2)]
+        self.dst = torch.empty_like(self.src[0])
+
+    def step(self, i):
+        self.dst.copy_(self.src[i % 2])
+
+    def value(self, sec):
+        return self.alg_bytes() / sec / 1e9
+
+    def dtype(self):
+        return "u8"
+
+    def alg_bytes(self):
+        return 2 * self.nbytes
+
+    def alg_flops(self):
+        return 0
+
+    def cpu_baseline(self, budget):
+        a = np.ones(self.nbytes // 4, np.uint8)
+        b = np.empty_like(a)
+        t0, runs = time.perf_counter(), 0
+        while runs < 3 or time.perf_counter() - t0 < min(budget, 2.0):
+            np.copyto(b, a)
+            runs += 1
+        sec = (time.perf_counter() - t0) / runs
+        return {"value": round(2 * a.nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"{runs} numpy copies of {a.nbytes >> 20} MiB"}
+
+    def config(self):
+        return {"workload": self.name, "bytes": self.nbytes}
+
+
 def _q4k_gemv(m):
-    return GemvWorkload("q4_k_gemv", 1, "q4_k", 12288, 4096, m or 1, "bf16", f"q4k_gemv_m{m or 1}_traffic")
+    return GemvWorkload("q4_k_gemv", 1, "q4_k", 12288, 4096, m or 1, "bf16",
+                        f"mv_q4k_kernel.q4_k_gemv_n12288_k4096_m{m or 1}")
 
 
 def _q40_gemv(m):
-    return GemvWorkload("q4_0_gemv", 0, "q4_0", 4096, 4096, m or 1, "f32", f"q40_gemv_m{m or 1}_traffic")
+    return GemvWorkload("q4_0_gemv", 0, "q4_0", 4096, 4096, m or 1, "f32",
+                        f"mv_kernel_q4_0.q4_0_gemv_n4096_k4096_m{m or 1}")
 
 
 WORKLOADS = {"q4_k_gemv": _q4k_gemv, "q4_0_gemv": _q40_gemv, "q4_k_gemm": GemmWorkload,
-             "mxfp4_moe": lambda m: MoeWorkload("mxfp4_moe", 3, m), "q4_k_moe": lambda m: MoeWorkload("q4_k_moe", 4, m)}
+             "mxfp4_moe": lambda m: MoeWorkload("mxfp4_moe", 3, m), "q4_k_moe": lambda m: MoeWorkload("q4_k_moe", 4, m),
+             "hbm_copy": CopyWorkload}
 
 
 # ---------------------------------------------------------------------------------------------------- main
