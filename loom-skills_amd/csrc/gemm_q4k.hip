@@ -108,18 +108,23 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
   __shared__ int src_row[BM];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int sel = wave & 1, kh = wave >> 1;   // sel: N-half (dense, dn) or matrix (gu: 0 gate, 1 up)
-  const int per = (int)(gridDim.x / 8);
-  const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
-  if (t >= a.tiles_total) return;
   const int M = a.M, N = a.N, K = a.K;
 
   int m0, n0, expert = 0;
   if constexpr (KIND == kDense) {
+    // XCD-aware order: workgroup b runs on XCD b % 8, which gets a contiguous range of tiles
+    const int per = (int)(gridDim.x / 8);
+    const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+    if (t >= a.tiles_total) return;
     m0 = (t % a.tiles_m) * BM;
     n0 = (t / a.tiles_m) * BN;
   } else {
-    const int tile = t / a.n_blocks;
-    n0 = (t % a.n_blocks) * BN;
+    // expert tiles dealt to the XCDs round-robin: the bucket writes the live tiles first, so a contiguous range per
+    // XCD would leave the XCDs holding the trailing unused tiles idle; a tile's column blocks share one XCD's L2
+    const int xcd = (int)(blockIdx.x & 7), xi = (int)(blockIdx.x >> 3);
+    const int tile = xcd + 8 * (xi / a.n_blocks);
+    if (tile >= a.tiles_m) return;
+    n0 = (xi % a.n_blocks) * BN;
     m0 = tile * BM;
     expert = a.tile_info[2 * tile];
     if (expert < 0) return;
@@ -335,7 +340,7 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
 
 template <int KIND, bool ACC, bool BF16OUT>
 int launch(const Args &a, hipStream_t s) {
-  const dim3 grid((unsigned)(8 * ((a.tiles_total + 7) / 8)));
+  const dim3 grid((unsigned)(KIND == kDense ? 8 * ((a.tiles_total + 7) / 8) : 8 * a.n_blocks * ((a.tiles_m + 7) / 8)));
   q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth><<<grid, 256, 0, s>>>(a);
   return launch_status();
 }
@@ -386,11 +391,13 @@ int qmm_grouped_q4k(int mode, int fused, int act, int64_t max_tiles, int64_t k, 
     a.up_off = fused ? RB * n : 0;
     a.w2 = fused ? nullptr : static_cast<const u8 *>(w2);
     a.n_blocks = (int)((n + 63) / 64);
+    a.tiles_m = (int)max_tiles;
     a.tiles_total = (int)max_tiles * a.n_blocks;
     return launch<kGU, false, false>(a, s);
   }
   a.ebytes = RB * n;
   a.n_blocks = (int)((n + 127) / 128);
+  a.tiles_m = (int)max_tiles;
   a.tiles_total = (int)max_tiles * a.n_blocks;
   return launch<kDN, false, false>(a, s);
 }

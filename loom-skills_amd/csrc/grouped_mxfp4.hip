@@ -18,10 +18,13 @@
 // 16h .. 16h+15 in bytes 0..15 and 32+16h .. 32+16h+15 in bytes 16..31, and its scale is the one of block h; both
 // operands therefore see the same two 32-value blocks per chunk.
 //
-// Tiling: a workgroup of four waves owns one 64-row expert tile; each wave computes 64 rows x 64 columns
-// (2 x 2 MFMA blocks) over all of K. gu: waves (mat, nh) = gate / up x two 64-column halves of a 128-column block;
-// the up waves hand their results to the gate waves through LDS for the activation. dn: four 64-column quarters of
-// a 256-column block. A step is one 64-value chunk: the tile's 64 activation rows (64 B each) and their scales are
+// Tiling: a workgroup of four waves owns one 64-row expert tile; each wave computes 64 rows x 64 weight columns
+// (2 x 2 MFMA blocks) over all of K. gu: wave w owns output columns 32 w .. 32 w + 31 of a 128-column block, its
+// two column blocks being those columns of the gate and of the up matrix, so the activation is applied in
+// registers. dn: four 64-column quarters of a 256-column block. Tiles are dealt to the eight XCDs round-robin
+// (workgroup b runs on XCD b % 8): the bucket writes the live tiles first, and a tile-major order would leave
+// the XCDs that get the trailing, unused tiles idle; a tile's column blocks stay on one XCD, sharing its
+// activation rows in that L2. A step is one 64-value chunk: the tile's 64 activation rows (64 B each) and their scales are
 // staged in LDS, double-buffered, one barrier per step; the weights stream straight into registers DEPTH steps
 // ahead through register rings with unconditional (clamped) loads.
 #include <type_traits>
@@ -33,7 +36,10 @@ using namespace qmm;
 namespace {
 
 #ifndef QMM_MX_DEPTH
-#define QMM_MX_DEPTH 4
+#define QMM_MX_DEPTH 2
+#endif
+#ifndef QMM_MX_WAVES
+#define QMM_MX_WAVES 3            // minimum waves per SIMD the register allocation must allow (3 workgroups per CU)
 #endif
 constexpr int kDepth = QMM_MX_DEPTH;
 static_assert(kDepth % 2 == 0, "the LDS double buffer follows the step parity");
@@ -53,7 +59,7 @@ struct MArgs {
   const int32_t *tile_info, *rowmap;
   int KU, E, act;
   float *y;
-  int n_blocks, tiles_total;
+  int n_blocks, max_tiles;
 };
 
 __device__ __forceinline__ float act_fn(int act, float g, float u) {
@@ -76,23 +82,20 @@ __device__ __forceinline__ void for_steps(F &&f, int c0, std::integer_sequence<i
 }
 
 template <int KIND, int DEPTH>
-__global__ __launch_bounds__(256, 1) void mxfp4_grouped_kernel(MArgs a) {
+__global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs a) {
   constexpr int BN = KIND == kGU ? 128 : 256;
   __shared__ __align__(16) u8 As[2][BM][APITCH];
   __shared__ u16 Ass[2][BM];   // the row's two E8M0 scales of the chunk (block 2c in the low byte)
   __shared__ int src_row[BM];
-  __shared__ __align__(16) float red[2][16 * 4][64];   // gu: the up waves' results, [nh][value][lane]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int per = (int)(gridDim.x / 8);
-  const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
-  if (t >= a.tiles_total) return;
+  const int xcd = (int)(blockIdx.x & 7), xi = (int)(blockIdx.x >> 3);
+  const int tile = xcd + 8 * (xi / a.n_blocks);
+  if (tile >= a.max_tiles) return;
   const int N = a.N, K = a.K, C = K / KC;
-  const int tile = t / a.n_blocks, n0 = (t % a.n_blocks) * BN, m0 = tile * BM;
+  const int n0 = (xi % a.n_blocks) * BN, m0 = tile * BM;
   int expert = a.tile_info[2 * tile];
   if (expert < 0) return;
   expert = expert >= a.E ? a.E - 1 : expert;
-  const int mat = KIND == kGU ? wave >> 1 : 0;   // gu: 0 gate, 1 up
-  const int nq = KIND == kGU ? wave & 1 : wave;   // 64-column slice of the block
 
   if (tid < BM) {
     int src;
@@ -114,25 +117,28 @@ __global__ __launch_bounds__(256, 1) void mxfp4_grouped_kernel(MArgs a) {
   const u16 *ascale = reinterpret_cast<const u16 *>(a.xs + (int64_t)asrc * (K / 32));
   auto clampc = [&](int c) __attribute__((always_inline)) { return c < C ? c : C - 1; };
 
-  // ---- weights: this lane's two columns and K half
+  // ---- weights: this lane's two columns (gu: one column of the gate and of the up matrix) and K half
   const int h = lane >> 5, lc = lane & 31;
-  const u8 *nb, *sb;
+  const u8 *nbj[2], *sbj[2];
+  int colj[2];
   if constexpr (KIND == kGU) {
     const u8 *gn = a.wn + (int64_t)expert * a.nib_ebytes, *gs = a.wsc + (int64_t)expert * a.sc_ebytes;
-    if (mat == 0) { nb = gn; sb = gs; }
-    else if (a.wn2) { nb = a.wn2 + (int64_t)expert * a.nib_ebytes; sb = a.wsc2 + (int64_t)expert * a.sc_ebytes; }
-    else { nb = gn + a.up_nib_off; sb = gs + a.up_sc_off; }
+    nbj[0] = gn; sbj[0] = gs;
+    if (a.wn2) { nbj[1] = a.wn2 + (int64_t)expert * a.nib_ebytes; sbj[1] = a.wsc2 + (int64_t)expert * a.sc_ebytes; }
+    else { nbj[1] = gn + a.up_nib_off; sbj[1] = gs + a.up_sc_off; }
+    colj[0] = colj[1] = n0 + 32 * wave + lc;
   } else {
-    nb = a.wn + (int64_t)expert * a.nib_ebytes;
-    sb = a.wsc + (int64_t)expert * a.sc_ebytes;
+    nbj[0] = nbj[1] = a.wn + (int64_t)expert * a.nib_ebytes;
+    sbj[0] = sbj[1] = a.wsc + (int64_t)expert * a.sc_ebytes;
+    colj[0] = n0 + 64 * wave + lc;
+    colj[1] = colj[0] + 32;
   }
   const u8 *wcn[2], *wcs[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    int col = n0 + 64 * nq + 32 * j + lc;
-    col = col < N ? col : N - 1;
-    wcn[j] = nb + (int64_t)col * (K / 2) + 16 * h;
-    wcs[j] = sb + (int64_t)col * (K / 32) + h;
+    const int col = colj[j] < N ? colj[j] : N - 1;
+    wcn[j] = nbj[j] + (int64_t)col * (K / 2) + 16 * h;
+    wcs[j] = sbj[j] + (int64_t)col * (K / 32) + h;
   }
 
   f32x16 acc[2][2];
@@ -207,31 +213,19 @@ __global__ __launch_bounds__(256, 1) void mxfp4_grouped_kernel(MArgs a) {
   for (int c0 = 0; c0 < CP; c0 += DEPTH)
     for_steps(step, c0, std::make_integer_sequence<int, DEPTH>{});
 
-  if constexpr (KIND == kGU) {
-    if (mat == 1) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) red[nq][(i * 2 + j) * 16 + r][lane] = acc[i][j][r];
-    }
-    __syncthreads();
-    if (mat == 1) return;
-  }
-
+  constexpr int NJ = KIND == kGU ? 1 : 2;   // gu: one output column per lane (gate j = 0, up j = 1)
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int lr = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-        const int col = n0 + 64 * nq + 32 * j + lc;
+        const int col = colj[j];
         if (col >= N) continue;
         float v = 0.f;
         if (src_row[lr] >= 0) {
-          if constexpr (KIND == kGU) v = act_fn(a.act, acc[i][j][r], red[nq][(i * 2 + j) * 16 + r][lane]);
+          if constexpr (KIND == kGU) v = act_fn(a.act, acc[i][0][r], acc[i][1][r]);
           else v = acc[i][j][r];
         }
         a.y[(int64_t)(m0 + lr) * N + col] = v;
@@ -240,7 +234,7 @@ __global__ __launch_bounds__(256, 1) void mxfp4_grouped_kernel(MArgs a) {
 
 template <int KIND>
 int launch(const MArgs &a, hipStream_t s) {
-  const dim3 grid((unsigned)(8 * ((a.tiles_total + 7) / 8)));
+  const dim3 grid((unsigned)(8 * a.n_blocks * ((a.max_tiles + 7) / 8)));
   mxfp4_grouped_kernel<KIND, kDepth><<<grid, 256, 0, s>>>(a);
   return launch_status();
 }
@@ -271,12 +265,12 @@ int qmm_grouped_mxfp4(int mode, int fused, int act, int64_t max_tiles, int64_t k
     a.wn2 = fused ? nullptr : static_cast<const u8 *>(w2);
     a.wsc2 = fused ? nullptr : static_cast<const u8 *>(ws2);
     a.n_blocks = (int)((n + 127) / 128);
-    a.tiles_total = (int)max_tiles * a.n_blocks;
+    a.max_tiles = (int)max_tiles;
     return launch<kGU>(a, s);
   }
   a.nib_ebytes = nrow * n;
   a.sc_ebytes = srow * n;
   a.n_blocks = (int)((n + 255) / 256);
-  a.tiles_total = (int)max_tiles * a.n_blocks;
+  a.max_tiles = (int)max_tiles;
   return launch<kDN>(a, s);
 }

@@ -81,6 +81,7 @@ def _mv_case(dev, fmt, n, k, m, x_dtype, seed=11):
     ("q4_k", 12288, 4096, 8, "bf16"),
     ("q4_0", 4096, 4096, 1, "f32"),       # the Q4_0 GEMV workload
     ("q4_k", 37, 768, 3, "f32"),          # 3 super-blocks, rows that do not fill a wave, partial token group
+    ("q4_k", 101, 4096, 3, "bf16"),       # rows that fill no four-row group or workgroup, odd token count
     ("q4_k", 50, 8192, 5, "bf16"),        # 32 super-blocks: two passes per row
     ("q4_0", 21, 4096, 2, "bf16"),
     ("mxfp4", 45, 2880, 1, "bf16"),       # GGUF 17-byte blocks, 90 per row
@@ -106,11 +107,12 @@ def test_mv_mxfp4s_split_planes(dev):
     torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("fmt,xd", [("q4_k", "bf16"), ("q4_k", "f32"), ("q4_0", "bf16"), ("mxfp4", "bf16")])
-def test_mv_multi_token_equals_single_token(dev, fmt, xd):
+@pytest.mark.parametrize("fmt,xd,k", [("q4_k", "bf16", 2048), ("q4_k", "bf16", 4096), ("q4_k", "bf16", 8192),
+                                      ("q4_k", "f32", 2048), ("q4_0", "bf16", 2048), ("mxfp4", "bf16", 2880)])
+def test_mv_multi_token_equals_single_token(dev, fmt, xd, k):
     """A token's result does not depend on the token count of the call (make_kernel_tests.py:264-268)."""
     import torch
-    n, k, m = 96, 2048 if fmt != "mxfp4" else 2880, 8
+    n, m = 100, 7
     y, _, w, _, xt = _mv_case(dev, fmt, n, k, m, xd, seed=3)
     wt = dev_u8(w, dev)
     ops = _qmm()
@@ -120,17 +122,39 @@ def test_mv_multi_token_equals_single_token(dev, fmt, xd):
     torch.cuda.synchronize()
 
 
-def test_mv_accumulate(dev):
+@pytest.mark.parametrize("xd", ["f32", "bf16"])
+def test_mv_accumulate(dev, xd):
     import torch
+    from qmm.synth import to_bf16_bits
     rng = np.random.default_rng(9)
     n, k = 64, 4096
     w = _weights("q4_k", rng, n, k)
     x = rng.standard_normal((2, k)).astype(np.float32)
+    if xd == "bf16":
+        xb = to_bf16_bits(x)
+        x, xt = bf16_values(xb), dev_bf16(xb, dev)
+    else:
+        xt = dev_f32(x, dev)
     y0 = rng.standard_normal((2, n)).astype(np.float32)
     yt = dev_f32(y0, dev)
-    _qmm().mv("q4_k", dev_u8(w, dev), dev_f32(x, dev), n, k, y=yt, accumulate=True)
+    _qmm().mv("q4_k", dev_u8(w, dev), xt, n, k, y=yt, accumulate=True)
     e = y0 + ref.gemv(x, of.dequant_q4_k(w, n, k))
     assert_close_rel_l2(host(yt), e, 1e-6 + 1e-3, "accumulate")
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("scale", [2.0 ** 20, 2.0 ** -30])
+def test_mv_bf16_activation_range(dev, scale):
+    """bf16 activations far outside the f16 range (2^20 x, 2^-30 x) through the Q4_K fast path: the kernel rescales
+    each token by a power of two before its f16 staging, so results match the oracle as for unit-scale inputs."""
+    import torch
+    from qmm.synth import to_bf16_bits
+    rng = np.random.default_rng(4)
+    n, k, m = 96, 4096, 2
+    w = _weights("q4_k", rng, n, k)
+    xb = to_bf16_bits((rng.standard_normal((m, k)) * scale).astype(np.float32))
+    y = host(_qmm().mv("q4_k", dev_u8(w, dev), dev_bf16(xb, dev), n, k))
+    assert_close_rel_l2(y, ref.gemv(bf16_values(xb), of.dequant_q4_k(w, n, k)), 1e-3, f"scale {scale}")
     torch.cuda.synchronize()
 
 
