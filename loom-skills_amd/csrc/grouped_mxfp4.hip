@@ -24,9 +24,13 @@
 // registers. dn: four 64-column quarters of a 256-column block. Tiles are dealt to the eight XCDs round-robin
 // (workgroup b runs on XCD b % 8): the bucket writes the live tiles first, and a tile-major order would leave
 // the XCDs that get the trailing, unused tiles idle; a tile's column blocks stay on one XCD, sharing its
-// activation rows in that L2. A step is one 64-value chunk: the tile's 64 activation rows (64 B each) and their scales are
-// staged in LDS, double-buffered, one barrier per step; the weights stream straight into registers DEPTH steps
-// ahead through register rings with unconditional (clamped) loads.
+// activation rows in that L2.
+//
+// Steps. All E8M0 scales of the workgroup (its 64 activation rows and 128 + 128 or 256 weight columns, K / 32
+// bytes each) are staged in LDS once; per-step byte loads of scales through the vector memory path cost more than
+// the weight stream. A super-step covers kSub 64-value chunks: the tile's activation codes for it are staged in
+// LDS (double-buffered, one barrier per super-step) and the weights stream straight into registers one super-step
+// ahead, kSub consecutive 32-byte chunks of a column issued back to back.
 #include <type_traits>
 
 #include "common.hpp"
@@ -36,14 +40,17 @@ using namespace qmm;
 namespace {
 
 #ifndef QMM_MX_DEPTH
-#define QMM_MX_DEPTH 2
+#define QMM_MX_DEPTH 1
 #endif
 #ifndef QMM_MX_WAVES
 #define QMM_MX_WAVES 3            // minimum waves per SIMD the register allocation must allow (3 workgroups per CU)
 #endif
 constexpr int kDepth = QMM_MX_DEPTH;
-static_assert(kDepth % 2 == 0, "the LDS double buffer follows the step parity");
-constexpr int BM = 64, KC = 64, APITCH = KC + 16;   // activation bytes per LDS row (80: 16-byte aligned rows)
+#ifndef QMM_MX_SUB
+#define QMM_MX_SUB 2
+#endif
+constexpr int kSub = QMM_MX_SUB;                      // 64-value chunks per super-step (one barrier each)
+constexpr int BM = 64, KC = 64, APITCH = kSub * KC + 16;   // activation bytes per LDS row (16-byte aligned rows)
 
 enum Kind { kGU = 1, kDN = 2 };
 typedef __attribute__((ext_vector_type(4))) u32 v4u;   // a native vector: the register rings stay in VGPRs
@@ -81,12 +88,28 @@ __device__ __forceinline__ void for_steps(F &&f, int c0, std::integer_sequence<i
   (f(std::integral_constant<int, I>{}, c0), ...);
 }
 
+// copies n bytes from global memory to LDS with the widest loads the alignment of both allows
+__device__ __forceinline__ void copy_to_lds(u8 *dst, const u8 *src, int64_t n, int tid) {
+  const uintptr_t al = reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) | (uintptr_t)n;
+  if ((al & 15) == 0) {
+    for (int64_t i = tid; i < n / 16; i += 256) reinterpret_cast<v4u *>(dst)[i] = reinterpret_cast<const v4u *>(src)[i];
+  } else if ((al & 3) == 0) {
+    for (int64_t i = tid; i < n / 4; i += 256) reinterpret_cast<u32 *>(dst)[i] = reinterpret_cast<const u32 *>(src)[i];
+  } else {
+    for (int64_t i = tid; i < n; i += 256) dst[i] = src[i];
+  }
+}
+
 template <int KIND, int DEPTH>
 __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs a) {
   constexpr int BN = KIND == kGU ? 128 : 256;
   __shared__ __align__(16) u8 As[2][BM][APITCH];
-  __shared__ u16 Ass[2][BM];   // the row's two E8M0 scales of the chunk (block 2c in the low byte)
   __shared__ int src_row[BM];
+  // Every E8M0 scale the workgroup needs, staged once: the tile's 64 activation rows and the block's weight columns
+  // (gu: 128 gate then 128 up columns; dn: 256 columns), K / 32 bytes each. Per-step byte loads of scales through
+  // the vector memory path (32 rows per instruction) would otherwise cost more than the weight stream itself.
+  extern __shared__ __align__(16) u8 dyn_lds[];
+  u8 *Asc = dyn_lds, *Wsc = dyn_lds + BM * (a.K / 32);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int xcd = (int)(blockIdx.x & 7), xi = (int)(blockIdx.x >> 3);
   const int tile = xcd + 8 * (xi / a.n_blocks);
@@ -110,12 +133,13 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
   }
   __syncthreads();
 
-  // ---- activation staging: thread tid carries 16 bytes of row tid / 4 and the row's two scale bytes
+  // ---- activation staging: per super-step (kSub chunks of 64 values) thread tid carries 16 bytes of every chunk of
+  //      row tid / 4 (piece tid % 4 of each chunk)
   const int arow_i = tid >> 2, apart = tid & 3;
   const int asrc = src_row[arow_i] >= 0 ? src_row[arow_i] : 0;
   const u8 *acode = a.x8 + (int64_t)asrc * K + 16 * apart;
-  const u16 *ascale = reinterpret_cast<const u16 *>(a.xs + (int64_t)asrc * (K / 32));
   auto clampc = [&](int c) __attribute__((always_inline)) { return c < C ? c : C - 1; };
+  const int SK = K / 32;   // scale bytes per row
 
   // ---- weights: this lane's two columns (gu: one column of the gate and of the up matrix) and K half
   const int h = lane >> 5, lc = lane & 31;
@@ -133,13 +157,28 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
     colj[0] = n0 + 64 * wave + lc;
     colj[1] = colj[0] + 32;
   }
-  const u8 *wcn[2], *wcs[2];
+  const u8 *wcn[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int col = colj[j] < N ? colj[j] : N - 1;
     wcn[j] = nbj[j] + (int64_t)col * (K / 2) + 16 * h;
-    wcs[j] = sbj[j] + (int64_t)col * (K / 32) + h;
   }
+  // the scale rows: activation rows (a gathered row each), then the weight column blocks (contiguous in memory)
+  for (int i = tid; i < BM * (SK / 2); i += 256) {
+    const int r = i / (SK / 2), q = i % (SK / 2);
+    const int sr = src_row[r] >= 0 ? src_row[r] : 0;
+    reinterpret_cast<u16 *>(Asc)[i] = reinterpret_cast<const u16 *>(a.xs + (int64_t)sr * SK)[q];
+  }
+  {
+    const int nblk = KIND == kGU ? 2 : 1, bcols = KIND == kGU ? 128 : 256;
+    const int cols = N - n0 < bcols ? N - n0 : bcols;   // columns past N are never stored
+#pragma unroll
+    for (int m = 0; m < nblk; ++m)
+      copy_to_lds(Wsc + m * 128 * SK, sbj[m] + (int64_t)n0 * SK, (int64_t)cols * SK, tid);
+  }
+  int wrow[2];   // the lane's columns as rows of Wsc
+#pragma unroll
+  for (int j = 0; j < 2; ++j) wrow[j] = (KIND == kGU ? 128 * j + 32 * wave : 64 * wave + 32 * j) + lc;
 
   f32x16 acc[2][2];
 #pragma unroll
@@ -149,24 +188,23 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  v4u aring[DEPTH], bring[DEPTH][2];
-  u32 asr[DEPTH], bsr[DEPTH][2];
-  auto load_a = [&](int slot, int c) __attribute__((always_inline)) {
-    const int cc = clampc(c);
-    aring[slot] = *reinterpret_cast<const v4u *>(acode + (int64_t)cc * KC);
-    asr[slot] = ascale[cc];
-  };
-  auto load_b = [&](int slot, int c) __attribute__((always_inline)) {
-    const int cc = clampc(c);
+  // Rings DEPTH super-steps deep. A super-step reads kSub consecutive 32-byte chunks of each weight column -- a
+  // whole 128-byte line for kSub = 4 -- with back-to-back loads, so the L1 merges them into one request per line.
+  v4u aring[DEPTH][kSub], bring[DEPTH][kSub][2];
+  auto load_a = [&](int slot, int st) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      bring[slot][j] = *reinterpret_cast<const v4u *>(wcn[j] + (int64_t)cc * 32);
-      bsr[slot][j] = wcs[j][2 * cc];
-    }
+    for (int i = 0; i < kSub; ++i) aring[slot][i] = *reinterpret_cast<const v4u *>(acode + (int64_t)clampc(kSub * st + i) * KC);
+  };
+  auto load_b = [&](int slot, int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i = 0; i < kSub; ++i)
+        bring[slot][i][j] = *reinterpret_cast<const v4u *>(wcn[j] + (int64_t)clampc(kSub * st + i) * 32);
   };
   auto stage = [&](int slot, int buf) __attribute__((always_inline)) {
-    *reinterpret_cast<v4u *>(&As[buf][arow_i][16 * apart]) = aring[slot];
-    Ass[buf][arow_i] = (u16)asr[slot];   // the row's four threads write the same value: no branch
+#pragma unroll
+    for (int i = 0; i < kSub; ++i) *reinterpret_cast<v4u *>(&As[buf][arow_i][KC * i + 16 * apart]) = aring[slot][i];
   };
   load_a(0, 0);
   stage(0, 0);
@@ -176,42 +214,47 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
             std::make_integer_sequence<int, DEPTH>{});
   __syncthreads();
 
-  // The chunk count is rounded up to a multiple of DEPTH. A padding chunk (c >= C) runs with both E8M0 scales 0:
-  // its products are at most 448 * 6 * 2^-254, far below the smallest f32 subnormal, so they add exactly zero.
-  // The loop body thus has no data-dependent branch; each step is instantiated with its ring slot as a constant
-  // (integral_constant), so the rings stay in registers.
-  auto step = [&](auto uc, int c0) __attribute__((always_inline)) {
+  // The super-step count is rounded up to a multiple of DEPTH. A padding chunk (c >= C) runs with both E8M0 scales
+  // 0: its products are at most 448 * 6 * 2^-254, far below the smallest f32 subnormal, so they add exactly zero.
+  // The loop body thus has no data-dependent branch; each super-step is instantiated with its ring slot as a
+  // constant (integral_constant), so the rings stay in registers.
+  auto step = [&](auto uc, int s0) __attribute__((always_inline)) {
     constexpr int u = decltype(uc)::value;
     constexpr int nx = (u + 1) % DEPTH;
-    constexpr int buf = u & 1;
-    const int c = c0 + u;
-    const bool live = c < C;
-    i32x8 af[2];
-    int sa[2];
+    const int st = s0 + u;
+    const int buf = st & 1;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const v4u v0 = *reinterpret_cast<const v4u *>(&As[buf][32 * i + lc][16 * h]);
-      const v4u v1 = *reinterpret_cast<const v4u *>(&As[buf][32 * i + lc][32 + 16 * h]);
-      af[i] = i32x8{(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w, (int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w};
-      sa[i] = live ? (Ass[buf][32 * i + lc] >> (8 * h)) & 0xFF : 0;
+    for (int i = 0; i < kSub; ++i) {
+      const bool live = kSub * st + i < C;
+      const int sc_off = 2 * clampc(kSub * st + i) + h;   // the lane's E8M0 byte of this chunk in a scale row
+      i32x8 af[2];
+      int sa[2];
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii) {
+        const v4u v0 = *reinterpret_cast<const v4u *>(&As[buf][32 * ii + lc][KC * i + 16 * h]);
+        const v4u v1 = *reinterpret_cast<const v4u *>(&As[buf][32 * ii + lc][KC * i + 32 + 16 * h]);
+        af[ii] = i32x8{(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w, (int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w};
+        sa[ii] = live ? Asc[(32 * ii + lc) * SK + sc_off] : 0;
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const v4u bv = bring[u][i][j];
+        const i32x8 bf = i32x8{(int)bv.x, (int)bv.y, (int)bv.z, (int)bv.w, 0, 0, 0, 0};
+        const int sb = live ? Wsc[wrow[j] * SK + sc_off] : 0;
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+          acc[ii][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[ii], bf, acc[ii][j], 0, 4, 0, sa[ii], 0, sb);
+      }
     }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const i32x8 bf = i32x8{(int)bring[u][j].x, (int)bring[u][j].y, (int)bring[u][j].z, (int)bring[u][j].w,
-                             0, 0, 0, 0};
-      const int sb = live ? (int)bsr[u][j] : 0;
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[i], bf, acc[i][j], 0, 4, 0, sa[i], 0, sb);
-    }
-    load_b(u, c + DEPTH);
+    load_b(u, st + DEPTH);
     stage(nx, buf ^ 1);
-    load_a(nx, c + 1 + DEPTH);
+    load_a(nx, st + 1 + DEPTH);
     __syncthreads();
   };
-  const int CP = (C + DEPTH - 1) / DEPTH * DEPTH;
-  for (int c0 = 0; c0 < CP; c0 += DEPTH)
-    for_steps(step, c0, std::make_integer_sequence<int, DEPTH>{});
+  const int S = (C + kSub - 1) / kSub;
+  const int SP = (S + DEPTH - 1) / DEPTH * DEPTH;
+  for (int s0 = 0; s0 < SP; s0 += DEPTH)
+    for_steps(step, s0, std::make_integer_sequence<int, DEPTH>{});
 
   constexpr int NJ = KIND == kGU ? 1 : 2;   // gu: one output column per lane (gate j = 0, up j = 1)
 #pragma unroll
@@ -235,7 +278,17 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
 template <int KIND>
 int launch(const MArgs &a, hipStream_t s) {
   const dim3 grid((unsigned)(8 * a.n_blocks * ((a.max_tiles + 7) / 8)));
-  mxfp4_grouped_kernel<KIND, kDepth><<<grid, 256, 0, s>>>(a);
+  const size_t dyn = (size_t)(BM + 256) * (a.K / 32);
+  if (dyn > 32768) {   // beyond the default dynamic LDS limit (K > 3276): raise it once
+    static bool raised = false;
+    if (!raised) {
+      if (hipFuncSetAttribute(reinterpret_cast<const void *>(&mxfp4_grouped_kernel<KIND, kDepth>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) != hipSuccess)
+        return QMM_ERR_LAUNCH;
+      raised = true;
+    }
+  }
+  mxfp4_grouped_kernel<KIND, kDepth><<<grid, 256, dyn, s>>>(a);
   return launch_status();
 }
 
@@ -246,7 +299,7 @@ int qmm_grouped_mxfp4(int mode, int fused, int act, int64_t max_tiles, int64_t k
                       const int32_t *tile_info, const int32_t *rowmap, const void *x, const void *x_scales,
                       int64_t x_rows, const void *w, const void *ws, const void *w2, const void *ws2, float *y,
                       hipStream_t s) {
-  if (k % 64) return QMM_ERR_SHAPE;
+  if (k % 64 || k > 12288) return QMM_ERR_SHAPE;   // the workgroup stages (64 + 256) x K / 32 scale bytes in LDS
   if (!x_scales || !ws) return QMM_ERR_NULL;
   if (!aligned(x_scales, 2)) return QMM_ERR_ALIGN;
   if (!aligned(x, 16) || !aligned(w, 16) || (w2 && !aligned(w2, 16))) return QMM_ERR_ALIGN;
