@@ -17,87 +17,77 @@ constexpr int kTile = 64;
 constexpr float kNormFloor = 6.103515625e-05f;
 
 // ------------------------------------------------------------------------------------------------- top-k
-// One wave per token; lane l holds experts l, l+64, l+128, l+192. KU rounds of a wave argmax on the selection
-// score, ties to the lower expert id (the reference's workgroup max then min-index, S/gen_moe.py:219-235).
-// The score is the logit (+ bias) for gating 1 and 3 and for gating 2 without a bias: those selections are
-// monotone in the logit, so choosing on the exact f32 logit reproduces the float64 oracle's choice.
+// One wave per token; lane l holds experts l, l+64, l+128, l+192. The selection is a ranking: the wave writes its
+// selection scores to LDS and every lane counts, for each of its experts, how many experts beat it (higher score,
+// ties to the lower id -- the reference's workgroup max then min-index, S/gen_moe.py:219-235); an expert of rank
+// r < KU is pick r. The score is the logit (+ bias) for gating 1 and 3 and for gating 2 without a bias: those
+// selections are monotone in the logit, so choosing on the exact f32 logit reproduces the float64 oracle's choice.
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+
+constexpr int kTopkMaxE = 256;
 
 __global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ logits, int64_t tokens, int E, int KU,
                                                    int gating, int norm, float scale, const float *__restrict__ bias,
                                                    int32_t *__restrict__ ids, float *__restrict__ wts) {
-  const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= tokens) return;
+  __shared__ __align__(16) float score[4][kTopkMaxE];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t t = (int64_t)blockIdx.x * 4 + wv;
+  if (t >= tokens) return;               // a whole wave: nothing below synchronizes the workgroup
   const float *lg = logits + t * E;
   float l[4], sel[4];
+  bool in[4];
   const float NEG = -3.0e38f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = lane + 64 * i;
-    const bool in = e < E;
-    l[i] = in ? lg[e] : NEG;
-    const float b = (in && bias) ? bias[e] : 0.f;
-    if (gating == 3) l[i] = in ? l[i] + b : NEG;   // the router bias is part of the logit (gating 3)
-    float s = l[i];
-    if (gating == 2 && bias) s = in ? 1.f / (1.f + expf(-l[i])) + b : NEG;
-    sel[i] = in ? s : NEG;
+    in[i] = e < E;
+    l[i] = in[i] ? lg[e] : NEG;
+    const float b = (in[i] && bias) ? bias[e] : 0.f;
+    if (gating == 3) l[i] = in[i] ? l[i] + b : NEG;   // the router bias is part of the logit (gating 3)
+    float sv = l[i];
+    if (gating == 2 && bias) sv = in[i] ? 1.f / (1.f + expf(-l[i])) + b : NEG;
+    sel[i] = in[i] ? sv : NEG;
+    score[wv][e] = sel[i];                // experts past E hold -3e38 and lose every comparison
   }
-  // probabilities the weights come from
-  float prob_den = 1.f, lmax = 0.f;
-  if (gating == 1) {
-    float m = fmaxf(fmaxf(l[0], l[1]), fmaxf(l[2], l[3]));
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  int rank[4] = {0, 0, 0, 0};
+  const int E4 = (E + 3) & ~3;
+  for (int e2 = 0; e2 < E4; e2 += 4) {
+    const f32x4 q = *reinterpret_cast<const f32x4 *>(&score[wv][e2]);
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    lmax = m;
-    float s = 0.f;
+    for (int jj = 0; jj < 4; ++jj)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s += (lane + 64 * i < E) ? expf(l[i] - lmax) : 0.f;
-    prob_den = wave_sum(s);
+      for (int i = 0; i < 4; ++i) rank[i] += better(q[jj], e2 + jj, sel[i], lane + 64 * i) ? 1 : 0;
   }
-  float wk[8];
-  int ik[8];
-  for (int r = 0; r < KU; ++r) {
-    float bv = NEG;
-    int bi = 1 << 30;
+  // the weights: probabilities over all experts (gating 1), sigmoids (gating 2) or a softmax over the picks (3)
+  float lmax = fmaxf(fmaxf(l[0], l[1]), fmaxf(l[2], l[3]));
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (better(sel[i], lane + 64 * i, bv, bi)) { bv = sel[i]; bi = lane + 64 * i; }
+  for (int off = 32; off >= 1; off >>= 1) lmax = fmaxf(lmax, __shfl_xor(lmax, off, 64));
+  float w[4], ws = 0.f;
+  bool pick[4];
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, 64);
-      const int oi = __shfl_xor(bi, off, 64);
-      if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  for (int i = 0; i < 4; ++i) {
+    pick[i] = in[i] && rank[i] < KU;
+    const float ex = in[i] ? expf(l[i] - lmax) : 0.f;
+    w[i] = gating == 2 ? 1.f / (1.f + expf(-l[i])) : ex;
+    ws += gating == 1 ? ex : (pick[i] ? w[i] : 0.f);
+  }
+  float den = wave_sum(ws);                // gating 1: the softmax denominator; 3: the picks' sum; 2: the sum
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (gating != 2) w[i] = w[i] / den;
+    sum += pick[i] ? w[i] : 0.f;
+  }
+  const float nden = norm ? fmaxf(gating == 2 ? den : wave_sum(sum), kNormFloor) : 1.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (pick[i]) {
+      ids[t * KU + rank[i]] = lane + 64 * i;
+      wts[t * KU + rank[i]] = (norm ? w[i] / nden : w[i]) * scale;
     }
-    // every lane now agrees on the winner bi; its owner removes it and everybody learns its logit
-    float lw = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (lane + 64 * i == bi) { lw = l[i]; sel[i] = NEG; }
-    lw = __shfl(lw, bi & 63, 64);
-    ik[r] = bi;
-    wk[r] = lw;
-  }
-  if (lane == 0) {
-    float w[8];
-    float sum = 0.f;
-    if (gating == 3) {   // softmax over the picked (round 0 holds the largest)
-      for (int r = 0; r < KU; ++r) { w[r] = expf(wk[r] - wk[0]); sum += w[r]; }
-      for (int r = 0; r < KU; ++r) w[r] = w[r] / sum;
-      sum = 0.f;
-      for (int r = 0; r < KU; ++r) sum += w[r];
-    } else {
-      for (int r = 0; r < KU; ++r) {
-        w[r] = gating == 1 ? expf(wk[r] - lmax) / prob_den : 1.f / (1.f + expf(-wk[r]));
-        sum += w[r];
-      }
-    }
-    const float den = norm ? fmaxf(sum, kNormFloor) : 1.f;
-    for (int r = 0; r < KU; ++r) {
-      ids[t * KU + r] = ik[r];
-      wts[t * KU + r] = (norm ? w[r] / den : w[r]) * scale;
-    }
-  }
 }
 
 // ------------------------------------------------------------------------------------------------ bucket
@@ -244,6 +234,39 @@ __global__ __launch_bounds__(256) void combine_kernel(int64_t tokens, int64_t ro
 // ------------------------------------------------------------------------------------------ row scale f16
 // One workgroup per row: e = clamp(exponent(max |x|) - 13, 0, 100), x16 = f16(x 2^-e) (round to nearest even),
 // scales = (2^-e, 2^e). x is f32 or bf16.
+// The same with 16-byte accesses, for H % 4 == 0 and 16-byte aligned ys / y: workgroup (t, part) covers 1024
+// values of token t, thread c four of them, and every one of the KU rows is loaded before the fma chain (same
+// order, same arithmetic as combine_kernel).
+__global__ __launch_bounds__(256) void combine_vec_kernel(int64_t tokens, int64_t rows, int64_t H, int KU,
+                                                          const float *__restrict__ ys, const int32_t *__restrict__ pos,
+                                                          const float *__restrict__ wts, int accumulate,
+                                                          float *__restrict__ y) {
+  const int64_t t = blockIdx.y;
+  const int64_t c4 = (int64_t)blockIdx.x * 256 + threadIdx.x;   // float4 index within the row
+  if (c4 * 4 >= H) return;
+  int64_t row[8];
+  float w[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    if (k < KU) {
+      row[k] = pos ? pos[t * KU + k] : t * KU + k;
+      w[k] = wts[t * KU + k];
+    }
+  }
+  f32x4 v[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (k < KU) v[k] = (row[k] >= 0 && row[k] < rows) ? reinterpret_cast<const f32x4 *>(ys + row[k] * H)[c4] : f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 acc = accumulate ? reinterpret_cast<const f32x4 *>(y + t * H)[c4] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (k < KU) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = __builtin_fmaf(w[k], v[k][j], acc[j]);
+    }
+  reinterpret_cast<f32x4 *>(y + t * H)[c4] = acc;
+}
+
 __device__ __forceinline__ float load_act(const void *x, int bf, int64_t i) {
   return bf ? bf16_to_f32(static_cast<const u16 *>(x)[i]) : static_cast<const float *>(x)[i];
 }
@@ -271,64 +294,130 @@ __global__ __launch_bounds__(256) void row_scale_kernel(int64_t rows, int64_t k,
   }
 }
 
+// The same with 16-byte accesses: thread c of the row handles 8 consecutive values, holding up to kRsChunks such
+// chunks in registers between the row maximum and the conversion (rows of up to 256 x 8 x kRsChunks values; the
+// host takes the scalar kernel above for wider, misaligned or k % 8 != 0 rows).
+constexpr int kRsChunks = 4;
+typedef __attribute__((ext_vector_type(4))) u32 v4u;
+
+template <bool BF>
+__device__ __forceinline__ void load8(const void *x, int64_t i8, float (&v)[8]) {
+  if constexpr (BF) {
+    const v4u q = reinterpret_cast<const v4u *>(x)[i8];
+    const u32 d[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { v[2 * j] = bf16_to_f32(d[j] & 0xFFFFu); v[2 * j + 1] = bf16_to_f32(d[j] >> 16); }
+  } else {
+    const v4u a = reinterpret_cast<const v4u *>(x)[2 * i8], b = reinterpret_cast<const v4u *>(x)[2 * i8 + 1];
+    const u32 d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = u32_as_f32(d[j]);
+  }
+}
+
+template <bool BF>
+__global__ __launch_bounds__(256) void row_scale_vec_kernel(int64_t rows, int64_t k, const void *__restrict__ x,
+                                                            float *__restrict__ scales, _Float16 *__restrict__ x16,
+                                                            const int32_t *__restrict__ tile_info) {
+  const int64_t r = blockIdx.x;
+  if (tile_info && tile_info[2 * (r / kTile)] < 0) return;
+  __shared__ float wmax[4];
+  const int64_t nch = k / 8, base = r * nch;
+  float v[kRsChunks][8];
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < kRsChunks; ++i) {
+    const int64_t c = threadIdx.x + 256 * i;
+    if (c < nch) {
+      load8<BF>(x, base + c, v[i]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[i][j]));
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const int biased = (int)((f32_as_u32(m) >> 23) & 255u);
+  const int e = min(max(biased - 127 - 13, 0), 100);
+  const float sc = u32_as_f32((u32)(127 - e) << 23), inv = u32_as_f32((u32)(127 + e) << 23);
+#pragma unroll
+  for (int i = 0; i < kRsChunks; ++i) {
+    const int64_t c = threadIdx.x + 256 * i;
+    if (c < nch) {
+      u32 o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o[j] = (u32)__builtin_bit_cast(u16, (_Float16)(v[i][2 * j] * sc)) |
+               ((u32)__builtin_bit_cast(u16, (_Float16)(v[i][2 * j + 1] * sc)) << 16);
+      reinterpret_cast<v4u *>(x16)[base + c] = v4u{o[0], o[1], o[2], o[3]};
+    }
+  }
+  if (threadIdx.x == 0) {
+    scales[2 * r] = sc;
+    scales[2 * r + 1] = inv;
+  }
+}
+
 // ---------------------------------------------------------------------------------------------- MXFP8 quant
-// One thread per 32 values. s = clamp(floor(log2(amax)) - 7, -127, 127) keeps every |x| 2^-s below 256, under the
-// E4M3 maximum 448; the conversion is v_cvt_pk_fp8_f32 (round to nearest even, OCP E4M3FN on gfx950).
+// OCP MX: one E8M0 scale per 32 values along a row, E4M3 codes. s = clamp(floor(log2(amax)) - 7, -127, 127) keeps
+// every |x| 2^-s below 256, under the E4M3 maximum 448; the conversion is v_cvt_pk_fp8_f32 (round to nearest even,
+// OCP E4M3FN on gfx950). Consecutive lanes take consecutive 16-byte pieces of the rows (4 f32 or 8 bf16 values); a
+// block is the group of 8 (f32) or 4 (bf16) lanes holding it, whose maximum comes from a butterfly inside the group.
 constexpr int kMxBlock = 32;
 
-__global__ __launch_bounds__(256) void quant_mxfp8_kernel(int64_t rows, int64_t k, const void *__restrict__ xv,
-                                                          int bf, const int32_t *__restrict__ tile_info,
-                                                          u8 *__restrict__ codes, u8 *__restrict__ scales) {
-  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t per_row = k / kMxBlock;
-  if (g >= rows * per_row) return;
-  const int64_t r = g / per_row;
-  if (tile_info && tile_info[2 * (r / kTile)] < 0) return;
-  float v[kMxBlock];
-  if (bf) {
-    const uint4 *p = reinterpret_cast<const uint4 *>(static_cast<const u16 *>(xv) + g * kMxBlock);
+template <bool BF>
+__global__ __launch_bounds__(256) void quant_mxfp8_vec_kernel(int64_t rows, int64_t k, const void *__restrict__ xv,
+                                                              const int32_t *__restrict__ tile_info,
+                                                              u8 *__restrict__ codes, u8 *__restrict__ scales) {
+  constexpr int VPL = BF ? 8 : 4, LPB = kMxBlock / VPL;
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // 16-byte piece of the input
+  const int64_t pieces = rows * (k / VPL);
+  const bool in = g < pieces;
+  const int64_t gg = in ? g : pieces - 1;
+  const int64_t r = gg / (k / VPL);
+  const bool live = in && !(tile_info && tile_info[2 * (r / kTile)] < 0);
+  float v[VPL];
+  if constexpr (BF) {
+    const v4u q = reinterpret_cast<const v4u *>(xv)[gg];
+    const u32 d[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-    for (int i = 0; i < kMxBlock / 8; ++i) {
-      const uint4 q = p[i];
-      const u32 d[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[8 * i + 2 * j] = bf16_to_f32(d[j] & 0xFFFFu);
-        v[8 * i + 2 * j + 1] = bf16_to_f32(d[j] >> 16);
-      }
-    }
+    for (int j = 0; j < 4; ++j) { v[2 * j] = bf16_to_f32(d[j] & 0xFFFFu); v[2 * j + 1] = bf16_to_f32(d[j] >> 16); }
   } else {
-    const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(xv) + g * kMxBlock);
+    const f32x4 q = reinterpret_cast<const f32x4 *>(xv)[gg];
 #pragma unroll
-    for (int i = 0; i < kMxBlock / 4; ++i) {
-      const float4 q = p[i];
-      v[4 * i] = q.x; v[4 * i + 1] = q.y; v[4 * i + 2] = q.z; v[4 * i + 3] = q.w;
-    }
+    for (int j = 0; j < 4; ++j) v[j] = q[j];
   }
   float amax = 0.f;
 #pragma unroll
-  for (int i = 0; i < kMxBlock; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  int s = -127;
+  for (int i = 0; i < VPL; ++i) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+  for (int off = 1; off < LPB; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  int sx = -127;
   if (amax > 0.f) {
     int ex;
     frexpf(amax, &ex);        // amax = f 2^ex, f in [0.5, 1)
-    s = min(max(ex - 1 - 7, -127), 127);
+    sx = min(max(ex - 1 - 7, -127), 127);
   }
-  u32 out[kMxBlock / 4];
+  if (!live) return;
+  u32 out[VPL / 4];
 #pragma unroll
-  for (int i = 0; i < kMxBlock / 4; ++i) {
+  for (int i = 0; i < VPL / 4; ++i) {
     int w = 0;
-    w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * i], -s), ldexpf(v[4 * i + 1], -s), w, false);
-    w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * i + 2], -s), ldexpf(v[4 * i + 3], -s), w, true);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * i], -sx), ldexpf(v[4 * i + 1], -sx), w, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * i + 2], -sx), ldexpf(v[4 * i + 3], -sx), w, true);
     out[i] = (u32)w;
   }
-  uint4 *o = reinterpret_cast<uint4 *>(codes + g * kMxBlock);
-#pragma unroll
-  for (int i = 0; i < kMxBlock / 16; ++i) o[i] = make_uint4(out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]);
-  scales[g] = (u8)(s + 127);
+  if constexpr (BF) {
+    typedef __attribute__((ext_vector_type(2))) u32 v2u;
+    reinterpret_cast<v2u *>(codes)[g] = v2u{out[0], out[1]};
+  } else {
+    reinterpret_cast<u32 *>(codes)[g] = out[0];
+  }
+  if ((threadIdx.x & (LPB - 1)) == 0) scales[g / LPB] = (u8)(sx + 127);
 }
 
-// -------------------------------------------------------------------------------------------- MXFP4 repack
 __global__ __launch_bounds__(256) void repack_mxfp4_kernel(int64_t groups, const u8 *__restrict__ w,
                                                            u8 *__restrict__ nib, u8 *__restrict__ sc) {
   const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -386,7 +475,11 @@ int qmm_moe_combine(int64_t tokens, int64_t rows, int64_t H, int KU, const float
   if (tokens <= 0 || H <= 0 || rows <= 0 || tokens > (1ll << 24)) return QMM_ERR_SHAPE;
   if (!pos && rows < tokens * KU) return QMM_ERR_SHAPE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  combine_kernel<<<(unsigned)tokens, 256, 0, s>>>(tokens, rows, H, KU, ys, pos, wts, accumulate, y);
+  if (H % 4 == 0 && aligned(ys, 16) && aligned(y, 16) && tokens <= 65535)
+    combine_vec_kernel<<<dim3((unsigned)((H / 4 + 255) / 256), (unsigned)tokens), 256, 0, s>>>(tokens, rows, H, KU, ys,
+                                                                                                pos, wts, accumulate, y);
+  else
+    combine_kernel<<<(unsigned)tokens, 256, 0, s>>>(tokens, rows, H, KU, ys, pos, wts, accumulate, y);
   return launch_status();
 }
 
@@ -397,8 +490,13 @@ int qmm_row_scale_f16(int64_t rows, int64_t k, const void *x, int x_dtype, float
   if (rows <= 0 || k <= 0 || rows > (1ll << 24)) return QMM_ERR_SHAPE;
   if (tile_info && rows % kTile) return QMM_ERR_SHAPE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  row_scale_kernel<<<(unsigned)rows, 256, 0, s>>>(rows, k, x, x_dtype == QMM_BF16, scales,
-                                                  static_cast<_Float16 *>(x16), tile_info);
+  _Float16 *o = static_cast<_Float16 *>(x16);
+  if (k % 8 == 0 && k <= 8 * 256 * kRsChunks && aligned(x, 16) && aligned(x16, 16)) {
+    if (x_dtype == QMM_BF16) row_scale_vec_kernel<true><<<(unsigned)rows, 256, 0, s>>>(rows, k, x, scales, o, tile_info);
+    else row_scale_vec_kernel<false><<<(unsigned)rows, 256, 0, s>>>(rows, k, x, scales, o, tile_info);
+  } else {
+    row_scale_kernel<<<(unsigned)rows, 256, 0, s>>>(rows, k, x, x_dtype == QMM_BF16, scales, o, tile_info);
+  }
   return launch_status();
 }
 
@@ -410,9 +508,13 @@ int qmm_quant_mxfp8(int64_t rows, int64_t k, const void *x, int x_dtype, const i
   if (tile_info && rows % kTile) return QMM_ERR_SHAPE;
   if (!aligned(x, 16) || !aligned(codes, 16)) return QMM_ERR_ALIGN;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int64_t groups = rows * (k / kMxBlock);
-  quant_mxfp8_kernel<<<(unsigned)((groups + 255) / 256), 256, 0, s>>>(rows, k, x, x_dtype == QMM_BF16, tile_info,
-                                                                      codes, scales);
+  if (x_dtype == QMM_BF16) {
+    const int64_t pieces = rows * (k / 8);
+    quant_mxfp8_vec_kernel<true><<<(unsigned)((pieces + 255) / 256), 256, 0, s>>>(rows, k, x, tile_info, codes, scales);
+  } else {
+    const int64_t pieces = rows * (k / 4);
+    quant_mxfp8_vec_kernel<false><<<(unsigned)((pieces + 255) / 256), 256, 0, s>>>(rows, k, x, tile_info, codes, scales);
+  }
   return launch_status();
 }
 
