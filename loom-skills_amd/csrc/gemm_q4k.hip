@@ -101,11 +101,18 @@ struct Args {
   int tiles_m, n_blocks, tiles_total;
 };
 
-template <int KIND, bool ACC, bool BF16OUT, int DEPTH>
+// Scale tables: a workgroup decodes the (d sc, -dmin m) f16 pair of every sub-block of its 128 weight columns once
+// into LDS (4 bytes per sub-block, 16 K bytes) when that fits (K <= kStagedMaxK); each step then reads its two
+// pairs per column with one 8-byte LDS read instead of loading and decoding the super-block header again.
+constexpr int kStagedMaxK = 6144;
+
+template <int KIND, bool ACC, bool BF16OUT, int DEPTH, bool STAGED>
 __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
   constexpr int BN = KIND == kGU ? 64 : 128;
+  extern __shared__ __align__(16) u32 scl[];   // STAGED: [128 columns][K / 32] (dsc | nmn << 16)
   __shared__ __align__(16) _Float16 As[2][2][BM][APITCH];   // [buffer][K-half][row][k]
   __shared__ int src_row[BM];
+  __shared__ float rinv[BM];   // the row's inverse activation scale (1 without scales)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int sel = wave & 1, kh = wave >> 1;   // sel: N-half (dense, dn) or matrix (gu: 0 gate, 1 up)
   const int M = a.M, N = a.N, K = a.K;
@@ -131,6 +138,7 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
     expert = expert >= a.E ? a.E - 1 : expert;
   }
   // activation row of each tile row (-1: a dead row, written as zero)
+  int my_src = -1;
   if (tid < BM) {
     int src;
     if constexpr (KIND == kDense) src = m0 + tid < M ? m0 + tid : -1;
@@ -142,8 +150,12 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
       src = a.rowmap[m0 + tid] >= 0 ? m0 + tid : -1;
     }
     src_row[tid] = src;
+    rinv[tid] = (a.scales && src >= 0) ? a.scales[2 * src + 1] : 1.f;
+    my_src = src;
   }
-  __syncthreads();
+  // whether rows 32..63 hold a live row: if not, the upper 32-row MFMA blocks are skipped (their outputs are the
+  // zeros of dead rows) -- expert tiles of prefill batches are often less than half full
+  const bool upper = __syncthreads_or(tid >= 32 && my_src >= 0) != 0;
 
   const int64_t RB = (int64_t)K / 256 * 144;
   const int S = K / KSTEP, S0 = S / 2;
@@ -151,15 +163,22 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
   // ---- A staging map: chunk c = i * 256 + tid of 16 bytes; K-half, row, 16-byte column. Loads are unconditional
   // (dead rows read activation row 0 and their outputs are zeroed; steps past S0 reload step S0 - 1 and get zero
   // weights in the math).
-  const _Float16 *arow[4];
+  // The loads go through a buffer resource over the activation rows: a dead row's offset lies past its end
+  // (0x80000000), where the hardware returns zeros without touching memory, so a tile of a few live rows fetches
+  // only those.
+  const __amdgpu_buffer_rsrc_t xrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16 *>(a.x16), (short)0, (int)((int64_t)a.x_rows * K * 2), 0x00020000);
+  u32 aoff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int c = i * 256 + tid, ckh = c >> 9, row = (c >> 3) & 63, col = c & 7;
     const int src = src_row[row];
-    arow[i] = a.x16 + (int64_t)(src >= 0 ? src : 0) * K + (int64_t)ckh * S0 * KSTEP + col * 8;
+    aoff[i] = src >= 0 ? (u32)(((int64_t)src * K + (int64_t)ckh * S0 * KSTEP + col * 8) * 2) : 0x80000000u;
   }
   auto a_load = [&](int i, int s) -> uint4 {
-    return *reinterpret_cast<const uint4 *>(arow[i] + (int64_t)(s < S0 ? s : S0 - 1) * KSTEP);
+    typedef __attribute__((ext_vector_type(4))) u32 u32x4;
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)(aoff[i] + (u32)((s < S0 ? s : S0 - 1) * KSTEP * 2)), 0, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
   };
   auto a_dst = [&](int i, int buf) -> uint4 * {
     const int c = i * 256 + tid, ckh = c >> 9, row = (c >> 3) & 63, col = c & 7;
@@ -190,6 +209,46 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
   auto b_head = [&](int j, int s) -> uint4 {
     return ld16(wcol[j] + (int64_t)((kh * S0 + (s < S0 ? s : S0 - 1)) >> 2) * 144);
   };
+  const int SB = K / 32;   // sub-blocks per column
+  if constexpr (STAGED) {
+    // local column cl = sel * 64 + 32 j + lc: dense / dn columns n0 + cl, gu: gate n0 + cl (cl < 64), up n0 + cl - 64
+    // every header of the workgroup's columns, kHdrBatch loads in flight per thread before any is decoded
+    constexpr int kHdrBatch = 4;
+    const int nh = 128 * (K / 256);
+    for (int b0 = 0; b0 < nh; b0 += kHdrBatch * 256) {
+      uint4 hd[kHdrBatch];
+#pragma unroll
+      for (int q = 0; q < kHdrBatch; ++q) {
+        int i = b0 + tid + 256 * q;
+        i = i < nh ? i : nh - 1;
+        const int cl = i / (K / 256), b = i % (K / 256);
+        const int msel = cl >> 6;
+        const u8 *mb;
+        if constexpr (KIND == kDense) mb = a.w;
+        else if constexpr (KIND == kGU) {
+          const u8 *g = a.w + (int64_t)expert * a.ebytes;
+          mb = msel ? (a.w2 ? a.w2 + (int64_t)expert * a.ebytes : g + a.up_off) : g;
+        } else {
+          mb = a.w + (int64_t)expert * a.ebytes;
+        }
+        int c = n0 + (KIND == kGU ? cl - 64 * msel : cl);
+        c = c < N ? c : N - 1;
+        hd[q] = ld16(mb + (int64_t)c * RB + (int64_t)b * 144);
+      }
+#pragma unroll
+      for (int q = 0; q < kHdrBatch; ++q) {
+        const int i = b0 + tid + 256 * q;
+        if (i >= nh) continue;
+        const int cl = i / (K / 256), b = i % (K / 256);
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+          h2 dsc, nmn;
+          sub_scale(hd[q], g, dsc, nmn);
+          scl[cl * SB + 8 * b + g] = (u32)__builtin_bit_cast(u16, dsc[0]) | ((u32)__builtin_bit_cast(u16, nmn[0]) << 16);
+        }
+      }
+    }
+  }
 
   f32x16 acc[2][2];
 #pragma unroll
@@ -208,7 +267,10 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
   };
   auto load_b = [&](int slot, int st) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) { cring[slot][j] = b_code(j, st); hring[slot][j] = b_head(j, st); }
+    for (int j = 0; j < 2; ++j) {
+      cring[slot][j] = b_code(j, st);
+      if constexpr (!STAGED) hring[slot][j] = b_head(j, st);
+    }
   };
   load_a(0, 0);
 #pragma unroll
@@ -228,13 +290,26 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
     for (int u = 0; u < DEPTH; ++u) {
       const int s = s0 + u;
       const int buf = u & 1;   // DEPTH is even, so s & 1 == u & 1
-      const int page = (kh * S0 + (s < S0 ? s : S0 - 1)) & 3;
+      const int gstep = kh * S0 + (s < S0 ? s : S0 - 1);
+      const int page = gstep & 3;
+      typedef __attribute__((ext_vector_type(2))) u32 u32x2;
+      u32x2 sp[2];
+      if constexpr (STAGED) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) sp[j] = *reinterpret_cast<const u32x2 *>(&scl[(sel * 64 + 32 * j + lc) * SB + 2 * gstep]);
+      }
 #pragma unroll
       for (int gl = 0; gl < 2; ++gl) {
         h2 dsc[2], nmn[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          sub_scale(hring[u][j], 2 * page + gl, dsc[j], nmn[j]);
+          if constexpr (STAGED) {
+            const u32 v = gl ? sp[j].y : sp[j].x;
+            dsc[j] = as_h2((v & 0xFFFFu) * 0x10001u);
+            nmn[j] = as_h2((v >> 16) * 0x10001u);
+          } else {
+            sub_scale(hring[u][j], 2 * page + gl, dsc[j], nmn[j]);
+          }
           if (s >= S0) dsc[j] = nmn[j] = h2{0, 0};   // a padding step: zero weights
         }
 #pragma unroll
@@ -245,14 +320,15 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
             const u32 q0 = s2 ? cring[u][j].z : cring[u][j].x, q1 = s2 ? cring[u][j].w : cring[u][j].y;
             bf[j] = gl ? deq8<true>(q0, q1, dsc[j], nmn[j]) : deq8<false>(q0, q1, dsc[j], nmn[j]);
           }
+          af[0] = *reinterpret_cast<const f16x8 *>(&As[buf][kh][lc][32 * gl + 16 * h + 8 * s2]);
 #pragma unroll
-          for (int i = 0; i < 2; ++i)
-            af[i] = *reinterpret_cast<const f16x8 *>(&As[buf][kh][32 * i + lc][32 * gl + 16 * h + 8 * s2]);
-#pragma unroll
-          for (int i = 0; i < 2; ++i)
+          for (int j = 0; j < 2; ++j) acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[0], bf[j], acc[0][j], 0, 0, 0);
+          if (upper) {
+            af[1] = *reinterpret_cast<const f16x8 *>(&As[buf][kh][32 + lc][32 * gl + 16 * h + 8 * s2]);
 #pragma unroll
             for (int j = 0; j < 2; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+              acc[1][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[1], bf[j], acc[1][j], 0, 0, 0);
+          }
         }
       }
       load_b(u, s + DEPTH);
@@ -317,8 +393,7 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
         const int src = src_row[lr];
         const int64_t o = (int64_t)row * N + col;
         if constexpr (KIND == kDense) {
-          float v = acc[i][j][r];
-          if (a.scales) v *= a.scales[2 * row + 1];
+          float v = acc[i][j][r] * rinv[lr];
           if constexpr (BF16OUT) {
             if constexpr (ACC) v += bf16_to_f32(yb[o]);
             yb[o] = (u16)f32_to_bf16_rne(v);
@@ -329,7 +404,7 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
         } else {
           float v = 0.f;
           if (src >= 0) {
-            const float inv = a.scales ? a.scales[2 * src + 1] : 1.f;
+            const float inv = rinv[lr];
             if constexpr (KIND == kGU) v = act_fn(a.act, acc[i][j][r] * inv, red_at(0, i, j, r) * inv);
             else v = acc[i][j][r] * inv;
           }
@@ -341,7 +416,22 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
 template <int KIND, bool ACC, bool BF16OUT>
 int launch(const Args &a, hipStream_t s) {
   const dim3 grid((unsigned)(KIND == kDense ? 8 * ((a.tiles_total + 7) / 8) : 8 * a.n_blocks * ((a.tiles_m + 7) / 8)));
-  q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth><<<grid, 256, 0, s>>>(a);
+  if (a.K <= kStagedMaxK) {
+    const size_t dyn = (size_t)128 * (a.K / 32) * 4;
+    if (dyn > 32768) {   // beyond the default dynamic LDS limit: raise it once
+      static bool raised = false;
+      if (!raised) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, true>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)((size_t)128 * (kStagedMaxK / 32) * 4)) !=
+            hipSuccess)
+          return QMM_ERR_LAUNCH;
+        raised = true;
+      }
+    }
+    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, true><<<grid, 256, dyn, s>>>(a);
+  } else {
+    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, false><<<grid, 256, 0, s>>>(a);
+  }
   return launch_status();
 }
 
@@ -359,6 +449,7 @@ extern "C" int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, c
   if (rows <= 0 || n <= 0 || k <= 0 || k % 256) return QMM_ERR_SHAPE;
   if (rows > (1 << 24) || n > (1 << 24) || k > (1 << 20)) return QMM_ERR_SHAPE;
   if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 4)) return QMM_ERR_ALIGN;
+  if (rows * k * 2 >= (1ll << 31)) return QMM_ERR_SHAPE;   // activation rows are addressed by a 32-bit buffer offset
   Args a{};
   a.M = (int)rows; a.N = (int)n; a.K = (int)k;
   a.x16 = static_cast<const _Float16 *>(x); a.scales = scales; a.x_rows = (int)rows;
@@ -378,6 +469,7 @@ int qmm_grouped_q4k(int mode, int fused, int act, int64_t max_tiles, int64_t k, 
                     const int32_t *tile_info, const int32_t *rowmap, const void *x, const float *x_scales,
                     int64_t x_rows, const void *w, const void *w2, float *y, hipStream_t s) {
   if (k % 256) return QMM_ERR_SHAPE;
+  if (x_rows * k * 2 >= (1ll << 31)) return QMM_ERR_SHAPE;   // activation rows are addressed by a 32-bit buffer offset
   if (!aligned(x, 16) || !aligned(w, 16) || (w2 && !aligned(w2, 16))) return QMM_ERR_ALIGN;
   const int64_t RB = k / 256 * 144;
   Args a{};

@@ -88,15 +88,37 @@ __device__ __forceinline__ void for_steps(F &&f, int c0, std::integer_sequence<i
   (f(std::integral_constant<int, I>{}, c0), ...);
 }
 
+// Element i of an n-element copy into LDS, for every i, 256 threads: kBatch loads in flight per thread before
+// their stores (a plain loop would wait for each load before the next). get(i) loads element i (i < n).
+constexpr int kBatch = 8;
+template <class T, class G>
+__device__ __forceinline__ void batched_copy(T *dst, int64_t n, int tid, G &&get) {
+  for (int64_t b = 0; b < n; b += kBatch * 256) {
+    T v[kBatch];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const int64_t i = b + tid + 256 * q;
+      v[q] = get(i < n ? i : n - 1);
+    }
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const int64_t i = b + tid + 256 * q;
+      if (i < n) dst[i] = v[q];
+    }
+  }
+}
+
 // copies n bytes from global memory to LDS with the widest loads the alignment of both allows
 __device__ __forceinline__ void copy_to_lds(u8 *dst, const u8 *src, int64_t n, int tid) {
   const uintptr_t al = reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) | (uintptr_t)n;
   if ((al & 15) == 0) {
-    for (int64_t i = tid; i < n / 16; i += 256) reinterpret_cast<v4u *>(dst)[i] = reinterpret_cast<const v4u *>(src)[i];
+    const v4u *s = reinterpret_cast<const v4u *>(src);
+    batched_copy(reinterpret_cast<v4u *>(dst), n / 16, tid, [&](int64_t i) { return s[i]; });
   } else if ((al & 3) == 0) {
-    for (int64_t i = tid; i < n / 4; i += 256) reinterpret_cast<u32 *>(dst)[i] = reinterpret_cast<const u32 *>(src)[i];
+    const u32 *s = reinterpret_cast<const u32 *>(src);
+    batched_copy(reinterpret_cast<u32 *>(dst), n / 4, tid, [&](int64_t i) { return s[i]; });
   } else {
-    for (int64_t i = tid; i < n; i += 256) dst[i] = src[i];
+    batched_copy(dst, n, tid, [&](int64_t i) { return src[i]; });
   }
 }
 
@@ -120,6 +142,7 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
   if (expert < 0) return;
   expert = expert >= a.E ? a.E - 1 : expert;
 
+  int my_src = -1;
   if (tid < BM) {
     int src;
     if constexpr (KIND == kGU) {
@@ -130,14 +153,20 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
       src = a.rowmap[m0 + tid] >= 0 ? m0 + tid : -1;
     }
     src_row[tid] = src;
+    my_src = src;
   }
-  __syncthreads();
+  // whether rows 32..63 hold a live row: if not, the upper 32-row MFMA blocks are skipped (their outputs are the
+  // zeros of dead rows) -- expert tiles of prefill batches are often less than half full
+  const bool upper = __syncthreads_or(tid >= 32 && my_src >= 0) != 0;
 
   // ---- activation staging: per super-step (kSub chunks of 64 values) thread tid carries 16 bytes of every chunk of
   //      row tid / 4 (piece tid % 4 of each chunk)
   const int arow_i = tid >> 2, apart = tid & 3;
-  const int asrc = src_row[arow_i] >= 0 ? src_row[arow_i] : 0;
-  const u8 *acode = a.x8 + (int64_t)asrc * K + 16 * apart;
+  // a buffer resource over the activation codes: a dead row's offset lies past the end (0x80000000) and loads
+  // zeros without touching memory, so a tile of few live rows fetches only those
+  const __amdgpu_buffer_rsrc_t xrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<u8 *>(a.x8), (short)0, (int)((int64_t)a.x_rows * K), 0x00020000);
+  const u32 aoff = src_row[arow_i] >= 0 ? (u32)((int64_t)src_row[arow_i] * K + 16 * apart) : 0x80000000u;
   auto clampc = [&](int c) __attribute__((always_inline)) { return c < C ? c : C - 1; };
   const int SK = K / 32;   // scale bytes per row
 
@@ -164,11 +193,11 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
     wcn[j] = nbj[j] + (int64_t)col * (K / 2) + 16 * h;
   }
   // the scale rows: activation rows (a gathered row each), then the weight column blocks (contiguous in memory)
-  for (int i = tid; i < BM * (SK / 2); i += 256) {
-    const int r = i / (SK / 2), q = i % (SK / 2);
+  batched_copy(reinterpret_cast<u16 *>(Asc), (int64_t)BM * (SK / 2), tid, [&](int64_t i) {
+    const int r = (int)(i / (SK / 2)), q = (int)(i % (SK / 2));
     const int sr = src_row[r] >= 0 ? src_row[r] : 0;
-    reinterpret_cast<u16 *>(Asc)[i] = reinterpret_cast<const u16 *>(a.xs + (int64_t)sr * SK)[q];
-  }
+    return reinterpret_cast<const u16 *>(a.xs + (int64_t)sr * SK)[q];
+  });
   {
     const int nblk = KIND == kGU ? 2 : 1, bcols = KIND == kGU ? 128 : 256;
     const int cols = N - n0 < bcols ? N - n0 : bcols;   // columns past N are never stored
@@ -193,7 +222,8 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
   v4u aring[DEPTH][kSub], bring[DEPTH][kSub][2];
   auto load_a = [&](int slot, int st) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < kSub; ++i) aring[slot][i] = *reinterpret_cast<const v4u *>(acode + (int64_t)clampc(kSub * st + i) * KC);
+    for (int i = 0; i < kSub; ++i)
+      aring[slot][i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)(aoff + (u32)(clampc(kSub * st + i) * KC)), 0, 0);
   };
   auto load_b = [&](int slot, int st) __attribute__((always_inline)) {
 #pragma unroll
@@ -227,23 +257,35 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
     for (int i = 0; i < kSub; ++i) {
       const bool live = kSub * st + i < C;
       const int sc_off = 2 * clampc(kSub * st + i) + h;   // the lane's E8M0 byte of this chunk in a scale row
-      i32x8 af[2];
-      int sa[2];
-#pragma unroll
-      for (int ii = 0; ii < 2; ++ii) {
+      auto afrag = [&](int ii, i32x8 &af, int &sa) __attribute__((always_inline)) {
         const v4u v0 = *reinterpret_cast<const v4u *>(&As[buf][32 * ii + lc][KC * i + 16 * h]);
         const v4u v1 = *reinterpret_cast<const v4u *>(&As[buf][32 * ii + lc][KC * i + 32 + 16 * h]);
-        af[ii] = i32x8{(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w, (int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w};
-        sa[ii] = live ? Asc[(32 * ii + lc) * SK + sc_off] : 0;
-      }
+        af = i32x8{(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w, (int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w};
+        sa = live ? Asc[(32 * ii + lc) * SK + sc_off] : 0;
+      };
+      i32x8 bf[2];
+      int sb[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const v4u bv = bring[u][i][j];
-        const i32x8 bf = i32x8{(int)bv.x, (int)bv.y, (int)bv.z, (int)bv.w, 0, 0, 0, 0};
-        const int sb = live ? Wsc[wrow[j] * SK + sc_off] : 0;
+        bf[j] = i32x8{(int)bv.x, (int)bv.y, (int)bv.z, (int)bv.w, 0, 0, 0, 0};
+        sb[j] = live ? Wsc[wrow[j] * SK + sc_off] : 0;
+      }
+      {
+        i32x8 af;
+        int sa;
+        afrag(0, af, sa);
 #pragma unroll
-        for (int ii = 0; ii < 2; ++ii)
-          acc[ii][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[ii], bf, acc[ii][j], 0, 4, 0, sa[ii], 0, sb);
+        for (int j = 0; j < 2; ++j)
+          acc[0][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af, bf[j], acc[0][j], 0, 4, 0, sa, 0, sb[j]);
+      }
+      if (upper) {
+        i32x8 af;
+        int sa;
+        afrag(1, af, sa);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[1][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af, bf[j], acc[1][j], 0, 4, 0, sa, 0, sb[j]);
       }
     }
     load_b(u, st + DEPTH);
@@ -300,6 +342,7 @@ int qmm_grouped_mxfp4(int mode, int fused, int act, int64_t max_tiles, int64_t k
                       int64_t x_rows, const void *w, const void *ws, const void *w2, const void *ws2, float *y,
                       hipStream_t s) {
   if (k % 64 || k > 12288) return QMM_ERR_SHAPE;   // the workgroup stages (64 + 256) x K / 32 scale bytes in LDS
+  if (x_rows * k >= (1ll << 31)) return QMM_ERR_SHAPE;   // activation rows are addressed by a 32-bit buffer offset
   if (!x_scales || !ws) return QMM_ERR_NULL;
   if (!aligned(x_scales, 2)) return QMM_ERR_ALIGN;
   if (!aligned(x, 16) || !aligned(w, 16) || (w2 && !aligned(w2, 16))) return QMM_ERR_ALIGN;

@@ -40,7 +40,8 @@ def _check(y, want, what):
     np.testing.assert_allclose(y, want, atol=3e-2 * float(np.std(want)), rtol=1e-2)
 
 
-@pytest.mark.parametrize("M,N,K", [(512, 4096, 4096), (70, 200, 768), (64, 128, 256), (130, 384, 1280)])
+@pytest.mark.parametrize("M,N,K", [(512, 4096, 4096), (70, 200, 768), (64, 128, 256), (130, 384, 1280),
+                                   (64, 128, 8192)])   # K = 8192: the kernel without the staged scale table
 def test_gemm_f32_out(dev, M, N, K):
     import qmm.ops as ops
     wt, xt, want, _, _ = _case(dev, M, N, K, seed=M + N + K)
