@@ -21,12 +21,12 @@
 // Tiling: a workgroup of four waves owns one 64-row expert tile; each wave computes 64 rows x 64 weight columns
 // (2 x 2 MFMA blocks) over all of K. gu: wave w owns output columns 32 w .. 32 w + 31 of a 128-column block, its
 // two column blocks being those columns of the gate and of the up matrix, so the activation is applied in
-// registers. dn: four 64-column quarters of a 256-column block. Tiles are dealt to the eight XCDs round-robin
+// registers. dn: wave w owns the 32 columns 32 w .. 32 w + 31 of a 128-column block. Tiles are dealt to the eight XCDs round-robin
 // (workgroup b runs on XCD b % 8): the bucket writes the live tiles first, and a tile-major order would leave
 // the XCDs that get the trailing, unused tiles idle; a tile's column blocks stay on one XCD, sharing its
 // activation rows in that L2.
 //
-// Steps. All E8M0 scales of the workgroup (its 64 activation rows and 128 + 128 or 256 weight columns, K / 32
+// Steps. All E8M0 scales of the workgroup (its 64 activation rows and 128 + 128 or 128 weight columns, K / 32
 // bytes each) are staged in LDS once; per-step byte loads of scales through the vector memory path cost more than
 // the weight stream. A super-step covers kSub 64-value chunks: the tile's activation codes for it are staged in
 // LDS (double-buffered, one barrier per super-step) and the weights stream straight into registers one super-step
@@ -124,11 +124,12 @@ __device__ __forceinline__ void copy_to_lds(u8 *dst, const u8 *src, int64_t n, i
 
 template <int KIND, int DEPTH>
 __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs a) {
-  constexpr int BN = KIND == kGU ? 128 : 256;
+  constexpr int BN = 128;                   // output columns per workgroup
+  constexpr int NJ = KIND == kGU ? 2 : 1;    // 32-column weight blocks per wave (gu: gate and up)
   __shared__ __align__(16) u8 As[2][BM][APITCH];
   __shared__ int src_row[BM];
   // Every E8M0 scale the workgroup needs, staged once: the tile's 64 activation rows and the block's weight columns
-  // (gu: 128 gate then 128 up columns; dn: 256 columns), K / 32 bytes each. Per-step byte loads of scales through
+  // (gu: 128 gate then 128 up columns; dn: 128 columns), K / 32 bytes each. Per-step byte loads of scales through
   // the vector memory path (32 rows per instruction) would otherwise cost more than the weight stream itself.
   extern __shared__ __align__(16) u8 dyn_lds[];
   u8 *Asc = dyn_lds, *Wsc = dyn_lds + BM * (a.K / 32);
@@ -172,54 +173,35 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
 
   // ---- weights: this lane's two columns (gu: one column of the gate and of the up matrix) and K half
   const int h = lane >> 5, lc = lane & 31;
-  const u8 *nbj[2], *sbj[2];
-  int colj[2];
+  const u8 *nbj[NJ], *sbj[NJ];
+  const int col = n0 + 32 * wave + lc;       // the lane's output column
   if constexpr (KIND == kGU) {
     const u8 *gn = a.wn + (int64_t)expert * a.nib_ebytes, *gs = a.wsc + (int64_t)expert * a.sc_ebytes;
     nbj[0] = gn; sbj[0] = gs;
     if (a.wn2) { nbj[1] = a.wn2 + (int64_t)expert * a.nib_ebytes; sbj[1] = a.wsc2 + (int64_t)expert * a.sc_ebytes; }
     else { nbj[1] = gn + a.up_nib_off; sbj[1] = gs + a.up_sc_off; }
-    colj[0] = colj[1] = n0 + 32 * wave + lc;
   } else {
-    nbj[0] = nbj[1] = a.wn + (int64_t)expert * a.nib_ebytes;
-    sbj[0] = sbj[1] = a.wsc + (int64_t)expert * a.sc_ebytes;
-    colj[0] = n0 + 64 * wave + lc;
-    colj[1] = colj[0] + 32;
+    nbj[0] = a.wn + (int64_t)expert * a.nib_ebytes;
+    sbj[0] = a.wsc + (int64_t)expert * a.sc_ebytes;
   }
-  const u8 *wcn[2];
+  const u8 *wcn[NJ];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int col = colj[j] < N ? colj[j] : N - 1;
-    wcn[j] = nbj[j] + (int64_t)col * (K / 2) + 16 * h;
-  }
-  // the scale rows: activation rows (a gathered row each), then the weight column blocks (contiguous in memory)
-  batched_copy(reinterpret_cast<u16 *>(Asc), (int64_t)BM * (SK / 2), tid, [&](int64_t i) {
-    const int r = (int)(i / (SK / 2)), q = (int)(i % (SK / 2));
-    const int sr = src_row[r] >= 0 ? src_row[r] : 0;
-    return reinterpret_cast<const u16 *>(a.xs + (int64_t)sr * SK)[q];
-  });
-  {
-    const int nblk = KIND == kGU ? 2 : 1, bcols = KIND == kGU ? 128 : 256;
-    const int cols = N - n0 < bcols ? N - n0 : bcols;   // columns past N are never stored
+  for (int j = 0; j < NJ; ++j) wcn[j] = nbj[j] + (int64_t)(col < N ? col : N - 1) * (K / 2) + 16 * h;
+  int wrow[NJ];   // the lane's weight columns as rows of Wsc (gu: the gate block, then the up block)
 #pragma unroll
-    for (int m = 0; m < nblk; ++m)
-      copy_to_lds(Wsc + m * 128 * SK, sbj[m] + (int64_t)n0 * SK, (int64_t)cols * SK, tid);
-  }
-  int wrow[2];   // the lane's columns as rows of Wsc
-#pragma unroll
-  for (int j = 0; j < 2; ++j) wrow[j] = (KIND == kGU ? 128 * j + 32 * wave : 64 * wave + 32 * j) + lc;
+  for (int j = 0; j < NJ; ++j) wrow[j] = 128 * j + 32 * wave + lc;
 
-  f32x16 acc[2][2];
+  f32x16 acc[2][NJ];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   // Rings DEPTH super-steps deep. A super-step reads kSub consecutive 32-byte chunks of each weight column -- a
   // whole 128-byte line for kSub = 4 -- with back-to-back loads, so the L1 merges them into one request per line.
-  v4u aring[DEPTH][kSub], bring[DEPTH][kSub][2];
+  v4u aring[DEPTH][kSub], bring[DEPTH][kSub][NJ];
   auto load_a = [&](int slot, int st) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < kSub; ++i)
@@ -227,7 +209,7 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
   };
   auto load_b = [&](int slot, int st) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int i = 0; i < kSub; ++i)
         bring[slot][i][j] = *reinterpret_cast<const v4u *>(wcn[j] + (int64_t)clampc(kSub * st + i) * 32);
@@ -236,12 +218,26 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
 #pragma unroll
     for (int i = 0; i < kSub; ++i) *reinterpret_cast<v4u *>(&As[buf][arow_i][KC * i + 16 * apart]) = aring[slot][i];
   };
+  // The first activation chunk, then the weights, so the stream is running while the scales are staged; staging
+  // the first chunk waits only for its own load (loads complete in issue order), and precedes the loads that
+  // reuse its ring slot.
   load_a(0, 0);
+  for_slots([&](auto uc) { constexpr int u = decltype(uc)::value; load_b(u, u); },
+            std::make_integer_sequence<int, DEPTH>{});
   stage(0, 0);
   for_slots([&](auto uc) { constexpr int u = decltype(uc)::value; load_a((u + 1) % DEPTH, u + 1); },
             std::make_integer_sequence<int, DEPTH>{});
-  for_slots([&](auto uc) { constexpr int u = decltype(uc)::value; load_b(u, u); },
-            std::make_integer_sequence<int, DEPTH>{});
+  // the scale rows: activation rows (a gathered row each), then the weight column blocks (contiguous in memory)
+  batched_copy(reinterpret_cast<u16 *>(Asc), (int64_t)BM * (SK / 2), tid, [&](int64_t i) {
+    const int r = (int)(i / (SK / 2)), q = (int)(i % (SK / 2));
+    const int sr = src_row[r] >= 0 ? src_row[r] : 0;
+    return reinterpret_cast<const u16 *>(a.xs + (int64_t)sr * SK)[q];
+  });
+  {
+    const int cols = N - n0 < BN ? N - n0 : BN;   // columns past N are never stored
+#pragma unroll
+    for (int m = 0; m < NJ; ++m) copy_to_lds(Wsc + m * BN * SK, sbj[m] + (int64_t)n0 * SK, (int64_t)cols * SK, tid);
+  }
   __syncthreads();
 
   // The super-step count is rounded up to a multiple of DEPTH. A padding chunk (c >= C) runs with both E8M0 scales
@@ -263,10 +259,10 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
         af = i32x8{(int)v0.x, (int)v0.y, (int)v0.z, (int)v0.w, (int)v1.x, (int)v1.y, (int)v1.z, (int)v1.w};
         sa = live ? Asc[(32 * ii + lc) * SK + sc_off] : 0;
       };
-      i32x8 bf[2];
-      int sb[2];
+      i32x8 bf[NJ];
+      int sb[NJ];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < NJ; ++j) {
         const v4u bv = bring[u][i][j];
         bf[j] = i32x8{(int)bv.x, (int)bv.y, (int)bv.z, (int)bv.w, 0, 0, 0, 0};
         sb[j] = live ? Wsc[wrow[j] * SK + sc_off] : 0;
@@ -276,7 +272,7 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
         int sa;
         afrag(0, af, sa);
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < NJ; ++j)
           acc[0][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af, bf[j], acc[0][j], 0, 4, 0, sa, 0, sb[j]);
       }
       if (upper) {
@@ -284,7 +280,7 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
         int sa;
         afrag(1, af, sa);
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < NJ; ++j)
           acc[1][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af, bf[j], acc[1][j], 0, 4, 0, sa, 0, sb[j]);
       }
     }
@@ -298,29 +294,25 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
   for (int s0 = 0; s0 < SP; s0 += DEPTH)
     for_steps(step, s0, std::make_integer_sequence<int, DEPTH>{});
 
-  constexpr int NJ = KIND == kGU ? 1 : 2;   // gu: one output column per lane (gate j = 0, up j = 1)
+  if (col >= N) return;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < NJ; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int lr = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-        const int col = colj[j];
-        if (col >= N) continue;
-        float v = 0.f;
-        if (src_row[lr] >= 0) {
-          if constexpr (KIND == kGU) v = act_fn(a.act, acc[i][0][r], acc[i][1][r]);
-          else v = acc[i][j][r];
-        }
-        a.y[(int64_t)(m0 + lr) * N + col] = v;
+    for (int r = 0; r < 16; ++r) {
+      const int lr = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+      float v = 0.f;
+      if (src_row[lr] >= 0) {
+        if constexpr (KIND == kGU) v = act_fn(a.act, acc[i][0][r], acc[i][1][r]);
+        else v = acc[i][0][r];
       }
+      a.y[(int64_t)(m0 + lr) * N + col] = v;
+    }
 }
 
 template <int KIND>
 int launch(const MArgs &a, hipStream_t s) {
   const dim3 grid((unsigned)(8 * a.n_blocks * ((a.max_tiles + 7) / 8)));
-  const size_t dyn = (size_t)(BM + 256) * (a.K / 32);
+  const size_t dyn = (size_t)(BM + (KIND == kGU ? 256 : 128)) * (a.K / 32);
   if (dyn > 32768) {   // beyond the default dynamic LDS limit (K > 3276): raise it once
     static bool raised = false;
     if (!raised) {
@@ -366,7 +358,7 @@ int qmm_grouped_mxfp4(int mode, int fused, int act, int64_t max_tiles, int64_t k
   }
   a.nib_ebytes = nrow * n;
   a.sc_ebytes = srow * n;
-  a.n_blocks = (int)((n + 255) / 256);
+  a.n_blocks = (int)((n + 127) / 128);
   a.max_tiles = (int)max_tiles;
   return launch<kDN>(a, s);
 }
