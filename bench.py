@@ -6,6 +6,8 @@
 A step is one launch of the hot path over one batch of synthetic input:
 
     q4_k_gemv   (default) Q4_K decode GEMV, W [12288, 4096] (Qwen3-8B FFN gate/up), x bf16 [M, 4096], y f32
+    q4_k_gemv_q8  the same GEMV on the int8-activation path (the reference's default decode path): the bf16 rows are
+                quantized to Q8_1 inside the kernel and multiplied with exact int32 group dot products
     q4_0_gemv   Q4_0 decode GEMV, W [4096, 4096], x f32 [1, 4096], y f32
     q4_k_gemm   Q4_K prefill GEMM, x bf16 [512, 4096] (row scale to f16, then the MFMA GEMM), W [4096, 4096],
                 y bf16 [512, 4096] (Qwen3-8B attn o_proj)
@@ -69,9 +71,9 @@ class GemvWorkload:
     """Decode GEMV y = x W^T over rotated weight copies; one step = one qmm_mv launch."""
     metric, unit, bound = METRIC, "GB/s", "hbm"
 
-    def __init__(self, name, index, fmt, n, k, m, x_dtype, traffic_name):
+    def __init__(self, name, index, fmt, n, k, m, x_dtype, traffic_name, q8=False):
         self.name, self.index, self.fmt, self.n, self.k, self.m = name, index, fmt, n, k, m
-        self.x_dtype, self.traffic_name = x_dtype, traffic_name
+        self.x_dtype, self.traffic_name, self.q8 = x_dtype, traffic_name, q8
 
     def setup(self, dev):
         import torch
@@ -94,7 +96,10 @@ class GemvWorkload:
         self.copies = copies
 
     def step(self, i):
-        self.ops.mv(self.fmt, self.ws[i % self.copies], self.x, self.n, self.k, y=self.y)
+        if self.q8:
+            self.ops.mv_q8(self.fmt, self.ws[i % self.copies], self.x, self.n, self.k, y=self.y)
+        else:
+            self.ops.mv(self.fmt, self.ws[i % self.copies], self.x, self.n, self.k, y=self.y)
 
     kernel_step = None
 
@@ -102,6 +107,8 @@ class GemvWorkload:
         return self.alg_bytes() / sec / 1e9
 
     def dtype(self):
+        if self.q8:
+            return f"{self.fmt} x int8 (Q8_1 of {self.x_dtype}, quantized in the kernel) -> f32, int32 group dots"
         return "q4_k x bf16 -> f32" if self.fmt == "q4_k" else "q4_0 x f32 -> f32"
 
     def alg_bytes(self):
@@ -112,15 +119,17 @@ class GemvWorkload:
         return 2 * self.m * self.n * self.k
 
     def cpu_baseline(self, budget):
-        from oracle import cpu_baseline
-        sec, runs, threads = cpu_baseline.time_gemv(self.fmt, self.raw, self.n, self.k, self.x_host, budget_s=budget)
+        from oracle import cpu_baseline, ref
+        x = ref.q8_1(self.x_host) if self.q8 else self.x_host
+        sec, runs, threads = cpu_baseline.time_gemv(self.fmt, self.raw, self.n, self.k, x, budget_s=budget)
         return {"value": round(self.alg_bytes() / sec / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
                 "sample": f"{runs} full {self.fmt} GEMVs (N={self.n}, K={self.k}, M={self.m}): numpy oracle dequant "
                           f"in 256-row chunks + f32 matmul on {threads} threads, median {sec * 1e3:.1f} ms per GEMV"}
 
     def config(self):
         return {"workload": self.name, "format": self.fmt, "N": self.n, "K": self.k, "M": self.m,
-                "x_dtype": self.x_dtype, "y_dtype": "f32", "weight_copies_rotated": self.copies,
+                "x_dtype": self.x_dtype, "activations": "q8_1" if self.q8 else self.x_dtype, "y_dtype": "f32",
+                "weight_copies_rotated": self.copies,
                 "rotated_bytes": self.copies * self.wbytes}
 
 
@@ -366,12 +375,17 @@ def _q4k_gemv(m):
                         f"mv_q4k_kernel.q4_k_gemv_n12288_k4096_m{m or 1}")
 
 
+def _q4k_gemv_q8(m):
+    return GemvWorkload("q4_k_gemv_q8", 1, "q4_k", 12288, 4096, m or 1, "bf16",
+                        f"mv_q4k_q8_kernel.q4_k_gemv_q8_n12288_k4096_m{m or 1}", q8=True)
+
+
 def _q40_gemv(m):
     return GemvWorkload("q4_0_gemv", 0, "q4_0", 4096, 4096, m or 1, "f32",
                         f"mv_kernel_q4_0.q4_0_gemv_n4096_k4096_m{m or 1}")
 
 
-WORKLOADS = {"q4_k_gemv": _q4k_gemv, "q4_0_gemv": _q40_gemv, "q4_k_gemm": GemmWorkload,
+WORKLOADS = {"q4_k_gemv": _q4k_gemv, "q4_k_gemv_q8": _q4k_gemv_q8, "q4_0_gemv": _q40_gemv, "q4_k_gemm": GemmWorkload,
              "mxfp4_moe": lambda m: MoeWorkload("mxfp4_moe", 3, m), "q4_k_moe": lambda m: MoeWorkload("q4_k_moe", 4, m),
              "hbm_copy": CopyWorkload}
 

@@ -38,7 +38,13 @@ enum qmm_status {
 };
 
 enum qmm_format { QMM_Q4_0 = 0, QMM_Q4_K = 1, QMM_MXFP4 = 2, QMM_MXFP4S = 3 };
-enum qmm_dtype { QMM_F32 = 0, QMM_F16 = 1, QMM_BF16 = 2, QMM_MXFP8 = 3 /* E4M3 codes + E8M0 per 32 */ };
+enum qmm_dtype {
+  QMM_F32 = 0,
+  QMM_F16 = 1,
+  QMM_BF16 = 2,
+  QMM_MXFP8 = 3, /* E4M3 codes + E8M0 per 32 */
+  QMM_Q8 = 4     /* planar Q8_1: int8 codes [rows, K], then at byte rows*K f32 (f16-rounded d, code sum) per 32 */
+};
 enum qmm_gemm_mode { QMM_GEMM_STORE = 0, QMM_GEMM_ACC = 1, QMM_GEMM_SWIGLU = 2 };
 enum qmm_act { QMM_ACT_SILU = 0, QMM_ACT_SWIGLU_OAI = 1 };
 
@@ -64,6 +70,22 @@ int qmm_dequant(int fmt, const void *w, const void *ws, int64_t rows, int64_t k,
  * whatever `tokens` is, so a multi-token call equals one-token calls bit for bit. */
 int qmm_mv(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
            const void *w, const void *ws, float *y, qmm_stream_t stream);
+
+/* Q8_1 activation quantizer, g_quant_q8 (S/gen_llm.py:684-749; llama.cpp quantize_q8_1): per group of 32 values
+ * d = amax / 127, q = sign(x/d) floor(|x/d| + 1/2) (0 when d = 0). x: f32 or bf16 [rows, k], k % 32 == 0; xq: the
+ * planar buffer (QMM_Q8) of rows * k code bytes followed by rows * k / 32 f32 pairs (f16-rounded d, sum of codes),
+ * 16-byte aligned. */
+int qmm_quant_q8(int64_t rows, int64_t k, const void *x, int x_dtype, void *xq, qmm_stream_t stream);
+
+/* Decode matrix-vector product on Q8_1 activations, the g_mv_{fmt}_k{K}[_t{TG}]_q8[_r{R}] family
+ * (S/gen_llm.py:1288-1301, iq_dot :1024-1071; the reference's default decode path): per 32-value group an exact
+ * integer dot di of weight codes and activation codes, then for Q4_K (di d sc_g - xs dmin m_g) da and for Q4_0
+ * (d da) di with codes q - 8, summed in f32. fmt QMM_Q4_K (k % 256 == 0) or QMM_Q4_0 (k % 64 == 0). x: the planar
+ * buffer of qmm_quant_q8 (x_dtype QMM_Q8) for tokens rows, or -- Q4_K with k = 4096 or 8192 only -- f32 / bf16
+ * [tokens, k] rows, quantized inside the kernel exactly as qmm_quant_q8 does (same result bit for bit). y: f32
+ * [tokens, n]. A multi-token call equals one-token calls bit for bit. */
+int qmm_mv_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
+              const void *w, float *y, qmm_stream_t stream);
 
 /* Prefill GEMM, the g_gemm_{fmt}_{store|acc|swiglu}[_m128|_m256] family
  * (S/gen_gemm.py:535-703, :706, :1224; launch args S/gen_gemm.py:549-556):

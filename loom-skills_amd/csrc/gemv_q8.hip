@@ -1,0 +1,422 @@
+// Decode matvecs on Q8_1 activations, the reference's default decode path (ACT_Q8 = 1, S/gen_llm.py:519):
+//
+//   qmm_quant_q8   x f32 / bf16 [rows, K] -> planar Q8_1               g_quant_q8, S/gen_llm.py:684-749
+//   qmm_mv_q8      y[t, r] (+)= sum over 32-value groups g of the row   g_mv_{fmt}_k{K}[_t{TG}]_q8[_r{R}],
+//                                                                        S/gen_llm.py:1288-1301
+//
+// Planar Q8_1 (the reference's layout): int8 codes [rows][K/32][32], then at byte rows * K the f32 pairs
+// (f16-rounded d, sum of the group's codes) [rows][K/32][2]. Per group of 32 (llama.cpp quantize_q8_1, oracle
+// make_kernel_tests.py:32-39): d = amax / 127, q = sign(x/d) floor(|x/d| + 1/2), q = 0 when d = 0.
+//
+// Weight side (iq_dot, S/gen_llm.py:1024-1071): a group's integer dot di = sum q_w q_x is exact (v_dot4_i32_i8
+// over eight dwords). Q4_K keeps its unsigned 4-bit codes; with sc = d sc_g and mn = dmin m_g (f32) the group adds
+// (di sc - xs mn) da, da the f16-rounded activation scale and xs the code sum. Q4_0 codes are q - 8: di is taken on
+// the unsigned nibbles and 8 xs subtracted (the same integer), and the group adds (sc da) di with sc = d.
+//
+// Kernels. The quantizer gives each 32-value group to four consecutive lanes (8 values each). The generic matvec
+// is the item walk of gemv.hip with Q8 activation fragments (any K % 256 for Q4_K, K % 64 for Q4_0). The Q4_K fast
+// path (K = 4096, 8192) is the layout of gemv_q4k.hip -- a lane owns half a super-block, five 128-bit weight loads
+// -- with the token's codes and group pairs staged once per workgroup in LDS; given f32 / bf16 activations it
+// quantizes them while staging, with the quantizer's own arithmetic, so both input forms give identical results.
+#include "bfly.hpp"
+
+using namespace qmm;
+
+namespace {
+
+typedef __attribute__((ext_vector_type(4))) u32 v4u;
+typedef __attribute__((ext_vector_type(2))) u32 v2u;
+
+__device__ __forceinline__ int sdot4(u32 a, u32 b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// 8 activations of the lane as f32: from 16 bytes of bf16 or 32 bytes of f32 at element offset e
+__device__ __forceinline__ void load8_act(const void *x, bool bf, int64_t e, float (&v)[8]) {
+  if (bf) {
+    const v4u q = *reinterpret_cast<const v4u *>(static_cast<const u16 *>(x) + e);
+    const u32 d[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { v[2 * j] = bf16_to_f32(d[j] & 0xFFFFu); v[2 * j + 1] = bf16_to_f32(d[j] >> 16); }
+  } else {
+    const v4u a = *reinterpret_cast<const v4u *>(static_cast<const float *>(x) + e);
+    const v4u b = *reinterpret_cast<const v4u *>(static_cast<const float *>(x) + e + 4);
+    const u32 d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = u32_as_f32(d[j]);
+  }
+}
+
+// One 32-value group held by four consecutive lanes of a wave (8 values each, the group's first lane a multiple of
+// 4): the lane's 8 codes as two dwords, and the group's f16-rounded d and code sum.
+__device__ __forceinline__ void q8_group4(const float (&v)[8], u32 &c0, u32 &c1, float &d16, float &sum) {
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  const float d = amax / 127.f;
+  int s = 0;
+  u32 c[2] = {0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float t = d > 0.f ? v[i] / d : 0.f;
+    const int q = (int)copysignf(floorf(fabsf(t) + 0.5f), t);
+    s += q;
+    c[i >> 2] |= ((u32)q & 0xFFu) << (8 * (i & 3));
+  }
+  s += __shfl_xor(s, 1, 64);
+  s += __shfl_xor(s, 2, 64);
+  c0 = c[0];
+  c1 = c[1];
+  d16 = (float)(_Float16)d;
+  sum = (float)s;
+}
+
+// --------------------------------------------------------------------------------------------- quantizer
+__global__ __launch_bounds__(256) void quant_q8_kernel(int64_t rows, int64_t k, const void *__restrict__ x, int bf,
+                                                       u8 *__restrict__ xq) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;   // 8-value chunk
+  const int64_t chunks = rows * (k / 8);
+  const bool in = i < chunks;
+  const int64_t ic = in ? i : chunks - 1;                       // the group's lanes stay together (chunks % 4 == 0)
+  float v[8];
+  load8_act(x, bf, ic * 8, v);
+  u32 c0, c1;
+  float d16, sum;
+  q8_group4(v, c0, c1, d16, sum);
+  if (!in) return;
+  reinterpret_cast<v2u *>(xq)[ic] = v2u{c0, c1};
+  if ((threadIdx.x & 3) == 0) {
+    float *meta = reinterpret_cast<float *>(xq + rows * k);
+    reinterpret_cast<float2 *>(meta)[ic / 4] = make_float2(d16, sum);
+  }
+}
+
+// ------------------------------------------------------------------------------------ generic matvec
+// Activation fragment of an item of 64 values = groups A and B: 8 code dwords each and their (d, code sum).
+struct XQ {
+  u32 a[8], b[8];
+  float da, sa, db, sb;
+};
+
+__device__ __forceinline__ void xq_load(const u8 *codes, const float *meta, int64_t g, bool live, XQ &x) {
+  const v4u *c = reinterpret_cast<const v4u *>(codes + 32 * g);
+  const v4u m = live ? *reinterpret_cast<const v4u *>(meta + 2 * g) : v4u{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const v4u p = live ? c[i] : v4u{0u, 0u, 0u, 0u}, q = live ? c[2 + i] : v4u{0u, 0u, 0u, 0u};
+    x.a[4 * i] = p.x; x.a[4 * i + 1] = p.y; x.a[4 * i + 2] = p.z; x.a[4 * i + 3] = p.w;
+    x.b[4 * i] = q.x; x.b[4 * i + 1] = q.y; x.b[4 * i + 2] = q.z; x.b[4 * i + 3] = q.w;
+  }
+  x.da = u32_as_f32(m.x); x.sa = u32_as_f32(m.y); x.db = u32_as_f32(m.z); x.sb = u32_as_f32(m.w);
+}
+
+// Q4_K: item = 4 * block + page j; groups 8 block + 2 j (low nibbles) and + 1 (high nibbles)
+struct Q4K8 {
+  struct W { v4u h, q0, q1; };
+  static __device__ __forceinline__ int items(int64_t k) { return (int)(k / 256) * 4; }
+  static __device__ __forceinline__ int64_t group(int item) { return (int64_t)(item >> 2) * 8 + 2 * (item & 3); }
+  static __device__ __forceinline__ void load_w(const u8 *row, int item, bool live, W &w) {
+    const u8 *b = row + (int64_t)(item >> 2) * 144;
+    const int j = item & 3;
+    const v4u z{0u, 0u, 0u, 0u};
+    w.h = live ? *reinterpret_cast<const v4u *>(b) : z;
+    w.q0 = live ? *reinterpret_cast<const v4u *>(b + 16 + 32 * j) : z;
+    w.q1 = live ? *reinterpret_cast<const v4u *>(b + 32 + 32 * j) : z;
+  }
+  static __device__ __forceinline__ float dot(const W &w, const XQ &x, int item) {
+    const int j = item & 3;
+    u32 sc0, m0, sc1, m1;
+    q4k_scale_min(w.h.y, w.h.z, w.h.w, 2 * j, sc0, m0);
+    q4k_scale_min(w.h.y, w.h.z, w.h.w, 2 * j + 1, sc1, m1);
+    const float d = f16_to_f32(w.h.x), dmin = f16_to_f32(w.h.x >> 16);
+    const u32 q[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+    int ia = 0, ib = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      ia = sdot4(q[i] & 0x0F0F0F0Fu, x.a[i], ia);
+      ib = sdot4((q[i] >> 4) & 0x0F0F0F0Fu, x.b[i], ib);
+    }
+    const float ga = ((float)ia * (d * (float)sc0) - x.sa * (dmin * (float)m0)) * x.da;
+    const float gb = ((float)ib * (d * (float)sc1) - x.sb * (dmin * (float)m1)) * x.db;
+    return ga + gb;
+  }
+};
+
+// Q4_0: item = pair of blocks p (36 bytes at 36 p, 4-byte aligned when K % 64 == 0); groups 2 p and 2 p + 1
+struct Q408 {
+  struct W { u32 v[9]; };
+  static __device__ __forceinline__ int items(int64_t k) { return (int)(k / 64); }
+  static __device__ __forceinline__ int64_t group(int item) { return 2 * (int64_t)item; }
+  static __device__ __forceinline__ void load_w(const u8 *row, int item, bool live, W &w) {
+    const u32 *p = reinterpret_cast<const u32 *>(row + (int64_t)item * 36);
+#pragma unroll
+    for (int i = 0; i < 9; ++i) w.v[i] = live ? p[i] : 0u;
+  }
+  static __device__ __forceinline__ float dot(const W &w, const XQ &x, int) {
+    const float d[2] = {f16_to_f32(w.v[0]), f16_to_f32(w.v[4] >> 16)};
+    const u32 q0[4] = {__builtin_amdgcn_alignbit(w.v[1], w.v[0], 16), __builtin_amdgcn_alignbit(w.v[2], w.v[1], 16),
+                       __builtin_amdgcn_alignbit(w.v[3], w.v[2], 16), __builtin_amdgcn_alignbit(w.v[4], w.v[3], 16)};
+    const u32 q1[4] = {w.v[5], w.v[6], w.v[7], w.v[8]};
+    // a block's low nibbles are its values 0..15 (activation dwords 0..3), its high nibbles values 16..31
+    int ia = 0, ib = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ia = sdot4(q0[i] & 0x0F0F0F0Fu, x.a[i], ia);
+      ia = sdot4((q0[i] >> 4) & 0x0F0F0F0Fu, x.a[4 + i], ia);
+      ib = sdot4(q1[i] & 0x0F0F0F0Fu, x.b[i], ib);
+      ib = sdot4((q1[i] >> 4) & 0x0F0F0F0Fu, x.b[4 + i], ib);
+    }
+    ia -= 8 * (int)x.sa;   // codes q - 8: the code sum is an exact integer
+    ib -= 8 * (int)x.sb;
+    return (d[0] * x.da) * (float)ia + (d[1] * x.db) * (float)ib;
+  }
+};
+
+constexpr int kWaves = 4, kRW = 4;
+
+template <class P, int TG>
+__global__ __launch_bounds__(256) void mv_q8_kernel(int64_t n, int64_t tokens, int64_t k, int accumulate,
+                                                    const u8 *__restrict__ codes, const float *__restrict__ meta,
+                                                    const u8 *__restrict__ w, int64_t rb, float *__restrict__ y) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t t0 = (int64_t)blockIdx.x * TG;
+  const int64_t row0 = ((int64_t)blockIdx.y * kWaves + wave) * kRW;
+  if (row0 >= n) return;
+  const int nitems = P::items(k);
+  const int64_t G = k / 32;
+  float acc[kRW][TG];
+#pragma unroll
+  for (int r = 0; r < kRW; ++r)
+#pragma unroll
+    for (int t = 0; t < TG; ++t) acc[r][t] = 0.f;
+  for (int it0 = 0; it0 < nitems; it0 += 64) {
+    const int item = it0 + lane;
+    const bool live = item < nitems;
+    XQ xs[TG];
+#pragma unroll
+    for (int t = 0; t < TG; ++t) {
+      const int64_t tok = t0 + t;
+      xq_load(codes + tok * k, meta + 2 * tok * G, P::group(item), live && tok < tokens, xs[t]);
+    }
+    typename P::W wv[kRW];
+#pragma unroll
+    for (int r = 0; r < kRW; ++r) P::load_w(w + (row0 + r) * rb, item, live && (row0 + r) < n, wv[r]);
+#pragma unroll
+    for (int r = 0; r < kRW; ++r)
+#pragma unroll
+      for (int t = 0; t < TG; ++t) acc[r][t] += P::dot(wv[r], xs[t], item);
+  }
+#pragma unroll
+  for (int r = 0; r < kRW; ++r)
+#pragma unroll
+    for (int t = 0; t < TG; ++t) acc[r][t] = wave_sum(acc[r][t]);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < kRW; ++r)
+#pragma unroll
+      for (int t = 0; t < TG; ++t) {
+        const int64_t row = row0 + r, tok = t0 + t;
+        if (row < n && tok < tokens) {
+          float *py = y + tok * n + row;
+          *py = accumulate ? *py + acc[r][t] : acc[r][t];
+        }
+      }
+  }
+}
+
+// ------------------------------------------------------------------------------ Q4_K fast path (K 4096 / 8192)
+constexpr int kFWaves = 8, kFThreads = kFWaves * 64;
+
+template <int TG, int KB, bool STAGEQ>
+__global__ __launch_bounds__(kFThreads) void mv_q4k_q8_kernel(int64_t n, int64_t tokens, int accumulate,
+                                                               const void *__restrict__ x, int bf,
+                                                               const u8 *__restrict__ w, float *__restrict__ y) {
+  constexpr int K = KB * 4096;
+  constexpr int L = 32 * KB;            // lanes per row
+  constexpr int RPP = 64 / L;           // rows per wave
+  constexpr int WG_ROWS = kFWaves * RPP;
+  constexpr int64_t RB = (int64_t)K / 256 * 144;
+  constexpr int NCH = K / 8;            // 8-value chunks of a token row
+  constexpr int CPT = (NCH + kFThreads - 1) / kFThreads;
+
+  __shared__ __align__(16) u32 xc[TG][K / 4];         // int8 codes
+  __shared__ __align__(16) float xm[TG][K / 32][2];   // (f16-rounded d, code sum) per group
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t t0 = (int64_t)blockIdx.y * TG;
+  const int64_t wrow0 = (int64_t)blockIdx.x * WG_ROWS + wave * RPP;
+  const int rp = lane / L, item = lane % L, b = item >> 1, h = item & 1;
+
+  // ---- activation loads first, then the weights (vector loads complete in issue order)
+  float xv[TG][CPT][8];
+  v4u qv[TG][CPT];
+#pragma unroll
+  for (int t = 0; t < TG; ++t) {
+    const int64_t tok = t0 + t < tokens ? t0 + t : tokens - 1;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + i * kFThreads;
+      const int cc = c < NCH ? c : NCH - 1;
+      if constexpr (STAGEQ) {
+        load8_act(x, bf, tok * K + 8 * cc, xv[t][i]);
+      } else {
+        // planar: 8 codes = 2 dwords; the 16-byte read covers chunks cc and cc + 1 (taken by even threads only)
+        qv[t][i] = *reinterpret_cast<const v4u *>(static_cast<const u8 *>(x) + tok * K + 8 * (cc & ~1));
+      }
+    }
+  }
+  v4u wd[5];
+  {
+    int64_t row = wrow0 + rp;
+    row = row < n ? row : n - 1;        // rows past n read row n-1 and are never stored
+    const v4u *bp = reinterpret_cast<const v4u *>(w + row * RB + (int64_t)b * 144);
+    wd[0] = bp[0];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wd[1 + i] = bp[1 + 4 * h + i];
+  }
+
+  // ---- stage the codes and group pairs
+#pragma unroll
+  for (int t = 0; t < TG; ++t) {
+    const int64_t tok = t0 + t < tokens ? t0 + t : tokens - 1;
+    if constexpr (STAGEQ) {
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        const int c = tid + i * kFThreads;
+        if (c >= NCH) break;            // whole waves: NCH and kFThreads are multiples of 64
+        u32 c0, c1;
+        float d16, sum;
+        q8_group4(xv[t][i], c0, c1, d16, sum);
+        xc[t][2 * c] = c0;
+        xc[t][2 * c + 1] = c1;
+        if ((c & 3) == 0) { xm[t][c >> 2][0] = d16; xm[t][c >> 2][1] = sum; }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        const int c = tid + i * kFThreads;
+        if (c < NCH && (c & 1) == 0) *reinterpret_cast<v4u *>(&xc[t][2 * c]) = qv[t][i];
+      }
+      const float *meta = reinterpret_cast<const float *>(static_cast<const u8 *>(x) + tokens * K) + tok * (K / 16);
+      for (int g = tid; g < K / 32; g += kFThreads) {
+        const float2 m = reinterpret_cast<const float2 *>(meta)[g];
+        xm[t][g][0] = m.x;
+        xm[t][g][1] = m.y;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- the lane's half super-block: pages 2h, 2h+1 = groups 8b + 4h + (0..3)
+  float acc[TG];
+  const v4u hd = wd[0];
+  const float d = f16_to_f32(hd.x), dmin = f16_to_f32(hd.x >> 16);
+  const u32 q[16] = {wd[1].x, wd[1].y, wd[1].z, wd[1].w, wd[2].x, wd[2].y, wd[2].z, wd[2].w,
+                     wd[3].x, wd[3].y, wd[3].z, wd[3].w, wd[4].x, wd[4].y, wd[4].z, wd[4].w};
+#pragma unroll
+  for (int t = 0; t < TG; ++t) {
+    const int g0 = 8 * b + 4 * h;
+    float part = 0.f;
+#pragma unroll
+    for (int pg = 0; pg < 2; ++pg) {
+      const v4u *xa = reinterpret_cast<const v4u *>(&xc[t][8 * (g0 + 2 * pg)]);   // group g0 + 2 pg
+      const v4u *xb = reinterpret_cast<const v4u *>(&xc[t][8 * (g0 + 2 * pg + 1)]);
+      const v4u a0 = xa[0], a1 = xa[1], b0 = xb[0], b1 = xb[1];
+      const u32 av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      const u32 bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+      int ia = 0, ib = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const u32 Q = q[8 * pg + i];
+        ia = sdot4(Q & 0x0F0F0F0Fu, av[i], ia);
+        ib = sdot4((Q >> 4) & 0x0F0F0F0Fu, bv[i], ib);
+      }
+      u32 sc0, m0, sc1, m1;
+      q4k_scale_min(hd.y, hd.z, hd.w, 4 * h + 2 * pg, sc0, m0);
+      q4k_scale_min(hd.y, hd.z, hd.w, 4 * h + 2 * pg + 1, sc1, m1);
+      const float *ma = xm[t][g0 + 2 * pg], *mb = xm[t][g0 + 2 * pg + 1];
+      part += ((float)ia * (d * (float)sc0) - ma[1] * (dmin * (float)m0)) * ma[0];
+      part += ((float)ib * (d * (float)sc1) - mb[1] * (dmin * (float)m1)) * mb[0];
+    }
+    acc[t] = part;
+  }
+
+  int idx;
+  const float tot = group_reduce<TG, L>(acc, lane, idx);
+  constexpr int low_mask = (L >> log2i(TG)) - 1;
+  if ((lane & low_mask) == 0) {
+    const int64_t row = wrow0 + rp, tok = t0 + idx;
+    if (row < n && tok < tokens) {
+      float *py = y + tok * n + row;
+      *py = accumulate ? *py + tot : tot;
+    }
+  }
+}
+
+template <int TG, int KB, bool STAGEQ>
+int launch_fast(int64_t n, int64_t tokens, int accumulate, const void *x, int bf, const void *w, float *y,
+                hipStream_t s) {
+  constexpr int WG_ROWS = kFWaves * (2 / KB);
+  const dim3 grid((unsigned)((n + WG_ROWS - 1) / WG_ROWS), (unsigned)((tokens + TG - 1) / TG));
+  mv_q4k_q8_kernel<TG, KB, STAGEQ><<<grid, kFThreads, 0, s>>>(n, tokens, accumulate, x, bf,
+                                                             static_cast<const u8 *>(w), y);
+  return launch_status();
+}
+
+template <int KB, bool STAGEQ>
+int launch_fast_tg(int64_t n, int64_t tokens, int accumulate, const void *x, int bf, const void *w, float *y,
+                   hipStream_t s) {
+  return tokens >= 2 ? launch_fast<2, KB, STAGEQ>(n, tokens, accumulate, x, bf, w, y, s)
+                     : launch_fast<1, KB, STAGEQ>(n, tokens, accumulate, x, bf, w, y, s);
+}
+
+}  // namespace
+
+extern "C" int qmm_quant_q8(int64_t rows, int64_t k, const void *x, int x_dtype, void *xq, qmm_stream_t stream) {
+  if (!x || !xq) return QMM_ERR_NULL;
+  if (x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
+  if (rows <= 0 || k <= 0 || k % 32 || rows > (1ll << 24)) return QMM_ERR_SHAPE;
+  if (!aligned(x, 16) || !aligned(xq, 16)) return QMM_ERR_ALIGN;
+  const int64_t chunks = rows * (k / 8);
+  quant_q8_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      rows, k, x, x_dtype == QMM_BF16, static_cast<u8 *>(xq));
+  return launch_status();
+}
+
+extern "C" int qmm_mv_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
+                         const void *w, float *y, qmm_stream_t stream) {
+  if (!x || !w || !y) return QMM_ERR_NULL;
+  if (fmt != QMM_Q4_K && fmt != QMM_Q4_0) return QMM_ERR_FORMAT;
+  if (x_dtype != QMM_Q8 && x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
+  if (k <= 0 || n <= 0 || tokens <= 0 || n > (1ll << 30) || tokens > (1ll << 24) || k > (1ll << 20))
+    return QMM_ERR_SHAPE;
+  if (fmt == QMM_Q4_K && k % 256) return QMM_ERR_SHAPE;
+  if (fmt == QMM_Q4_0 && k % 64) return QMM_ERR_SHAPE;
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 4)) return QMM_ERR_ALIGN;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool fast = fmt == QMM_Q4_K && (k == 4096 || k == 8192) && tokens <= 65535ll * 2;
+  if (x_dtype != QMM_Q8) {
+    // f32 / bf16 rows are quantized while staged; only the fast path stages (others take planar Q8 from
+    // qmm_quant_q8)
+    if (!fast) return QMM_ERR_SHAPE;
+    const int bf = x_dtype == QMM_BF16;
+    return k == 4096 ? launch_fast_tg<1, true>(n, tokens, accumulate, x, bf, w, y, s)
+                     : launch_fast_tg<2, true>(n, tokens, accumulate, x, bf, w, y, s);
+  }
+  if (fast)
+    return k == 4096 ? launch_fast_tg<1, false>(n, tokens, accumulate, x, 0, w, y, s)
+                     : launch_fast_tg<2, false>(n, tokens, accumulate, x, 0, w, y, s);
+  const u8 *codes = static_cast<const u8 *>(x);
+  const float *meta = reinterpret_cast<const float *>(codes + tokens * k);
+  const int64_t rb = fmt == QMM_Q4_K ? k / 256 * 144 : k / 32 * 18;
+  constexpr int TG = 2;
+  const dim3 grid((unsigned)((tokens + TG - 1) / TG), (unsigned)((n + kWaves * kRW - 1) / (kWaves * kRW)));
+  if (grid.x > 2147483647u || grid.y > 65535u) return QMM_ERR_SHAPE;
+  if (fmt == QMM_Q4_K)
+    mv_q8_kernel<Q4K8, TG><<<grid, 256, 0, s>>>(n, tokens, k, accumulate, codes, meta, static_cast<const u8 *>(w), rb, y);
+  else
+    mv_q8_kernel<Q408, TG><<<grid, 256, 0, s>>>(n, tokens, k, accumulate, codes, meta, static_cast<const u8 *>(w), rb, y);
+  return launch_status();
+}

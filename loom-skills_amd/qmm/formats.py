@@ -10,7 +10,7 @@ SPLIT = frozenset({"mxfp4s"})                                   # weight plane +
 SCALE_DIV = {"mxfp4s": 16}                                      # nibble-plane bytes per scale-plane byte
 
 CODE = {"q4_0": 0, "q4_k": 1, "mxfp4": 2, "mxfp4s": 3}          # enum qmm_format
-DTYPE = {"f32": 0, "f16": 1, "bf16": 2, "mxfp8": 3}             # enum qmm_dtype
+DTYPE = {"f32": 0, "f16": 1, "bf16": 2, "mxfp8": 3, "q8": 4}    # enum qmm_dtype
 MX_BLOCK = 32                                                   # values per E8M0 scale of an MXFP8 operand
 GEMM_MODE = {"store": 0, "acc": 1, "swiglu": 2}                 # enum qmm_gemm_mode
 ACT = {"silu": 0, "swiglu_oai": 1}                              # enum qmm_act

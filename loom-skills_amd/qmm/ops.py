@@ -75,6 +75,43 @@ def mv(fmt, w, x, n, k, y=None, accumulate=False, ws=None):
     return y
 
 
+def q8_bytes(rows, k):
+    """Bytes of the planar Q8_1 buffer of `rows` rows of k values: codes, then an f32 pair per 32 values."""
+    return rows * k + rows * (k // 32) * 8
+
+
+def quant_q8(x, xq=None):
+    """Planar Q8_1 (g_quant_q8, S/gen_llm.py:684-749) of f32 / bf16 rows x [rows, k]: a uint8 tensor of
+    q8_bytes(rows, k) bytes (int8 codes [rows, k], then f32 (f16-rounded d, code sum) per 32 values)."""
+    _dev(x, xq)
+    rows, k = x.shape
+    xq = torch.empty(q8_bytes(rows, k), dtype=torch.uint8, device=x.device) if xq is None else xq
+    _lib.call("qmm_quant_q8", rows, k, _ptr(x), _dt(x), _ptr(xq), _stream())
+    return xq
+
+
+def mv_q8(fmt, w, x, n, k, tokens=None, y=None, accumulate=False):
+    """The int8-activation decode matvec (g_mv_{fmt}_k{K}[_t{TG}]_q8, S/gen_llm.py:1288-1301): x is the planar Q8_1
+    buffer of `tokens` rows (uint8, from quant_q8), or f32 / bf16 rows [tokens, k], which the Q4_K K = 4096 / 8192
+    kernel quantizes itself and any other shape quantizes through quant_q8 first (identical results)."""
+    _dev(w, x, y)
+    if x.dtype == torch.uint8:
+        if tokens is None:
+            raise ValueError("a planar Q8_1 buffer needs its token count")
+        xd = DTYPE["q8"]
+    else:
+        tokens = x.shape[0]
+        if x.shape[-1] != k:
+            raise ValueError(f"x has {x.shape[-1]} columns, K is {k}")
+        if not (fmt == "q4_k" and k in (4096, 8192)):
+            x, xd = quant_q8(x), DTYPE["q8"]
+        else:
+            xd = _dt(x)
+    y = torch.empty((tokens, n), dtype=torch.float32, device=w.device) if y is None else y
+    _lib.call("qmm_mv_q8", CODE[fmt], k, n, tokens, int(bool(accumulate)), _ptr(x), xd, _ptr(w), _ptr(y), _stream())
+    return y
+
+
 def gemm(fmt, mode, x, w, n, k, w2=None, scales=None, out_dtype=torch.float32, y=None):
     """Y = (X16 W^T) inv (store) or Y += ... (acc). x is the row-scaled f16 operand with its scales (the reference's
     g_row_scale_f16 output), or bf16 / f32 rows, which are row-scaled here first (qmm_row_scale_f16)."""

@@ -71,14 +71,32 @@ def e4m3_decode(b):
 
 
 # ----------------------------------------------------------------------------------------- activation quantizers
-def q8_1(xs):
-    """llama.cpp quantize_q8_1 per 32 values: d = amax/127, q = sign(x/d) floor(|x/d| + 0.5), dequantized with the
-    f16-rounded d (make_kernel_tests.py:32-39)."""
-    g = np.asarray(xs, np.float32).reshape(xs.shape[0], -1, 32)
+def q8_1_codes(xs):
+    """llama.cpp quantize_q8_1 per 32 values in f32 arithmetic (make_kernel_tests.py:32-39; g_quant_q8,
+    S/gen_llm.py:684-749): d = amax/127, q = sign(x/d) floor(|x/d| + 0.5) (0 when d == 0). Returns the int8 codes
+    [rows, K], the stored scales f32(f16(d)) and the code sums, both [rows, K/32]."""
+    xs = np.asarray(xs, np.float32)
+    g = xs.reshape(xs.shape[0], -1, 32)
     d = np.abs(g).max(-1, keepdims=True) / np.float32(127)
     v = np.divide(g, d, out=np.zeros_like(g), where=d > 0)
-    q = np.sign(v) * np.floor(np.abs(v) + 0.5)
-    return (q * d.astype(np.float16).astype(np.float32)).reshape(xs.shape)
+    q = np.sign(v) * np.floor(np.abs(v) + np.float32(0.5))
+    codes = q.astype(np.int8).reshape(xs.shape)
+    return codes, d[..., 0].astype(np.float16).astype(np.float32), q.sum(-1, dtype=np.float32)
+
+
+def q8_1(xs):
+    """The Q8_1 activations as the oracle multiplies them: codes times the f16-rounded d (make_kernel_tests.py:32-39)."""
+    codes, d16, _ = q8_1_codes(xs)
+    g = codes.astype(np.float32).reshape(codes.shape[0], -1, 32)
+    return (g * d16[..., None]).reshape(codes.shape)
+
+
+def q8_planar(xs):
+    """The planar Q8_1 buffer of g_quant_q8 (S/gen_llm.py:684-690): int8 codes [rows][K/32][32], then at byte
+    rows * K the f32 pairs (f16-rounded d, code sum) [rows][K/32][2]; returned as uint8 bytes."""
+    codes, d16, sums = q8_1_codes(xs)
+    meta = np.stack([d16, sums], -1).astype(np.float32)
+    return np.concatenate([codes.view(np.uint8).reshape(-1), meta.view(np.uint8).reshape(-1)])
 
 
 def row_scale_exponent(x):

@@ -50,6 +50,29 @@ def test_q8_1_closed_form():
     assert g[1] == 3 * np.float32(np.float16(1.0)) and g[2] == -3.0
 
 
+def test_q8_1_codes_and_planar_layout():
+    """codes * f16(d) is q8_1; the group sum is the sum of codes; a zero group has d = 0 and zero codes; the planar
+    buffer holds the codes first and the (d, sum) pairs after rows * K bytes (S/gen_llm.py:684-690)."""
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((3, 96)) * np.exp(rng.uniform(-4, 4, (3, 1)))).astype(np.float32)
+    x[1, 32:64] = 0.0
+    codes, d16, sums = ref.q8_1_codes(x)
+    assert codes.dtype == np.int8 and codes.shape == x.shape and d16.shape == sums.shape == (3, 3)
+    assert np.array_equal(ref.q8_1(x), (codes.astype(np.float32).reshape(3, 3, 32) * d16[..., None]).reshape(3, 96))
+    assert np.array_equal(sums, codes.reshape(3, 3, 32).sum(-1).astype(np.float32))
+    assert d16[1, 1] == 0 and not codes[1, 32:64].any()
+    assert np.abs(codes.reshape(3, 3, 32)).max(-1).tolist() == [[127] * 3, [127, 0, 127], [127] * 3]
+    buf = ref.q8_planar(x)
+    assert buf.size == 3 * 96 + 3 * 3 * 8
+    assert np.array_equal(buf[:288].view(np.int8).reshape(3, 96), codes)
+    meta = buf[288:].view(np.float32).reshape(3, 3, 2)
+    assert np.array_equal(meta[..., 0], d16) and np.array_equal(meta[..., 1], sums)
+    # a plausible mistake -- rounding half to even -- changes the codes of exact halves
+    y = np.zeros((1, 32), np.float32)
+    y[0, 0], y[0, 1] = 127.0, 0.5
+    assert ref.q8_1_codes(y)[0][0, 1] == 1 and np.rint(np.float32(0.5)) == 0
+
+
 # ------------------------------------------------------------------------------------------------------- E4M3
 def all_e4m3():
     b = np.arange(256, dtype=np.uint8)
