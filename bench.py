@@ -5,9 +5,12 @@
 
 A step is one launch of the hot path over one batch of synthetic input:
 
-    q4_k_gemv   (default) Q4_K decode GEMV, W [12288, 4096] (Qwen3-8B FFN gate/up), x bf16 [M, 4096], y f32
-    q4_k_gemv_q8  the same GEMV on the int8-activation path (the reference's default decode path): the bf16 rows are
-                quantized to Q8_1 inside the kernel and multiplied with exact int32 group dot products
+    q4_k_gemv_q8  (default) Q4_K decode GEMV, W [12288, 4096] (Qwen3-8B FFN gate/up), x bf16 [M, 4096], y f32, on
+                the int8-activation path the reference takes by default: the bf16 rows are quantized to Q8_1 inside
+                the kernel and multiplied with exact int32 group dot products
+    q4_k_gemv   the same GEMV on the f16-activation path (x staged as f16, v_dot2_f32_f16)
+    q4_k_gemv_q8p the int8-activation GEMV on its reference boundary: x is the planar Q8_1 buffer qmm_quant_q8 makes
+                (once per layer input, shared by the matvecs that read it), quantized before the timed region
     q4_0_gemv   Q4_0 decode GEMV, W [4096, 4096], x f32 [1, 4096], y f32
     q4_k_gemm   Q4_K prefill GEMM, x bf16 [512, 4096] (row scale to f16, then the MFMA GEMM), W [4096, 4096],
                 y bf16 [512, 4096] (Qwen3-8B attn o_proj)
@@ -45,7 +48,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=2000)
     p.add_argument("--warmup", type=int, default=200)
-    p.add_argument("--workload", default="q4_k_gemv", choices=sorted(WORKLOADS))
+    p.add_argument("--workload", default="q4_k_gemv_q8", choices=sorted(WORKLOADS))
     p.add_argument("--m", type=int, default=None, help="tokens per GEMV (q4_k_gemv: 1, 4 or 8)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
@@ -94,9 +97,13 @@ class GemvWorkload:
         self.y = torch.empty((self.m, self.n), dtype=torch.float32, device=dev)
         self.ops = ops
         self.copies = copies
+        if self.q8 == "planar":
+            self.xq = ops.quant_q8(self.x)
 
     def step(self, i):
-        if self.q8:
+        if self.q8 == "planar":
+            self.ops.mv_q8(self.fmt, self.ws[i % self.copies], self.xq, self.n, self.k, tokens=self.m, y=self.y)
+        elif self.q8:
             self.ops.mv_q8(self.fmt, self.ws[i % self.copies], self.x, self.n, self.k, y=self.y)
         else:
             self.ops.mv(self.fmt, self.ws[i % self.copies], self.x, self.n, self.k, y=self.y)
@@ -107,11 +114,15 @@ class GemvWorkload:
         return self.alg_bytes() / sec / 1e9
 
     def dtype(self):
+        if self.q8 == "planar":
+            return f"{self.fmt} x int8 (planar Q8_1 from qmm_quant_q8) -> f32, int32 group dots"
         if self.q8:
             return f"{self.fmt} x int8 (Q8_1 of {self.x_dtype}, quantized in the kernel) -> f32, int32 group dots"
         return "q4_k x bf16 -> f32" if self.fmt == "q4_k" else "q4_0 x f32 -> f32"
 
     def alg_bytes(self):
+        if self.q8 == "planar":   # the planar Q8_1 buffer: a code byte per value and 8 bytes per 32 values
+            return self.wbytes + self.m * (self.k + self.k // 32 * 8) + self.m * self.n * 4
         xb = 2 if self.x_dtype == "bf16" else 4
         return self.wbytes + self.m * self.k * xb + self.m * self.n * 4
 
@@ -128,7 +139,8 @@ class GemvWorkload:
 
     def config(self):
         return {"workload": self.name, "format": self.fmt, "N": self.n, "K": self.k, "M": self.m,
-                "x_dtype": self.x_dtype, "activations": "q8_1" if self.q8 else self.x_dtype, "y_dtype": "f32",
+                "x_dtype": "q8_1 planar" if self.q8 == "planar" else self.x_dtype,
+                "activations": "q8_1" if self.q8 else self.x_dtype, "y_dtype": "f32",
                 "weight_copies_rotated": self.copies,
                 "rotated_bytes": self.copies * self.wbytes}
 
@@ -377,7 +389,12 @@ def _q4k_gemv(m):
 
 def _q4k_gemv_q8(m):
     return GemvWorkload("q4_k_gemv_q8", 1, "q4_k", 12288, 4096, m or 1, "bf16",
-                        f"mv_q4k_q8_kernel.q4_k_gemv_q8_n12288_k4096_m{m or 1}", q8=True)
+                        f"mv_q4k_q8s_kernel.q4_k_gemv_q8_n12288_k4096_m{m or 1}", q8=True)
+
+
+def _q4k_gemv_q8p(m):
+    return GemvWorkload("q4_k_gemv_q8p", 1, "q4_k", 12288, 4096, m or 1, "bf16",
+                        f"mv_q4k_q8s_kernel.q4_k_gemv_q8p_n12288_k4096_m{m or 1}", q8="planar")
 
 
 def _q40_gemv(m):
@@ -385,7 +402,7 @@ def _q40_gemv(m):
                         f"mv_kernel_q4_0.q4_0_gemv_n4096_k4096_m{m or 1}")
 
 
-WORKLOADS = {"q4_k_gemv": _q4k_gemv, "q4_k_gemv_q8": _q4k_gemv_q8, "q4_0_gemv": _q40_gemv, "q4_k_gemm": GemmWorkload,
+WORKLOADS = {"q4_k_gemv": _q4k_gemv, "q4_k_gemv_q8": _q4k_gemv_q8, "q4_k_gemv_q8p": _q4k_gemv_q8p, "q4_0_gemv": _q40_gemv, "q4_k_gemm": GemmWorkload,
              "mxfp4_moe": lambda m: MoeWorkload("mxfp4_moe", 3, m), "q4_k_moe": lambda m: MoeWorkload("q4_k_moe", 4, m),
              "hbm_copy": CopyWorkload}
 

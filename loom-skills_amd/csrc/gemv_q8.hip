@@ -15,9 +15,9 @@
 //
 // Kernels. The quantizer gives each 32-value group to four consecutive lanes (8 values each). The generic matvec
 // is the item walk of gemv.hip with Q8 activation fragments (any K % 256 for Q4_K, K % 64 for Q4_0). The Q4_K fast
-// path (K = 4096, 8192) is the layout of gemv_q4k.hip -- a lane owns half a super-block, five 128-bit weight loads
-// -- with the token's codes and group pairs staged once per workgroup in LDS; given f32 / bf16 activations it
-// quantizes them while staging, with the quantizer's own arithmetic, so both input forms give identical results.
+// path (K = 4096, 8192) splits K between the eight waves of a workgroup (see mv_q4k_q8s_kernel); given f32 / bf16
+// activations it quantizes them while staging, with the quantizer's own arithmetic, so both input forms give
+// identical results.
 #include "bfly.hpp"
 
 using namespace qmm;
@@ -226,128 +226,165 @@ __global__ __launch_bounds__(256) void mv_q8_kernel(int64_t n, int64_t tokens, i
   }
 }
 
-// ------------------------------------------------------------------------------ Q4_K fast path (K 4096 / 8192)
-constexpr int kFWaves = 8, kFThreads = kFWaves * 64;
+// ---------------------------------------------------------------- Q4_K K-sliced path (K 4096 / 8192)
+// Wave w of a workgroup owns the K-slice [512 KB w, 512 KB (w + 1)) of the workgroup's RW = 16 / KB rows; lane
+// (r, it) takes half super-block it of row r inside the slice (five 128-bit loads). The wave quantizes its own
+// slice of the activations into its own LDS area, so only a wavefront fence -- no workgroup barrier -- stands
+// between the weight loads and the math, and it moves the lane's 128 activation codes into registers before it
+// waits for its weights: once they land only ALU work is left. The slices' row sums meet in LDS at the end (one
+// barrier, a fixed order).
+constexpr int kSWaves = 8;
+#ifndef QMM_Q8_SLOTS
+#define QMM_Q8_SLOTS 1
+#endif
+constexpr int kSSlots = QMM_Q8_SLOTS;   // row groups per wave (they share the lane's activations)
 
 template <int TG, int KB, bool STAGEQ>
-__global__ __launch_bounds__(kFThreads) void mv_q4k_q8_kernel(int64_t n, int64_t tokens, int accumulate,
-                                                               const void *__restrict__ x, int bf,
-                                                               const u8 *__restrict__ w, float *__restrict__ y) {
-  constexpr int K = KB * 4096;
-  constexpr int L = 32 * KB;            // lanes per row
-  constexpr int RPP = 64 / L;           // rows per wave
-  constexpr int WG_ROWS = kFWaves * RPP;
+__global__ __launch_bounds__(kSWaves * 64) void mv_q4k_q8s_kernel(int64_t n, int64_t tokens, int accumulate,
+                                                                 const void *__restrict__ x, int bf,
+                                                                 const u8 *__restrict__ w, float *__restrict__ y) {
+  constexpr int K = KB * 4096, IPR = 4 * KB, RG = 64 / IPR, RW = RG * kSSlots, SLICE = 512 * KB, NG = SLICE / 32;
   constexpr int64_t RB = (int64_t)K / 256 * 144;
-  constexpr int NCH = K / 8;            // 8-value chunks of a token row
-  constexpr int CPT = (NCH + kFThreads - 1) / kFThreads;
-
-  __shared__ __align__(16) u32 xc[TG][K / 4];         // int8 codes
-  __shared__ __align__(16) float xm[TG][K / 32][2];   // (f16-rounded d, code sum) per group
+  __shared__ __align__(16) u32 xc[kSWaves][TG][SLICE / 4];
+  __shared__ __align__(16) float xm[kSWaves][TG][NG][2];
+  __shared__ float red[kSWaves][RW][TG];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t t0 = (int64_t)blockIdx.y * TG;
-  const int64_t wrow0 = (int64_t)blockIdx.x * WG_ROWS + wave * RPP;
-  const int rp = lane / L, item = lane % L, b = item >> 1, h = item & 1;
+  const int64_t row0 = (int64_t)blockIdx.x * RW;
+  const int r = lane / IPR, it = lane % IPR;
+  const int sl = it >> 1, h = it & 1;              // slice-local super-block and half
+  const int64_t k0 = (int64_t)wave * SLICE;        // the slice's first value
 
-  // ---- activation loads first, then the weights (vector loads complete in issue order)
-  float xv[TG][CPT][8];
-  v4u qv[TG][CPT];
+  // ---- the slice's activations first, then the weights
+  float xv[TG][KB][8];
+  v2u qv[TG][KB];
+  float2 mv[TG];
 #pragma unroll
   for (int t = 0; t < TG; ++t) {
     const int64_t tok = t0 + t < tokens ? t0 + t : tokens - 1;
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + i * kFThreads;
-      const int cc = c < NCH ? c : NCH - 1;
-      if constexpr (STAGEQ) {
-        load8_act(x, bf, tok * K + 8 * cc, xv[t][i]);
-      } else {
-        // planar: 8 codes = 2 dwords; the 16-byte read covers chunks cc and cc + 1 (taken by even threads only)
-        qv[t][i] = *reinterpret_cast<const v4u *>(static_cast<const u8 *>(x) + tok * K + 8 * (cc & ~1));
-      }
+    for (int j = 0; j < KB; ++j) {
+      const int c = lane + 64 * j;               // 8-value chunk of the slice
+      if constexpr (STAGEQ) load8_act(x, bf, tok * K + k0 + 8 * c, xv[t][j]);
+      else qv[t][j] = *reinterpret_cast<const v2u *>(static_cast<const u8 *>(x) + tok * K + k0 + 8 * c);
+    }
+    if constexpr (!STAGEQ) {
+      const float2 *meta = reinterpret_cast<const float2 *>(static_cast<const u8 *>(x) + tokens * K);
+      mv[t] = meta[tok * (K / 32) + k0 / 32 + (lane < NG ? lane : 0)];
     }
   }
-  v4u wd[5];
-  {
-    int64_t row = wrow0 + rp;
-    row = row < n ? row : n - 1;        // rows past n read row n-1 and are never stored
-    const v4u *bp = reinterpret_cast<const v4u *>(w + row * RB + (int64_t)b * 144);
-    wd[0] = bp[0];
+  v4u wd[kSSlots][5];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) wd[1 + i] = bp[1 + 4 * h + i];
+  for (int so = 0; so < kSSlots; ++so) {
+    int64_t row = row0 + r + RG * so;
+    row = row < n ? row : n - 1;        // rows past n read row n-1 and are never stored
+    const v4u *bp = reinterpret_cast<const v4u *>(w + row * RB + (k0 / 256 + sl) * 144);
+    wd[so][0] = bp[0];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wd[so][1 + i] = bp[1 + 4 * h + i];
   }
 
-  // ---- stage the codes and group pairs
+  // ---- the wave's slice: codes and group pairs into its own LDS area
 #pragma unroll
   for (int t = 0; t < TG; ++t) {
-    const int64_t tok = t0 + t < tokens ? t0 + t : tokens - 1;
-    if constexpr (STAGEQ) {
 #pragma unroll
-      for (int i = 0; i < CPT; ++i) {
-        const int c = tid + i * kFThreads;
-        if (c >= NCH) break;            // whole waves: NCH and kFThreads are multiples of 64
+    for (int j = 0; j < KB; ++j) {
+      const int c = lane + 64 * j;
+      if constexpr (STAGEQ) {
         u32 c0, c1;
         float d16, sum;
-        q8_group4(xv[t][i], c0, c1, d16, sum);
-        xc[t][2 * c] = c0;
-        xc[t][2 * c + 1] = c1;
-        if ((c & 3) == 0) { xm[t][c >> 2][0] = d16; xm[t][c >> 2][1] = sum; }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < CPT; ++i) {
-        const int c = tid + i * kFThreads;
-        if (c < NCH && (c & 1) == 0) *reinterpret_cast<v4u *>(&xc[t][2 * c]) = qv[t][i];
-      }
-      const float *meta = reinterpret_cast<const float *>(static_cast<const u8 *>(x) + tokens * K) + tok * (K / 16);
-      for (int g = tid; g < K / 32; g += kFThreads) {
-        const float2 m = reinterpret_cast<const float2 *>(meta)[g];
-        xm[t][g][0] = m.x;
-        xm[t][g][1] = m.y;
+        q8_group4(xv[t][j], c0, c1, d16, sum);
+        xc[wave][t][2 * c] = c0;
+        xc[wave][t][2 * c + 1] = c1;
+        if ((c & 3) == 0) { xm[wave][t][c >> 2][0] = d16; xm[wave][t][c >> 2][1] = sum; }
+      } else {
+        xc[wave][t][2 * c] = qv[t][j].x;
+        xc[wave][t][2 * c + 1] = qv[t][j].y;
       }
     }
+    if constexpr (!STAGEQ) {
+      if (lane < NG) { xm[wave][t][lane][0] = mv[t].x; xm[wave][t][lane][1] = mv[t].y; }
+    }
   }
-  __syncthreads();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // ---- the lane's half super-block: pages 2h, 2h+1 = groups 8b + 4h + (0..3)
-  float acc[TG];
-  const v4u hd = wd[0];
+  // ---- the lane's 4 groups (8 sl + 4 h + 0..3): codes and pairs into registers before the weights are awaited
+  const int g0 = 8 * sl + 4 * h;
+  u32 xa[TG][4][8];
+  float md[TG][4], ms[TG][4];
+#pragma unroll
+  for (int t = 0; t < TG; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const v4u p0 = *reinterpret_cast<const v4u *>(&xc[wave][t][8 * (g0 + g)]);
+      const v4u p1 = *reinterpret_cast<const v4u *>(&xc[wave][t][8 * (g0 + g) + 4]);
+      xa[t][g][0] = p0.x; xa[t][g][1] = p0.y; xa[t][g][2] = p0.z; xa[t][g][3] = p0.w;
+      xa[t][g][4] = p1.x; xa[t][g][5] = p1.y; xa[t][g][6] = p1.z; xa[t][g][7] = p1.w;
+      md[t][g] = xm[wave][t][g0 + g][0];
+      ms[t][g] = xm[wave][t][g0 + g][1];
+    }
+#pragma unroll
+  for (int t = 0; t < TG; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) asm volatile("" ::"v"(xa[t][g][i]));
+      asm volatile("" ::"v"(md[t][g]), "v"(ms[t][g]));
+    }
+
+  // ---- math: pages 2h (groups g0, g0 + 1) and 2h + 1 (groups g0 + 2, g0 + 3)
+#pragma unroll
+  for (int so = 0; so < kSSlots; ++so) {
+  const v4u hd = wd[so][0];
   const float d = f16_to_f32(hd.x), dmin = f16_to_f32(hd.x >> 16);
-  const u32 q[16] = {wd[1].x, wd[1].y, wd[1].z, wd[1].w, wd[2].x, wd[2].y, wd[2].z, wd[2].w,
-                     wd[3].x, wd[3].y, wd[3].z, wd[3].w, wd[4].x, wd[4].y, wd[4].z, wd[4].w};
+  const u32 q[16] = {wd[so][1].x, wd[so][1].y, wd[so][1].z, wd[so][1].w, wd[so][2].x, wd[so][2].y, wd[so][2].z,
+                     wd[so][2].w, wd[so][3].x, wd[so][3].y, wd[so][3].z, wd[so][3].w, wd[so][4].x, wd[so][4].y,
+                     wd[so][4].z, wd[so][4].w};
+  float sc[4], mn[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    u32 s_, m_;
+    q4k_scale_min(hd.y, hd.z, hd.w, 4 * h + g, s_, m_);
+    sc[g] = d * (float)s_;
+    mn[g] = dmin * (float)m_;
+  }
+  float part[TG];
 #pragma unroll
   for (int t = 0; t < TG; ++t) {
-    const int g0 = 8 * b + 4 * h;
-    float part = 0.f;
+    float p = 0.f;
 #pragma unroll
     for (int pg = 0; pg < 2; ++pg) {
-      const v4u *xa = reinterpret_cast<const v4u *>(&xc[t][8 * (g0 + 2 * pg)]);   // group g0 + 2 pg
-      const v4u *xb = reinterpret_cast<const v4u *>(&xc[t][8 * (g0 + 2 * pg + 1)]);
-      const v4u a0 = xa[0], a1 = xa[1], b0 = xb[0], b1 = xb[1];
-      const u32 av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-      const u32 bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
       int ia = 0, ib = 0;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const u32 Q = q[8 * pg + i];
-        ia = sdot4(Q & 0x0F0F0F0Fu, av[i], ia);
-        ib = sdot4((Q >> 4) & 0x0F0F0F0Fu, bv[i], ib);
+        ia = sdot4(Q & 0x0F0F0F0Fu, xa[t][2 * pg][i], ia);
+        ib = sdot4((Q >> 4) & 0x0F0F0F0Fu, xa[t][2 * pg + 1][i], ib);
       }
-      u32 sc0, m0, sc1, m1;
-      q4k_scale_min(hd.y, hd.z, hd.w, 4 * h + 2 * pg, sc0, m0);
-      q4k_scale_min(hd.y, hd.z, hd.w, 4 * h + 2 * pg + 1, sc1, m1);
-      const float *ma = xm[t][g0 + 2 * pg], *mb = xm[t][g0 + 2 * pg + 1];
-      part += ((float)ia * (d * (float)sc0) - ma[1] * (dmin * (float)m0)) * ma[0];
-      part += ((float)ib * (d * (float)sc1) - mb[1] * (dmin * (float)m1)) * mb[0];
+      p += ((float)ia * sc[2 * pg] - ms[t][2 * pg] * mn[2 * pg]) * md[t][2 * pg];
+      p += ((float)ib * sc[2 * pg + 1] - ms[t][2 * pg + 1] * mn[2 * pg + 1]) * md[t][2 * pg + 1];
     }
-    acc[t] = part;
+    // the row's IPR lanes of this slice: a butterfly leaves the slice sum in every one of them
+    p += xshfl<1>(p);
+    p += xshfl<2>(p);
+    if constexpr (IPR == 8) p += xshfl<4>(p);
+    part[t] = p;
   }
-
-  int idx;
-  const float tot = group_reduce<TG, L>(acc, lane, idx);
-  constexpr int low_mask = (L >> log2i(TG)) - 1;
-  if ((lane & low_mask) == 0) {
-    const int64_t row = wrow0 + rp, tok = t0 + idx;
+  if (it == 0) {
+#pragma unroll
+    for (int t = 0; t < TG; ++t) red[wave][r + RG * so][t] = part[t];
+  }
+  }
+  __syncthreads();
+  if (tid < RW * TG) {
+    const int rr = tid / TG, t = tid % TG;
+    float tot = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < kSWaves; ++wv) tot += red[wv][rr][t];
+    const int64_t row = row0 + rr, tok = t0 + t;
     if (row < n && tok < tokens) {
       float *py = y + tok * n + row;
       *py = accumulate ? *py + tot : tot;
@@ -356,20 +393,20 @@ __global__ __launch_bounds__(kFThreads) void mv_q4k_q8_kernel(int64_t n, int64_t
 }
 
 template <int TG, int KB, bool STAGEQ>
-int launch_fast(int64_t n, int64_t tokens, int accumulate, const void *x, int bf, const void *w, float *y,
-                hipStream_t s) {
-  constexpr int WG_ROWS = kFWaves * (2 / KB);
-  const dim3 grid((unsigned)((n + WG_ROWS - 1) / WG_ROWS), (unsigned)((tokens + TG - 1) / TG));
-  mv_q4k_q8_kernel<TG, KB, STAGEQ><<<grid, kFThreads, 0, s>>>(n, tokens, accumulate, x, bf,
-                                                             static_cast<const u8 *>(w), y);
+int launch_sliced(int64_t n, int64_t tokens, int accumulate, const void *x, int bf, const void *w, float *y,
+                  hipStream_t s) {
+  constexpr int RW = 16 / KB * kSSlots;
+  const dim3 grid((unsigned)((n + RW - 1) / RW), (unsigned)((tokens + TG - 1) / TG));
+  mv_q4k_q8s_kernel<TG, KB, STAGEQ><<<grid, kSWaves * 64, 0, s>>>(n, tokens, accumulate, x, bf,
+                                                                  static_cast<const u8 *>(w), y);
   return launch_status();
 }
 
 template <int KB, bool STAGEQ>
 int launch_fast_tg(int64_t n, int64_t tokens, int accumulate, const void *x, int bf, const void *w, float *y,
                    hipStream_t s) {
-  return tokens >= 2 ? launch_fast<2, KB, STAGEQ>(n, tokens, accumulate, x, bf, w, y, s)
-                     : launch_fast<1, KB, STAGEQ>(n, tokens, accumulate, x, bf, w, y, s);
+  return tokens >= 2 ? launch_sliced<2, KB, STAGEQ>(n, tokens, accumulate, x, bf, w, y, s)
+                     : launch_sliced<1, KB, STAGEQ>(n, tokens, accumulate, x, bf, w, y, s);
 }
 
 }  // namespace
