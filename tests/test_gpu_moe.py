@@ -7,9 +7,10 @@ weights, with the activation rounding of the path under test applied to its inpu
 the hidden rows and the expert activations with the f16 row scale (f16_rows, as the reference's own prefill case
 does, make_kernel_tests.py:3194-3196), the MXFP4 chain quantizes them to MXFP8 (E4M3 with one E8M0 per 32 values).
 Expert ids must match exactly, and the MoE output within rel-L2 1e-3. Shapes: the Qwen3-30B-A3B (128 experts, top-8,
-T = 64) and gpt-oss-20b (32 experts, top-4, T = 1 and 256) workloads, plus small shapes with an expert holding more
+T = 64) and gpt-oss-20b (32 experts, top-4, T = 1, 256 and 1024) workloads, plus small shapes with an expert holding more
 than 64 rows, dead tokens and swiglu_oai; and the reference's grouped-GEMM-alone case (make_kernel_tests.py:
-3423-3500): hand-made tiles of 64, 37, 0 (expert -1) and 5 rows with inputs scaled by 0.05, 1 and 20.
+3423-3500): hand-made tiles of 64, 37, 0 (expert -1) and 5 rows with inputs scaled by 0.05, 1 and 20. At T = 4096
+both chains are checked through batch invariance: the rows of a slice equal those of the chain run on the slice.
 """
 import numpy as np
 import pytest
@@ -111,13 +112,43 @@ def test_q4_k_moe_qwen3_30b_a3b_shape(dev, prefill):
     assert_close_rel_l2(y, want, 1e-3, f"q4_k moe prefill={prefill}")
 
 
-@pytest.mark.parametrize("T,prefill", [(256, True), (1, False)])
+@pytest.mark.parametrize("T,prefill", [(256, True), (1024, True), (1, False)])
 def test_mxfp4_moe_gpt_oss_20b_shape(dev, T, prefill):
     """32 experts, top-4 with softmax over the picked logits (gating 3), H = FE = 2880, fused gate_up,
     swiglu_oai; prefill quantizes activations to MXFP8 for the scaled MFMA, decode multiplies bf16 directly."""
     y, want, _ = _run_chain(dev, "mxfp4", 32, 4, 2880, 2880, T, 3, False, "swiglu_oai", True, prefill,
                             seed=20261203 + T)
     assert_close_rel_l2(y, want, 1e-3, f"mxfp4 moe T={T}")
+
+
+@pytest.mark.parametrize("fmt,E,KU,H,FE,gating,norm,act,fused", [
+    ("q4_k", 128, 8, 2048, 768, 1, True, "silu", False),            # Qwen3-30B-A3B
+    ("mxfp4", 32, 4, 2880, 2880, 3, False, "swiglu_oai", True),     # gpt-oss-20b
+])
+def test_moe_prefill_large_batch_rows_match_small_batch(dev, fmt, E, KU, H, FE, gating, norm, act, fused):
+    """T = 4096 (4 to 8 tiles an expert): every token's output is a function of that token alone (per-row
+    activation rounding, fixed K order in the grouped GEMMs, combine in slot order), so the rows of a 4096-token
+    chain equal bit for bit those of a 256-token chain run on a slice of the same tokens. Ties the large-batch
+    grid (many tiles an expert, round-robin tile order) to the sizes the oracle checks."""
+    import torch
+    from qmm import synth
+    ops = _ops()
+    rng = np.random.default_rng(31 + E)
+    ex = Experts(dev, fmt, rng, E, H, FE, fused)
+    wfmt, kw = ex.device(split=True)
+    T, lo, hi = 4096, 1500, 1756
+    xb = dev_bf16(synth.to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32)), dev)
+    logits = dev_f32(rng.standard_normal((T, E)).astype(np.float32), dev)
+    big, mid = ops.moe_prefill(wfmt, xb, logits, E, KU, H, FE, gating, norm, fused=fused, act=act, **kw)
+    small, _ = ops.moe_prefill(wfmt, xb[lo:hi].contiguous(), logits[lo:hi].contiguous(), E, KU, H, FE, gating,
+                               norm, fused=fused, act=act, **kw)
+    torch.cuda.synchronize()
+    ti = host(mid["tile_info"])
+    assert ti[:, 1].sum() == T * KU and ti[:, 1].max() <= 64
+    assert np.bincount(ti[ti[:, 0] >= 0, 0]).max() >= 4, "no expert spans several tiles"
+    b, s = host(big), host(small)
+    assert np.all(np.isfinite(b))
+    np.testing.assert_array_equal(b[lo:hi].view(np.uint32), s.view(np.uint32))
 
 
 @pytest.mark.parametrize("fmt,fused,act", [("q4_k", True, "swiglu_oai"), ("q4_k", False, "silu"),
