@@ -232,9 +232,12 @@ class MoeWorkload:
         self.logits = torch.from_numpy(d["logits"]).to(dev)
         if d["fmt"] == "mxfp4":
             E, H, FE = self.E, self.H, self.FE
+            # one-time weight preparation: GGUF blocks -> split planes -> MFMA-tiled planes
             gn, gs = ops.repack_mxfp4(u8(d["gate_up"]), E * 2 * FE, H)
             dn, ds = ops.repack_mxfp4(u8(d["down"]), E * H, FE)
-            self.fmt = "mxfp4s"
+            gn, gs = ops.tile_mxfp4(gn, gs, E * 2 * FE, H)
+            dn, ds = ops.tile_mxfp4(dn, ds, E * H, FE)
+            self.fmt = "mxfp4t"
             self.kw = dict(w_gate=gn, ws_gate=gs, w_down=dn, ws_down=ds, fused=True, act=d["act"])
             self.wbytes_expert = (2 * FE * H + H * FE) // 2 + (2 * FE * H + H * FE) // 32
             self.peak_key = "fp8"
@@ -249,11 +252,12 @@ class MoeWorkload:
         self.experts_hit = int(torch.unique(mid["ids"]).numel())
         # inputs of the dominant kernel (the grouped gate/up GEMM) for its own timing
         self.mid = mid
-        if self.fmt == "mxfp4s":
+        if self.fmt == "mxfp4t":
             self.gu_x, self.gu_xs = ops.quant_mxfp8(self.x)
+            self.gu_y = (torch.empty_like(mid["act8"]), torch.empty_like(mid["act_scales"]))
         else:
             self.gu_x, self.gu_xs = ops.row_scale_f16(self.x)
-        self.gu_y = torch.empty_like(mid["act"])
+            self.gu_y = torch.empty_like(mid["act"])
 
     def run_chain(self):
         return self.ops.moe_prefill(self.fmt, self.x, self.logits, self.E, self.KU, self.H, self.FE, self.d["gating"],
@@ -264,6 +268,11 @@ class MoeWorkload:
 
     def kernel_step(self, i):
         kw = self.kw
+        if self.fmt == "mxfp4t":   # the gate/up GEMM with its activation written as MXFP8 (the chain's kernel)
+            self.ops.moe_grouped_mxfp8(self.fmt, self.mid["tile_info"], self.mid["rowmap"], self.gu_x, kw["w_gate"],
+                                       self.FE, self.H, self.E, self.KU, ws=kw.get("ws_gate"), x_scales=self.gu_xs,
+                                       fused=kw["fused"], act=kw["act"], codes=self.gu_y[0], scales=self.gu_y[1])
+            return
         self.ops.moe_grouped(self.fmt, "gu", self.mid["tile_info"], self.mid["rowmap"], self.gu_x, kw["w_gate"],
                              self.FE, self.H, self.E, self.KU, w2=kw.get("w_up"), ws=kw.get("ws_gate"),
                              x_scales=self.gu_xs, fused=kw["fused"], act=kw["act"], y=self.gu_y)
@@ -282,9 +291,12 @@ class MoeWorkload:
         return 2 * self.T * self.KU * (self.H * 2 * self.FE + self.FE * self.H)
 
     def gu_bytes(self):
-        T, H = self.T, self.H
-        per = self.wbytes_expert * 2 // 3 if self.fmt == "mxfp4s" else (2 * self.FE * H) // 256 * 144
-        return self.experts_hit * per + T * H + T * self.KU * self.FE * 4
+        """weights of the experts hit, the activation rows in, the activation out (MXFP8 codes + scales for MXFP4,
+        f32 for Q4_K)"""
+        T, H, A = self.T, self.H, self.T * self.KU
+        if self.fmt == "mxfp4t":
+            return self.experts_hit * (self.wbytes_expert * 2 // 3) + T * H + T * H // 32 + A * self.FE * 33 // 32
+        return self.experts_hit * ((2 * self.FE * H) // 256 * 144) + T * H * 2 + A * self.FE * 4
 
     def gu_flops(self):
         return 2 * self.T * self.KU * self.H * 2 * self.FE
@@ -293,7 +305,7 @@ class MoeWorkload:
         return self.alg_flops() / sec / 1e12
 
     def dtype(self):
-        return ("mxfp4 x mxfp8 (E4M3, E8M0 per 32) -> f32" if self.fmt == "mxfp4s"
+        return ("mxfp4 x mxfp8 (E4M3, E8M0 per 32) -> f32" if self.fmt == "mxfp4t"
                 else "q4_k x f16 (row-scaled) -> f32")
 
     def cpu_baseline(self, budget):
@@ -302,11 +314,11 @@ class MoeWorkload:
         from qmm import synth
         import time as _t
         d = self.d
-        gfmt = "mxfp4" if self.fmt == "mxfp4s" else "q4_k"
+        gfmt = "mxfp4" if self.fmt == "mxfp4t" else "q4_k"
         E, KU, H, FE = self.E, self.KU, self.H, self.FE
         rb_h, rb_f = of.row_bytes(gfmt, H), of.row_bytes(gfmt, FE)
         def gate_up(e):
-            if self.fmt == "mxfp4s":
+            if self.fmt == "mxfp4t":
                 g = of.dequantize(gfmt, d["gate_up"][2 * FE * e * rb_h:(2 * FE * e + FE) * rb_h], FE, H)
                 u = of.dequantize(gfmt, d["gate_up"][(2 * FE * e + FE) * rb_h:2 * FE * (e + 1) * rb_h], FE, H)
                 return g, u
@@ -316,7 +328,7 @@ class MoeWorkload:
             return of.dequantize(gfmt, d["down"][H * e * rb_f:H * (e + 1) * rb_f], H, FE)
         x = synth.bf16_bits_to_f32(d["x_bf16"])
         ids, wts = ref.route(d["logits"], KU, d["gating"], d["norm"])
-        rnd = ref.mxfp8_values if self.fmt == "mxfp4s" else ref.f16_rows
+        rnd = ref.mxfp8_values if self.fmt == "mxfp4t" else ref.f16_rows
         # bounded sample: the first tokens whose experts fit the time budget (the whole chain on them)
         tokens = 0
         t0 = _t.perf_counter()
@@ -491,6 +503,10 @@ def main():
         "tflops": round(wl.alg_flops() / per_step_s / 1e12, 3),
         "wall_s_timed_region": round(wall, 4),
     }
+    if getattr(wl, "fmt", None) == "mxfp4t":
+        # the scaled MFMA runs E4M3 x E2M1 at the FP8 rate; the MXFP4 figure is the fraction of the FP4 peak
+        out["roofline"]["mfma_frac_fp4_peak"] = round(kf / per_launch_s / 1e12 / MFMA_PEAK_TFLOPS["fp4"], 4)
+        out["chain_frac_fp4_peak"] = round(out["tflops"] / MFMA_PEAK_TFLOPS["fp4"], 4)
     if not args.no_cpu:
         out["cpu_baseline"] = wl.cpu_baseline(args.cpu_budget)
     print(json.dumps(out), flush=True)

@@ -37,7 +37,8 @@ enum qmm_status {
   QMM_ERR_WORKSPACE = -8  /* workspace too small */
 };
 
-enum qmm_format { QMM_Q4_0 = 0, QMM_Q4_K = 1, QMM_MXFP4 = 2, QMM_MXFP4S = 3 };
+/* QMM_MXFP4T: MXFP4 in MFMA-tiled planes (qmm_tile_mxfp4), the grouped GEMM's fast weight layout. */
+enum qmm_format { QMM_Q4_0 = 0, QMM_Q4_K = 1, QMM_MXFP4 = 2, QMM_MXFP4S = 3, QMM_MXFP4T = 4 };
 enum qmm_dtype {
   QMM_F32 = 0,
   QMM_F16 = 1,
@@ -59,7 +60,8 @@ int64_t qmm_row_bytes(int fmt, int64_t k);
 /* Bit-exact dequantization of `rows` rows of K values to f32 [rows, K]
  * (the values @g_q4_0_values S/quant_values.loom:386-408, @g_q4_k_values S/gen_llm.py:288-326,
  *  @g_mxfp4_values S/gen_llm.py:786-841 and @g_mxfp4s_values S/gen_llm.py:844-895 produce).
- * w: weight bytes; ws: the E8M0 scale plane for QMM_MXFP4S, else NULL. */
+ * w: weight bytes; ws: the E8M0 scale plane for QMM_MXFP4S / QMM_MXFP4T, else NULL (QMM_MXFP4T: rows % 32 == 0,
+ * K % 64 == 0). */
 int qmm_dequant(int fmt, const void *w, const void *ws, int64_t rows, int64_t k, float *out, qmm_stream_t stream);
 
 /* Decode matrix-vector product, the g_mv_{fmt}_k{K}[_t{TG}][_r{R}] family
@@ -147,11 +149,25 @@ int qmm_moe_expert_mv_split(int mode, int fused, int act, int64_t k, int64_t n, 
  *   QMM_MXFP4S: weights in split planes, ws / ws2 the E8M0 planes [E, rows, k/32]; x is MXFP8 (x_dtype
  *               QMM_MXFP8) from qmm_quant_mxfp8: E4M3 codes u8 [x_rows, k] with x_scales u8 [x_rows, k/32];
  *               K % 64 == 0; scaled f8f6f4 MFMA, inv = 1.
+ *   QMM_MXFP4T: as QMM_MXFP4S with the weights in MFMA-tiled planes from qmm_tile_mxfp4 (each expert's [rows, k]
+ *               tiled on its own: n % 32 == 0; a fused gate_up expert tiles as 2n rows); the same results bit for
+ *               bit, read as contiguous 1 KB streams (no counterpart in the reference: a load-time layout).
  * x_rows: rows of x (gu: tokens; dn: >= max_tiles * 64). y: f32 [max_tiles * 64, n]. */
 int qmm_moe_grouped(int fmt, int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
                     const int32_t *tile_info, const int32_t *rowmap, const void *x, int x_dtype, const void *x_scales,
                     int64_t x_rows, const void *w, const void *ws, const void *w2, const void *ws2, float *y,
                     qmm_stream_t stream);
+
+/* The gate/up grouped GEMM (mode 0 of qmm_moe_grouped, MXFP4 weights) with the MXFP8 quantization of its output
+ * fused into the epilogue (no reference counterpart: the reference writes act f32 and its next kernel reads it back).
+ * codes u8 [max_tiles*64, n] and scales u8 [max_tiles*64, n/32] are exactly qmm_quant_mxfp8(act, tile_info) of the
+ * act qmm_moe_grouped would write (the down GEMM's A operand), bit for bit; rows of unused tiles are not written,
+ * dead rows come out as codes 0 and scale byte 0. fmt QMM_MXFP4S or QMM_MXFP4T; n % 32 == 0; codes 16-byte
+ * aligned. Other arguments as qmm_moe_grouped. */
+int qmm_moe_grouped_mxfp8(int fmt, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
+                          const int32_t *tile_info, const int32_t *rowmap, const void *x, const void *x_scales,
+                          int64_t x_rows, const void *w, const void *ws, const void *w2, const void *ws2,
+                          uint8_t *codes, uint8_t *scales, qmm_stream_t stream);
 
 /* Row-scaled f16 producer, g_row_scale_f16[_tiles] (S/gen_llm.py:1843-1915, S/gen_moe.py:503-527):
  * per row e = clamp(exponent(max|x|) - 13, 0, 100), x16 = f16(x * 2^-e), scales = (2^-e, 2^e).
@@ -172,6 +188,17 @@ int qmm_quant_mxfp8(int64_t rows, int64_t k, const void *x, int x_dtype, const i
  * S/formats.py:12-15): nibbles u8 [rows, k/2] (byte j = elements 2j low nibble, 2j+1 high nibble) and
  * E8M0 scales u8 [rows, k/32]. Bit-exact: every code and exponent is kept. */
 int qmm_repack_mxfp4(const void *w, int64_t rows, int64_t k, uint8_t *nibbles, uint8_t *scales, qmm_stream_t stream);
+
+/* One-time weight preparation for the grouped GEMM (no reference counterpart: the reference reads the split planes
+ * of S/formats.py:12-15 as they are): split planes (nibbles [rows, k/2], scales [rows, k/32]) -> MFMA-tiled planes.
+ * nib_t [rows/32][k/64][64 lanes][16 B]: tile (row block rb, chunk c) holds at lane l = 32 h + i the 16 nibble bytes
+ * of row 32 rb + i, values 64 c + 32 h .. 64 c + 32 h + 31 (the E2M1 operand of lane l of the scaled MFMA);
+ * sc_t [rows/32][ceil(k/256)][64 lanes][4 B]: byte q of lane l in group g is the E8M0 scale of that lane's block
+ * in chunk 4 g + q (0 past K). A byte permutation: qmm_dequant(QMM_MXFP4T) gives the split planes' values bit for
+ * bit. rows % 32 == 0, k % 64 == 0; nib_t has rows * k / 2 bytes, sc_t qmm_mxfp4t_scale_bytes(rows, k). */
+int qmm_tile_mxfp4(const void *nibbles, const void *scales, int64_t rows, int64_t k, void *nib_t, void *sc_t,
+                   qmm_stream_t stream);
+int64_t qmm_mxfp4t_scale_bytes(int64_t rows, int64_t k);
 
 /* MoE combine, g_moe_combine / g_moe_combine_sorted (S/gen_moe.py:730-762, :1231-1280):
  *   y[t, c] = fma(w[t,KU-1], v[KU-1], ... fma(w[t,0], v[0], accumulate ? y[t, c] : 0))

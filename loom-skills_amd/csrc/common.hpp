@@ -47,6 +47,25 @@ __device__ __forceinline__ void q4k_scale_min(u32 s0, u32 s1, u32 s2, int g, u32
   mn = hi ? ((a3 >> 4) | ((a2 >> 6) << 4)) : (a2 & 63u);
 }
 
+// OCP MX E8M0 exponent of a 32-value block whose largest magnitude is amax: s = clamp(floor(log2(amax)) - 7, -127,
+// 127) (-127 for amax = 0), which keeps every |x| 2^-s below 256, under the E4M3 maximum 448. The scale byte is
+// s + 127.
+__device__ __forceinline__ int mxfp8_exponent(float amax) {
+  int sx = -127;
+  if (amax > 0.f) {
+    int ex;
+    frexpf(amax, &ex);        // amax = f 2^ex, f in [0.5, 1)
+    sx = min(max(ex - 1 - 7, -127), 127);
+  }
+  return sx;
+}
+// E4M3 codes of (a, b) x 2^-sx in bytes 0-1 (HI = false) or 2-3 (HI = true) of w: v_cvt_pk_fp8_f32, round to
+// nearest even, OCP E4M3FN on gfx950.
+template <bool HI>
+__device__ __forceinline__ int e4m3_pack2(float a, float b, int sx, int w) {
+  return __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(a, -sx), ldexpf(b, -sx), w, HI);
+}
+
 // ----------------------------------------------------------------------------------------- wave reductions
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -68,6 +87,7 @@ inline int64_t block_values(int fmt) {
     case QMM_Q4_K: return 256;
     case QMM_MXFP4: return 32;
     case QMM_MXFP4S: return 32;
+    case QMM_MXFP4T: return 32;
     default: return 0;
   }
 }
@@ -77,6 +97,7 @@ inline int64_t block_bytes(int fmt) {
     case QMM_Q4_K: return 144;
     case QMM_MXFP4: return 17;
     case QMM_MXFP4S: return 16;
+    case QMM_MXFP4T: return 16;
     default: return 0;
   }
 }

@@ -5,9 +5,12 @@
 //   Q4_K   w = (f32(d) * sc) * q - f32(dmin) * m      S/gen_llm.py:269-326
 //   MXFP4  w = kvalues[code] * 2^(e - 128)            S/gen_llm.py:786-841 (code 8 -> +0)
 //   MXFP4S w = E2M1(code) * 2^(e - 127)               S/st_tensors.py:26-33 (code 8 -> -0)
+//   MXFP4T the same values from MFMA-tiled planes (grouped_mxfp4.hip)
 #include "common.hpp"
 
 using namespace qmm;
+
+int qmm_dequant_mxfp4t(const void *w, const void *ws, int64_t rows, int64_t k, float *out, hipStream_t s);
 
 namespace {
 
@@ -104,9 +107,10 @@ const char *qmm_strerror(int status) {
 int64_t qmm_row_bytes(int fmt, int64_t k) { return row_bytes(fmt, k); }
 
 int qmm_dequant(int fmt, const void *w, const void *ws, int64_t rows, int64_t k, float *out, qmm_stream_t stream) {
-  if (fmt < QMM_Q4_0 || fmt > QMM_MXFP4S) return QMM_ERR_FORMAT;
-  if (!w || !out || (fmt == QMM_MXFP4S && !ws)) return QMM_ERR_NULL;
+  if (fmt < QMM_Q4_0 || fmt > QMM_MXFP4T) return QMM_ERR_FORMAT;
+  if (!w || !out || ((fmt == QMM_MXFP4S || fmt == QMM_MXFP4T) && !ws)) return QMM_ERR_NULL;
   if (rows <= 0 || row_bytes(fmt, k) == 0) return QMM_ERR_SHAPE;
+  if (fmt == QMM_MXFP4T) return qmm_dequant_mxfp4t(w, ws, rows, k, out, reinterpret_cast<hipStream_t>(stream));
   if (fmt == QMM_Q4_K && !aligned(w, 4)) return QMM_ERR_ALIGN;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t groups = rows * (k / 32);

@@ -172,7 +172,7 @@ int dispatch_mv(bool bf, int64_t k, int64_t n, int64_t tokens, int accumulate, c
 template <bool B> using MXG = MXFP4<B, false>;
 template <bool B> using MXS = MXFP4<B, true>;
 
-bool valid_fmt(int fmt) { return fmt >= QMM_Q4_0 && fmt <= QMM_MXFP4S; }
+bool valid_fmt(int fmt) { return fmt >= QMM_Q4_0 && fmt <= QMM_MXFP4S; }   // no GEMV on MFMA-tiled planes
 
 // Alignment the row engine needs: 16-byte rows for Q4_K / MXFP4S, 4-byte rows for Q4_0 pairs.
 int check_weights(int fmt, int64_t k, const void *w, const void *ws) {

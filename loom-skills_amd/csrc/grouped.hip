@@ -1,21 +1,21 @@
 // qmm_moe_grouped: argument checks shared by the grouped expert GEMMs and the dispatch to the Q4_K (f16 MFMA,
-// gemm_q4k.hip) and MXFP4 split-plane (scaled f8f6f4 MFMA, grouped_mxfp4.hip) kernels.
+// gemm_q4k.hip) and MXFP4 split-plane / MFMA-tiled (scaled f8f6f4 MFMA, grouped_mxfp4.hip) kernels.
 #include "common.hpp"
 
 int qmm_grouped_q4k(int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
                     const int32_t *tile_info, const int32_t *rowmap, const void *x, const float *x_scales,
                     int64_t x_rows, const void *w, const void *w2, float *y, hipStream_t s);
-int qmm_grouped_mxfp4(int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
+int qmm_grouped_mxfp4(int tiled, int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
                       const int32_t *tile_info, const int32_t *rowmap, const void *x, const void *x_scales,
                       int64_t x_rows, const void *w, const void *ws, const void *w2, const void *ws2, float *y,
-                      hipStream_t s);
+                      uint8_t *y8, uint8_t *ys8, hipStream_t s);
 
 extern "C" int qmm_moe_grouped(int fmt, int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E,
                                int KU, const int32_t *tile_info, const int32_t *rowmap, const void *x, int x_dtype,
                                const void *x_scales, int64_t x_rows, const void *w, const void *ws, const void *w2,
                                const void *ws2, float *y, qmm_stream_t stream) {
   using namespace qmm;
-  if (fmt != QMM_Q4_K && fmt != QMM_MXFP4S) return QMM_ERR_FORMAT;
+  if (fmt != QMM_Q4_K && fmt != QMM_MXFP4S && fmt != QMM_MXFP4T) return QMM_ERR_FORMAT;
   if (mode != 0 && mode != 1) return QMM_ERR_RANGE;
   if (act != QMM_ACT_SILU && act != QMM_ACT_SWIGLU_OAI) return QMM_ERR_RANGE;
   if (E <= 0 || E > 1024 || KU <= 0 || KU > 8) return QMM_ERR_RANGE;
@@ -31,6 +31,23 @@ extern "C" int qmm_moe_grouped(int fmt, int mode, int fused, int act, int64_t ma
                            static_cast<const float *>(x_scales), x_rows, w, w2, y, s);
   }
   if (x_dtype != QMM_MXFP8) return QMM_ERR_DTYPE;
-  return qmm_grouped_mxfp4(mode, fused, act, max_tiles, k, n, E, KU, tile_info, rowmap, x, x_scales, x_rows, w, ws,
-                           w2, ws2, y, s);
+  return qmm_grouped_mxfp4(fmt == QMM_MXFP4T, mode, fused, act, max_tiles, k, n, E, KU, tile_info, rowmap, x,
+                           x_scales, x_rows, w, ws, w2, ws2, y, nullptr, nullptr, s);
+}
+
+extern "C" int qmm_moe_grouped_mxfp8(int fmt, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E,
+                                     int KU, const int32_t *tile_info, const int32_t *rowmap, const void *x,
+                                     const void *x_scales, int64_t x_rows, const void *w, const void *ws,
+                                     const void *w2, const void *ws2, uint8_t *codes, uint8_t *scales,
+                                     qmm_stream_t stream) {
+  using namespace qmm;
+  if (fmt != QMM_MXFP4S && fmt != QMM_MXFP4T) return QMM_ERR_FORMAT;
+  if (act != QMM_ACT_SILU && act != QMM_ACT_SWIGLU_OAI) return QMM_ERR_RANGE;
+  if (E <= 0 || E > 1024 || KU <= 0 || KU > 8) return QMM_ERR_RANGE;
+  if (!tile_info || !rowmap || !x || !w || !codes || !scales) return QMM_ERR_NULL;
+  if (max_tiles <= 0 || max_tiles > (1 << 18) || k <= 0 || n <= 0 || k > (1 << 20) || n > (1 << 20) || n % 32)
+    return QMM_ERR_SHAPE;
+  if (x_rows <= 0) return QMM_ERR_SHAPE;
+  return qmm_grouped_mxfp4(fmt == QMM_MXFP4T, 0, fused, act, max_tiles, k, n, E, KU, tile_info, rowmap, x, x_scales,
+                           x_rows, w, ws, w2, ws2, nullptr, codes, scales, reinterpret_cast<hipStream_t>(stream));
 }

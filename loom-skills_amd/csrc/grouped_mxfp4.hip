@@ -18,41 +18,58 @@
 // 16h .. 16h+15 in bytes 0..15 and 32+16h .. 32+16h+15 in bytes 16..31, and its scale is the one of block h; both
 // operands therefore see the same two 32-value blocks per chunk.
 //
+// Weight layouts. kSplit reads the split planes as they are: one load instruction then touches 32 weight rows
+// (1440 bytes apart at K = 2880), 32 bytes each, which streams at about 4.5-5 TB/s. kTiled reads the MFMA-tiled
+// planes of qmm_tile_mxfp4: the 1 KB tile (row block rb of 32 rows, chunk c of 64 values) holds at bytes
+// 16 l .. 16 l + 15 exactly lane l's E2M1 operand (row 32 rb + l % 32, values 64 c + 32 (l / 32) ..), tiles ordered
+// (rb, c), so a wave streams one contiguous run of 1 KB loads over K (about 7.4 TB/s for the same bytes); the E8M0
+// plane holds per (rb, group of four chunks) 256 bytes, lane l's four scale bytes at 4 l, so one dword load per
+// lane brings the scales of four chunks.
+//
 // Tiling: a workgroup of four waves owns one 64-row expert tile; each wave computes 64 rows x 64 weight columns
 // (2 x 2 MFMA blocks) over all of K. gu: wave w owns output columns 32 w .. 32 w + 31 of a 128-column block, its
 // two column blocks being those columns of the gate and of the up matrix, so the activation is applied in
-// registers. dn: wave w owns the 32 columns 32 w .. 32 w + 31 of a 128-column block. Tiles are dealt to the eight XCDs round-robin
-// (workgroup b runs on XCD b % 8): the bucket writes the live tiles first, and a tile-major order would leave
-// the XCDs that get the trailing, unused tiles idle; a tile's column blocks stay on one XCD, sharing its
-// activation rows in that L2.
+// registers. dn: wave w owns the 32 columns 32 w .. 32 w + 31 of a 128-column block. Workgroup b runs on XCD b % 8;
+// the live tiles (those with an expert) are cut into eight contiguous ranges, one per XCD, and each XCD walks its
+// range tile-fastest: the workgroups resident together on an XCD are then the tiles of one or a few experts on the
+// same column blocks, so an expert's weights come from HBM once and its other tiles read them from that XCD's L2.
 //
-// Steps. All E8M0 scales of the workgroup (its 64 activation rows and 128 + 128 or 128 weight columns, K / 32
-// bytes each) are staged in LDS once; per-step byte loads of scales through the vector memory path cost more than
-// the weight stream. A super-step covers kSub 64-value chunks: the tile's activation codes for it are staged in
-// LDS (double-buffered, one barrier per super-step) and the weights stream straight into registers one super-step
-// ahead, kSub consecutive 32-byte chunks of a column issued back to back.
+// Steps. The E8M0 scales of the tile's 64 activation rows (and, for kSplit, of its 128 + 128 or 128 weight columns),
+// K / 32 bytes each, are staged in LDS once; per-step byte loads of split-plane scales through the vector memory
+// path cost more than the weight stream (kTiled streams its scales as dwords instead). A super-step covers kSub
+// 64-value chunks: the tile's activation codes for it are staged in LDS (double-buffered, one barrier per
+// super-step) and the weights stream straight into registers one super-step ahead.
 #include <type_traits>
 
+#include "bfly.hpp"
 #include "common.hpp"
 
 using namespace qmm;
 
 namespace {
 
-#ifndef QMM_MX_DEPTH
-#define QMM_MX_DEPTH 1
+// Pipeline shape per kernel: DEPTH super-steps of weight loads in flight, SUB 64-value chunks per super-step (one
+// barrier each). The down GEMM streams one weight column block per wave (the gate/up GEMM two), so it needs a deeper
+// ring to keep as many bytes in flight.
+#ifndef QMM_MX_DEPTH_GU
+#define QMM_MX_DEPTH_GU 1
+#endif
+#ifndef QMM_MX_SUB_GU
+#define QMM_MX_SUB_GU 2
+#endif
+#ifndef QMM_MX_DEPTH_DN
+#define QMM_MX_DEPTH_DN 1
+#endif
+#ifndef QMM_MX_SUB_DN
+#define QMM_MX_SUB_DN 2
 #endif
 #ifndef QMM_MX_WAVES
 #define QMM_MX_WAVES 3            // minimum waves per SIMD the register allocation must allow (3 workgroups per CU)
 #endif
-constexpr int kDepth = QMM_MX_DEPTH;
-#ifndef QMM_MX_SUB
-#define QMM_MX_SUB 2
-#endif
-constexpr int kSub = QMM_MX_SUB;                      // 64-value chunks per super-step (one barrier each)
-constexpr int BM = 64, KC = 64, APITCH = kSub * KC + 16;   // activation bytes per LDS row (16-byte aligned rows)
+constexpr int BM = 64, KC = 64;
 
-enum Kind { kGU = 1, kDN = 2 };
+enum Kind { kGU = 1, kDN = 2, kGU8 = 3 };   // kGU8: gu with its output quantized to MXFP8
+enum Layout { kSplit = 0, kTiled = 1 };
 typedef __attribute__((ext_vector_type(4))) u32 v4u;   // a native vector: the register rings stay in VGPRs
 
 struct MArgs {
@@ -66,6 +83,7 @@ struct MArgs {
   const int32_t *tile_info, *rowmap;
   int KU, E, act;
   float *y;
+  u8 *y8, *ys8;                    // kGU8: E4M3 codes [rows, N] and E8M0 scales [rows, N/32] of the activation
   int n_blocks, max_tiles;
 };
 
@@ -90,8 +108,7 @@ __device__ __forceinline__ void for_steps(F &&f, int c0, std::integer_sequence<i
 
 // Element i of an n-element copy into LDS, for every i, 256 threads: kBatch loads in flight per thread before
 // their stores (a plain loop would wait for each load before the next). get(i) loads element i (i < n).
-constexpr int kBatch = 8;
-template <class T, class G>
+template <int kBatch = 8, class T, class G>
 __device__ __forceinline__ void batched_copy(T *dst, int64_t n, int tid, G &&get) {
   for (int64_t b = 0; b < n; b += kBatch * 256) {
     T v[kBatch];
@@ -122,36 +139,126 @@ __device__ __forceinline__ void copy_to_lds(u8 *dst, const u8 *src, int64_t n, i
   }
 }
 
-template <int KIND, int DEPTH>
+template <int KIND, int LAYOUT, int DEPTH, int kSub>
 __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs a) {
+  constexpr int APITCH = kSub * KC + 16;     // activation bytes per LDS row (16-byte aligned rows)
   constexpr int BN = 128;                   // output columns per workgroup
-  constexpr int NJ = KIND == kGU ? 2 : 1;    // 32-column weight blocks per wave (gu: gate and up)
+  constexpr bool GU = KIND != kDN;
+  constexpr int NJ = GU ? 2 : 1;             // 32-column weight blocks per wave (gu: gate and up)
   __shared__ __align__(16) u8 As[2][BM][APITCH];
   __shared__ int src_row[BM];
-  // Every E8M0 scale the workgroup needs, staged once: the tile's 64 activation rows and the block's weight columns
-  // (gu: 128 gate then 128 up columns; dn: 128 columns), K / 32 bytes each. Per-step byte loads of scales through
-  // the vector memory path (32 rows per instruction) would otherwise cost more than the weight stream itself.
+  __shared__ int live_end;
+  // E8M0 scales staged once: the tile's 64 activation rows and, for kSplit, the block's weight columns (gu: 128 gate
+  // then 128 up columns; dn: 128 columns), K / 32 bytes each.
   extern __shared__ __align__(16) u8 dyn_lds[];
   u8 *Asc = dyn_lds, *Wsc = dyn_lds + BM * (a.K / 32);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  // ---- which tile and column block: the live tiles [0, L) (L = 1 + the last tile with an expert) in eight
+  //      contiguous ranges, range x on XCD x, walked tile-fastest
+  if (tid == 0) live_end = 0;
+  __syncthreads();
+  {
+    int last = 0;
+    for (int t = tid; t < a.max_tiles; t += 256)
+      if (a.tile_info[2 * t] >= 0) last = t + 1;
+    if (last) atomicMax(&live_end, last);
+  }
+  __syncthreads();
+  const int L = live_end;
   const int xcd = (int)(blockIdx.x & 7), xi = (int)(blockIdx.x >> 3);
-  const int tile = xcd + 8 * (xi / a.n_blocks);
-  if (tile >= a.max_tiles) return;
+  const int t_begin = (int)(((int64_t)xcd * L) >> 3), t_end = (int)(((int64_t)(xcd + 1) * L) >> 3);
+  const int cnt = t_end - t_begin;
+  if (cnt <= 0 || xi >= cnt * a.n_blocks) return;
+  const int tile = t_begin + xi % cnt;
   const int N = a.N, K = a.K, C = K / KC;
-  const int n0 = (xi % a.n_blocks) * BN, m0 = tile * BM;
+  const int n0 = (xi / cnt) * BN, m0 = tile * BM;
+  // the tile's expert and row map are loaded together; the weight stream starts as soon as the expert is known,
+  // before the row map, the activation rows and their scales (every workgroup starts at once, so each dependent
+  // round trip before the first weight load is time the HBM idles)
+  const int rm = tid < BM ? a.rowmap[m0 + tid] : -1;
   int expert = a.tile_info[2 * tile];
   if (expert < 0) return;
   expert = expert >= a.E ? a.E - 1 : expert;
 
+  auto clampc = [&](int c) __attribute__((always_inline)) { return c < C ? c : C - 1; };
+  const int SK = K / 32;           // scale bytes per row
+  const int C4 = (C + 3) >> 2;     // kTiled: groups of four chunks per row block
+
+  // ---- weights: this lane's two columns (gu: one column of the gate and of the up matrix) and K half
+  const int h = lane >> 5, lc = lane & 31;
+  const int col = n0 + 32 * wave + lc;       // the lane's output column
+  const u8 *nbj[NJ], *sbj[NJ];
+  if constexpr (GU) {
+    const u8 *gn = a.wn + (int64_t)expert * a.nib_ebytes, *gs = a.wsc + (int64_t)expert * a.sc_ebytes;
+    nbj[0] = gn; sbj[0] = gs;
+    if (a.wn2) { nbj[1] = a.wn2 + (int64_t)expert * a.nib_ebytes; sbj[1] = a.wsc2 + (int64_t)expert * a.sc_ebytes; }
+    else { nbj[1] = gn + a.up_nib_off; sbj[1] = gs + a.up_sc_off; }
+  } else {
+    nbj[0] = a.wn + (int64_t)expert * a.nib_ebytes;
+    sbj[0] = a.wsc + (int64_t)expert * a.sc_ebytes;
+  }
+  // the lane's weight stream: split -- its column's row at K half h; tiled -- lane slot of the wave's row block
+  // (waves past the last column read the last block and store nothing)
+  const u8 *wcn[NJ];
+  const u8 *wcs[NJ];
+  int wrow[NJ];   // kSplit: the lane's weight columns as rows of Wsc (gu: the gate block, then the up block)
+  if constexpr (LAYOUT == kTiled) {
+    int rb = (n0 >> 5) + wave;
+    rb = rb < (N >> 5) ? rb : (N >> 5) - 1;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      wcn[j] = nbj[j] + (int64_t)rb * C * 1024 + 16 * lane;
+      wcs[j] = sbj[j] + (int64_t)rb * C4 * 256 + 4 * lane;
+      wrow[j] = 0;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      wcn[j] = nbj[j] + (int64_t)(col < N ? col : N - 1) * (K / 2) + 16 * h;
+      wcs[j] = nullptr;
+      wrow[j] = 128 * j + 32 * wave + lc;
+    }
+  }
+  constexpr int CSTRIDE = LAYOUT == kTiled ? 1024 : 32;   // bytes between consecutive chunks of the lane's stream
+
+  f32x16 acc[2][NJ];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  // Rings DEPTH super-steps deep; kTiled also carries the scale dword of the super-step's chunk group (kSub divides
+  // four, so the kSub chunks of a super-step share one).
+  v4u aring[DEPTH][kSub], bring[DEPTH][kSub][NJ];
+  u32 sring[DEPTH][NJ];
+  auto load_b = [&](int slot, int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int i = 0; i < kSub; ++i)
+        bring[slot][i][j] = *reinterpret_cast<const v4u *>(wcn[j] + (int64_t)clampc(kSub * st + i) * CSTRIDE);
+    if constexpr (LAYOUT == kTiled) {
+      int g = (kSub * st) >> 2;
+      g = g < C4 ? g : C4 - 1;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) sring[slot][j] = *reinterpret_cast<const u32 *>(wcs[j] + (int64_t)g * 256);
+    }
+  };
+  // the weight stream: the first DEPTH super-steps
+  for_slots([&](auto uc) { constexpr int u = decltype(uc)::value; load_b(u, u); },
+            std::make_integer_sequence<int, DEPTH>{});
+
   int my_src = -1;
   if (tid < BM) {
     int src;
-    if constexpr (KIND == kGU) {
-      const int rm = a.rowmap[m0 + tid];
+    if constexpr (GU) {
       src = rm >= 0 ? rm / a.KU : -1;
       src = src < a.x_rows ? src : -1;
     } else {
-      src = a.rowmap[m0 + tid] >= 0 ? m0 + tid : -1;
+      src = rm >= 0 ? m0 + tid : -1;
     }
     src_row[tid] = src;
     my_src = src;
@@ -168,72 +275,28 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
   const __amdgpu_buffer_rsrc_t xrs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<u8 *>(a.x8), (short)0, (int)((int64_t)a.x_rows * K), 0x00020000);
   const u32 aoff = src_row[arow_i] >= 0 ? (u32)((int64_t)src_row[arow_i] * K + 16 * apart) : 0x80000000u;
-  auto clampc = [&](int c) __attribute__((always_inline)) { return c < C ? c : C - 1; };
-  const int SK = K / 32;   // scale bytes per row
-
-  // ---- weights: this lane's two columns (gu: one column of the gate and of the up matrix) and K half
-  const int h = lane >> 5, lc = lane & 31;
-  const u8 *nbj[NJ], *sbj[NJ];
-  const int col = n0 + 32 * wave + lc;       // the lane's output column
-  if constexpr (KIND == kGU) {
-    const u8 *gn = a.wn + (int64_t)expert * a.nib_ebytes, *gs = a.wsc + (int64_t)expert * a.sc_ebytes;
-    nbj[0] = gn; sbj[0] = gs;
-    if (a.wn2) { nbj[1] = a.wn2 + (int64_t)expert * a.nib_ebytes; sbj[1] = a.wsc2 + (int64_t)expert * a.sc_ebytes; }
-    else { nbj[1] = gn + a.up_nib_off; sbj[1] = gs + a.up_sc_off; }
-  } else {
-    nbj[0] = a.wn + (int64_t)expert * a.nib_ebytes;
-    sbj[0] = a.wsc + (int64_t)expert * a.sc_ebytes;
-  }
-  const u8 *wcn[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) wcn[j] = nbj[j] + (int64_t)(col < N ? col : N - 1) * (K / 2) + 16 * h;
-  int wrow[NJ];   // the lane's weight columns as rows of Wsc (gu: the gate block, then the up block)
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) wrow[j] = 128 * j + 32 * wave + lc;
-
-  f32x16 acc[2][NJ];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-  // Rings DEPTH super-steps deep. A super-step reads kSub consecutive 32-byte chunks of each weight column -- a
-  // whole 128-byte line for kSub = 4 -- with back-to-back loads, so the L1 merges them into one request per line.
-  v4u aring[DEPTH][kSub], bring[DEPTH][kSub][NJ];
   auto load_a = [&](int slot, int st) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < kSub; ++i)
       aring[slot][i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)(aoff + (u32)(clampc(kSub * st + i) * KC)), 0, 0);
   };
-  auto load_b = [&](int slot, int st) __attribute__((always_inline)) {
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-#pragma unroll
-      for (int i = 0; i < kSub; ++i)
-        bring[slot][i][j] = *reinterpret_cast<const v4u *>(wcn[j] + (int64_t)clampc(kSub * st + i) * 32);
-  };
   auto stage = [&](int slot, int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < kSub; ++i) *reinterpret_cast<v4u *>(&As[buf][arow_i][KC * i + 16 * apart]) = aring[slot][i];
   };
-  // The first activation chunk, then the weights, so the stream is running while the scales are staged; staging
-  // the first chunk waits only for its own load (loads complete in issue order), and precedes the loads that
-  // reuse its ring slot.
+  // the first activation chunk and the activation rows' scales (a gathered row each; up to K = 4096 one batch of
+  // loads) are issued together and land one round trip after the first weights; then the chunk is staged and the
+  // next ones go into the ring. kSplit also stages the weight column blocks' scales.
   load_a(0, 0);
-  for_slots([&](auto uc) { constexpr int u = decltype(uc)::value; load_b(u, u); },
-            std::make_integer_sequence<int, DEPTH>{});
-  stage(0, 0);
-  for_slots([&](auto uc) { constexpr int u = decltype(uc)::value; load_a((u + 1) % DEPTH, u + 1); },
-            std::make_integer_sequence<int, DEPTH>{});
-  // the scale rows: activation rows (a gathered row each), then the weight column blocks (contiguous in memory)
-  batched_copy(reinterpret_cast<u16 *>(Asc), (int64_t)BM * (SK / 2), tid, [&](int64_t i) {
+  batched_copy<16>(reinterpret_cast<u16 *>(Asc), (int64_t)BM * (SK / 2), tid, [&](int64_t i) {
     const int r = (int)(i / (SK / 2)), q = (int)(i % (SK / 2));
     const int sr = src_row[r] >= 0 ? src_row[r] : 0;
     return reinterpret_cast<const u16 *>(a.xs + (int64_t)sr * SK)[q];
   });
-  {
+  stage(0, 0);
+  for_slots([&](auto uc) { constexpr int u = decltype(uc)::value; load_a((u + 1) % DEPTH, u + 1); },
+            std::make_integer_sequence<int, DEPTH>{});
+  if constexpr (LAYOUT == kSplit) {
     const int cols = N - n0 < BN ? N - n0 : BN;   // columns past N are never stored
 #pragma unroll
     for (int m = 0; m < NJ; ++m) copy_to_lds(Wsc + m * BN * SK, sbj[m] + (int64_t)n0 * SK, (int64_t)cols * SK, tid);
@@ -251,8 +314,9 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
     const int buf = st & 1;
 #pragma unroll
     for (int i = 0; i < kSub; ++i) {
-      const bool live = kSub * st + i < C;
-      const int sc_off = 2 * clampc(kSub * st + i) + h;   // the lane's E8M0 byte of this chunk in a scale row
+      const int c = kSub * st + i;
+      const bool live = c < C;
+      const int sc_off = 2 * clampc(c) + h;   // the lane's E8M0 byte of this chunk in a scale row
       auto afrag = [&](int ii, i32x8 &af, int &sa) __attribute__((always_inline)) {
         const v4u v0 = *reinterpret_cast<const v4u *>(&As[buf][32 * ii + lc][KC * i + 16 * h]);
         const v4u v1 = *reinterpret_cast<const v4u *>(&As[buf][32 * ii + lc][KC * i + 32 + 16 * h]);
@@ -265,7 +329,8 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
       for (int j = 0; j < NJ; ++j) {
         const v4u bv = bring[u][i][j];
         bf[j] = i32x8{(int)bv.x, (int)bv.y, (int)bv.z, (int)bv.w, 0, 0, 0, 0};
-        sb[j] = live ? Wsc[wrow[j] * SK + sc_off] : 0;
+        if constexpr (LAYOUT == kTiled) sb[j] = live ? (int)((sring[u][j] >> (8 * (c & 3))) & 255u) : 0;
+        else sb[j] = live ? Wsc[wrow[j] * SK + sc_off] : 0;
       }
       {
         i32x8 af;
@@ -294,6 +359,45 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
   for (int s0 = 0; s0 < SP; s0 += DEPTH)
     for_steps(step, s0, std::make_integer_sequence<int, DEPTH>{});
 
+  if constexpr (KIND == kGU8) {
+    // The activation quantized to MXFP8 in registers, as qmm_quant_mxfp8 quantizes it: the 32 columns of a row's
+    // block are the 32 lanes of a half-wave, so its maximum is a butterfly over lane bits 0-4 (DPP and ds_swizzle
+    // partners; every lane of the half ends with the maximum). Codes and scales go
+    // through LDS (the activation buffers are free after the loop's last barrier) and leave as whole 16-byte pieces
+    // of each row. Dead rows quantize zeros: codes 0, scale byte 0.
+    static_assert(sizeof(As) >= BM * (BN + 16) + BM * 4, "epilogue staging");
+    u8 *Ot = &As[0][0][0];                    // [64][BN + 16] codes
+    u8 *Osc = Ot + BM * (BN + 16);            // [64][4] scale bytes
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int lr = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+        const float v = src_row[lr] >= 0 ? act_fn(a.act, acc[i][0][r], acc[i][1][r]) : 0.f;
+        float m = fabsf(v);
+        m = fmaxf(m, xshfl<1>(m));
+        m = fmaxf(m, xshfl<2>(m));
+        m = fmaxf(m, xshfl<4>(m));
+        m = fmaxf(m, xshfl<8>(m));
+        m = fmaxf(m, xshfl<16>(m));
+        const int sx = mxfp8_exponent(m);
+        Ot[lr * (BN + 16) + 32 * wave + lc] = (u8)(e4m3_pack2<false>(v, 0.f, sx, 0) & 0xFF);
+        if (lc == 0) Osc[lr * 4 + wave] = (u8)(sx + 127);
+      }
+    __syncthreads();
+    const int cols = N - n0 < BN ? N - n0 : BN;   // a multiple of 32
+    for (int q = tid; q < BM * (BN / 16); q += 256) {
+      const int row = q / (BN / 16), piece = q % (BN / 16);
+      if (16 * piece < cols)
+        *reinterpret_cast<v4u *>(a.y8 + (int64_t)(m0 + row) * N + n0 + 16 * piece) =
+            *reinterpret_cast<const v4u *>(Ot + row * (BN + 16) + 16 * piece);
+    }
+    {
+      const int row = tid >> 2, blk = tid & 3;
+      if (32 * blk < cols) a.ys8[(int64_t)(m0 + row) * (N / 32) + n0 / 32 + blk] = Osc[row * 4 + blk];
+    }
+    return;
+  }
   if (col >= N) return;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -302,48 +406,121 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
       const int lr = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
       float v = 0.f;
       if (src_row[lr] >= 0) {
-        if constexpr (KIND == kGU) v = act_fn(a.act, acc[i][0][r], acc[i][1][r]);
+        if constexpr (GU) v = act_fn(a.act, acc[i][0][r], acc[i][1][r]);
         else v = acc[i][0][r];
       }
       a.y[(int64_t)(m0 + lr) * N + col] = v;
     }
 }
 
-template <int KIND>
+template <int KIND, int LAYOUT>
 int launch(const MArgs &a, hipStream_t s) {
+  constexpr int kDepth = KIND == kDN ? QMM_MX_DEPTH_DN : QMM_MX_DEPTH_GU;
+  constexpr int kSub = KIND == kDN ? QMM_MX_SUB_DN : QMM_MX_SUB_GU;
   const dim3 grid((unsigned)(8 * a.n_blocks * ((a.max_tiles + 7) / 8)));
-  const size_t dyn = (size_t)(BM + (KIND == kGU ? 256 : 128)) * (a.K / 32);
+  const size_t dyn = (size_t)(BM + (LAYOUT == kSplit ? (KIND != kDN ? 256 : 128) : 0)) * (a.K / 32);
   if (dyn > 32768) {   // beyond the default dynamic LDS limit (K > 3276): raise it once
     static bool raised = false;
     if (!raised) {
-      if (hipFuncSetAttribute(reinterpret_cast<const void *>(&mxfp4_grouped_kernel<KIND, kDepth>),
+      if (hipFuncSetAttribute(reinterpret_cast<const void *>(&mxfp4_grouped_kernel<KIND, LAYOUT, kDepth, kSub>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) != hipSuccess)
         return QMM_ERR_LAUNCH;
       raised = true;
     }
   }
-  mxfp4_grouped_kernel<KIND, kDepth><<<grid, 256, dyn, s>>>(a);
+  mxfp4_grouped_kernel<KIND, LAYOUT, kDepth, kSub><<<grid, 256, dyn, s>>>(a);
   return launch_status();
+}
+
+// MFMA-tiled planes from split planes (a byte permutation): one thread per 16-byte lane slot of a 1 KB tile, and
+// per (row block, chunk group) the 64 lanes' four scale bytes. Chunks past K in the last group get scale 0.
+__global__ void tile_mxfp4_kernel(const u8 *__restrict__ nib, const u8 *__restrict__ sc, int64_t rows, int K,
+                                  u8 *__restrict__ nib_t, u8 *__restrict__ sc_t) {
+  const int C = K / KC, C4 = (C + 3) >> 2;
+  const int64_t slots = rows / 32 * C * 64;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < slots) {
+    const int l = (int)(i & 63);
+    const int64_t tile = i >> 6, rb = tile / C;
+    const int c = (int)(tile % C);
+    const int64_t row = 32 * rb + (l & 31);
+    const uint4 v = *reinterpret_cast<const uint4 *>(nib + row * (K / 2) + 32 * c + 16 * (l >> 5));
+    *reinterpret_cast<uint4 *>(nib_t + 16 * i) = v;
+  }
+  const int64_t sslots = rows / 32 * C4 * 64;
+  if (i < sslots) {
+    const int l = (int)(i & 63);
+    const int64_t grp = i >> 6, rb = grp / C4;
+    const int g = (int)(grp % C4);
+    const int64_t row = 32 * rb + (l & 31);
+    u32 w = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = 4 * g + q;
+      if (c < C) w |= (u32)sc[row * (K / 32) + 2 * c + (l >> 5)] << (8 * q);
+    }
+    *reinterpret_cast<u32 *>(sc_t + 4 * i) = w;
+  }
+}
+
+// f32 values of MFMA-tiled planes, one thread per 32-value block (row r, block b): its 16 bytes sit in lane slot
+// 32 (b % 2) + r % 32 of tile (r / 32, b / 2), its E8M0 byte at byte (b / 2) % 4 of that lane's scale dword.
+__global__ void dequant_mxfp4t_kernel(const u8 *__restrict__ nib_t, const u8 *__restrict__ sc_t, int64_t rows, int K,
+                                      float *__restrict__ out) {
+  __shared__ float lut[16];
+  if (threadIdx.x < 16) {
+    const float m[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+    lut[threadIdx.x] = threadIdx.x < 8 ? m[threadIdx.x] : -m[threadIdx.x - 8];
+  }
+  __syncthreads();
+  const int C = K / KC, C4 = (C + 3) >> 2, NB = K / 32;
+  const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gi >= rows * NB) return;
+  const int64_t r = gi / NB;
+  const int b = (int)(gi % NB), c = b >> 1, l = 32 * (b & 1) + (int)(r & 31);
+  const int64_t rb = r >> 5;
+  const u8 *q = nib_t + ((rb * C + c) * 64 + l) * 16;
+  const float s = e8m0_scale(sc_t[((rb * C4 + (c >> 2)) * 64 + l) * 4 + (c & 3)]);
+  float *o = out + gi * 32;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const u32 v = q[j];
+    o[2 * j] = lut[v & 15u] * s;
+    o[2 * j + 1] = lut[v >> 4] * s;
+  }
 }
 
 }  // namespace
 
-// The MXFP4 (split planes) path of qmm_moe_grouped.
-int qmm_grouped_mxfp4(int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
+int64_t qmm_mxfp4t_scale_bytes(int64_t rows, int64_t k) {
+  if (rows <= 0 || rows % 32 || k <= 0 || k % 64) return 0;
+  return rows / 32 * ((k / 64 + 3) / 4) * 256;
+}
+
+// The MXFP4 paths of qmm_moe_grouped: split planes (tiled = 0) or MFMA-tiled planes (tiled = 1).
+int qmm_grouped_mxfp4(int tiled, int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
                       const int32_t *tile_info, const int32_t *rowmap, const void *x, const void *x_scales,
                       int64_t x_rows, const void *w, const void *ws, const void *w2, const void *ws2, float *y,
-                      hipStream_t s) {
+                      uint8_t *y8, uint8_t *ys8, hipStream_t s) {
   if (k % 64 || k > 12288) return QMM_ERR_SHAPE;   // the workgroup stages (64 + 256) x K / 32 scale bytes in LDS
+  if (tiled && n % 32) return QMM_ERR_SHAPE;       // tiled planes hold whole 32-row blocks
   if (x_rows * k >= (1ll << 31)) return QMM_ERR_SHAPE;   // activation rows are addressed by a 32-bit buffer offset
   if (!x_scales || !ws) return QMM_ERR_NULL;
   if (!aligned(x_scales, 2)) return QMM_ERR_ALIGN;
   if (!aligned(x, 16) || !aligned(w, 16) || (w2 && !aligned(w2, 16))) return QMM_ERR_ALIGN;
+  if (tiled && (!aligned(ws, 4) || (ws2 && !aligned(ws2, 4)))) return QMM_ERR_ALIGN;
+  const bool out8 = y8 != nullptr;   // gu with the activation quantized to MXFP8 in the epilogue
+  if (out8 && (mode != 0 || n % 32 || !ys8)) return mode != 0 ? QMM_ERR_RANGE : (ys8 ? QMM_ERR_SHAPE : QMM_ERR_NULL);
+  if (out8 && !aligned(y8, 16)) return QMM_ERR_ALIGN;
   MArgs a{};
   a.N = (int)n; a.K = (int)k;
   a.x8 = static_cast<const u8 *>(x); a.xs = static_cast<const u8 *>(x_scales); a.x_rows = (int)x_rows;
   a.wn = static_cast<const u8 *>(w); a.wsc = static_cast<const u8 *>(ws);
-  a.tile_info = tile_info; a.rowmap = rowmap; a.KU = KU; a.E = E; a.act = act; a.y = y;
-  const int64_t nrow = k / 2, srow = k / 32;
+  a.tile_info = tile_info; a.rowmap = rowmap; a.KU = KU; a.E = E; a.act = act; a.y = y; a.y8 = y8; a.ys8 = ys8;
+  a.n_blocks = (int)((n + 127) / 128);
+  a.max_tiles = (int)max_tiles;
+  const int64_t nrow = k / 2;                                        // nibble bytes per row (both layouts)
+  const int64_t srow = tiled ? qmm_mxfp4t_scale_bytes(32, k) / 32 : k / 32;   // scale bytes per row
   if (mode == 0) {
     if (!fused && (!w2 || !ws2)) return QMM_ERR_NULL;
     a.nib_ebytes = nrow * n * (fused ? 2 : 1);
@@ -352,13 +529,31 @@ int qmm_grouped_mxfp4(int mode, int fused, int act, int64_t max_tiles, int64_t k
     a.up_sc_off = fused ? srow * n : 0;
     a.wn2 = fused ? nullptr : static_cast<const u8 *>(w2);
     a.wsc2 = fused ? nullptr : static_cast<const u8 *>(ws2);
-    a.n_blocks = (int)((n + 127) / 128);
-    a.max_tiles = (int)max_tiles;
-    return launch<kGU>(a, s);
+    if (out8) return tiled ? launch<kGU8, kTiled>(a, s) : launch<kGU8, kSplit>(a, s);
+    return tiled ? launch<kGU, kTiled>(a, s) : launch<kGU, kSplit>(a, s);
   }
   a.nib_ebytes = nrow * n;
   a.sc_ebytes = srow * n;
-  a.n_blocks = (int)((n + 127) / 128);
-  a.max_tiles = (int)max_tiles;
-  return launch<kDN>(a, s);
+  return tiled ? launch<kDN, kTiled>(a, s) : launch<kDN, kSplit>(a, s);
+}
+
+extern "C" int qmm_tile_mxfp4(const void *nibbles, const void *scales, int64_t rows, int64_t k, void *nib_t,
+                              void *sc_t, qmm_stream_t stream) {
+  if (!nibbles || !scales || !nib_t || !sc_t) return QMM_ERR_NULL;
+  if (rows <= 0 || rows % 32 || k <= 0 || k % 64 || k > (1 << 30)) return QMM_ERR_SHAPE;
+  if (!aligned(nibbles, 16) || !aligned(nib_t, 16) || !aligned(sc_t, 4)) return QMM_ERR_ALIGN;
+  const int64_t slots = rows / 32 * (k / 64) * 64;   // >= the scale slots (C4 <= C)
+  tile_mxfp4_kernel<<<(unsigned)((slots + 255) / 256), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      static_cast<const u8 *>(nibbles), static_cast<const u8 *>(scales), rows, (int)k, static_cast<u8 *>(nib_t),
+      static_cast<u8 *>(sc_t));
+  return launch_status();
+}
+
+int qmm_dequant_mxfp4t(const void *w, const void *ws, int64_t rows, int64_t k, float *out, hipStream_t s) {
+  if (rows % 32 || k % 64) return QMM_ERR_SHAPE;
+  if (!aligned(ws, 4)) return QMM_ERR_ALIGN;
+  const int64_t groups = rows * (k / 32);
+  dequant_mxfp4t_kernel<<<(unsigned)((groups + 255) / 256), 256, 0, s>>>(static_cast<const u8 *>(w),
+                                                                         static_cast<const u8 *>(ws), rows, (int)k, out);
+  return launch_status();
 }

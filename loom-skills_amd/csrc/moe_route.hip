@@ -361,9 +361,7 @@ __global__ __launch_bounds__(256) void row_scale_vec_kernel(int64_t rows, int64_
 }
 
 // ---------------------------------------------------------------------------------------------- MXFP8 quant
-// OCP MX: one E8M0 scale per 32 values along a row, E4M3 codes. s = clamp(floor(log2(amax)) - 7, -127, 127) keeps
-// every |x| 2^-s below 256, under the E4M3 maximum 448; the conversion is v_cvt_pk_fp8_f32 (round to nearest even,
-// OCP E4M3FN on gfx950). Consecutive lanes take consecutive 16-byte pieces of the rows (4 f32 or 8 bf16 values); a
+// OCP MX: one E8M0 scale per 32 values along a row, E4M3 codes (mxfp8_exponent, e4m3_pack2). Consecutive lanes take consecutive 16-byte pieces of the rows (4 f32 or 8 bf16 values); a
 // block is the group of 8 (f32) or 4 (bf16) lanes holding it, whose maximum comes from a butterfly inside the group.
 constexpr int kMxBlock = 32;
 
@@ -394,19 +392,14 @@ __global__ __launch_bounds__(256) void quant_mxfp8_vec_kernel(int64_t rows, int6
   for (int i = 0; i < VPL; ++i) amax = fmaxf(amax, fabsf(v[i]));
 #pragma unroll
   for (int off = 1; off < LPB; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-  int sx = -127;
-  if (amax > 0.f) {
-    int ex;
-    frexpf(amax, &ex);        // amax = f 2^ex, f in [0.5, 1)
-    sx = min(max(ex - 1 - 7, -127), 127);
-  }
+  const int sx = mxfp8_exponent(amax);
   if (!live) return;
   u32 out[VPL / 4];
 #pragma unroll
   for (int i = 0; i < VPL / 4; ++i) {
     int w = 0;
-    w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * i], -sx), ldexpf(v[4 * i + 1], -sx), w, false);
-    w = __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(v[4 * i + 2], -sx), ldexpf(v[4 * i + 3], -sx), w, true);
+    w = e4m3_pack2<false>(v[4 * i], v[4 * i + 1], sx, w);
+    w = e4m3_pack2<true>(v[4 * i + 2], v[4 * i + 3], sx, w);
     out[i] = (u32)w;
   }
   if constexpr (BF) {

@@ -26,12 +26,16 @@ SIGNATURES = {
                                 c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
     "qmm_moe_grouped": [c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_int, c_vp,
                         c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
+    "qmm_moe_grouped_mxfp8": [c_int, c_int, c_int, c_i64, c_i64, c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_vp,
+                              c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
     "qmm_row_scale_f16": [c_i64, c_i64, c_vp, c_int, c_vp, c_vp, c_vp, c_vp],
     "qmm_quant_mxfp8": [c_i64, c_i64, c_vp, c_int, c_vp, c_vp, c_vp, c_vp],
     "qmm_repack_mxfp4": [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp],
+    "qmm_tile_mxfp4": [c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp],
+    "qmm_mxfp4t_scale_bytes": [c_i64, c_i64],
     "qmm_moe_combine": [c_i64, c_i64, c_i64, c_int, c_vp, c_vp, c_vp, c_int, c_vp, c_vp],
 }
-RESTYPE = {"qmm_strerror": ctypes.c_char_p, "qmm_row_bytes": c_i64}
+RESTYPE = {"qmm_strerror": ctypes.c_char_p, "qmm_row_bytes": c_i64, "qmm_mxfp4t_scale_bytes": c_i64}
 
 
 class QmmError(RuntimeError):

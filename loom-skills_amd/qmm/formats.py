@@ -4,12 +4,13 @@ Mirrors the reference's format table (skills/loom-port-llm/starter/formats.py:5-
 for the formats this library decodes. The integer codes are this library's own (include/qmm.h, enum qmm_format).
 """
 
-FMT = {"q4_0": 18, "q4_k": 144, "mxfp4": 17, "mxfp4s": 16}     # bytes per block (mxfp4s: the nibble plane only)
-SB = {"q4_0": 32, "q4_k": 256, "mxfp4": 32, "mxfp4s": 32}      # values per block
-SPLIT = frozenset({"mxfp4s"})                                   # weight plane + scale plane (two operands)
+# mxfp4t: MXFP4 in MFMA-tiled planes (this library's load-time layout for the grouped GEMM, qmm_tile_mxfp4)
+FMT = {"q4_0": 18, "q4_k": 144, "mxfp4": 17, "mxfp4s": 16, "mxfp4t": 16}   # bytes per block (split: nibble plane)
+SB = {"q4_0": 32, "q4_k": 256, "mxfp4": 32, "mxfp4s": 32, "mxfp4t": 32}    # values per block
+SPLIT = frozenset({"mxfp4s", "mxfp4t"})                         # weight plane + scale plane (two operands)
 SCALE_DIV = {"mxfp4s": 16}                                      # nibble-plane bytes per scale-plane byte
 
-CODE = {"q4_0": 0, "q4_k": 1, "mxfp4": 2, "mxfp4s": 3}          # enum qmm_format
+CODE = {"q4_0": 0, "q4_k": 1, "mxfp4": 2, "mxfp4s": 3, "mxfp4t": 4}   # enum qmm_format
 DTYPE = {"f32": 0, "f16": 1, "bf16": 2, "mxfp8": 3, "q8": 4}    # enum qmm_dtype
 MX_BLOCK = 32                                                   # values per E8M0 scale of an MXFP8 operand
 GEMM_MODE = {"store": 0, "acc": 1, "swiglu": 2}                 # enum qmm_gemm_mode
@@ -25,5 +26,8 @@ def row_bytes(fmt, k):
 
 
 def scale_row_bytes(fmt, k):
-    """Bytes of one row of a split format's scale plane (K/32 E8M0 bytes)."""
+    """Bytes of one row of a split format's scale plane: K/32 E8M0 bytes (mxfp4s), or the tiled plane's share of a
+    32-row block, 8 bytes per started group of four 64-value chunks (mxfp4t)."""
+    if fmt == "mxfp4t":
+        return (k // 64 + 3) // 4 * 8
     return row_bytes(fmt, k) // SCALE_DIV[fmt] if fmt in SPLIT else 0

@@ -15,8 +15,9 @@ S/ = skills/loom-port-llm/starter/):
     row_scale_f16     g_row_scale_f16[_tiles]                 S/gen_llm.py:1843-1915, S/gen_moe.py:503-527
     dequant           the @g_<fmt>_values helpers (bit-exact f32 values)
 
-plus the gfx950-specific producers ``quant_mxfp8`` (A operand of the scaled MFMA) and ``repack_mxfp4`` (GGUF
-MXFP4 blocks to split planes, a one-time weight preparation).
+plus the gfx950-specific producers ``quant_mxfp8`` (A operand of the scaled MFMA), ``repack_mxfp4`` (GGUF
+MXFP4 blocks to split planes) and ``tile_mxfp4`` (split planes to the MFMA-tiled planes the grouped GEMM streams
+fastest), the last two one-time weight preparations.
 
 Every function validates its arguments on the host (the C ABI returns a status that becomes ``QmmError``) and
 launches asynchronously on torch's current stream. Weights are uint8 tensors holding the raw GGUF block bytes.
@@ -162,6 +163,8 @@ def moe_expert_mv(fmt, mode, ids, x, w, n, k, E, KU, w2=None, ws=None, ws2=None,
                   bias=None, bias2=None, y=None):
     """Decode expert matvecs: mode 'gu' act[a] = act(Wg[e] x[a/KU], Wu[e] x[a/KU]) or 'dn' ys[a] = Wd[e] x[a]."""
     _dev(ids, x, w, w2, ws, ws2, bias, bias2, y)
+    if fmt == "mxfp4t":
+        raise ValueError("the decode expert matvecs read split planes (mxfp4s); mxfp4t is the grouped GEMM's layout")
     A = ids.numel()
     y = torch.empty((A, n), dtype=torch.float32, device=x.device) if y is None else y
     m = {"gu": 0, "dn": 1}[mode]
@@ -187,6 +190,21 @@ def moe_grouped(fmt, mode, tile_info, rowmap, x, w, n, k, E, KU, w2=None, ws=Non
               _ptr(tile_info), _ptr(rowmap), _ptr(x), xd, _ptr(x_scales), x.shape[0], _ptr(w), _ptr(ws), _ptr(w2),
               _ptr(ws2), _ptr(y), _stream())
     return y
+
+
+def moe_grouped_mxfp8(fmt, tile_info, rowmap, x, w, n, k, E, KU, w2=None, ws=None, ws2=None, x_scales=None,
+                      fused=False, act="silu", codes=None, scales=None):
+    """The MXFP4 gate/up grouped GEMM with its activation quantized to MXFP8 in the epilogue: (codes u8
+    [max_tiles*64, n], scales u8 [max_tiles*64, n/32]) == quant_mxfp8(moe_grouped(fmt, "gu", ...), tile_info) bit
+    for bit. x: E4M3 codes with x_scales (quant_mxfp8)."""
+    _dev(tile_info, rowmap, x, w, w2, ws, ws2, x_scales, codes, scales)
+    rows = tile_info.shape[0] * TILE
+    codes = torch.empty((rows, n), dtype=torch.uint8, device=x.device) if codes is None else codes
+    scales = torch.empty((rows, n // MX_BLOCK), dtype=torch.uint8, device=x.device) if scales is None else scales
+    _lib.call("qmm_moe_grouped_mxfp8", CODE[fmt], int(fused), ACT[act], tile_info.shape[0], k, n, E, KU,
+              _ptr(tile_info), _ptr(rowmap), _ptr(x), _ptr(x_scales), x.shape[0], _ptr(w), _ptr(ws), _ptr(w2),
+              _ptr(ws2), _ptr(codes), _ptr(scales), _stream())
+    return codes, scales
 
 
 def moe_combine(ys, wts, pos=None, y=None, accumulate=False):
@@ -229,6 +247,20 @@ def repack_mxfp4(w, rows, k):
     return nib, sc
 
 
+def tile_mxfp4(nib, sc, rows, k):
+    """Split planes (nibbles u8 [rows, k/2], scales u8 [rows, k/32]) -> MFMA-tiled planes (nib_t u8 [rows*k/2],
+    sc_t u8 [qmm_mxfp4t_scale_bytes]) for the grouped GEMM (format "mxfp4t"). rows % 32 == 0, k % 64 == 0; a
+    stack of experts tiles as one matrix when each expert's rows are a multiple of 32."""
+    _dev(nib, sc)
+    nb = _lib.load().qmm_mxfp4t_scale_bytes(rows, k)
+    if nb <= 0:
+        raise ValueError(f"mxfp4t needs rows % 32 == 0 and k % 64 == 0 (rows={rows}, k={k})")
+    nib_t = torch.empty(rows * k // 2, dtype=torch.uint8, device=nib.device)
+    sc_t = torch.empty(nb, dtype=torch.uint8, device=nib.device)
+    _lib.call("qmm_tile_mxfp4", _ptr(nib), _ptr(sc), rows, k, _ptr(nib_t), _ptr(sc_t), _stream())
+    return nib_t, sc_t
+
+
 def weight_bytes(fmt, rows, k):
     return rows * row_bytes(fmt, k)
 
@@ -248,16 +280,20 @@ def moe_prefill(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up
                         fused=fused, act=act)
         a16, as_ = row_scale_f16(a, tile_info=tile_info)
         ys = moe_grouped("q4_k", "dn", tile_info, rowmap, a16, w_down, H, FE, E, KU, x_scales=as_)
-    elif fmt == "mxfp4s":
+    elif fmt in ("mxfp4s", "mxfp4t"):
+        # the gate/up GEMM writes its activation as MXFP8 directly (the down GEMM's A operand)
         x8, xs = quant_mxfp8(x)
-        a = moe_grouped("mxfp4s", "gu", tile_info, rowmap, x8, w_gate, FE, H, E, KU, w2=w_up, ws=ws_gate,
-                        ws2=ws_up, x_scales=xs, fused=fused, act=act)
-        a8, as8 = quant_mxfp8(a, tile_info=tile_info)
-        ys = moe_grouped("mxfp4s", "dn", tile_info, rowmap, a8, w_down, H, FE, E, KU, ws=ws_down, x_scales=as8)
+        a8, as8 = moe_grouped_mxfp8(fmt, tile_info, rowmap, x8, w_gate, FE, H, E, KU, w2=w_up, ws=ws_gate,
+                                    ws2=ws_up, x_scales=xs, fused=fused, act=act)
+        a = None
+        ys = moe_grouped(fmt, "dn", tile_info, rowmap, a8, w_down, H, FE, E, KU, ws=ws_down, x_scales=as8)
     else:
         raise ValueError(f"no grouped path for {fmt}")
     y = moe_combine(ys, wts, pos=pos)
-    return y, {"ids": ids, "wts": wts, "tile_info": tile_info, "rowmap": rowmap, "pos": pos, "act": a, "ys": ys}
+    mid = {"ids": ids, "wts": wts, "tile_info": tile_info, "rowmap": rowmap, "pos": pos, "act": a, "ys": ys}
+    if a is None:
+        mid.update(act8=a8, act_scales=as8)
+    return y, mid
 
 
 def moe_decode(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=None, ws_gate=None, ws_down=None,

@@ -8,6 +8,8 @@ as the reference's decoders do, so any correct implementation reproduces them bi
 * Q4_K  (144 B / 256 values) S/gen_llm.py:234-326 (@g_k_scale_minimum, @g_k_metadata, @g_q4_k_values)
 * MXFP4 GGUF (17 B / 32)     S/gen_llm.py:786-841 (@g_mxfp4_values)
 * MXFP4 split planes         S/gen_llm.py:844-895 (@g_mxfp4s_values), S/st_tensors.py:17-33 (dequant_mxfp4)
+* MXFP4 MFMA-tiled planes    this library's load-time layout of the split planes (no reference counterpart); a byte
+                             permutation, so its values are the split planes' values
 """
 import numpy as np
 
@@ -137,6 +139,45 @@ def mxfp4_to_split(raw, rows, k):
     return pairs.reshape(rows, k // 2), e
 
 
+def mxfp4s_to_tiled(nibbles, scales, rows, k):
+    """Split planes -> MFMA-tiled planes, written element by element from the layout's definition:
+    nib_t[rb, c, l, :] = nibbles[32 rb + l % 32, 32 c + 16 (l // 32) : +16] and byte q of sc_t[rb, g, l, :] =
+    scales[32 rb + l % 32, 2 (4 g + q) + l // 32] (0 when chunk 4 g + q lies past K). rows % 32 == 0, k % 64 == 0."""
+    assert rows % 32 == 0 and k % 64 == 0, (rows, k)
+    nib = np.asarray(nibbles).view(np.uint8).reshape(rows, k // 2)
+    sc = np.asarray(scales).view(np.uint8).reshape(rows, k // 32)
+    RB, C = rows // 32, k // 64
+    C4 = (C + 3) // 4
+    lanes = np.arange(64)
+    li, lh = lanes % 32, lanes // 32
+    nt = np.empty((RB, C, 64, 16), np.uint8)
+    st = np.zeros((RB, C4, 64, 4), np.uint8)
+    for rb in range(RB):
+        r = 32 * rb + li
+        for c in range(C):
+            cols = 32 * c + 16 * lh[:, None] + np.arange(16)[None, :]
+            nt[rb, c] = nib[r[:, None], cols]
+            st[rb, c // 4, :, c % 4] = sc[r, 2 * c + lh]
+    return nt.reshape(-1), st.reshape(-1)
+
+
+def mxfp4t_to_split(nib_t, sc_t, rows, k):
+    """Inverse of mxfp4s_to_tiled (vectorized, an independent construction: index arithmetic instead of loops)."""
+    RB, C = rows // 32, k // 64
+    C4 = (C + 3) // 4
+    nt = np.asarray(nib_t).view(np.uint8).reshape(RB, C, 2, 32, 16)       # [rb, c, h, i, byte]
+    nib = nt.transpose(0, 3, 1, 2, 4).reshape(rows, k // 2)                # row 32 rb + i, byte 32 c + 16 h + j
+    st = np.asarray(sc_t).view(np.uint8).reshape(RB, C4, 2, 32, 4)        # [rb, g, h, i, q]
+    s = st.transpose(0, 3, 1, 4, 2).reshape(rows, C4 * 4 * 2)[:, : k // 32]  # block 2 (4 g + q) + h
+    return np.ascontiguousarray(nib), np.ascontiguousarray(s)
+
+
+def dequant_mxfp4t(nib_t, sc_t, rows, k):
+    """MXFP4 MFMA-tiled planes: the values of the split planes they permute."""
+    nib, sc = mxfp4t_to_split(nib_t, sc_t, rows, k)
+    return dequant_mxfp4s(nib, sc, rows, k)
+
+
 def dequantize(fmt, raw, rows, k, scales=None):
     if fmt == "q4_0":
         return dequant_q4_0(raw, rows, k)
@@ -146,4 +187,6 @@ def dequantize(fmt, raw, rows, k, scales=None):
         return dequant_mxfp4(raw, rows, k)
     if fmt == "mxfp4s":
         return dequant_mxfp4s(raw, scales, rows, k)
+    if fmt == "mxfp4t":
+        return dequant_mxfp4t(raw, scales, rows, k)
     raise ValueError(fmt)

@@ -69,6 +69,9 @@ def test_host_only_entry_points(lib):
     assert lib.qmm_row_bytes(0, 2816) == 1584
     assert lib.qmm_row_bytes(2, 2880) == 1530
     assert lib.qmm_row_bytes(3, 2880) == 1440
+    assert lib.qmm_row_bytes(4, 2880) == 1440          # MFMA-tiled planes: the split nibble plane's bytes
+    assert lib.qmm_mxfp4t_scale_bytes(64, 2880) == 2 * 12 * 256   # 45 chunks -> 12 groups of four
+    assert lib.qmm_mxfp4t_scale_bytes(48, 2880) == 0 and lib.qmm_mxfp4t_scale_bytes(64, 2848) == 0
     assert lib.qmm_row_bytes(1, 100) == 0
     assert lib.qmm_row_bytes(7, 256) == 0
     assert lib.qmm_strerror(-2) == b"invalid shape"
@@ -108,6 +111,21 @@ def test_argument_validation_without_a_device(lib):
     # quantizer / repack shapes
     assert lib.qmm_quant_mxfp8(4, 48, fake, 0, n, fake, fake, n) == st["QMM_ERR_SHAPE"]
     assert lib.qmm_repack_mxfp4(fake, 4, 48, fake, fake, n) == st["QMM_ERR_SHAPE"]
+    # MFMA-tiled planes: whole 32-row blocks and 64-value chunks; no GEMV or decode matvec reads them
+    assert lib.qmm_tile_mxfp4(fake, fake, 48, 64, fake, fake, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_tile_mxfp4(fake, fake, 32, 96, fake, fake, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_tile_mxfp4(fake, n, 32, 64, fake, fake, n) == st["QMM_ERR_NULL"]
+    assert lib.qmm_dequant(4, fake, fake, 48, 64, fake, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_mv(4, 64, 4, 1, 0, fake, 0, fake, fake, fake, n) == st["QMM_ERR_FORMAT"]
+    assert lib.qmm_moe_grouped(4, 0, 1, 0, 4, 128, 48, 4, 2, fake, fake, fake, 3, fake, 8, fake, fake, n, n,
+                               fake, n) == st["QMM_ERR_SHAPE"]          # n % 32 != 0
+    # the gate/up GEMM with MXFP8 output: MXFP4 weights only, whole 32-column blocks, both outputs
+    assert lib.qmm_moe_grouped_mxfp8(1, 1, 0, 4, 256, 64, 4, 2, fake, fake, fake, fake, 8, fake, n, n, n, fake, fake,
+                                     n) == st["QMM_ERR_FORMAT"]
+    assert lib.qmm_moe_grouped_mxfp8(4, 1, 0, 4, 128, 48, 4, 2, fake, fake, fake, fake, 8, fake, fake, n, n, fake,
+                                     fake, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_moe_grouped_mxfp8(4, 1, 0, 4, 128, 64, 4, 2, fake, fake, fake, fake, 8, fake, fake, n, n, fake,
+                                     n, n) == st["QMM_ERR_NULL"]
 
 
 def test_python_surface_refuses_host_tensors():

@@ -55,8 +55,9 @@ class Experts:
     def down(self, e):
         return self.rows(self.d, self.H * e, self.H * (e + 1), self.FE)
 
-    def device(self, split):
-        """kwargs of ops.moe_prefill / moe_decode; split: MXFP4 as split planes (repacked on the device)."""
+    def device(self, split, tiled=False):
+        """kwargs of ops.moe_prefill / moe_decode; split: MXFP4 as split planes (repacked on the device); tiled:
+        then tiled for the grouped GEMM (format mxfp4t)."""
         ops = _ops()
         dv = lambda a: dev_u8(a, self.dev)
         if self.fmt == "q4_k" or not split:
@@ -75,17 +76,24 @@ class Experts:
             kw = dict(w_gate=gn, ws_gate=gs, w_up=un, ws_up=us)
         dn, ds = ops.repack_mxfp4(dv(self.d), E * H, FE)
         kw.update(w_down=dn, ws_down=ds)
-        return "mxfp4s", kw
+        if not tiled:
+            return "mxfp4s", kw
+        rows = {"gate": E * FE * (2 if self.fused else 1), "up": E * FE, "down": E * H}
+        for m in ("gate", "up", "down"):
+            if "w_" + m in kw:
+                kw["w_" + m], kw["ws_" + m] = ops.tile_mxfp4(kw["w_" + m], kw["ws_" + m], rows[m],
+                                                            FE if m == "down" else H)
+        return "mxfp4t", kw
 
 
-def _run_chain(dev, fmt, E, KU, H, FE, T, gating, norm, act, fused, prefill, seed, live_logits=None):
+def _run_chain(dev, fmt, E, KU, H, FE, T, gating, norm, act, fused, prefill, seed, live_logits=None, tiled=False):
     import torch
     from qmm import synth
     rng = np.random.default_rng(seed)
     ex = Experts(dev, fmt, rng, E, H, FE, fused)
     xb = synth.to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32))
     logits = rng.standard_normal((T, E)).astype(np.float32) if live_logits is None else live_logits
-    wfmt, kw = ex.device(split=prefill)
+    wfmt, kw = ex.device(split=prefill, tiled=tiled)
     chain = _ops().moe_prefill if prefill else _ops().moe_decode
     y, mid = chain(wfmt, dev_bf16(xb, dev), dev_f32(logits, dev), E, KU, H, FE, gating, norm, fused=fused, act=act,
                    **kw)
@@ -112,20 +120,23 @@ def test_q4_k_moe_qwen3_30b_a3b_shape(dev, prefill):
     assert_close_rel_l2(y, want, 1e-3, f"q4_k moe prefill={prefill}")
 
 
-@pytest.mark.parametrize("T,prefill", [(256, True), (1024, True), (1, False)])
-def test_mxfp4_moe_gpt_oss_20b_shape(dev, T, prefill):
+@pytest.mark.parametrize("T,prefill,tiled", [(256, True, False), (256, True, True), (1024, True, True),
+                                             (1, False, False)])
+def test_mxfp4_moe_gpt_oss_20b_shape(dev, T, prefill, tiled):
     """32 experts, top-4 with softmax over the picked logits (gating 3), H = FE = 2880, fused gate_up,
-    swiglu_oai; prefill quantizes activations to MXFP8 for the scaled MFMA, decode multiplies bf16 directly."""
+    swiglu_oai; prefill quantizes activations to MXFP8 for the scaled MFMA (weights as split planes or MFMA-tiled
+    planes), decode multiplies bf16 directly."""
     y, want, _ = _run_chain(dev, "mxfp4", 32, 4, 2880, 2880, T, 3, False, "swiglu_oai", True, prefill,
-                            seed=20261203 + T)
-    assert_close_rel_l2(y, want, 1e-3, f"mxfp4 moe T={T}")
+                            seed=20261203 + T, tiled=tiled)
+    assert_close_rel_l2(y, want, 1e-3, f"mxfp4 moe T={T} tiled={tiled}")
 
 
-@pytest.mark.parametrize("fmt,E,KU,H,FE,gating,norm,act,fused", [
-    ("q4_k", 128, 8, 2048, 768, 1, True, "silu", False),            # Qwen3-30B-A3B
-    ("mxfp4", 32, 4, 2880, 2880, 3, False, "swiglu_oai", True),     # gpt-oss-20b
+@pytest.mark.parametrize("fmt,E,KU,H,FE,gating,norm,act,fused,tiled", [
+    ("q4_k", 128, 8, 2048, 768, 1, True, "silu", False, False),            # Qwen3-30B-A3B
+    ("mxfp4", 32, 4, 2880, 2880, 3, False, "swiglu_oai", True, False),     # gpt-oss-20b, split planes
+    ("mxfp4", 32, 4, 2880, 2880, 3, False, "swiglu_oai", True, True),      # gpt-oss-20b, MFMA-tiled planes
 ])
-def test_moe_prefill_large_batch_rows_match_small_batch(dev, fmt, E, KU, H, FE, gating, norm, act, fused):
+def test_moe_prefill_large_batch_rows_match_small_batch(dev, fmt, E, KU, H, FE, gating, norm, act, fused, tiled):
     """T = 4096 (4 to 8 tiles an expert): every token's output is a function of that token alone (per-row
     activation rounding, fixed K order in the grouped GEMMs, combine in slot order), so the rows of a 4096-token
     chain equal bit for bit those of a 256-token chain run on a slice of the same tokens. Ties the large-batch
@@ -135,7 +146,7 @@ def test_moe_prefill_large_batch_rows_match_small_batch(dev, fmt, E, KU, H, FE, 
     ops = _ops()
     rng = np.random.default_rng(31 + E)
     ex = Experts(dev, fmt, rng, E, H, FE, fused)
-    wfmt, kw = ex.device(split=True)
+    wfmt, kw = ex.device(split=True, tiled=tiled)
     T, lo, hi = 4096, 1500, 1756
     xb = dev_bf16(synth.to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32)), dev)
     logits = dev_f32(rng.standard_normal((T, E)).astype(np.float32), dev)
@@ -151,14 +162,16 @@ def test_moe_prefill_large_batch_rows_match_small_batch(dev, fmt, E, KU, H, FE, 
     np.testing.assert_array_equal(b[lo:hi].view(np.uint32), s.view(np.uint32))
 
 
-@pytest.mark.parametrize("fmt,fused,act", [("q4_k", True, "swiglu_oai"), ("q4_k", False, "silu"),
-                                           ("mxfp4", False, "silu"), ("mxfp4", True, "swiglu_oai")])
-def test_moe_prefill_small_shapes_heavy_expert(dev, fmt, fused, act):
-    E, KU, H, FE, T = 8, 2, 512, 256 if fmt == "q4_k" else 320, 100
+@pytest.mark.parametrize("fmt,fused,act,tiled", [("q4_k", True, "swiglu_oai", False), ("q4_k", False, "silu", False),
+                                                 ("mxfp4", False, "silu", False), ("mxfp4", True, "swiglu_oai", False),
+                                                 ("mxfp4", False, "silu", True), ("mxfp4", True, "swiglu_oai", True)])
+def test_moe_prefill_small_shapes_heavy_expert(dev, fmt, fused, act, tiled):
+    E, KU, H, FE, T = 8, 2, 512, 256 if fmt == "q4_k" else 320, 100   # FE = 320: a half-filled last column block
     rng = np.random.default_rng(5)
     logits = rng.standard_normal((T, E)).astype(np.float32)
     logits[:80, 3] += 6.0                      # expert 3 gets more than 64 rows: two tiles
-    y, want, mid = _run_chain(dev, fmt, E, KU, H, FE, T, 1, True, act, fused, True, seed=11, live_logits=logits)
+    y, want, mid = _run_chain(dev, fmt, E, KU, H, FE, T, 1, True, act, fused, True, seed=11, live_logits=logits,
+                              tiled=tiled)
     ti = host(mid["tile_info"])
     assert (ti[:, 0] == 3).sum() == 2
     assert_close_rel_l2(y, want, 1e-3, f"{fmt} small moe")
@@ -203,3 +216,85 @@ def test_quant_mxfp8_matches_oracle(dev):
     np.testing.assert_array_equal(host(scales), es)
     c = host(codes)
     assert np.all(ref.e4m3_decode(c) == ref.e4m3_decode(ec))
+
+
+@pytest.mark.parametrize("T,E,H,FE", [(256, 32, 2880, 2880), (100, 8, 512, 320)])
+def test_grouped_mxfp4_tiled_equals_split_bit_for_bit(dev, T, E, H, FE):
+    """The MFMA-tiled planes feed the scaled MFMA the same operands in the same K order as the split planes, so
+    both grouped GEMMs (fused gate_up with swiglu_oai, and down) give identical bits on every live row."""
+    import torch
+    from qmm import synth
+    ops = _ops()
+    rng = np.random.default_rng(40 + T)
+    KU = 4 if E == 32 else 2
+    ex = Experts(dev, "mxfp4", rng, E, H, FE, True)
+    _, ks = ex.device(split=True)
+    _, kt = ex.device(split=True, tiled=True)
+    xb = dev_bf16(synth.to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32)), dev)
+    logits = dev_f32(rng.standard_normal((T, E)).astype(np.float32), dev)
+    ids, _ = ops.moe_topk(logits, KU, 3, False)
+    ti, rm, _ = ops.moe_bucket(ids, E)
+    x8, xs = ops.quant_mxfp8(xb)
+    live = host(rm) >= 0
+    a_s = ops.moe_grouped("mxfp4s", "gu", ti, rm, x8, ks["w_gate"], FE, H, E, KU, ws=ks["ws_gate"], x_scales=xs,
+                          fused=True, act="swiglu_oai")
+    a_t = ops.moe_grouped("mxfp4t", "gu", ti, rm, x8, kt["w_gate"], FE, H, E, KU, ws=kt["ws_gate"], x_scales=xs,
+                          fused=True, act="swiglu_oai")
+    a8, as8 = ops.quant_mxfp8(a_s, tile_info=ti)
+    y_s = ops.moe_grouped("mxfp4s", "dn", ti, rm, a8, ks["w_down"], H, FE, E, KU, ws=ks["ws_down"], x_scales=as8)
+    y_t = ops.moe_grouped("mxfp4t", "dn", ti, rm, a8, kt["w_down"], H, FE, E, KU, ws=kt["ws_down"], x_scales=as8)
+    torch.cuda.synchronize()
+    for s, t, what in ((a_s, a_t, "gate_up"), (y_s, y_t, "down")):
+        hs, ht = host(s)[live], host(t)[live]
+        assert np.all(np.isfinite(hs)) and np.abs(hs).max() > 0
+        np.testing.assert_array_equal(ht.view(np.uint32), hs.view(np.uint32), err_msg=what)
+
+
+def test_tile_mxfp4_bit_exact(dev):
+    """qmm_tile_mxfp4 against the oracle's element-by-element construction; qmm_dequant of the tiled planes
+    against the split planes' values."""
+    from qmm import synth
+    ops = _ops()
+    rng = np.random.default_rng(41)
+    for rows, k in ((64, 2880), (96, 320), (32, 64)):
+        w = synth.mxfp4_weights(rng, rows, k)
+        nib, sc = ops.repack_mxfp4(dev_u8(w, dev), rows, k)
+        nt, st = ops.tile_mxfp4(nib, sc, rows, k)
+        en, es = of.mxfp4s_to_tiled(host(nib), host(sc), rows, k)
+        np.testing.assert_array_equal(host(nt), en)
+        np.testing.assert_array_equal(host(st), es)
+        got = host(ops.dequant("mxfp4t", nt, rows, k, ws=st))
+        want = of.dequant_mxfp4s(host(nib), host(sc), rows, k)
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("T,E,H,FE,tiled", [(256, 32, 2880, 2880, True), (256, 32, 2880, 2880, False),
+                                            (100, 8, 512, 320, True)])
+def test_grouped_gate_up_mxfp8_output_equals_quantized_act(dev, T, E, H, FE, tiled):
+    """The gate/up GEMM with the MXFP8 quantization fused into its epilogue writes exactly the codes and scales
+    quant_mxfp8 makes of the f32 activation the plain gate/up GEMM writes (every row of every live tile, dead rows
+    as zeros)."""
+    import torch
+    from qmm import synth
+    ops = _ops()
+    rng = np.random.default_rng(50 + T + FE)
+    KU = 4 if E == 32 else 2
+    ex = Experts(dev, "mxfp4", rng, E, H, FE, True)
+    wfmt, kw = ex.device(split=True, tiled=tiled)
+    xb = dev_bf16(synth.to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32)), dev)
+    logits = dev_f32(rng.standard_normal((T, E)).astype(np.float32), dev)
+    ids, _ = ops.moe_topk(logits, KU, 3, False)
+    ti, rm, _ = ops.moe_bucket(ids, E)
+    x8, xs = ops.quant_mxfp8(xb)
+    a = ops.moe_grouped(wfmt, "gu", ti, rm, x8, kw["w_gate"], FE, H, E, KU, ws=kw["ws_gate"], x_scales=xs,
+                        fused=True, act="swiglu_oai")
+    ec, es = ops.quant_mxfp8(a, tile_info=ti)
+    c, s = ops.moe_grouped_mxfp8(wfmt, ti, rm, x8, kw["w_gate"], FE, H, E, KU, ws=kw["ws_gate"], x_scales=xs,
+                                 fused=True, act="swiglu_oai")
+    torch.cuda.synchronize()
+    used = np.repeat(host(ti)[:, 0] >= 0, 64)
+    dead = used & (host(rm) < 0)
+    np.testing.assert_array_equal(host(c)[used], host(ec)[used])
+    np.testing.assert_array_equal(host(s)[used], host(es)[used])
+    assert np.all(host(c)[dead] == 0) and np.all(host(s)[dead] == 0)
+    assert np.any(host(c)[used & ~dead] != 0)

@@ -281,3 +281,53 @@ def test_row_bytes_table():
     assert of.row_bytes("mxfp4s", 2880) == 1440
     with pytest.raises(AssertionError):
         of.row_bytes("q4_k", 100)
+
+
+# --------------------------------------------------------------------------------------- MXFP4 MFMA-tiled planes
+def _split_planes(rng, rows, k):
+    nib = rng.integers(0, 256, (rows, k // 2), dtype=np.uint8)
+    sc = (127 + rng.integers(-8, 1, (rows, k // 32))).astype(np.uint8)
+    return nib, sc
+
+
+def test_mxfp4t_byte_addresses_follow_the_layout_definition():
+    """Every nibble byte and scale byte lands at the address the layout defines, computed here as a flat offset:
+    nibble byte j of row r -> ((r // 32 * C + j // 32) * 64 + 32 * ((j % 32) // 16) + r % 32) * 16 + j % 16;
+    scale of block b of row r -> ((r // 32 * C4 + b // 8) * 64 + 32 * (b % 2) + r % 32) * 4 + (b // 2) % 4."""
+    rng = np.random.default_rng(11)
+    rows, k = 64, 2880                        # C = 45 chunks: the last group of four holds one real chunk
+    C, C4 = k // 64, (k // 64 + 3) // 4
+    nib, sc = _split_planes(rng, rows, k)
+    nt, st = of.mxfp4s_to_tiled(nib, sc, rows, k)
+    assert nt.size == rows * k // 2 and st.size == rows // 32 * C4 * 256
+    r, j = np.meshgrid(np.arange(rows), np.arange(k // 2), indexing="ij")
+    off = ((r // 32 * C + j // 32) * 64 + 32 * ((j % 32) // 16) + r % 32) * 16 + j % 16
+    assert np.array_equal(nt[off], nib)
+    r, b = np.meshgrid(np.arange(rows), np.arange(k // 32), indexing="ij")
+    soff = ((r // 32 * C4 + b // 8) * 64 + 32 * (b % 2) + r % 32) * 4 + (b // 2) % 4
+    assert np.array_equal(st[soff], sc)
+    used = np.zeros(st.size, bool)
+    used[soff.ravel()] = True
+    assert np.all(st[~used] == 0)             # chunks past K carry scale 0
+
+
+def test_mxfp4t_round_trip_and_values():
+    rng = np.random.default_rng(12)
+    for rows, k in ((32, 64), (96, 2880), (64, 768)):
+        nib, sc = _split_planes(rng, rows, k)
+        nt, st = of.mxfp4s_to_tiled(nib, sc, rows, k)
+        n2, s2 = of.mxfp4t_to_split(nt, st, rows, k)
+        assert np.array_equal(n2, nib) and np.array_equal(s2, sc)
+        want = of.dequant_mxfp4s(nib, sc, rows, k)
+        got = of.dequant_mxfp4t(nt, st, rows, k)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_mxfp4t_lane_half_swap_negative_control():
+    """Swapping the two lane halves of every tile (K values 0..31 <-> 32..63 of each chunk) must change the values."""
+    rng = np.random.default_rng(13)
+    rows, k = 32, 256
+    nib, sc = _split_planes(rng, rows, k)
+    nt, st = of.mxfp4s_to_tiled(nib, sc, rows, k)
+    bad = nt.reshape(-1, 2, 32, 16)[:, ::-1].reshape(-1)
+    assert not np.array_equal(of.dequant_mxfp4t(bad, st, rows, k), of.dequant_mxfp4s(nib, sc, rows, k))
