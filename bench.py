@@ -7,7 +7,9 @@ A step is one launch of the hot path over one batch of synthetic input:
 
     q4_k_gemv_q8  (default) Q4_K decode GEMV, W [12288, 4096] (Qwen3-8B FFN gate/up), x bf16 [M, 4096], y f32, on
                 the int8-activation path the reference takes by default: the bf16 rows are quantized to Q8_1 inside
-                the kernel and multiplied with exact int32 group dot products
+                the kernel and multiplied with exact int32 group dot products; the weights are repacked once (before
+                timing) into the lane-ordered tiled layout (qmm_tile_q4k), a byte permutation of the GGUF blocks
+    q4_k_gemv_q8_gguf the same GEMV reading the GGUF Q4_K blocks as they are
     q4_k_gemv   the same GEMV on the f16-activation path (x staged as f16, v_dot2_f32_f16)
     q4_k_gemv_q8p the int8-activation GEMV on its reference boundary: x is the planar Q8_1 buffer qmm_quant_q8 makes
                 (once per layer input, shared by the matvecs that read it), quantized before the timed region
@@ -74,9 +76,10 @@ class GemvWorkload:
     """Decode GEMV y = x W^T over rotated weight copies; one step = one qmm_mv launch."""
     metric, unit, bound = METRIC, "GB/s", "hbm"
 
-    def __init__(self, name, index, fmt, n, k, m, x_dtype, traffic_name, q8=False):
+    def __init__(self, name, index, fmt, n, k, m, x_dtype, traffic_name, q8=False, tiled=False):
         self.name, self.index, self.fmt, self.n, self.k, self.m = name, index, fmt, n, k, m
-        self.x_dtype, self.traffic_name, self.q8 = x_dtype, traffic_name, q8
+        self.x_dtype, self.traffic_name, self.q8, self.tiled = x_dtype, traffic_name, q8, tiled
+        self.kfmt = "q4_kt" if tiled else fmt   # the weights the kernel reads (tiled: repacked once at load)
 
     def setup(self, dev):
         import torch
@@ -90,6 +93,8 @@ class GemvWorkload:
             self.x_host = d["x"]
             x = torch.from_numpy(d["x"]).to(dev)
         w0 = torch.from_numpy(self.raw).to(dev)
+        if self.tiled:   # one-time weight preparation: GGUF Q4_K blocks -> the lane-ordered tiled layout
+            w0 = ops.tile_q4k(w0, self.n, self.k)
         self.wbytes = w0.numel()
         copies = max(2, -(-ROTATE_BYTES // self.wbytes))
         self.ws = [w0] + [w0.clone() for _ in range(copies - 1)]
@@ -102,9 +107,9 @@ class GemvWorkload:
 
     def step(self, i):
         if self.q8 == "planar":
-            self.ops.mv_q8(self.fmt, self.ws[i % self.copies], self.xq, self.n, self.k, tokens=self.m, y=self.y)
+            self.ops.mv_q8(self.kfmt, self.ws[i % self.copies], self.xq, self.n, self.k, tokens=self.m, y=self.y)
         elif self.q8:
-            self.ops.mv_q8(self.fmt, self.ws[i % self.copies], self.x, self.n, self.k, y=self.y)
+            self.ops.mv_q8(self.kfmt, self.ws[i % self.copies], self.x, self.n, self.k, y=self.y)
         else:
             self.ops.mv(self.fmt, self.ws[i % self.copies], self.x, self.n, self.k, y=self.y)
 
@@ -138,7 +143,8 @@ class GemvWorkload:
                           f"in 256-row chunks + f32 matmul on {threads} threads, median {sec * 1e3:.1f} ms per GEMV"}
 
     def config(self):
-        return {"workload": self.name, "format": self.fmt, "N": self.n, "K": self.k, "M": self.m,
+        return {"workload": self.name, "format": self.fmt, "layout": "tiled (q4_kt)" if self.tiled else "gguf",
+                "N": self.n, "K": self.k, "M": self.m,
                 "x_dtype": "q8_1 planar" if self.q8 == "planar" else self.x_dtype,
                 "activations": "q8_1" if self.q8 else self.x_dtype, "y_dtype": "f32",
                 "weight_copies_rotated": self.copies,
@@ -401,12 +407,17 @@ def _q4k_gemv(m):
 
 def _q4k_gemv_q8(m):
     return GemvWorkload("q4_k_gemv_q8", 1, "q4_k", 12288, 4096, m or 1, "bf16",
-                        f"mv_q4k_q8s_kernel.q4_k_gemv_q8_n12288_k4096_m{m or 1}", q8=True)
+                        f"mv_q4kt_q8_kernel.q4_k_gemv_q8_n12288_k4096_m{m or 1}", q8=True, tiled=True)
+
+
+def _q4k_gemv_q8_gguf(m):
+    return GemvWorkload("q4_k_gemv_q8_gguf", 1, "q4_k", 12288, 4096, m or 1, "bf16",
+                        f"mv_q4k_q8s_kernel.q4_k_gemv_q8_gguf_n12288_k4096_m{m or 1}", q8=True)
 
 
 def _q4k_gemv_q8p(m):
     return GemvWorkload("q4_k_gemv_q8p", 1, "q4_k", 12288, 4096, m or 1, "bf16",
-                        f"mv_q4k_q8s_kernel.q4_k_gemv_q8p_n12288_k4096_m{m or 1}", q8="planar")
+                        f"mv_q4kt_q8_kernel.q4_k_gemv_q8p_n12288_k4096_m{m or 1}", q8="planar", tiled=True)
 
 
 def _q40_gemv(m):
@@ -414,7 +425,8 @@ def _q40_gemv(m):
                         f"mv_kernel_q4_0.q4_0_gemv_n4096_k4096_m{m or 1}")
 
 
-WORKLOADS = {"q4_k_gemv": _q4k_gemv, "q4_k_gemv_q8": _q4k_gemv_q8, "q4_k_gemv_q8p": _q4k_gemv_q8p, "q4_0_gemv": _q40_gemv, "q4_k_gemm": GemmWorkload,
+WORKLOADS = {"q4_k_gemv": _q4k_gemv, "q4_k_gemv_q8": _q4k_gemv_q8, "q4_k_gemv_q8_gguf": _q4k_gemv_q8_gguf,
+             "q4_k_gemv_q8p": _q4k_gemv_q8p, "q4_0_gemv": _q40_gemv, "q4_k_gemm": GemmWorkload,
              "mxfp4_moe": lambda m: MoeWorkload("mxfp4_moe", 3, m), "q4_k_moe": lambda m: MoeWorkload("q4_k_moe", 4, m),
              "hbm_copy": CopyWorkload}
 

@@ -37,8 +37,9 @@ enum qmm_status {
   QMM_ERR_WORKSPACE = -8  /* workspace too small */
 };
 
-/* QMM_MXFP4T: MXFP4 in MFMA-tiled planes (qmm_tile_mxfp4), the grouped GEMM's fast weight layout. */
-enum qmm_format { QMM_Q4_0 = 0, QMM_Q4_K = 1, QMM_MXFP4 = 2, QMM_MXFP4S = 3, QMM_MXFP4T = 4 };
+/* QMM_MXFP4T: MXFP4 in MFMA-tiled planes (qmm_tile_mxfp4), the grouped GEMM's fast weight layout.
+ * QMM_Q4_KT: Q4_K in the lane-ordered tiled layout (qmm_tile_q4k), the int8-activation decode GEMV's fast layout. */
+enum qmm_format { QMM_Q4_0 = 0, QMM_Q4_K = 1, QMM_MXFP4 = 2, QMM_MXFP4S = 3, QMM_MXFP4T = 4, QMM_Q4_KT = 5 };
 enum qmm_dtype {
   QMM_F32 = 0,
   QMM_F16 = 1,
@@ -61,7 +62,7 @@ int64_t qmm_row_bytes(int fmt, int64_t k);
  * (the values @g_q4_0_values S/quant_values.loom:386-408, @g_q4_k_values S/gen_llm.py:288-326,
  *  @g_mxfp4_values S/gen_llm.py:786-841 and @g_mxfp4s_values S/gen_llm.py:844-895 produce).
  * w: weight bytes; ws: the E8M0 scale plane for QMM_MXFP4S / QMM_MXFP4T, else NULL (QMM_MXFP4T: rows % 32 == 0,
- * K % 64 == 0). */
+ * K % 64 == 0; QMM_Q4_KT: rows % 16 == 0, K % 512 == 0). */
 int qmm_dequant(int fmt, const void *w, const void *ws, int64_t rows, int64_t k, float *out, qmm_stream_t stream);
 
 /* Decode matrix-vector product, the g_mv_{fmt}_k{K}[_t{TG}][_r{R}] family
@@ -85,7 +86,10 @@ int qmm_quant_q8(int64_t rows, int64_t k, const void *x, int x_dtype, void *xq, 
  * (d da) di with codes q - 8, summed in f32. fmt QMM_Q4_K (k % 256 == 0) or QMM_Q4_0 (k % 64 == 0). x: the planar
  * buffer of qmm_quant_q8 (x_dtype QMM_Q8) for tokens rows, or -- Q4_K with k = 4096 or 8192 only -- f32 / bf16
  * [tokens, k] rows, quantized inside the kernel exactly as qmm_quant_q8 does (same result bit for bit). y: f32
- * [tokens, n]. A multi-token call equals one-token calls bit for bit. */
+ * [tokens, n]. A multi-token call equals one-token calls bit for bit.
+ * fmt QMM_Q4_KT: the weights in the tiled layout of qmm_tile_q4k (n % 16 == 0, K % 512 == 0, K / 512 a multiple of
+ * at most 4 of a count of at most 8 waves); x planar Q8_1 or f32 / bf16 rows for every such K. For K = 4096 the
+ * results equal the QMM_Q4_K call's bit for bit. */
 int qmm_mv_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
               const void *w, float *y, qmm_stream_t stream);
 
@@ -188,6 +192,14 @@ int qmm_quant_mxfp8(int64_t rows, int64_t k, const void *x, int x_dtype, const i
  * S/formats.py:12-15): nibbles u8 [rows, k/2] (byte j = elements 2j low nibble, 2j+1 high nibble) and
  * E8M0 scales u8 [rows, k/32]. Bit-exact: every code and exponent is kept. */
 int qmm_repack_mxfp4(const void *w, int64_t rows, int64_t k, uint8_t *nibbles, uint8_t *scales, qmm_stream_t stream);
+
+/* One-time weight preparation for the int8-activation decode GEMV (no reference counterpart: the reference reads the
+ * GGUF blocks as they are): GGUF Q4_K rows [rows, k] -> the tiled layout QMM_Q4_KT. Units of 16 rows x 512 values
+ * (two super-blocks a row), ordered (row block, slice), 4608 bytes each: the 32 16-byte headers ([f16 d][f16 dmin]
+ * [12 scale bytes]) of super-block sb of row r at 16 (2 r + sb), then four 1 KB code planes, plane q holding at
+ * 16 l (l = 4 r + 2 sb + h) code bytes 16 (4 h + q) .. +15 of that super-block. A byte permutation (same size);
+ * qmm_dequant(QMM_Q4_KT) gives the GGUF values bit for bit. rows % 16 == 0, k % 512 == 0. */
+int qmm_tile_q4k(const void *w, int64_t rows, int64_t k, void *w_t, qmm_stream_t stream);
 
 /* One-time weight preparation for the grouped GEMM (no reference counterpart: the reference reads the split planes
  * of S/formats.py:12-15 as they are): split planes (nibbles [rows, k/2], scales [rows, k/32]) -> MFMA-tiled planes.

@@ -88,6 +88,7 @@ inline int64_t block_values(int fmt) {
     case QMM_MXFP4: return 32;
     case QMM_MXFP4S: return 32;
     case QMM_MXFP4T: return 32;
+    case QMM_Q4_KT: return 256;
     default: return 0;
   }
 }
@@ -98,6 +99,7 @@ inline int64_t block_bytes(int fmt) {
     case QMM_MXFP4: return 17;
     case QMM_MXFP4S: return 16;
     case QMM_MXFP4T: return 16;
+    case QMM_Q4_KT: return 144;
     default: return 0;
   }
 }

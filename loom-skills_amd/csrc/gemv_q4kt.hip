@@ -1,0 +1,383 @@
+// The Q4_K decode matvec on Q8_1 activations over the tiled weight layout (qmm_tile_q4k), and that layout's
+// repack and dequant kernels.
+//
+// Tiled layout: units of 16 rows x 512 values (two super-blocks a row), ordered (row block, slice), 4608 bytes
+// each. A unit holds the 32 16-byte headers ([f16 d][f16 dmin][12 scale bytes]) of super-block sb of row r at
+// 16 (2 r + sb), then four 1 KB code planes: plane q holds at 16 l, l = 4 r + 2 sb + h, code bytes
+// 16 (4 h + q) .. 16 (4 h + q) + 15 of that super-block. Lane l of a wave is exactly the lane that multiplies
+// half h of super-block sb of row r, so the wave's five loads per unit (a header, four code planes) are each one
+// contiguous run of bytes, where the GGUF layout spreads every load instruction over 16 rows 2304 bytes apart
+// (measured on MI355X for a 28.3 MB matrix: 6.14 us to read the GGUF pattern, 5.67 us the tiled one).
+//
+// Matvec (the g_mv_q4_k_k{K}_q8 family, S/gen_llm.py:1288-1301, iq_dot :1024-1071): a workgroup owns one row block
+// (16 rows); its NW waves split K, wave w taking slices U w .. U w + U - 1 (K = 512 U NW). Each wave quantizes its
+// own activation slices to Q8_1 in LDS (or copies planar Q8_1 codes), exactly as qmm_quant_q8 does, and each lane
+// then adds, per 32-value group of its half super-block, (di d sc - xs dmin m) da with di the exact int32 dot of
+// codes. The row's four lanes meet in a butterfly, the waves in LDS in a fixed order; for K = 4096 the arithmetic
+// and its order are those of the GGUF-layout kernel, so both give the same bits.
+#include <type_traits>
+
+#include "bfly.hpp"
+
+using namespace qmm;
+
+namespace {
+
+typedef __attribute__((ext_vector_type(4))) u32 v4u;
+typedef __attribute__((ext_vector_type(2))) u32 v2u;
+
+constexpr int kUnit = 4608, kMaxWaves = 8;
+
+__device__ __forceinline__ int sdot4(u32 a, u32 b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// 8 activations of the lane as f32: from 16 bytes of bf16 or 32 bytes of f32 at element offset e
+__device__ __forceinline__ void load8(const void *x, bool bf, int64_t e, float (&v)[8]) {
+  if (bf) {
+    const v4u q = *reinterpret_cast<const v4u *>(static_cast<const u16 *>(x) + e);
+    const u32 d[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { v[2 * j] = bf16_to_f32(d[j] & 0xFFFFu); v[2 * j + 1] = bf16_to_f32(d[j] >> 16); }
+  } else {
+    const v4u a = *reinterpret_cast<const v4u *>(static_cast<const float *>(x) + e);
+    const v4u b = *reinterpret_cast<const v4u *>(static_cast<const float *>(x) + e + 4);
+    const u32 d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = u32_as_f32(d[j]);
+  }
+}
+
+// Q8_1 of one 32-value group held by four consecutive lanes (8 values each): the lane's codes as two dwords, the
+// group's f16-rounded d and code sum (llama.cpp quantize_q8_1; the arithmetic of qmm_quant_q8)
+__device__ __forceinline__ void q8_group(const float (&v)[8], u32 &c0, u32 &c1, float &d16, float &sum) {
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  const float d = amax / 127.f;
+  int s = 0;
+  u32 c[2] = {0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float t = d > 0.f ? v[i] / d : 0.f;
+    const int q = (int)copysignf(floorf(fabsf(t) + 0.5f), t);
+    s += q;
+    c[i >> 2] |= ((u32)q & 0xFFu) << (8 * (i & 3));
+  }
+  s += __shfl_xor(s, 1, 64);
+  s += __shfl_xor(s, 2, 64);
+  c0 = c[0];
+  c1 = c[1];
+  d16 = (float)(_Float16)d;
+  sum = (float)s;
+}
+
+template <int TG, int U, bool STAGEQ>
+__global__ __launch_bounds__(kMaxWaves * 64) void mv_q4kt_q8_kernel(int64_t n, int64_t tokens, int64_t K,
+                                                                   int accumulate, const void *__restrict__ x, int bf,
+                                                                   const u8 *__restrict__ w, float *__restrict__ y) {
+  constexpr int SLICE = 512 * U, NG = SLICE / 32;   // values / Q8 groups of a wave
+  __shared__ __align__(16) u32 xc[kMaxWaves][TG][SLICE / 4];
+  __shared__ __align__(16) float xm[kMaxWaves][TG][NG][2];
+  __shared__ float red[kMaxWaves][16][TG];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NW = (int)(blockDim.x >> 6);
+  const int64_t t0 = (int64_t)blockIdx.y * TG;
+  const int64_t rb = blockIdx.x;                    // row block: rows 16 rb .. 16 rb + 15
+  const int r = lane >> 2, sb = (lane >> 1) & 1, h = lane & 1;
+  const int64_t k0 = (int64_t)wave * SLICE;         // the wave's first value
+
+  // ---- the wave's activations first, then its weights: U units (a header and four code planes each) through two
+  //      register slots, units 0 and 1 now and unit u + 2 once unit u is consumed
+  float xv[TG][U][8];
+  v2u qv[TG][U];
+  float2 mv[TG];
+#pragma unroll
+  for (int t = 0; t < TG; ++t) {
+    const int64_t tok = t0 + t < tokens ? t0 + t : tokens - 1;
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const int c = lane + 64 * j;                 // 8-value chunk of the wave's values
+      if constexpr (STAGEQ) load8(x, bf, tok * K + k0 + 8 * c, xv[t][j]);
+      else qv[t][j] = *reinterpret_cast<const v2u *>(static_cast<const u8 *>(x) + tok * K + k0 + 8 * c);
+    }
+    if constexpr (!STAGEQ) {
+      const float2 *meta = reinterpret_cast<const float2 *>(static_cast<const u8 *>(x) + tokens * K);
+      mv[t] = meta[tok * (K / 32) + k0 / 32 + (lane < NG ? lane : 0)];
+    }
+  }
+  constexpr int NSLOT = U == 1 ? 1 : 2;
+  v4u wd[NSLOT][5];
+  auto load_unit = [&](int slot, int u) __attribute__((always_inline)) {
+    const v4u *up = reinterpret_cast<const v4u *>(w + (rb * (K / 512) + (int64_t)wave * U + u) * kUnit);
+    wd[slot][0] = up[lane >> 1];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) wd[slot][1 + q] = up[32 + 64 * q + lane];
+  };
+#pragma unroll
+  for (int u = 0; u < NSLOT; ++u) load_unit(u, u);
+
+  // ---- the wave's slices: codes and group pairs into its own LDS area
+#pragma unroll
+  for (int t = 0; t < TG; ++t) {
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const int c = lane + 64 * j;
+      if constexpr (STAGEQ) {
+        u32 c0, c1;
+        float d16, sum;
+        q8_group(xv[t][j], c0, c1, d16, sum);
+        xc[wave][t][2 * c] = c0;
+        xc[wave][t][2 * c + 1] = c1;
+        if ((c & 3) == 0) { xm[wave][t][c >> 2][0] = d16; xm[wave][t][c >> 2][1] = sum; }
+      } else {
+        xc[wave][t][2 * c] = qv[t][j].x;
+        xc[wave][t][2 * c + 1] = qv[t][j].y;
+      }
+    }
+    if constexpr (!STAGEQ) {
+      if (lane < NG) { xm[wave][t][lane][0] = mv[t].x; xm[wave][t][lane][1] = mv[t].y; }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // a token's activation fragment of the lane's 4 groups of unit u (16 u + 8 sb + 4 h + 0..3): codes (8 dwords a
+  // group) and (d, code sum) pairs, from LDS
+  auto frag = [&](int t, int u, u32 (&xa)[4][8], float (&md)[4], float (&ms)[4]) __attribute__((always_inline)) {
+    const int g0 = 16 * u + 8 * sb + 4 * h;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const v4u p0 = *reinterpret_cast<const v4u *>(&xc[wave][t][8 * (g0 + g)]);
+      const v4u p1 = *reinterpret_cast<const v4u *>(&xc[wave][t][8 * (g0 + g) + 4]);
+      xa[g][0] = p0.x; xa[g][1] = p0.y; xa[g][2] = p0.z; xa[g][3] = p0.w;
+      xa[g][4] = p1.x; xa[g][5] = p1.y; xa[g][6] = p1.z; xa[g][7] = p1.w;
+      md[g] = xm[wave][t][g0 + g][0];
+      ms[g] = xm[wave][t][g0 + g][1];
+    }
+  };
+  // Up to two tokens every fragment a unit needs is read at once (for the first unit before the weights are
+  // awaited); beyond two tokens one token's at a time inside the token loop, so the registers do not grow with the
+  // token count.
+  constexpr bool kHoist = TG <= 2;
+  constexpr int TH = kHoist ? TG : 1;
+  u32 xah[TH][4][8];
+  float mdh[TH][4], msh[TH][4];
+  float part[TG];
+
+  // the math of unit u held in slot `slot`: adds the lane's partial sums of its half super-block into part[]
+  auto unit_math = [&](int u, auto slotc, bool first) __attribute__((always_inline)) {
+    constexpr int slot = decltype(slotc)::value;
+    if constexpr (kHoist) {
+#pragma unroll
+      for (int t = 0; t < TG; ++t) frag(t, u, xah[t], mdh[t], msh[t]);
+      if (first) {
+#pragma unroll
+        for (int t = 0; t < TG; ++t)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+#pragma unroll
+            for (int i2 = 0; i2 < 8; ++i2) asm volatile("" ::"v"(xah[t][g][i2]));
+            asm volatile("" ::"v"(mdh[t][g]), "v"(msh[t][g]));
+          }
+      }
+    }
+    const v4u hd = wd[slot][0];
+    const float d = f16_to_f32(hd.x), dmin = f16_to_f32(hd.x >> 16);
+    const u32 q[16] = {wd[slot][1].x, wd[slot][1].y, wd[slot][1].z, wd[slot][1].w, wd[slot][2].x, wd[slot][2].y,
+                       wd[slot][2].z, wd[slot][2].w, wd[slot][3].x, wd[slot][3].y, wd[slot][3].z, wd[slot][3].w,
+                       wd[slot][4].x, wd[slot][4].y, wd[slot][4].z, wd[slot][4].w};
+    if constexpr (U > 1) {
+      if (u + 2 < U) load_unit(slot, u + 2);
+    }
+    u32 lo[16], hi[16];   // the code nibbles as int8 lanes, shared by every token
+#pragma unroll
+    for (int i2 = 0; i2 < 16; ++i2) { lo[i2] = q[i2] & 0x0F0F0F0Fu; hi[i2] = (q[i2] >> 4) & 0x0F0F0F0Fu; }
+    float sc[4], mn[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      u32 s_, m_;
+      q4k_scale_min(hd.y, hd.z, hd.w, 4 * h + g, s_, m_);
+      sc[g] = d * (float)s_;
+      mn[g] = dmin * (float)m_;
+    }
+    auto token = [&](int t, const u32 (&xa)[4][8], const float (&md)[4], const float (&ms)[4])
+        __attribute__((always_inline)) {
+      float p = 0.f;
+#pragma unroll
+      for (int pg = 0; pg < 2; ++pg) {   // code pages 2 h and 2 h + 1: low nibbles group 2 pg, high 2 pg + 1
+        int ia = 0, ib = 0;
+#pragma unroll
+        for (int i2 = 0; i2 < 8; ++i2) {
+          ia = sdot4(lo[8 * pg + i2], xa[2 * pg][i2], ia);
+          ib = sdot4(hi[8 * pg + i2], xa[2 * pg + 1][i2], ib);
+        }
+        p += ((float)ia * sc[2 * pg] - ms[2 * pg] * mn[2 * pg]) * md[2 * pg];
+        p += ((float)ib * sc[2 * pg + 1] - ms[2 * pg + 1] * mn[2 * pg + 1]) * md[2 * pg + 1];
+      }
+      part[t] = u == 0 ? p : part[t] + p;
+    };
+    if constexpr (kHoist) {
+#pragma unroll
+      for (int t = 0; t < TG; ++t) token(t, xah[t], mdh[t], msh[t]);
+    } else {
+#pragma unroll
+      for (int t = 0; t < TG; ++t) {
+        u32 xa[4][8];
+        float md[4], ms[4];
+        frag(t, u, xa, md, ms);
+        token(t, xa, md, ms);
+      }
+    }
+  };
+  if constexpr (U == 1) {
+    unit_math(0, std::integral_constant<int, 0>{}, true);
+  } else {
+    // units in pairs (slots 0 and 1 as constants); the pair loop is not unrolled, so only one pair's fragments
+    // are live at a time
+#pragma unroll 1
+    for (int u = 0; u < U; u += 2) {
+      unit_math(u, std::integral_constant<int, 0>{}, u == 0);
+      if (u + 1 < U) unit_math(u + 1, std::integral_constant<int, 1>{}, false);
+    }
+  }
+  // the row's four lanes of this wave (its two super-blocks' halves) meet in a butterfly, then the waves in LDS
+#pragma unroll
+  for (int t = 0; t < TG; ++t) {
+    float p = part[t];
+    p += xshfl<1>(p);
+    p += xshfl<2>(p);
+    part[t] = p;
+  }
+  if ((lane & 3) == 0) {
+#pragma unroll
+    for (int t = 0; t < TG; ++t) red[wave][r][t] = part[t];
+  }
+  __syncthreads();
+  if (tid < 16 * TG) {
+    const int rr = tid / TG, t = tid % TG;
+    float tot = 0.f;
+    for (int wv = 0; wv < NW; ++wv) tot += red[wv][rr][t];
+    const int64_t row = 16 * rb + rr, tok = t0 + t;
+    if (tok < tokens) {
+      float *py = y + tok * n + row;
+      *py = accumulate ? *py + tot : tot;
+    }
+  }
+}
+
+template <int TG, int U, bool STAGEQ>
+int launch_tg(int64_t n, int64_t tokens, int64_t k, int accumulate, const void *x, int bf, const void *w, float *y,
+              int nw, hipStream_t s) {
+  const dim3 grid((unsigned)(n / 16), (unsigned)((tokens + TG - 1) / TG));
+  mv_q4kt_q8_kernel<TG, U, STAGEQ><<<grid, nw * 64, 0, s>>>(n, tokens, k, accumulate, x, bf,
+                                                           static_cast<const u8 *>(w), y);
+  return launch_status();
+}
+
+template <int U, bool STAGEQ>
+int launch_u(int64_t n, int64_t tokens, int64_t k, int accumulate, const void *x, int bf, const void *w, float *y,
+             int nw, hipStream_t s) {
+  // up to 8 tokens a workgroup share its weight loads (the activations of a token stage U x 8 registers a lane,
+  // so the token group shrinks as the slices a wave grow: 8, 4, 2, 1 for U = 1..4); the group is the smallest
+  // power of two holding every token, a workgroup's spare slots repeating its last token without storing it
+  constexpr int TGMAX = U == 1 ? 8 : U == 2 ? 4 : U == 3 ? 2 : 1;
+  constexpr int T8 = TGMAX >= 8 ? 8 : 1, T4 = TGMAX >= 4 ? 4 : 1, T2 = TGMAX >= 2 ? 2 : 1;
+  if (tokens >= 5 && T8 == 8) return launch_tg<T8, U, STAGEQ>(n, tokens, k, accumulate, x, bf, w, y, nw, s);
+  if (tokens >= 3 && T4 == 4) return launch_tg<T4, U, STAGEQ>(n, tokens, k, accumulate, x, bf, w, y, nw, s);
+  if (tokens >= 2 && T2 == 2) return launch_tg<T2, U, STAGEQ>(n, tokens, k, accumulate, x, bf, w, y, nw, s);
+  return launch_tg<1, U, STAGEQ>(n, tokens, k, accumulate, x, bf, w, y, nw, s);
+}
+
+// One thread per 16-byte piece of the tiled matrix: pieces 0..31 of a unit are the headers of (row p / 2,
+// super-block p % 2), the others the code planes (see the layout above).
+__global__ void tile_q4k_kernel(const u8 *__restrict__ src, int64_t rows, int64_t K, u8 *__restrict__ dst) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t S = K / 512, units = rows / 16 * S;
+  if (i >= units * (kUnit / 16)) return;
+  const int64_t unit = i / (kUnit / 16);
+  const int p = (int)(i % (kUnit / 16));
+  const int64_t rb = unit / S, sl = unit % S;
+  int r, sb, off;
+  if (p < 32) {
+    r = p >> 1; sb = p & 1; off = 0;
+  } else {
+    const int q = (p - 32) >> 6, l = (p - 32) & 63;
+    r = l >> 2; sb = (l >> 1) & 1;
+    off = 16 + 16 * (4 * (l & 1) + q);
+  }
+  const u8 *blk = src + (16 * rb + r) * (K / 256 * 144) + (2 * sl + sb) * 144 + off;
+  *reinterpret_cast<v4u *>(dst + 16 * i) = *reinterpret_cast<const v4u *>(blk);
+}
+
+// f32 values of a tiled Q4_K matrix, one thread per 32-value sub-block, the value helper's arithmetic
+// (S/gen_llm.py:269-326): (f32(d) sc) q - f32(dmin) m.
+__global__ void dequant_q4kt_kernel(const u8 *__restrict__ w, int64_t rows, int64_t K, float *__restrict__ out) {
+  const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t G = K / 32;
+  if (gi >= rows * G) return;
+  const int64_t row = gi / G;
+  const int g = (int)(gi % G), b = g >> 3, s = g & 7;
+  const int i = (int)(row & 15), sb = b & 1;
+  const u8 *unit = w + ((row >> 4) * (K / 512) + (b >> 1)) * kUnit;
+  const u32 *hd = reinterpret_cast<const u32 *>(unit + 16 * (2 * i + sb));
+  u32 sc, mn;
+  q4k_scale_min(hd[1], hd[2], hd[3], s, sc, mn);
+  const float scale = f16_to_f32(hd[0]) * (float)sc;
+  const float minimum = f16_to_f32(hd[0] >> 16) * (float)mn;
+  const int shift = 4 * (s & 1);
+  float *o = out + gi * 32;
+#pragma unroll
+  for (int l = 0; l < 32; ++l) {
+    const int c = 32 * (s >> 1) + l;   // code byte of the super-block
+    const u8 v = unit[512 + 1024 * ((c >> 4) & 3) + 16 * (4 * i + 2 * sb + (c >> 6)) + (c & 15)];
+    o[l] = __fsub_rn(__fmul_rn(scale, (float)((v >> shift) & 15u)), minimum);
+  }
+}
+
+}  // namespace
+
+// The tiled-layout path of qmm_mv_q8 (fmt QMM_Q4_KT): rows % 16 == 0, K % 512 == 0, K = 512 U NW with U <= 4
+// slices a wave and NW <= 8 waves.
+int qmm_mv_q4kt_q8(int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype, const void *w,
+                   float *y, hipStream_t s) {
+  if (n % 16 || k % 512 || n / 16 > 2147483647ll || tokens > 65535) return QMM_ERR_SHAPE;   // grid.y <= 65535
+  const int64_t slices = k / 512;
+  int U = 1;
+  while (U <= 4 && (slices % U || slices / U > kMaxWaves)) ++U;
+  if (U > 4) return QMM_ERR_SHAPE;
+  const int nw = (int)(slices / U);
+  const bool stage = x_dtype != QMM_Q8;
+  const int bf = x_dtype == QMM_BF16;
+  switch (U) {
+    case 1: return stage ? launch_u<1, true>(n, tokens, k, accumulate, x, bf, w, y, nw, s)
+                         : launch_u<1, false>(n, tokens, k, accumulate, x, bf, w, y, nw, s);
+    case 2: return stage ? launch_u<2, true>(n, tokens, k, accumulate, x, bf, w, y, nw, s)
+                         : launch_u<2, false>(n, tokens, k, accumulate, x, bf, w, y, nw, s);
+    case 3: return stage ? launch_u<3, true>(n, tokens, k, accumulate, x, bf, w, y, nw, s)
+                         : launch_u<3, false>(n, tokens, k, accumulate, x, bf, w, y, nw, s);
+    default: return stage ? launch_u<4, true>(n, tokens, k, accumulate, x, bf, w, y, nw, s)
+                          : launch_u<4, false>(n, tokens, k, accumulate, x, bf, w, y, nw, s);
+  }
+}
+
+int qmm_dequant_q4kt(const void *w, int64_t rows, int64_t k, float *out, hipStream_t s) {
+  if (rows % 16 || k % 512) return QMM_ERR_SHAPE;
+  if (!aligned(w, 4)) return QMM_ERR_ALIGN;
+  const int64_t groups = rows * (k / 32);
+  dequant_q4kt_kernel<<<(unsigned)((groups + 255) / 256), 256, 0, s>>>(static_cast<const u8 *>(w), rows, k, out);
+  return launch_status();
+}
+
+extern "C" int qmm_tile_q4k(const void *w, int64_t rows, int64_t k, void *w_t, qmm_stream_t stream) {
+  if (!w || !w_t) return QMM_ERR_NULL;
+  if (rows <= 0 || rows % 16 || k <= 0 || k % 512 || k > (1 << 20)) return QMM_ERR_SHAPE;
+  if (!aligned(w, 16) || !aligned(w_t, 16)) return QMM_ERR_ALIGN;
+  const int64_t pieces = rows / 16 * (k / 512) * (kUnit / 16);
+  tile_q4k_kernel<<<(unsigned)((pieces + 255) / 256), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      static_cast<const u8 *>(w), rows, k, static_cast<u8 *>(w_t));
+  return launch_status();
+}

@@ -422,10 +422,13 @@ extern "C" int qmm_quant_q8(int64_t rows, int64_t k, const void *x, int x_dtype,
   return launch_status();
 }
 
+int qmm_mv_q4kt_q8(int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype, const void *w,
+                   float *y, hipStream_t s);
+
 extern "C" int qmm_mv_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
                          const void *w, float *y, qmm_stream_t stream) {
   if (!x || !w || !y) return QMM_ERR_NULL;
-  if (fmt != QMM_Q4_K && fmt != QMM_Q4_0) return QMM_ERR_FORMAT;
+  if (fmt != QMM_Q4_K && fmt != QMM_Q4_0 && fmt != QMM_Q4_KT) return QMM_ERR_FORMAT;
   if (x_dtype != QMM_Q8 && x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
   if (k <= 0 || n <= 0 || tokens <= 0 || n > (1ll << 30) || tokens > (1ll << 24) || k > (1ll << 20))
     return QMM_ERR_SHAPE;
@@ -433,6 +436,7 @@ extern "C" int qmm_mv_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accu
   if (fmt == QMM_Q4_0 && k % 64) return QMM_ERR_SHAPE;
   if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 4)) return QMM_ERR_ALIGN;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (fmt == QMM_Q4_KT) return qmm_mv_q4kt_q8(k, n, tokens, accumulate, x, x_dtype, w, y, s);
   const bool fast = fmt == QMM_Q4_K && (k == 4096 || k == 8192) && tokens <= 65535ll * 2;
   if (x_dtype != QMM_Q8) {
     // f32 / bf16 rows are quantized while staged; only the fast path stages (others take planar Q8 from

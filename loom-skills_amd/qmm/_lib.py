@@ -32,6 +32,7 @@ SIGNATURES = {
     "qmm_quant_mxfp8": [c_i64, c_i64, c_vp, c_int, c_vp, c_vp, c_vp, c_vp],
     "qmm_repack_mxfp4": [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp],
     "qmm_tile_mxfp4": [c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp],
+    "qmm_tile_q4k": [c_vp, c_i64, c_i64, c_vp, c_vp],
     "qmm_mxfp4t_scale_bytes": [c_i64, c_i64],
     "qmm_moe_combine": [c_i64, c_i64, c_i64, c_int, c_vp, c_vp, c_vp, c_int, c_vp, c_vp],
 }

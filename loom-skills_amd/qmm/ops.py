@@ -94,7 +94,8 @@ def quant_q8(x, xq=None):
 def mv_q8(fmt, w, x, n, k, tokens=None, y=None, accumulate=False):
     """The int8-activation decode matvec (g_mv_{fmt}_k{K}[_t{TG}]_q8, S/gen_llm.py:1288-1301): x is the planar Q8_1
     buffer of `tokens` rows (uint8, from quant_q8), or f32 / bf16 rows [tokens, k], which the Q4_K K = 4096 / 8192
-    kernel quantizes itself and any other shape quantizes through quant_q8 first (identical results)."""
+    and (up to two tokens) tiled-layout q4_kt kernels quantize themselves and any other call quantizes through
+    quant_q8 first (identical results)."""
     _dev(w, x, y)
     if x.dtype == torch.uint8:
         if tokens is None:
@@ -104,7 +105,9 @@ def mv_q8(fmt, w, x, n, k, tokens=None, y=None, accumulate=False):
         tokens = x.shape[0]
         if x.shape[-1] != k:
             raise ValueError(f"x has {x.shape[-1]} columns, K is {k}")
-        if not (fmt == "q4_k" and k in (4096, 8192)):
+        # the kernels that quantize f32 / bf16 rows themselves do so in every workgroup; from three tokens on a
+        # separate quant_q8 pass is cheaper for the tiled layout (same bits either way)
+        if not ((fmt == "q4_k" and k in (4096, 8192)) or (fmt == "q4_kt" and tokens <= 2)):
             x, xd = quant_q8(x), DTYPE["q8"]
         else:
             xd = _dt(x)
@@ -245,6 +248,15 @@ def repack_mxfp4(w, rows, k):
     sc = torch.empty((rows, k // 32), dtype=torch.uint8, device=w.device)
     _lib.call("qmm_repack_mxfp4", _ptr(w), rows, k, _ptr(nib), _ptr(sc), _stream())
     return nib, sc
+
+
+def tile_q4k(w, rows, k):
+    """GGUF Q4_K rows (uint8, rows * k / 256 * 144 bytes) -> the tiled layout (format "q4_kt") the int8-activation
+    decode GEMV streams contiguously. rows % 16 == 0, k % 512 == 0; a byte permutation of the same size."""
+    _dev(w)
+    w_t = torch.empty(rows * row_bytes("q4_k", k), dtype=torch.uint8, device=w.device)
+    _lib.call("qmm_tile_q4k", _ptr(w), rows, k, _ptr(w_t), _stream())
+    return w_t
 
 
 def tile_mxfp4(nib, sc, rows, k):

@@ -10,6 +10,8 @@ as the reference's decoders do, so any correct implementation reproduces them bi
 * MXFP4 split planes         S/gen_llm.py:844-895 (@g_mxfp4s_values), S/st_tensors.py:17-33 (dequant_mxfp4)
 * MXFP4 MFMA-tiled planes    this library's load-time layout of the split planes (no reference counterpart); a byte
                              permutation, so its values are the split planes' values
+* Q4_K tiled                 this library's load-time layout of GGUF Q4_K for the decode GEMV (lane-ordered units of
+                             16 rows x 512 values); a byte permutation of the GGUF blocks
 """
 import numpy as np
 
@@ -178,6 +180,48 @@ def dequant_mxfp4t(nib_t, sc_t, rows, k):
     return dequant_mxfp4s(nib, sc, rows, k)
 
 
+def q4_k_to_tiled(raw, rows, k):
+    """GGUF Q4_K rows -> the lane-ordered tiled layout of the decode GEMV, written from the layout's definition:
+    units of 16 rows x 512 values (two super-blocks a row), ordered (row block, slice), 4608 bytes each: the 32
+    16-byte headers ([f16 d][f16 dmin][12 scale bytes]) of super-block sb of row r at 16 (2 r + sb), then four
+    1 KB code planes, plane q holding at 16 l (l = 4 r + 2 sb + h) code bytes 16 (4 h + q) .. +16 of that super-block.
+    rows % 16 == 0, k % 512 == 0."""
+    assert rows % 16 == 0 and k % 512 == 0, (rows, k)
+    b = _blocks(raw, "q4_k").reshape(rows, k // 256, 144)
+    S = k // 512
+    out = np.empty(rows * k // 256 * 144, np.uint8)
+    for rb in range(rows // 16):
+        for sl in range(S):
+            u = (rb * S + sl) * 4608
+            for r in range(16):
+                for sb in range(2):
+                    blk = b[16 * rb + r, 2 * sl + sb]
+                    out[u + 16 * (2 * r + sb): u + 16 * (2 * r + sb) + 16] = blk[0:16]
+                    for h in range(2):
+                        lane = 4 * r + 2 * sb + h
+                        for q in range(4):
+                            o = u + 512 + 1024 * q + 16 * lane
+                            c = 16 + 16 * (4 * h + q)
+                            out[o: o + 16] = blk[c: c + 16]
+    return out
+
+
+def q4_kt_to_gguf(raw_t, rows, k):
+    """Inverse of q4_k_to_tiled (vectorized: an independent construction by index arithmetic)."""
+    S = k // 512
+    t = np.asarray(raw_t).view(np.uint8).reshape(rows // 16, S, 4608)
+    hdr = t[:, :, :512].reshape(rows // 16, S, 16, 2, 16)                   # [rb, sl, r, sb, 16]
+    codes = t[:, :, 512:].reshape(rows // 16, S, 4, 16, 2, 2, 16)           # [rb, sl, q, r, sb, h, 16]
+    codes = codes.transpose(0, 1, 3, 4, 5, 2, 6).reshape(rows // 16, S, 16, 2, 128)   # [rb, sl, r, sb, (h q 16)]
+    blk = np.concatenate([hdr, codes], axis=-1)                               # [rb, sl, r, sb, 144]
+    return np.ascontiguousarray(blk.transpose(0, 2, 1, 3, 4)).reshape(-1)    # rows in order, super-blocks in order
+
+
+def dequant_q4_kt(raw_t, rows, k):
+    """Q4_K in the tiled GEMV layout: the values of the GGUF blocks it permutes."""
+    return dequant_q4_k(q4_kt_to_gguf(raw_t, rows, k), rows, k)
+
+
 def dequantize(fmt, raw, rows, k, scales=None):
     if fmt == "q4_0":
         return dequant_q4_0(raw, rows, k)
@@ -189,4 +233,6 @@ def dequantize(fmt, raw, rows, k, scales=None):
         return dequant_mxfp4s(raw, scales, rows, k)
     if fmt == "mxfp4t":
         return dequant_mxfp4t(raw, scales, rows, k)
+    if fmt == "q4_kt":
+        return dequant_q4_kt(raw, rows, k)
     raise ValueError(fmt)

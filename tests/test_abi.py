@@ -70,6 +70,7 @@ def test_host_only_entry_points(lib):
     assert lib.qmm_row_bytes(2, 2880) == 1530
     assert lib.qmm_row_bytes(3, 2880) == 1440
     assert lib.qmm_row_bytes(4, 2880) == 1440          # MFMA-tiled planes: the split nibble plane's bytes
+    assert lib.qmm_row_bytes(5, 4096) == 2304          # tiled Q4_K: the GGUF row's bytes
     assert lib.qmm_mxfp4t_scale_bytes(64, 2880) == 2 * 12 * 256   # 45 chunks -> 12 groups of four
     assert lib.qmm_mxfp4t_scale_bytes(48, 2880) == 0 and lib.qmm_mxfp4t_scale_bytes(64, 2848) == 0
     assert lib.qmm_row_bytes(1, 100) == 0
@@ -113,6 +114,14 @@ def test_argument_validation_without_a_device(lib):
     assert lib.qmm_repack_mxfp4(fake, 4, 48, fake, fake, n) == st["QMM_ERR_SHAPE"]
     # MFMA-tiled planes: whole 32-row blocks and 64-value chunks; no GEMV or decode matvec reads them
     assert lib.qmm_tile_mxfp4(fake, fake, 48, 64, fake, fake, n) == st["QMM_ERR_SHAPE"]
+    # tiled Q4_K: whole 16-row blocks and 512-value slices; at most 4 slices a wave of at most 8 waves
+    assert lib.qmm_tile_q4k(fake, 24, 512, fake, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_tile_q4k(fake, 16, 768, fake, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_tile_q4k(fake, 16, 512, n, n) == st["QMM_ERR_NULL"]
+    assert lib.qmm_mv_q8(5, 4096, 24, 1, 0, fake, 2, fake, fake, n) == st["QMM_ERR_SHAPE"]     # n % 16
+    assert lib.qmm_mv_q8(5, 768, 16, 1, 0, fake, 2, fake, fake, n) == st["QMM_ERR_SHAPE"]      # K % 512
+    assert lib.qmm_mv_q8(5, 512 * 37, 16, 1, 0, fake, 2, fake, fake, n) == st["QMM_ERR_SHAPE"]  # 37 slices
+    assert lib.qmm_dequant(5, fake, n, 16, 768, fake, n) == st["QMM_ERR_SHAPE"]
     assert lib.qmm_tile_mxfp4(fake, fake, 32, 96, fake, fake, n) == st["QMM_ERR_SHAPE"]
     assert lib.qmm_tile_mxfp4(fake, n, 32, 64, fake, fake, n) == st["QMM_ERR_NULL"]
     assert lib.qmm_dequant(4, fake, fake, 48, 64, fake, n) == st["QMM_ERR_SHAPE"]

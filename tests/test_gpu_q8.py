@@ -138,3 +138,85 @@ def test_mv_q8_rejects_bad_arguments(dev):
     assert lib.qmm_mv_q8(1, 300, 1, 1, 0, x.data_ptr(), 4, w.data_ptr(), y.data_ptr(), s) == -2    # K % 256
     assert lib.qmm_quant_q8(1, 40, x.data_ptr(), 2, w.data_ptr(), s) == -2                          # K % 32
     torch.cuda.synchronize()
+
+
+# ------------------------------------------------------------------------------ Q4_K in the tiled GEMV layout
+def test_tile_q4k_bit_exact(dev):
+    """qmm_tile_q4k against the oracle's element-by-element construction; qmm_dequant of the tiled bytes against
+    the GGUF values."""
+    import torch
+    ops = _ops()
+    rng = np.random.default_rng(61)
+    for n, k in ((32, 4096), (48, 1536)):
+        w = _weights("q4_k", rng, n, k)
+        wt = ops.tile_q4k(dev_u8(w, dev), n, k)
+        np.testing.assert_array_equal(host(wt), of.q4_k_to_tiled(w, n, k))
+        got = host(ops.dequant("q4_kt", wt, n, k))
+        assert_bits_equal(got, of.dequant_q4_k(w, n, k), f"q4_kt dequant {n}x{k}")
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 8])
+def test_mv_q8_tiled_equals_gguf_layout_at_k4096(dev, m):
+    """At K = 4096 the tiled-layout GEMV does the GGUF-layout kernel's arithmetic in its order: identical bits, for
+    activations quantized in the kernel and for planar Q8_1."""
+    import torch
+    ops = _ops()
+    rng = np.random.default_rng(62 + m)
+    n, k = 12288 if m == 1 else 320, 4096
+    w = dev_u8(_weights("q4_k", rng, n, k), dev)
+    wt = ops.tile_q4k(w, n, k)
+    xt, _ = _x(rng, m, k, "bf16", dev)
+    assert_bits_equal(host(ops.mv_q8("q4_kt", wt, xt, n, k)), host(ops.mv_q8("q4_k", w, xt, n, k)), f"m={m}")
+    xq = ops.quant_q8(xt)
+    assert_bits_equal(host(ops.mv_q8("q4_kt", wt, xq, n, k, tokens=m)), host(ops.mv_q8("q4_k", w, xq, n, k, tokens=m)),
+                      f"planar m={m}")
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("n,k,m,dtype", [
+    (16, 512, 1, "bf16"),      # one wave, one slice
+    (48, 1536, 3, "f32"),      # three waves
+    (32, 5120, 2, "bf16"),     # two slices a wave, five waves
+    (64, 8192, 5, "bf16"),     # two slices a wave, eight waves
+    (16, 12288, 2, "f32"),     # three slices a wave
+    (32, 16384, 3, "bf16"),    # four slices a wave (one token a workgroup)
+])
+def test_mv_q8_tiled_matches_oracle(dev, n, k, m, dtype):
+    """Every slices-per-wave configuration against the float64 oracle on Q8_1 activations; a multi-token call
+    equals one-token calls bit for bit; accumulate adds to y."""
+    import torch
+    ops = _ops()
+    rng = np.random.default_rng(n + k + m)
+    w = _weights("q4_k", rng, n, k)
+    wt = ops.tile_q4k(dev_u8(w, dev), n, k)
+    xt, xv = _x(rng, m, k, dtype, dev)
+    y = host(ops.mv_q8("q4_kt", wt, xt, n, k))
+    want = ref.gemv(ref.q8_1(xv), of.dequant_q4_k(w, n, k))
+    assert_close_rel_l2(y, want, 1e-3, f"q4_kt mv_q8 n={n} k={k} m={m}")
+    for t in range(m):
+        assert_bits_equal(host(ops.mv_q8("q4_kt", wt, xt[t:t + 1].contiguous(), n, k))[0], y[t], f"token {t}")
+    y0 = rng.standard_normal((m, n)).astype(np.float32)
+    yt = dev_f32(y0, dev)
+    ops.mv_q8("q4_kt", wt, xt, n, k, y=yt, accumulate=True)
+    assert_close_rel_l2(host(yt), y0 + want, 1e-3, "accumulate")
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("m", [4, 8])
+def test_mv_q8_tiled_in_kernel_quantization_equals_planar(dev, m):
+    """Four and eight tokens a workgroup through the C ABI with bf16 rows (each workgroup quantizes them) equal
+    quant_q8 + the planar kernel bit for bit."""
+    import torch
+    from qmm import _lib
+    ops = _ops()
+    rng = np.random.default_rng(70 + m)
+    n, k = 64, 4096
+    wt = ops.tile_q4k(dev_u8(_weights("q4_k", rng, n, k), dev), n, k)
+    xt, _ = _x(rng, m, k, "bf16", dev)
+    y = torch.empty((m, n), dtype=torch.float32, device=dev)
+    _lib.call("qmm_mv_q8", 5, k, n, m, 0, xt.data_ptr(), 2, wt.data_ptr(), y.data_ptr(),
+              torch.cuda.current_stream().cuda_stream)
+    planar = host(ops.mv_q8("q4_kt", wt, ops.quant_q8(xt), n, k, tokens=m))
+    assert_bits_equal(host(y), planar, f"m={m}")
+    torch.cuda.synchronize()

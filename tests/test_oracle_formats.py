@@ -331,3 +331,35 @@ def test_mxfp4t_lane_half_swap_negative_control():
     nt, st = of.mxfp4s_to_tiled(nib, sc, rows, k)
     bad = nt.reshape(-1, 2, 32, 16)[:, ::-1].reshape(-1)
     assert not np.array_equal(of.dequant_mxfp4t(bad, st, rows, k), of.dequant_mxfp4s(nib, sc, rows, k))
+
+
+# ------------------------------------------------------------------------------------------- Q4_K tiled layout
+def test_q4_kt_byte_addresses_follow_the_layout_definition():
+    """Every byte of every GGUF Q4_K block lands where the tiled layout puts it, computed as a flat offset: for row
+    r, super-block b and byte j of its 144, unit u = (r // 16) * (K / 512) + b // 2, sb = b % 2, i = r % 16;
+    header byte j < 16 -> 4608 u + 16 (2 i + sb) + j; code byte c = j - 16 -> 4608 u + 512 + 1024 ((c // 16) % 4)
+    + 16 (4 i + 2 sb + c // 64) + c % 16."""
+    from qmm import synth
+    rng = np.random.default_rng(21)
+    rows, k = 32, 1536
+    raw = synth.q4_k_weights(rng, rows, k).reshape(rows, k // 256, 144)
+    t = of.q4_k_to_tiled(raw, rows, k)
+    assert t.size == raw.size
+    r, b, j = np.meshgrid(np.arange(rows), np.arange(k // 256), np.arange(144), indexing="ij")
+    u = (r // 16) * (k // 512) + b // 2
+    sb, i, c = b % 2, r % 16, j - 16
+    off = np.where(j < 16, 4608 * u + 16 * (2 * i + sb) + j,
+                   4608 * u + 512 + 1024 * ((c // 16) % 4) + 16 * (4 * i + 2 * sb + c // 64) + c % 16)
+    assert np.array_equal(np.sort(off.ravel()), np.arange(raw.size))    # a permutation
+    assert np.array_equal(t[off], raw)
+
+
+def test_q4_kt_round_trip_and_values():
+    from qmm import synth
+    rng = np.random.default_rng(22)
+    for rows, k in ((16, 512), (48, 4096)):
+        raw = synth.q4_k_weights(rng, rows, k)
+        t = of.q4_k_to_tiled(raw, rows, k)
+        assert np.array_equal(of.q4_kt_to_gguf(t, rows, k), np.asarray(raw).reshape(-1))
+        want = of.dequant_q4_k(raw, rows, k)
+        assert np.array_equal(of.dequant_q4_kt(t, rows, k).view(np.uint32), want.view(np.uint32))
