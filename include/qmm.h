@@ -74,6 +74,13 @@ int qmm_dequant(int fmt, const void *w, const void *ws, int64_t rows, int64_t k,
 int qmm_mv(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
            const void *w, const void *ws, float *y, qmm_stream_t stream);
 
+/* Decode swiglu matvec, g_mv_{fmt}_k{K}_swiglu[_t{TG}] (S/gen_llm.py:1159-1197; launch args (n, tokens, accumulate,
+ * x, w, w2, y)): y[t, r] = (accumulate ? y[t, r] : 0) + silu(sum_k x[t, k] W[r, k]) * (sum_k x[t, k] W2[r, k]),
+ * silu(g) = g / (1 + e^-g), fp32 accumulation. fmt QMM_Q4_0 / QMM_Q4_K / QMM_MXFP4 (the reference has no swiglu
+ * matvec on split planes); w (gate) and w2 (up) [n, k]; x f32 / bf16 [tokens, k]; y f32 [tokens, n]. */
+int qmm_mv_swiglu(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
+                  const void *w, const void *w2, float *y, qmm_stream_t stream);
+
 /* Q8_1 activation quantizer, g_quant_q8 (S/gen_llm.py:684-749; llama.cpp quantize_q8_1): per group of 32 values
  * d = amax / 127, q = sign(x/d) floor(|x/d| + 1/2) (0 when d = 0). x: f32 or bf16 [rows, k], k % 32 == 0; xq: the
  * planar buffer (QMM_Q8) of rows * k code bytes followed by rows * k / 32 f32 pairs (f16-rounded d, sum of codes),
@@ -100,7 +107,10 @@ int qmm_mv_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, con
  * x: f16 [rows, k] (x_dtype QMM_F16), the reference's row-scaled x16 from qmm_row_scale_f16; scales: f32 [rows, 2]
  * with inv = scales[row, 1] (the reference's (2^-e, 2^e) pairs), or NULL for inv = 1; y: [rows, n] of y_dtype
  * (QMM_F32 as the reference, or QMM_BF16, rounded to nearest even). fp32 accumulation. Q4_K weights, K % 256 == 0;
- * the weights are dequantized to f16 as the reference stages them: fma_f16(f16(q), f16(d sc), f16(-dmin m)). */
+ * the weights are dequantized to f16 as the reference stages them: fma_f16(f16(q), f16(d sc), f16(-dmin m)).
+ * QMM_GEMM_SWIGLU: w is the gate matrix and w2 the up matrix (both [n, k]); silu(g) = g / (1 + e^-g).
+ * Skip-padding (the reference's default GEMM_SKIP_PADDING): with scales, a 64-row tile whose rows all have
+ * scales[row, 0] == 0 (padding rows of qmm_row_scale_f16_live) does no work and its y rows are not written. */
 int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, const void *x, int x_dtype, const float *scales,
              const void *w, const void *w2, void *y, int y_dtype, qmm_stream_t stream);
 
@@ -179,6 +189,12 @@ int qmm_moe_grouped_mxfp8(int fmt, int fused, int act, int64_t max_tiles, int64_
  * (QMM_F32 as the reference, or QMM_BF16). This is the A operand qmm_gemm takes. */
 int qmm_row_scale_f16(int64_t rows, int64_t k, const void *x, int x_dtype, float *scales, void *x16,
                       const int32_t *tile_info, qmm_stream_t stream);
+
+/* g_row_scale_f16_live (S/gen_llm.py:1915-1937): qmm_row_scale_f16 over an epoch's rows, where a padding row
+ * (info i32 [rows, 4] with info[row, 2] == 0) gets scale and inverse 0 and zero f16 values without its x row being
+ * read. qmm_gemm skips a 64-row tile whose rows all have scale 0 (GEMM_SKIP_PADDING, S/gen_gemm.py:2188-2220). */
+int qmm_row_scale_f16_live(int64_t rows, const int32_t *info, int64_t k, const void *x, int x_dtype, float *scales,
+                           void *x16, qmm_stream_t stream);
 
 /* MXFP8 activation quantizer, the A operand of the gfx950 scaled MFMA (no reference counterpart: the reference's
  * fp8 producers, S/gen_mxfp4s.py:852-969, quantize with a per-row power-of-two scale for gfx12 WMMA). One E8M0

@@ -43,7 +43,9 @@ static_assert(kDepth % 2 == 0, "the LDS double buffer follows the step parity");
 constexpr int APITCH = KSTEP + 8;   // f16 per LDS row: 144 bytes, rows 16-byte aligned, reads 2-way at most
 typedef __attribute__((ext_vector_type(2))) _Float16 h2;
 
-enum Kind { kDense = 0, kGU = 1, kDN = 2 };
+// kDense: Y (+)= X W^T; kSwiglu: Y = silu(X Wg^T inv) (X Wu^T inv) over dense rows (the GEMM's swiglu mode);
+// kGU / kDN: the grouped gate/up and down GEMMs over bucketed expert tiles
+enum Kind { kDense = 0, kGU = 1, kDN = 2, kSwiglu = 3 };
 
 __device__ __forceinline__ h2 as_h2(u32 v) { return __builtin_bit_cast(h2, v); }
 __device__ __forceinline__ u32 as_u32(h2 v) { return __builtin_bit_cast(u32, v); }
@@ -108,7 +110,9 @@ constexpr int kStagedMaxK = 6144;
 
 template <int KIND, bool ACC, bool BF16OUT, int DEPTH, bool STAGED>
 __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
-  constexpr int BN = KIND == kGU ? 64 : 128;
+  constexpr bool kTwoW = KIND == kGU || KIND == kSwiglu;        // two weight matrices (gate, up): wave pairs
+  constexpr bool kDenseRows = KIND == kDense || KIND == kSwiglu;  // rows m0 .. m0 + 63 of x, tiles row-major
+  constexpr int BN = kTwoW ? 64 : 128;
   extern __shared__ __align__(16) u32 scl[];   // STAGED: [128 columns][K / 32] (dsc | nmn << 16)
   __shared__ __align__(16) _Float16 As[2][2][BM][APITCH];   // [buffer][K-half][row][k]
   __shared__ int src_row[BM];
@@ -118,7 +122,7 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
   const int M = a.M, N = a.N, K = a.K;
 
   int m0, n0, expert = 0;
-  if constexpr (KIND == kDense) {
+  if constexpr (kDenseRows) {
     // XCD-aware order: workgroup b runs on XCD b % 8, which gets a contiguous range of tiles
     const int per = (int)(gridDim.x / 8);
     const int t = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
@@ -141,7 +145,7 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
   int my_src = -1;
   if (tid < BM) {
     int src;
-    if constexpr (KIND == kDense) src = m0 + tid < M ? m0 + tid : -1;
+    if constexpr (kDenseRows) src = m0 + tid < M ? m0 + tid : -1;
     else if constexpr (KIND == kGU) {
       const int rm = a.rowmap[m0 + tid];
       src = rm >= 0 ? rm / a.KU : -1;
@@ -152,6 +156,13 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
     src_row[tid] = src;
     rinv[tid] = (a.scales && src >= 0) ? a.scales[2 * src + 1] : 1.f;
     my_src = src;
+  }
+  if constexpr (kDenseRows) {
+    // skip-padding: a tile whose rows all have scale 0 (padding rows) does no work and writes nothing
+    if (a.scales) {
+      const bool live = tid < BM && my_src >= 0 && a.scales[2 * my_src] != 0.f;
+      if (__syncthreads_or(live) == 0) return;
+    }
   }
   // whether rows 32..63 hold a live row: if not, the upper 32-row MFMA blocks are skipped (their outputs are the
   // zeros of dead rows) -- expert tiles of prefill batches are often less than half full
@@ -189,6 +200,7 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
   const int h = lane >> 5, lc = lane & 31;
   const u8 *wbase;
   if constexpr (KIND == kDense) wbase = a.w;
+  else if constexpr (KIND == kSwiglu) wbase = sel ? a.w2 : a.w;
   else if constexpr (KIND == kGU) {
     const u8 *g = a.w + (int64_t)expert * a.ebytes;
     wbase = sel ? (a.w2 ? a.w2 + (int64_t)expert * a.ebytes : g + a.up_off) : g;
@@ -198,7 +210,7 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
   const u8 *wcol[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    int c = n0 + (KIND == kGU ? 0 : sel * 64) + 32 * j + lc;
+    int c = n0 + (kTwoW ? 0 : sel * 64) + 32 * j + lc;
     c = c < N ? c : N - 1;
     wcol[j] = wbase + (int64_t)c * RB;
   }
@@ -225,13 +237,14 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
         const int msel = cl >> 6;
         const u8 *mb;
         if constexpr (KIND == kDense) mb = a.w;
+        else if constexpr (KIND == kSwiglu) mb = msel ? a.w2 : a.w;
         else if constexpr (KIND == kGU) {
           const u8 *g = a.w + (int64_t)expert * a.ebytes;
           mb = msel ? (a.w2 ? a.w2 + (int64_t)expert * a.ebytes : g + a.up_off) : g;
         } else {
           mb = a.w + (int64_t)expert * a.ebytes;
         }
-        int c = n0 + (KIND == kGU ? cl - 64 * msel : cl);
+        int c = n0 + (kTwoW ? cl - 64 * msel : cl);
         c = c < N ? c : N - 1;
         hd[q] = ld16(mb + (int64_t)c * RB + (int64_t)b * 144);
       }
@@ -361,7 +374,7 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] += red_at(sel, i, j, r);
 
-  if constexpr (KIND == kGU) {
+  if constexpr (kTwoW) {
     // the up wave (K-half 0) hands its result to the gate wave; every wave takes part in the barriers
     __syncthreads();
     if (kh == 0 && sel == 1) {
@@ -388,12 +401,14 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
       for (int r = 0; r < 16; ++r) {
         const int lr = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
         const int row = m0 + lr;
-        const int col = n0 + (KIND == kGU ? 0 : sel * 64) + 32 * j + lc;
-        if (col >= N || (KIND == kDense && row >= M)) continue;
+        const int col = n0 + (kTwoW ? 0 : sel * 64) + 32 * j + lc;
+        if (col >= N || (kDenseRows && row >= M)) continue;
         const int src = src_row[lr];
         const int64_t o = (int64_t)row * N + col;
-        if constexpr (KIND == kDense) {
-          float v = acc[i][j][r] * rinv[lr];
+        if constexpr (kDenseRows) {
+          float v;
+          if constexpr (KIND == kSwiglu) v = act_fn(QMM_ACT_SILU, acc[i][j][r] * rinv[lr], red_at(0, i, j, r) * rinv[lr]);
+          else v = acc[i][j][r] * rinv[lr];
           if constexpr (BF16OUT) {
             if constexpr (ACC) v += bf16_to_f32(yb[o]);
             yb[o] = (u16)f32_to_bf16_rne(v);
@@ -415,7 +430,8 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
 
 template <int KIND, bool ACC, bool BF16OUT>
 int launch(const Args &a, hipStream_t s) {
-  const dim3 grid((unsigned)(KIND == kDense ? 8 * ((a.tiles_total + 7) / 8) : 8 * a.n_blocks * ((a.tiles_m + 7) / 8)));
+  constexpr bool kDenseRows = KIND == kDense || KIND == kSwiglu;
+  const dim3 grid((unsigned)(kDenseRows ? 8 * ((a.tiles_total + 7) / 8) : 8 * a.n_blocks * ((a.tiles_m + 7) / 8)));
   if (a.K <= kStagedMaxK) {
     const size_t dyn = (size_t)128 * (a.K / 32) * 4;
     if (dyn > 32768) {   // beyond the default dynamic LDS limit: raise it once
@@ -440,24 +456,27 @@ int launch(const Args &a, hipStream_t s) {
 extern "C" int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, const void *x, int x_dtype,
                         const float *scales, const void *w, const void *w2, void *y, int y_dtype,
                         qmm_stream_t stream) {
-  (void)w2;
   if (fmt != QMM_Q4_K) return QMM_ERR_FORMAT;
-  if (mode != QMM_GEMM_STORE && mode != QMM_GEMM_ACC) return QMM_ERR_RANGE;
-  if (!x || !w || !y) return QMM_ERR_NULL;
+  if (mode != QMM_GEMM_STORE && mode != QMM_GEMM_ACC && mode != QMM_GEMM_SWIGLU) return QMM_ERR_RANGE;
+  if (!x || !w || !y || (mode == QMM_GEMM_SWIGLU && !w2)) return QMM_ERR_NULL;
   if (x_dtype != QMM_F16) return QMM_ERR_DTYPE;   // bf16 / f32 rows go through qmm_row_scale_f16 first
   if (y_dtype != QMM_F32 && y_dtype != QMM_BF16) return QMM_ERR_DTYPE;
   if (rows <= 0 || n <= 0 || k <= 0 || k % 256) return QMM_ERR_SHAPE;
   if (rows > (1 << 24) || n > (1 << 24) || k > (1 << 20)) return QMM_ERR_SHAPE;
-  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 4)) return QMM_ERR_ALIGN;
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 4) || (w2 && !aligned(w2, 16))) return QMM_ERR_ALIGN;
   if (rows * k * 2 >= (1ll << 31)) return QMM_ERR_SHAPE;   // activation rows are addressed by a 32-bit buffer offset
   Args a{};
   a.M = (int)rows; a.N = (int)n; a.K = (int)k;
   a.x16 = static_cast<const _Float16 *>(x); a.scales = scales; a.x_rows = (int)rows;
-  a.w = static_cast<const u8 *>(w); a.y = y;
+  a.w = static_cast<const u8 *>(w); a.w2 = static_cast<const u8 *>(w2); a.y = y;
   a.tiles_m = (int)((rows + BM - 1) / BM);
-  a.tiles_total = a.tiles_m * (int)((n + 127) / 128);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool acc = mode == QMM_GEMM_ACC, bf = y_dtype == QMM_BF16;
+  if (mode == QMM_GEMM_SWIGLU) {   // 64 output columns a workgroup: its wave pairs take the gate and the up matrix
+    a.tiles_total = a.tiles_m * (int)((n + 63) / 64);
+    return bf ? launch<kSwiglu, false, true>(a, s) : launch<kSwiglu, false, false>(a, s);
+  }
+  a.tiles_total = a.tiles_m * (int)((n + 127) / 128);
   if (acc && bf) return launch<kDense, true, true>(a, s);
   if (acc) return launch<kDense, true, false>(a, s);
   if (bf) return launch<kDense, false, true>(a, s);

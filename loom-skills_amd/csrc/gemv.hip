@@ -89,14 +89,14 @@ __global__ __launch_bounds__(256) void expert_mv_kernel(int64_t n, int64_t assig
                                                         const u8 *__restrict__ ws, const u8 *__restrict__ w2,
                                                         const u8 *__restrict__ ws2, int64_t rb, int64_t srb,
                                                         int64_t ebytes, int64_t esbytes, const float *__restrict__ bias,
-                                                        const float *__restrict__ bias2, int act,
+                                                        const float *__restrict__ bias2, int act, int accumulate,
                                                         float *__restrict__ y) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t a = blockIdx.x;
   const int64_t row0 = ((int64_t)blockIdx.y * kWavesPerBlock + wave) * RW;
   if (row0 >= n || a >= assignments) return;
-  int e = ids[a];
+  int e = ids ? ids[a] : 0;                // no ids: one expert (the dense swiglu matvec)
   e = e < 0 ? 0 : (e >= E ? E - 1 : e);   // ids are clamped into range as the reference does (S/gen_moe.py:592-596)
   const u8 *xr = x + (GU ? a / KU : a) * x_row_bytes;
   const u8 *we = w + e * ebytes, *wse = ws + e * esbytes;
@@ -140,7 +140,7 @@ __global__ __launch_bounds__(256) void expert_mv_kernel(int64_t n, int64_t assig
         if (bias2) u += bias2[e * n + row];
         v = act_fn(act, g, u);
       }
-      y[a * n + row] = v;
+      y[a * n + row] = accumulate ? y[a * n + row] + v : v;
     }
   }
 }
@@ -218,13 +218,25 @@ template <class P, bool GU>
 int launch_expert(int64_t k, int64_t n, int E, int KU, int64_t assignments, const int32_t *ids, const void *x,
                   int64_t x_row_bytes, const void *w, const void *ws, const void *w2, const void *ws2, int64_t rb,
                   int64_t srb, int64_t ebytes, int64_t esbytes, const float *bias, const float *bias2, int act,
-                  float *y, hipStream_t s) {
+                  float *y, hipStream_t s, int accumulate = 0) {
   const dim3 grid((unsigned)assignments, (unsigned)((n + kWavesPerBlock * kRW - 1) / (kWavesPerBlock * kRW)));
   expert_mv_kernel<P, kRW, GU><<<grid, 256, 0, s>>>(
       n, assignments, KU, E, k, ids, static_cast<const u8 *>(x), x_row_bytes, static_cast<const u8 *>(w),
       static_cast<const u8 *>(ws), static_cast<const u8 *>(w2), static_cast<const u8 *>(ws2), rb, srb, ebytes, esbytes,
-      bias, bias2, act, y);
+      bias, bias2, act, accumulate, y);
   return launch_status();
+}
+
+// The dense swiglu matvec: the gate/up expert kernel with one expert (no ids) and one token a row of x.
+template <template <bool> class P>
+int launch_swiglu(bool bf, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, const void *w,
+                  const void *w2, int64_t rb, float *y, hipStream_t s) {
+  const int64_t xb = k * (bf ? 2 : 4);
+  if (bf)
+    return launch_expert<P<true>, true>(k, n, 1, 1, tokens, nullptr, x, xb, w, w, w2, w2, rb, 0, rb * n, 0, nullptr,
+                                        nullptr, QMM_ACT_SILU, y, s, accumulate);
+  return launch_expert<P<false>, true>(k, n, 1, 1, tokens, nullptr, x, xb, w, w, w2, w2, rb, 0, rb * n, 0, nullptr,
+                                       nullptr, QMM_ACT_SILU, y, s, accumulate);
 }
 
 template <template <bool> class P>
@@ -282,6 +294,25 @@ static int expert_mv_impl(int fmt, int mode, int fused, int act, int64_t k, int6
     case QMM_Q4_0: return dispatch_expert<Q40>(gu, bf, k, n, E, KU, assignments, ids, x, w, wsg, wu, wsu, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
     case QMM_MXFP4: return dispatch_expert<MXG>(gu, bf, k, n, E, KU, assignments, ids, x, w, wsg, wu, wsu, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
     default: return dispatch_expert<MXS>(gu, bf, k, n, E, KU, assignments, ids, x, w, wsg, wu, wsu, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
+  }
+}
+
+extern "C" int qmm_mv_swiglu(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x,
+                             int x_dtype, const void *w, const void *w2, float *y, qmm_stream_t stream) {
+  if (fmt != QMM_Q4_0 && fmt != QMM_Q4_K && fmt != QMM_MXFP4) return QMM_ERR_FORMAT;   // no split planes
+  if (!x || !w || !w2 || !y) return QMM_ERR_NULL;
+  if (n <= 0 || tokens <= 0 || tokens > (1 << 24) || row_bytes(fmt, k) == 0) return QMM_ERR_SHAPE;
+  if (x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
+  if (int st = check_weights(fmt, k, w, nullptr)) return st;
+  if (int st = check_weights(fmt, k, w2, nullptr)) return st;
+  if (!aligned(x, 16) || !aligned(y, 4)) return QMM_ERR_ALIGN;
+  const int64_t rb = row_bytes(fmt, k);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool bf = x_dtype == QMM_BF16;
+  switch (fmt) {
+    case QMM_Q4_K: return launch_swiglu<Q4K>(bf, k, n, tokens, accumulate, x, w, w2, rb, y, s);
+    case QMM_Q4_0: return launch_swiglu<Q40>(bf, k, n, tokens, accumulate, x, w, w2, rb, y, s);
+    default: return launch_swiglu<MXG>(bf, k, n, tokens, accumulate, x, w, w2, rb, y, s);
   }
 }
 

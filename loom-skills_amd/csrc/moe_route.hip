@@ -271,11 +271,25 @@ __device__ __forceinline__ float load_act(const void *x, int bf, int64_t i) {
   return bf ? bf16_to_f32(static_cast<const u16 *>(x)[i]) : static_cast<const float *>(x)[i];
 }
 
+// A padding row (info != NULL and info[row, 2] == 0, the reference's g_row_scale_f16_live) gets scale and inverse 0
+// and zero f16 values without its x row being read; the prefill GEMM skips a 64-row tile whose scales are all 0.
+__device__ __forceinline__ bool pad_row(const int32_t *info, int64_t r, int64_t k, float *scales, _Float16 *x16) {
+  if (!info || info[4 * r + 2] != 0) return false;
+  for (int64_t c = threadIdx.x; c < k; c += 256) x16[r * k + c] = (_Float16)0.f;
+  if (threadIdx.x == 0) {
+    scales[2 * r] = 0.f;
+    scales[2 * r + 1] = 0.f;
+  }
+  return true;
+}
+
 __global__ __launch_bounds__(256) void row_scale_kernel(int64_t rows, int64_t k, const void *__restrict__ x, int bf,
                                                         float *__restrict__ scales, _Float16 *__restrict__ x16,
-                                                        const int32_t *__restrict__ tile_info) {
+                                                        const int32_t *__restrict__ tile_info,
+                                                        const int32_t *__restrict__ info) {
   const int64_t r = blockIdx.x;
   if (tile_info && tile_info[2 * (r / kTile)] < 0) return;
+  if (pad_row(info, r, k, scales, x16)) return;
   __shared__ float wmax[4];
   float m = 0.f;
   for (int64_t c = threadIdx.x; c < k; c += 256) m = fmaxf(m, fabsf(load_act(x, bf, r * k + c)));
@@ -318,9 +332,11 @@ __device__ __forceinline__ void load8(const void *x, int64_t i8, float (&v)[8]) 
 template <bool BF>
 __global__ __launch_bounds__(256) void row_scale_vec_kernel(int64_t rows, int64_t k, const void *__restrict__ x,
                                                             float *__restrict__ scales, _Float16 *__restrict__ x16,
-                                                            const int32_t *__restrict__ tile_info) {
+                                                            const int32_t *__restrict__ tile_info,
+                                                            const int32_t *__restrict__ info) {
   const int64_t r = blockIdx.x;
   if (tile_info && tile_info[2 * (r / kTile)] < 0) return;
+  if (pad_row(info, r, k, scales, x16)) return;
   __shared__ float wmax[4];
   const int64_t nch = k / 8, base = r * nch;
   float v[kRsChunks][8];
@@ -476,21 +492,33 @@ int qmm_moe_combine(int64_t tokens, int64_t rows, int64_t H, int KU, const float
   return launch_status();
 }
 
-int qmm_row_scale_f16(int64_t rows, int64_t k, const void *x, int x_dtype, float *scales, void *x16,
-                      const int32_t *tile_info, qmm_stream_t stream) {
+static int row_scale(int64_t rows, int64_t k, const void *x, int x_dtype, float *scales, void *x16,
+                     const int32_t *tile_info, const int32_t *info, hipStream_t s) {
   if (!x || !scales || !x16) return QMM_ERR_NULL;
   if (x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
   if (rows <= 0 || k <= 0 || rows > (1ll << 24)) return QMM_ERR_SHAPE;
   if (tile_info && rows % kTile) return QMM_ERR_SHAPE;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   _Float16 *o = static_cast<_Float16 *>(x16);
   if (k % 8 == 0 && k <= 8 * 256 * kRsChunks && aligned(x, 16) && aligned(x16, 16)) {
-    if (x_dtype == QMM_BF16) row_scale_vec_kernel<true><<<(unsigned)rows, 256, 0, s>>>(rows, k, x, scales, o, tile_info);
-    else row_scale_vec_kernel<false><<<(unsigned)rows, 256, 0, s>>>(rows, k, x, scales, o, tile_info);
+    if (x_dtype == QMM_BF16)
+      row_scale_vec_kernel<true><<<(unsigned)rows, 256, 0, s>>>(rows, k, x, scales, o, tile_info, info);
+    else
+      row_scale_vec_kernel<false><<<(unsigned)rows, 256, 0, s>>>(rows, k, x, scales, o, tile_info, info);
   } else {
-    row_scale_kernel<<<(unsigned)rows, 256, 0, s>>>(rows, k, x, x_dtype == QMM_BF16, scales, o, tile_info);
+    row_scale_kernel<<<(unsigned)rows, 256, 0, s>>>(rows, k, x, x_dtype == QMM_BF16, scales, o, tile_info, info);
   }
   return launch_status();
+}
+
+int qmm_row_scale_f16(int64_t rows, int64_t k, const void *x, int x_dtype, float *scales, void *x16,
+                      const int32_t *tile_info, qmm_stream_t stream) {
+  return row_scale(rows, k, x, x_dtype, scales, x16, tile_info, nullptr, reinterpret_cast<hipStream_t>(stream));
+}
+
+int qmm_row_scale_f16_live(int64_t rows, const int32_t *info, int64_t k, const void *x, int x_dtype, float *scales,
+                           void *x16, qmm_stream_t stream) {
+  if (!info) return QMM_ERR_NULL;
+  return row_scale(rows, k, x, x_dtype, scales, x16, nullptr, info, reinterpret_cast<hipStream_t>(stream));
 }
 
 int qmm_quant_mxfp8(int64_t rows, int64_t k, const void *x, int x_dtype, const int32_t *tile_info, uint8_t *codes,

@@ -15,6 +15,7 @@ SIGNATURES = {
     "qmm_row_bytes": [c_int, c_i64],
     "qmm_dequant": [c_int, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp],
     "qmm_mv": [c_int, c_i64, c_i64, c_i64, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_vp],
+    "qmm_mv_swiglu": [c_int, c_i64, c_i64, c_i64, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_vp],
     "qmm_quant_q8": [c_i64, c_i64, c_vp, c_int, c_vp, c_vp],
     "qmm_mv_q8": [c_int, c_i64, c_i64, c_i64, c_int, c_vp, c_int, c_vp, c_vp, c_vp],
     "qmm_gemm": [c_int, c_int, c_i64, c_i64, c_i64, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_int, c_vp],
@@ -29,6 +30,7 @@ SIGNATURES = {
     "qmm_moe_grouped_mxfp8": [c_int, c_int, c_int, c_i64, c_i64, c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_vp,
                               c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
     "qmm_row_scale_f16": [c_i64, c_i64, c_vp, c_int, c_vp, c_vp, c_vp, c_vp],
+    "qmm_row_scale_f16_live": [c_i64, c_vp, c_i64, c_vp, c_int, c_vp, c_vp, c_vp],
     "qmm_quant_mxfp8": [c_i64, c_i64, c_vp, c_int, c_vp, c_vp, c_vp, c_vp],
     "qmm_repack_mxfp4": [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp],
     "qmm_tile_mxfp4": [c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp],

@@ -76,6 +76,16 @@ def mv(fmt, w, x, n, k, y=None, accumulate=False, ws=None):
     return y
 
 
+def mv_swiglu(fmt, w, w2, x, n, k, y=None, accumulate=False):
+    """y[t, r] (+)= silu(x W^T) * (x W2^T) (g_mv_{fmt}_k{K}_swiglu); x f32 or bf16 [tokens, k]; y f32 [tokens, n]."""
+    _dev(w, w2, x, y)
+    tokens = x.shape[0]
+    y = torch.empty((tokens, n), dtype=torch.float32, device=x.device) if y is None else y
+    _lib.call("qmm_mv_swiglu", CODE[fmt], k, n, tokens, int(bool(accumulate)), _ptr(x), _dt(x), _ptr(w), _ptr(w2),
+              _ptr(y), _stream())
+    return y
+
+
 def q8_bytes(rows, k):
     """Bytes of the planar Q8_1 buffer of `rows` rows of k values: codes, then an f32 pair per 32 values."""
     return rows * k + rows * (k // 32) * 8
@@ -117,8 +127,10 @@ def mv_q8(fmt, w, x, n, k, tokens=None, y=None, accumulate=False):
 
 
 def gemm(fmt, mode, x, w, n, k, w2=None, scales=None, out_dtype=torch.float32, y=None):
-    """Y = (X16 W^T) inv (store) or Y += ... (acc). x is the row-scaled f16 operand with its scales (the reference's
-    g_row_scale_f16 output), or bf16 / f32 rows, which are row-scaled here first (qmm_row_scale_f16)."""
+    """Y = (X16 W^T) inv (store), Y += ... (acc) or Y = silu(X16 W^T inv) (X16 W2^T inv) (swiglu, w2 the up matrix).
+    x is the row-scaled f16 operand with its scales (the reference's g_row_scale_f16 output), or bf16 / f32 rows,
+    which are row-scaled here first (qmm_row_scale_f16). With scales, 64-row tiles whose rows all have scale 0
+    (padding rows of row_scale_f16(x, info=...)) are skipped and their y rows are not written."""
     _dev(x, w, w2, scales, y)
     rows = x.shape[0]
     if x.dtype != torch.float16:
@@ -221,13 +233,19 @@ def moe_combine(ys, wts, pos=None, y=None, accumulate=False):
     return y
 
 
-def row_scale_f16(x, tile_info=None, x16=None, scales=None):
-    """(x16 f16 [rows, k], scales f32 [rows, 2]) with the per-row power-of-two scale; x f32 or bf16 [rows, k]."""
-    _dev(x, tile_info, x16, scales)
+def row_scale_f16(x, tile_info=None, x16=None, scales=None, info=None):
+    """(x16 f16 [rows, k], scales f32 [rows, 2]) with the per-row power-of-two scale; x f32 or bf16 [rows, k].
+    info (i32 [rows, 4], g_row_scale_f16_live): rows with info[row, 2] == 0 are padding, scale 0 and zero values."""
+    _dev(x, tile_info, x16, scales, info)
     rows, k = x.shape
     x16 = torch.empty((rows, k), dtype=torch.float16, device=x.device) if x16 is None else x16
     scales = torch.empty((rows, 2), dtype=torch.float32, device=x.device) if scales is None else scales
-    _lib.call("qmm_row_scale_f16", rows, k, _ptr(x), _dt(x), _ptr(scales), _ptr(x16), _ptr(tile_info), _stream())
+    if info is not None:
+        if tile_info is not None:
+            raise ValueError("info (epoch rows) and tile_info (expert tiles) are separate producers")
+        _lib.call("qmm_row_scale_f16_live", rows, _ptr(info), k, _ptr(x), _dt(x), _ptr(scales), _ptr(x16), _stream())
+    else:
+        _lib.call("qmm_row_scale_f16", rows, k, _ptr(x), _dt(x), _ptr(scales), _ptr(x16), _ptr(tile_info), _stream())
     return x16, scales
 
 
@@ -323,13 +341,18 @@ def moe_decode(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=
 GEMM_MIN_TOKENS = 64   # %gemm: epochs of 64+ tokens take the GEMM / grouped chain (S/gen_llm.py:6107-6126)
 
 
-def linear(fmt, x, w, n, k, y=None, mode="store", ws=None):
-    """Projection y (+)= x W^T with the reference's per-epoch choice (linear, S/gen_llm.py:4568-4625): the prefill
-    GEMM for 64+ tokens (Q4_K; the activation is row-scaled to f16 first), else the decode GEMV. y is f32."""
-    if mode not in ("store", "acc"):
+def linear(fmt, x, w, n, k, y=None, mode="store", ws=None, w2=None):
+    """Projection y (+)= x W^T, or swiglu y = silu(x W^T) (x W2^T), with the reference's per-epoch choice (linear,
+    S/gen_llm.py:4568-4625): the prefill GEMM for 64+ tokens (Q4_K; the activation is row-scaled to f16 first), else
+    the decode GEMV. y is f32."""
+    if mode not in ("store", "acc", "swiglu"):
         raise ValueError(f"linear mode {mode}")
+    if mode == "swiglu" and w2 is None:
+        raise ValueError("swiglu needs the up matrix w2")
     if x.shape[0] >= GEMM_MIN_TOKENS and fmt == "q4_k":
-        return gemm(fmt, mode, x, w, n, k, y=y)
+        return gemm(fmt, mode, x, w, n, k, w2=w2, y=y)
+    if mode == "swiglu":
+        return mv_swiglu(fmt, w, w2, x, n, k, y=y)
     return mv(fmt, w, x, n, k, y=y, accumulate=mode == "acc", ws=ws)
 
 

@@ -164,7 +164,8 @@ def rel_l2(actual, expected):
 def silu_mul(g, u):
     """silu(g) * u (S/gen_moe.py:27-32)."""
     g = np.asarray(g, np.float64)
-    return g / (1.0 + np.exp(-g)) * np.asarray(u, np.float64)
+    with np.errstate(over="ignore"):           # e^-g = inf for g < -709: g / inf = -0, the limit
+        return g / (1.0 + np.exp(-g)) * np.asarray(u, np.float64)
 
 
 def swiglu_oai(g, u, alpha=1.702, limit=7.0):
@@ -172,7 +173,8 @@ def swiglu_oai(g, u, alpha=1.702, limit=7.0):
     (S/gen_moe.py:33-46; make_kernel_tests.py:3208-3211)."""
     x = np.minimum(np.asarray(g, np.float64), limit)
     y = np.clip(np.asarray(u, np.float64), -limit, limit)
-    return x / (1.0 + np.exp(-alpha * x)) * (y + 1.0)
+    with np.errstate(over="ignore"):
+        return x / (1.0 + np.exp(-alpha * x)) * (y + 1.0)
 
 
 ACTIVATIONS = {"silu": silu_mul, "swiglu_oai": swiglu_oai}

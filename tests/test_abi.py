@@ -135,6 +135,13 @@ def test_argument_validation_without_a_device(lib):
                                      fake, n) == st["QMM_ERR_SHAPE"]
     assert lib.qmm_moe_grouped_mxfp8(4, 1, 0, 4, 128, 64, 4, 2, fake, fake, fake, fake, 8, fake, fake, n, n, fake,
                                      n, n) == st["QMM_ERR_NULL"]
+    # decode swiglu matvec: GGUF-layout weights only, both matrices; the GEMM's swiglu mode needs the up matrix
+    assert lib.qmm_mv_swiglu(3, 256, 4, 1, 0, fake, 0, fake, fake, fake, n) == st["QMM_ERR_FORMAT"]
+    assert lib.qmm_mv_swiglu(1, 256, 4, 1, 0, fake, 0, fake, n, fake, n) == st["QMM_ERR_NULL"]
+    assert lib.qmm_mv_swiglu(1, 100, 4, 1, 0, fake, 0, fake, fake, fake, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_mv_swiglu(1, 256, 4, 1, 0, fake, 0, fake, odd, fake, n) == st["QMM_ERR_ALIGN"]
+    assert lib.qmm_gemm(1, 2, 64, 256, 64, fake, 1, n, fake, n, fake, 0, n) == st["QMM_ERR_NULL"]
+    assert lib.qmm_row_scale_f16_live(64, n, 256, fake, 0, fake, fake, n) == st["QMM_ERR_NULL"]
 
 
 def test_python_surface_refuses_host_tensors():

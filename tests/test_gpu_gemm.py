@@ -112,3 +112,61 @@ def test_gemm_rejects_bad_arguments(dev):
         ops.gemm("q4_0", "store", torch.zeros((4, 256), dtype=torch.float16, device=dev), w, 4, 256)
     with pytest.raises(QmmError):
         ops.gemm("q4_k", "store", torch.zeros((4, 128), dtype=torch.float16, device=dev), w, 4, 128)
+
+
+@pytest.mark.parametrize("M,N,K,out", [(512, 12288, 4096, "f32"), (70, 200, 768, "bf16"), (64, 64, 256, "f32")])
+def test_gemm_swiglu(dev, M, N, K, out):
+    """g_gemm_q4_k_swiglu (S/gen_gemm.py:10, :688-691): Y = silu(X16 Wg^T inv) (X16 Wu^T inv). Shapes: the Qwen3-8B
+    FFN gate/up at a 512-token prefill, and partial row / column tiles. A bf16 store equals the f32 one rounded to
+    nearest even, bit for bit."""
+    import torch
+    import qmm.ops as ops
+    from qmm import synth
+    rng = np.random.default_rng(M + N + K + 7)
+    wg, wu = synth.q4_k_weights(rng, N, K), synth.q4_k_weights(rng, N, K)
+    xb = synth.to_bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    xv = synth.bf16_bits_to_f32(xb)
+    xr = ref.f16_rows(xv)
+    want = ref.silu_mul(ref.gemv(xr, of.dequant_q4_k(wg, N, K)), ref.gemv(xr, of.dequant_q4_k(wu, N, K)))
+    dt = torch.bfloat16 if out == "bf16" else torch.float32
+    y = ops.gemm("q4_k", "swiglu", dev_bf16(xb, dev), dev_u8(wg, dev), N, K, w2=dev_u8(wu, dev), out_dtype=dt)
+    y32 = host(ops.gemm("q4_k", "swiglu", dev_bf16(xb, dev), dev_u8(wg, dev), N, K, w2=dev_u8(wu, dev)))
+    torch.cuda.synchronize()
+    assert_close_rel_l2(y32, want, 1e-3, f"swiglu {M}x{N}x{K}")
+    if out == "bf16":
+        from helpers import assert_bits_equal
+        assert_bits_equal(host(y), ref.bf16_round(y32), "bf16 swiglu store")
+
+
+def test_gemm_skip_padding(dev):
+    """GEMM_SKIP_PADDING (S/gen_gemm.py:2188-2220) with g_row_scale_f16_live (S/gen_llm.py:1915-1937): padding rows
+    (info[row, 2] == 0) get scale 0 and zero values; a 64-row tile of padding only is not computed and its y rows
+    keep what they held; a tile mixing live and padding rows computes every row (padding rows come out 0)."""
+    import torch
+    import qmm.ops as ops
+    from qmm import synth
+    rng = np.random.default_rng(23)
+    M, N, K = 256, 192, 512
+    w = synth.q4_k_weights(rng, N, K)
+    xb = synth.to_bf16_bits(rng.standard_normal((M, K)).astype(np.float32))
+    xv = synth.bf16_bits_to_f32(xb)
+    live = np.ones(M, bool)
+    live[64:128] = False               # tile 1: padding only
+    live[192 + 40:] = False            # tile 3: 40 live rows, then padding
+    info = np.zeros((M, 4), np.int32)
+    info[:, 2] = live
+    it = torch.from_numpy(info).to(dev)
+    x16, sc = ops.row_scale_f16(dev_bf16(xb, dev), info=it)
+    x16p, scp = ops.row_scale_f16(dev_bf16(xb, dev))
+    assert np.array_equal(host(sc)[~live], np.zeros((int((~live).sum()), 2), np.float32))
+    assert np.all(host(x16)[~live] == 0)
+    np.testing.assert_array_equal(host(sc)[live], host(scp)[live])
+    np.testing.assert_array_equal(host(x16)[live].view(np.uint16), host(x16p)[live].view(np.uint16))
+    y = torch.full((M, N), 7.0, dtype=torch.float32, device=dev)
+    ops.gemm("q4_k", "store", x16, dev_u8(w, dev), N, K, scales=sc, y=y)
+    yh = host(y)
+    torch.cuda.synchronize()
+    want = ref.gemv(ref.f16_rows(xv), of.dequant_q4_k(w, N, K))
+    assert_close_rel_l2(yh[live], want[live], 1e-3, "live rows")
+    assert np.all(yh[64:128] == 7.0), "the padding-only tile was written"
+    assert np.all(yh[192 + 40:] == 0.0), "padding rows of a live tile are not zero"

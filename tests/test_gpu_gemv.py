@@ -180,3 +180,32 @@ def test_mv_rejects_bad_arguments(dev):
         ops.mv("q4_k", w, x.to(torch.float16), 4, 256)                                      # dtype
     with pytest.raises(QmmError):
         ops.mv("q4_0", w, torch.zeros((1, 32), dtype=torch.float32, device=dev), 4, 32)     # K % 64 for Q4_0
+
+
+@pytest.mark.parametrize("fmt,x_dtype,k", [("q4_k", "bf16", 4096), ("q4_k", "f32", 2048), ("q4_0", "f32", 1024),
+                                           ("mxfp4", "bf16", 2880)])
+def test_mv_swiglu(dev, fmt, x_dtype, k):
+    """g_mv_{fmt}_k{K}_swiglu (S/gen_llm.py:1159-1197): y (+)= silu(x Wg^T) (x Wu^T); three tokens, accumulate."""
+    import torch
+    import qmm.ops as ops
+    from qmm import synth
+    rng = np.random.default_rng(k + len(fmt))
+    n, m = 96, 3
+    gen = {"q4_k": synth.q4_k_weights, "q4_0": synth.q4_0_weights, "mxfp4": synth.mxfp4_weights}[fmt]
+    wg, wu = gen(rng, n, k), gen(rng, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    if x_dtype == "bf16":
+        b = synth.to_bf16_bits(x)
+        xt, xv = dev_bf16(b, dev), synth.bf16_bits_to_f32(b)
+    else:
+        xt, xv = dev_f32(x, dev), x
+    g = ref.gemv(xv, of.dequantize(fmt, wg, n, k))
+    u = ref.gemv(xv, of.dequantize(fmt, wu, n, k))
+    want = ref.silu_mul(g, u)
+    y = host(ops.mv_swiglu(fmt, dev_u8(wg, dev), dev_u8(wu, dev), xt, n, k))
+    assert_close_rel_l2(y, want, 1e-3, f"{fmt} swiglu")
+    y0 = rng.standard_normal((m, n)).astype(np.float32)
+    yt = dev_f32(y0, dev)
+    ops.mv_swiglu(fmt, dev_u8(wg, dev), dev_u8(wu, dev), xt, n, k, y=yt, accumulate=True)
+    assert_close_rel_l2(host(yt), y0 + want, 1e-3, f"{fmt} swiglu accumulate")
+    torch.cuda.synchronize()
