@@ -122,6 +122,25 @@ int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, const void *
 int qmm_moe_topk(const float *logits, int64_t tokens, int E, int KU, int gating, int norm, float scale,
                  const float *bias, int32_t *ids, float *wts, qmm_stream_t stream);
 
+/* The router with its matvec, g_moe_route / g_moe_route_tr / g_moe_route_tr_live (S/gen_moe.py:116-500; launch
+ * S/gen_llm.py:5373, :5380): logits f32 [tokens, E] = x W^T (fp32 accumulation; x f32 or bf16 [tokens, H], W the
+ * router weight ffn_gate_inp f32 or bf16 [E, H], H % 4 == 0), then qmm_moe_topk on them. logits is the caller's
+ * buffer and holds the logits afterwards. info (i32 [tokens, 4]) or NULL: tokens with info[t, 2] == 0 are padding
+ * of the epoch (_live) and get no ids or weights (qmm_moe_bucket with the same info never reads them). */
+int qmm_moe_route(int64_t tokens, int64_t H, int E, int KU, int gating, int norm, float scale, const void *x,
+                  int x_dtype, const void *w, int w_dtype, const float *bias, const int32_t *info, float *logits,
+                  int32_t *ids, float *wts, qmm_stream_t stream);
+
+/* Shared-expert gate, g_moe_shared_gate (S/gen_moe.py:780-823): sg f32 [tokens] = sigmoid(x[t] . w), x f32 or bf16
+ * [tokens, H], w (ffn_gate_inp_shexp) f32 or bf16 [H], H % 4 == 0, fp32 accumulation. */
+int qmm_moe_shared_gate(int64_t tokens, int64_t H, const void *x, int x_dtype, const void *w, int w_dtype, float *sg,
+                        qmm_stream_t stream);
+
+/* Per-expert output scale folded into the combine weights, g_moe_wscale (S/gen_moe.py:1010-1045; ffn_down_exps.scale):
+ * wts[t, k] *= scale[clamp(ids[t, k], 0, E - 1)]. ids i32 / wts f32 [tokens, KU], scale f32 [E]. */
+int qmm_moe_wscale(int64_t tokens, int KU, int E, const int32_t *ids, const float *scale, float *wts,
+                   qmm_stream_t stream);
+
 /* MoE bucket / permute, g_moe_bucket (S/gen_moe.py:829-955; scratch sizes S/gen_llm.py:5388-5432):
  * assignments a = t*KU + k of live tokens (info[t, 2] != 0; info i32 [tokens, 4] or NULL = all live) grouped by
  * expert into 64-row tiles in expert-id order, assignments in ascending a inside each expert's segment.
@@ -152,8 +171,8 @@ int qmm_moe_expert_mv_split(int mode, int fused, int act, int64_t k, int64_t n, 
 
 /* Grouped expert GEMM over bucketed rows, g_moe_ggu_{fmt}[_fused]_k{H} / g_moe_gdn_{fmt}_k{FE}
  * (S/gen_moe.py:1126-1228; launch args S/gen_llm.py:5376-5378):
- *   gu (mode 0): act[r] = act_fn(Wg[e] x[rowmap[r]/KU] inv, Wu[e] x[rowmap[r]/KU] inv)     (x rows gathered)
- *   dn (mode 1): ys[r]  = Wd[e] x[r] inv                                                   (x rows sorted)
+ *   gu (mode 0): act[r] = act_fn(Wg[e] x[t] inv + bias[e], Wu[e] x[t] inv + bias2[e]),  t = rowmap[r]/KU
+ *   dn (mode 1): ys[r]  = Wd[e] x[r] inv + bias[e]                                      (x rows sorted)
  * for every row r of every 64-row tile whose expert e = tile_info[tile, 0] >= 0; rows with rowmap[r] == -1 are
  * written as zeros, rows of unused tiles are not written. Weights as qmm_moe_expert_mv: w [E, n, k] (gu: gate;
  * fused != 0: [E, 2n, k], each expert's n gate rows then its n up rows; w2 the up tensor otherwise).
@@ -166,11 +185,13 @@ int qmm_moe_expert_mv_split(int mode, int fused, int act, int64_t k, int64_t n, 
  *   QMM_MXFP4T: as QMM_MXFP4S with the weights in MFMA-tiled planes from qmm_tile_mxfp4 (each expert's [rows, k]
  *               tiled on its own: n % 32 == 0; a fused gate_up expert tiles as 2n rows); the same results bit for
  *               bit, read as contiguous 1 KB streams (no counterpart in the reference: a load-time layout).
- * x_rows: rows of x (gu: tokens; dn: >= max_tiles * 64). y: f32 [max_tiles * 64, n]. */
+ * x_rows: rows of x (gu: tokens; dn: >= max_tiles * 64). y: f32 [max_tiles * 64, n].
+ * bias / bias2: the per-expert output biases f32 [E, n] (gpt-oss ffn_{gate,up,down}_exps.bias, _gemm_bias_act
+ * S/gen_moe.py:958-1007), added after the row inverse and before the activation; NULL = none (bias2: gu only). */
 int qmm_moe_grouped(int fmt, int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
                     const int32_t *tile_info, const int32_t *rowmap, const void *x, int x_dtype, const void *x_scales,
-                    int64_t x_rows, const void *w, const void *ws, const void *w2, const void *ws2, float *y,
-                    qmm_stream_t stream);
+                    int64_t x_rows, const void *w, const void *ws, const void *w2, const void *ws2, const float *bias,
+                    const float *bias2, float *y, qmm_stream_t stream);
 
 /* The gate/up grouped GEMM (mode 0 of qmm_moe_grouped, MXFP4 weights) with the MXFP8 quantization of its output
  * fused into the epilogue (no reference counterpart: the reference writes act f32 and its next kernel reads it back).
@@ -181,7 +202,8 @@ int qmm_moe_grouped(int fmt, int mode, int fused, int act, int64_t max_tiles, in
 int qmm_moe_grouped_mxfp8(int fmt, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
                           const int32_t *tile_info, const int32_t *rowmap, const void *x, const void *x_scales,
                           int64_t x_rows, const void *w, const void *ws, const void *w2, const void *ws2,
-                          uint8_t *codes, uint8_t *scales, qmm_stream_t stream);
+                          const float *bias, const float *bias2, uint8_t *codes, uint8_t *scales,
+                          qmm_stream_t stream);
 
 /* Row-scaled f16 producer, g_row_scale_f16[_tiles] (S/gen_llm.py:1843-1915, S/gen_moe.py:503-527):
  * per row e = clamp(exponent(max|x|) - 13, 0, 100), x16 = f16(x * 2^-e), scales = (2^-e, 2^e).
@@ -234,6 +256,12 @@ int64_t qmm_mxfp4t_scale_bytes(int64_t rows, int64_t k);
  * ys f32 [rows, H]; wts f32 [tokens, KU]; y f32 [tokens, H]. */
 int qmm_moe_combine(int64_t tokens, int64_t rows, int64_t H, int KU, const float *ys, const int32_t *pos,
                     const float *wts, int accumulate, float *y, qmm_stream_t stream);
+
+/* The combine of a layer with gated shared experts, shared_gated (S/gen_moe.py:765-779): y[t] holds the shared
+ * experts' output, y[t] = sg[t] y[t] + sum_k w[t,k] ys[row(t,k)] (the product first, then the fma chain in k
+ * order). sg f32 [tokens] from qmm_moe_shared_gate; other arguments as qmm_moe_combine. */
+int qmm_moe_combine_gated(int64_t tokens, int64_t rows, int64_t H, int KU, const float *ys, const int32_t *pos,
+                          const float *wts, const float *sg, float *y, qmm_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -2,12 +2,13 @@
 // grouped expert GEMMs g_moe_ggu_q4_k[_fused]_k{H} / g_moe_gdn_q4_k_k{FE} (S/gen_moe.py:1126-1228).
 //
 //   dense   Y[r, c]   = (acc ? Y[r, c] : 0) + inv[r] sum_k X16[r, k] W[c, k]
-//   gu      act[r, c] = act_fn(inv[t] sum_k X16[t, k] Wg[e][c, k], inv[t] sum_k X16[t, k] Wu[e][c, k]),
-//                       t = rowmap[r] / KU  (rows gathered from the token rows)
-//   dn      ys[r, c]  = inv[r] sum_k A16[r, k] Wd[e][c, k]                       (rows already sorted)
+//   gu      act[r, c] = act_fn(inv[t] sum_k X16[t, k] Wg[e][c, k] + bg[e, c], inv[t] sum_k X16[t, k] Wu[e][c, k]
+//                       + bu[e, c]),  t = rowmap[r] / KU  (rows gathered from the token rows)
+//   dn      ys[r, c]  = inv[r] sum_k A16[r, k] Wd[e][c, k] + bd[e, c]            (rows already sorted)
 //
 // for every row r of every 64-row tile whose expert e = tile_info[tile, 0] >= 0; rows with rowmap[r] < 0 are
-// written as zeros. X16 / A16 are the row-scaled f16 operands the reference's g_row_scale_f16[_tiles] produces
+// written as zeros. The optional expert biases (gpt-oss ffn_{gate,up,down}_exps.bias) are added after the row
+// inverse, before the activation (_gemm_bias_act, S/gen_moe.py:958-1007). X16 / A16 are the row-scaled f16 operands the reference's g_row_scale_f16[_tiles] produces
 // (S/gen_llm.py:1843-1915, S/gen_moe.py:503-527) and inv = their scales[row, 1]. W is Q4_K, dequantized to f16 in
 // registers the way the reference stages it (S/gen_gemm.py:499-530): w = fma_f16(f16(q), f16(d sc), f16(-dmin m)).
 // fp32 accumulation throughout.
@@ -98,6 +99,7 @@ struct Args {
   int64_t ebytes;              // bytes of one expert's matrix (grouped)
   int64_t up_off;              // gu: byte offset of the up matrix from the gate matrix of an expert (fused)
   const int32_t *tile_info, *rowmap;
+  const float *bias, *bias2;   // grouped: per-expert output biases [E, N] (gu: gate, up; dn: bias only) or NULL
   int KU, E, act;
   void *y;
   int tiles_m, n_blocks, tiles_total;
@@ -420,8 +422,14 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
           float v = 0.f;
           if (src >= 0) {
             const float inv = rinv[lr];
-            if constexpr (KIND == kGU) v = act_fn(a.act, acc[i][j][r] * inv, red_at(0, i, j, r) * inv);
-            else v = acc[i][j][r] * inv;
+            const int64_t bo = (int64_t)expert * N + col;
+            const float b = a.bias ? a.bias[bo] : 0.f;
+            if constexpr (KIND == kGU) {
+              const float b2 = a.bias2 ? a.bias2[bo] : 0.f;
+              v = act_fn(a.act, acc[i][j][r] * inv + b, red_at(0, i, j, r) * inv + b2);
+            } else {
+              v = acc[i][j][r] * inv + b;
+            }
           }
           yf[o] = v;
         }
@@ -486,7 +494,8 @@ extern "C" int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, c
 // The Q4_K path of qmm_moe_grouped (grouped.hip checks the arguments shared with the MXFP4 path).
 int qmm_grouped_q4k(int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
                     const int32_t *tile_info, const int32_t *rowmap, const void *x, const float *x_scales,
-                    int64_t x_rows, const void *w, const void *w2, float *y, hipStream_t s) {
+                    int64_t x_rows, const void *w, const void *w2, const float *bias, const float *bias2, float *y,
+                    hipStream_t s) {
   if (k % 256) return QMM_ERR_SHAPE;
   if (x_rows * k * 2 >= (1ll << 31)) return QMM_ERR_SHAPE;   // activation rows are addressed by a 32-bit buffer offset
   if (!aligned(x, 16) || !aligned(w, 16) || (w2 && !aligned(w2, 16))) return QMM_ERR_ALIGN;
@@ -495,6 +504,7 @@ int qmm_grouped_q4k(int mode, int fused, int act, int64_t max_tiles, int64_t k, 
   a.M = (int)(max_tiles * BM); a.N = (int)n; a.K = (int)k;
   a.x16 = static_cast<const _Float16 *>(x); a.scales = x_scales; a.x_rows = (int)x_rows;
   a.tile_info = tile_info; a.rowmap = rowmap; a.KU = KU; a.E = E; a.act = act; a.y = y;
+  a.bias = bias; a.bias2 = mode == 0 ? bias2 : nullptr;
   a.w = static_cast<const u8 *>(w);
   if (mode == 0) {
     if (!fused && !w2) return QMM_ERR_NULL;

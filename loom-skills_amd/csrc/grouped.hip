@@ -4,16 +4,18 @@
 
 int qmm_grouped_q4k(int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
                     const int32_t *tile_info, const int32_t *rowmap, const void *x, const float *x_scales,
-                    int64_t x_rows, const void *w, const void *w2, float *y, hipStream_t s);
+                    int64_t x_rows, const void *w, const void *w2, const float *bias, const float *bias2, float *y,
+                    hipStream_t s);
 int qmm_grouped_mxfp4(int tiled, int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
                       const int32_t *tile_info, const int32_t *rowmap, const void *x, const void *x_scales,
-                      int64_t x_rows, const void *w, const void *ws, const void *w2, const void *ws2, float *y,
-                      uint8_t *y8, uint8_t *ys8, hipStream_t s);
+                      int64_t x_rows, const void *w, const void *ws, const void *w2, const void *ws2,
+                      const float *bias, const float *bias2, float *y, uint8_t *y8, uint8_t *ys8, hipStream_t s);
 
 extern "C" int qmm_moe_grouped(int fmt, int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E,
                                int KU, const int32_t *tile_info, const int32_t *rowmap, const void *x, int x_dtype,
                                const void *x_scales, int64_t x_rows, const void *w, const void *ws, const void *w2,
-                               const void *ws2, float *y, qmm_stream_t stream) {
+                               const void *ws2, const float *bias, const float *bias2, float *y,
+                               qmm_stream_t stream) {
   using namespace qmm;
   if (fmt != QMM_Q4_K && fmt != QMM_MXFP4S && fmt != QMM_MXFP4T) return QMM_ERR_FORMAT;
   if (mode != 0 && mode != 1) return QMM_ERR_RANGE;
@@ -23,23 +25,23 @@ extern "C" int qmm_moe_grouped(int fmt, int mode, int fused, int act, int64_t ma
   if (max_tiles <= 0 || max_tiles > (1 << 18) || k <= 0 || n <= 0 || k > (1 << 20) || n > (1 << 20))
     return QMM_ERR_SHAPE;
   if (x_rows <= 0 || (mode == 1 && x_rows < max_tiles * 64)) return QMM_ERR_SHAPE;
-  if (!aligned(y, 4)) return QMM_ERR_ALIGN;
+  if (!aligned(y, 4) || !aligned(bias, 4) || !aligned(bias2, 4)) return QMM_ERR_ALIGN;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (fmt == QMM_Q4_K) {
     if (x_dtype != QMM_F16) return QMM_ERR_DTYPE;
     return qmm_grouped_q4k(mode, fused, act, max_tiles, k, n, E, KU, tile_info, rowmap, x,
-                           static_cast<const float *>(x_scales), x_rows, w, w2, y, s);
+                           static_cast<const float *>(x_scales), x_rows, w, w2, bias, bias2, y, s);
   }
   if (x_dtype != QMM_MXFP8) return QMM_ERR_DTYPE;
   return qmm_grouped_mxfp4(fmt == QMM_MXFP4T, mode, fused, act, max_tiles, k, n, E, KU, tile_info, rowmap, x,
-                           x_scales, x_rows, w, ws, w2, ws2, y, nullptr, nullptr, s);
+                           x_scales, x_rows, w, ws, w2, ws2, bias, bias2, y, nullptr, nullptr, s);
 }
 
 extern "C" int qmm_moe_grouped_mxfp8(int fmt, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E,
                                      int KU, const int32_t *tile_info, const int32_t *rowmap, const void *x,
                                      const void *x_scales, int64_t x_rows, const void *w, const void *ws,
-                                     const void *w2, const void *ws2, uint8_t *codes, uint8_t *scales,
-                                     qmm_stream_t stream) {
+                                     const void *w2, const void *ws2, const float *bias, const float *bias2,
+                                     uint8_t *codes, uint8_t *scales, qmm_stream_t stream) {
   using namespace qmm;
   if (fmt != QMM_MXFP4S && fmt != QMM_MXFP4T) return QMM_ERR_FORMAT;
   if (act != QMM_ACT_SILU && act != QMM_ACT_SWIGLU_OAI) return QMM_ERR_RANGE;
@@ -48,6 +50,8 @@ extern "C" int qmm_moe_grouped_mxfp8(int fmt, int fused, int act, int64_t max_ti
   if (max_tiles <= 0 || max_tiles > (1 << 18) || k <= 0 || n <= 0 || k > (1 << 20) || n > (1 << 20) || n % 32)
     return QMM_ERR_SHAPE;
   if (x_rows <= 0) return QMM_ERR_SHAPE;
+  if (!aligned(bias, 4) || !aligned(bias2, 4)) return QMM_ERR_ALIGN;
   return qmm_grouped_mxfp4(fmt == QMM_MXFP4T, 0, fused, act, max_tiles, k, n, E, KU, tile_info, rowmap, x, x_scales,
-                           x_rows, w, ws, w2, ws2, nullptr, codes, scales, reinterpret_cast<hipStream_t>(stream));
+                           x_rows, w, ws, w2, ws2, bias, bias2, nullptr, codes, scales,
+                           reinterpret_cast<hipStream_t>(stream));
 }

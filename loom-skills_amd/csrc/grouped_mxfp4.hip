@@ -2,11 +2,12 @@
 // kernels of the reference's MoE prefill chain (S/gen_moe.py:1126-1228; its fp8 MXFP4 GEMM, S/gen_mxfp4s.py:1-21,
 // is the gfx12 WMMA counterpart):
 //
-//   gu   act[r, c] = act_fn(sum_k X8[t, k] Wg[e][c, k], sum_k X8[t, k] Wu[e][c, k]),  t = rowmap[r] / KU
-//   dn   ys[r, c]  = sum_k A8[r, k] Wd[e][c, k]                                        (rows already sorted)
+//   gu   act[r, c] = act_fn(sum_k X8[t, k] Wg[e][c, k] + bg[e, c], sum_k X8[t, k] Wu[e][c, k] + bu[e, c]),
+//                    t = rowmap[r] / KU
+//   dn   ys[r, c]  = sum_k A8[r, k] Wd[e][c, k] + bd[e, c]                             (rows already sorted)
 //
 // for every row r of every 64-row tile with expert e = tile_info[tile, 0] >= 0 (rows with rowmap[r] < 0 are written
-// as zeros). W is MXFP4 in split planes: nibbles [E, rows, K/2] ("pairs": byte j holds elements 2j, 2j+1) and
+// as zeros); the expert biases are optional (gpt-oss, S/gen_moe.py:958-1007). W is MXFP4 in split planes: nibbles [E, rows, K/2] ("pairs": byte j holds elements 2j, 2j+1) and
 // E8M0 scales [E, rows, K/32]. X8 / A8 are MXFP8 activations from qmm_quant_mxfp8: E4M3 codes [rows, K] with one
 // E8M0 scale per 32 values along K. fp32 accumulation.
 //
@@ -81,6 +82,7 @@ struct MArgs {
   int64_t nib_ebytes, sc_ebytes;   // bytes of one expert's nibble / scale plane
   int64_t up_nib_off, up_sc_off;   // fused gu: offset of the up rows inside an expert
   const int32_t *tile_info, *rowmap;
+  const float *bias, *bias2;       // per-expert output biases [E, N] (gu: gate, up; dn: bias only) or NULL
   int KU, E, act;
   float *y;
   u8 *y8, *ys8;                    // kGU8: E4M3 codes [rows, N] and E8M0 scales [rows, N/32] of the activation
@@ -368,12 +370,14 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
     static_assert(sizeof(As) >= BM * (BN + 16) + BM * 4, "epilogue staging");
     u8 *Ot = &As[0][0][0];                    // [64][BN + 16] codes
     u8 *Osc = Ot + BM * (BN + 16);            // [64][4] scale bytes
+    const int64_t bo = (int64_t)expert * N + (col < N ? col : N - 1);
+    const float bg = a.bias ? a.bias[bo] : 0.f, bu = a.bias2 ? a.bias2[bo] : 0.f;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int lr = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-        const float v = src_row[lr] >= 0 ? act_fn(a.act, acc[i][0][r], acc[i][1][r]) : 0.f;
+        const float v = src_row[lr] >= 0 ? act_fn(a.act, acc[i][0][r] + bg, acc[i][1][r] + bu) : 0.f;
         float m = fabsf(v);
         m = fmaxf(m, xshfl<1>(m));
         m = fmaxf(m, xshfl<2>(m));
@@ -399,6 +403,8 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
     return;
   }
   if (col >= N) return;
+  const float bg = a.bias ? a.bias[(int64_t)expert * N + col] : 0.f;
+  const float bu = (GU && a.bias2) ? a.bias2[(int64_t)expert * N + col] : 0.f;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -406,8 +412,8 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
       const int lr = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
       float v = 0.f;
       if (src_row[lr] >= 0) {
-        if constexpr (GU) v = act_fn(a.act, acc[i][0][r], acc[i][1][r]);
-        else v = acc[i][0][r];
+        if constexpr (GU) v = act_fn(a.act, acc[i][0][r] + bg, acc[i][1][r] + bu);
+        else v = acc[i][0][r] + bg;
       }
       a.y[(int64_t)(m0 + lr) * N + col] = v;
     }
@@ -500,8 +506,8 @@ int64_t qmm_mxfp4t_scale_bytes(int64_t rows, int64_t k) {
 // The MXFP4 paths of qmm_moe_grouped: split planes (tiled = 0) or MFMA-tiled planes (tiled = 1).
 int qmm_grouped_mxfp4(int tiled, int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
                       const int32_t *tile_info, const int32_t *rowmap, const void *x, const void *x_scales,
-                      int64_t x_rows, const void *w, const void *ws, const void *w2, const void *ws2, float *y,
-                      uint8_t *y8, uint8_t *ys8, hipStream_t s) {
+                      int64_t x_rows, const void *w, const void *ws, const void *w2, const void *ws2,
+                      const float *bias, const float *bias2, float *y, uint8_t *y8, uint8_t *ys8, hipStream_t s) {
   if (k % 64 || k > 12288) return QMM_ERR_SHAPE;   // the workgroup stages (64 + 256) x K / 32 scale bytes in LDS
   if (tiled && n % 32) return QMM_ERR_SHAPE;       // tiled planes hold whole 32-row blocks
   if (x_rows * k >= (1ll << 31)) return QMM_ERR_SHAPE;   // activation rows are addressed by a 32-bit buffer offset
@@ -517,6 +523,7 @@ int qmm_grouped_mxfp4(int tiled, int mode, int fused, int act, int64_t max_tiles
   a.x8 = static_cast<const u8 *>(x); a.xs = static_cast<const u8 *>(x_scales); a.x_rows = (int)x_rows;
   a.wn = static_cast<const u8 *>(w); a.wsc = static_cast<const u8 *>(ws);
   a.tile_info = tile_info; a.rowmap = rowmap; a.KU = KU; a.E = E; a.act = act; a.y = y; a.y8 = y8; a.ys8 = ys8;
+  a.bias = bias; a.bias2 = mode == 0 ? bias2 : nullptr;
   a.n_blocks = (int)((n + 127) / 128);
   a.max_tiles = (int)max_tiles;
   const int64_t nrow = k / 2;                                        // nibble bytes per row (both layouts)

@@ -1,9 +1,13 @@
 // MoE routing, permutation and combine, plus the activation producers of the grouped GEMMs.
 //
 //   qmm_moe_topk       top-k of router logits + gating weights      g_moe_route[_tr], S/gen_moe.py:116-500
+//   qmm_moe_route      router matvec x W_router^T, then qmm_moe_topk g_moe_route[_tr][_live], S/gen_moe.py:116-500
+//   qmm_moe_shared_gate sg[t] = sigmoid(x[t] . w)                   g_moe_shared_gate, S/gen_moe.py:780-823
+//   qmm_moe_wscale     wts[t, k] *= scale[ids[t, k]]                g_moe_wscale, S/gen_moe.py:1010-1045
 //   qmm_moe_bucket     canonical bucket of assignments into 64-row expert tiles
 //                                                                    g_moe_bucket, S/gen_moe.py:829-955
 //   qmm_moe_combine    y[t] (+)= sum_k w[t,k] ys[row(t,k)]           g_moe_combine[_sorted], S/gen_moe.py:730-762, :1231-1280
+//   qmm_moe_combine_gated  y[t] = sg[t] y[t] + sum_k ...             shared_gated combine, S/gen_moe.py:765-779
 //   qmm_row_scale_f16  per-row power-of-two scale + f16 copy         g_row_scale_f16[_tiles], S/gen_llm.py:1843-1915
 //   qmm_quant_mxfp8    E4M3 + E8M0-per-32 operand of the scaled MFMA
 //   qmm_repack_mxfp4   GGUF 17-byte MXFP4 blocks -> split planes
@@ -28,11 +32,13 @@ constexpr int kTopkMaxE = 256;
 
 __global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ logits, int64_t tokens, int E, int KU,
                                                    int gating, int norm, float scale, const float *__restrict__ bias,
-                                                   int32_t *__restrict__ ids, float *__restrict__ wts) {
+                                                   const int32_t *__restrict__ info, int32_t *__restrict__ ids,
+                                                   float *__restrict__ wts) {
   __shared__ __align__(16) float score[4][kTopkMaxE];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int64_t t = (int64_t)blockIdx.x * 4 + wv;
   if (t >= tokens) return;               // a whole wave: nothing below synchronizes the workgroup
+  if (info && info[4 * t + 2] == 0) return;   // a padding token of the epoch (_live): no ids, no weights
   const float *lg = logits + t * E;
   float l[4], sel[4];
   bool in[4];
@@ -88,6 +94,71 @@ __global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ log
       ids[t * KU + rank[i]] = lane + 64 * i;
       wts[t * KU + rank[i]] = (norm ? w[i] / nden : w[i]) * scale;
     }
+}
+
+// ------------------------------------------------------------------------------------------------ router
+// out[t, e] = sum_k x[t, k] W[e, k] with fp32 accumulation: the router matvec of g_moe_route[_tr] (S/gen_moe.py:
+// 116-252, :255-460) and, with one row and the sigmoid, g_moe_shared_gate (S/gen_moe.py:780-823). One wave per
+// (row e, group of kRouteTok tokens), row fastest so the waves of a token group share its x rows in L2; lane l
+// reads the 4-value chunks l, l + 64, ... of the row (one 1 KB contiguous piece per wave load for f32 weights)
+// and the same chunks of each token's x. The lane sums its chunks in order, then the butterfly sums the lanes.
+constexpr int kRouteTok = 8;
+
+template <bool BF>
+__device__ __forceinline__ f32x4 load4(const void *p, int64_t i4) {
+  if constexpr (BF) {
+    const uint2 q = reinterpret_cast<const uint2 *>(p)[i4];
+    return f32x4{bf16_to_f32(q.x & 0xFFFFu), bf16_to_f32(q.x >> 16), bf16_to_f32(q.y & 0xFFFFu),
+                 bf16_to_f32(q.y >> 16)};
+  } else {
+    return reinterpret_cast<const f32x4 *>(p)[i4];
+  }
+}
+
+template <bool XBF, bool WBF>
+__global__ __launch_bounds__(256) void router_kernel(int64_t tokens, int64_t H, int E, const void *__restrict__ x,
+                                                     const void *__restrict__ w, int sigmoid, float *__restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int e = (int)(gw % E);
+  const int64_t t0 = gw / E * kRouteTok;
+  if (t0 >= tokens) return;
+  const int64_t C = H / 4;                 // 4-value chunks of a row
+  int64_t xrow[kRouteTok];
+#pragma unroll
+  for (int r = 0; r < kRouteTok; ++r) xrow[r] = (t0 + r < tokens ? t0 + r : tokens - 1) * C;   // tail: reread
+  float acc[kRouteTok];
+#pragma unroll
+  for (int r = 0; r < kRouteTok; ++r) acc[r] = 0.f;
+  const int64_t wrow = (int64_t)e * C;
+#pragma unroll 2
+  for (int64_t c = lane; c < C; c += 64) {
+    const f32x4 wv = load4<WBF>(w, wrow + c);
+#pragma unroll
+    for (int r = 0; r < kRouteTok; ++r) {
+      const f32x4 xv = load4<XBF>(x, xrow[r] + c);
+      acc[r] = __builtin_fmaf(wv.x, xv.x, acc[r]);
+      acc[r] = __builtin_fmaf(wv.y, xv.y, acc[r]);
+      acc[r] = __builtin_fmaf(wv.z, xv.z, acc[r]);
+      acc[r] = __builtin_fmaf(wv.w, xv.w, acc[r]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kRouteTok; ++r) {
+    const float v = wave_sum(acc[r]);
+    if (lane == 0 && t0 + r < tokens) out[(t0 + r) * E + e] = sigmoid ? 1.f / (1.f + expf(-v)) : v;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ wscale
+// wts[a] *= scale[clamp(ids[a], 0, E - 1)] (g_moe_wscale: a per-expert output scale folded into the combine weights)
+__global__ __launch_bounds__(256) void wscale_kernel(int64_t n, int E, const int32_t *__restrict__ ids,
+                                                     const float *__restrict__ scale, float *__restrict__ wts) {
+  const int64_t a = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (a >= n) return;
+  int e = ids[a];
+  e = e < 0 ? 0 : (e >= E ? E - 1 : e);
+  wts[a] = wts[a] * scale[e];
 }
 
 // ------------------------------------------------------------------------------------------------ bucket
@@ -213,7 +284,7 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(int64_t tokens, 
 __global__ __launch_bounds__(256) void combine_kernel(int64_t tokens, int64_t rows, int64_t H, int KU,
                                                       const float *__restrict__ ys, const int32_t *__restrict__ pos,
                                                       const float *__restrict__ wts, int accumulate,
-                                                      float *__restrict__ y) {
+                                                      const float *__restrict__ sg, float *__restrict__ y) {
   const int64_t t = blockIdx.x;
   int64_t row[8];
   float w[8];
@@ -221,8 +292,9 @@ __global__ __launch_bounds__(256) void combine_kernel(int64_t tokens, int64_t ro
     row[k] = pos ? pos[t * KU + k] : t * KU + k;
     w[k] = wts[t * KU + k];
   }
+  const float g = sg ? sg[t] : 1.f;
   for (int64_t c = threadIdx.x; c < H; c += blockDim.x) {
-    float acc = accumulate ? y[t * H + c] : 0.f;
+    float acc = accumulate ? (sg ? y[t * H + c] * g : y[t * H + c]) : 0.f;
     for (int k = 0; k < KU; ++k) {
       const float v = (row[k] >= 0 && row[k] < rows) ? ys[row[k] * H + c] : 0.f;
       acc = __builtin_fmaf(w[k], v, acc);
@@ -240,7 +312,7 @@ __global__ __launch_bounds__(256) void combine_kernel(int64_t tokens, int64_t ro
 __global__ __launch_bounds__(256) void combine_vec_kernel(int64_t tokens, int64_t rows, int64_t H, int KU,
                                                           const float *__restrict__ ys, const int32_t *__restrict__ pos,
                                                           const float *__restrict__ wts, int accumulate,
-                                                          float *__restrict__ y) {
+                                                          const float *__restrict__ sg, float *__restrict__ y) {
   const int64_t t = blockIdx.y;
   const int64_t c4 = (int64_t)blockIdx.x * 256 + threadIdx.x;   // float4 index within the row
   if (c4 * 4 >= H) return;
@@ -258,6 +330,11 @@ __global__ __launch_bounds__(256) void combine_vec_kernel(int64_t tokens, int64_
   for (int k = 0; k < 8; ++k)
     if (k < KU) v[k] = (row[k] >= 0 && row[k] < rows) ? reinterpret_cast<const f32x4 *>(ys + row[k] * H)[c4] : f32x4{0.f, 0.f, 0.f, 0.f};
   f32x4 acc = accumulate ? reinterpret_cast<const f32x4 *>(y + t * H)[c4] : f32x4{0.f, 0.f, 0.f, 0.f};
+  if (sg) {                                // the shared experts' output in y, scaled by the token's gate first
+    const float g = sg[t];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = acc[j] * g;
+  }
 #pragma unroll
   for (int k = 0; k < 8; ++k)
     if (k < KU) {
@@ -462,7 +539,58 @@ int qmm_moe_topk(const float *logits, int64_t tokens, int E, int KU, int gating,
   if (gating < 1 || gating > 3 || (gating == 1 && bias)) return QMM_ERR_RANGE;
   if (tokens <= 0 || tokens > (1ll << 24)) return QMM_ERR_SHAPE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  topk_kernel<<<(unsigned)((tokens + 3) / 4), 256, 0, s>>>(logits, tokens, E, KU, gating, norm, scale, bias, ids, wts);
+  topk_kernel<<<(unsigned)((tokens + 3) / 4), 256, 0, s>>>(logits, tokens, E, KU, gating, norm, scale, bias, nullptr,
+                                                            ids, wts);
+  return launch_status();
+}
+
+static int router(int64_t tokens, int64_t H, int E, const void *x, int x_dtype, const void *w, int w_dtype,
+                  int sigmoid, float *out, hipStream_t s) {
+  if (x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
+  if (w_dtype != QMM_F32 && w_dtype != QMM_BF16) return QMM_ERR_DTYPE;
+  if (H <= 0 || H % 4 || H > (1 << 20)) return QMM_ERR_SHAPE;
+  const bool xb = x_dtype == QMM_BF16, wb = w_dtype == QMM_BF16;
+  if (!aligned(x, xb ? 8 : 16) || !aligned(w, wb ? 8 : 16) || !aligned(out, 4)) return QMM_ERR_ALIGN;
+  const int64_t waves = (int64_t)E * ((tokens + kRouteTok - 1) / kRouteTok);
+  const unsigned grid = (unsigned)((waves + 3) / 4);
+  if (xb) {
+    if (wb) router_kernel<true, true><<<grid, 256, 0, s>>>(tokens, H, E, x, w, sigmoid, out);
+    else router_kernel<true, false><<<grid, 256, 0, s>>>(tokens, H, E, x, w, sigmoid, out);
+  } else {
+    if (wb) router_kernel<false, true><<<grid, 256, 0, s>>>(tokens, H, E, x, w, sigmoid, out);
+    else router_kernel<false, false><<<grid, 256, 0, s>>>(tokens, H, E, x, w, sigmoid, out);
+  }
+  return launch_status();
+}
+
+int qmm_moe_route(int64_t tokens, int64_t H, int E, int KU, int gating, int norm, float scale, const void *x,
+                  int x_dtype, const void *w, int w_dtype, const float *bias, const int32_t *info, float *logits,
+                  int32_t *ids, float *wts, qmm_stream_t stream) {
+  if (!x || !w || !logits || !ids || !wts) return QMM_ERR_NULL;
+  if (E <= 0 || E > 256 || KU <= 0 || KU > 8 || KU > E) return QMM_ERR_RANGE;
+  if (gating < 1 || gating > 3 || (gating == 1 && bias)) return QMM_ERR_RANGE;
+  if (tokens <= 0 || tokens > (1ll << 24)) return QMM_ERR_SHAPE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (int st = router(tokens, H, E, x, x_dtype, w, w_dtype, 0, logits, s)) return st;
+  topk_kernel<<<(unsigned)((tokens + 3) / 4), 256, 0, s>>>(logits, tokens, E, KU, gating, norm, scale, bias, info,
+                                                            ids, wts);
+  return launch_status();
+}
+
+int qmm_moe_shared_gate(int64_t tokens, int64_t H, const void *x, int x_dtype, const void *w, int w_dtype, float *sg,
+                        qmm_stream_t stream) {
+  if (!x || !w || !sg) return QMM_ERR_NULL;
+  if (tokens <= 0 || tokens > (1ll << 24)) return QMM_ERR_SHAPE;
+  return router(tokens, H, 1, x, x_dtype, w, w_dtype, 1, sg, reinterpret_cast<hipStream_t>(stream));
+}
+
+int qmm_moe_wscale(int64_t tokens, int KU, int E, const int32_t *ids, const float *scale, float *wts,
+                   qmm_stream_t stream) {
+  if (!ids || !scale || !wts) return QMM_ERR_NULL;
+  if (E <= 0 || E > 1024 || KU <= 0 || KU > 8) return QMM_ERR_RANGE;
+  if (tokens <= 0 || tokens > (1ll << 24)) return QMM_ERR_SHAPE;
+  const int64_t n = tokens * KU;
+  wscale_kernel<<<(unsigned)((n + 255) / 256), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(n, E, ids, scale, wts);
   return launch_status();
 }
 
@@ -477,19 +605,30 @@ int qmm_moe_bucket(int64_t tokens, int KU, int E, int64_t max_tiles, const int32
   return launch_status();
 }
 
-int qmm_moe_combine(int64_t tokens, int64_t rows, int64_t H, int KU, const float *ys, const int32_t *pos,
-                    const float *wts, int accumulate, float *y, qmm_stream_t stream) {
+static int combine(int64_t tokens, int64_t rows, int64_t H, int KU, const float *ys, const int32_t *pos,
+                   const float *wts, int accumulate, const float *sg, float *y, qmm_stream_t stream) {
   if (!ys || !wts || !y) return QMM_ERR_NULL;
   if (KU <= 0 || KU > 8) return QMM_ERR_RANGE;
   if (tokens <= 0 || H <= 0 || rows <= 0 || tokens > (1ll << 24)) return QMM_ERR_SHAPE;
   if (!pos && rows < tokens * KU) return QMM_ERR_SHAPE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (H % 4 == 0 && aligned(ys, 16) && aligned(y, 16) && tokens <= 65535)
-    combine_vec_kernel<<<dim3((unsigned)((H / 4 + 255) / 256), (unsigned)tokens), 256, 0, s>>>(tokens, rows, H, KU, ys,
-                                                                                                pos, wts, accumulate, y);
+    combine_vec_kernel<<<dim3((unsigned)((H / 4 + 255) / 256), (unsigned)tokens), 256, 0, s>>>(
+        tokens, rows, H, KU, ys, pos, wts, accumulate, sg, y);
   else
-    combine_kernel<<<(unsigned)tokens, 256, 0, s>>>(tokens, rows, H, KU, ys, pos, wts, accumulate, y);
+    combine_kernel<<<(unsigned)tokens, 256, 0, s>>>(tokens, rows, H, KU, ys, pos, wts, accumulate, sg, y);
   return launch_status();
+}
+
+int qmm_moe_combine(int64_t tokens, int64_t rows, int64_t H, int KU, const float *ys, const int32_t *pos,
+                    const float *wts, int accumulate, float *y, qmm_stream_t stream) {
+  return combine(tokens, rows, H, KU, ys, pos, wts, accumulate, nullptr, y, stream);
+}
+
+int qmm_moe_combine_gated(int64_t tokens, int64_t rows, int64_t H, int KU, const float *ys, const int32_t *pos,
+                          const float *wts, const float *sg, float *y, qmm_stream_t stream) {
+  if (!sg) return QMM_ERR_NULL;
+  return combine(tokens, rows, H, KU, ys, pos, wts, 1, sg, y, stream);
 }
 
 static int row_scale(int64_t rows, int64_t k, const void *x, int x_dtype, float *scales, void *x16,

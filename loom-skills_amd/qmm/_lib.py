@@ -26,9 +26,14 @@ SIGNATURES = {
     "qmm_moe_expert_mv_split": [c_int, c_int, c_int, c_i64, c_i64, c_int, c_int, c_i64, c_vp, c_vp, c_int, c_vp,
                                 c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
     "qmm_moe_grouped": [c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_int, c_vp,
-                        c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
+                        c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
     "qmm_moe_grouped_mxfp8": [c_int, c_int, c_int, c_i64, c_i64, c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_vp,
-                              c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
+                              c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
+    "qmm_moe_route": [c_i64, c_i64, c_int, c_int, c_int, c_int, c_float, c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_vp,
+                      c_vp, c_vp, c_vp],
+    "qmm_moe_shared_gate": [c_i64, c_i64, c_vp, c_int, c_vp, c_int, c_vp, c_vp],
+    "qmm_moe_wscale": [c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_vp],
+    "qmm_moe_combine_gated": [c_i64, c_i64, c_i64, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
     "qmm_row_scale_f16": [c_i64, c_i64, c_vp, c_int, c_vp, c_vp, c_vp, c_vp],
     "qmm_row_scale_f16_live": [c_i64, c_vp, c_i64, c_vp, c_int, c_vp, c_vp, c_vp],
     "qmm_quant_mxfp8": [c_i64, c_i64, c_vp, c_int, c_vp, c_vp, c_vp, c_vp],

@@ -6,12 +6,16 @@ S/ = skills/loom-port-llm/starter/):
     mv                g_mv_{fmt}_k{K}[_t{TG}][_r{R}]          S/gen_llm.py:1159-1378, launch args :1187-1197
     gemm              g_gemm_{fmt}_{store|acc|swiglu}[_m*]    S/gen_gemm.py:535-703, launch args :549-556
     moe_topk          g_moe_route / g_moe_route_tr            S/gen_moe.py:116-500
+    moe_route         the same with the router matvec         S/gen_moe.py:116-500 (+ _live, :474-500)
+    moe_shared_gate   g_moe_shared_gate                       S/gen_moe.py:780-823
+    moe_wscale        g_moe_wscale                            S/gen_moe.py:1010-1045
     moe_bucket        g_moe_bucket                            S/gen_moe.py:829-955
     moe_expert_mv     g_moe_gu_* / g_moe_dn_*                 S/gen_moe.py:535-727
     moe_grouped       g_moe_ggu_* / g_moe_gdn_*               S/gen_moe.py:1126-1228
-    moe_combine       g_moe_combine[_sorted]                  S/gen_moe.py:730-762, :1231-1280
+    moe_combine       g_moe_combine[_sorted] [shared_gated]   S/gen_moe.py:730-779, :1231-1280
     moe_prefill       the prefill chain of moe_routed          S/gen_llm.py:5324-5385 (t >= 64)
     moe_decode        the decode chain of moe_routed           S/gen_llm.py:5324-5385 (t < 64)
+    moe_layer         shared experts + routed experts          moe_layer, S/gen_llm.py:5306-5321
     row_scale_f16     g_row_scale_f16[_tiles]                 S/gen_llm.py:1843-1915, S/gen_moe.py:503-527
     dequant           the @g_<fmt>_values helpers (bit-exact f32 values)
 
@@ -155,6 +159,37 @@ def moe_topk(logits, KU, gating, norm, scale=1.0, bias=None):
     return ids, wts
 
 
+def moe_route(x, w_router, KU, gating, norm, scale=1.0, bias=None, info=None, logits=None):
+    """(ids, wts, logits f32 [T, E]) from the hidden rows x f32 / bf16 [T, H] and the router weight f32 / bf16
+    [E, H]: logits = x W^T, then moe_topk. With info (i32 [T, 4]) padding tokens (info[t, 2] == 0) get no ids."""
+    _dev(x, w_router, bias, info, logits)
+    T, H = x.shape
+    E = w_router.shape[0]
+    logits = torch.empty((T, E), dtype=torch.float32, device=x.device) if logits is None else logits
+    ids = torch.empty((T, KU), dtype=torch.int32, device=x.device)
+    wts = torch.empty((T, KU), dtype=torch.float32, device=x.device)
+    _lib.call("qmm_moe_route", T, H, E, KU, gating, int(bool(norm)), float(scale), _ptr(x), _dt(x), _ptr(w_router),
+              _dt(w_router), _ptr(bias), _ptr(info), _ptr(logits), _ptr(ids), _ptr(wts), _stream())
+    return ids, wts, logits
+
+
+def moe_shared_gate(x, w):
+    """sg f32 [T] = sigmoid(x[t] . w) (the Qwen-MoE shared-expert gate ffn_gate_inp_shexp, w f32 / bf16 [H])."""
+    _dev(x, w)
+    T, H = x.shape
+    sg = torch.empty(T, dtype=torch.float32, device=x.device)
+    _lib.call("qmm_moe_shared_gate", T, H, _ptr(x), _dt(x), _ptr(w), _dt(w), _ptr(sg), _stream())
+    return sg
+
+
+def moe_wscale(ids, wts, scale):
+    """wts[t, k] *= scale[clamp(ids[t, k], 0, E - 1)] in place (ffn_down_exps.scale folded into the weights)."""
+    _dev(ids, wts, scale)
+    T, KU = ids.shape
+    _lib.call("qmm_moe_wscale", T, KU, scale.shape[0], _ptr(ids), _ptr(scale), _ptr(wts), _stream())
+    return wts
+
+
 def max_tiles(tokens, KU, E):
     """Worst-case bucketed tiles: T*KU/64 + E (S/gen_llm.py:5407-5411)."""
     return tokens * KU // TILE + E
@@ -193,40 +228,48 @@ def moe_expert_mv(fmt, mode, ids, x, w, n, k, E, KU, w2=None, ws=None, ws2=None,
 
 
 def moe_grouped(fmt, mode, tile_info, rowmap, x, w, n, k, E, KU, w2=None, ws=None, ws2=None, x_scales=None,
-                fused=False, act="silu", y=None):
+                fused=False, act="silu", y=None, bias=None, bias2=None):
     """Grouped expert GEMM over bucketed 64-row tiles (include/qmm.h, qmm_moe_grouped).
     q4_k: x f16 row-scaled rows with x_scales f32 [rows, 2] (row_scale_f16); mxfp4s: x E4M3 codes uint8 [rows, k]
-    with x_scales uint8 [rows, k/64] (quant_mxfp8). y: f32 [max_tiles * 64, n]."""
-    _dev(tile_info, rowmap, x, w, w2, ws, ws2, x_scales, y)
+    with x_scales uint8 [rows, k/64] (quant_mxfp8). y: f32 [max_tiles * 64, n]. bias / bias2: per-expert output
+    biases f32 [E, n] (gu: gate and up; dn: bias)."""
+    _dev(tile_info, rowmap, x, w, w2, ws, ws2, x_scales, y, bias, bias2)
     n_tiles = tile_info.shape[0]
     y = torch.empty((n_tiles * TILE, n), dtype=torch.float32, device=x.device) if y is None else y
     xd = DTYPE["mxfp8"] if x.dtype == torch.uint8 else _dt(x)
     _lib.call("qmm_moe_grouped", CODE[fmt], {"gu": 0, "dn": 1}[mode], int(fused), ACT[act], n_tiles, k, n, E, KU,
               _ptr(tile_info), _ptr(rowmap), _ptr(x), xd, _ptr(x_scales), x.shape[0], _ptr(w), _ptr(ws), _ptr(w2),
-              _ptr(ws2), _ptr(y), _stream())
+              _ptr(ws2), _ptr(bias), _ptr(bias2), _ptr(y), _stream())
     return y
 
 
 def moe_grouped_mxfp8(fmt, tile_info, rowmap, x, w, n, k, E, KU, w2=None, ws=None, ws2=None, x_scales=None,
-                      fused=False, act="silu", codes=None, scales=None):
+                      fused=False, act="silu", codes=None, scales=None, bias=None, bias2=None):
     """The MXFP4 gate/up grouped GEMM with its activation quantized to MXFP8 in the epilogue: (codes u8
     [max_tiles*64, n], scales u8 [max_tiles*64, n/32]) == quant_mxfp8(moe_grouped(fmt, "gu", ...), tile_info) bit
     for bit. x: E4M3 codes with x_scales (quant_mxfp8)."""
-    _dev(tile_info, rowmap, x, w, w2, ws, ws2, x_scales, codes, scales)
+    _dev(tile_info, rowmap, x, w, w2, ws, ws2, x_scales, codes, scales, bias, bias2)
     rows = tile_info.shape[0] * TILE
     codes = torch.empty((rows, n), dtype=torch.uint8, device=x.device) if codes is None else codes
     scales = torch.empty((rows, n // MX_BLOCK), dtype=torch.uint8, device=x.device) if scales is None else scales
     _lib.call("qmm_moe_grouped_mxfp8", CODE[fmt], int(fused), ACT[act], tile_info.shape[0], k, n, E, KU,
               _ptr(tile_info), _ptr(rowmap), _ptr(x), _ptr(x_scales), x.shape[0], _ptr(w), _ptr(ws), _ptr(w2),
-              _ptr(ws2), _ptr(codes), _ptr(scales), _stream())
+              _ptr(ws2), _ptr(bias), _ptr(bias2), _ptr(codes), _ptr(scales), _stream())
     return codes, scales
 
 
-def moe_combine(ys, wts, pos=None, y=None, accumulate=False):
-    """y[t] (+)= sum_k w[t, k] ys[row(t, k)], row = pos[t*KU + k] (sorted rows) or t*KU + k."""
-    _dev(ys, wts, pos, y)
+def moe_combine(ys, wts, pos=None, y=None, accumulate=False, sg=None):
+    """y[t] (+)= sum_k w[t, k] ys[row(t, k)], row = pos[t*KU + k] (sorted rows) or t*KU + k. With sg (f32 [T], the
+    shared-expert gate) y holds the shared experts' output and becomes sg[t] y[t] + sum_k ..."""
+    _dev(ys, wts, pos, y, sg)
     T, KU = wts.shape
     H = ys.shape[1]
+    if sg is not None:
+        if y is None:
+            raise ValueError("the gated combine scales the shared experts' output already in y")
+        _lib.call("qmm_moe_combine_gated", T, ys.shape[0], H, KU, _ptr(ys), _ptr(pos), _ptr(wts), _ptr(sg), _ptr(y),
+                  _stream())
+        return y
     y = torch.empty((T, H), dtype=torch.float32, device=ys.device) if y is None else y
     _lib.call("qmm_moe_combine", T, ys.shape[0], H, KU, _ptr(ys), _ptr(pos), _ptr(wts), int(bool(accumulate)),
               _ptr(y), _stream())
@@ -296,45 +339,69 @@ def weight_bytes(fmt, rows, k):
 
 
 # ------------------------------------------------------------------------------------------------ MoE chains
+def _route(x, logits, KU, gating, norm, scale, bias, router, down_scale, info=None):
+    """ids, wts (and the logits) of a chain: from given logits (moe_topk) or from the router weight (moe_route),
+    then the per-expert down scales folded into the weights (g_moe_wscale)."""
+    if (logits is None) == (router is None):
+        raise ValueError("give the router logits or the router weight, one of them")
+    if logits is None:
+        ids, wts, logits = moe_route(x, router, KU, gating, norm, scale=scale, bias=bias, info=info)
+    else:
+        ids, wts = moe_topk(logits, KU, gating, norm, scale=scale, bias=bias)
+    if down_scale is not None:
+        moe_wscale(ids, wts, down_scale)
+    return ids, wts, logits
+
+
 def moe_prefill(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=None, ws_gate=None, ws_down=None,
-                ws_up=None, fused=False, act="silu", scale=1.0, bias=None):
+                ws_up=None, fused=False, act="silu", scale=1.0, bias=None, router=None, expert_bias=None,
+                down_scale=None, y=None, sg=None):
     """The reference's prefill MoE chain (moe_routed with t >= 64, S/gen_llm.py:5324-5385): route, bucket into
     64-row expert tiles, grouped gate/up GEMM with the activation, grouped down GEMM, combine.
-    q4_k: activations row-scaled to f16 (g_row_scale_f16[_tiles]); mxfp4s: quantized to MXFP8.
-    x bf16 / f32 [T, H], logits f32 [T, E]. Returns (y f32 [T, H], intermediates dict)."""
-    ids, wts = moe_topk(logits, KU, gating, norm, scale=scale, bias=bias)
+    q4_k: activations row-scaled to f16 (g_row_scale_f16[_tiles]); mxfp4s / mxfp4t: quantized to MXFP8.
+    x bf16 / f32 [T, H]; logits f32 [T, E], or None with router (the weight f32 / bf16 [E, H]); expert_bias
+    (bg [E, FE], bu [E, FE], bd [E, H]) or None; down_scale f32 [E] or None; y: None (y = routed output), or the
+    shared experts' output the routed output is added to (scaled first by sg, the shared gate, when given).
+    Returns (y f32 [T, H], intermediates dict)."""
+    ids, wts, logits = _route(x, logits, KU, gating, norm, scale, bias, router, down_scale)
+    bg, bu, bd = expert_bias if expert_bias is not None else (None, None, None)
     tile_info, rowmap, pos = moe_bucket(ids, E)
     if fmt == "q4_k":
         x16, xs = row_scale_f16(x)
         a = moe_grouped("q4_k", "gu", tile_info, rowmap, x16, w_gate, FE, H, E, KU, w2=w_up, x_scales=xs,
-                        fused=fused, act=act)
+                        fused=fused, act=act, bias=bg, bias2=bu)
         a16, as_ = row_scale_f16(a, tile_info=tile_info)
-        ys = moe_grouped("q4_k", "dn", tile_info, rowmap, a16, w_down, H, FE, E, KU, x_scales=as_)
+        ys = moe_grouped("q4_k", "dn", tile_info, rowmap, a16, w_down, H, FE, E, KU, x_scales=as_, bias=bd)
     elif fmt in ("mxfp4s", "mxfp4t"):
         # the gate/up GEMM writes its activation as MXFP8 directly (the down GEMM's A operand)
         x8, xs = quant_mxfp8(x)
         a8, as8 = moe_grouped_mxfp8(fmt, tile_info, rowmap, x8, w_gate, FE, H, E, KU, w2=w_up, ws=ws_gate,
-                                    ws2=ws_up, x_scales=xs, fused=fused, act=act)
+                                    ws2=ws_up, x_scales=xs, fused=fused, act=act, bias=bg, bias2=bu)
         a = None
-        ys = moe_grouped(fmt, "dn", tile_info, rowmap, a8, w_down, H, FE, E, KU, ws=ws_down, x_scales=as8)
+        ys = moe_grouped(fmt, "dn", tile_info, rowmap, a8, w_down, H, FE, E, KU, ws=ws_down, x_scales=as8, bias=bd)
     else:
         raise ValueError(f"no grouped path for {fmt}")
-    y = moe_combine(ys, wts, pos=pos)
-    mid = {"ids": ids, "wts": wts, "tile_info": tile_info, "rowmap": rowmap, "pos": pos, "act": a, "ys": ys}
+    y = moe_combine(ys, wts, pos=pos, y=y, accumulate=y is not None, sg=sg)
+    mid = {"ids": ids, "wts": wts, "logits": logits, "tile_info": tile_info, "rowmap": rowmap, "pos": pos, "act": a,
+           "ys": ys}
     if a is None:
         mid.update(act8=a8, act_scales=as8)
     return y, mid
 
 
 def moe_decode(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=None, ws_gate=None, ws_down=None,
-               ws_up=None, fused=False, act="silu", scale=1.0, bias=None):
+               ws_up=None, fused=False, act="silu", scale=1.0, bias=None, router=None, expert_bias=None,
+               down_scale=None, y=None, sg=None):
     """The reference's decode MoE chain (moe_routed with t < 64): route, per-assignment expert matvecs
-    (g_moe_gu_* then g_moe_dn_*), combine in assignment order. Returns (y f32 [T, H], intermediates dict)."""
-    ids, wts = moe_topk(logits, KU, gating, norm, scale=scale, bias=bias)
-    a = moe_expert_mv(fmt, "gu", ids, x, w_gate, FE, H, E, KU, w2=w_up, ws=ws_gate, ws2=ws_up, fused=fused, act=act)
-    ys = moe_expert_mv(fmt, "dn", ids, a, w_down, H, FE, E, KU, ws=ws_down)
-    y = moe_combine(ys, wts)
-    return y, {"ids": ids, "wts": wts, "act": a, "ys": ys}
+    (g_moe_gu_* then g_moe_dn_*), combine in assignment order. Arguments as moe_prefill.
+    Returns (y f32 [T, H], intermediates dict)."""
+    ids, wts, logits = _route(x, logits, KU, gating, norm, scale, bias, router, down_scale)
+    bg, bu, bd = expert_bias if expert_bias is not None else (None, None, None)
+    a = moe_expert_mv(fmt, "gu", ids, x, w_gate, FE, H, E, KU, w2=w_up, ws=ws_gate, ws2=ws_up, fused=fused, act=act,
+                      bias=bg, bias2=bu)
+    ys = moe_expert_mv(fmt, "dn", ids, a, w_down, H, FE, E, KU, ws=ws_down, bias=bd)
+    y = moe_combine(ys, wts, y=y, accumulate=y is not None, sg=sg)
+    return y, {"ids": ids, "wts": wts, "logits": logits, "act": a, "ys": ys}
 
 
 # ---------------------------------------------------------------------------------------------------- dispatch
@@ -363,3 +430,19 @@ def moe_routed(fmt, x, logits, E, KU, H, FE, gating, norm, **kw):
     if chain is moe_decode and fmt == "mxfp4s" and "w_gate" in kw and kw.get("ws_gate") is None:
         raise ValueError("mxfp4s weights need their scale planes")
     return chain(fmt, x, logits, E, KU, H, FE, gating, norm, **kw)
+
+
+def moe_layer(fmt, x, logits, E, KU, H, FE, gating, norm, shared=None, **kw):
+    """One MoE FFN layer (moe_layer, S/gen_llm.py:5306-5321): the shared experts, a dense swiglu FFN of width FS
+    stored into y, then the routed experts added into y; with a shared gate the shared output is scaled per token by
+    sigmoid(x . w_gate_inp_shexp) inside the combine. shared: None or a dict with fmt, w_gate, w_up, w_down, FS and
+    optionally fmt_down and gate (the f32 / bf16 [H] gate weight). Returns (y f32 [T, H], intermediates dict)."""
+    if shared is None:
+        return moe_routed(fmt, x, logits, E, KU, H, FE, gating, norm, **kw)
+    FS, sf = shared["FS"], shared["fmt"]
+    f = linear(sf, x, shared["w_gate"], FS, H, mode="swiglu", w2=shared["w_up"])
+    y = linear(shared.get("fmt_down", sf), f, shared["w_down"], H, FS)
+    sg = moe_shared_gate(x, shared["gate"]) if shared.get("gate") is not None else None
+    y, mid = moe_routed(fmt, x, logits, E, KU, H, FE, gating, norm, y=y, sg=sg, **kw)
+    mid.update(shared_act=f, sg=sg)
+    return y, mid

@@ -181,6 +181,25 @@ ACTIVATIONS = {"silu": silu_mul, "swiglu_oai": swiglu_oai}
 
 
 # ---------------------------------------------------------------------------------------------------- routing
+def router_logits(x, w):
+    """logits = x W_router^T in float64 (route_ref, make_kernel_tests.py:3166-3167); W f32 [E, H] (bf16 weights as
+    their f32 values)."""
+    return np.asarray(x, np.float64) @ np.asarray(w, np.float64).T
+
+
+def shared_gate(x, w):
+    """sg[t] = sigmoid(x[t] . w), the shared-expert gate (make_kernel_tests.py:3252)."""
+    d = np.asarray(x, np.float64) @ np.asarray(w, np.float64)
+    with np.errstate(over="ignore"):
+        return 1.0 / (1.0 + np.exp(-d))
+
+
+def wscale(ids, wts, scale):
+    """wts[t, k] scale[clamp(ids[t, k], 0, E - 1)] (g_moe_wscale; ktest_more.py:99-111)."""
+    scale = np.asarray(scale)
+    return np.asarray(wts) * scale[np.clip(ids, 0, len(scale) - 1)]
+
+
 def route(logits, KU, gating, norm, bias=None, scale=1.0):
     """Top-KU experts and weights from router logits (make_kernel_tests.py:3166-3184, with the logits given):
     gating 1 softmax over E then pick; 2 sigmoid (+ selection bias); 3 pick on logit + bias, weights = softmax
@@ -261,14 +280,17 @@ def bucket(ids, E, max_tiles_, live=None):
 
 
 # ------------------------------------------------------------------------------------------------------ combine
-def combine(ys_rows, pos_or_none, wts, y0=None):
+def combine(ys_rows, pos_or_none, wts, y0=None, sg=None):
     """y[t] = (y0[t] or 0) + sum_k w[t,k] ys[row(t,k)], row = pos[t,k] (sorted) or t*KU+k (decode); a row of -1
-    contributes 0 (S/gen_moe.py:730-762, :1231-1280)."""
+    contributes 0 (S/gen_moe.py:730-762, :1231-1280). With sg the shared output y0 is scaled first: sg[t] y0[t]
+    (shared_gated, S/gen_moe.py:765-779)."""
     wts = np.asarray(wts, np.float64)
     T, KU = wts.shape
     ys = np.asarray(ys_rows, np.float64)
     rows = np.arange(T * KU).reshape(T, KU) if pos_or_none is None else np.asarray(pos_or_none).reshape(T, KU)
     y = np.zeros((T, ys.shape[1])) if y0 is None else np.asarray(y0, np.float64).copy()
+    if sg is not None:
+        y *= np.asarray(sg, np.float64)[:, None]
     for k in range(KU):
         r = rows[:, k]
         v = np.where((r >= 0)[:, None], ys[np.maximum(r, 0)], 0.0)
@@ -277,11 +299,12 @@ def combine(ys_rows, pos_or_none, wts, y0=None):
 
 
 # ---------------------------------------------------------------------------------------------------- MoE chain
-def moe(x, ids, wts, gate_up, down, act="silu", x_round=None, act_round=None):
+def moe(x, ids, wts, gate_up, down, act="silu", x_round=None, act_round=None, bias=None):
     """Routed-expert FFN in float64 (make_kernel_tests.py:3197-3221): for each assignment (t, k) with e = ids[t,k]:
-    g = Wg[e] xr[t], u = Wu[e] xr[t], a = act(g, u), y[t] += w[t,k] Wd[e] ar. xr / ar are x and a after the
-    activation rounding of the kernel path being checked (identity, f16_rows or mxfp8_values).
-    gate_up(e) -> (Wg [FE,H], Wu [FE,H]) and down(e) -> Wd [H,FE] return exactly dequantized expert weights.
+    g = Wg[e] xr[t] + bg[e], u = Wu[e] xr[t] + bu[e], a = act(g, u), y[t] += w[t,k] (Wd[e] ar + bd[e]). xr / ar
+    are x and a after the activation rounding of the kernel path being checked (identity, f16_rows or
+    mxfp8_values). gate_up(e) -> (Wg [FE,H], Wu [FE,H]) and down(e) -> Wd [H,FE] return exactly dequantized expert
+    weights; bias: None or (bg [E,FE], bu [E,FE], bd [E,H]), the expert biases (make_kernel_tests.py:3207, :3215).
     Returns (y [T,H], act_rows [T*KU, FE] before rounding)."""
     x = np.asarray(x, np.float64)
     T, KU = ids.shape
@@ -293,12 +316,19 @@ def moe(x, ids, wts, gate_up, down, act="silu", x_round=None, act_round=None):
         tok, slot = np.nonzero(mask)
         Wg, Wu = gate_up(int(e))
         Wd = down(int(e))
-        a = fn(xr[tok] @ np.asarray(Wg, np.float64).T, xr[tok] @ np.asarray(Wu, np.float64).T)
+        g = xr[tok] @ np.asarray(Wg, np.float64).T
+        u = xr[tok] @ np.asarray(Wu, np.float64).T
+        if bias is not None:
+            g = g + np.asarray(bias[0][e], np.float64)
+            u = u + np.asarray(bias[1][e], np.float64)
+        a = fn(g, u)
         if acts is None:
             acts = np.zeros((T * KU, a.shape[1]))
             y = np.zeros((T, Wd.shape[0]))
         acts[tok * KU + slot] = a
         ar = a if act_round is None else act_round(a)
         out = ar @ np.asarray(Wd, np.float64).T
+        if bias is not None:
+            out = out + np.asarray(bias[2][e], np.float64)
         np.add.at(y, tok, wts[tok, slot][:, None] * out)
     return y, acts

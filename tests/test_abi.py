@@ -127,14 +127,16 @@ def test_argument_validation_without_a_device(lib):
     assert lib.qmm_dequant(4, fake, fake, 48, 64, fake, n) == st["QMM_ERR_SHAPE"]
     assert lib.qmm_mv(4, 64, 4, 1, 0, fake, 0, fake, fake, fake, n) == st["QMM_ERR_FORMAT"]
     assert lib.qmm_moe_grouped(4, 0, 1, 0, 4, 128, 48, 4, 2, fake, fake, fake, 3, fake, 8, fake, fake, n, n,
-                               fake, n) == st["QMM_ERR_SHAPE"]          # n % 32 != 0
+                               n, n, fake, n) == st["QMM_ERR_SHAPE"]          # n % 32 != 0
+    assert lib.qmm_moe_grouped(4, 0, 1, 0, 4, 128, 64, 4, 2, fake, fake, fake, 3, fake, 8, fake, fake, n, n,
+                               odd, n, fake, n) == st["QMM_ERR_ALIGN"]         # biases are f32
     # the gate/up GEMM with MXFP8 output: MXFP4 weights only, whole 32-column blocks, both outputs
-    assert lib.qmm_moe_grouped_mxfp8(1, 1, 0, 4, 256, 64, 4, 2, fake, fake, fake, fake, 8, fake, n, n, n, fake, fake,
-                                     n) == st["QMM_ERR_FORMAT"]
-    assert lib.qmm_moe_grouped_mxfp8(4, 1, 0, 4, 128, 48, 4, 2, fake, fake, fake, fake, 8, fake, fake, n, n, fake,
-                                     fake, n) == st["QMM_ERR_SHAPE"]
-    assert lib.qmm_moe_grouped_mxfp8(4, 1, 0, 4, 128, 64, 4, 2, fake, fake, fake, fake, 8, fake, fake, n, n, fake,
-                                     n, n) == st["QMM_ERR_NULL"]
+    assert lib.qmm_moe_grouped_mxfp8(1, 1, 0, 4, 256, 64, 4, 2, fake, fake, fake, fake, 8, fake, n, n, n, n, n,
+                                     fake, fake, n) == st["QMM_ERR_FORMAT"]
+    assert lib.qmm_moe_grouped_mxfp8(4, 1, 0, 4, 128, 48, 4, 2, fake, fake, fake, fake, 8, fake, fake, n, n, n, n,
+                                     fake, fake, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_moe_grouped_mxfp8(4, 1, 0, 4, 128, 64, 4, 2, fake, fake, fake, fake, 8, fake, fake, n, n, n, n,
+                                     fake, n, n) == st["QMM_ERR_NULL"]
     # decode swiglu matvec: GGUF-layout weights only, both matrices; the GEMM's swiglu mode needs the up matrix
     assert lib.qmm_mv_swiglu(3, 256, 4, 1, 0, fake, 0, fake, fake, fake, n) == st["QMM_ERR_FORMAT"]
     assert lib.qmm_mv_swiglu(1, 256, 4, 1, 0, fake, 0, fake, n, fake, n) == st["QMM_ERR_NULL"]

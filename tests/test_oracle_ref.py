@@ -280,3 +280,70 @@ def test_moe_chain_matches_loop():
             assert np.allclose(acts[t * KU + k], a)
             want[t] += wts[t, k] * (Wd[e] @ a)
     assert np.allclose(y, want, rtol=1e-12)
+
+
+def test_moe_chain_with_expert_biases():
+    """The gpt-oss expert biases: with zero weights the chain reduces to y[t] = sum_k w (Wd act(bg, bu) + bd), and a
+    random case matches the per-assignment loop of make_kernel_tests.py:3204-3215 (bias before the activation,
+    down bias inside the weighted sum)."""
+    rng = np.random.default_rng(16)
+    T, KU, E, H, FE = 5, 2, 4, 6, 3
+    x = rng.standard_normal((T, H))
+    bg, bu, bd = rng.standard_normal((E, FE)), rng.standard_normal((E, FE)), rng.standard_normal((E, H))
+    ids, wts = ref.route(rng.standard_normal((T, E)), KU, 3, False)
+    Z = np.zeros((E, FE, H))
+    Wd = rng.standard_normal((E, H, FE))
+    y0, _ = ref.moe(x, ids, wts, lambda e: (Z[e], Z[e]), lambda e: Wd[e], act="swiglu_oai", bias=(bg, bu, bd))
+    want0 = np.zeros((T, H))
+    for t in range(T):
+        for k in range(KU):
+            e = ids[t, k]
+            want0[t] += wts[t, k] * (Wd[e] @ ref.swiglu_oai(bg[e], bu[e]) + bd[e])
+    assert np.allclose(y0, want0, rtol=1e-13)
+    Wg, Wu = rng.standard_normal((E, FE, H)), rng.standard_normal((E, FE, H))
+    y, _ = ref.moe(x, ids, wts, lambda e: (Wg[e], Wu[e]), lambda e: Wd[e], act="silu", bias=(bg, bu, bd))
+    want = np.zeros((T, H))
+    for t in range(T):
+        for k in range(KU):
+            e = ids[t, k]
+            g, u = Wg[e] @ x[t] + bg[e], Wu[e] @ x[t] + bu[e]
+            want[t] += wts[t, k] * (Wd[e] @ (g / (1 + np.exp(-g)) * u) + bd[e])
+    assert np.allclose(y, want, rtol=1e-12)
+
+
+def test_router_logits_and_shared_gate_brute_force():
+    rng = np.random.default_rng(17)
+    T, E, H = 3, 5, 7
+    x, w = rng.standard_normal((T, H)), rng.standard_normal((E, H))
+    lg = ref.router_logits(x, w)
+    for t in range(T):
+        for e in range(E):
+            assert lg[t, e] == pytest.approx(sum(float(x[t, k]) * float(w[e, k]) for k in range(H)), rel=1e-12)
+    sg = ref.shared_gate(x, w[0])
+    assert np.allclose(sg, 1 / (1 + np.exp(-lg[:, 0])), rtol=1e-14)
+    assert ref.shared_gate(np.full((1, 2), -800.0), np.ones(2))[0] == 0.0      # no overflow: the limit
+    assert ref.shared_gate(np.zeros((1, 2)), np.ones(2))[0] == 0.5
+
+
+def test_wscale_clamps_ids():
+    """ktest_more.py:99-111: ids out of range use the first / last expert's scale."""
+    rng = np.random.default_rng(18)
+    E, T, KU = 6, 3, 4
+    ids = rng.integers(0, E, (T, KU)).astype(np.int32)
+    ids[0, 0], ids[1, 1] = -1, E + 5
+    wts = rng.random((T, KU))
+    sc = 0.5 + rng.random(E)
+    out = ref.wscale(ids, wts, sc)
+    assert out[0, 0] == wts[0, 0] * sc[0] and out[1, 1] == wts[1, 1] * sc[E - 1]
+    assert out[2, 3] == wts[2, 3] * sc[ids[2, 3]]
+
+
+def test_gated_combine():
+    """shared_gated (S/gen_moe.py:765-779): y = sg y0 + sum_k w ys; sg = 1 is the plain accumulate."""
+    rng = np.random.default_rng(19)
+    T, KU, H = 4, 2, 5
+    ys = rng.standard_normal((T * KU, H))
+    wts, y0, sg = rng.random((T, KU)), rng.standard_normal((T, H)), rng.random(T)
+    got = ref.combine(ys, None, wts, y0, sg=sg)
+    assert np.allclose(got, sg[:, None] * y0 + (wts[:, :, None] * ys.reshape(T, KU, H)).sum(1), rtol=1e-14)
+    assert np.array_equal(ref.combine(ys, None, wts, y0, sg=np.ones(T)), ref.combine(ys, None, wts, y0))
