@@ -39,7 +39,7 @@ enum qmm_status {
 
 /* QMM_MXFP4T: MXFP4 in MFMA-tiled planes (qmm_tile_mxfp4), the grouped GEMM's fast weight layout.
  * QMM_Q4_KT: Q4_K in the lane-ordered tiled layout (qmm_tile_q4k), the int8-activation decode GEMV's fast layout. */
-enum qmm_format { QMM_Q4_0 = 0, QMM_Q4_K = 1, QMM_MXFP4 = 2, QMM_MXFP4S = 3, QMM_MXFP4T = 4, QMM_Q4_KT = 5 };
+enum qmm_format { QMM_Q4_0 = 0, QMM_Q4_K = 1, QMM_MXFP4 = 2, QMM_MXFP4S = 3, QMM_MXFP4T = 4, QMM_Q4_KT = 5, QMM_Q6_K = 6 };
 enum qmm_dtype {
   QMM_F32 = 0,
   QMM_F16 = 1,

@@ -89,6 +89,7 @@ inline int64_t block_values(int fmt) {
     case QMM_MXFP4S: return 32;
     case QMM_MXFP4T: return 32;
     case QMM_Q4_KT: return 256;
+    case QMM_Q6_K: return 256;
     default: return 0;
   }
 }
@@ -100,6 +101,7 @@ inline int64_t block_bytes(int fmt) {
     case QMM_MXFP4S: return 16;
     case QMM_MXFP4T: return 16;
     case QMM_Q4_KT: return 144;
+    case QMM_Q6_K: return 210;
     default: return 0;
   }
 }

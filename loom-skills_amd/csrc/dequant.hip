@@ -3,6 +3,7 @@
 // Each thread decodes one 32-value group into f32, with the single rounding of the reference's value helpers:
 //   Q4_0   w = f32(d) * (q - 8)                       S/quant_values.loom:386-408
 //   Q4_K   w = (f32(d) * sc) * q - f32(dmin) * m      S/gen_llm.py:269-326
+//   Q6_K   w = (f32(d) * sc) * (q - 32)               S/gen_llm.py:320-397 (super-blocks 2-byte aligned)
 //   MXFP4  w = kvalues[code] * 2^(e - 128)            S/gen_llm.py:786-841 (code 8 -> +0)
 //   MXFP4S w = E2M1(code) * 2^(e - 127)               S/st_tensors.py:26-33 (code 8 -> -0)
 //   MXFP4T the same values from MFMA-tiled planes (grouped_mxfp4.hip)
@@ -51,6 +52,26 @@ __global__ void dequant_q4_k_kernel(const u8 *__restrict__ w, int64_t groups, fl
   for (int l = 0; l < 32; ++l) {
     const float q = (float)((qs[l] >> shift) & 15u);
     o[l] = __fsub_rn(__fmul_rn(scale, q), minimum);
+  }
+}
+
+// One 32-value group g = 4 half + j of a Q6_K super-block: code q = ((ql[64 half + 32 (j % 2) + l] >> 4 (j / 2)) &
+// 15) | (((qh[32 half + l] >> 2 j) & 3) << 4), scale sc[8 half + 2 j + l / 16]. Byte loads: blocks are 210 bytes.
+__global__ void dequant_q6_k_kernel(const u8 *__restrict__ w, int64_t groups, float *__restrict__ out) {
+  const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gi >= groups) return;
+  const u8 *b = w + (gi >> 3) * 210;
+  const int g = (int)(gi & 7), half = g >> 2, j = g & 3;
+  const float d = f16_to_f32((u32)b[208] | ((u32)b[209] << 8));
+  const float s0 = d * (float)(signed char)b[192 + 8 * half + 2 * j];
+  const float s1 = d * (float)(signed char)b[192 + 8 * half + 2 * j + 1];
+  const u8 *ql = b + 64 * half + 32 * (j & 1), *qh = b + 128 + 32 * half;
+  const int ls = 4 * (j >> 1), hs = 2 * j;
+  float *o = out + gi * 32;
+#pragma unroll
+  for (int l = 0; l < 32; ++l) {
+    const int q = (int)(((ql[l] >> ls) & 15u) | (((qh[l] >> hs) & 3u) << 4));
+    o[l] = __fmul_rn(l < 16 ? s0 : s1, (float)(q - 32));
   }
 }
 
@@ -109,7 +130,7 @@ const char *qmm_strerror(int status) {
 int64_t qmm_row_bytes(int fmt, int64_t k) { return row_bytes(fmt, k); }
 
 int qmm_dequant(int fmt, const void *w, const void *ws, int64_t rows, int64_t k, float *out, qmm_stream_t stream) {
-  if (fmt < QMM_Q4_0 || fmt > QMM_Q4_KT) return QMM_ERR_FORMAT;
+  if (fmt < QMM_Q4_0 || fmt > QMM_Q6_K) return QMM_ERR_FORMAT;
   if (!w || !out || ((fmt == QMM_MXFP4S || fmt == QMM_MXFP4T) && !ws)) return QMM_ERR_NULL;
   if (rows <= 0 || row_bytes(fmt, k) == 0) return QMM_ERR_SHAPE;
   if (fmt == QMM_MXFP4T) return qmm_dequant_mxfp4t(w, ws, rows, k, out, reinterpret_cast<hipStream_t>(stream));
@@ -124,6 +145,7 @@ int qmm_dequant(int fmt, const void *w, const void *ws, int64_t rows, int64_t k,
     case QMM_Q4_0: dequant_q4_0_kernel<<<grid, threads, 0, s>>>(wb, groups, out); break;
     case QMM_Q4_K: dequant_q4_k_kernel<<<grid, threads, 0, s>>>(wb, groups, out); break;
     case QMM_MXFP4: dequant_mxfp4_kernel<<<grid, threads, 0, s>>>(wb, groups, out); break;
+    case QMM_Q6_K: dequant_q6_k_kernel<<<grid, threads, 0, s>>>(wb, groups, out); break;
     default: dequant_mxfp4s_kernel<<<grid, threads, 0, s>>>(wb, static_cast<const u8 *>(ws), groups, out); break;
   }
   return launch_status();

@@ -172,14 +172,16 @@ int dispatch_mv(bool bf, int64_t k, int64_t n, int64_t tokens, int accumulate, c
 template <bool B> using MXG = MXFP4<B, false>;
 template <bool B> using MXS = MXFP4<B, true>;
 
-bool valid_fmt(int fmt) { return fmt >= QMM_Q4_0 && fmt <= QMM_MXFP4S; }   // no GEMV on MFMA-tiled planes
+// no GEMV here on the tiled layouts (the grouped GEMM's MXFP4 tiles; tiled Q4_K has its own int8 GEMV)
+bool valid_fmt(int fmt) { return (fmt >= QMM_Q4_0 && fmt <= QMM_MXFP4S) || fmt == QMM_Q6_K; }
 
-// Alignment the row engine needs: 16-byte rows for Q4_K / MXFP4S, 4-byte rows for Q4_0 pairs.
+// Alignment the row engine needs: 16-byte rows for Q4_K / MXFP4S, 4-byte rows for Q4_0 pairs, a 4-byte aligned
+// tensor for Q6_K (its 210-byte super-blocks then start on even addresses the loader can realign).
 int check_weights(int fmt, int64_t k, const void *w, const void *ws) {
   if (!w || (fmt == QMM_MXFP4S && !ws)) return QMM_ERR_NULL;
   if (fmt == QMM_Q4_0 && k % 64) return QMM_ERR_SHAPE;
   if ((fmt == QMM_Q4_K || fmt == QMM_MXFP4S) && !aligned(w, 16)) return QMM_ERR_ALIGN;
-  if (fmt == QMM_Q4_0 && !aligned(w, 4)) return QMM_ERR_ALIGN;
+  if ((fmt == QMM_Q4_0 || fmt == QMM_Q6_K) && !aligned(w, 4)) return QMM_ERR_ALIGN;
   return QMM_OK;
 }
 
@@ -208,6 +210,7 @@ extern "C" int qmm_mv(int fmt, int64_t k, int64_t n, int64_t tokens, int accumul
       }
       return dispatch_mv<Q4K>(bf, k, n, tokens, accumulate, x, w, w, rb, 0, y, s);
     case QMM_Q4_0: return dispatch_mv<Q40>(bf, k, n, tokens, accumulate, x, w, w, rb, 0, y, s);
+    case QMM_Q6_K: return dispatch_mv<Q6K>(bf, k, n, tokens, accumulate, x, w, w, rb, 0, y, s);
     case QMM_MXFP4: return dispatch_mv<MXG>(bf, k, n, tokens, accumulate, x, w, w, rb, 0, y, s);
     default: return dispatch_mv<MXS>(bf, k, n, tokens, accumulate, x, w, ws, rb, srb, y, s);
   }
@@ -293,13 +296,14 @@ static int expert_mv_impl(int fmt, int mode, int fused, int act, int64_t k, int6
     case QMM_Q4_K: return dispatch_expert<Q4K>(gu, bf, k, n, E, KU, assignments, ids, x, w, wsg, wu, wsu, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
     case QMM_Q4_0: return dispatch_expert<Q40>(gu, bf, k, n, E, KU, assignments, ids, x, w, wsg, wu, wsu, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
     case QMM_MXFP4: return dispatch_expert<MXG>(gu, bf, k, n, E, KU, assignments, ids, x, w, wsg, wu, wsu, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
+    case QMM_Q6_K: return dispatch_expert<Q6K>(gu, bf, k, n, E, KU, assignments, ids, x, w, wsg, wu, wsu, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
     default: return dispatch_expert<MXS>(gu, bf, k, n, E, KU, assignments, ids, x, w, wsg, wu, wsu, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
   }
 }
 
 extern "C" int qmm_mv_swiglu(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x,
                              int x_dtype, const void *w, const void *w2, float *y, qmm_stream_t stream) {
-  if (fmt != QMM_Q4_0 && fmt != QMM_Q4_K && fmt != QMM_MXFP4) return QMM_ERR_FORMAT;   // no split planes
+  if (fmt != QMM_Q4_0 && fmt != QMM_Q4_K && fmt != QMM_MXFP4 && fmt != QMM_Q6_K) return QMM_ERR_FORMAT;
   if (!x || !w || !w2 || !y) return QMM_ERR_NULL;
   if (n <= 0 || tokens <= 0 || tokens > (1 << 24) || row_bytes(fmt, k) == 0) return QMM_ERR_SHAPE;
   if (x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
@@ -312,6 +316,7 @@ extern "C" int qmm_mv_swiglu(int fmt, int64_t k, int64_t n, int64_t tokens, int 
   switch (fmt) {
     case QMM_Q4_K: return launch_swiglu<Q4K>(bf, k, n, tokens, accumulate, x, w, w2, rb, y, s);
     case QMM_Q4_0: return launch_swiglu<Q40>(bf, k, n, tokens, accumulate, x, w, w2, rb, y, s);
+    case QMM_Q6_K: return launch_swiglu<Q6K>(bf, k, n, tokens, accumulate, x, w, w2, rb, y, s);
     default: return launch_swiglu<MXG>(bf, k, n, tokens, accumulate, x, w, w2, rb, y, s);
   }
 }

@@ -19,6 +19,7 @@
 // activations it quantizes them while staging, with the quantizer's own arithmetic, so both input forms give
 // identical results.
 #include "bfly.hpp"
+#include "rowdot.hpp"
 
 using namespace qmm;
 
@@ -171,6 +172,41 @@ struct Q408 {
     ia -= 8 * (int)x.sa;   // codes q - 8: the code sum is an exact integer
     ib -= 8 * (int)x.sb;
     return (d[0] * x.da) * (float)ia + (d[1] * x.db) * (float)ib;
+  }
+};
+
+// Q6_K: item = 4 b + 2 half + jh (rowdot.hpp q6k_load); groups 2 item (values 0..31) and 2 item + 1. The codes are
+// taken unsigned and 32 times the activation code sum of each 16-value run removed, the same integer as the
+// reference's signed codes q - 32 (iq_dot, S/gen_llm.py:1036-1044): per group (ilo s0 + ihi s1) da, s = d sc.
+struct Q6K8 {
+  using W = Q6W;
+  static __device__ __forceinline__ int items(int64_t k) { return (int)(k / 256) * 4; }
+  static __device__ __forceinline__ int64_t group(int item) { return 2 * (int64_t)item; }
+  static __device__ __forceinline__ void load_w(const u8 *row, int item, bool live, W &w) {
+    q6k_load(row, item, live, w);
+  }
+  static __device__ __forceinline__ float dot(const W &w, const XQ &x, int item) {
+    u32 ca[8], cb[8];
+    q6k_codes(w, item & 1, ca, cb);
+    float s[4];
+    q6k_scales(w, s);
+    int i16[4];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      int ia = 0, za = 0, ib = 0, zb = 0;
+#pragma unroll
+      for (int i = 4 * q; i < 4 * q + 4; ++i) {
+        ia = sdot4(ca[i], x.a[i], ia);
+        za = sdot4(0x20202020u, x.a[i], za);
+        ib = sdot4(cb[i], x.b[i], ib);
+        zb = sdot4(0x20202020u, x.b[i], zb);
+      }
+      i16[q] = ia - za;
+      i16[2 + q] = ib - zb;
+    }
+    const float ga = __builtin_fmaf((float)i16[1], s[1], (float)i16[0] * s[0]) * x.da;
+    const float gb = __builtin_fmaf((float)i16[3], s[3], (float)i16[2] * s[2]) * x.db;
+    return ga + gb;
   }
 };
 
@@ -428,13 +464,14 @@ int qmm_mv_q4kt_q8(int64_t k, int64_t n, int64_t tokens, int accumulate, const v
 extern "C" int qmm_mv_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
                          const void *w, float *y, qmm_stream_t stream) {
   if (!x || !w || !y) return QMM_ERR_NULL;
-  if (fmt != QMM_Q4_K && fmt != QMM_Q4_0 && fmt != QMM_Q4_KT) return QMM_ERR_FORMAT;
+  if (fmt != QMM_Q4_K && fmt != QMM_Q4_0 && fmt != QMM_Q4_KT && fmt != QMM_Q6_K) return QMM_ERR_FORMAT;
   if (x_dtype != QMM_Q8 && x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
   if (k <= 0 || n <= 0 || tokens <= 0 || n > (1ll << 30) || tokens > (1ll << 24) || k > (1ll << 20))
     return QMM_ERR_SHAPE;
   if (fmt == QMM_Q4_K && k % 256) return QMM_ERR_SHAPE;
   if (fmt == QMM_Q4_0 && k % 64) return QMM_ERR_SHAPE;
-  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 4)) return QMM_ERR_ALIGN;
+  if (fmt == QMM_Q6_K && k % 256) return QMM_ERR_SHAPE;
+  if (!aligned(x, 16) || !aligned(w, fmt == QMM_Q6_K ? 4 : 16) || !aligned(y, 4)) return QMM_ERR_ALIGN;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (fmt == QMM_Q4_KT) return qmm_mv_q4kt_q8(k, n, tokens, accumulate, x, x_dtype, w, y, s);
   const bool fast = fmt == QMM_Q4_K && (k == 4096 || k == 8192) && tokens <= 65535ll * 2;
@@ -451,12 +488,14 @@ extern "C" int qmm_mv_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accu
                      : launch_fast_tg<2, false>(n, tokens, accumulate, x, 0, w, y, s);
   const u8 *codes = static_cast<const u8 *>(x);
   const float *meta = reinterpret_cast<const float *>(codes + tokens * k);
-  const int64_t rb = fmt == QMM_Q4_K ? k / 256 * 144 : k / 32 * 18;
+  const int64_t rb = row_bytes(fmt, k);
   constexpr int TG = 2;
   const dim3 grid((unsigned)((tokens + TG - 1) / TG), (unsigned)((n + kWaves * kRW - 1) / (kWaves * kRW)));
   if (grid.x > 2147483647u || grid.y > 65535u) return QMM_ERR_SHAPE;
   if (fmt == QMM_Q4_K)
     mv_q8_kernel<Q4K8, TG><<<grid, 256, 0, s>>>(n, tokens, k, accumulate, codes, meta, static_cast<const u8 *>(w), rb, y);
+  else if (fmt == QMM_Q6_K)
+    mv_q8_kernel<Q6K8, TG><<<grid, 256, 0, s>>>(n, tokens, k, accumulate, codes, meta, static_cast<const u8 *>(w), rb, y);
   else
     mv_q8_kernel<Q408, TG><<<grid, 256, 0, s>>>(n, tokens, k, accumulate, codes, meta, static_cast<const u8 *>(w), rb, y);
   return launch_status();

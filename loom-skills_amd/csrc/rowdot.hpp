@@ -7,6 +7,8 @@
 //   Q4_0    pair of blocks (36 B, 9 dwords)        36                  64
 //   MXFP4   one 17-byte GGUF block                 17 (byte loads)     32
 //   MXFP4S  one 16-byte nibble chunk + scale byte  16 + 1              32
+//   Q6_K    (super-block b, half, jh): groups      64 ql + 32 qh + 4   64 (groups 4 half + 2 jh, + 1)
+//           4 half + 2 jh and + 1 of the block     scale bytes + d
 //
 // bf16 activations: 4-bit codes become bf16 (128 + q) with one or into the exponent field and v_dot2_f32_bf16
 // multiplies two codes with two activations per lane op; the +128 is removed with the item's sum of x.
@@ -290,6 +292,144 @@ struct MXFP4 {
       byte_dot<3>(w.q[i], x, 4 * i + 3, p1);
     }
     return (p0 + p1) * e8m0_scale(w.e);
+  }
+};
+
+// ------------------------------------------------------------------------------------------------- Q6_K
+// item = 4 b + 2 half + jh: groups j = 2 jh and 2 jh + 1 of half `half` of super-block b, the 64 values
+// 256 b + 128 half + 64 jh .. + 64. Group j's code l: ((ql[64 half + 32 (j % 2) + l] >> 4 (j / 2)) & 15) |
+// (((qh[32 half + l] >> 2 j) & 3) << 4); so the item needs the half's 64 ql bytes (nibble jh), its 32 qh bytes
+// (fields 2 jh, 2 jh + 1), the 4 scale bytes at 8 half + 4 jh and d (S/gen_llm.py:320-325). Super-blocks are
+// 210 bytes, so with 4-byte aligned weights a block starts on a 4-byte or a 2-byte boundary: the loader reads
+// dwords from the aligned address below and shifts every dword pair by the block's misalignment (alignbit), never
+// reading past the block (d comes as a 16-bit load).
+struct Q6W {
+  u32 l[16], h[8], sc, d;
+};
+
+__device__ __forceinline__ void q6k_load(const u8 *row, int item, bool live, Q6W &w) {
+  const u8 *b = row + (int64_t)(item >> 2) * 210;
+  const int half = (item >> 1) & 1, jh = item & 1;
+  const uintptr_t a = reinterpret_cast<uintptr_t>(b);
+  const u32 sh = (u32)(a & 2u) * 8u;
+  const u32 *p = reinterpret_cast<const u32 *>(a & ~(uintptr_t)3);
+  u32 t[17], u[9];
+#pragma unroll
+  for (int i = 0; i < 17; ++i) t[i] = live ? p[16 * half + i] : 0u;
+#pragma unroll
+  for (int i = 0; i < 9; ++i) u[i] = live ? p[32 + 8 * half + i] : 0u;
+  const u32 c0 = live ? p[48 + 2 * half + jh] : 0u;
+  const u32 c1 = (live && sh) ? p[49 + 2 * half + jh] : 0u;   // only a misaligned block's scales straddle
+#pragma unroll
+  for (int i = 0; i < 16; ++i) w.l[i] = __builtin_amdgcn_alignbit(t[i + 1], t[i], sh);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) w.h[i] = __builtin_amdgcn_alignbit(u[i + 1], u[i], sh);
+  w.sc = __builtin_amdgcn_alignbit(c1, c0, sh);
+  w.d = live ? (u32)*reinterpret_cast<const u16 *>(b + 208) : 0u;
+}
+
+// the 6-bit codes of the item's groups as bytes: ca (values 0..31), cb (values 32..63)
+__device__ __forceinline__ void q6k_codes(const Q6W &w, int jh, u32 (&ca)[8], u32 (&cb)[8]) {
+  const u32 ls = 4u * (u32)jh;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    ca[i] = ((w.l[i] >> ls) & 0x0F0F0F0Fu) | (((w.h[i] >> ls) & 0x03030303u) << 4);
+    cb[i] = ((w.l[8 + i] >> ls) & 0x0F0F0F0Fu) | (((w.h[i] >> (ls + 2u)) & 0x03030303u) << 4);
+  }
+}
+
+// the four 16-value scales f32(d) * sc of the item, exact
+__device__ __forceinline__ void q6k_scales(const Q6W &w, float (&s)[4]) {
+  const float d = f16_to_f32(w.d);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s[i] = d * (float)(signed char)((w.sc >> (8 * i)) & 0xFFu);
+}
+
+template <bool BF16X>
+struct Q6K {
+  static constexpr int kValues = 64;
+  struct X {
+    typename std::conditional<BF16X, XB<8>, XF<8>>::type v;
+    float s16[4];   // sums of the four 16-value runs
+  };
+  using W = Q6W;
+  static __device__ __forceinline__ int items(int64_t k) { return (int)(k / 256) * 4; }
+  static __device__ __forceinline__ void load_x(const void *xrow, int item, bool live, X &x) {
+    const int64_t off = (int64_t)item * 64;
+    if constexpr (BF16X) {
+      xb_load<8>(static_cast<const u16 *>(xrow) + off, live, x.v);
+      constexpr u32 kOnes = 0x3F803F80u;   // bf16 (1, 1)
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        float sa = 0.f, sb = 0.f;
+#pragma unroll
+        for (int i = 4 * q; i < 4 * q + 4; ++i) {
+          sa = dot2(kOnes, x.v.a02[i], dot2(kOnes, x.v.a13[i], sa));
+          sb = dot2(kOnes, x.v.b02[i], dot2(kOnes, x.v.b13[i], sb));
+        }
+        x.s16[q] = sa;
+        x.s16[2 + q] = sb;
+      }
+    } else {
+      xf_load<8>(static_cast<const float *>(xrow) + off, live, x.v);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        float sa = 0.f, sb = 0.f;
+#pragma unroll
+        for (int i = 16 * q; i < 16 * q + 16; ++i) {
+          sa += x.v.a[i];
+          sb += x.v.b[i];
+        }
+        x.s16[q] = sa;
+        x.s16[2 + q] = sb;
+      }
+    }
+  }
+  static __device__ __forceinline__ void load_w(const u8 *row, const u8 *, int item, bool live, W &w) {
+    q6k_load(row, item, live, w);
+  }
+  // sum over the four runs of s_run (sum (q - 32) x): the run sum of (128 + q) x (bf16: codes or-ed into bf16 128)
+  // or q x (f32), less 160 or 32 times the run's sum of x
+  static __device__ __forceinline__ float dot(const W &w, const X &x, int item) {
+    u32 ca[8], cb[8];
+    q6k_codes(w, item & 1, ca, cb);
+    float s[4];
+    q6k_scales(w, s);
+    float p[4];
+    if constexpr (BF16X) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
+#pragma unroll
+        for (int i = 4 * q; i < 4 * q + 4; ++i) {
+          a0 = dot2((ca[i] & 0x00FF00FFu) | kBf16_128, x.v.a02[i], a0);
+          a1 = dot2(((ca[i] >> 8) & 0x00FF00FFu) | kBf16_128, x.v.a13[i], a1);
+          b0 = dot2((cb[i] & 0x00FF00FFu) | kBf16_128, x.v.b02[i], b0);
+          b1 = dot2(((cb[i] >> 8) & 0x00FF00FFu) | kBf16_128, x.v.b13[i], b1);
+        }
+        p[q] = __builtin_fmaf(-160.f, x.s16[q], a0 + a1);
+        p[2 + q] = __builtin_fmaf(-160.f, x.s16[2 + q], b0 + b1);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
+#pragma unroll
+        for (int i = 4 * q; i < 4 * q + 4; ++i) {
+          a0 = __builtin_fmaf((float)(ca[i] & 0xFFu), x.v.a[4 * i + 0], a0);
+          a1 = __builtin_fmaf((float)((ca[i] >> 8) & 0xFFu), x.v.a[4 * i + 1], a1);
+          a0 = __builtin_fmaf((float)((ca[i] >> 16) & 0xFFu), x.v.a[4 * i + 2], a0);
+          a1 = __builtin_fmaf((float)(ca[i] >> 24), x.v.a[4 * i + 3], a1);
+          b0 = __builtin_fmaf((float)(cb[i] & 0xFFu), x.v.b[4 * i + 0], b0);
+          b1 = __builtin_fmaf((float)((cb[i] >> 8) & 0xFFu), x.v.b[4 * i + 1], b1);
+          b0 = __builtin_fmaf((float)((cb[i] >> 16) & 0xFFu), x.v.b[4 * i + 2], b0);
+          b1 = __builtin_fmaf((float)(cb[i] >> 24), x.v.b[4 * i + 3], b1);
+        }
+        p[q] = __builtin_fmaf(-32.f, x.s16[q], a0 + a1);
+        p[2 + q] = __builtin_fmaf(-32.f, x.s16[2 + q], b0 + b1);
+      }
+    }
+    return __builtin_fmaf(s[0], p[0], s[1] * p[1]) + __builtin_fmaf(s[2], p[2], s[3] * p[3]);
   }
 };
 

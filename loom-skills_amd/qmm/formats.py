@@ -6,12 +6,12 @@ for the formats this library decodes. The integer codes are this library's own (
 
 # mxfp4t: MXFP4 in MFMA-tiled planes (this library's load-time layout for the grouped GEMM, qmm_tile_mxfp4)
 # q4_kt: Q4_K in the lane-ordered tiled layout of the int8-activation decode GEMV (qmm_tile_q4k)
-FMT = {"q4_0": 18, "q4_k": 144, "mxfp4": 17, "mxfp4s": 16, "mxfp4t": 16, "q4_kt": 144}   # bytes per block
-SB = {"q4_0": 32, "q4_k": 256, "mxfp4": 32, "mxfp4s": 32, "mxfp4t": 32, "q4_kt": 256}    # values per block
+FMT = {"q4_0": 18, "q4_k": 144, "mxfp4": 17, "mxfp4s": 16, "mxfp4t": 16, "q4_kt": 144, "q6_k": 210}   # bytes per block
+SB = {"q4_0": 32, "q4_k": 256, "mxfp4": 32, "mxfp4s": 32, "mxfp4t": 32, "q4_kt": 256, "q6_k": 256}    # values per block
 SPLIT = frozenset({"mxfp4s", "mxfp4t"})                         # weight plane + scale plane (two operands)
 SCALE_DIV = {"mxfp4s": 16}                                      # nibble-plane bytes per scale-plane byte
 
-CODE = {"q4_0": 0, "q4_k": 1, "mxfp4": 2, "mxfp4s": 3, "mxfp4t": 4, "q4_kt": 5}   # enum qmm_format
+CODE = {"q4_0": 0, "q4_k": 1, "mxfp4": 2, "mxfp4s": 3, "mxfp4t": 4, "q4_kt": 5, "q6_k": 6}   # enum qmm_format
 DTYPE = {"f32": 0, "f16": 1, "bf16": 2, "mxfp8": 3, "q8": 4}    # enum qmm_dtype
 MX_BLOCK = 32                                                   # values per E8M0 scale of an MXFP8 operand
 GEMM_MODE = {"store": 0, "acc": 1, "swiglu": 2}                 # enum qmm_gemm_mode

@@ -391,15 +391,16 @@ def moe_prefill(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up
 
 def moe_decode(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=None, ws_gate=None, ws_down=None,
                ws_up=None, fused=False, act="silu", scale=1.0, bias=None, router=None, expert_bias=None,
-               down_scale=None, y=None, sg=None):
+               down_scale=None, y=None, sg=None, fmt_down=None):
     """The reference's decode MoE chain (moe_routed with t < 64): route, per-assignment expert matvecs
-    (g_moe_gu_* then g_moe_dn_*), combine in assignment order. Arguments as moe_prefill.
+    (g_moe_gu_* then g_moe_dn_*), combine in assignment order. Arguments as moe_prefill; fmt_down: the down
+    tensor's format when it differs (Q4_K_M files: Q4_K gate / up, Q6_K down, S/gen_llm.py:5336-5340).
     Returns (y f32 [T, H], intermediates dict)."""
     ids, wts, logits = _route(x, logits, KU, gating, norm, scale, bias, router, down_scale)
     bg, bu, bd = expert_bias if expert_bias is not None else (None, None, None)
     a = moe_expert_mv(fmt, "gu", ids, x, w_gate, FE, H, E, KU, w2=w_up, ws=ws_gate, ws2=ws_up, fused=fused, act=act,
                       bias=bg, bias2=bu)
-    ys = moe_expert_mv(fmt, "dn", ids, a, w_down, H, FE, E, KU, ws=ws_down, bias=bd)
+    ys = moe_expert_mv(fmt_down or fmt, "dn", ids, a, w_down, H, FE, E, KU, ws=ws_down, bias=bd)
     y = moe_combine(ys, wts, y=y, accumulate=y is not None, sg=sg)
     return y, {"ids": ids, "wts": wts, "logits": logits, "act": a, "ys": ys}
 

@@ -74,6 +74,15 @@ def q4_k_weights(rng, rows, k, sigma=0.01):
     return raw.reshape(-1)
 
 
+def q6_k_weights(rng, rows, k, sigma=0.002):
+    """Q6_K bytes [rows * k/256 * 210]: ql[128], qh[64], 16 int8 scales, f16 d per super-block (code bytes and
+    scales uniform)."""
+    nb = rows * k // 256
+    raw = rng.integers(0, 256, (nb, 210), dtype=np.uint8)
+    raw[:, 208:210] = _abs_f16(rng, sigma, nb).view(np.uint8).reshape(nb, 2)
+    return raw.reshape(-1)
+
+
 def mxfp4_weights(rng, rows, k, e_lo=-8, e_hi=0):
     """MXFP4 GGUF bytes [rows * k/32 * 17]: E8M0 byte 127 + U{e_lo..e_hi} then 16 code bytes per block."""
     nb = rows * k // 32
@@ -86,7 +95,7 @@ def mxfp4_weights(rng, rows, k, e_lo=-8, e_hi=0):
 
 
 def weights(fmt, rng, rows, k):
-    return {"q4_0": q4_0_weights, "q4_k": q4_k_weights, "mxfp4": mxfp4_weights}[fmt](rng, rows, k)
+    return {"q4_0": q4_0_weights, "q4_k": q4_k_weights, "mxfp4": mxfp4_weights, "q6_k": q6_k_weights}[fmt](rng, rows, k)
 
 
 def normal_f32(rng, shape):

@@ -6,6 +6,8 @@ as the reference's decoders do, so any correct implementation reproduces them bi
 * Q4_0  (18 B / 32 values)   S/quant_values.loom:386-408, S/moe_q4_0.py:1-38,
                              .github/devlab/kbench/moe_q4_0/gen_bench.py:19-25
 * Q4_K  (144 B / 256 values) S/gen_llm.py:234-326 (@g_k_scale_minimum, @g_k_metadata, @g_q4_k_values)
+* Q6_K  (210 B / 256 values) S/gen_llm.py:320-397 (@g_q6_k_values); ggml's dequantize_row_q6_K (gguf-py
+                             quants.Q6_K, the reference's oracle dependency, make_kernel_tests.py:44-55) restated
 * MXFP4 GGUF (17 B / 32)     S/gen_llm.py:786-841 (@g_mxfp4_values)
 * MXFP4 split planes         S/gen_llm.py:844-895 (@g_mxfp4s_values), S/st_tensors.py:17-33 (dequant_mxfp4)
 * MXFP4 MFMA-tiled planes    this library's load-time layout of the split planes (no reference counterpart); a byte
@@ -16,8 +18,8 @@ as the reference's decoders do, so any correct implementation reproduces them bi
 import numpy as np
 
 # bytes per block and values per block (S/formats.py:5-19)
-BLOCK_BYTES = {"q4_0": 18, "q4_k": 144, "mxfp4": 17, "mxfp4s": 16}
-BLOCK_VALUES = {"q4_0": 32, "q4_k": 256, "mxfp4": 32, "mxfp4s": 32}
+BLOCK_BYTES = {"q4_0": 18, "q4_k": 144, "mxfp4": 17, "mxfp4s": 16, "q6_k": 210}
+BLOCK_VALUES = {"q4_0": 32, "q4_k": 256, "mxfp4": 32, "mxfp4s": 32, "q6_k": 256}
 
 # E2M1 magnitudes; bit 3 of a code is the sign (S/st_tensors.py:17-22)
 E2M1 = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], np.float64)
@@ -217,6 +219,31 @@ def q4_kt_to_gguf(raw_t, rows, k):
     return np.ascontiguousarray(blk.transpose(0, 2, 1, 3, 4)).reshape(-1)    # rows in order, super-blocks in order
 
 
+def q6_k_fields(raw):
+    """(d f32 [nb], sc i32 [nb, 16], q i32 [nb, 256]) of Q6_K super-blocks: ql = bytes 0..127, qh = 128..191, int8
+    scales = 192..207, f16 d = 208..209. Value c = 128 half + 32 j + l (group g = 4 half + j) has the 6-bit code
+    q = ((ql[64 half + 32 (j % 2) + l] >> 4 (j // 2)) & 15) | (((qh[32 half + l] >> 2 j) & 3) << 4) and the scale
+    sc[8 half + 2 j + l // 16] (S/gen_llm.py:320-325)."""
+    b = _blocks(raw, "q6_k")
+    ql = b[:, 0:128].reshape(-1, 2, 2, 32).astype(np.int32)      # [nb, half, j % 2, l]
+    qh = b[:, 128:192].reshape(-1, 2, 1, 32).astype(np.int32)    # [nb, half, -, l]
+    j = np.arange(4).reshape(1, 1, 4, 1)
+    low = (ql[:, :, j[0, 0, :, 0] % 2, :] >> (4 * (j // 2))) & 15  # [nb, half, j, l]
+    high = (qh >> (2 * j)) & 3
+    q = (low | (high << 4)).reshape(-1, 256)
+    sc = b[:, 192:208].view(np.int8).astype(np.int32)
+    return _f16(b[:, 208:210]), sc, q
+
+
+def dequant_q6_k(raw, rows, k):
+    """Q6_K: value = (f32(d) * sc) * (q - 32), the two products in that order in f32 (S/gen_llm.py:386-396); the
+    first is exact (11 x 8 bits), the second rounds once."""
+    d, sc, q = q6_k_fields(raw)
+    scale = (d[:, None] * sc.astype(np.float32)).astype(np.float32)            # [nb, 16], exact
+    s = np.repeat(scale, 16, axis=1)                                            # 16 consecutive values share one
+    return (s * (q - 32).astype(np.float32)).astype(np.float32).reshape(rows, k)
+
+
 def dequant_q4_kt(raw_t, rows, k):
     """Q4_K in the tiled GEMV layout: the values of the GGUF blocks it permutes."""
     return dequant_q4_k(q4_kt_to_gguf(raw_t, rows, k), rows, k)
@@ -235,4 +262,6 @@ def dequantize(fmt, raw, rows, k, scales=None):
         return dequant_mxfp4t(raw, scales, rows, k)
     if fmt == "q4_kt":
         return dequant_q4_kt(raw, rows, k)
+    if fmt == "q6_k":
+        return dequant_q6_k(raw, rows, k)
     raise ValueError(fmt)

@@ -71,6 +71,7 @@ def test_host_only_entry_points(lib):
     assert lib.qmm_row_bytes(3, 2880) == 1440
     assert lib.qmm_row_bytes(4, 2880) == 1440          # MFMA-tiled planes: the split nibble plane's bytes
     assert lib.qmm_row_bytes(5, 4096) == 2304          # tiled Q4_K: the GGUF row's bytes
+    assert lib.qmm_row_bytes(6, 768) == 630            # Q6_K: 210 bytes per 256 values
     assert lib.qmm_mxfp4t_scale_bytes(64, 2880) == 2 * 12 * 256   # 45 chunks -> 12 groups of four
     assert lib.qmm_mxfp4t_scale_bytes(48, 2880) == 0 and lib.qmm_mxfp4t_scale_bytes(64, 2848) == 0
     assert lib.qmm_row_bytes(1, 100) == 0
@@ -144,6 +145,21 @@ def test_argument_validation_without_a_device(lib):
     assert lib.qmm_mv_swiglu(1, 256, 4, 1, 0, fake, 0, fake, odd, fake, n) == st["QMM_ERR_ALIGN"]
     assert lib.qmm_gemm(1, 2, 64, 256, 64, fake, 1, n, fake, n, fake, 0, n) == st["QMM_ERR_NULL"]
     assert lib.qmm_row_scale_f16_live(64, n, 256, fake, 0, fake, fake, n) == st["QMM_ERR_NULL"]
+    # Q6_K: K % 256, a 4-byte aligned tensor
+    assert lib.qmm_mv(6, 320, 4, 1, 0, fake, 0, fake, n, fake, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_mv(6, 256, 4, 1, 0, fake, 0, odd, n, fake, n) == st["QMM_ERR_ALIGN"]
+    assert lib.qmm_mv_q8(6, 256, 4, 1, 0, fake, 4, odd, fake, n) == st["QMM_ERR_ALIGN"]
+    assert lib.qmm_dequant(6, fake, n, 4, 320, fake, n) == st["QMM_ERR_SHAPE"]
+    # router / shared gate / wscale / gated combine
+    assert lib.qmm_moe_route(4, 2882, 32, 4, 3, 0, ctypes.c_float(1), fake, 0, fake, 0, n, n, fake, fake, fake,
+                             n) == st["QMM_ERR_SHAPE"]                        # H % 4
+    assert lib.qmm_moe_route(4, 2880, 32, 4, 1, 0, ctypes.c_float(1), fake, 0, fake, 0, fake, n, fake, fake, fake,
+                             n) == st["QMM_ERR_RANGE"]                        # gating 1 takes no bias
+    assert lib.qmm_moe_route(4, 2880, 32, 4, 3, 0, ctypes.c_float(1), fake, 0, fake, 3, n, n, fake, fake, fake,
+                             n) == st["QMM_ERR_DTYPE"]
+    assert lib.qmm_moe_shared_gate(4, 2048, fake, 0, n, 0, fake, n) == st["QMM_ERR_NULL"]
+    assert lib.qmm_moe_wscale(4, 9, 32, fake, fake, fake, n) == st["QMM_ERR_RANGE"]
+    assert lib.qmm_moe_combine_gated(4, 16, 8, 4, fake, n, fake, n, fake, n) == st["QMM_ERR_NULL"]
 
 
 def test_python_surface_refuses_host_tensors():

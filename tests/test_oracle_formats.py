@@ -10,6 +10,10 @@ Each decoder is checked against something other than itself:
          then high nibbles, get_scale_min_k4 for the 6-bit fields) against the vectorized one, bit for bit; a
          hand-built known-answer block; the scale packer's round trip over all 64 x 64 (sc, m) pairs at every
          sub-block; the reference's real Q4_K bytes (Qwen3-0.6B ffn_gate / ffn_up).
+* Q6_K   no Q6_K bytes or vectors exist in the reference: a scalar decoder that follows ggml's
+         dequantize_row_q6_K loop (four values per ql / qh lane, then the pointer advance) against the vectorized
+         one (group formula of S/gen_llm.py:320-325), bit for bit; two hand-built known-answer blocks; the sign of
+         the int8 scales and the single rounding of the value.
 * MXFP4  the reference's split-plane KAT (tests/test_safetensors_source.py:200-206) and its scalar vLLM-table
          decoder (:92-103) on random planes; GGUF blocks against a scalar ggml decoder (kvalues x 2^(e-128) with
          the e < 2 subnormal rule), and GGUF <-> split equivalence up to the sign of zero.
@@ -199,6 +203,83 @@ def test_q4_k_real_weights(name):
     hi = d[:, None] * sc * 15 - dmin[:, None] * m
     g = got.reshape(-1, 8, 32)
     assert np.all(g >= lo[:, :, None] - 1e-7) and np.all(g <= hi[:, :, None] + 1e-7)
+
+
+# ------------------------------------------------------------------------------------------------------- Q6_K
+def q6_k_scalar(raw):
+    """ggml's dequantize_row_q6_K, element by element: per 128-value half, the lane l of 32 yields four values
+    l, l+32, l+64, l+96 from ql[l] and ql[l+32] (low nibbles, then high nibbles) and the four 2-bit fields of
+    qh[l], with the scale sc[l/16 + 0, 2, 4, 6]; pointers then advance by 64 ql, 32 qh and 8 scale bytes."""
+    b = np.asarray(raw, np.uint8).reshape(-1, 210)
+    out = np.zeros((b.shape[0], 256), np.float32)
+    for i, blk in enumerate(b):
+        d = np.frombuffer(blk[208:210].tobytes(), "<f2")[0].astype(np.float32)
+        sc = blk[192:208].view(np.int8)
+        for n in range(2):
+            ql, qh, s = blk[64 * n:64 * n + 64], blk[128 + 32 * n:160 + 32 * n], sc[8 * n:8 * n + 8]
+            for l in range(32):
+                i16 = l // 16
+                h = int(qh[l])
+                q1 = (int(ql[l]) & 15) | ((h >> 0) & 3) << 4
+                q2 = (int(ql[l + 32]) & 15) | ((h >> 2) & 3) << 4
+                q3 = (int(ql[l]) >> 4) | ((h >> 4) & 3) << 4
+                q4 = (int(ql[l + 32]) >> 4) | ((h >> 6) & 3) << 4
+                for off, q, si in ((0, q1, 0), (32, q2, 2), (64, q3, 4), (96, q4, 6)):
+                    out[i, 128 * n + l + off] = np.float32(d * np.float32(s[i16 + si])) * np.float32(q - 32)
+    return out
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_q6_k_vectorized_equals_scalar_ggml_loop(seed):
+    from qmm import synth
+    rng = np.random.default_rng(900 + seed)
+    raw = synth.q6_k_weights(rng, 3, 512, sigma=0.5 if seed else 0.002)
+    got = of.dequant_q6_k(raw, 3, 512)
+    assert np.array_equal(got.view(np.uint32), q6_k_scalar(raw).reshape(3, 512).view(np.uint32))
+
+
+def test_q6_k_known_answer_blocks():
+    """Hand-built blocks. (1) every ql byte 0x21, every qh byte 0xE4 (fields 0, 1, 2, 3), scales 1..16, d = 0.5:
+    group j of either half has code 1, 17, 34, 50 (values -31, -15, 2, 18 times 0.5 sc). (2) ql[i] = i, qh = 0,
+    scales 1, d = 1: value c = 128 h + 32 j + l is ((64 h + 32 (j % 2) + l) >> 4 (j // 2) & 15) - 32."""
+    blk = np.zeros(210, np.uint8)
+    blk[0:128] = 0x21
+    blk[128:192] = 0xE4
+    blk[192:208] = np.arange(1, 17, dtype=np.int8).view(np.uint8)
+    blk[208:210] = np.array([0.5], "<f2").view(np.uint8)
+    got = of.dequant_q6_k(blk, 1, 256).reshape(2, 4, 32)
+    for h in range(2):
+        for j in range(4):
+            for l in range(32):
+                want = 0.5 * (8 * h + 2 * j + l // 16 + 1) * (-31, -15, 2, 18)[j]
+                assert got[h, j, l] == want, (h, j, l)
+    blk = np.zeros(210, np.uint8)
+    blk[0:128] = np.arange(128, dtype=np.uint8)
+    blk[192:208] = 1
+    blk[208:210] = np.array([1.0], "<f2").view(np.uint8)
+    got = of.dequant_q6_k(blk, 1, 256).reshape(2, 4, 32)
+    for h in range(2):
+        for j in range(4):
+            for l in range(32):
+                assert got[h, j, l] == (((64 * h + 32 * (j % 2) + l) >> (4 * (j // 2))) & 15) - 32
+
+
+def test_q6_k_signed_scales_and_single_rounding():
+    """A negated int8 scale negates its 16 values; the second product rounds once in f32 (d sc exact, then x q)."""
+    from qmm import synth
+    rng = np.random.default_rng(901)
+    raw = synth.q6_k_weights(rng, 1, 256, sigma=3.0)
+    blk = raw.reshape(210).copy()
+    sc = blk[192:208].view(np.int8).copy()
+    sc[sc == -128] = 5
+    blk[192:208] = sc.view(np.uint8)
+    neg = blk.copy()
+    neg[192:208] = (-sc).astype(np.int8).view(np.uint8)
+    a, b = of.dequant_q6_k(blk, 1, 256), of.dequant_q6_k(neg, 1, 256)
+    assert np.array_equal(a, -b)
+    d, s, q = of.q6_k_fields(blk)
+    exact = np.float64(d[0]) * np.repeat(s[0], 16).astype(np.float64) * (q[0] - 32)
+    assert np.array_equal(a.reshape(-1), exact.astype(np.float32))   # one rounding of the exact product
 
 
 # ------------------------------------------------------------------------------------------------------ MXFP4
