@@ -38,7 +38,9 @@ enum qmm_status {
 };
 
 /* QMM_MXFP4T: MXFP4 in MFMA-tiled planes (qmm_tile_mxfp4), the grouped GEMM's fast weight layout.
- * QMM_Q4_KT: Q4_K in the lane-ordered tiled layout (qmm_tile_q4k), the int8-activation decode GEMV's fast layout. */
+ * QMM_Q4_KT: Q4_K in the lane-ordered tiled layout (qmm_tile_q4k), the int8-activation decode GEMV's fast layout.
+ * QMM_Q6_K: GGUF Q6_K (210 bytes per 256 values; ffn_down of the Q4_K_M files), read in place from a 4-byte aligned
+ *           tensor (its super-blocks start on even addresses). */
 enum qmm_format { QMM_Q4_0 = 0, QMM_Q4_K = 1, QMM_MXFP4 = 2, QMM_MXFP4S = 3, QMM_MXFP4T = 4, QMM_Q4_KT = 5, QMM_Q6_K = 6 };
 enum qmm_dtype {
   QMM_F32 = 0,
@@ -106,8 +108,9 @@ int qmm_mv_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, con
  *   swiglu: Y = silu((X W^T) inv) * ((X W2^T) inv)
  * x: f16 [rows, k] (x_dtype QMM_F16), the reference's row-scaled x16 from qmm_row_scale_f16; scales: f32 [rows, 2]
  * with inv = scales[row, 1] (the reference's (2^-e, 2^e) pairs), or NULL for inv = 1; y: [rows, n] of y_dtype
- * (QMM_F32 as the reference, or QMM_BF16, rounded to nearest even). fp32 accumulation. Q4_K weights, K % 256 == 0;
- * the weights are dequantized to f16 as the reference stages them: fma_f16(f16(q), f16(d sc), f16(-dmin m)).
+ * (QMM_F32 as the reference, or QMM_BF16, rounded to nearest even). fp32 accumulation. K % 256 == 0. Weights are
+ * dequantized to f16 as the reference stages them: Q4_K fma_f16(f16(q), f16(d sc), f16(-dmin m)); Q6_K (fmt
+ * QMM_Q6_K, S/gen_gemm.py:369-444) fma_f16(f16(q), f16(d sc), f16(-32 d sc)) with q the unsigned 6-bit code.
  * QMM_GEMM_SWIGLU: w is the gate matrix and w2 the up matrix (both [n, k]); silu(g) = g / (1 + e^-g).
  * Skip-padding (the reference's default GEMM_SKIP_PADDING): with scales, a 64-row tile whose rows all have
  * scales[row, 0] == 0 (padding rows of qmm_row_scale_f16_live) does no work and its y rows are not written. */
@@ -179,6 +182,8 @@ int qmm_moe_expert_mv_split(int mode, int fused, int act, int64_t k, int64_t n, 
  *   QMM_Q4_K:   x is the row-scaled f16 operand (x_dtype QMM_F16) from qmm_row_scale_f16 with its scales f32
  *               [x_rows, 2] in x_scales (inv = scales[row, 1]); K % 256 == 0; f16 MFMA, weights staged as
  *               fma_f16(f16(q), f16(d sc), f16(-dmin m)).
+ *   QMM_Q6_K:   as QMM_Q4_K with Q6_K weights (staged as qmm_gemm stages them); g_moe_gdn_q6_k of the Q4_K_M
+ *               expert layout (Q4_K gate / up, Q6_K down).
  *   QMM_MXFP4S: weights in split planes, ws / ws2 the E8M0 planes [E, rows, k/32]; x is MXFP8 (x_dtype
  *               QMM_MXFP8) from qmm_quant_mxfp8: E4M3 codes u8 [x_rows, k] with x_scales u8 [x_rows, k/32];
  *               K % 64 == 0; scaled f8f6f4 MFMA, inv = 1.

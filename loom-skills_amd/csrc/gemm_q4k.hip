@@ -54,10 +54,7 @@ __device__ __forceinline__ u32 as_u32(h2 v) { return __builtin_bit_cast(u32, v);
 // 8 f16 weights of one column in K order from two code dwords (values 0..3 and 4..7 of the run) of one nibble
 // plane: bytes become (1024 + q) f16 pairs with one v_perm each, the 1024 is removed exactly, then one rounding
 // fma with the sub-block's f16 scale and negated minimum.
-template <bool HI>
-__device__ __forceinline__ f16x8 deq8(u32 q0, u32 q1, h2 dsc, h2 nmn) {
-  const u32 n0 = HI ? (q0 >> 4) & 0x0F0F0F0Fu : q0 & 0x0F0F0F0Fu;
-  const u32 n1 = HI ? (q1 >> 4) & 0x0F0F0F0Fu : q1 & 0x0F0F0F0Fu;
+__device__ __forceinline__ f16x8 deq8_codes(u32 n0, u32 n1, h2 dsc, h2 nmn) {
   const u32 k64 = 0x64646464u;
   const h2 m1024 = as_h2(0xE400E400u);
   const u32 t[4] = {__builtin_amdgcn_perm(k64, n0, 0x04010400u), __builtin_amdgcn_perm(k64, n0, 0x04030402u),
@@ -68,6 +65,18 @@ __device__ __forceinline__ f16x8 deq8(u32 q0, u32 q1, h2 dsc, h2 nmn) {
   typedef __attribute__((ext_vector_type(4))) u32 u32x4;
   return __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]});
 }
+template <bool HI>
+__device__ __forceinline__ f16x8 deq8(u32 q0, u32 q1, h2 dsc, h2 nmn) {
+  return deq8_codes(HI ? (q0 >> 4) & 0x0F0F0F0Fu : q0 & 0x0F0F0F0Fu, HI ? (q1 >> 4) & 0x0F0F0F0Fu : q1 & 0x0F0F0F0Fu,
+                    dsc, nmn);
+}
+
+// Q6_K (210-byte super-blocks, only 2-byte aligned): 16-byte pieces are loaded at any even address (the HSA
+// runtime runs the GPU in unaligned access mode; the compiler emits global_load_dwordx4 for them).
+typedef uint4 uint4_a2 __attribute__((aligned(2)));
+typedef u32 u32_a2 __attribute__((aligned(2)));
+__device__ __forceinline__ uint4 ld16u(const u8 *p) { return *reinterpret_cast<const uint4_a2 *>(p); }
+__device__ __forceinline__ u32 ld4u(const u8 *p) { return *reinterpret_cast<const u32_a2 *>(p); }
 
 // f16 (d sc, -dmin m) of sub-block g from a super-block header, broadcast to both halves
 __device__ __forceinline__ void sub_scale(const uint4 &hd, int g, h2 &dsc, h2 &nmn) {
@@ -110,8 +119,9 @@ struct Args {
 // pairs per column with one 8-byte LDS read instead of loading and decoding the super-block header again.
 constexpr int kStagedMaxK = 6144;
 
-template <int KIND, bool ACC, bool BF16OUT, int DEPTH, bool STAGED>
+template <int KIND, bool ACC, bool BF16OUT, int DEPTH, bool STAGED, bool Q6>
 __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
+  static_assert(!(Q6 && STAGED), "Q6_K scales are read with the codes");
   constexpr bool kTwoW = KIND == kGU || KIND == kSwiglu;        // two weight matrices (gate, up): wave pairs
   constexpr bool kDenseRows = KIND == kDense || KIND == kSwiglu;  // rows m0 .. m0 + 63 of x, tiles row-major
   constexpr int BN = kTwoW ? 64 : 128;
@@ -170,7 +180,7 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
   // zeros of dead rows) -- expert tiles of prefill batches are often less than half full
   const bool upper = __syncthreads_or(tid >= 32 && my_src >= 0) != 0;
 
-  const int64_t RB = (int64_t)K / 256 * 144;
+  const int64_t RB = (int64_t)K / 256 * (Q6 ? 210 : 144);
   const int S = K / KSTEP, S0 = S / 2;
 
   // ---- A staging map: chunk c = i * 256 + tid of 16 bytes; K-half, row, 16-byte column. Loads are unconditional
@@ -219,6 +229,18 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
   auto b_code = [&](int j, int s) -> uint4 {
     const int gs = kh * S0 + (s < S0 ? s : S0 - 1);
     return ld16(wcol[j] + (int64_t)(gs >> 2) * 144 + 16 + 32 * (gs & 3) + 16 * h);
+  };
+  // Q6_K page gs & 3 = (half, jh): groups j = 2 jh (ql bytes 64 half + l) and 2 jh + 1 (64 half + 32 + l), both with
+  // qh bytes 32 half + l; lane half h takes l = 16 h .. 16 h + 15, the scales sc[8 half + 4 jh + h] and [.. + 2 + h]
+  auto b_q6 = [&](int j, int s, uint4 &qa, uint4 &qb, uint4 &qh, u32 &sc, u32 &dd) {
+    const int gs = kh * S0 + (s < S0 ? s : S0 - 1);
+    const u8 *blk = wcol[j] + (int64_t)(gs >> 2) * 210;
+    const int half = (gs >> 1) & 1, jh = gs & 1;
+    qa = ld16u(blk + 64 * half + 16 * h);
+    qb = ld16u(blk + 64 * half + 32 + 16 * h);
+    qh = ld16u(blk + 128 + 32 * half + 16 * h);
+    sc = ld4u(blk + 192 + 8 * half + 4 * jh);
+    dd = *reinterpret_cast<const u16 *>(blk + 208);
   };
   auto b_head = [&](int j, int s) -> uint4 {
     return ld16(wcol[j] + (int64_t)((kh * S0 + (s < S0 ? s : S0 - 1)) >> 2) * 144);
@@ -276,6 +298,8 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
   // Register rings, DEPTH steps deep: A chunks of steps s+1 .. s+DEPTH, B code/header of steps s .. s+DEPTH-1.
   // Step t lives in slot t % DEPTH; the step loop is unrolled DEPTH times so every slot index is static.
   uint4 aring[DEPTH][4], cring[DEPTH][2], hring[DEPTH][2];
+  uint4 q6b[DEPTH][2], q6h[DEPTH][2];   // Q6_K: ql of group B and qh (cring holds ql of group A)
+  u32 q6s[DEPTH][2], q6d[DEPTH][2];
   auto load_a = [&](int slot, int st) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) aring[slot][i] = a_load(i, st);
@@ -283,8 +307,12 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
   auto load_b = [&](int slot, int st) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      cring[slot][j] = b_code(j, st);
-      if constexpr (!STAGED) hring[slot][j] = b_head(j, st);
+      if constexpr (Q6) {
+        b_q6(j, st, cring[slot][j], q6b[slot][j], q6h[slot][j], q6s[slot][j], q6d[slot][j]);
+      } else {
+        cring[slot][j] = b_code(j, st);
+        if constexpr (!STAGED) hring[slot][j] = b_head(j, st);
+      }
     }
   };
   load_a(0, 0);
@@ -318,7 +346,13 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
         h2 dsc[2], nmn[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          if constexpr (STAGED) {
+          if constexpr (Q6) {
+            // f16 (d sc, -32 d sc) of the lane's 16-value run: d sc is exact in f32 (S/gen_gemm.py:435-444)
+            const float sv = f16_to_f32(q6d[u][j]) * (float)(signed char)((q6s[u][j] >> (8 * (2 * gl + h))) & 0xFFu);
+            const _Float16 a16 = (_Float16)sv, b16 = (_Float16)(-32.f * sv);
+            dsc[j] = h2{a16, a16};
+            nmn[j] = h2{b16, b16};
+          } else if constexpr (STAGED) {
             const u32 v = gl ? sp[j].y : sp[j].x;
             dsc[j] = as_h2((v & 0xFFFFu) * 0x10001u);
             nmn[j] = as_h2((v >> 16) * 0x10001u);
@@ -332,8 +366,19 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
           f16x8 bf[2], af[2];
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
-            const u32 q0 = s2 ? cring[u][j].z : cring[u][j].x, q1 = s2 ? cring[u][j].w : cring[u][j].y;
-            bf[j] = gl ? deq8<true>(q0, q1, dsc[j], nmn[j]) : deq8<false>(q0, q1, dsc[j], nmn[j]);
+            if constexpr (Q6) {
+              // codes ((ql >> 4 jh) & 15) | (((qh >> (4 jh + 2 gl)) & 3) << 4), four to a dword
+              const uint4 &ql = gl ? q6b[u][j] : cring[u][j];
+              const u32 l0 = s2 ? ql.z : ql.x, l1 = s2 ? ql.w : ql.y;
+              const u32 h0 = s2 ? q6h[u][j].z : q6h[u][j].x, h1 = s2 ? q6h[u][j].w : q6h[u][j].y;
+              const u32 ls = 4u * (u32)(page & 1), hs = ls + 2u * (u32)gl;
+              const u32 c0 = ((l0 >> ls) & 0x0F0F0F0Fu) | (((h0 >> hs) & 0x03030303u) << 4);
+              const u32 c1 = ((l1 >> ls) & 0x0F0F0F0Fu) | (((h1 >> hs) & 0x03030303u) << 4);
+              bf[j] = deq8_codes(c0, c1, dsc[j], nmn[j]);
+            } else {
+              const u32 q0 = s2 ? cring[u][j].z : cring[u][j].x, q1 = s2 ? cring[u][j].w : cring[u][j].y;
+              bf[j] = gl ? deq8<true>(q0, q1, dsc[j], nmn[j]) : deq8<false>(q0, q1, dsc[j], nmn[j]);
+            }
           }
           af[0] = *reinterpret_cast<const f16x8 *>(&As[buf][kh][lc][32 * gl + 16 * h + 8 * s2]);
 #pragma unroll
@@ -436,25 +481,29 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
       }
 }
 
-template <int KIND, bool ACC, bool BF16OUT>
+template <int KIND, bool ACC, bool BF16OUT, bool Q6 = false>
 int launch(const Args &a, hipStream_t s) {
   constexpr bool kDenseRows = KIND == kDense || KIND == kSwiglu;
   const dim3 grid((unsigned)(kDenseRows ? 8 * ((a.tiles_total + 7) / 8) : 8 * a.n_blocks * ((a.tiles_m + 7) / 8)));
+  if constexpr (Q6) {
+    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, false, true><<<grid, 256, 0, s>>>(a);
+    return launch_status();
+  }
   if (a.K <= kStagedMaxK) {
     const size_t dyn = (size_t)128 * (a.K / 32) * 4;
     if (dyn > 32768) {   // beyond the default dynamic LDS limit: raise it once
       static bool raised = false;
       if (!raised) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, true>),
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, true, false>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)((size_t)128 * (kStagedMaxK / 32) * 4)) !=
             hipSuccess)
           return QMM_ERR_LAUNCH;
         raised = true;
       }
     }
-    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, true><<<grid, 256, dyn, s>>>(a);
+    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, true, false><<<grid, 256, dyn, s>>>(a);
   } else {
-    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, false><<<grid, 256, 0, s>>>(a);
+    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, false, false><<<grid, 256, 0, s>>>(a);
   }
   return launch_status();
 }
@@ -464,14 +513,15 @@ int launch(const Args &a, hipStream_t s) {
 extern "C" int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, const void *x, int x_dtype,
                         const float *scales, const void *w, const void *w2, void *y, int y_dtype,
                         qmm_stream_t stream) {
-  if (fmt != QMM_Q4_K) return QMM_ERR_FORMAT;
+  if (fmt != QMM_Q4_K && fmt != QMM_Q6_K) return QMM_ERR_FORMAT;
   if (mode != QMM_GEMM_STORE && mode != QMM_GEMM_ACC && mode != QMM_GEMM_SWIGLU) return QMM_ERR_RANGE;
   if (!x || !w || !y || (mode == QMM_GEMM_SWIGLU && !w2)) return QMM_ERR_NULL;
   if (x_dtype != QMM_F16) return QMM_ERR_DTYPE;   // bf16 / f32 rows go through qmm_row_scale_f16 first
   if (y_dtype != QMM_F32 && y_dtype != QMM_BF16) return QMM_ERR_DTYPE;
   if (rows <= 0 || n <= 0 || k <= 0 || k % 256) return QMM_ERR_SHAPE;
   if (rows > (1 << 24) || n > (1 << 24) || k > (1 << 20)) return QMM_ERR_SHAPE;
-  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 4) || (w2 && !aligned(w2, 16))) return QMM_ERR_ALIGN;
+  const int wal = fmt == QMM_Q6_K ? 4 : 16;
+  if (!aligned(x, 16) || !aligned(w, wal) || !aligned(y, 4) || (w2 && !aligned(w2, wal))) return QMM_ERR_ALIGN;
   if (rows * k * 2 >= (1ll << 31)) return QMM_ERR_SHAPE;   // activation rows are addressed by a 32-bit buffer offset
   Args a{};
   a.M = (int)rows; a.N = (int)n; a.K = (int)k;
@@ -480,26 +530,36 @@ extern "C" int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, c
   a.tiles_m = (int)((rows + BM - 1) / BM);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool acc = mode == QMM_GEMM_ACC, bf = y_dtype == QMM_BF16;
+  const bool q6 = fmt == QMM_Q6_K;
   if (mode == QMM_GEMM_SWIGLU) {   // 64 output columns a workgroup: its wave pairs take the gate and the up matrix
     a.tiles_total = a.tiles_m * (int)((n + 63) / 64);
+    if (q6) return bf ? launch<kSwiglu, false, true, true>(a, s) : launch<kSwiglu, false, false, true>(a, s);
     return bf ? launch<kSwiglu, false, true>(a, s) : launch<kSwiglu, false, false>(a, s);
   }
   a.tiles_total = a.tiles_m * (int)((n + 127) / 128);
+  if (q6) {
+    if (acc && bf) return launch<kDense, true, true, true>(a, s);
+    if (acc) return launch<kDense, true, false, true>(a, s);
+    if (bf) return launch<kDense, false, true, true>(a, s);
+    return launch<kDense, false, false, true>(a, s);
+  }
   if (acc && bf) return launch<kDense, true, true>(a, s);
   if (acc) return launch<kDense, true, false>(a, s);
   if (bf) return launch<kDense, false, true>(a, s);
   return launch<kDense, false, false>(a, s);
 }
 
-// The Q4_K path of qmm_moe_grouped (grouped.hip checks the arguments shared with the MXFP4 path).
-int qmm_grouped_q4k(int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
+// The Q4_K / Q6_K path of qmm_moe_grouped (grouped.hip checks the arguments shared with the MXFP4 path).
+int qmm_grouped_q4k(int fmt, int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
                     const int32_t *tile_info, const int32_t *rowmap, const void *x, const float *x_scales,
                     int64_t x_rows, const void *w, const void *w2, const float *bias, const float *bias2, float *y,
                     hipStream_t s) {
   if (k % 256) return QMM_ERR_SHAPE;
   if (x_rows * k * 2 >= (1ll << 31)) return QMM_ERR_SHAPE;   // activation rows are addressed by a 32-bit buffer offset
-  if (!aligned(x, 16) || !aligned(w, 16) || (w2 && !aligned(w2, 16))) return QMM_ERR_ALIGN;
-  const int64_t RB = k / 256 * 144;
+  const bool q6 = fmt == QMM_Q6_K;
+  const int wal = q6 ? 4 : 16;
+  if (!aligned(x, 16) || !aligned(w, wal) || (w2 && !aligned(w2, wal))) return QMM_ERR_ALIGN;
+  const int64_t RB = k / 256 * (q6 ? 210 : 144);
   Args a{};
   a.M = (int)(max_tiles * BM); a.N = (int)n; a.K = (int)k;
   a.x16 = static_cast<const _Float16 *>(x); a.scales = x_scales; a.x_rows = (int)x_rows;
@@ -514,11 +574,11 @@ int qmm_grouped_q4k(int mode, int fused, int act, int64_t max_tiles, int64_t k, 
     a.n_blocks = (int)((n + 63) / 64);
     a.tiles_m = (int)max_tiles;
     a.tiles_total = (int)max_tiles * a.n_blocks;
-    return launch<kGU, false, false>(a, s);
+    return q6 ? launch<kGU, false, false, true>(a, s) : launch<kGU, false, false>(a, s);
   }
   a.ebytes = RB * n;
   a.n_blocks = (int)((n + 127) / 128);
   a.tiles_m = (int)max_tiles;
   a.tiles_total = (int)max_tiles * a.n_blocks;
-  return launch<kDN, false, false>(a, s);
+  return q6 ? launch<kDN, false, false, true>(a, s) : launch<kDN, false, false>(a, s);
 }

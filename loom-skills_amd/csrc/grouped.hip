@@ -2,7 +2,7 @@
 // gemm_q4k.hip) and MXFP4 split-plane / MFMA-tiled (scaled f8f6f4 MFMA, grouped_mxfp4.hip) kernels.
 #include "common.hpp"
 
-int qmm_grouped_q4k(int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
+int qmm_grouped_q4k(int fmt, int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
                     const int32_t *tile_info, const int32_t *rowmap, const void *x, const float *x_scales,
                     int64_t x_rows, const void *w, const void *w2, const float *bias, const float *bias2, float *y,
                     hipStream_t s);
@@ -17,7 +17,7 @@ extern "C" int qmm_moe_grouped(int fmt, int mode, int fused, int act, int64_t ma
                                const void *ws2, const float *bias, const float *bias2, float *y,
                                qmm_stream_t stream) {
   using namespace qmm;
-  if (fmt != QMM_Q4_K && fmt != QMM_MXFP4S && fmt != QMM_MXFP4T) return QMM_ERR_FORMAT;
+  if (fmt != QMM_Q4_K && fmt != QMM_Q6_K && fmt != QMM_MXFP4S && fmt != QMM_MXFP4T) return QMM_ERR_FORMAT;
   if (mode != 0 && mode != 1) return QMM_ERR_RANGE;
   if (act != QMM_ACT_SILU && act != QMM_ACT_SWIGLU_OAI) return QMM_ERR_RANGE;
   if (E <= 0 || E > 1024 || KU <= 0 || KU > 8) return QMM_ERR_RANGE;
@@ -27,9 +27,9 @@ extern "C" int qmm_moe_grouped(int fmt, int mode, int fused, int act, int64_t ma
   if (x_rows <= 0 || (mode == 1 && x_rows < max_tiles * 64)) return QMM_ERR_SHAPE;
   if (!aligned(y, 4) || !aligned(bias, 4) || !aligned(bias2, 4)) return QMM_ERR_ALIGN;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (fmt == QMM_Q4_K) {
+  if (fmt == QMM_Q4_K || fmt == QMM_Q6_K) {
     if (x_dtype != QMM_F16) return QMM_ERR_DTYPE;
-    return qmm_grouped_q4k(mode, fused, act, max_tiles, k, n, E, KU, tile_info, rowmap, x,
+    return qmm_grouped_q4k(fmt, mode, fused, act, max_tiles, k, n, E, KU, tile_info, rowmap, x,
                            static_cast<const float *>(x_scales), x_rows, w, w2, bias, bias2, y, s);
   }
   if (x_dtype != QMM_MXFP8) return QMM_ERR_DTYPE;

@@ -355,23 +355,24 @@ def _route(x, logits, KU, gating, norm, scale, bias, router, down_scale, info=No
 
 def moe_prefill(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=None, ws_gate=None, ws_down=None,
                 ws_up=None, fused=False, act="silu", scale=1.0, bias=None, router=None, expert_bias=None,
-                down_scale=None, y=None, sg=None):
+                down_scale=None, y=None, sg=None, fmt_down=None):
     """The reference's prefill MoE chain (moe_routed with t >= 64, S/gen_llm.py:5324-5385): route, bucket into
     64-row expert tiles, grouped gate/up GEMM with the activation, grouped down GEMM, combine.
     q4_k: activations row-scaled to f16 (g_row_scale_f16[_tiles]); mxfp4s / mxfp4t: quantized to MXFP8.
     x bf16 / f32 [T, H]; logits f32 [T, E], or None with router (the weight f32 / bf16 [E, H]); expert_bias
     (bg [E, FE], bu [E, FE], bd [E, H]) or None; down_scale f32 [E] or None; y: None (y = routed output), or the
-    shared experts' output the routed output is added to (scaled first by sg, the shared gate, when given).
+    shared experts' output the routed output is added to (scaled first by sg, the shared gate, when given);
+    fmt_down: the down tensor's format when it differs (q4_k gate / up with q6_k down, the Q4_K_M expert layout).
     Returns (y f32 [T, H], intermediates dict)."""
     ids, wts, logits = _route(x, logits, KU, gating, norm, scale, bias, router, down_scale)
     bg, bu, bd = expert_bias if expert_bias is not None else (None, None, None)
     tile_info, rowmap, pos = moe_bucket(ids, E)
-    if fmt == "q4_k":
+    if fmt in ("q4_k", "q6_k"):
         x16, xs = row_scale_f16(x)
-        a = moe_grouped("q4_k", "gu", tile_info, rowmap, x16, w_gate, FE, H, E, KU, w2=w_up, x_scales=xs,
+        a = moe_grouped(fmt, "gu", tile_info, rowmap, x16, w_gate, FE, H, E, KU, w2=w_up, x_scales=xs,
                         fused=fused, act=act, bias=bg, bias2=bu)
         a16, as_ = row_scale_f16(a, tile_info=tile_info)
-        ys = moe_grouped("q4_k", "dn", tile_info, rowmap, a16, w_down, H, FE, E, KU, x_scales=as_, bias=bd)
+        ys = moe_grouped(fmt_down or fmt, "dn", tile_info, rowmap, a16, w_down, H, FE, E, KU, x_scales=as_, bias=bd)
     elif fmt in ("mxfp4s", "mxfp4t"):
         # the gate/up GEMM writes its activation as MXFP8 directly (the down GEMM's A operand)
         x8, xs = quant_mxfp8(x)
@@ -411,13 +412,13 @@ GEMM_MIN_TOKENS = 64   # %gemm: epochs of 64+ tokens take the GEMM / grouped cha
 
 def linear(fmt, x, w, n, k, y=None, mode="store", ws=None, w2=None):
     """Projection y (+)= x W^T, or swiglu y = silu(x W^T) (x W2^T), with the reference's per-epoch choice (linear,
-    S/gen_llm.py:4568-4625): the prefill GEMM for 64+ tokens (Q4_K; the activation is row-scaled to f16 first), else
+    S/gen_llm.py:4568-4625): the prefill GEMM for 64+ tokens (Q4_K, Q6_K; the activation is row-scaled to f16 first), else
     the decode GEMV. y is f32."""
     if mode not in ("store", "acc", "swiglu"):
         raise ValueError(f"linear mode {mode}")
     if mode == "swiglu" and w2 is None:
         raise ValueError("swiglu needs the up matrix w2")
-    if x.shape[0] >= GEMM_MIN_TOKENS and fmt == "q4_k":
+    if x.shape[0] >= GEMM_MIN_TOKENS and fmt in ("q4_k", "q6_k"):
         return gemm(fmt, mode, x, w, n, k, w2=w2, y=y)
     if mode == "swiglu":
         return mv_swiglu(fmt, w, w2, x, n, k, y=y)

@@ -150,6 +150,8 @@ def test_argument_validation_without_a_device(lib):
     assert lib.qmm_mv(6, 256, 4, 1, 0, fake, 0, odd, n, fake, n) == st["QMM_ERR_ALIGN"]
     assert lib.qmm_mv_q8(6, 256, 4, 1, 0, fake, 4, odd, fake, n) == st["QMM_ERR_ALIGN"]
     assert lib.qmm_dequant(6, fake, n, 4, 320, fake, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_gemm(6, 0, 64, 256, 64, fake, 1, n, odd, n, fake, 0, n) == st["QMM_ERR_ALIGN"]
+    assert lib.qmm_gemm(2, 0, 64, 256, 64, fake, 1, n, fake, n, fake, 0, n) == st["QMM_ERR_FORMAT"]
     # router / shared gate / wscale / gated combine
     assert lib.qmm_moe_route(4, 2882, 32, 4, 3, 0, ctypes.c_float(1), fake, 0, fake, 0, n, n, fake, fake, fake,
                              n) == st["QMM_ERR_SHAPE"]                        # H % 4

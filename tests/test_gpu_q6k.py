@@ -135,3 +135,69 @@ def test_moe_decode_q4_k_gate_up_q6_k_down(dev, T):
 
     want, _ = ref.moe(bf16_values(xb), eids, ewts, gate_up, down)
     assert_close_rel_l2(host(y), want, 1e-3, f"q4_k/q6_k moe decode T={T}")
+
+
+@pytest.mark.parametrize("M,N,K,mode,out", [
+    (512, 4096, 12288, "store", "bf16"),   # Qwen3-8B ffn_down at a 512-token prefill
+    (100, 200, 768, "store", "f32"),       # rows of 3 super-blocks: every other block 2 bytes off
+    (64, 128, 2816, "acc", "f32"),
+    (70, 96, 512, "swiglu", "f32"),
+])
+def test_gemm_q6_k(dev, M, N, K, mode, out):
+    """g_gemm_q6_k_store (the reference's default GEMM formats, S/gen_gemm.py:2187): weights staged to f16 as
+    fma_f16(f16(q), f16(d sc), f16(-32 d sc)) (S/gen_gemm.py:369-444), f16 row-scaled activations, fp32 accumulation.
+    Oracle: float64 X16 W^T inv with W exactly dequantized (as the Q4_K GEMM), rel-L2 1e-3."""
+    import torch
+    from qmm import synth
+    ops = _ops()
+    rng = np.random.default_rng(M + N + K)
+    w = synth.q6_k_weights(rng, N, K)
+    xt, xv = _x(rng, M, K, "bf16", dev)
+    xr = ref.f16_rows(xv)
+    W = of.dequant_q6_k(w, N, K)
+    dt = torch.bfloat16 if out == "bf16" else torch.float32
+    if mode == "swiglu":
+        w2 = synth.q6_k_weights(rng, N, K)
+        y = ops.gemm("q6_k", "swiglu", xt, dev_u8(w, dev), N, K, w2=dev_u8(w2, dev))
+        want = ref.silu_mul(ref.gemv(xr, W), ref.gemv(xr, of.dequant_q6_k(w2, N, K)))
+    elif mode == "acc":
+        y0 = rng.standard_normal((M, N)).astype(np.float32)
+        y = dev_f32(y0, dev)
+        ops.gemm("q6_k", "acc", xt, dev_u8(w, dev), N, K, y=y)
+        want = y0 + ref.gemv(xr, W)
+    else:
+        y = ops.gemm("q6_k", "store", xt, dev_u8(w, dev), N, K, out_dtype=dt)
+        want = ref.gemv(xr, W)
+    got = host(y)
+    torch.cuda.synchronize()
+    assert_close_rel_l2(got, want, 1e-3 if out == "f32" else 4e-3, f"q6_k gemm {mode} {M}x{N}x{K}")
+
+
+def test_moe_prefill_q4_k_gate_up_q6_k_down(dev):
+    """The Qwen3-30B-A3B Q4_K_M expert layout at prefill (T = 64 takes the grouped chain): grouped Q4_K gate / up,
+    grouped Q6_K down (K = 768, misaligned blocks)."""
+    import torch
+    from qmm import synth
+    ops = _ops()
+    E, KU, H, FE, T = 128, 8, 2048, 768, 64
+    rng = np.random.default_rng(77)
+    wg, wu = synth.q4_k_weights(rng, E * FE, H), synth.q4_k_weights(rng, E * FE, H)
+    wd = synth.q6_k_weights(rng, E * H, FE)
+    xb = synth.to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32))
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    y, mid = ops.moe_prefill("q4_k", dev_bf16(xb, dev), dev_f32(logits, dev), E, KU, H, FE, 1, True,
+                             w_gate=dev_u8(wg, dev), w_up=dev_u8(wu, dev), w_down=dev_u8(wd, dev), fmt_down="q6_k")
+    torch.cuda.synchronize()
+    eids, ewts = ref.route(logits, KU, 1, True)
+    np.testing.assert_array_equal(host(mid["ids"]), eids)
+    rbg, rbd = of.row_bytes("q4_k", H), of.row_bytes("q6_k", FE)
+
+    def gate_up(e):
+        return (of.dequant_q4_k(wg[e * FE * rbg:(e + 1) * FE * rbg], FE, H),
+                of.dequant_q4_k(wu[e * FE * rbg:(e + 1) * FE * rbg], FE, H))
+
+    def down(e):
+        return of.dequant_q6_k(wd[e * H * rbd:(e + 1) * H * rbd], H, FE)
+
+    want, _ = ref.moe(bf16_values(xb), eids, ewts, gate_up, down, x_round=ref.f16_rows, act_round=ref.f16_rows)
+    assert_close_rel_l2(host(y), want, 1e-3, "q4_k/q6_k moe prefill")
