@@ -315,13 +315,21 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
       }
     }
   };
+  // The prologue issues its loads in the loop's own order (a step issues the weights of step s + DEPTH, then the
+  // activations of step s + 1 + DEPTH). Vector loads complete in issue order for s_waitcnt, and the compiler places
+  // one wait per wait point valid on both paths into the loop header, so a prologue with another order (all
+  // activations first, say) would make the loop's waits stricter than the loop needs and drain the ring.
+  static_assert(DEPTH >= 2 && DEPTH % 2 == 0, "activation slots 0 and 1 hold steps 0 and 1 at once");
+  load_b(0, 0);
   load_a(0, 0);
+  load_a(1, 1);
 #pragma unroll
   for (int i = 0; i < 4; ++i) *a_dst(i, 0) = aring[0][i];
 #pragma unroll
-  for (int u = 1; u <= DEPTH; ++u) load_a(u % DEPTH, u);
-#pragma unroll
-  for (int u = 0; u < DEPTH; ++u) load_b(u, u);
+  for (int u = 1; u < DEPTH; ++u) {
+    load_b(u, u);
+    load_a((u + 1) % DEPTH, u + 1);
+  }
   __syncthreads();
 
   // The step count is rounded up to a multiple of DEPTH; steps past S0 get zero weights (no contribution), so the

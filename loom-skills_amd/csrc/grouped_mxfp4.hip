@@ -53,13 +53,13 @@ namespace {
 // barrier each). The down GEMM streams one weight column block per wave (the gate/up GEMM two), so it needs a deeper
 // ring to keep as many bytes in flight.
 #ifndef QMM_MX_DEPTH_GU
-#define QMM_MX_DEPTH_GU 1
+#define QMM_MX_DEPTH_GU 2
 #endif
 #ifndef QMM_MX_SUB_GU
 #define QMM_MX_SUB_GU 2
 #endif
 #ifndef QMM_MX_DEPTH_DN
-#define QMM_MX_DEPTH_DN 1
+#define QMM_MX_DEPTH_DN 2
 #endif
 #ifndef QMM_MX_SUB_DN
 #define QMM_MX_SUB_DN 2
@@ -147,7 +147,11 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
   constexpr int BN = 128;                   // output columns per workgroup
   constexpr bool GU = KIND != kDN;
   constexpr int NJ = GU ? 2 : 1;             // 32-column weight blocks per wave (gu: gate and up)
-  __shared__ __align__(16) u8 As[2][BM][APITCH];
+  // the activation double buffer; kGU8 reuses it after the loop for its f32 output, 32 rows at a time
+  constexpr int OPITCH = BN + 4;   // floats per output row: the 4-float skew spreads a column's rows over the banks
+  __shared__ __align__(16) u8 smem[2 * BM * APITCH];
+  static_assert(32 * OPITCH * 4 <= sizeof(smem), "epilogue staging");
+  auto As = reinterpret_cast<u8 (*)[BM][APITCH]>(smem);
   __shared__ int src_row[BM];
   __shared__ int live_end;
   // E8M0 scales staged once: the tile's 64 activation rows and, for kSplit, the block's weight columns (gu: 128 gate
@@ -249,9 +253,8 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
       for (int j = 0; j < NJ; ++j) sring[slot][j] = *reinterpret_cast<const u32 *>(wcs[j] + (int64_t)g * 256);
     }
   };
-  // the weight stream: the first DEPTH super-steps
-  for_slots([&](auto uc) { constexpr int u = decltype(uc)::value; load_b(u, u); },
-            std::make_integer_sequence<int, DEPTH>{});
+  // the weight stream: the first super-step (the others follow the activation staging, below)
+  load_b(0, 0);
 
   int my_src = -1;
   if (tid < BM) {
@@ -289,20 +292,33 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
   // the first activation chunk and the activation rows' scales (a gathered row each; up to K = 4096 one batch of
   // loads) are issued together and land one round trip after the first weights; then the chunk is staged and the
   // next ones go into the ring. kSplit also stages the weight column blocks' scales.
+  //
+  // The loads still in flight when the loop starts are issued in the order one loop iteration issues them
+  // (activations of super-step j + 1 + DEPTH, then weights of super-step j + DEPTH, for j = -DEPTH + 1 .. -1). The
+  // compiler places one s_waitcnt per wait point, valid on both paths into the loop header; a prologue whose last
+  // loads came in another order would make the loop's waits stricter than the loop itself needs (in the extreme,
+  // every weight load of the previous super-step waited on before the activations are staged).
   load_a(0, 0);
+  if constexpr (DEPTH > 1) load_a(1, 1);
   batched_copy<16>(reinterpret_cast<u16 *>(Asc), (int64_t)BM * (SK / 2), tid, [&](int64_t i) {
     const int r = (int)(i / (SK / 2)), q = (int)(i % (SK / 2));
     const int sr = src_row[r] >= 0 ? src_row[r] : 0;
     return reinterpret_cast<const u16 *>(a.xs + (int64_t)sr * SK)[q];
   });
-  stage(0, 0);
-  for_slots([&](auto uc) { constexpr int u = decltype(uc)::value; load_a((u + 1) % DEPTH, u + 1); },
-            std::make_integer_sequence<int, DEPTH>{});
   if constexpr (LAYOUT == kSplit) {
     const int cols = N - n0 < BN ? N - n0 : BN;   // columns past N are never stored
 #pragma unroll
     for (int m = 0; m < NJ; ++m) copy_to_lds(Wsc + m * BN * SK, sbj[m] + (int64_t)n0 * SK, (int64_t)cols * SK, tid);
   }
+  stage(0, 0);
+  if constexpr (DEPTH == 1) load_a(0, 1);
+  for_slots([&](auto uc) {
+    constexpr int j = decltype(uc)::value;
+    if constexpr (j > 0) {
+      load_a((j + 1) % DEPTH, j + 1);
+      load_b(j, j);
+    }
+  }, std::make_integer_sequence<int, DEPTH>{});
   __syncthreads();
 
   // The super-step count is rounded up to a multiple of DEPTH. A padding chunk (c >= C) runs with both E8M0 scales
@@ -351,9 +367,14 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
           acc[1][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af, bf[j], acc[1][j], 0, 4, 0, sa, 0, sb[j]);
       }
     }
-    load_b(u, st + DEPTH);
+    // Vector loads complete in issue order for the s_waitcnt counter, so a wait on a load also waits on every load
+    // issued before it. The activation chunk staged here (issued DEPTH super-steps ago, ahead of that super-step's
+    // weights) is therefore waited on before this super-step's loads are issued, and its own activation load goes
+    // out ahead of its weight load: that wait never covers the weights of the last DEPTH - 1 super-steps, which stay
+    // in flight across it.
     stage(nx, buf ^ 1);
     load_a(nx, st + 1 + DEPTH);
+    load_b(u, st + DEPTH);
     __syncthreads();
   };
   const int S = (C + kSub - 1) / kSub;
@@ -362,43 +383,45 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
     for_steps(step, s0, std::make_integer_sequence<int, DEPTH>{});
 
   if constexpr (KIND == kGU8) {
-    // The activation quantized to MXFP8 in registers, as qmm_quant_mxfp8 quantizes it: the 32 columns of a row's
-    // block are the 32 lanes of a half-wave, so its maximum is a butterfly over lane bits 0-4 (DPP and ds_swizzle
-    // partners; every lane of the half ends with the maximum). Codes and scales go
-    // through LDS (the activation buffers are free after the loop's last barrier) and leave as whole 16-byte pieces
-    // of each row. Dead rows quantize zeros: codes 0, scale byte 0.
-    static_assert(sizeof(As) >= BM * (BN + 16) + BM * 4, "epilogue staging");
-    u8 *Ot = &As[0][0][0];                    // [64][BN + 16] codes
-    u8 *Osc = Ot + BM * (BN + 16);            // [64][4] scale bytes
+    // The activation quantized to MXFP8 as qmm_quant_mxfp8 quantizes it. Per 32-row half of the tile, the f32
+    // activations go to LDS (the activation buffers are free after the loop's last barrier); then threads 2 b and
+    // 2 b + 1 own 32-value block b (row b / 4, columns 32 (b % 4) .. +31), 16 values each: their maximum is one lane
+    // exchange, and each thread's 16 E4M3 codes leave as one 16-byte store. Dead rows quantize zeros: codes 0, scale
+    // byte 0.
+    float *Of = reinterpret_cast<float *>(smem);
     const int64_t bo = (int64_t)expert * N + (col < N ? col : N - 1);
     const float bg = a.bias ? a.bias[bo] : 0.f, bu = a.bias2 ? a.bias2[bo] : 0.f;
+    const int cols = N - n0 < BN ? N - n0 : BN;   // a multiple of 32
+    const int qrow = tid >> 3, blk = (tid >> 1) & 3, part = tid & 1;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 2; ++i) {
+      if (i) __syncthreads();   // the first half's reads are done before the second half overwrites them
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int lr = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-        const float v = src_row[lr] >= 0 ? act_fn(a.act, acc[i][0][r] + bg, acc[i][1][r] + bu) : 0.f;
-        float m = fabsf(v);
-        m = fmaxf(m, xshfl<1>(m));
-        m = fmaxf(m, xshfl<2>(m));
-        m = fmaxf(m, xshfl<4>(m));
-        m = fmaxf(m, xshfl<8>(m));
-        m = fmaxf(m, xshfl<16>(m));
-        const int sx = mxfp8_exponent(m);
-        Ot[lr * (BN + 16) + 32 * wave + lc] = (u8)(e4m3_pack2<false>(v, 0.f, sx, 0) & 0xFF);
-        if (lc == 0) Osc[lr * 4 + wave] = (u8)(sx + 127);
+        const int lr = 8 * (r >> 2) + 4 * h + (r & 3);
+        Of[lr * OPITCH + 32 * wave + lc] =
+            src_row[32 * i + lr] >= 0 ? act_fn(a.act, acc[i][0][r] + bg, acc[i][1][r] + bu) : 0.f;
       }
-    __syncthreads();
-    const int cols = N - n0 < BN ? N - n0 : BN;   // a multiple of 32
-    for (int q = tid; q < BM * (BN / 16); q += 256) {
-      const int row = q / (BN / 16), piece = q % (BN / 16);
-      if (16 * piece < cols)
-        *reinterpret_cast<v4u *>(a.y8 + (int64_t)(m0 + row) * N + n0 + 16 * piece) =
-            *reinterpret_cast<const v4u *>(Ot + row * (BN + 16) + 16 * piece);
-    }
-    {
-      const int row = tid >> 2, blk = tid & 3;
-      if (32 * blk < cols) a.ys8[(int64_t)(m0 + row) * (N / 32) + n0 / 32 + blk] = Osc[row * 4 + blk];
+      __syncthreads();
+      const f32x4 *src = reinterpret_cast<const f32x4 *>(Of + qrow * OPITCH + 32 * blk + 16 * part);
+      f32x4 v[4];
+      float m = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        v[q] = src[q];
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v[q][0]), fabsf(v[q][1])), fmaxf(fabsf(v[q][2]), fabsf(v[q][3]))));
+      }
+      m = fmaxf(m, xshfl<1>(m));
+      const int sx = mxfp8_exponent(m);
+      v4u code;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        code[q] = (u32)e4m3_pack2<true>(v[q][2], v[q][3], sx, e4m3_pack2<false>(v[q][0], v[q][1], sx, 0));
+      const int64_t orow = m0 + 32 * i + qrow;
+      if (32 * blk < cols) {
+        *reinterpret_cast<v4u *>(a.y8 + orow * N + n0 + 32 * blk + 16 * part) = code;
+        if (!part) a.ys8[orow * (N / 32) + n0 / 32 + blk] = (u8)(sx + 127);
+      }
     }
     return;
   }

@@ -298,3 +298,32 @@ def test_grouped_gate_up_mxfp8_output_equals_quantized_act(dev, T, E, H, FE, til
     np.testing.assert_array_equal(host(s)[used], host(es)[used])
     assert np.all(host(c)[dead] == 0) and np.all(host(s)[dead] == 0)
     assert np.any(host(c)[used & ~dead] != 0)
+
+
+@pytest.mark.parametrize("fmt", ["mxfp4t", "q4_k"])
+def test_moe_prefill_chain_graph_replays_equal_eager(dev, fmt):
+    """The prefill chain captured in one HIP graph (as the benchmark runs it): every replay, with eager work and
+    synchronizations between replays, equals the eager chain bit for bit."""
+    import torch
+    from qmm import synth
+    rng = np.random.default_rng(20261230)
+    E, KU, H, FE, T = (32, 4, 2880, 2880, 256) if fmt == "mxfp4t" else (128, 8, 2048, 768, 64)
+    gating, norm, act = (3, False, "swiglu_oai") if fmt == "mxfp4t" else (1, True, "silu")
+    ex = Experts(dev, "mxfp4" if fmt == "mxfp4t" else "q4_k", rng, E, H, FE, fmt == "mxfp4t")
+    wfmt, kw = ex.device(split=True, tiled=fmt == "mxfp4t")
+    x = dev_bf16(synth.to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32)), dev)
+    logits = dev_f32(rng.standard_normal((T, E)).astype(np.float32), dev)
+    ops = _ops()
+    run = lambda: ops.moe_prefill(wfmt, x, logits, E, KU, H, FE, gating, norm, fused=ex.fused, act=act, **kw)[0]
+    want = host(run())
+    run()   # warm the allocator outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = run()
+    for i in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(host(y).view(np.uint32), want.view(np.uint32), err_msg=f"replay {i}")
+        ops.quant_mxfp8(x)   # eager work between replays
+        torch.cuda.synchronize()
