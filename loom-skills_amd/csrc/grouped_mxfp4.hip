@@ -89,13 +89,18 @@ struct MArgs {
   int n_blocks, max_tiles;
 };
 
+// The sigmoid as v_exp_f32 and v_rcp_f32 (each about 1 ulp; exp overflow gives rcp(inf) = 0, as the division would):
+// the epilogue runs once per output at the very end of every workgroup, where an IEEE division and a range-reduced
+// expf per value are a measurable tail. The outputs are MXFP8-quantized next (3 mantissa bits).
+__device__ __forceinline__ float sigmoid_fast(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+
 __device__ __forceinline__ float act_fn(int act, float g, float u) {
   if (act == QMM_ACT_SWIGLU_OAI) {
     const float xg = fminf(g, 7.0f);
     const float yu = fminf(fmaxf(u, -7.0f), 7.0f);
-    return xg / (1.0f + expf(-1.702f * xg)) * (yu + 1.0f);
+    return xg * sigmoid_fast(1.702f * xg) * (yu + 1.0f);
   }
-  return g / (1.0f + expf(-g)) * u;
+  return g * sigmoid_fast(g) * u;
 }
 
 // f(integral_constant<I>) for I = 0 .. N-1, in order: ring slots as compile-time constants
