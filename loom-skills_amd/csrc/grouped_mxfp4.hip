@@ -50,8 +50,10 @@ using namespace qmm;
 namespace {
 
 // Pipeline shape per kernel: DEPTH super-steps of weight loads in flight, SUB 64-value chunks per super-step (one
-// barrier each). The down GEMM streams one weight column block per wave (the gate/up GEMM two), so it needs a deeper
-// ring to keep as many bytes in flight.
+// barrier each). The down GEMM streams one weight column block per wave (the gate/up GEMM two), so its super-steps
+// are twice as long for as many bytes per barrier. Both epilogues store their outputs nontemporally: every
+// workgroup stores at its very end, and streamed stores drain during the epilogue instead of as dirty L2 lines at the
+// end of the kernel (gate/up -1 us, down -2 us at the gpt-oss-20b shape, T = 256).
 #ifndef QMM_MX_DEPTH_GU
 #define QMM_MX_DEPTH_GU 2
 #endif
@@ -62,7 +64,7 @@ namespace {
 #define QMM_MX_DEPTH_DN 2
 #endif
 #ifndef QMM_MX_SUB_DN
-#define QMM_MX_SUB_DN 2
+#define QMM_MX_SUB_DN 4
 #endif
 #ifndef QMM_MX_WAVES
 #define QMM_MX_WAVES 3            // minimum waves per SIMD the register allocation must allow (3 workgroups per CU)
@@ -424,7 +426,7 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
         code[q] = (u32)e4m3_pack2<true>(v[q][2], v[q][3], sx, e4m3_pack2<false>(v[q][0], v[q][1], sx, 0));
       const int64_t orow = m0 + 32 * i + qrow;
       if (32 * blk < cols) {
-        *reinterpret_cast<v4u *>(a.y8 + orow * N + n0 + 32 * blk + 16 * part) = code;
+        __builtin_nontemporal_store(code, reinterpret_cast<v4u *>(a.y8 + orow * N + n0 + 32 * blk + 16 * part));
         if (!part) a.ys8[orow * (N / 32) + n0 / 32 + blk] = (u8)(sx + 127);
       }
     }
@@ -443,7 +445,7 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
         if constexpr (GU) v = act_fn(a.act, acc[i][0][r] + bg, acc[i][1][r] + bu);
         else v = acc[i][0][r] + bg;
       }
-      a.y[(int64_t)(m0 + lr) * N + col] = v;
+      __builtin_nontemporal_store(v, a.y + (int64_t)(m0 + lr) * N + col);
     }
 }
 
