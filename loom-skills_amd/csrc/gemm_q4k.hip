@@ -119,18 +119,19 @@ struct Args {
 // pairs per column with one 8-byte LDS read instead of loading and decoding the super-block header again.
 constexpr int kStagedMaxK = 6144;
 
-template <int KIND, bool ACC, bool BF16OUT, int DEPTH, bool STAGED, bool Q6>
-__global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
+template <int KIND, bool ACC, bool BF16OUT, int DEPTH, bool STAGED, bool Q6, int KS>
+__global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
+  constexpr int NT = 128 * KS;   // threads: 2 column halves (or matrices) x KS K-parts
   static_assert(!(Q6 && STAGED), "Q6_K scales are read with the codes");
   constexpr bool kTwoW = KIND == kGU || KIND == kSwiglu;        // two weight matrices (gate, up): wave pairs
   constexpr bool kDenseRows = KIND == kDense || KIND == kSwiglu;  // rows m0 .. m0 + 63 of x, tiles row-major
   constexpr int BN = kTwoW ? 64 : 128;
   extern __shared__ __align__(16) u32 scl[];   // STAGED: [128 columns][K / 32] (dsc | nmn << 16)
-  __shared__ __align__(16) _Float16 As[2][2][BM][APITCH];   // [buffer][K-half][row][k]
+  __shared__ __align__(16) _Float16 As[2][KS][BM][APITCH];   // [buffer][K-part][row][k]
   __shared__ int src_row[BM];
   __shared__ float rinv[BM];   // the row's inverse activation scale (1 without scales)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int sel = wave & 1, kh = wave >> 1;   // sel: N-half (dense, dn) or matrix (gu: 0 gate, 1 up)
+  const int sel = wave & 1, kh = wave >> 1;   // sel: N-half (dense, dn) or matrix (gu: 0 gate, 1 up); kh: K-part
   const int M = a.M, N = a.N, K = a.K;
 
   int m0, n0, expert = 0;
@@ -181,9 +182,9 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
   const bool upper = __syncthreads_or(tid >= 32 && my_src >= 0) != 0;
 
   const int64_t RB = (int64_t)K / 256 * (Q6 ? 210 : 144);
-  const int S = K / KSTEP, S0 = S / 2;
+  const int S = K / KSTEP, S0 = S / KS;
 
-  // ---- A staging map: chunk c = i * 256 + tid of 16 bytes; K-half, row, 16-byte column. Loads are unconditional
+  // ---- A staging map: chunk c = i * NT + tid of 16 bytes; K-part, row, 16-byte column. Loads are unconditional
   // (dead rows read activation row 0 and their outputs are zeroed; steps past S0 reload step S0 - 1 and get zero
   // weights in the math).
   // The loads go through a buffer resource over the activation rows: a dead row's offset lies past its end
@@ -194,7 +195,7 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
   u32 aoff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int c = i * 256 + tid, ckh = c >> 9, row = (c >> 3) & 63, col = c & 7;
+    const int c = i * NT + tid, ckh = c >> 9, row = (c >> 3) & 63, col = c & 7;
     const int src = src_row[row];
     aoff[i] = src >= 0 ? (u32)(((int64_t)src * K + (int64_t)ckh * S0 * KSTEP + col * 8) * 2) : 0x80000000u;
   }
@@ -204,7 +205,7 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
     return make_uint4(v.x, v.y, v.z, v.w);
   };
   auto a_dst = [&](int i, int buf) -> uint4 * {
-    const int c = i * 256 + tid, ckh = c >> 9, row = (c >> 3) & 63, col = c & 7;
+    const int c = i * NT + tid, ckh = c >> 9, row = (c >> 3) & 63, col = c & 7;
     return reinterpret_cast<uint4 *>(&As[buf][ckh][row][col * 8]);
   };
 
@@ -251,11 +252,11 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
     // every header of the workgroup's columns, kHdrBatch loads in flight per thread before any is decoded
     constexpr int kHdrBatch = 4;
     const int nh = 128 * (K / 256);
-    for (int b0 = 0; b0 < nh; b0 += kHdrBatch * 256) {
+    for (int b0 = 0; b0 < nh; b0 += kHdrBatch * NT) {
       uint4 hd[kHdrBatch];
 #pragma unroll
       for (int q = 0; q < kHdrBatch; ++q) {
-        int i = b0 + tid + 256 * q;
+        int i = b0 + tid + NT * q;
         i = i < nh ? i : nh - 1;
         const int cl = i / (K / 256), b = i % (K / 256);
         const int msel = cl >> 6;
@@ -274,7 +275,7 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
       }
 #pragma unroll
       for (int q = 0; q < kHdrBatch; ++q) {
-        const int i = b0 + tid + 256 * q;
+        const int i = b0 + tid + NT * q;
         if (i >= nh) continue;
         const int cl = i / (K / 256), b = i % (K / 256);
 #pragma unroll
@@ -333,8 +334,8 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
   __syncthreads();
 
   // The step count is rounded up to a multiple of DEPTH; steps past S0 get zero weights (no contribution), so the
-  // loop body has no data-dependent branch and every wave runs the same barriers. Both K-halves have S0 steps
-  // (K is a multiple of 256, so K / 64 is even).
+  // loop body has no data-dependent branch and every wave runs the same barriers. Every K-part has S0 steps
+  // (K is a multiple of 256, so K / 64 is a multiple of 4).
   const int SP = (S0 + DEPTH - 1) / DEPTH * DEPTH;
   for (int s0 = 0; s0 < SP; s0 += DEPTH) {
 #pragma unroll
@@ -408,26 +409,34 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
     }
   }
 
-  // ---- sum the K-halves through LDS (K-half 1 hands its partial to K-half 0)
-  float *red = reinterpret_cast<float *>(&As[0][0][0][0]);   // [sel][64 values][64 lanes]
+  // ---- sum the K-parts through LDS in a fixed tree: with four parts, 2 and 3 hand theirs to 0 and 1, then 1 to 0
+  float *red = reinterpret_cast<float *>(&As[0][0][0][0]);   // [slot][sel][64 values][64 lanes]
+  static_assert(sizeof(As) >= (KS / 2) * 2 * 64 * 64 * 4, "K-part reduction staging");
   auto red_at = [&](int sl, int i, int j, int r) -> float & {
     return red[(sl * 64 + (i * 2 + j) * 16 + r) * 64 + lane];
   };
-  if (kh == 1) {
+  auto hand = [&](int from, int to) __attribute__((always_inline)) {   // parts [from, 2 from) add into [to, ..)
+    if (kh >= from && kh < 2 * from) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) red_at(sel, i, j, r) = acc[i][j][r];
-  }
-  __syncthreads();
+          for (int r = 0; r < 16; ++r) red_at(2 * (kh - from) + sel, i, j, r) = acc[i][j][r];
+    }
+    __syncthreads();
+    if (kh < to) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] += red_at(sel, i, j, r);
+          for (int r = 0; r < 16; ++r) acc[i][j][r] += red_at(2 * kh + sel, i, j, r);
+    }
+    __syncthreads();
+  };
+  if constexpr (KS == 4) hand(2, 2);
+  hand(1, 1);
 
   if constexpr (kTwoW) {
     // the up wave (K-half 0) hands its result to the gate wave; every wave takes part in the barriers
@@ -443,7 +452,7 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
     __syncthreads();
     if (sel == 1) return;
   }
-  if (kh == 1) return;
+  if (kh != 0) return;
 
   // ---- epilogue
   float *yf = static_cast<float *>(a.y);
@@ -489,29 +498,36 @@ __global__ __launch_bounds__(256, 1) void q4k_mfma_kernel(Args a) {
       }
 }
 
+// Dense Q4_K rows (the prefill GEMM) run eight waves a workgroup, K in four parts: a 64 x 128 tile's workgroup then
+// has two waves a SIMD, so one wave's dequantization overlaps the other's MFMAs (the grid of a 512-row GEMM is one
+// workgroup a CU). The grouped GEMMs keep two K-parts (their expert tiles are many and their K short), and so does
+// Q6_K.
 template <int KIND, bool ACC, bool BF16OUT, bool Q6 = false>
 int launch(const Args &a, hipStream_t s) {
   constexpr bool kDenseRows = KIND == kDense || KIND == kSwiglu;
+  constexpr int KS = kDenseRows && !Q6 ? 4 : 2;   // Q6_K's wider rings would spill at two waves a SIMD
+  // staged scale tables beside the K-parts' activation buffers: 16 K bytes, within 160 KB of LDS
+  constexpr int kMaxK = KS == 4 ? 5120 : kStagedMaxK;
   const dim3 grid((unsigned)(kDenseRows ? 8 * ((a.tiles_total + 7) / 8) : 8 * a.n_blocks * ((a.tiles_m + 7) / 8)));
   if constexpr (Q6) {
-    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, false, true><<<grid, 256, 0, s>>>(a);
+    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, false, true, KS><<<grid, 128 * KS, 0, s>>>(a);
     return launch_status();
   }
-  if (a.K <= kStagedMaxK) {
+  if (a.K <= kMaxK) {
     const size_t dyn = (size_t)128 * (a.K / 32) * 4;
     if (dyn > 32768) {   // beyond the default dynamic LDS limit: raise it once
       static bool raised = false;
       if (!raised) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, true, false>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)((size_t)128 * (kStagedMaxK / 32) * 4)) !=
+        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, true, false, KS>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)((size_t)128 * (kMaxK / 32) * 4)) !=
             hipSuccess)
           return QMM_ERR_LAUNCH;
         raised = true;
       }
     }
-    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, true, false><<<grid, 256, dyn, s>>>(a);
+    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, true, false, KS><<<grid, 128 * KS, dyn, s>>>(a);
   } else {
-    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, false, false><<<grid, 256, 0, s>>>(a);
+    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, false, false, KS><<<grid, 128 * KS, 0, s>>>(a);
   }
   return launch_status();
 }
