@@ -115,7 +115,7 @@ struct Args {
 };
 
 // Scale tables: a workgroup decodes the (d sc, -dmin m) f16 pair of every sub-block of its 128 weight columns once
-// into LDS (4 bytes per sub-block, 16 K bytes) when that fits (K <= kStagedMaxK); each step then reads its two
+// into LDS (4 bytes per sub-block, 16 (K + 64) bytes) when that fits (K <= kStagedMaxK); each step then reads its two
 // pairs per column with one 8-byte LDS read instead of loading and decoding the super-block header again.
 constexpr int kStagedMaxK = 6144;
 
@@ -126,7 +126,7 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
   constexpr bool kTwoW = KIND == kGU || KIND == kSwiglu;        // two weight matrices (gate, up): wave pairs
   constexpr bool kDenseRows = KIND == kDense || KIND == kSwiglu;  // rows m0 .. m0 + 63 of x, tiles row-major
   constexpr int BN = kTwoW ? 64 : 128;
-  extern __shared__ __align__(16) u32 scl[];   // STAGED: [128 columns][K / 32] (dsc | nmn << 16)
+  extern __shared__ __align__(16) u32 scl[];   // STAGED: [128 columns][K / 32 + 2] (dsc | nmn << 16)
   __shared__ __align__(16) _Float16 As[2][KS][BM][APITCH];   // [buffer][K-part][row][k]
   __shared__ int src_row[BM];
   __shared__ float rinv[BM];   // the row's inverse activation scale (1 without scales)
@@ -246,7 +246,9 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
   auto b_head = [&](int j, int s) -> uint4 {
     return ld16(wcol[j] + (int64_t)((kh * S0 + (s < S0 ? s : S0 - 1)) >> 2) * 144);
   };
-  const int SB = K / 32;   // sub-blocks per column
+  // sub-blocks per column, and the staged table's row pitch in dwords: two more than K / 32 (a multiple of 8), so
+  // the 32 columns a wave reads at once start two banks apart instead of all in one bank
+  const int SB = K / 32, SBP = SB + 2;
   if constexpr (STAGED) {
     // local column cl = sel * 64 + 32 j + lc: dense / dn columns n0 + cl, gu: gate n0 + cl (cl < 64), up n0 + cl - 64
     // every header of the workgroup's columns, kHdrBatch loads in flight per thread before any is decoded
@@ -282,7 +284,7 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
         for (int g = 0; g < 8; ++g) {
           h2 dsc, nmn;
           sub_scale(hd[q], g, dsc, nmn);
-          scl[cl * SB + 8 * b + g] = (u32)__builtin_bit_cast(u16, dsc[0]) | ((u32)__builtin_bit_cast(u16, nmn[0]) << 16);
+          scl[cl * SBP + 8 * b + g] = (u32)__builtin_bit_cast(u16, dsc[0]) | ((u32)__builtin_bit_cast(u16, nmn[0]) << 16);
         }
       }
     }
@@ -348,7 +350,7 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
       u32x2 sp[2];
       if constexpr (STAGED) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) sp[j] = *reinterpret_cast<const u32x2 *>(&scl[(sel * 64 + 32 * j + lc) * SB + 2 * gstep]);
+        for (int j = 0; j < 2; ++j) sp[j] = *reinterpret_cast<const u32x2 *>(&scl[(sel * 64 + 32 * j + lc) * SBP + 2 * gstep]);
       }
 #pragma unroll
       for (int gl = 0; gl < 2; ++gl) {
@@ -506,7 +508,7 @@ template <int KIND, bool ACC, bool BF16OUT, bool Q6 = false>
 int launch(const Args &a, hipStream_t s) {
   constexpr bool kDenseRows = KIND == kDense || KIND == kSwiglu;
   constexpr int KS = kDenseRows && !Q6 ? 4 : 2;   // Q6_K's wider rings would spill at two waves a SIMD
-  // staged scale tables beside the K-parts' activation buffers: 16 K bytes, within 160 KB of LDS
+  // staged scale tables beside the K-parts' activation buffers: 16 (K + 64) bytes, within 160 KB of LDS
   constexpr int kMaxK = KS == 4 ? 5120 : kStagedMaxK;
   const dim3 grid((unsigned)(kDenseRows ? 8 * ((a.tiles_total + 7) / 8) : 8 * a.n_blocks * ((a.tiles_m + 7) / 8)));
   if constexpr (Q6) {
@@ -514,12 +516,12 @@ int launch(const Args &a, hipStream_t s) {
     return launch_status();
   }
   if (a.K <= kMaxK) {
-    const size_t dyn = (size_t)128 * (a.K / 32) * 4;
+    const size_t dyn = (size_t)128 * (a.K / 32 + 2) * 4;
     if (dyn > 32768) {   // beyond the default dynamic LDS limit: raise it once
       static bool raised = false;
       if (!raised) {
         if (hipFuncSetAttribute(reinterpret_cast<const void *>(&q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, true, false, KS>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)((size_t)128 * (kMaxK / 32) * 4)) !=
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)((size_t)128 * (kMaxK / 32 + 2) * 4)) !=
             hipSuccess)
           return QMM_ERR_LAUNCH;
         raised = true;
