@@ -1,32 +1,38 @@
 #!/usr/bin/env python3
 """Throughput of the quantized-weight matmul path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--workload NAME] [--m M] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--workload NAME] [--m M] [--no-cpu] [--no-secondary]
 
-A step is one launch of the hot path over one batch of synthetic input:
+A step is one pass of the hot path over one batch of synthetic input. The default run measures the headline workload
+(`value`), then every other workload of the metric as a compact entry of `secondary` (skipped when --workload names
+one workload, or with --no-secondary):
 
-    q4_k_gemv_q8  (default) Q4_K decode GEMV, W [12288, 4096] (Qwen3-8B FFN gate/up), x bf16 [M, 4096], y f32, on
+    q4_k_gemv_q8  (headline) Q4_K decode GEMV, W [12288, 4096] (Qwen3-8B FFN gate/up), x bf16 [M, 4096], y f32, on
                 the int8-activation path the reference takes by default: the bf16 rows are quantized to Q8_1 inside
                 the kernel and multiplied with exact int32 group dot products; the weights are repacked once (before
-                timing) into the lane-ordered tiled layout (qmm_tile_q4k), a byte permutation of the GGUF blocks
-    q4_k_gemv_q8_gguf the same GEMV reading the GGUF Q4_K blocks as they are
-    q4_k_gemv   the same GEMV on the f16-activation path (x staged as f16, v_dot2_f32_f16)
-    q4_k_gemv_q8p the int8-activation GEMV on its reference boundary: x is the planar Q8_1 buffer qmm_quant_q8 makes
-                (once per layer input, shared by the matvecs that read it), quantized before the timed region
+                timing) into the lane-ordered tiled layout (qmm_tile_q4k), a byte permutation of the GGUF blocks.
+                Secondary at M = 4 and 8.
+    q4_k_swiglu_q8 the int8 swiglu matvec silu(x Wg^T) (x Wu^T), Wg, Wu [12288, 4096] Q4_K tiled, x bf16 [M, 4096]
+    q4_k_gemv_q8_gguf the int8 GEMV reading the GGUF Q4_K blocks as they are
+    q4_k_gemv   the Q4_K GEMV on the f16-activation path (x bf16 staged as f16, v_dot2_f32_f16)
+    q4_k_gemv_q8p the int8 GEMV on its reference boundary: x is the planar Q8_1 buffer qmm_quant_q8 makes
     q4_0_gemv   Q4_0 decode GEMV, W [4096, 4096], x f32 [1, 4096], y f32
     q4_k_gemm   Q4_K prefill GEMM, x bf16 [512, 4096] (row scale to f16, then the MFMA GEMM), W [4096, 4096],
                 y bf16 [512, 4096] (Qwen3-8B attn o_proj)
-    mxfp4_moe   MXFP4 MoE prefill chain at the gpt-oss-20b shape (32 experts, top-4, H = FE = 2880), T tokens
-                (--m, default 256): top-k, bucket, MXFP8 quantize, grouped gate_up (scaled MFMA) + swiglu_oai,
-                quantize, grouped down, combine
+    mxfp4_moe   MXFP4 MoE at the gpt-oss-20b shape (32 experts, top-4, H = FE = 2880), T tokens (--m): T < 64 the
+                decode chain (top-k, gate/up and down expert matvecs on split planes, combine), else the prefill chain
+                (top-k, bucket, MXFP8 quantize, grouped gate_up on the scaled MFMA + swiglu_oai with the MXFP8
+                quantization of its output fused, grouped down, combine). Secondary at T = 1, 256, 1024 and 4096.
     q4_k_moe    Q4_K MoE prefill chain at the Qwen3-30B-A3B shape (128 experts, top-8, H = 2048, FE = 768), T = 64
     hbm_copy    calibration: a 256 MiB device copy, whose counter readings scale FETCH_SIZE / WRITE_SIZE to bytes
 
-Consecutive steps read different copies of the weight (more than 300 MB in rotation), so the 256 MB MALL cannot
-serve them and the figure is an HBM figure. The K timed steps are captured in one HIP graph and replayed on the
-launching stream between two HIP events; value = algorithmic bytes x K / elapsed. The JSON line also carries the
-roofline of the kernel (achieved = algorithmic bytes per launch / average launch time from the same events) and
-a CPU baseline: the numpy oracle timed on this host's cores on a bounded sample of the same workload.
+Consecutive steps read different copies of the weights (more than 300 MB in rotation), so the 256 MB MALL cannot
+serve them and the figures are HBM figures. The K timed steps are captured in one HIP graph. A GPU spin kernel is
+enqueued ahead of the timed region, so the whole graph is queued on the device before the first timed kernel starts
+and the two HIP events on the launching stream see the kernels, not the host's graph submission; value = algorithmic
+work x K / elapsed. `roofline` is the dominant kernel's: algorithmic bytes (or FLOPs) per launch over its average
+launch time, each launch of that kernel timed between its own pair of HIP events. `cpu_baseline` times the numpy oracle on this
+host's cores on the same workload (dequant and matmul separately and together).
 """
 import argparse
 import json
@@ -43,17 +49,25 @@ METRIC = "Q4_K GEMV GB/s (% HBM peak); MXFP4 MoE prefill TFLOP/s (% MFMA peak)"
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "fp16": 2500.0, "fp8": 5000.0, "fp4": 10100.0}
 ROTATE_BYTES = 300 * 2 ** 20
+SPIN_CYCLES = 4_000_000   # the spin ahead of a timed graph: about 2 ms, longer than the host's graph submission
+
+# (workload, M or T) measured after the headline by the default run
+SECONDARY = [("q4_k_gemv_q8", 4), ("q4_k_gemv_q8", 8), ("q4_k_swiglu_q8", 1), ("q4_k_gemv", 1), ("q4_0_gemv", 1),
+             ("q4_k_gemm", 512), ("mxfp4_moe", 1), ("mxfp4_moe", 256), ("mxfp4_moe", 1024), ("mxfp4_moe", 4096),
+             ("q4_k_moe", 64)]
 
 
 def parse():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=2000)
-    p.add_argument("--warmup", type=int, default=200)
-    p.add_argument("--workload", default="q4_k_gemv_q8", choices=sorted(WORKLOADS))
-    p.add_argument("--m", type=int, default=None, help="tokens per GEMV (q4_k_gemv: 1, 4 or 8)")
-    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--workload", default=None, choices=sorted(WORKLOADS))
+    p.add_argument("--m", type=int, default=None, help="tokens (GEMV: M; MoE: T)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    p.add_argument("--no-secondary", action="store_true", help="measure the headline workload only")
+    p.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work (headline)")
+    p.add_argument("--cpu-budget-secondary", type=float, default=3.0, help="seconds of CPU work per secondary")
     p.add_argument("--no-graph", action="store_true", help="launch steps one by one instead of a HIP graph")
     return p.parse_args()
 
@@ -71,20 +85,40 @@ def traffic_from_profile(name):
     return None
 
 
+_WEIGHTS = {}
+
+
+def cached_workload(index, **kw):
+    """synth.workload with the weights of each workload generated once per process (every token count of a workload
+    sees the same weights and the inputs a fresh call would draw)."""
+    from qmm import synth
+    return synth.workload(index, cache=_WEIGHTS, **kw)
+
+
+def cpu_entry(res, work, unit, scale, kind_sample):
+    """cpu_baseline dict from a cpu_baseline timing result: value = work / total time in `unit` (work / scale)."""
+    out = {"value": round(work / res["total_s"] / scale, 6), "unit": unit, "cores": res["threads"], "kind": "port",
+           "dequant_ms": round(res["dequant_s"] * 1e3, 3), "matmul_ms": round(res["matmul_s"] * 1e3, 3),
+           "total_ms": round(res["total_s"] * 1e3, 3), "sample": kind_sample}
+    return out
+
+
 # ------------------------------------------------------------------------------------------------ workloads
 class GemvWorkload:
-    """Decode GEMV y = x W^T over rotated weight copies; one step = one qmm_mv launch."""
+    """Decode GEMV y = x W^T over rotated weight copies; one step = one qmm_mv / qmm_mv_q8 launch (or the swiglu
+    matvec over a gate and an up matrix)."""
     metric, unit, bound = METRIC, "GB/s", "hbm"
 
-    def __init__(self, name, index, fmt, n, k, m, x_dtype, traffic_name, q8=False, tiled=False):
+    def __init__(self, name, index, fmt, n, k, m, x_dtype, traffic_name, q8=False, tiled=False, swiglu=False):
         self.name, self.index, self.fmt, self.n, self.k, self.m = name, index, fmt, n, k, m
         self.x_dtype, self.traffic_name, self.q8, self.tiled = x_dtype, traffic_name, q8, tiled
+        self.swiglu = swiglu
         self.kfmt = "q4_kt" if tiled else fmt   # the weights the kernel reads (tiled: repacked once at load)
 
     def setup(self, dev):
         import torch
         from qmm import ops, synth
-        d = synth.workload(self.index, m=self.m)
+        d = cached_workload(self.index, m=self.m)
         self.raw = d["w"]
         if self.x_dtype == "bf16":
             self.x_host = synth.bf16_bits_to_f32(d["x_bf16"])
@@ -93,8 +127,12 @@ class GemvWorkload:
             self.x_host = d["x"]
             x = torch.from_numpy(d["x"]).to(dev)
         w0 = torch.from_numpy(self.raw).to(dev)
+        if self.swiglu:   # the up matrix: the gate matrix's code bytes in reverse order (same distributions)
+            self.raw_up = np.ascontiguousarray(self.raw.reshape(-1, 144)[::-1]).reshape(-1)
+            w0 = torch.cat([w0, torch.from_numpy(self.raw_up).to(dev)])
         if self.tiled:   # one-time weight preparation: GGUF Q4_K blocks -> the lane-ordered tiled layout
-            w0 = ops.tile_q4k(w0, self.n, self.k)
+            parts = [ops.tile_q4k(p, self.n, self.k) for p in w0.chunk(2 if self.swiglu else 1)]
+            w0 = torch.cat(parts) if len(parts) > 1 else parts[0]
         self.wbytes = w0.numel()
         copies = max(2, -(-ROTATE_BYTES // self.wbytes))
         self.ws = [w0] + [w0.clone() for _ in range(copies - 1)]
@@ -106,12 +144,16 @@ class GemvWorkload:
             self.xq = ops.quant_q8(self.x)
 
     def step(self, i):
-        if self.q8 == "planar":
-            self.ops.mv_q8(self.kfmt, self.ws[i % self.copies], self.xq, self.n, self.k, tokens=self.m, y=self.y)
+        w = self.ws[i % self.copies]
+        if self.swiglu:
+            g, u = w.chunk(2)
+            self.ops.mv_swiglu_q8(self.kfmt, g, u, self.x, self.n, self.k, y=self.y)
+        elif self.q8 == "planar":
+            self.ops.mv_q8(self.kfmt, w, self.xq, self.n, self.k, tokens=self.m, y=self.y)
         elif self.q8:
-            self.ops.mv_q8(self.kfmt, self.ws[i % self.copies], self.x, self.n, self.k, y=self.y)
+            self.ops.mv_q8(self.kfmt, w, self.x, self.n, self.k, y=self.y)
         else:
-            self.ops.mv(self.fmt, self.ws[i % self.copies], self.x, self.n, self.k, y=self.y)
+            self.ops.mv(self.fmt, w, self.x, self.n, self.k, y=self.y)
 
     kernel_step = None
 
@@ -123,7 +165,7 @@ class GemvWorkload:
             return f"{self.fmt} x int8 (planar Q8_1 from qmm_quant_q8) -> f32, int32 group dots"
         if self.q8:
             return f"{self.fmt} x int8 (Q8_1 of {self.x_dtype}, quantized in the kernel) -> f32, int32 group dots"
-        return "q4_k x bf16 -> f32" if self.fmt == "q4_k" else "q4_0 x f32 -> f32"
+        return "q4_k x f16 (bf16 x) -> f32" if self.fmt == "q4_k" else "q4_0 x f32 -> f32"
 
     def alg_bytes(self):
         if self.q8 == "planar":   # the planar Q8_1 buffer: a code byte per value and 8 bytes per 32 values
@@ -132,38 +174,40 @@ class GemvWorkload:
         return self.wbytes + self.m * self.k * xb + self.m * self.n * 4
 
     def alg_flops(self):
-        return 2 * self.m * self.n * self.k
+        return 2 * self.m * self.n * self.k * (2 if self.swiglu else 1)
 
     def cpu_baseline(self, budget):
         from oracle import cpu_baseline, ref
         x = ref.q8_1(self.x_host) if self.q8 else self.x_host
-        sec, runs, threads = cpu_baseline.time_gemv(self.fmt, self.raw, self.n, self.k, x, budget_s=budget)
-        return {"value": round(self.alg_bytes() / sec / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
-                "sample": f"{runs} full {self.fmt} GEMVs (N={self.n}, K={self.k}, M={self.m}): numpy oracle dequant "
-                          f"in 256-row chunks + f32 matmul on {threads} threads, median {sec * 1e3:.1f} ms per GEMV"}
+        n = self.n * (2 if self.swiglu else 1)
+        raw = np.concatenate([self.raw, self.raw_up]) if self.swiglu else self.raw
+        res = cpu_baseline.time_gemv(self.fmt, raw, n, self.k, x, budget_s=budget)
+        return cpu_entry(res, self.alg_bytes(), "GB/s", 1e9,
+                         f"{res['runs']} full {self.fmt} GEMVs (N={n}, K={self.k}, M={self.m}): numpy oracle, "
+                         f"dequant fused in 256-row chunks + f32 matmul on {res['threads']} threads")
 
     def config(self):
         return {"workload": self.name, "format": self.fmt, "layout": "tiled (q4_kt)" if self.tiled else "gguf",
                 "N": self.n, "K": self.k, "M": self.m,
                 "x_dtype": "q8_1 planar" if self.q8 == "planar" else self.x_dtype,
                 "activations": "q8_1" if self.q8 else self.x_dtype, "y_dtype": "f32",
-                "weight_copies_rotated": self.copies,
-                "rotated_bytes": self.copies * self.wbytes}
+                "weight_copies_rotated": self.copies, "rotated_bytes": self.copies * self.wbytes}
 
 
 class GemmWorkload:
     """Q4_K prefill GEMM: one step = row-scale bf16 x to f16 + the GEMM (bf16 out) on the next weight copy."""
     metric, unit, bound = "Q4_K prefill GEMM TFLOP/s (Qwen3-8B o_proj, 512 x 4096 x 4096)", "TFLOP/s", "mfma"
     peak_key = "fp16"
-    name, traffic_name = "q4_k_gemm", "q4k_mfma_kernel_dense.q4_k_gemm_m512_n4096_k4096"
+    name = "q4_k_gemm"
 
     def __init__(self, m):
         self.m, self.n, self.k = m or 512, 4096, 4096
+        self.traffic_name = f"q4k_mfma_kernel_dense.q4_k_gemm_m{self.m}_n4096_k4096"
 
     def setup(self, dev):
         import torch
-        from qmm import ops, synth
-        d = synth.workload(2, m=self.m)
+        from qmm import ops
+        d = cached_workload(2, m=self.m)
         self.raw, self.x_bits = d["w"], d["x_bf16"]
         w0 = torch.from_numpy(self.raw).to(dev)
         self.wbytes = w0.numel()
@@ -200,11 +244,10 @@ class GemmWorkload:
         from oracle import cpu_baseline
         from qmm import synth
         x = synth.bf16_bits_to_f32(self.x_bits)
-        sec, runs, threads = cpu_baseline.time_gemv("q4_k", self.raw, self.n, self.k, x, budget_s=budget)
-        return {"value": round(self.alg_flops() / sec / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
-                "kind": "port",
-                "sample": f"{runs} full GEMMs (M={self.m}, N={self.n}, K={self.k}): numpy oracle dequant in 256-row "
-                          f"chunks + f32 matmul on {threads} threads, median {sec * 1e3:.1f} ms per GEMM"}
+        res = cpu_baseline.time_gemv("q4_k", self.raw, self.n, self.k, x, budget_s=budget)
+        return cpu_entry(res, self.alg_flops(), "TFLOP/s", 1e12,
+                         f"{res['runs']} full GEMMs (M={self.m}, N={self.n}, K={self.k}): numpy oracle, dequant "
+                         f"fused in 256-row chunks + f32 matmul on {res['threads']} threads")
 
     def config(self):
         return {"workload": self.name, "format": "q4_k", "M": self.m, "N": self.n, "K": self.k, "x_dtype": "bf16",
@@ -212,45 +255,51 @@ class GemmWorkload:
 
 
 class MoeWorkload:
-    """MoE prefill chain; one step = the whole chain over one batch of T tokens, on one of two copies of the expert
-    weights in turn (see setup)."""
-    unit, higher = "TFLOP/s", True
+    """The routed-expert chain (ops.moe_routed: the decode chain for T < 64, the prefill chain from 64 tokens); one
+    step = the whole chain over one batch of T tokens, on one of two copies of the expert weights in turn."""
+    unit = "TFLOP/s"
 
     def __init__(self, name, index, m):
         self.name, self.index = name, index
         if index == 3:
             self.T = m or 256
             self.metric = METRIC
-            self.traffic_name = f"mxfp4_grouped_kernel_gu8.mxfp4_moe_gpt_oss_20b_t{self.T}"
         else:
             self.T = m or 64
-            self.metric = "Q4_K MoE prefill TFLOP/s (Qwen3-30B-A3B, 128 experts, top-8, T = 64)"
-            self.traffic_name = f"q4k_mfma_kernel_gu.q4_k_moe_qwen3_30b_a3b_t{self.T}"
+            self.metric = "Q4_K MoE prefill TFLOP/s (Qwen3-30B-A3B, 128 experts, top-8)"
+        self.decode = self.T < 64
+        kern = ("expert_mv" if self.decode else "mxfp4_grouped_kernel_gu8") if index == 3 else \
+            ("expert_mv" if self.decode else "q4k_mfma_kernel_gu")
+        model = "mxfp4_moe_gpt_oss_20b" if index == 3 else "q4_k_moe_qwen3_30b_a3b"
+        self.traffic_name = f"{kern}.{model}_t{self.T}"
 
     def setup(self, dev):
         import torch
-        from qmm import ops, synth
-        d = synth.workload(self.index, T=self.T)
+        from qmm import ops
+        d = cached_workload(self.index, T=self.T)
         self.d = d
         self.E, self.KU, self.H, self.FE = d["E"], d["KU"], d["H"], d["FE"]
         u8 = lambda a: torch.from_numpy(a).to(dev)
         self.x = torch.from_numpy(d["x_bf16"].view(np.int16)).to(dev).view(torch.bfloat16)
         self.logits = torch.from_numpy(d["logits"]).to(dev)
+        E, H, FE = self.E, self.H, self.FE
         if d["fmt"] == "mxfp4":
-            E, H, FE = self.E, self.H, self.FE
-            # one-time weight preparation: GGUF blocks -> split planes -> MFMA-tiled planes
+            # one-time weight preparation: GGUF blocks -> split planes (decode) -> MFMA-tiled planes (prefill)
             gn, gs = ops.repack_mxfp4(u8(d["gate_up"]), E * 2 * FE, H)
             dn, ds = ops.repack_mxfp4(u8(d["down"]), E * H, FE)
-            gn, gs = ops.tile_mxfp4(gn, gs, E * 2 * FE, H)
-            dn, ds = ops.tile_mxfp4(dn, ds, E * H, FE)
-            self.fmt = "mxfp4t"
+            if self.decode:
+                self.fmt = "mxfp4s"
+            else:
+                gn, gs = ops.tile_mxfp4(gn, gs, E * 2 * FE, H)
+                dn, ds = ops.tile_mxfp4(dn, ds, E * H, FE)
+                self.fmt = "mxfp4t"
             self.kw = dict(w_gate=gn, ws_gate=gs, w_down=dn, ws_down=ds, fused=True, act=d["act"])
             self.wbytes_expert = (2 * FE * H + H * FE) // 2 + (2 * FE * H + H * FE) // 32
             self.peak_key = "fp8"
         else:
             self.fmt = "q4_k"
             self.kw = dict(w_gate=u8(d["gate"]), w_up=u8(d["up"]), w_down=u8(d["down"]), fused=False, act=d["act"])
-            self.wbytes_expert = (2 * self.FE * self.H + self.H * self.FE) // 256 * 144
+            self.wbytes_expert = (2 * FE * H + H * FE) // 256 * 144
             self.peak_key = "fp16"
         self.ops = ops
         # a second copy of every expert tensor, alternated from step to step: one layer's experts (441 MB MXFP4,
@@ -261,9 +310,11 @@ class MoeWorkload:
         y, mid = self.run_chain()
         torch.cuda.synchronize()
         self.experts_hit = int(torch.unique(mid["ids"]).numel())
-        # inputs of the dominant kernel (the grouped gate/up GEMM) for its own timing
         self.mid = mid
-        if self.fmt == "mxfp4t":
+        # inputs of the dominant kernel (the gate/up GEMM or expert matvec) for its own timing
+        if self.decode:
+            self.gu_y = torch.empty_like(mid["act"])
+        elif self.fmt == "mxfp4t":
             self.gu_x, self.gu_xs = ops.quant_mxfp8(self.x)
             self.gu_y = (torch.empty_like(mid["act8"]), torch.empty_like(mid["act_scales"]))
         else:
@@ -271,22 +322,26 @@ class MoeWorkload:
             self.gu_y = torch.empty_like(mid["act"])
 
     def run_chain(self, i=0):
-        return self.ops.moe_prefill(self.fmt, self.x, self.logits, self.E, self.KU, self.H, self.FE, self.d["gating"],
-                                    self.d["norm"], **self.kws[i % self.copies])
+        return self.ops.moe_routed(self.fmt, self.x, self.logits, self.E, self.KU, self.H, self.FE, self.d["gating"],
+                                   self.d["norm"], **self.kws[i % self.copies])
 
     def step(self, i):
         self.run_chain(i)
 
     def kernel_step(self, i):
         kw = self.kws[i % self.copies]
-        if self.fmt == "mxfp4t":   # the gate/up GEMM with its activation written as MXFP8 (the chain's kernel)
+        if self.decode:   # the gate/up expert matvecs of the decode chain
+            self.ops.moe_expert_mv(self.fmt, "gu", self.mid["ids"], self.x, kw["w_gate"], self.FE, self.H, self.E,
+                                   self.KU, w2=kw.get("w_up"), ws=kw.get("ws_gate"), fused=kw["fused"],
+                                   act=kw["act"], y=self.gu_y)
+        elif self.fmt == "mxfp4t":   # the gate/up GEMM with its activation written as MXFP8 (the chain's kernel)
             self.ops.moe_grouped_mxfp8(self.fmt, self.mid["tile_info"], self.mid["rowmap"], self.gu_x, kw["w_gate"],
                                        self.FE, self.H, self.E, self.KU, ws=kw.get("ws_gate"), x_scales=self.gu_xs,
                                        fused=kw["fused"], act=kw["act"], codes=self.gu_y[0], scales=self.gu_y[1])
-            return
-        self.ops.moe_grouped(self.fmt, "gu", self.mid["tile_info"], self.mid["rowmap"], self.gu_x, kw["w_gate"],
-                             self.FE, self.H, self.E, self.KU, w2=kw.get("w_up"), ws=kw.get("ws_gate"),
-                             x_scales=self.gu_xs, fused=kw["fused"], act=kw["act"], y=self.gu_y)
+        else:
+            self.ops.moe_grouped(self.fmt, "gu", self.mid["tile_info"], self.mid["rowmap"], self.gu_x, kw["w_gate"],
+                                 self.FE, self.H, self.E, self.KU, w2=kw.get("w_up"), ws=kw.get("ws_gate"),
+                                 x_scales=self.gu_xs, fused=kw["fused"], act=kw["act"], y=self.gu_y)
 
     @property
     def bound(self):
@@ -302,12 +357,13 @@ class MoeWorkload:
         return 2 * self.T * self.KU * (self.H * 2 * self.FE + self.FE * self.H)
 
     def gu_bytes(self):
-        """weights of the experts hit, the activation rows in, the activation out (MXFP8 codes + scales for MXFP4,
-        f32 for Q4_K)"""
+        """weights of the experts hit, the activation rows in, the activation out (MXFP8 codes + scales for the
+        MXFP4 grouped GEMM, f32 otherwise)"""
         T, H, A = self.T, self.H, self.T * self.KU
+        wgu = self.experts_hit * (self.wbytes_expert * 2 // 3)
         if self.fmt == "mxfp4t":
-            return self.experts_hit * (self.wbytes_expert * 2 // 3) + T * H + T * H // 32 + A * self.FE * 33 // 32
-        return self.experts_hit * ((2 * self.FE * H) // 256 * 144) + T * H * 2 + A * self.FE * 4
+            return wgu + T * H + T * H // 32 + A * self.FE * 33 // 32
+        return wgu + T * H * 2 + A * self.FE * 4
 
     def gu_flops(self):
         return 2 * self.T * self.KU * self.H * 2 * self.FE
@@ -316,48 +372,44 @@ class MoeWorkload:
         return self.alg_flops() / sec / 1e12
 
     def dtype(self):
-        return ("mxfp4 x mxfp8 (E4M3, E8M0 per 32) -> f32" if self.fmt == "mxfp4t"
-                else "q4_k x f16 (row-scaled) -> f32")
+        if self.fmt == "mxfp4t":
+            return "mxfp4 x mxfp8 (E4M3, E8M0 per 32) -> f32"
+        if self.fmt == "mxfp4s":
+            return "mxfp4 x bf16 -> f32 (expert matvecs)"
+        return "q4_k x f16 (row-scaled) -> f32"
 
     def cpu_baseline(self, budget):
+        from oracle import cpu_baseline
         from oracle import formats as of
         from oracle import ref
         from qmm import synth
-        import time as _t
         d = self.d
-        gfmt = "mxfp4" if self.fmt == "mxfp4t" else "q4_k"
+        gfmt = "mxfp4" if self.fmt.startswith("mxfp4") else "q4_k"
         E, KU, H, FE = self.E, self.KU, self.H, self.FE
         rb_h, rb_f = of.row_bytes(gfmt, H), of.row_bytes(gfmt, FE)
-        def gate_up(e):
-            if self.fmt == "mxfp4t":
-                g = of.dequantize(gfmt, d["gate_up"][2 * FE * e * rb_h:(2 * FE * e + FE) * rb_h], FE, H)
-                u = of.dequantize(gfmt, d["gate_up"][(2 * FE * e + FE) * rb_h:2 * FE * (e + 1) * rb_h], FE, H)
-                return g, u
-            return (of.dequantize(gfmt, d["gate"][FE * e * rb_h:FE * (e + 1) * rb_h], FE, H),
-                    of.dequantize(gfmt, d["up"][FE * e * rb_h:FE * (e + 1) * rb_h], FE, H))
-        def down(e):
-            return of.dequantize(gfmt, d["down"][H * e * rb_f:H * (e + 1) * rb_f], H, FE)
+
+        def experts(e):
+            if gfmt == "mxfp4":
+                gu = d["gate_up"][2 * FE * e * rb_h:2 * FE * (e + 1) * rb_h]
+                g = of.dequantize(gfmt, gu[:FE * rb_h], FE, H)
+                u = of.dequantize(gfmt, gu[FE * rb_h:], FE, H)
+            else:
+                g = of.dequantize(gfmt, d["gate"][FE * e * rb_h:FE * (e + 1) * rb_h], FE, H)
+                u = of.dequantize(gfmt, d["up"][FE * e * rb_h:FE * (e + 1) * rb_h], FE, H)
+            return g, u, of.dequantize(gfmt, d["down"][H * e * rb_f:H * (e + 1) * rb_f], H, FE)
+
         x = synth.bf16_bits_to_f32(d["x_bf16"])
-        ids, wts = ref.route(d["logits"], KU, d["gating"], d["norm"])
-        rnd = ref.mxfp8_values if self.fmt == "mxfp4t" else ref.f16_rows
-        # bounded sample: the first tokens whose experts fit the time budget (the whole chain on them)
-        tokens = 0
-        t0 = _t.perf_counter()
-        while tokens < self.T and _t.perf_counter() - t0 < budget:
-            n = min(self.T - tokens, max(1, self.T // 16))
-            ref.moe(x[tokens:tokens + n], ids[tokens:tokens + n], wts[tokens:tokens + n], gate_up, down,
-                    act=d["act"], x_round=rnd, act_round=rnd)
-            tokens += n
-        sec = _t.perf_counter() - t0
-        flops = 2 * tokens * KU * (H * 2 * FE + FE * H)
-        return {"value": round(flops / sec / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
-                "sample": f"{tokens} of {self.T} tokens through the numpy oracle's MoE chain (per-expert exact "
-                          f"dequant + float64 matmuls, single-threaded numpy), {sec:.1f} s"}
+        rnd = {"mxfp4t": ref.mxfp8_values, "q4_k": ref.f16_rows}.get(self.fmt)
+        res = cpu_baseline.time_moe(x, d["logits"], KU, d["gating"], d["norm"], d["act"], experts, budget_s=budget,
+                                    x_round=rnd, act_round=rnd)
+        return cpu_entry(res, self.alg_flops(), "TFLOP/s", 1e12,
+                         f"{res['runs']} full chains (T={self.T}, {res['experts_hit']} experts hit): numpy oracle, "
+                         f"per-expert dequant + f32 matmuls on {res['threads']} threads")
 
     def config(self):
-        return {"workload": self.name, "format": self.fmt, "E": self.E, "top_k": self.KU, "H": self.H,
-                "FE": self.FE, "T": self.T, "gating": self.d["gating"], "act": self.d["act"],
-                "experts_hit": self.experts_hit, "weight_copies_rotated": self.copies}
+        return {"workload": self.name, "format": self.fmt, "chain": "decode" if self.decode else "prefill",
+                "E": self.E, "top_k": self.KU, "H": self.H, "FE": self.FE, "T": self.T, "gating": self.d["gating"],
+                "act": self.d["act"], "experts_hit": self.experts_hit, "weight_copies_rotated": self.copies}
 
 
 class CopyWorkload:
@@ -415,6 +467,11 @@ def _q4k_gemv_q8(m):
                         f"mv_q4kt_q8_kernel.q4_k_gemv_q8_n12288_k4096_m{m or 1}", q8=True, tiled=True)
 
 
+def _q4k_swiglu_q8(m):
+    return GemvWorkload("q4_k_swiglu_q8", 1, "q4_k", 12288, 4096, m or 1, "bf16",
+                        f"mv_q4kt_q8_kernel.q4_k_swiglu_q8_n12288_k4096_m{m or 1}", q8=True, tiled=True, swiglu=True)
+
+
 def _q4k_gemv_q8_gguf(m):
     return GemvWorkload("q4_k_gemv_q8_gguf", 1, "q4_k", 12288, 4096, m or 1, "bf16",
                         f"mv_q4k_q8s_kernel.q4_k_gemv_q8_gguf_n12288_k4096_m{m or 1}", q8=True)
@@ -431,9 +488,111 @@ def _q40_gemv(m):
 
 
 WORKLOADS = {"q4_k_gemv": _q4k_gemv, "q4_k_gemv_q8": _q4k_gemv_q8, "q4_k_gemv_q8_gguf": _q4k_gemv_q8_gguf,
-             "q4_k_gemv_q8p": _q4k_gemv_q8p, "q4_0_gemv": _q40_gemv, "q4_k_gemm": GemmWorkload,
-             "mxfp4_moe": lambda m: MoeWorkload("mxfp4_moe", 3, m), "q4_k_moe": lambda m: MoeWorkload("q4_k_moe", 4, m),
-             "hbm_copy": CopyWorkload}
+             "q4_k_gemv_q8p": _q4k_gemv_q8p, "q4_k_swiglu_q8": _q4k_swiglu_q8, "q4_0_gemv": _q40_gemv,
+             "q4_k_gemm": GemmWorkload, "mxfp4_moe": lambda m: MoeWorkload("mxfp4_moe", 3, m),
+             "q4_k_moe": lambda m: MoeWorkload("q4_k_moe", 4, m), "hbm_copy": CopyWorkload}
+
+
+# ---------------------------------------------------------------------------------------------------- timing
+def timed(step_fn, steps, warmup, no_graph=False):
+    """ms for `steps` steps between two HIP events on the launching stream, and the wall time of that region.
+    Graph mode captures the steps in one HIP graph; a spin kernel ahead of the first event holds the stream while the
+    host submits the graph, so the events time the kernels and the gaps between them only."""
+    import torch
+    stream = torch.cuda.current_stream()
+
+    def run(count, start):
+        for i in range(count):
+            step_fn(start + i)
+
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if no_graph:
+        run(warmup, 0)
+        torch.cuda.synchronize()
+        torch.cuda._sleep(SPIN_CYCLES)
+        wall0 = time.perf_counter()
+        t0.record(stream)
+        run(steps, warmup)
+        t1.record(stream)
+    else:
+        gw, gt = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gw):
+            run(max(warmup, 1), 0)
+        with torch.cuda.graph(gt):
+            run(steps, warmup)
+        torch.cuda.synchronize()
+        gw.replay()
+        torch.cuda.synchronize()
+        torch.cuda._sleep(SPIN_CYCLES)
+        wall0 = time.perf_counter()
+        t0.record(stream)
+        gt.replay()
+        t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1), time.perf_counter() - wall0
+
+
+def kernel_times(fn, steps, warmup):
+    """Per-launch durations (ms) of fn(warmup) .. fn(warmup + steps - 1), each launch between its own pair of HIP
+    events on the launching stream. The launches are eager and queued behind a spin kernel that outlasts the host's
+    enqueueing, so every start event is followed at once by its kernel."""
+    import torch
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        fn(i)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    torch.cuda._sleep(max(SPIN_CYCLES, 400_000 * steps))   # about 160 us of spin per queued launch
+    for i, (a, b) in enumerate(evs):
+        a.record(stream)
+        fn(warmup + i)
+        b.record(stream)
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in evs]
+
+
+def measure(wl, args, cpu_budget):
+    """Times one set-up workload; returns its result fields (the headline line's, or a secondary entry's)."""
+    ms, wall = timed(wl.step, args.steps, args.warmup, args.no_graph)
+    per_step_s = ms / 1e3 / args.steps
+    kt = kernel_times(wl.kernel_step or wl.step, args.steps, args.warmup)
+    per_launch_s = float(np.mean(kt)) / 1e3
+    kb = wl.gu_bytes() if hasattr(wl, "gu_bytes") else wl.alg_bytes()
+    kf = wl.gu_flops() if hasattr(wl, "gu_flops") else wl.alg_flops()
+    if wl.bound == "hbm":
+        achieved, peak, unit = kb / per_launch_s / 1e9, HBM_PEAK_GBS, "GB/s"
+    else:
+        achieved, peak, unit = kf / per_launch_s / 1e12, MFMA_PEAK_TFLOPS[wl.peak_key], "TFLOP/s"
+    roof = {"bound": wl.bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic_from_profile(wl.traffic_name),
+            "kernel": wl.traffic_name.split(".")[0], "avg_launch_us": round(per_launch_s * 1e6, 3),
+            "median_launch_us": round(float(np.median(kt)) * 1e3, 3),
+            "alg_bytes_per_launch": kb, "alg_flops_per_launch": kf}
+    res = {"value": round(wl.value(per_step_s), 3), "unit": wl.unit, "ms_per_step": round(ms / args.steps, 6),
+           "roofline": roof, "gbs": round(wl.alg_bytes() / per_step_s / 1e9, 2),
+           "tflops": round(wl.alg_flops() / per_step_s / 1e12, 3), "wall_s_timed_region": round(wall, 4)}
+    if getattr(wl, "peak_key", None) == "fp8":
+        # the scaled MFMA runs E4M3 x E2M1 at the FP8 rate; the MXFP4 figure is the fraction of the FP4 peak
+        res["chain_frac_fp4_peak"] = round(res["tflops"] / MFMA_PEAK_TFLOPS["fp4"], 4)
+        res["chain_frac_fp8_rate"] = round(res["tflops"] / MFMA_PEAK_TFLOPS["fp8"], 4)
+    if cpu_budget:
+        res["cpu_baseline"] = wl.cpu_baseline(cpu_budget)
+    return res
+
+
+def secondary_entry(name, m, wl, res):
+    """The compact form of a secondary workload's result."""
+    r = res["roofline"]
+    out = {"workload": name, "m": m, "value": res["value"], "unit": res["unit"],
+           "us_per_step": round(res["ms_per_step"] * 1e3, 3), "gbs": res["gbs"], "tflops": res["tflops"],
+           "roofline": {k: r[k] for k in ("bound", "achieved", "unit", "frac", "traffic", "kernel", "avg_launch_us")}}
+    if "chain_frac_fp4_peak" in res:
+        out["chain_frac_fp4_peak"] = res["chain_frac_fp4_peak"]
+    if "cpu_baseline" in res:
+        c = res["cpu_baseline"]
+        out["cpu"] = {k: c[k] for k in ("value", "unit", "cores", "dequant_ms", "matmul_ms", "total_ms") if k in c}
+    return out
 
 
 # ---------------------------------------------------------------------------------------------------- main
@@ -449,83 +608,47 @@ def main():
         print("bench.py needs a GPU (torch.cuda.is_available() is False)", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
-    wl = WORKLOADS[args.workload](args.m)
+    name = args.workload or "q4_k_gemv_q8"
+    wl = WORKLOADS[name](args.m)
     wl.setup(dev)
-    stream = torch.cuda.current_stream()
-
-    def timed(step_fn):
-        """ms for args.steps steps (HIP-graph replay between two events on the launching stream) and the wall time"""
-        def run(count, start):
-            for i in range(count):
-                step_fn(start + i)
-        torch.cuda.synchronize()
-        if args.no_graph:
-            run(args.warmup, 0)
-            torch.cuda.synchronize()
-            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            wall0 = time.perf_counter()
-            t0.record(stream)
-            run(args.steps, args.warmup)
-            t1.record(stream)
-        else:
-            gw, gt = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
-            with torch.cuda.graph(gw):
-                run(max(args.warmup, 1), 0)
-            with torch.cuda.graph(gt):
-                run(args.steps, args.warmup)
-            torch.cuda.synchronize()
-            if args.warmup:
-                gw.replay()
-            torch.cuda.synchronize()
-            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            wall0 = time.perf_counter()
-            t0.record(stream)
-            gt.replay()
-            t1.record(stream)
-        torch.cuda.synchronize()
-        return t0.elapsed_time(t1), time.perf_counter() - wall0
-
-    ms, wall = timed(wl.step)
-    per_step_s = ms / 1e3 / args.steps
-    value = wl.value(per_step_s)
-    kms = timed(wl.kernel_step)[0] if wl.kernel_step is not None else ms
-    per_launch_s = kms / 1e3 / args.steps
-    kb = wl.gu_bytes() if hasattr(wl, "gu_bytes") else wl.alg_bytes()
-    kf = wl.gu_flops() if hasattr(wl, "gu_flops") else wl.alg_flops()
-    if wl.bound == "hbm":
-        achieved, peak, unit = kb / per_launch_s / 1e9, HBM_PEAK_GBS, "GB/s"
-    else:
-        achieved, peak, unit = kf / per_launch_s / 1e12, MFMA_PEAK_TFLOPS[wl.peak_key], "TFLOP/s"
-    traffic = traffic_from_profile(wl.traffic_name)
+    res = measure(wl, args, 0 if args.no_cpu else args.cpu_budget)
     out = {
         "metric": wl.metric,
-        "value": round(value, 3),
+        "value": res["value"],
         "unit": wl.unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms / args.steps, 6),
+        "ms_per_step": res["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": wl.dtype(),
         "data": "synthetic (seeded generators of the workload's distributions)",
         "config": wl.config(),
-        "roofline": {"bound": wl.bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
-                     "frac": round(achieved / peak, 4), "traffic": traffic,
-                     "alg_bytes_per_launch": kb, "alg_flops_per_launch": kf,
-                     "avg_launch_us": round(per_launch_s * 1e6, 3),
-                     "mfma_frac": round(kf / per_launch_s / 1e12 / MFMA_PEAK_TFLOPS.get(getattr(wl, "peak_key", "fp16"), 2500.0), 4)},
-        "gbs": round(wl.alg_bytes() / per_step_s / 1e9, 2),
-        "tflops": round(wl.alg_flops() / per_step_s / 1e12, 3),
-        "wall_s_timed_region": round(wall, 4),
+        "roofline": res["roofline"],
     }
-    if getattr(wl, "fmt", None) == "mxfp4t":
-        # the scaled MFMA runs E4M3 x E2M1 at the FP8 rate; the MXFP4 figure is the fraction of the FP4 peak
-        out["roofline"]["mfma_frac_fp4_peak"] = round(kf / per_launch_s / 1e12 / MFMA_PEAK_TFLOPS["fp4"], 4)
-        out["chain_frac_fp4_peak"] = round(out["tflops"] / MFMA_PEAK_TFLOPS["fp4"], 4)
-    if not args.no_cpu:
-        out["cpu_baseline"] = wl.cpu_baseline(args.cpu_budget)
+    out.update({k: v for k, v in res.items() if k not in out and k != "cpu_baseline"})
+    if "cpu_baseline" in res:
+        out["cpu_baseline"] = res["cpu_baseline"]
+    del wl
+    if args.workload is None and not args.no_secondary:
+        sec = []
+        for sname, m in SECONDARY:
+            torch.cuda.empty_cache()
+            w2 = WORKLOADS[sname](m)
+            try:
+                w2.setup(dev)
+                r2 = measure(w2, args, 0 if args.no_cpu else args.cpu_budget_secondary)
+            except Exception as e:   # a failing secondary is reported in its entry, not fatal to the line
+                sec.append({"workload": sname, "m": m, "error": f"{type(e).__name__}: {str(e)[:120]}"})
+                print(f"secondary {sname} m={m}: {e}", file=sys.stderr, flush=True)
+                continue
+            sec.append(secondary_entry(sname, m, w2, r2))
+            print(f"secondary {sname} m={m}: {r2['value']} {r2['unit']} frac {r2['roofline']['frac']}",
+                  file=sys.stderr, flush=True)
+            del w2
+        out["secondary"] = sec
     print(json.dumps(out), flush=True)
     return 0
 

@@ -102,6 +102,23 @@ int qmm_quant_q8(int64_t rows, int64_t k, const void *x, int x_dtype, void *xq, 
 int qmm_mv_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
               const void *w, float *y, qmm_stream_t stream);
 
+/* The two-matrix decode matvecs on Q8_1 activations (S/gen_llm.py:1159-1197, int8 variants; the reference's default
+ * decode path for the FFN gate / up and for attention q + gate):
+ *   g_mv_{fmt}_k{K}_swiglu[_t{TG}]_q8[_r{R}], launch args (n, tokens, accumulate, x, w, w2, y):
+ *       y[t, r] = (accumulate ? y[t, r] : 0) + silu(g) u,   silu(g) = g / (1 + e^-g)
+ *   g_mv_{fmt}_k{K}_pair[_t{TG}]_q8[_r{R}], launch args (n, tokens, accumulate, x, w, w2, y, y2):
+ *       y[t, r] (+)= g,  y2[t, r] (+)= u
+ * with g = x W^T and u = x W2^T computed as qmm_mv_q8 computes one matrix (per 32-value group an exact int32 dot of
+ * codes, f32 fixups, the same reductions), so each is bit for bit the one-matrix kernel's of the same layout and K
+ * (for GGUF Q4_K at K = 4096 / 8192 that is the tiled layout's, since the one-matrix GGUF call takes its K-sliced
+ * kernel there). fmt QMM_Q4_KT: W and W2 in the tiled layout of qmm_tile_q4k, x planar Q8_1 or f32 / bf16 rows
+ * (quantized in the kernel exactly as qmm_quant_q8 does); QMM_Q4_K / QMM_Q4_0 / QMM_Q6_K (GGUF): x planar Q8_1.
+ * W, W2: [n, k]; y, y2: f32 [tokens, n]. A multi-token call equals one-token calls bit for bit. */
+int qmm_mv_swiglu_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
+                     const void *w, const void *w2, float *y, qmm_stream_t stream);
+int qmm_mv_pair_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
+                   const void *w, const void *w2, float *y, float *y2, qmm_stream_t stream);
+
 /* Prefill GEMM, the g_gemm_{fmt}_{store|acc|swiglu}[_m128|_m256] family
  * (S/gen_gemm.py:535-703, :706, :1224; launch args S/gen_gemm.py:549-556):
  *   store:  Y = (X W^T) * inv[row]        acc: Y += (X W^T) * inv[row]
@@ -110,12 +127,26 @@ int qmm_mv_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, con
  * with inv = scales[row, 1] (the reference's (2^-e, 2^e) pairs), or NULL for inv = 1; y: [rows, n] of y_dtype
  * (QMM_F32 as the reference, or QMM_BF16, rounded to nearest even). fp32 accumulation. K % 256 == 0. Weights are
  * dequantized to f16 as the reference stages them: Q4_K fma_f16(f16(q), f16(d sc), f16(-dmin m)); Q6_K (fmt
- * QMM_Q6_K, S/gen_gemm.py:369-444) fma_f16(f16(q), f16(d sc), f16(-32 d sc)) with q the unsigned 6-bit code.
+ * QMM_Q6_K, S/gen_gemm.py:369-444) fma_f16(f16(q), f16(d sc), f16(-32 d sc)) with q the unsigned 6-bit code; Q4_0
+ * (fmt QMM_Q4_0, the reference's native Q4_0 staging S/moe_q4_0.py:11-38, S/gen_gemm.py:40-45) f16(q - 8) * d with
+ * one f16 rounding, i.e. f16(d (q - 8)) for every finite d. MXFP4 weights go through qmm_gemm_mxfp4.
  * QMM_GEMM_SWIGLU: w is the gate matrix and w2 the up matrix (both [n, k]); silu(g) = g / (1 + e^-g).
  * Skip-padding (the reference's default GEMM_SKIP_PADDING): with scales, a 64-row tile whose rows all have
  * scales[row, 0] == 0 (padding rows of qmm_row_scale_f16_live) does no work and its y rows are not written. */
 int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, const void *x, int x_dtype, const float *scales,
              const void *w, const void *w2, void *y, int y_dtype, qmm_stream_t stream);
+
+/* Prefill GEMM on MXFP4 weights, the g_gemm_mxfp4s_{store|swiglu}_f8_m256 family (S/gen_mxfp4s.py:50-101; launch args
+ * (rows, k, n, x, scales, w, ws [, w2, w2s], y)), on the gfx950 scaled f8f6f4 MFMA:
+ *   store: Y = X8 W^T      acc: Y += X8 W^T      swiglu: Y = silu(X8 W^T) (X8 W2^T)
+ * x: the MXFP8 activation of qmm_quant_mxfp8, E4M3 codes u8 [rows, k] with x_scales its E8M0 plane u8 [rows, k/32]
+ * (one scale per 32 values, applied by the MFMA; the reference's gfx12 kernel scales fp8 rows by one power of two
+ * each). fmt QMM_MXFP4S: w nibble plane [n, k/2], ws E8M0 plane [n, k/32]; QMM_MXFP4T: the MFMA-tiled planes of
+ * qmm_tile_mxfp4 (n % 32 == 0). k % 64 == 0, k <= 12288. y: [rows, n] of y_dtype (QMM_F32, or QMM_BF16 rounded to
+ * nearest even). fp32 accumulation. GGUF MXFP4 blocks go through qmm_repack_mxfp4 once at load. */
+int qmm_gemm_mxfp4(int fmt, int mode, int64_t rows, int64_t k, int64_t n, const void *x, const void *x_scales,
+                   const void *w, const void *ws, const void *w2, const void *ws2, void *y, int y_dtype,
+                   qmm_stream_t stream);
 
 /* MoE router top-k from logits, g_moe_route / g_moe_route_tr after the router matvec
  * (S/gen_moe.py:116-252, :255-500; llama.cpp gating: 1 softmax, 2 sigmoid, 3 softmax over the picked logits):
@@ -164,6 +195,19 @@ int qmm_moe_expert_mv(int fmt, int mode, int fused, int act, int64_t k, int64_t 
                       int64_t assignments, const int32_t *ids, const void *x, int x_dtype, const void *w,
                       const void *w2, const float *bias, const float *bias2, float *y, qmm_stream_t stream);
 
+/* The decode expert matvecs on Q8_1 activations, g_moe_gu_{fmt}[_fused]_q8_k{H}_r{R} / g_moe_dn_{fmt}_q8_k{FE}_r{R}
+ * (S/gen_moe.py:535-727 with int8 activations; the reference's default MOE_Q8 decode chain, S/gen_llm.py:5290-5303,
+ * :5381-5383: the router input quantized once, the gate/up output quantized by qmm_quant_q8 before the down matvec):
+ *   gu (mode 0): act[a] = act_fn(Wg[e] xq[a/KU], Wu[e] xq[a/KU])      e = clamp(ids[a], 0, E - 1)
+ *   dn (mode 1): ys[a]  = Wd[e] xq[a]
+ * with each product computed as qmm_mv_q8 computes it (exact int32 group dots, f32 fixups). fmt QMM_Q4_K / QMM_Q4_0 /
+ * QMM_Q6_K; weights as qmm_moe_expert_mv (fused: one [E, 2n, k] gate_up tensor). x: the planar Q8_1 buffer of
+ * qmm_quant_q8 over x_rows rows (gu: the assignments / KU tokens; dn: the assignments). bias / bias2 as
+ * qmm_moe_expert_mv (the reference builds this path without expert biases), NULL = none. y: f32 [assignments, n]. */
+int qmm_moe_expert_mv_q8(int fmt, int mode, int fused, int act, int64_t k, int64_t n, int E, int KU,
+                         int64_t assignments, const int32_t *ids, const void *x, const void *w, const void *w2,
+                         const float *bias, const float *bias2, float *y, qmm_stream_t stream);
+
 /* qmm_moe_expert_mv for MXFP4 split planes (the reference's mxfp4s expert tensors, S/gen_llm.py:844-895):
  * w / w2 are nibble planes [E, rows, k/2] and ws / ws2 their E8M0 scale planes [E, rows, k/32]; with fused != 0
  * w and ws hold each expert's n gate rows then its n up rows and w2 / ws2 are ignored. */
@@ -173,7 +217,10 @@ int qmm_moe_expert_mv_split(int mode, int fused, int act, int64_t k, int64_t n, 
                             qmm_stream_t stream);
 
 /* Grouped expert GEMM over bucketed rows, g_moe_ggu_{fmt}[_fused]_k{H} / g_moe_gdn_{fmt}_k{FE}
- * (S/gen_moe.py:1126-1228; launch args S/gen_llm.py:5376-5378):
+ * (S/gen_moe.py:1126-1228). The name fields (fmt, mode gu / dn, fused, the activation, E and KU, which the reference
+ * compiles into the kernel) come first, then the launch arguments in the reference's order
+ * (max_rows, k, n, xrows, tile_info, rowmap, x16, scales, w [, w2] [, biases], y) (S/gen_llm.py:5376-5378), with the
+ * split-plane scale planes beside their nibble planes:
  *   gu (mode 0): act[r] = act_fn(Wg[e] x[t] inv + bias[e], Wu[e] x[t] inv + bias2[e]),  t = rowmap[r]/KU
  *   dn (mode 1): ys[r]  = Wd[e] x[r] inv + bias[e]                                      (x rows sorted)
  * for every row r of every 64-row tile whose expert e = tile_info[tile, 0] >= 0; rows with rowmap[r] == -1 are
@@ -184,29 +231,31 @@ int qmm_moe_expert_mv_split(int mode, int fused, int act, int64_t k, int64_t n, 
  *               fma_f16(f16(q), f16(d sc), f16(-dmin m)).
  *   QMM_Q6_K:   as QMM_Q4_K with Q6_K weights (staged as qmm_gemm stages them); g_moe_gdn_q6_k of the Q4_K_M
  *               expert layout (Q4_K gate / up, Q6_K down).
+ *   QMM_Q4_0:   as QMM_Q4_K with Q4_0 weights, staged f16(d (q - 8)) (specialize_grouped, S/moe_q4_0.py:41-61).
  *   QMM_MXFP4S: weights in split planes, ws / ws2 the E8M0 planes [E, rows, k/32]; x is MXFP8 (x_dtype
  *               QMM_MXFP8) from qmm_quant_mxfp8: E4M3 codes u8 [x_rows, k] with x_scales u8 [x_rows, k/32];
  *               K % 64 == 0; scaled f8f6f4 MFMA, inv = 1.
  *   QMM_MXFP4T: as QMM_MXFP4S with the weights in MFMA-tiled planes from qmm_tile_mxfp4 (each expert's [rows, k]
  *               tiled on its own: n % 32 == 0; a fused gate_up expert tiles as 2n rows); the same results bit for
  *               bit, read as contiguous 1 KB streams (no counterpart in the reference: a load-time layout).
- * x_rows: rows of x (gu: tokens; dn: >= max_tiles * 64). y: f32 [max_tiles * 64, n].
+ * max_rows: rows of the sorted outputs, max_tiles * 64 (a multiple of 64). x_rows: rows of x (gu: tokens; dn: >=
+ * max_rows). y: f32 [max_rows, n].
  * bias / bias2: the per-expert output biases f32 [E, n] (gpt-oss ffn_{gate,up,down}_exps.bias, _gemm_bias_act
  * S/gen_moe.py:958-1007), added after the row inverse and before the activation; NULL = none (bias2: gu only). */
-int qmm_moe_grouped(int fmt, int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
-                    const int32_t *tile_info, const int32_t *rowmap, const void *x, int x_dtype, const void *x_scales,
-                    int64_t x_rows, const void *w, const void *ws, const void *w2, const void *ws2, const float *bias,
-                    const float *bias2, float *y, qmm_stream_t stream);
+int qmm_moe_grouped(int fmt, int mode, int fused, int act, int E, int KU, int64_t max_rows, int64_t k, int64_t n,
+                    int64_t x_rows, const int32_t *tile_info, const int32_t *rowmap, const void *x, int x_dtype,
+                    const void *x_scales, const void *w, const void *ws, const void *w2, const void *ws2,
+                    const float *bias, const float *bias2, float *y, qmm_stream_t stream);
 
 /* The gate/up grouped GEMM (mode 0 of qmm_moe_grouped, MXFP4 weights) with the MXFP8 quantization of its output
  * fused into the epilogue (no reference counterpart: the reference writes act f32 and its next kernel reads it back).
- * codes u8 [max_tiles*64, n] and scales u8 [max_tiles*64, n/32] are exactly qmm_quant_mxfp8(act, tile_info) of the
+ * codes u8 [max_rows, n] and scales u8 [max_rows, n/32] are exactly qmm_quant_mxfp8(act, tile_info) of the
  * act qmm_moe_grouped would write (the down GEMM's A operand), bit for bit; rows of unused tiles are not written,
  * dead rows come out as codes 0 and scale byte 0. fmt QMM_MXFP4S or QMM_MXFP4T; n % 32 == 0; codes 16-byte
  * aligned. Other arguments as qmm_moe_grouped. */
-int qmm_moe_grouped_mxfp8(int fmt, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
-                          const int32_t *tile_info, const int32_t *rowmap, const void *x, const void *x_scales,
-                          int64_t x_rows, const void *w, const void *ws, const void *w2, const void *ws2,
+int qmm_moe_grouped_mxfp8(int fmt, int fused, int act, int E, int KU, int64_t max_rows, int64_t k, int64_t n,
+                          int64_t x_rows, const int32_t *tile_info, const int32_t *rowmap, const void *x,
+                          const void *x_scales, const void *w, const void *ws, const void *w2, const void *ws2,
                           const float *bias, const float *bias2, uint8_t *codes, uint8_t *scales,
                           qmm_stream_t stream);
 

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "../../include/qmm.h"
 
 namespace qmm {
@@ -79,6 +81,18 @@ inline bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_
 inline int launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? QMM_OK : QMM_ERR_LAUNCH;
+}
+
+// Raises kernel fn's dynamic-LDS limit to `bytes` (the largest any launch of it asks for) on the current device, once
+// per device: `done` holds one bit per device id (ids >= 32 are raised on every call, which is harmless).
+inline int raise_dyn_lds(const void *fn, int bytes, std::atomic<unsigned> &done) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return QMM_ERR_LAUNCH;
+  const unsigned bit = dev < 32 ? 1u << dev : 0u;
+  if (bit && (done.load(std::memory_order_relaxed) & bit)) return QMM_OK;
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) return QMM_ERR_LAUNCH;
+  done.fetch_or(bit, std::memory_order_relaxed);
+  return QMM_OK;
 }
 
 inline int64_t block_values(int fmt) {

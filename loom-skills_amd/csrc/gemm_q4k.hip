@@ -1,5 +1,6 @@
-// Q4_K matmuls on the f16 MFMA: the prefill GEMM g_gemm_q4_k_{store|acc} (S/gen_gemm.py:535-703) and the MoE
-// grouped expert GEMMs g_moe_ggu_q4_k[_fused]_k{H} / g_moe_gdn_q4_k_k{FE} (S/gen_moe.py:1126-1228).
+// GGUF-block matmuls on the f16 MFMA (Q4_K, Q6_K, Q4_0): the prefill GEMM g_gemm_{fmt}_{store|acc|swiglu}
+// (S/gen_gemm.py:535-703) and the MoE grouped expert GEMMs g_moe_ggu_{fmt}[_fused]_k{H} / g_moe_gdn_{fmt}_k{FE}
+// (S/gen_moe.py:1126-1228; the Q4_0 expert staging of S/moe_q4_0.py:11-61).
 //
 //   dense   Y[r, c]   = (acc ? Y[r, c] : 0) + inv[r] sum_k X16[r, k] W[c, k]
 //   gu      act[r, c] = act_fn(inv[t] sum_k X16[t, k] Wg[e][c, k] + bg[e, c], inv[t] sum_k X16[t, k] Wu[e][c, k]
@@ -9,9 +10,10 @@
 // for every row r of every 64-row tile whose expert e = tile_info[tile, 0] >= 0; rows with rowmap[r] < 0 are
 // written as zeros. The optional expert biases (gpt-oss ffn_{gate,up,down}_exps.bias) are added after the row
 // inverse, before the activation (_gemm_bias_act, S/gen_moe.py:958-1007). X16 / A16 are the row-scaled f16 operands the reference's g_row_scale_f16[_tiles] produces
-// (S/gen_llm.py:1843-1915, S/gen_moe.py:503-527) and inv = their scales[row, 1]. W is Q4_K, dequantized to f16 in
-// registers the way the reference stages it (S/gen_gemm.py:499-530): w = fma_f16(f16(q), f16(d sc), f16(-dmin m)).
-// fp32 accumulation throughout.
+// (S/gen_llm.py:1843-1915, S/gen_moe.py:503-527) and inv = their scales[row, 1]. W is dequantized to f16 in
+// registers the way the reference stages it: Q4_K w = fma_f16(f16(q), f16(d sc), f16(-dmin m)) (S/gen_gemm.py:499-530),
+// Q6_K w = fma_f16(f16(q), f16(d sc), f16(-32 d sc)) (S/gen_gemm.py:369-444), Q4_0 w = f16(q - 8) * d with one f16
+// rounding (S/moe_q4_0.py:11-38: exactly f16(d (q - 8)) for every finite f16 d). fp32 accumulation throughout.
 //
 // Tiling (gfx950, wave64). A workgroup has four waves and one 64-row tile. Dense and dn: the tile is 64 x 128 and
 // wave (nh, kh) computes the 64 x 64 quadrant nh over K-half kh; gu: the tile is 64 x 64 and wave (mat, kh)
@@ -23,9 +25,12 @@
 // run DEPTH steps ahead of the math through register rings; the loads are unconditional (clamped addresses), so no
 // branch splits the load stream and the compiler keeps them in flight.
 //
-// MFMA operand order. Lane l of a 32x32x16 step holds 8 K values of row/column l % 32, octet l / 32. Lane half h
-// takes code bytes 16h .. 16h+15 of a page, i.e. values 16h .. 16h+15 of both of the page's sub-blocks; K16 step
-// s2 of a sub-block uses the lane's values 8 s2 .. 8 s2 + 7. The A fragment is read from LDS at the same K.
+// MFMA operand order. Lane l of a 32x32x16 step holds 8 K values of row/column l % 32, octet l / 32. Q4_K / Q6_K:
+// lane half h takes code bytes 16h .. 16h+15 of a page, i.e. values 16h .. 16h+15 of both of the page's sub-blocks
+// (gl = 0, 1); K16 step s2 of a sub-block uses the lane's values 8 s2 .. 8 s2 + 7, step position 32 gl + 16 h + 8 s2.
+// Q4_0: a 64-value step is two blocks and lane half h takes block h's 16 code bytes, whose low nibbles (gl = 0) are
+// the block's values 0..15 and high nibbles (gl = 1) values 16..31: step position 32 h + 16 gl + 8 s2. The A fragment
+// is read from LDS at the same K.
 //
 // Tile order is XCD-aware: consecutive tile ids land on one XCD (dense: the M tiles of one N tile, which share
 // weight columns; grouped: the column blocks of one expert tile, which share its activation rows).
@@ -47,6 +52,8 @@ typedef __attribute__((ext_vector_type(2))) _Float16 h2;
 // kDense: Y (+)= X W^T; kSwiglu: Y = silu(X Wg^T inv) (X Wu^T inv) over dense rows (the GEMM's swiglu mode);
 // kGU / kDN: the grouped gate/up and down GEMMs over bucketed expert tiles
 enum Kind { kDense = 0, kGU = 1, kDN = 2, kSwiglu = 3 };
+// weight formats: GGUF Q4_K (144-byte super-blocks), Q6_K (210), Q4_0 (18-byte blocks of 32)
+enum WFmt { kWQ4K = 0, kWQ6K = 1, kWQ40 = 2 };
 
 __device__ __forceinline__ h2 as_h2(u32 v) { return __builtin_bit_cast(h2, v); }
 __device__ __forceinline__ u32 as_u32(h2 v) { return __builtin_bit_cast(u32, v); }
@@ -69,6 +76,21 @@ template <bool HI>
 __device__ __forceinline__ f16x8 deq8(u32 q0, u32 q1, h2 dsc, h2 nmn) {
   return deq8_codes(HI ? (q0 >> 4) & 0x0F0F0F0Fu : q0 & 0x0F0F0F0Fu, HI ? (q1 >> 4) & 0x0F0F0F0Fu : q1 & 0x0F0F0F0Fu,
                     dsc, nmn);
+}
+// Q4_0: 8 f16 weights from two code dwords: (1024 + q) - 1032 = q - 8 exactly, then one rounding f16 multiply by d
+// (f16(d (q - 8)), the reference's staging, also where -8 d would overflow f16)
+template <bool HI>
+__device__ __forceinline__ f16x8 deq8_q40(u32 q0, u32 q1, h2 d) {
+  const u32 n0 = HI ? (q0 >> 4) & 0x0F0F0F0Fu : q0 & 0x0F0F0F0Fu, n1 = HI ? (q1 >> 4) & 0x0F0F0F0Fu : q1 & 0x0F0F0F0Fu;
+  const u32 k64 = 0x64646464u;
+  const h2 m1032 = __builtin_bit_cast(h2, 0xE408E408u);
+  const u32 t[4] = {__builtin_amdgcn_perm(k64, n0, 0x04010400u), __builtin_amdgcn_perm(k64, n0, 0x04030402u),
+                    __builtin_amdgcn_perm(k64, n1, 0x04010400u), __builtin_amdgcn_perm(k64, n1, 0x04030402u)};
+  u32 o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = __builtin_bit_cast(u32, (__builtin_bit_cast(h2, t[i]) + m1032) * d);
+  typedef __attribute__((ext_vector_type(4))) u32 u32x4;
+  return __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]});
 }
 
 // Q6_K (210-byte super-blocks, only 2-byte aligned): 16-byte pieces are loaded at any even address (the HSA
@@ -119,10 +141,11 @@ struct Args {
 // pairs per column with one 8-byte LDS read instead of loading and decoding the super-block header again.
 constexpr int kStagedMaxK = 6144;
 
-template <int KIND, bool ACC, bool BF16OUT, int DEPTH, bool STAGED, bool Q6, int KS>
+template <int KIND, bool ACC, bool BF16OUT, int DEPTH, bool STAGED, int WF, int KS>
 __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
   constexpr int NT = 128 * KS;   // threads: 2 column halves (or matrices) x KS K-parts
-  static_assert(!(Q6 && STAGED), "Q6_K scales are read with the codes");
+  constexpr bool Q6 = WF == kWQ6K, Q40 = WF == kWQ40;
+  static_assert(!(WF != kWQ4K && STAGED), "Q6_K / Q4_0 scales are read with the codes");
   constexpr bool kTwoW = KIND == kGU || KIND == kSwiglu;        // two weight matrices (gate, up): wave pairs
   constexpr bool kDenseRows = KIND == kDense || KIND == kSwiglu;  // rows m0 .. m0 + 63 of x, tiles row-major
   constexpr int BN = kTwoW ? 64 : 128;
@@ -181,7 +204,7 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
   // zeros of dead rows) -- expert tiles of prefill batches are often less than half full
   const bool upper = __syncthreads_or(tid >= 32 && my_src >= 0) != 0;
 
-  const int64_t RB = (int64_t)K / 256 * (Q6 ? 210 : 144);
+  const int64_t RB = Q40 ? (int64_t)K / 32 * 18 : (int64_t)K / 256 * (Q6 ? 210 : 144);
   const int S = K / KSTEP, S0 = S / KS;
 
   // ---- A staging map: chunk c = i * NT + tid of 16 bytes; K-part, row, 16-byte column. Loads are unconditional
@@ -243,6 +266,13 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
     sc = ld4u(blk + 192 + 8 * half + 4 * jh);
     dd = *reinterpret_cast<const u16 *>(blk + 208);
   };
+  // Q4_0 step gs: blocks 2 gs and 2 gs + 1; lane half h takes block 2 gs + h (16 code bytes after its f16 d)
+  auto b_q40 = [&](int j, int s, uint4 &q, u32 &dd) {
+    const int gs = kh * S0 + (s < S0 ? s : S0 - 1);
+    const u8 *blk = wcol[j] + (int64_t)(2 * gs + h) * 18;
+    q = ld16u(blk + 2);
+    dd = *reinterpret_cast<const u16 *>(blk);
+  };
   auto b_head = [&](int j, int s) -> uint4 {
     return ld16(wcol[j] + (int64_t)((kh * S0 + (s < S0 ? s : S0 - 1)) >> 2) * 144);
   };
@@ -302,7 +332,7 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
   // Step t lives in slot t % DEPTH; the step loop is unrolled DEPTH times so every slot index is static.
   uint4 aring[DEPTH][4], cring[DEPTH][2], hring[DEPTH][2];
   uint4 q6b[DEPTH][2], q6h[DEPTH][2];   // Q6_K: ql of group B and qh (cring holds ql of group A)
-  u32 q6s[DEPTH][2], q6d[DEPTH][2];
+  u32 q6s[DEPTH][2], q6d[DEPTH][2];      // Q6_K scales and d; Q4_0: d in q6d (cring holds the codes)
   auto load_a = [&](int slot, int st) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) aring[slot][i] = a_load(i, st);
@@ -312,6 +342,8 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
     for (int j = 0; j < 2; ++j) {
       if constexpr (Q6) {
         b_q6(j, st, cring[slot][j], q6b[slot][j], q6h[slot][j], q6s[slot][j], q6d[slot][j]);
+      } else if constexpr (Q40) {
+        b_q40(j, st, cring[slot][j], q6d[slot][j]);
       } else {
         cring[slot][j] = b_code(j, st);
         if constexpr (!STAGED) hring[slot][j] = b_head(j, st);
@@ -357,7 +389,11 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
         h2 dsc[2], nmn[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          if constexpr (Q6) {
+          if constexpr (Q40) {
+            const _Float16 d16 = __builtin_bit_cast(_Float16, (u16)q6d[u][j]);
+            dsc[j] = h2{d16, d16};
+            nmn[j] = h2{0, 0};
+          } else if constexpr (Q6) {
             // f16 (d sc, -32 d sc) of the lane's 16-value run: d sc is exact in f32 (S/gen_gemm.py:435-444)
             const float sv = f16_to_f32(q6d[u][j]) * (float)(signed char)((q6s[u][j] >> (8 * (2 * gl + h))) & 0xFFu);
             const _Float16 a16 = (_Float16)sv, b16 = (_Float16)(-32.f * sv);
@@ -386,16 +422,20 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
               const u32 c0 = ((l0 >> ls) & 0x0F0F0F0Fu) | (((h0 >> hs) & 0x03030303u) << 4);
               const u32 c1 = ((l1 >> ls) & 0x0F0F0F0Fu) | (((h1 >> hs) & 0x03030303u) << 4);
               bf[j] = deq8_codes(c0, c1, dsc[j], nmn[j]);
+            } else if constexpr (Q40) {
+              const u32 q0 = s2 ? cring[u][j].z : cring[u][j].x, q1 = s2 ? cring[u][j].w : cring[u][j].y;
+              bf[j] = gl ? deq8_q40<true>(q0, q1, dsc[j]) : deq8_q40<false>(q0, q1, dsc[j]);
             } else {
               const u32 q0 = s2 ? cring[u][j].z : cring[u][j].x, q1 = s2 ? cring[u][j].w : cring[u][j].y;
               bf[j] = gl ? deq8<true>(q0, q1, dsc[j], nmn[j]) : deq8<false>(q0, q1, dsc[j], nmn[j]);
             }
           }
-          af[0] = *reinterpret_cast<const f16x8 *>(&As[buf][kh][lc][32 * gl + 16 * h + 8 * s2]);
+          const int ak = Q40 ? 32 * h + 16 * gl + 8 * s2 : 32 * gl + 16 * h + 8 * s2;   // the lane's K position
+          af[0] = *reinterpret_cast<const f16x8 *>(&As[buf][kh][lc][ak]);
 #pragma unroll
           for (int j = 0; j < 2; ++j) acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[0], bf[j], acc[0][j], 0, 0, 0);
           if (upper) {
-            af[1] = *reinterpret_cast<const f16x8 *>(&As[buf][kh][32 + lc][32 * gl + 16 * h + 8 * s2]);
+            af[1] = *reinterpret_cast<const f16x8 *>(&As[buf][kh][32 + lc][ak]);
 #pragma unroll
             for (int j = 0; j < 2; ++j)
               acc[1][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[1], bf[j], acc[1][j], 0, 0, 0);
@@ -504,49 +544,60 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
 // has two waves a SIMD, so one wave's dequantization overlaps the other's MFMAs (the grid of a 512-row GEMM is one
 // workgroup a CU). The grouped GEMMs keep two K-parts (their expert tiles are many and their K short), and so does
 // Q6_K.
-template <int KIND, bool ACC, bool BF16OUT, bool Q6 = false>
+template <int KIND, bool ACC, bool BF16OUT, int WF = kWQ4K>
 int launch(const Args &a, hipStream_t s) {
   constexpr bool kDenseRows = KIND == kDense || KIND == kSwiglu;
-  constexpr int KS = kDenseRows && !Q6 ? 4 : 2;   // Q6_K's wider rings would spill at two waves a SIMD
+  constexpr int KS = kDenseRows && WF != kWQ6K ? 4 : 2;   // Q6_K's wider rings would spill at two waves a SIMD
   // staged scale tables beside the K-parts' activation buffers: 16 (K + 64) bytes, within 160 KB of LDS
   constexpr int kMaxK = KS == 4 ? 5120 : kStagedMaxK;
   const dim3 grid((unsigned)(kDenseRows ? 8 * ((a.tiles_total + 7) / 8) : 8 * a.n_blocks * ((a.tiles_m + 7) / 8)));
-  if constexpr (Q6) {
-    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, false, true, KS><<<grid, 128 * KS, 0, s>>>(a);
+  if constexpr (WF != kWQ4K) {
+    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, false, WF, KS><<<grid, 128 * KS, 0, s>>>(a);
     return launch_status();
   }
   if (a.K <= kMaxK) {
     const size_t dyn = (size_t)128 * (a.K / 32 + 2) * 4;
-    if (dyn > 32768) {   // beyond the default dynamic LDS limit: raise it once
-      static bool raised = false;
-      if (!raised) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void *>(&q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, true, false, KS>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)((size_t)128 * (kMaxK / 32 + 2) * 4)) !=
-            hipSuccess)
-          return QMM_ERR_LAUNCH;
-        raised = true;
-      }
+    if (dyn > 32768) {   // beyond the default dynamic LDS limit: raised to the largest table this kernel stages
+      static std::atomic<unsigned> raised{0};
+      if (int st = raise_dyn_lds(reinterpret_cast<const void *>(&q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, true, kWQ4K, KS>),
+                                 (int)((size_t)128 * (kMaxK / 32 + 2) * 4), raised))
+        return st;
     }
-    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, true, false, KS><<<grid, 128 * KS, dyn, s>>>(a);
+    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, true, kWQ4K, KS><<<grid, 128 * KS, dyn, s>>>(a);
   } else {
-    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, false, false, KS><<<grid, 128 * KS, 0, s>>>(a);
+    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, false, kWQ4K, KS><<<grid, 128 * KS, 0, s>>>(a);
   }
   return launch_status();
 }
+
+// the instantiation of (KIND, ACC, BF16OUT) for the weight format
+template <int KIND, bool ACC, bool BF16OUT>
+int launch_fmt(int fmt, const Args &a, hipStream_t s) {
+  if (fmt == QMM_Q6_K) return launch<KIND, ACC, BF16OUT, kWQ6K>(a, s);
+  if (fmt == QMM_Q4_0) return launch<KIND, ACC, BF16OUT, kWQ40>(a, s);
+  return launch<KIND, ACC, BF16OUT, kWQ4K>(a, s);
+}
+
+// bytes per row of K values, and the weight alignment the loads need (Q4_K: 16; Q6_K: 4, super-blocks realigned from
+// even addresses; Q4_0: 2, 16-byte code runs read from even addresses)
+int64_t fmt_row_bytes(int fmt, int64_t k) {
+  return fmt == QMM_Q4_0 ? k / 32 * 18 : k / 256 * (fmt == QMM_Q6_K ? 210 : 144);
+}
+int fmt_align(int fmt) { return fmt == QMM_Q4_K ? 16 : fmt == QMM_Q6_K ? 4 : 2; }
 
 }  // namespace
 
 extern "C" int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, const void *x, int x_dtype,
                         const float *scales, const void *w, const void *w2, void *y, int y_dtype,
                         qmm_stream_t stream) {
-  if (fmt != QMM_Q4_K && fmt != QMM_Q6_K) return QMM_ERR_FORMAT;
+  if (fmt != QMM_Q4_K && fmt != QMM_Q6_K && fmt != QMM_Q4_0) return QMM_ERR_FORMAT;   // MXFP4: qmm_gemm_mxfp4
   if (mode != QMM_GEMM_STORE && mode != QMM_GEMM_ACC && mode != QMM_GEMM_SWIGLU) return QMM_ERR_RANGE;
   if (!x || !w || !y || (mode == QMM_GEMM_SWIGLU && !w2)) return QMM_ERR_NULL;
   if (x_dtype != QMM_F16) return QMM_ERR_DTYPE;   // bf16 / f32 rows go through qmm_row_scale_f16 first
   if (y_dtype != QMM_F32 && y_dtype != QMM_BF16) return QMM_ERR_DTYPE;
   if (rows <= 0 || n <= 0 || k <= 0 || k % 256) return QMM_ERR_SHAPE;
   if (rows > (1 << 24) || n > (1 << 24) || k > (1 << 20)) return QMM_ERR_SHAPE;
-  const int wal = fmt == QMM_Q6_K ? 4 : 16;
+  const int wal = fmt_align(fmt);
   if (!aligned(x, 16) || !aligned(w, wal) || !aligned(y, 4) || (w2 && !aligned(w2, wal))) return QMM_ERR_ALIGN;
   if (rows * k * 2 >= (1ll << 31)) return QMM_ERR_SHAPE;   // activation rows are addressed by a 32-bit buffer offset
   Args a{};
@@ -556,36 +607,27 @@ extern "C" int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, c
   a.tiles_m = (int)((rows + BM - 1) / BM);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool acc = mode == QMM_GEMM_ACC, bf = y_dtype == QMM_BF16;
-  const bool q6 = fmt == QMM_Q6_K;
   if (mode == QMM_GEMM_SWIGLU) {   // 64 output columns a workgroup: its wave pairs take the gate and the up matrix
     a.tiles_total = a.tiles_m * (int)((n + 63) / 64);
-    if (q6) return bf ? launch<kSwiglu, false, true, true>(a, s) : launch<kSwiglu, false, false, true>(a, s);
-    return bf ? launch<kSwiglu, false, true>(a, s) : launch<kSwiglu, false, false>(a, s);
+    return bf ? launch_fmt<kSwiglu, false, true>(fmt, a, s) : launch_fmt<kSwiglu, false, false>(fmt, a, s);
   }
   a.tiles_total = a.tiles_m * (int)((n + 127) / 128);
-  if (q6) {
-    if (acc && bf) return launch<kDense, true, true, true>(a, s);
-    if (acc) return launch<kDense, true, false, true>(a, s);
-    if (bf) return launch<kDense, false, true, true>(a, s);
-    return launch<kDense, false, false, true>(a, s);
-  }
-  if (acc && bf) return launch<kDense, true, true>(a, s);
-  if (acc) return launch<kDense, true, false>(a, s);
-  if (bf) return launch<kDense, false, true>(a, s);
-  return launch<kDense, false, false>(a, s);
+  if (acc && bf) return launch_fmt<kDense, true, true>(fmt, a, s);
+  if (acc) return launch_fmt<kDense, true, false>(fmt, a, s);
+  if (bf) return launch_fmt<kDense, false, true>(fmt, a, s);
+  return launch_fmt<kDense, false, false>(fmt, a, s);
 }
 
-// The Q4_K / Q6_K path of qmm_moe_grouped (grouped.hip checks the arguments shared with the MXFP4 path).
+// The Q4_K / Q6_K / Q4_0 path of qmm_moe_grouped (grouped.hip checks the arguments shared with the MXFP4 path).
 int qmm_grouped_q4k(int fmt, int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
                     const int32_t *tile_info, const int32_t *rowmap, const void *x, const float *x_scales,
                     int64_t x_rows, const void *w, const void *w2, const float *bias, const float *bias2, float *y,
                     hipStream_t s) {
   if (k % 256) return QMM_ERR_SHAPE;
   if (x_rows * k * 2 >= (1ll << 31)) return QMM_ERR_SHAPE;   // activation rows are addressed by a 32-bit buffer offset
-  const bool q6 = fmt == QMM_Q6_K;
-  const int wal = q6 ? 4 : 16;
+  const int wal = fmt_align(fmt);
   if (!aligned(x, 16) || !aligned(w, wal) || (w2 && !aligned(w2, wal))) return QMM_ERR_ALIGN;
-  const int64_t RB = k / 256 * (q6 ? 210 : 144);
+  const int64_t RB = fmt_row_bytes(fmt, k);
   Args a{};
   a.M = (int)(max_tiles * BM); a.N = (int)n; a.K = (int)k;
   a.x16 = static_cast<const _Float16 *>(x); a.scales = x_scales; a.x_rows = (int)x_rows;
@@ -600,11 +642,11 @@ int qmm_grouped_q4k(int fmt, int mode, int fused, int act, int64_t max_tiles, in
     a.n_blocks = (int)((n + 63) / 64);
     a.tiles_m = (int)max_tiles;
     a.tiles_total = (int)max_tiles * a.n_blocks;
-    return q6 ? launch<kGU, false, false, true>(a, s) : launch<kGU, false, false>(a, s);
+    return launch_fmt<kGU, false, false>(fmt, a, s);
   }
   a.ebytes = RB * n;
   a.n_blocks = (int)((n + 127) / 128);
   a.tiles_m = (int)max_tiles;
   a.tiles_total = (int)max_tiles * a.n_blocks;
-  return q6 ? launch<kDN, false, false, true>(a, s) : launch<kDN, false, false>(a, s);
+  return launch_fmt<kDN, false, false>(fmt, a, s);
 }

@@ -15,6 +15,11 @@
 // then adds, per 32-value group of its half super-block, (di d sc - xs dmin m) da with di the exact int32 dot of
 // codes. The row's four lanes meet in a butterfly, the waves in LDS in a fixed order; for K = 4096 the arithmetic
 // and its order are those of the GGUF-layout kernel, so both give the same bits.
+//
+// Two-matrix variants stream a second matrix W2 of the same shape in the same waves, with the same per-lane arithmetic
+// and reductions for each: swiglu y = silu(x W^T) (x W2^T) (g_mv_q4_k_k{K}_swiglu[_t{TG}]_q8, S/gen_llm.py:1159-1197)
+// and pair y = x W^T, y2 = x W2^T (g_mv_q4_k_k{K}_pair[_t{TG}]_q8, S/gen_llm.py:1166-1176), each row of a pair
+// equal bit for bit to the one-matrix kernel's.
 #include <type_traits>
 
 #include "bfly.hpp"
@@ -27,6 +32,7 @@ typedef __attribute__((ext_vector_type(4))) u32 v4u;
 typedef __attribute__((ext_vector_type(2))) u32 v2u;
 
 constexpr int kUnit = 4608, kMaxWaves = 8;
+enum Mode { kPlain = 0, kSwiglu = 1, kPair = 2 };
 
 __device__ __forceinline__ int sdot4(u32 a, u32 b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
@@ -74,14 +80,16 @@ __device__ __forceinline__ void q8_group(const float (&v)[8], u32 &c0, u32 &c1, 
   sum = (float)s;
 }
 
-template <int TG, int U, bool STAGEQ>
+template <int TG, int U, bool STAGEQ, int MODE>
 __global__ __launch_bounds__(kMaxWaves * 64) void mv_q4kt_q8_kernel(int64_t n, int64_t tokens, int64_t K,
                                                                    int accumulate, const void *__restrict__ x, int bf,
-                                                                   const u8 *__restrict__ w, float *__restrict__ y) {
+                                                                   const u8 *__restrict__ w, const u8 *__restrict__ w2,
+                                                                   float *__restrict__ y, float *__restrict__ y2) {
   constexpr int SLICE = 512 * U, NG = SLICE / 32;   // values / Q8 groups of a wave
+  constexpr int NM = MODE == kPlain ? 1 : 2;        // weight matrices streamed
   __shared__ __align__(16) u32 xc[kMaxWaves][TG][SLICE / 4];
   __shared__ __align__(16) float xm[kMaxWaves][TG][NG][2];
-  __shared__ float red[kMaxWaves][16][TG];
+  __shared__ float red[kMaxWaves][NM][16][TG];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NW = (int)(blockDim.x >> 6);
   const int64_t t0 = (int64_t)blockIdx.y * TG;
@@ -89,8 +97,8 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mv_q4kt_q8_kernel(int64_t n, i
   const int r = lane >> 2, sb = (lane >> 1) & 1, h = lane & 1;
   const int64_t k0 = (int64_t)wave * SLICE;         // the wave's first value
 
-  // ---- the wave's activations first, then its weights: U units (a header and four code planes each) through two
-  //      register slots, units 0 and 1 now and unit u + 2 once unit u is consumed
+  // ---- the wave's activations first, then its weights: U units (a header and four code planes each) through
+  //      NSLOT register slots, units 0 .. NSLOT - 1 now and unit u + NSLOT once unit u is consumed
   float xv[TG][U][8];
   v2u qv[TG][U];
   float2 mv[TG];
@@ -108,13 +116,18 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mv_q4kt_q8_kernel(int64_t n, i
       mv[t] = meta[tok * (K / 32) + k0 / 32 + (lane < NG ? lane : 0)];
     }
   }
-  constexpr int NSLOT = U == 1 ? 1 : 2;
-  v4u wd[NSLOT][5];
+  // register slots of the weight ring: two (units u and u + 1 in flight) for one matrix; one for two matrices, whose
+  // unit already keeps ten 16-byte loads in flight (two slots would spill from U = 2 on)
+  constexpr int NSLOT = (U == 1 || NM == 2) ? 1 : 2;
+  v4u wd[NM][NSLOT][5];
   auto load_unit = [&](int slot, int u) __attribute__((always_inline)) {
-    const v4u *up = reinterpret_cast<const v4u *>(w + (rb * (K / 512) + (int64_t)wave * U + u) * kUnit);
-    wd[slot][0] = up[lane >> 1];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) wd[slot][1 + q] = up[32 + 64 * q + lane];
+    for (int m = 0; m < NM; ++m) {
+      const v4u *up = reinterpret_cast<const v4u *>((m ? w2 : w) + (rb * (K / 512) + (int64_t)wave * U + u) * kUnit);
+      wd[m][slot][0] = up[lane >> 1];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) wd[m][slot][1 + q] = up[32 + 64 * q + lane];
+    }
   };
 #pragma unroll
   for (int u = 0; u < NSLOT; ++u) load_unit(u, u);
@@ -166,7 +179,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mv_q4kt_q8_kernel(int64_t n, i
   constexpr int TH = kHoist ? TG : 1;
   u32 xah[TH][4][8];
   float mdh[TH][4], msh[TH][4];
-  float part[TG];
+  float part[NM][TG];
 
   // the math of unit u held in slot `slot`: adds the lane's partial sums of its half super-block into part[]
   auto unit_math = [&](int u, auto slotc, bool first) __attribute__((always_inline)) {
@@ -185,40 +198,53 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mv_q4kt_q8_kernel(int64_t n, i
           }
       }
     }
-    const v4u hd = wd[slot][0];
-    const float d = f16_to_f32(hd.x), dmin = f16_to_f32(hd.x >> 16);
-    const u32 q[16] = {wd[slot][1].x, wd[slot][1].y, wd[slot][1].z, wd[slot][1].w, wd[slot][2].x, wd[slot][2].y,
-                       wd[slot][2].z, wd[slot][2].w, wd[slot][3].x, wd[slot][3].y, wd[slot][3].z, wd[slot][3].w,
-                       wd[slot][4].x, wd[slot][4].y, wd[slot][4].z, wd[slot][4].w};
-    if constexpr (U > 1) {
-      if (u + 2 < U) load_unit(slot, u + 2);
+    v4u hd[NM];
+    u32 q[NM][16];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      hd[m] = wd[m][slot][0];
+#pragma unroll
+      for (int i2 = 0; i2 < 4; ++i2) {
+        q[m][4 * i2] = wd[m][slot][1 + i2].x; q[m][4 * i2 + 1] = wd[m][slot][1 + i2].y;
+        q[m][4 * i2 + 2] = wd[m][slot][1 + i2].z; q[m][4 * i2 + 3] = wd[m][slot][1 + i2].w;
+      }
     }
-    u32 lo[16], hi[16];   // the code nibbles as int8 lanes, shared by every token
+    if constexpr (U > 1) {
+      if (u + NSLOT < U) load_unit(slot, u + NSLOT);
+    }
+    u32 lo[NM][16], hi[NM][16];   // the code nibbles as int8 lanes, shared by every token
+    float sc[NM][4], mn[NM][4];
 #pragma unroll
-    for (int i2 = 0; i2 < 16; ++i2) { lo[i2] = q[i2] & 0x0F0F0F0Fu; hi[i2] = (q[i2] >> 4) & 0x0F0F0F0Fu; }
-    float sc[4], mn[4];
+    for (int m = 0; m < NM; ++m) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      u32 s_, m_;
-      q4k_scale_min(hd.y, hd.z, hd.w, 4 * h + g, s_, m_);
-      sc[g] = d * (float)s_;
-      mn[g] = dmin * (float)m_;
+      for (int i2 = 0; i2 < 16; ++i2) { lo[m][i2] = q[m][i2] & 0x0F0F0F0Fu; hi[m][i2] = (q[m][i2] >> 4) & 0x0F0F0F0Fu; }
+      const float d = f16_to_f32(hd[m].x), dmin = f16_to_f32(hd[m].x >> 16);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        u32 s_, m_;
+        q4k_scale_min(hd[m].y, hd[m].z, hd[m].w, 4 * h + g, s_, m_);
+        sc[m][g] = d * (float)s_;
+        mn[m][g] = dmin * (float)m_;
+      }
     }
     auto token = [&](int t, const u32 (&xa)[4][8], const float (&md)[4], const float (&ms)[4])
         __attribute__((always_inline)) {
-      float p = 0.f;
 #pragma unroll
-      for (int pg = 0; pg < 2; ++pg) {   // code pages 2 h and 2 h + 1: low nibbles group 2 pg, high 2 pg + 1
-        int ia = 0, ib = 0;
+      for (int m = 0; m < NM; ++m) {
+        float p = 0.f;
 #pragma unroll
-        for (int i2 = 0; i2 < 8; ++i2) {
-          ia = sdot4(lo[8 * pg + i2], xa[2 * pg][i2], ia);
-          ib = sdot4(hi[8 * pg + i2], xa[2 * pg + 1][i2], ib);
+        for (int pg = 0; pg < 2; ++pg) {   // code pages 2 h and 2 h + 1: low nibbles group 2 pg, high 2 pg + 1
+          int ia = 0, ib = 0;
+#pragma unroll
+          for (int i2 = 0; i2 < 8; ++i2) {
+            ia = sdot4(lo[m][8 * pg + i2], xa[2 * pg][i2], ia);
+            ib = sdot4(hi[m][8 * pg + i2], xa[2 * pg + 1][i2], ib);
+          }
+          p += ((float)ia * sc[m][2 * pg] - ms[2 * pg] * mn[m][2 * pg]) * md[2 * pg];
+          p += ((float)ib * sc[m][2 * pg + 1] - ms[2 * pg + 1] * mn[m][2 * pg + 1]) * md[2 * pg + 1];
         }
-        p += ((float)ia * sc[2 * pg] - ms[2 * pg] * mn[2 * pg]) * md[2 * pg];
-        p += ((float)ib * sc[2 * pg + 1] - ms[2 * pg + 1] * mn[2 * pg + 1]) * md[2 * pg + 1];
+        part[m][t] = u == 0 ? p : part[m][t] + p;
       }
-      part[t] = u == 0 ? p : part[t] + p;
     };
     if constexpr (kHoist) {
 #pragma unroll
@@ -235,6 +261,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mv_q4kt_q8_kernel(int64_t n, i
   };
   if constexpr (U == 1) {
     unit_math(0, std::integral_constant<int, 0>{}, true);
+  } else if constexpr (NSLOT == 1) {
+#pragma unroll 1
+    for (int u = 0; u < U; ++u) unit_math(u, std::integral_constant<int, 0>{}, u == 0);
   } else {
     // units in pairs (slots 0 and 1 as constants); the pair loop is not unrolled, so only one pair's fragments
     // are live at a time
@@ -246,50 +275,80 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mv_q4kt_q8_kernel(int64_t n, i
   }
   // the row's four lanes of this wave (its two super-blocks' halves) meet in a butterfly, then the waves in LDS
 #pragma unroll
-  for (int t = 0; t < TG; ++t) {
-    float p = part[t];
-    p += xshfl<1>(p);
-    p += xshfl<2>(p);
-    part[t] = p;
-  }
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int t = 0; t < TG; ++t) {
+      float p = part[m][t];
+      p += xshfl<1>(p);
+      p += xshfl<2>(p);
+      part[m][t] = p;
+    }
   if ((lane & 3) == 0) {
 #pragma unroll
-    for (int t = 0; t < TG; ++t) red[wave][r][t] = part[t];
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int t = 0; t < TG; ++t) red[wave][m][r][t] = part[m][t];
   }
   __syncthreads();
   if (tid < 16 * TG) {
     const int rr = tid / TG, t = tid % TG;
-    float tot = 0.f;
-    for (int wv = 0; wv < NW; ++wv) tot += red[wv][rr][t];
+    float tot[NM];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      tot[m] = 0.f;
+      for (int wv = 0; wv < NW; ++wv) tot[m] += red[wv][m][rr][t];
+    }
     const int64_t row = 16 * rb + rr, tok = t0 + t;
     if (tok < tokens) {
       float *py = y + tok * n + row;
-      *py = accumulate ? *py + tot : tot;
+      if constexpr (MODE == kSwiglu) {
+        const float v = tot[0] / (1.0f + expf(-tot[0])) * tot[NM - 1];
+        *py = accumulate ? *py + v : v;
+      } else {
+        *py = accumulate ? *py + tot[0] : tot[0];
+      }
+      if constexpr (MODE == kPair) {
+        float *py2 = y2 + tok * n + row;
+        *py2 = accumulate ? *py2 + tot[NM - 1] : tot[NM - 1];
+      }
     }
   }
 }
 
-template <int TG, int U, bool STAGEQ>
-int launch_tg(int64_t n, int64_t tokens, int64_t k, int accumulate, const void *x, int bf, const void *w, float *y,
-              int nw, hipStream_t s) {
-  const dim3 grid((unsigned)(n / 16), (unsigned)((tokens + TG - 1) / TG));
-  mv_q4kt_q8_kernel<TG, U, STAGEQ><<<grid, nw * 64, 0, s>>>(n, tokens, k, accumulate, x, bf,
-                                                           static_cast<const u8 *>(w), y);
+// the launch arguments of one call (the weights and outputs of the second matrix for swiglu / pair)
+struct TArgs {
+  int64_t n, tokens, k;
+  int accumulate;
+  const void *x;
+  int bf;
+  const void *w, *w2;
+  float *y, *y2;
+  int nw;
+};
+
+template <int TG, int U, bool STAGEQ, int MODE>
+int launch_tg(const TArgs &a, hipStream_t s) {
+  const dim3 grid((unsigned)(a.n / 16), (unsigned)((a.tokens + TG - 1) / TG));
+  mv_q4kt_q8_kernel<TG, U, STAGEQ, MODE><<<grid, a.nw * 64, 0, s>>>(
+      a.n, a.tokens, a.k, a.accumulate, a.x, a.bf, static_cast<const u8 *>(a.w), static_cast<const u8 *>(a.w2), a.y,
+      a.y2);
   return launch_status();
 }
 
-template <int U, bool STAGEQ>
-int launch_u(int64_t n, int64_t tokens, int64_t k, int accumulate, const void *x, int bf, const void *w, float *y,
-             int nw, hipStream_t s) {
+template <int U, bool STAGEQ, int MODE>
+int launch_u(const TArgs &a, hipStream_t s) {
   // up to 8 tokens a workgroup share its weight loads (the activations of a token stage U x 8 registers a lane,
-  // so the token group shrinks as the slices a wave grow: 8, 4, 2, 1 for U = 1..4); the group is the smallest
-  // power of two holding every token, a workgroup's spare slots repeating its last token without storing it
-  constexpr int TGMAX = U == 1 ? 8 : U == 2 ? 4 : U == 3 ? 2 : 1;
+  // so the token group shrinks as the slices a wave grow: 8, 4, 2, 1 for U = 1..4, halved again when two matrices
+  // stream); the group is the smallest power of two holding every token, a workgroup's spare slots repeating its
+  // last token without storing it
+  constexpr int TG1 = U == 1 ? 8 : U == 2 ? 4 : U == 3 ? 2 : 1;
+  constexpr int TGMAX = MODE == kPlain ? TG1 : (TG1 > 1 ? TG1 / 2 : 1);
   constexpr int T8 = TGMAX >= 8 ? 8 : 1, T4 = TGMAX >= 4 ? 4 : 1, T2 = TGMAX >= 2 ? 2 : 1;
-  if (tokens >= 5 && T8 == 8) return launch_tg<T8, U, STAGEQ>(n, tokens, k, accumulate, x, bf, w, y, nw, s);
-  if (tokens >= 3 && T4 == 4) return launch_tg<T4, U, STAGEQ>(n, tokens, k, accumulate, x, bf, w, y, nw, s);
-  if (tokens >= 2 && T2 == 2) return launch_tg<T2, U, STAGEQ>(n, tokens, k, accumulate, x, bf, w, y, nw, s);
-  return launch_tg<1, U, STAGEQ>(n, tokens, k, accumulate, x, bf, w, y, nw, s);
+  const int64_t tokens = a.tokens;
+  if (tokens >= 5 && T8 == 8) return launch_tg<T8, U, STAGEQ, MODE>(a, s);
+  if (tokens >= 3 && T4 == 4) return launch_tg<T4, U, STAGEQ, MODE>(a, s);
+  if (tokens >= 2 && T2 == 2) return launch_tg<T2, U, STAGEQ, MODE>(a, s);
+  return launch_tg<1, U, STAGEQ, MODE>(a, s);
 }
 
 // One thread per 16-byte piece of the tiled matrix: pieces 0..31 of a unit are the headers of (row p / 2,
@@ -338,31 +397,38 @@ __global__ void dequant_q4kt_kernel(const u8 *__restrict__ w, int64_t rows, int6
   }
 }
 
-}  // namespace
 
-// The tiled-layout path of qmm_mv_q8 (fmt QMM_Q4_KT): rows % 16 == 0, K % 512 == 0, K = 512 U NW with U <= 4
-// slices a wave and NW <= 8 waves.
-int qmm_mv_q4kt_q8(int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype, const void *w,
-                   float *y, hipStream_t s) {
-  if (n % 16 || k % 512 || n / 16 > 2147483647ll || tokens > 65535) return QMM_ERR_SHAPE;   // grid.y <= 65535
-  const int64_t slices = k / 512;
+template <int MODE>
+int launch_mode(TArgs &a, int x_dtype, hipStream_t s) {
+  if (a.n % 16 || a.k % 512 || a.n / 16 > 2147483647ll || a.tokens > 65535) return QMM_ERR_SHAPE;   // grid.y <= 65535
+  const int64_t slices = a.k / 512;
   int U = 1;
   while (U <= 4 && (slices % U || slices / U > kMaxWaves)) ++U;
   if (U > 4) return QMM_ERR_SHAPE;
-  const int nw = (int)(slices / U);
+  a.nw = (int)(slices / U);
   const bool stage = x_dtype != QMM_Q8;
-  const int bf = x_dtype == QMM_BF16;
+  a.bf = x_dtype == QMM_BF16;
   switch (U) {
-    case 1: return stage ? launch_u<1, true>(n, tokens, k, accumulate, x, bf, w, y, nw, s)
-                         : launch_u<1, false>(n, tokens, k, accumulate, x, bf, w, y, nw, s);
-    case 2: return stage ? launch_u<2, true>(n, tokens, k, accumulate, x, bf, w, y, nw, s)
-                         : launch_u<2, false>(n, tokens, k, accumulate, x, bf, w, y, nw, s);
-    case 3: return stage ? launch_u<3, true>(n, tokens, k, accumulate, x, bf, w, y, nw, s)
-                         : launch_u<3, false>(n, tokens, k, accumulate, x, bf, w, y, nw, s);
-    default: return stage ? launch_u<4, true>(n, tokens, k, accumulate, x, bf, w, y, nw, s)
-                          : launch_u<4, false>(n, tokens, k, accumulate, x, bf, w, y, nw, s);
+    case 1: return stage ? launch_u<1, true, MODE>(a, s) : launch_u<1, false, MODE>(a, s);
+    case 2: return stage ? launch_u<2, true, MODE>(a, s) : launch_u<2, false, MODE>(a, s);
+    case 3: return stage ? launch_u<3, true, MODE>(a, s) : launch_u<3, false, MODE>(a, s);
+    default: return stage ? launch_u<4, true, MODE>(a, s) : launch_u<4, false, MODE>(a, s);
   }
 }
+
+}  // namespace
+
+// The tiled-layout path of qmm_mv_q8 (fmt QMM_Q4_KT): rows % 16 == 0, K % 512 == 0, K = 512 U NW with U <= 4
+// slices a wave and NW <= 8 waves. mode 0: y = x W^T; 1 (swiglu): y = silu(x W^T) (x W2^T); 2 (pair): y = x W^T and
+// y2 = x W2^T.
+int qmm_mv_q4kt_q8(int mode, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
+                   const void *w, const void *w2, float *y, float *y2, hipStream_t s) {
+  TArgs a{n, tokens, k, accumulate, x, 0, w, w2, y, y2, 0};
+  if (mode == kSwiglu) return launch_mode<kSwiglu>(a, x_dtype, s);
+  if (mode == kPair) return launch_mode<kPair>(a, x_dtype, s);
+  return launch_mode<kPlain>(a, x_dtype, s);
+}
+
 
 int qmm_dequant_q4kt(const void *w, int64_t rows, int64_t k, float *out, hipStream_t s) {
   if (rows % 16 || k % 512) return QMM_ERR_SHAPE;

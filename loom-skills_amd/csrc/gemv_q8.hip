@@ -17,7 +17,12 @@
 // is the item walk of gemv.hip with Q8 activation fragments (any K % 256 for Q4_K, K % 64 for Q4_0). The Q4_K fast
 // path (K = 4096, 8192) splits K between the eight waves of a workgroup (see mv_q4k_q8s_kernel); given f32 / bf16
 // activations it quantizes them while staging, with the quantizer's own arithmetic, so both input forms give
-// identical results.
+// identical results. The generic matvec also streams two matrices of one input: swiglu y = silu(x W^T) (x W2^T)
+// (g_mv_{fmt}_k{K}_swiglu[_t{TG}]_q8) and pair y = x W^T, y2 = x W2^T (g_mv_{fmt}_k{K}_pair[_t{TG}]_q8,
+// S/gen_llm.py:1159-1197), each matrix's rows rounded as the one-matrix kernel rounds them.
+//
+//   qmm_moe_expert_mv_q8  the decode expert matvecs on Q8_1 activations, g_moe_{gu|dn}_{fmt}[_fused]_q8_k{K}_r{R}
+//                         (S/gen_moe.py:535-727 with iq; the MOE_Q8 default of S/gen_llm.py:5290-5303)
 #include "bfly.hpp"
 #include "rowdot.hpp"
 
@@ -210,23 +215,40 @@ struct Q6K8 {
   }
 };
 
-constexpr int kWaves = 4, kRW = 4;
+constexpr int kWaves = 4;
+enum Mode { kPlain = 0, kSwiglu = 1, kPair = 2 };
 
-template <class P, int TG>
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
+__device__ __forceinline__ float act_fn(int act, float g, float u) {
+  if (act == QMM_ACT_SWIGLU_OAI) {
+    const float xg = fminf(g, 7.0f);
+    const float yu = fminf(fmaxf(u, -7.0f), 7.0f);
+    return xg / (1.0f + expf(-1.702f * xg)) * (yu + 1.0f);
+  }
+  return silu_mul(g, u);
+}
+
+// RW rows per wave (4 for one matrix, 2 when two stream), TG tokens per workgroup sharing every weight load
+template <class P, int TG, int MODE, int RW>
 __global__ __launch_bounds__(256) void mv_q8_kernel(int64_t n, int64_t tokens, int64_t k, int accumulate,
                                                     const u8 *__restrict__ codes, const float *__restrict__ meta,
-                                                    const u8 *__restrict__ w, int64_t rb, float *__restrict__ y) {
+                                                    const u8 *__restrict__ w, const u8 *__restrict__ w2, int64_t rb,
+                                                    float *__restrict__ y, float *__restrict__ y2) {
+  constexpr int NM = MODE == kPlain ? 1 : 2;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t t0 = (int64_t)blockIdx.x * TG;
-  const int64_t row0 = ((int64_t)blockIdx.y * kWaves + wave) * kRW;
+  const int64_t row0 = ((int64_t)blockIdx.y * kWaves + wave) * RW;
   if (row0 >= n) return;
   const int nitems = P::items(k);
   const int64_t G = k / 32;
-  float acc[kRW][TG];
+  float acc[NM][RW][TG];
 #pragma unroll
-  for (int r = 0; r < kRW; ++r)
+  for (int m = 0; m < NM; ++m)
 #pragma unroll
-    for (int t = 0; t < TG; ++t) acc[r][t] = 0.f;
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+      for (int t = 0; t < TG; ++t) acc[m][r][t] = 0.f;
   for (int it0 = 0; it0 < nitems; it0 += 64) {
     const int item = it0 + lane;
     const bool live = item < nitems;
@@ -236,29 +258,108 @@ __global__ __launch_bounds__(256) void mv_q8_kernel(int64_t n, int64_t tokens, i
       const int64_t tok = t0 + t;
       xq_load(codes + tok * k, meta + 2 * tok * G, P::group(item), live && tok < tokens, xs[t]);
     }
-    typename P::W wv[kRW];
+    typename P::W wv[NM][RW];
 #pragma unroll
-    for (int r = 0; r < kRW; ++r) P::load_w(w + (row0 + r) * rb, item, live && (row0 + r) < n, wv[r]);
+    for (int m = 0; m < NM; ++m)
 #pragma unroll
-    for (int r = 0; r < kRW; ++r)
+      for (int r = 0; r < RW; ++r) P::load_w((m ? w2 : w) + (row0 + r) * rb, item, live && (row0 + r) < n, wv[m][r]);
 #pragma unroll
-      for (int t = 0; t < TG; ++t) acc[r][t] += P::dot(wv[r], xs[t], item);
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int t = 0; t < TG; ++t) acc[m][r][t] += P::dot(wv[m][r], xs[t], item);
   }
 #pragma unroll
-  for (int r = 0; r < kRW; ++r)
+  for (int m = 0; m < NM; ++m)
 #pragma unroll
-    for (int t = 0; t < TG; ++t) acc[r][t] = wave_sum(acc[r][t]);
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+      for (int t = 0; t < TG; ++t) acc[m][r][t] = wave_sum(acc[m][r][t]);
   if (lane == 0) {
 #pragma unroll
-    for (int r = 0; r < kRW; ++r)
+    for (int r = 0; r < RW; ++r)
 #pragma unroll
       for (int t = 0; t < TG; ++t) {
         const int64_t row = row0 + r, tok = t0 + t;
         if (row < n && tok < tokens) {
           float *py = y + tok * n + row;
-          *py = accumulate ? *py + acc[r][t] : acc[r][t];
+          const float v = MODE == kSwiglu ? silu_mul(acc[0][r][t], acc[NM - 1][r][t]) : acc[0][r][t];
+          *py = accumulate ? *py + v : v;
+          if constexpr (MODE == kPair) {
+            float *py2 = y2 + tok * n + row;
+            *py2 = accumulate ? *py2 + acc[NM - 1][r][t] : acc[NM - 1][r][t];
+          }
         }
       }
+  }
+}
+
+// The decode expert matvecs on Q8_1 activations: one assignment a per workgroup column (blockIdx.x), RW = 4 output
+// rows per wave; e = clamp(ids[a], 0, E - 1) (S/gen_moe.py:592-596). gu: act[a] = act_fn(Wg[e] xq[a / KU], Wu[e]
+// xq[a / KU]) (+ the expert biases before the activation); dn: ys[a] = Wd[e] xq[a] (+ bias). xq is the planar Q8_1
+// buffer of x_rows rows (gu: the tokens; dn: the assignments).
+template <class P, bool GU>
+__global__ __launch_bounds__(256) void expert_mv_q8_kernel(int64_t n, int64_t assignments, int KU, int E, int64_t k,
+                                                           const int32_t *__restrict__ ids, const u8 *__restrict__ codes,
+                                                           const float *__restrict__ meta, const u8 *__restrict__ w,
+                                                           const u8 *__restrict__ w2, int64_t rb, int64_t ebytes,
+                                                           const float *__restrict__ bias,
+                                                           const float *__restrict__ bias2, int act,
+                                                           float *__restrict__ y) {
+  constexpr int RW = 4, NM = GU ? 2 : 1;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t a = blockIdx.x;
+  const int64_t row0 = ((int64_t)blockIdx.y * kWaves + wave) * RW;
+  if (row0 >= n || a >= assignments) return;
+  int e = ids[a];
+  e = e < 0 ? 0 : (e >= E ? E - 1 : e);
+  const int64_t xr = GU ? a / KU : a;
+  const int64_t G = k / 32;
+  const u8 *xc = codes + xr * k;
+  const float *xm = meta + 2 * xr * G;
+  const u8 *we[NM];
+  we[0] = w + e * ebytes;
+  if constexpr (GU) we[NM - 1] = w2 + e * ebytes;
+  const int nitems = P::items(k);
+  float acc[NM][RW];
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int r = 0; r < RW; ++r) acc[m][r] = 0.f;
+  for (int it0 = 0; it0 < nitems; it0 += 64) {
+    const int item = it0 + lane;
+    const bool live = item < nitems;
+    XQ xs;
+    xq_load(xc, xm, P::group(item), live, xs);
+    typename P::W wv[NM][RW];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int r = 0; r < RW; ++r) P::load_w(we[m] + (row0 + r) * rb, item, live && (row0 + r) < n, wv[m][r]);
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int r = 0; r < RW; ++r) acc[m][r] += P::dot(wv[m][r], xs, item);
+  }
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+#pragma unroll
+    for (int r = 0; r < RW; ++r) acc[m][r] = wave_sum(acc[m][r]);
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int64_t row = row0 + r;
+    if (lane == r && row < n) {
+      float g = acc[0][r];
+      if (bias) g += bias[e * n + row];
+      float v = g;
+      if constexpr (GU) {
+        float u = acc[NM - 1][r];
+        if (bias2) u += bias2[e * n + row];
+        v = act_fn(act, g, u);
+      }
+      y[a * n + row] = v;
+    }
   }
 }
 
@@ -458,22 +559,52 @@ extern "C" int qmm_quant_q8(int64_t rows, int64_t k, const void *x, int x_dtype,
   return launch_status();
 }
 
-int qmm_mv_q4kt_q8(int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype, const void *w,
-                   float *y, hipStream_t s);
+int qmm_mv_q4kt_q8(int mode, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
+                   const void *w, const void *w2, float *y, float *y2, hipStream_t s);
 
-extern "C" int qmm_mv_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
-                         const void *w, float *y, qmm_stream_t stream) {
+namespace {
+// the generic (GGUF-layout, planar Q8_1) matvec of one format in one mode
+template <class P, int MODE>
+int launch_generic(int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, const void *w, const void *w2,
+                   int64_t rb, float *y, float *y2, hipStream_t s) {
+  constexpr int TG = 2, RW = MODE == kPlain ? 4 : 2;
+  const u8 *codes = static_cast<const u8 *>(x);
+  const float *meta = reinterpret_cast<const float *>(codes + tokens * k);
+  const dim3 grid((unsigned)((tokens + TG - 1) / TG), (unsigned)((n + kWaves * RW - 1) / (kWaves * RW)));
+  if (grid.x > 2147483647u || grid.y > 65535u) return QMM_ERR_SHAPE;
+  mv_q8_kernel<P, TG, MODE, RW><<<grid, 256, 0, s>>>(n, tokens, k, accumulate, codes, meta, static_cast<const u8 *>(w),
+                                                    static_cast<const u8 *>(w2), rb, y, y2);
+  return launch_status();
+}
+
+template <int MODE>
+int generic_fmt(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, const void *w,
+                const void *w2, float *y, float *y2, hipStream_t s) {
+  const int64_t rb = row_bytes(fmt, k);
+  if (fmt == QMM_Q4_K) return launch_generic<Q4K8, MODE>(k, n, tokens, accumulate, x, w, w2, rb, y, y2, s);
+  if (fmt == QMM_Q6_K) return launch_generic<Q6K8, MODE>(k, n, tokens, accumulate, x, w, w2, rb, y, y2, s);
+  return launch_generic<Q408, MODE>(k, n, tokens, accumulate, x, w, w2, rb, y, y2, s);
+}
+
+// checks shared by the int8 matvec entry points: formats with integer codes (GGUF Q4_K / Q4_0 / Q6_K and tiled Q4_K)
+int check_q8(int fmt, int64_t k, int64_t n, int64_t tokens, const void *x, int x_dtype, const void *w, const float *y) {
   if (!x || !w || !y) return QMM_ERR_NULL;
   if (fmt != QMM_Q4_K && fmt != QMM_Q4_0 && fmt != QMM_Q4_KT && fmt != QMM_Q6_K) return QMM_ERR_FORMAT;
   if (x_dtype != QMM_Q8 && x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
   if (k <= 0 || n <= 0 || tokens <= 0 || n > (1ll << 30) || tokens > (1ll << 24) || k > (1ll << 20))
     return QMM_ERR_SHAPE;
-  if (fmt == QMM_Q4_K && k % 256) return QMM_ERR_SHAPE;
+  if ((fmt == QMM_Q4_K || fmt == QMM_Q6_K) && k % 256) return QMM_ERR_SHAPE;
   if (fmt == QMM_Q4_0 && k % 64) return QMM_ERR_SHAPE;
-  if (fmt == QMM_Q6_K && k % 256) return QMM_ERR_SHAPE;
   if (!aligned(x, 16) || !aligned(w, fmt == QMM_Q6_K ? 4 : 16) || !aligned(y, 4)) return QMM_ERR_ALIGN;
+  return QMM_OK;
+}
+}  // namespace
+
+extern "C" int qmm_mv_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
+                         const void *w, float *y, qmm_stream_t stream) {
+  if (int st = check_q8(fmt, k, n, tokens, x, x_dtype, w, y)) return st;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (fmt == QMM_Q4_KT) return qmm_mv_q4kt_q8(k, n, tokens, accumulate, x, x_dtype, w, y, s);
+  if (fmt == QMM_Q4_KT) return qmm_mv_q4kt_q8(kPlain, k, n, tokens, accumulate, x, x_dtype, w, nullptr, y, nullptr, s);
   const bool fast = fmt == QMM_Q4_K && (k == 4096 || k == 8192) && tokens <= 65535ll * 2;
   if (x_dtype != QMM_Q8) {
     // f32 / bf16 rows are quantized while staged; only the fast path stages (others take planar Q8 from
@@ -486,17 +617,80 @@ extern "C" int qmm_mv_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accu
   if (fast)
     return k == 4096 ? launch_fast_tg<1, false>(n, tokens, accumulate, x, 0, w, y, s)
                      : launch_fast_tg<2, false>(n, tokens, accumulate, x, 0, w, y, s);
+  return generic_fmt<kPlain>(fmt, k, n, tokens, accumulate, x, w, nullptr, y, nullptr, s);
+}
+
+// The two-matrix int8 matvecs (mode kSwiglu / kPair): the tiled Q4_K kernel takes planar Q8_1 or f32 / bf16 rows, the
+// GGUF layouts planar Q8_1.
+static int mv2_q8(int mode, int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
+                  const void *w, const void *w2, float *y, float *y2, qmm_stream_t stream) {
+  if (int st = check_q8(fmt, k, n, tokens, x, x_dtype, w, y)) return st;
+  if (!w2 || (mode == kPair && !y2)) return QMM_ERR_NULL;
+  if (!aligned(w2, fmt == QMM_Q6_K ? 4 : 16) || (y2 && !aligned(y2, 4))) return QMM_ERR_ALIGN;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (fmt == QMM_Q4_KT) return qmm_mv_q4kt_q8(mode, k, n, tokens, accumulate, x, x_dtype, w, w2, y, y2, s);
+  if (x_dtype != QMM_Q8) return QMM_ERR_DTYPE;   // GGUF layouts: the planar Q8_1 buffer of qmm_quant_q8
+  return mode == kSwiglu ? generic_fmt<kSwiglu>(fmt, k, n, tokens, accumulate, x, w, w2, y, nullptr, s)
+                         : generic_fmt<kPair>(fmt, k, n, tokens, accumulate, x, w, w2, y, y2, s);
+}
+
+extern "C" int qmm_mv_swiglu_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x,
+                                int x_dtype, const void *w, const void *w2, float *y, qmm_stream_t stream) {
+  return mv2_q8(kSwiglu, fmt, k, n, tokens, accumulate, x, x_dtype, w, w2, y, nullptr, stream);
+}
+
+extern "C" int qmm_mv_pair_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x,
+                              int x_dtype, const void *w, const void *w2, float *y, float *y2, qmm_stream_t stream) {
+  return mv2_q8(kPair, fmt, k, n, tokens, accumulate, x, x_dtype, w, w2, y, y2, stream);
+}
+
+namespace {
+template <class P>
+int launch_expert_q8(bool gu, int64_t k, int64_t n, int E, int KU, int64_t assignments, const int32_t *ids,
+                     const void *x, const void *w, const void *w2, int64_t rb, int64_t ebytes, const float *bias,
+                     const float *bias2, int act, float *y, hipStream_t s) {
+  const int64_t x_rows = gu ? assignments / KU : assignments;
   const u8 *codes = static_cast<const u8 *>(x);
-  const float *meta = reinterpret_cast<const float *>(codes + tokens * k);
-  const int64_t rb = row_bytes(fmt, k);
-  constexpr int TG = 2;
-  const dim3 grid((unsigned)((tokens + TG - 1) / TG), (unsigned)((n + kWaves * kRW - 1) / (kWaves * kRW)));
-  if (grid.x > 2147483647u || grid.y > 65535u) return QMM_ERR_SHAPE;
-  if (fmt == QMM_Q4_K)
-    mv_q8_kernel<Q4K8, TG><<<grid, 256, 0, s>>>(n, tokens, k, accumulate, codes, meta, static_cast<const u8 *>(w), rb, y);
-  else if (fmt == QMM_Q6_K)
-    mv_q8_kernel<Q6K8, TG><<<grid, 256, 0, s>>>(n, tokens, k, accumulate, codes, meta, static_cast<const u8 *>(w), rb, y);
+  const float *meta = reinterpret_cast<const float *>(codes + x_rows * k);
+  const dim3 grid((unsigned)assignments, (unsigned)((n + kWaves * 4 - 1) / (kWaves * 4)));
+  if (grid.y > 65535u) return QMM_ERR_SHAPE;
+  if (gu)
+    expert_mv_q8_kernel<P, true><<<grid, 256, 0, s>>>(n, assignments, KU, E, k, ids, codes, meta,
+                                                      static_cast<const u8 *>(w), static_cast<const u8 *>(w2), rb,
+                                                      ebytes, bias, bias2, act, y);
   else
-    mv_q8_kernel<Q408, TG><<<grid, 256, 0, s>>>(n, tokens, k, accumulate, codes, meta, static_cast<const u8 *>(w), rb, y);
+    expert_mv_q8_kernel<P, false><<<grid, 256, 0, s>>>(n, assignments, KU, E, k, ids, codes, meta,
+                                                       static_cast<const u8 *>(w), nullptr, rb, ebytes, bias, nullptr,
+                                                       act, y);
   return launch_status();
+}
+}  // namespace
+
+extern "C" int qmm_moe_expert_mv_q8(int fmt, int mode, int fused, int act, int64_t k, int64_t n, int E, int KU,
+                                    int64_t assignments, const int32_t *ids, const void *x, const void *w,
+                                    const void *w2, const float *bias, const float *bias2, float *y,
+                                    qmm_stream_t stream) {
+  if (fmt != QMM_Q4_K && fmt != QMM_Q4_0 && fmt != QMM_Q6_K) return QMM_ERR_FORMAT;
+  if (mode != 0 && mode != 1) return QMM_ERR_RANGE;
+  if (act != QMM_ACT_SILU && act != QMM_ACT_SWIGLU_OAI) return QMM_ERR_RANGE;
+  if (E <= 0 || E > 1024 || KU <= 0 || KU > 8) return QMM_ERR_RANGE;
+  if (!ids || !x || !w || !y) return QMM_ERR_NULL;
+  const bool gu = mode == 0;
+  if (gu && !fused && !w2) return QMM_ERR_NULL;
+  const int64_t rb = row_bytes(fmt, k);
+  if (n <= 0 || assignments <= 0 || assignments > (1 << 24) || rb == 0 || n > (1 << 24)) return QMM_ERR_SHAPE;
+  if (fmt == QMM_Q4_0 && k % 64) return QMM_ERR_SHAPE;
+  if (gu && assignments % KU) return QMM_ERR_SHAPE;
+  const int wal = fmt == QMM_Q4_K ? 16 : 4;
+  if (!aligned(x, 16) || !aligned(w, wal) || (w2 && !aligned(w2, wal)) || !aligned(y, 4)) return QMM_ERR_ALIGN;
+  if (!aligned(bias, 4) || !aligned(bias2, 4)) return QMM_ERR_ALIGN;
+  // a fused [E, 2n, k] gate_up tensor: expert e's n gate rows, then its n up rows (S/gen_moe.py:538)
+  const int64_t ebytes = rb * n * (gu && fused ? 2 : 1);
+  const void *wu = gu && fused ? static_cast<const void *>(static_cast<const u8 *>(w) + rb * n) : w2;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (fmt == QMM_Q4_K)
+    return launch_expert_q8<Q4K8>(gu, k, n, E, KU, assignments, ids, x, w, wu, rb, ebytes, bias, bias2, act, y, s);
+  if (fmt == QMM_Q6_K)
+    return launch_expert_q8<Q6K8>(gu, k, n, E, KU, assignments, ids, x, w, wu, rb, ebytes, bias, bias2, act, y, s);
+  return launch_expert_q8<Q408>(gu, k, n, E, KU, assignments, ids, x, w, wu, rb, ebytes, bias, bias2, act, y, s);
 }

@@ -1,6 +1,7 @@
-// MXFP4 grouped expert GEMMs on the gfx950 scaled MFMA, the g_moe_ggu_mxfp4s[_fused]_k{H} / g_moe_gdn_mxfp4s_k{FE}
-// kernels of the reference's MoE prefill chain (S/gen_moe.py:1126-1228; its fp8 MXFP4 GEMM, S/gen_mxfp4s.py:1-21,
-// is the gfx12 WMMA counterpart):
+// MXFP4 matmuls on the gfx950 scaled MFMA: the grouped expert GEMMs g_moe_ggu_mxfp4s[_fused]_k{H} /
+// g_moe_gdn_mxfp4s_k{FE} of the reference's MoE prefill chain (S/gen_moe.py:1126-1228), and the dense prefill GEMM
+// g_gemm_mxfp4s_{store|swiglu}_f8_m256 (S/gen_mxfp4s.py:50-101, the gfx12 fp8 WMMA counterpart), which is the same
+// kernel over dense 64-row tiles of one weight matrix (qmm_gemm_mxfp4):
 //
 //   gu   act[r, c] = act_fn(sum_k X8[t, k] Wg[e][c, k] + bg[e, c], sum_k X8[t, k] Wu[e][c, k] + bu[e, c]),
 //                    t = rowmap[r] / KU
@@ -73,10 +74,14 @@ constexpr int BM = 64, KC = 64;
 
 enum Kind { kGU = 1, kDN = 2, kGU8 = 3 };   // kGU8: gu with its output quantized to MXFP8
 enum Layout { kSplit = 0, kTiled = 1 };
+// where the output goes: the grouped GEMMs' sorted f32 rows, or a dense GEMM's y (f32 / bf16, stored or added to);
+// a dense kGU is the swiglu GEMM silu(X Wg^T) (X Wu^T) over rows 0 .. M - 1 of x
+enum Out { kOutGrouped = 0, kOutF32 = 1, kOutF32Acc = 2, kOutBF16 = 3, kOutBF16Acc = 4 };
 typedef __attribute__((ext_vector_type(4))) u32 v4u;   // a native vector: the register rings stay in VGPRs
 
 struct MArgs {
   int N, K;
+  int M;                        // dense: rows of x and y
   const u8 *x8, *xs;            // activation codes [rows, K], scales [rows, K/32]
   int x_rows;
   const u8 *wn, *wsc;           // gate (or down) nibbles / scales of expert 0
@@ -148,8 +153,10 @@ __device__ __forceinline__ void copy_to_lds(u8 *dst, const u8 *src, int64_t n, i
   }
 }
 
-template <int KIND, int LAYOUT, int DEPTH, int kSub>
+template <int KIND, int LAYOUT, int DEPTH, int kSub, int OUT>
 __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs a) {
+  constexpr bool DENSE = OUT != kOutGrouped;
+  static_assert(!(DENSE && KIND == kGU8), "the MXFP8 epilogue writes the grouped activation");
   constexpr int APITCH = kSub * KC + 16;     // activation bytes per LDS row (16-byte aligned rows)
   constexpr int BN = 128;                   // output columns per workgroup
   constexpr bool GU = KIND != kDN;
@@ -169,16 +176,19 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
 
   // ---- which tile and column block: the live tiles [0, L) (L = 1 + the last tile with an expert) in eight
   //      contiguous ranges, range x on XCD x, walked tile-fastest
-  if (tid == 0) live_end = 0;
-  __syncthreads();
-  {
-    int last = 0;
-    for (int t = tid; t < a.max_tiles; t += 256)
-      if (a.tile_info[2 * t] >= 0) last = t + 1;
-    if (last) atomicMax(&live_end, last);
+  int L = a.max_tiles;   // dense: every 64-row tile of x
+  if constexpr (!DENSE) {
+    if (tid == 0) live_end = 0;
+    __syncthreads();
+    {
+      int last = 0;
+      for (int t = tid; t < a.max_tiles; t += 256)
+        if (a.tile_info[2 * t] >= 0) last = t + 1;
+      if (last) atomicMax(&live_end, last);
+    }
+    __syncthreads();
+    L = live_end;
   }
-  __syncthreads();
-  const int L = live_end;
   const int xcd = (int)(blockIdx.x & 7), xi = (int)(blockIdx.x >> 3);
   const int t_begin = (int)(((int64_t)xcd * L) >> 3), t_end = (int)(((int64_t)(xcd + 1) * L) >> 3);
   const int cnt = t_end - t_begin;
@@ -189,10 +199,15 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
   // the tile's expert and row map are loaded together; the weight stream starts as soon as the expert is known,
   // before the row map, the activation rows and their scales (every workgroup starts at once, so each dependent
   // round trip before the first weight load is time the HBM idles)
-  const int rm = tid < BM ? a.rowmap[m0 + tid] : -1;
-  int expert = a.tile_info[2 * tile];
-  if (expert < 0) return;
-  expert = expert >= a.E ? a.E - 1 : expert;
+  int rm, expert = 0;
+  if constexpr (DENSE) {
+    rm = tid < BM && m0 + tid < a.M ? m0 + tid : -1;
+  } else {
+    rm = tid < BM ? a.rowmap[m0 + tid] : -1;
+    expert = a.tile_info[2 * tile];
+    if (expert < 0) return;
+    expert = expert >= a.E ? a.E - 1 : expert;
+  }
 
   auto clampc = [&](int c) __attribute__((always_inline)) { return c < C ? c : C - 1; };
   const int SK = K / 32;           // scale bytes per row
@@ -266,7 +281,9 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
   int my_src = -1;
   if (tid < BM) {
     int src;
-    if constexpr (GU) {
+    if constexpr (DENSE) {
+      src = rm;
+    } else if constexpr (GU) {
       src = rm >= 0 ? rm / a.KU : -1;
       src = src < a.x_rows ? src : -1;
     } else {
@@ -433,6 +450,28 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
     return;
   }
   if (col >= N) return;
+  if constexpr (DENSE) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (row >= a.M) continue;
+        float v;
+        if constexpr (GU) v = act_fn(QMM_ACT_SILU, acc[i][0][r], acc[i][1][r]);
+        else v = acc[i][0][r];
+        const int64_t o = (int64_t)row * N + col;
+        if constexpr (OUT == kOutF32 || OUT == kOutF32Acc) {
+          if constexpr (OUT == kOutF32Acc) v += a.y[o];
+          a.y[o] = v;
+        } else {
+          u16 *yb = reinterpret_cast<u16 *>(a.y);
+          if constexpr (OUT == kOutBF16Acc) v += bf16_to_f32(yb[o]);
+          yb[o] = (u16)f32_to_bf16_rne(v);
+        }
+      }
+    return;
+  }
   const float bg = a.bias ? a.bias[(int64_t)expert * N + col] : 0.f;
   const float bu = (GU && a.bias2) ? a.bias2[(int64_t)expert * N + col] : 0.f;
 #pragma unroll
@@ -449,22 +488,26 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
     }
 }
 
-template <int KIND, int LAYOUT>
+constexpr int kMaxK = 12288;   // the workgroup stages (64 + 256) x K / 32 scale bytes in LDS
+
+template <int KIND, int LAYOUT, int OUT = kOutGrouped>
 int launch(const MArgs &a, hipStream_t s) {
   constexpr int kDepth = KIND == kDN ? QMM_MX_DEPTH_DN : QMM_MX_DEPTH_GU;
   constexpr int kSub = KIND == kDN ? QMM_MX_SUB_DN : QMM_MX_SUB_GU;
+  constexpr int kRows = BM + (LAYOUT == kSplit ? (KIND != kDN ? 256 : 128) : 0);   // scale rows staged in LDS
   const dim3 grid((unsigned)(8 * a.n_blocks * ((a.max_tiles + 7) / 8)));
-  const size_t dyn = (size_t)(BM + (LAYOUT == kSplit ? (KIND != kDN ? 256 : 128) : 0)) * (a.K / 32);
-  if (dyn > 32768) {   // beyond the default dynamic LDS limit (K > 3276): raise it once
-    static bool raised = false;
-    if (!raised) {
-      if (hipFuncSetAttribute(reinterpret_cast<const void *>(&mxfp4_grouped_kernel<KIND, LAYOUT, kDepth, kSub>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) != hipSuccess)
-        return QMM_ERR_LAUNCH;
-      raised = true;
+  const size_t dyn = (size_t)kRows * (a.K / 32);
+  if constexpr ((size_t)kRows * (kMaxK / 32) > 32768) {
+    // beyond the default dynamic LDS limit: raised once per device to the largest K this kernel takes, so the order
+    // of calls with different K does not matter
+    if (dyn > 32768) {
+      static std::atomic<unsigned> raised{0};
+      if (int st = raise_dyn_lds(reinterpret_cast<const void *>(&mxfp4_grouped_kernel<KIND, LAYOUT, kDepth, kSub, OUT>),
+                                 kRows * (kMaxK / 32), raised))
+        return st;
     }
   }
-  mxfp4_grouped_kernel<KIND, LAYOUT, kDepth, kSub><<<grid, 256, dyn, s>>>(a);
+  mxfp4_grouped_kernel<KIND, LAYOUT, kDepth, kSub, OUT><<<grid, 256, dyn, s>>>(a);
   return launch_status();
 }
 
@@ -538,7 +581,7 @@ int qmm_grouped_mxfp4(int tiled, int mode, int fused, int act, int64_t max_tiles
                       const int32_t *tile_info, const int32_t *rowmap, const void *x, const void *x_scales,
                       int64_t x_rows, const void *w, const void *ws, const void *w2, const void *ws2,
                       const float *bias, const float *bias2, float *y, uint8_t *y8, uint8_t *ys8, hipStream_t s) {
-  if (k % 64 || k > 12288) return QMM_ERR_SHAPE;   // the workgroup stages (64 + 256) x K / 32 scale bytes in LDS
+  if (k % 64 || k > kMaxK) return QMM_ERR_SHAPE;   // the workgroup stages (64 + 256) x K / 32 scale bytes in LDS
   if (tiled && n % 32) return QMM_ERR_SHAPE;       // tiled planes hold whole 32-row blocks
   if (x_rows * k >= (1ll << 31)) return QMM_ERR_SHAPE;   // activation rows are addressed by a 32-bit buffer offset
   if (!x_scales || !ws) return QMM_ERR_NULL;
@@ -572,6 +615,44 @@ int qmm_grouped_mxfp4(int tiled, int mode, int fused, int act, int64_t max_tiles
   a.nib_ebytes = nrow * n;
   a.sc_ebytes = srow * n;
   return tiled ? launch<kDN, kTiled>(a, s) : launch<kDN, kSplit>(a, s);
+}
+
+// The dense prefill GEMM on MXFP4 weights (split planes or MFMA-tiled planes): the grouped kernels over dense
+// 64-row tiles of x, one weight matrix (store / acc) or a gate and an up matrix (swiglu).
+extern "C" int qmm_gemm_mxfp4(int fmt, int mode, int64_t rows, int64_t k, int64_t n, const void *x,
+                              const void *x_scales, const void *w, const void *ws, const void *w2, const void *ws2,
+                              void *y, int y_dtype, qmm_stream_t stream) {
+  if (fmt != QMM_MXFP4S && fmt != QMM_MXFP4T) return QMM_ERR_FORMAT;
+  if (mode != QMM_GEMM_STORE && mode != QMM_GEMM_ACC && mode != QMM_GEMM_SWIGLU) return QMM_ERR_RANGE;
+  if (y_dtype != QMM_F32 && y_dtype != QMM_BF16) return QMM_ERR_DTYPE;
+  if (!x || !x_scales || !w || !ws || !y || (mode == QMM_GEMM_SWIGLU && (!w2 || !ws2))) return QMM_ERR_NULL;
+  if (rows <= 0 || k <= 0 || n <= 0 || k % 64 || k > kMaxK || rows > (1 << 24) || n > (1 << 24)) return QMM_ERR_SHAPE;
+  const bool tiled = fmt == QMM_MXFP4T;
+  if (tiled && n % 32) return QMM_ERR_SHAPE;        // tiled planes hold whole 32-row blocks
+  if (rows * k >= (1ll << 31)) return QMM_ERR_SHAPE;   // activation rows are addressed by a 32-bit buffer offset
+  if (!aligned(x, 16) || !aligned(x_scales, 2) || !aligned(w, 16) || (w2 && !aligned(w2, 16)) || !aligned(y, 4))
+    return QMM_ERR_ALIGN;
+  if (tiled && (!aligned(ws, 4) || (ws2 && !aligned(ws2, 4)))) return QMM_ERR_ALIGN;
+  MArgs a{};
+  a.N = (int)n; a.K = (int)k; a.M = (int)rows;
+  a.x8 = static_cast<const u8 *>(x); a.xs = static_cast<const u8 *>(x_scales); a.x_rows = (int)rows;
+  a.wn = static_cast<const u8 *>(w); a.wsc = static_cast<const u8 *>(ws);
+  a.wn2 = static_cast<const u8 *>(w2); a.wsc2 = static_cast<const u8 *>(ws2);
+  a.E = 1; a.KU = 1; a.act = QMM_ACT_SILU; a.y = static_cast<float *>(y);
+  a.n_blocks = (int)((n + 127) / 128);
+  a.max_tiles = (int)((rows + BM - 1) / BM);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool bf = y_dtype == QMM_BF16;
+  if (mode == QMM_GEMM_SWIGLU) {
+    if (bf) return tiled ? launch<kGU, kTiled, kOutBF16>(a, s) : launch<kGU, kSplit, kOutBF16>(a, s);
+    return tiled ? launch<kGU, kTiled, kOutF32>(a, s) : launch<kGU, kSplit, kOutF32>(a, s);
+  }
+  if (mode == QMM_GEMM_ACC) {
+    if (bf) return tiled ? launch<kDN, kTiled, kOutBF16Acc>(a, s) : launch<kDN, kSplit, kOutBF16Acc>(a, s);
+    return tiled ? launch<kDN, kTiled, kOutF32Acc>(a, s) : launch<kDN, kSplit, kOutF32Acc>(a, s);
+  }
+  if (bf) return tiled ? launch<kDN, kTiled, kOutBF16>(a, s) : launch<kDN, kSplit, kOutBF16>(a, s);
+  return tiled ? launch<kDN, kTiled, kOutF32>(a, s) : launch<kDN, kSplit, kOutF32>(a, s);
 }
 
 extern "C" int qmm_tile_mxfp4(const void *nibbles, const void *scales, int64_t rows, int64_t k, void *nib_t,

@@ -25,10 +25,15 @@ SIGNATURES = {
                           c_vp, c_vp, c_vp, c_vp, c_vp],
     "qmm_moe_expert_mv_split": [c_int, c_int, c_int, c_i64, c_i64, c_int, c_int, c_i64, c_vp, c_vp, c_int, c_vp,
                                 c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
-    "qmm_moe_grouped": [c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_int, c_vp,
-                        c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
-    "qmm_moe_grouped_mxfp8": [c_int, c_int, c_int, c_i64, c_i64, c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_vp,
-                              c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
+    "qmm_moe_grouped": [c_int, c_int, c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_int,
+                        c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
+    "qmm_moe_grouped_mxfp8": [c_int, c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp,
+                              c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
+    "qmm_gemm_mxfp4": [c_int, c_int, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_vp],
+    "qmm_mv_swiglu_q8": [c_int, c_i64, c_i64, c_i64, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_vp],
+    "qmm_mv_pair_q8": [c_int, c_i64, c_i64, c_i64, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp],
+    "qmm_moe_expert_mv_q8": [c_int, c_int, c_int, c_int, c_i64, c_i64, c_int, c_int, c_i64, c_vp, c_vp, c_vp, c_vp,
+                             c_vp, c_vp, c_vp, c_vp],
     "qmm_moe_route": [c_i64, c_i64, c_int, c_int, c_int, c_int, c_float, c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_vp,
                       c_vp, c_vp, c_vp],
     "qmm_moe_shared_gate": [c_i64, c_i64, c_vp, c_int, c_vp, c_int, c_vp, c_vp],

@@ -4,13 +4,18 @@ The functions mirror the reference's kernel families (paths relative to the refe
 S/ = skills/loom-port-llm/starter/):
 
     mv                g_mv_{fmt}_k{K}[_t{TG}][_r{R}]          S/gen_llm.py:1159-1378, launch args :1187-1197
+    mv_q8             g_mv_{fmt}_k{K}[_t{TG}]_q8[_r{R}]       S/gen_llm.py:1288-1301 (int8 activations)
+    mv_swiglu_q8      g_mv_{fmt}_k{K}_swiglu[_t{TG}]_q8       S/gen_llm.py:1159-1197
+    mv_pair_q8        g_mv_{fmt}_k{K}_pair[_t{TG}]_q8         S/gen_llm.py:1166-1176
     gemm              g_gemm_{fmt}_{store|acc|swiglu}[_m*]    S/gen_gemm.py:535-703, launch args :549-556
+    gemm_mxfp4        g_gemm_mxfp4s_{store|swiglu}_f8_m256    S/gen_mxfp4s.py:50-101
     moe_topk          g_moe_route / g_moe_route_tr            S/gen_moe.py:116-500
     moe_route         the same with the router matvec         S/gen_moe.py:116-500 (+ _live, :474-500)
     moe_shared_gate   g_moe_shared_gate                       S/gen_moe.py:780-823
     moe_wscale        g_moe_wscale                            S/gen_moe.py:1010-1045
     moe_bucket        g_moe_bucket                            S/gen_moe.py:829-955
     moe_expert_mv     g_moe_gu_* / g_moe_dn_*                 S/gen_moe.py:535-727
+    moe_expert_mv_q8  g_moe_gu_*_q8_* / g_moe_dn_*_q8_*       S/gen_moe.py:535-727 (MOE_Q8, S/gen_llm.py:5290-5303)
     moe_grouped       g_moe_ggu_* / g_moe_gdn_*               S/gen_moe.py:1126-1228
     moe_combine       g_moe_combine[_sorted] [shared_gated]   S/gen_moe.py:730-779, :1231-1280
     moe_prefill       the prefill chain of moe_routed          S/gen_llm.py:5324-5385 (t >= 64)
@@ -60,6 +65,23 @@ def _dev(*ts):
             raise ValueError("qmm ops take contiguous tensors")
 
 
+def _out(y, shape, dtype, dev, accumulate=False):
+    """The output tensor: a new one, or y checked against the shape and dtype the kernel writes (the C ABI cannot see
+    sizes, so a wrong y would be written out of bounds). Accumulating needs the caller's y."""
+    if y is None:
+        if accumulate:
+            raise ValueError("accumulating into y needs y")
+        return torch.empty(shape, dtype=dtype, device=dev)
+    if tuple(y.shape) != tuple(shape) or y.dtype != dtype:
+        raise ValueError(f"y is {tuple(y.shape)} {y.dtype}, the kernel writes {tuple(shape)} {dtype}")
+    return y
+
+
+def _cols(x, k, what="x"):
+    if x.shape[-1] != k:
+        raise ValueError(f"{what} has {x.shape[-1]} columns, K is {k}")
+
+
 def dequant(fmt, w, rows, k, ws=None, out=None):
     """f32 [rows, k] values of the weight bytes, bit-exact to the reference's value helpers."""
     _dev(w, ws)
@@ -72,9 +94,8 @@ def mv(fmt, w, x, n, k, y=None, accumulate=False, ws=None):
     """y[t, r] (+)= sum_k x[t, k] W[r, k]; x f32 or bf16 [tokens, k]; returns y f32 [tokens, n]."""
     _dev(w, x, y, ws)
     tokens = x.shape[0]
-    if x.shape[-1] != k:
-        raise ValueError(f"x has {x.shape[-1]} columns, K is {k}")
-    y = torch.empty((tokens, n), dtype=torch.float32, device=x.device) if y is None else y
+    _cols(x, k)
+    y = _out(y, (tokens, n), torch.float32, x.device, accumulate)
     _lib.call("qmm_mv", CODE[fmt], k, n, tokens, int(bool(accumulate)), _ptr(x), _dt(x), _ptr(w), _ptr(ws),
               _ptr(y), _stream())
     return y
@@ -84,7 +105,8 @@ def mv_swiglu(fmt, w, w2, x, n, k, y=None, accumulate=False):
     """y[t, r] (+)= silu(x W^T) * (x W2^T) (g_mv_{fmt}_k{K}_swiglu); x f32 or bf16 [tokens, k]; y f32 [tokens, n]."""
     _dev(w, w2, x, y)
     tokens = x.shape[0]
-    y = torch.empty((tokens, n), dtype=torch.float32, device=x.device) if y is None else y
+    _cols(x, k)
+    y = _out(y, (tokens, n), torch.float32, x.device, accumulate)
     _lib.call("qmm_mv_swiglu", CODE[fmt], k, n, tokens, int(bool(accumulate)), _ptr(x), _dt(x), _ptr(w), _ptr(w2),
               _ptr(y), _stream())
     return y
@@ -111,40 +133,101 @@ def mv_q8(fmt, w, x, n, k, tokens=None, y=None, accumulate=False):
     and (up to two tokens) tiled-layout q4_kt kernels quantize themselves and any other call quantizes through
     quant_q8 first (identical results)."""
     _dev(w, x, y)
-    if x.dtype == torch.uint8:
-        if tokens is None:
-            raise ValueError("a planar Q8_1 buffer needs its token count")
-        xd = DTYPE["q8"]
-    else:
-        tokens = x.shape[0]
-        if x.shape[-1] != k:
-            raise ValueError(f"x has {x.shape[-1]} columns, K is {k}")
-        # the kernels that quantize f32 / bf16 rows themselves do so in every workgroup; from three tokens on a
-        # separate quant_q8 pass is cheaper for the tiled layout (same bits either way)
-        if not ((fmt == "q4_k" and k in (4096, 8192)) or (fmt == "q4_kt" and tokens <= 2)):
-            x, xd = quant_q8(x), DTYPE["q8"]
-        else:
-            xd = _dt(x)
-    y = torch.empty((tokens, n), dtype=torch.float32, device=w.device) if y is None else y
+    x, xd, tokens = _q8_input(fmt, x, k, tokens, staged_tokens=2)
+    y = _out(y, (tokens, n), torch.float32, w.device, accumulate)
     _lib.call("qmm_mv_q8", CODE[fmt], k, n, tokens, int(bool(accumulate)), _ptr(x), xd, _ptr(w), _ptr(y), _stream())
     return y
 
 
-def gemm(fmt, mode, x, w, n, k, w2=None, scales=None, out_dtype=torch.float32, y=None):
+def _q8_input(fmt, x, k, tokens, staged_tokens):
+    """(x, its dtype code, tokens) for an int8 matvec: a planar Q8_1 buffer as it is (uint8, `tokens` rows), or f32 /
+    bf16 rows, which the Q4_K K = 4096 / 8192 and (up to `staged_tokens` tokens) tiled-layout kernels quantize
+    themselves and every other call quantizes through quant_q8 first (identical results)."""
+    if x.dtype == torch.uint8:
+        if tokens is None:
+            raise ValueError("a planar Q8_1 buffer needs its token count")
+        if x.numel() < q8_bytes(tokens, k):
+            raise ValueError(f"the planar Q8_1 buffer holds {x.numel()} bytes, {tokens} rows of K {k} need "
+                             f"{q8_bytes(tokens, k)}")
+        return x, DTYPE["q8"], tokens
+    tokens = x.shape[0]
+    _cols(x, k)
+    # the kernels that quantize f32 / bf16 rows themselves do so in every workgroup; from three tokens on a separate
+    # quant_q8 pass is cheaper for the tiled layout (same bits either way)
+    if (fmt == "q4_k" and k in (4096, 8192) and staged_tokens >= 2) or (fmt == "q4_kt" and tokens <= staged_tokens):
+        return x, _dt(x), tokens
+    return quant_q8(x), DTYPE["q8"], tokens
+
+
+def mv_swiglu_q8(fmt, w, w2, x, n, k, tokens=None, y=None, accumulate=False):
+    """The int8 swiglu matvec y (+)= silu(x W^T) (x W2^T) (g_mv_{fmt}_k{K}_swiglu[_t{TG}]_q8): gate W and up W2
+    [n, k]; x a planar Q8_1 buffer (with tokens) or f32 / bf16 rows (quantized as quant_q8 does). fmt q4_kt (tiled
+    layout) or GGUF q4_k / q4_0 / q6_k. Returns y f32 [tokens, n]."""
+    _dev(w, w2, x, y)
+    x, xd, tokens = _q8_input(fmt, x, k, tokens, staged_tokens=2 if fmt == "q4_kt" else 0)
+    y = _out(y, (tokens, n), torch.float32, w.device, accumulate)
+    _lib.call("qmm_mv_swiglu_q8", CODE[fmt], k, n, tokens, int(bool(accumulate)), _ptr(x), xd, _ptr(w), _ptr(w2),
+              _ptr(y), _stream())
+    return y
+
+
+def mv_pair_q8(fmt, w, w2, x, n, k, tokens=None, y=None, y2=None, accumulate=False):
+    """Two int8 matvecs of one input in one launch (g_mv_{fmt}_k{K}_pair[_t{TG}]_q8): y (+)= x W^T, y2 (+)= x W2^T,
+    each equal bit for bit to the one-matrix kernel's of the same layout. Returns (y, y2) f32 [tokens, n]."""
+    _dev(w, w2, x, y, y2)
+    x, xd, tokens = _q8_input(fmt, x, k, tokens, staged_tokens=2 if fmt == "q4_kt" else 0)
+    y = _out(y, (tokens, n), torch.float32, w.device, accumulate)
+    y2 = _out(y2, (tokens, n), torch.float32, w.device, accumulate)
+    _lib.call("qmm_mv_pair_q8", CODE[fmt], k, n, tokens, int(bool(accumulate)), _ptr(x), xd, _ptr(w), _ptr(w2),
+              _ptr(y), _ptr(y2), _stream())
+    return y, y2
+
+
+def gemm(fmt, mode, x, w, n, k, w2=None, scales=None, out_dtype=torch.float32, y=None, ws=None, ws2=None):
     """Y = (X16 W^T) inv (store), Y += ... (acc) or Y = silu(X16 W^T inv) (X16 W2^T inv) (swiglu, w2 the up matrix).
-    x is the row-scaled f16 operand with its scales (the reference's g_row_scale_f16 output), or bf16 / f32 rows,
-    which are row-scaled here first (qmm_row_scale_f16). With scales, 64-row tiles whose rows all have scale 0
-    (padding rows of row_scale_f16(x, info=...)) are skipped and their y rows are not written."""
+    GGUF q4_k / q6_k / q4_0: x is the row-scaled f16 operand with its scales (the reference's g_row_scale_f16
+    output), or bf16 / f32 rows, which are row-scaled here first (qmm_row_scale_f16). With scales, 64-row tiles whose
+    rows all have scale 0 (padding rows of row_scale_f16(x, info=...)) are skipped and their y rows are not written.
+    mxfp4s / mxfp4t (ws / ws2 the weights' scale planes): see gemm_mxfp4; x is E4M3 codes with their E8M0 scales, or
+    bf16 / f32 rows, quantized to MXFP8 here first."""
+    if fmt in SPLIT or fmt == "mxfp4t":
+        return gemm_mxfp4(fmt, mode, x, w, ws, n, k, w2=w2, ws2=ws2, x_scales=scales, out_dtype=out_dtype, y=y)
     _dev(x, w, w2, scales, y)
+    if mode == "swiglu" and w2 is None:
+        raise ValueError("swiglu needs the up matrix w2")
     rows = x.shape[0]
+    _cols(x, k)
     if x.dtype != torch.float16:
         if scales is not None:
             raise ValueError("scales come with an f16 operand; pass bf16 / f32 rows without them")
         x, scales = row_scale_f16(x)
-    if y is None:
-        y = torch.empty((rows, n), dtype=out_dtype, device=x.device)
+    elif scales is not None and tuple(scales.shape) != (rows, 2):
+        raise ValueError(f"scales are {tuple(scales.shape)}, the operand has {rows} rows")
+    y = _out(y, (rows, n), out_dtype if y is None else y.dtype, x.device, mode == "acc")
     _lib.call("qmm_gemm", CODE[fmt], GEMM_MODE[mode], rows, k, n, _ptr(x), _dt(x), _ptr(scales), _ptr(w), _ptr(w2),
               _ptr(y), _dt(y), _stream())
+    return y
+
+
+def gemm_mxfp4(fmt, mode, x, w, ws, n, k, w2=None, ws2=None, x_scales=None, out_dtype=torch.float32, y=None):
+    """The MXFP4 prefill GEMM on the scaled MFMA (g_gemm_mxfp4s_{store|swiglu}_f8_m256): store Y = X8 W^T, acc
+    Y += X8 W^T, swiglu Y = silu(X8 W^T) (X8 W2^T). x: E4M3 codes u8 [rows, k] with x_scales u8 [rows, k/32]
+    (quant_mxfp8), or f32 / bf16 rows quantized here first. w / ws: split planes (mxfp4s) or MFMA-tiled planes
+    (mxfp4t) of [n, k]. y: [rows, n] f32 or bf16."""
+    _dev(x, w, ws, w2, ws2, x_scales, y)
+    if mode == "swiglu" and (w2 is None or ws2 is None):
+        raise ValueError("swiglu needs the up matrix w2 and its scales ws2")
+    rows = x.shape[0]
+    _cols(x, k)
+    if x.dtype != torch.uint8:
+        if x_scales is not None:
+            raise ValueError("x_scales come with E4M3 codes; pass bf16 / f32 rows without them")
+        x, x_scales = quant_mxfp8(x)
+    elif x_scales is None or tuple(x_scales.shape) != (rows, k // MX_BLOCK):
+        raise ValueError("E4M3 codes need their E8M0 scales [rows, k/32]")
+    y = _out(y, (rows, n), out_dtype if y is None else y.dtype, x.device, mode == "acc")
+    _lib.call("qmm_gemm_mxfp4", CODE[fmt], GEMM_MODE[mode], rows, k, n, _ptr(x), _ptr(x_scales), _ptr(w), _ptr(ws),
+              _ptr(w2), _ptr(ws2), _ptr(y), _dt(y), _stream())
     return y
 
 
@@ -216,7 +299,8 @@ def moe_expert_mv(fmt, mode, ids, x, w, n, k, E, KU, w2=None, ws=None, ws2=None,
     if fmt == "mxfp4t":
         raise ValueError("the decode expert matvecs read split planes (mxfp4s); mxfp4t is the grouped GEMM's layout")
     A = ids.numel()
-    y = torch.empty((A, n), dtype=torch.float32, device=x.device) if y is None else y
+    _cols(x, k)
+    y = _out(y, (A, n), torch.float32, x.device)
     m = {"gu": 0, "dn": 1}[mode]
     if fmt in SPLIT:
         _lib.call("qmm_moe_expert_mv_split", m, int(fused), ACT[act], k, n, E, KU, A, _ptr(ids), _ptr(x), _dt(x),
@@ -227,18 +311,41 @@ def moe_expert_mv(fmt, mode, ids, x, w, n, k, E, KU, w2=None, ws=None, ws2=None,
     return y
 
 
+def moe_expert_mv_q8(fmt, mode, ids, x, w, n, k, E, KU, w2=None, fused=False, act="silu", bias=None, bias2=None,
+                     y=None, x_rows=None):
+    """Decode expert matvecs on Q8_1 activations (g_moe_gu_{fmt}[_fused]_q8_k{H}_r{R} / g_moe_dn_{fmt}_q8_k{FE}_r{R}):
+    x is the planar Q8_1 buffer of x_rows rows (gu: the tokens, dn: the assignments), or f32 / bf16 rows quantized
+    here first (quant_q8). fmt q4_k / q4_0 / q6_k. Returns y f32 [assignments, n]."""
+    _dev(ids, x, w, w2, bias, bias2, y)
+    A = ids.numel()
+    rows = A // KU if mode == "gu" else A
+    if x.dtype != torch.uint8:
+        _cols(x, k)
+        if x.shape[0] != rows:
+            raise ValueError(f"x has {x.shape[0]} rows, the {mode} matvec reads {rows}")
+        x = quant_q8(x)
+    elif x.numel() < q8_bytes(rows, k):
+        raise ValueError(f"the planar Q8_1 buffer holds {x.numel()} bytes, {rows} rows of K {k} need "
+                         f"{q8_bytes(rows, k)}")
+    y = _out(y, (A, n), torch.float32, x.device)
+    _lib.call("qmm_moe_expert_mv_q8", CODE[fmt], {"gu": 0, "dn": 1}[mode], int(fused), ACT[act], k, n, E, KU, A,
+              _ptr(ids), _ptr(x), _ptr(w), _ptr(w2), _ptr(bias), _ptr(bias2), _ptr(y), _stream())
+    return y
+
+
 def moe_grouped(fmt, mode, tile_info, rowmap, x, w, n, k, E, KU, w2=None, ws=None, ws2=None, x_scales=None,
                 fused=False, act="silu", y=None, bias=None, bias2=None):
     """Grouped expert GEMM over bucketed 64-row tiles (include/qmm.h, qmm_moe_grouped).
-    q4_k: x f16 row-scaled rows with x_scales f32 [rows, 2] (row_scale_f16); mxfp4s: x E4M3 codes uint8 [rows, k]
-    with x_scales uint8 [rows, k/64] (quant_mxfp8). y: f32 [max_tiles * 64, n]. bias / bias2: per-expert output
-    biases f32 [E, n] (gu: gate and up; dn: bias)."""
+    q4_k / q6_k / q4_0: x f16 row-scaled rows with x_scales f32 [rows, 2] (row_scale_f16); mxfp4s / mxfp4t: x E4M3
+    codes uint8 [rows, k] with x_scales uint8 [rows, k/32] (quant_mxfp8). y: f32 [max_tiles * 64, n]. bias / bias2:
+    per-expert output biases f32 [E, n] (gu: gate and up; dn: bias)."""
     _dev(tile_info, rowmap, x, w, w2, ws, ws2, x_scales, y, bias, bias2)
-    n_tiles = tile_info.shape[0]
-    y = torch.empty((n_tiles * TILE, n), dtype=torch.float32, device=x.device) if y is None else y
+    _cols(x, k)
+    max_rows = tile_info.shape[0] * TILE
+    y = _out(y, (max_rows, n), torch.float32, x.device)
     xd = DTYPE["mxfp8"] if x.dtype == torch.uint8 else _dt(x)
-    _lib.call("qmm_moe_grouped", CODE[fmt], {"gu": 0, "dn": 1}[mode], int(fused), ACT[act], n_tiles, k, n, E, KU,
-              _ptr(tile_info), _ptr(rowmap), _ptr(x), xd, _ptr(x_scales), x.shape[0], _ptr(w), _ptr(ws), _ptr(w2),
+    _lib.call("qmm_moe_grouped", CODE[fmt], {"gu": 0, "dn": 1}[mode], int(fused), ACT[act], E, KU, max_rows, k, n,
+              x.shape[0], _ptr(tile_info), _ptr(rowmap), _ptr(x), xd, _ptr(x_scales), _ptr(w), _ptr(ws), _ptr(w2),
               _ptr(ws2), _ptr(bias), _ptr(bias2), _ptr(y), _stream())
     return y
 
@@ -249,12 +356,13 @@ def moe_grouped_mxfp8(fmt, tile_info, rowmap, x, w, n, k, E, KU, w2=None, ws=Non
     [max_tiles*64, n], scales u8 [max_tiles*64, n/32]) == quant_mxfp8(moe_grouped(fmt, "gu", ...), tile_info) bit
     for bit. x: E4M3 codes with x_scales (quant_mxfp8)."""
     _dev(tile_info, rowmap, x, w, w2, ws, ws2, x_scales, codes, scales, bias, bias2)
+    _cols(x, k)
     rows = tile_info.shape[0] * TILE
-    codes = torch.empty((rows, n), dtype=torch.uint8, device=x.device) if codes is None else codes
-    scales = torch.empty((rows, n // MX_BLOCK), dtype=torch.uint8, device=x.device) if scales is None else scales
-    _lib.call("qmm_moe_grouped_mxfp8", CODE[fmt], int(fused), ACT[act], tile_info.shape[0], k, n, E, KU,
-              _ptr(tile_info), _ptr(rowmap), _ptr(x), _ptr(x_scales), x.shape[0], _ptr(w), _ptr(ws), _ptr(w2),
-              _ptr(ws2), _ptr(bias), _ptr(bias2), _ptr(codes), _ptr(scales), _stream())
+    codes = _out(codes, (rows, n), torch.uint8, x.device)
+    scales = _out(scales, (rows, n // MX_BLOCK), torch.uint8, x.device)
+    _lib.call("qmm_moe_grouped_mxfp8", CODE[fmt], int(fused), ACT[act], E, KU, rows, k, n, x.shape[0],
+              _ptr(tile_info), _ptr(rowmap), _ptr(x), _ptr(x_scales), _ptr(w), _ptr(ws), _ptr(w2), _ptr(ws2),
+              _ptr(bias), _ptr(bias2), _ptr(codes), _ptr(scales), _stream())
     return codes, scales
 
 
@@ -364,10 +472,15 @@ def moe_prefill(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up
     shared experts' output the routed output is added to (scaled first by sg, the shared gate, when given);
     fmt_down: the down tensor's format when it differs (q4_k gate / up with q6_k down, the Q4_K_M expert layout).
     Returns (y f32 [T, H], intermediates dict)."""
+    if fmt == "mxfp4":   # GGUF blocks: split planes for the scaled MFMA (one-time weight preparation, done per call)
+        fmt, (w_gate, ws_gate), (w_down, ws_down) = "mxfp4s", repack_mxfp4(w_gate, E * FE * (2 if fused else 1), H), \
+            repack_mxfp4(w_down, E * H, FE)
+        if w_up is not None:
+            w_up, ws_up = repack_mxfp4(w_up, E * FE, H)
     ids, wts, logits = _route(x, logits, KU, gating, norm, scale, bias, router, down_scale)
     bg, bu, bd = expert_bias if expert_bias is not None else (None, None, None)
     tile_info, rowmap, pos = moe_bucket(ids, E)
-    if fmt in ("q4_k", "q6_k"):
+    if fmt in ("q4_k", "q6_k", "q4_0"):
         x16, xs = row_scale_f16(x)
         a = moe_grouped(fmt, "gu", tile_info, rowmap, x16, w_gate, FE, H, E, KU, w2=w_up, x_scales=xs,
                         fused=fused, act=act, bias=bg, bias2=bu)
@@ -390,15 +503,34 @@ def moe_prefill(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up
     return y, mid
 
 
+Q8_FORMATS = ("q4_0", "q4_k", "q6_k")   # formats with integer-code expert matvecs (gen_llm ICODES)
+
+
 def moe_decode(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=None, ws_gate=None, ws_down=None,
                ws_up=None, fused=False, act="silu", scale=1.0, bias=None, router=None, expert_bias=None,
-               down_scale=None, y=None, sg=None, fmt_down=None):
+               down_scale=None, y=None, sg=None, fmt_down=None, q8=False):
     """The reference's decode MoE chain (moe_routed with t < 64): route, per-assignment expert matvecs
     (g_moe_gu_* then g_moe_dn_*), combine in assignment order. Arguments as moe_prefill; fmt_down: the down
     tensor's format when it differs (Q4_K_M files: Q4_K gate / up, Q6_K down, S/gen_llm.py:5336-5340).
+    q8: the int8-activation chain (the reference's MOE_Q8 default, S/gen_llm.py:5290-5303, :5381-5383): x is
+    quantized to Q8_1 once, the gate/up matvecs contract integer codes, their output is quantized again (g_quant_q8)
+    for the down matvecs; formats q4_0 / q4_k / q6_k. "auto" takes it where the reference does: both formats have
+    integer codes and the experts have no biases (gen_llm.moe_iq).
     Returns (y f32 [T, H], intermediates dict)."""
+    fd = fmt_down or fmt
+    if q8 == "auto":
+        q8 = fmt in Q8_FORMATS and fd in Q8_FORMATS and expert_bias is None
+    if q8 and (fmt not in Q8_FORMATS or fd not in Q8_FORMATS):
+        raise ValueError(f"the int8 expert matvecs take {Q8_FORMATS} (gate/up {fmt}, down {fd})")
     ids, wts, logits = _route(x, logits, KU, gating, norm, scale, bias, router, down_scale)
     bg, bu, bd = expert_bias if expert_bias is not None else (None, None, None)
+    if q8:
+        xq = quant_q8(x)
+        a = moe_expert_mv_q8(fmt, "gu", ids, xq, w_gate, FE, H, E, KU, w2=w_up, fused=fused, act=act, bias=bg,
+                             bias2=bu)
+        ys = moe_expert_mv_q8(fd, "dn", ids, quant_q8(a), w_down, H, FE, E, KU, bias=bd)
+        y = moe_combine(ys, wts, y=y, accumulate=y is not None, sg=sg)
+        return y, {"ids": ids, "wts": wts, "logits": logits, "act": a, "ys": ys}
     a = moe_expert_mv(fmt, "gu", ids, x, w_gate, FE, H, E, KU, w2=w_up, ws=ws_gate, ws2=ws_up, fused=fused, act=act,
                       bias=bg, bias2=bu)
     ys = moe_expert_mv(fmt_down or fmt, "dn", ids, a, w_down, H, FE, E, KU, ws=ws_down, bias=bd)
@@ -410,16 +542,22 @@ def moe_decode(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=
 GEMM_MIN_TOKENS = 64   # %gemm: epochs of 64+ tokens take the GEMM / grouped chain (S/gen_llm.py:6107-6126)
 
 
-def linear(fmt, x, w, n, k, y=None, mode="store", ws=None, w2=None):
+def linear(fmt, x, w, n, k, y=None, mode="store", ws=None, w2=None, ws2=None):
     """Projection y (+)= x W^T, or swiglu y = silu(x W^T) (x W2^T), with the reference's per-epoch choice (linear,
-    S/gen_llm.py:4568-4625): the prefill GEMM for 64+ tokens (Q4_K, Q6_K; the activation is row-scaled to f16 first), else
-    the decode GEMV. y is f32."""
+    S/gen_llm.py:4568-4625): the prefill GEMM for 64+ tokens (GGUF q4_k / q6_k / q4_0 on the f16 MFMA, the activation
+    row-scaled to f16 first; MXFP4 on the scaled MFMA, the activation quantized to MXFP8 first -- GGUF mxfp4 blocks
+    are repacked to split planes for it), else the decode GEMV. y is f32."""
     if mode not in ("store", "acc", "swiglu"):
         raise ValueError(f"linear mode {mode}")
     if mode == "swiglu" and w2 is None:
         raise ValueError("swiglu needs the up matrix w2")
-    if x.shape[0] >= GEMM_MIN_TOKENS and fmt in ("q4_k", "q6_k"):
-        return gemm(fmt, mode, x, w, n, k, w2=w2, y=y)
+    if x.shape[0] >= GEMM_MIN_TOKENS:
+        if fmt == "mxfp4":   # GGUF blocks -> split planes (a one-time weight preparation a model does at load)
+            (w, ws), (w2, ws2) = repack_mxfp4(w, n, k), (repack_mxfp4(w2, n, k) if w2 is not None else (None, None))
+            fmt = "mxfp4s"
+        if fmt in ("q4_k", "q6_k", "q4_0", "mxfp4s", "mxfp4t"):
+            return gemm(fmt, mode, x, w, n, k, w2=w2, y=y, ws=ws, ws2=ws2)
+        raise ValueError(f"no prefill GEMM reads {fmt} weights")
     if mode == "swiglu":
         return mv_swiglu(fmt, w, w2, x, n, k, y=y)
     return mv(fmt, w, x, n, k, y=y, accumulate=mode == "acc", ws=ws)
@@ -429,8 +567,10 @@ def moe_routed(fmt, x, logits, E, KU, H, FE, gating, norm, **kw):
     """The routed experts of one MoE layer (moe_routed, S/gen_llm.py:5324-5385): the grouped prefill chain for 64+
     tokens, the per-assignment decode chain below. Returns (y f32 [T, H], intermediates dict)."""
     chain = moe_prefill if x.shape[0] >= GEMM_MIN_TOKENS else moe_decode
-    if chain is moe_decode and fmt == "mxfp4s" and "w_gate" in kw and kw.get("ws_gate") is None:
+    if fmt == "mxfp4s" and "w_gate" in kw and kw.get("ws_gate") is None:
         raise ValueError("mxfp4s weights need their scale planes")
+    if chain is moe_prefill:
+        kw.pop("q8", None)   # the prefill chain's activations are the GEMMs' (f16 rows, MXFP8)
     return chain(fmt, x, logits, E, KU, H, FE, gating, norm, **kw)
 
 

@@ -102,34 +102,58 @@ def normal_f32(rng, shape):
     return rng.standard_normal(shape).astype(np.float32)
 
 
-def workload(index, **kw):
-    """Inputs of one workload as host numpy arrays (see the module docstring)."""
-    rng = rng_for(index)
+def _weights(index, rng, kw):
+    """The weights (and shape fields) of workload `index`, drawn first from its generator."""
     if index == 0:
         n, k = kw.get("n", 4096), kw.get("k", 4096)
-        w = q4_0_weights(rng, n, k)
-        return {"fmt": "q4_0", "n": n, "k": k, "w": w, "x": normal_f32(rng, (kw.get("m", 1), k))}
+        return {"fmt": "q4_0", "n": n, "k": k, "w": q4_0_weights(rng, n, k)}
     if index in (1, 2):
         n, k = (12288, 4096) if index == 1 else (4096, 4096)
         n, k = kw.get("n", n), kw.get("k", k)
-        m = kw.get("m", 1 if index == 1 else 512)
-        w = q4_k_weights(rng, n, k)
-        return {"fmt": "q4_k", "n": n, "k": k, "w": w, "x_bf16": to_bf16_bits(normal_f32(rng, (m, k)))}
+        return {"fmt": "q4_k", "n": n, "k": k, "w": q4_k_weights(rng, n, k)}
     if index == 3:
-        E, KU, H, FE, T = kw.get("E", 32), kw.get("KU", 4), kw.get("H", 2880), kw.get("FE", 2880), kw.get("T", 256)
+        E, KU, H, FE = kw.get("E", 32), kw.get("KU", 4), kw.get("H", 2880), kw.get("FE", 2880)
         gate_up = mxfp4_weights(rng, E * 2 * FE, H)
         down = mxfp4_weights(rng, E * H, FE)
-        x = to_bf16_bits(normal_f32(rng, (T, H)))
-        logits = normal_f32(rng, (T, E))
-        return {"fmt": "mxfp4", "E": E, "KU": KU, "H": H, "FE": FE, "T": T, "gate_up": gate_up, "down": down,
-                "x_bf16": x, "logits": logits, "gating": 3, "norm": False, "act": "swiglu_oai", "fused": True}
+        return {"fmt": "mxfp4", "E": E, "KU": KU, "H": H, "FE": FE, "gate_up": gate_up, "down": down, "gating": 3,
+                "norm": False, "act": "swiglu_oai", "fused": True}
     if index == 4:
-        E, KU, H, FE, T = kw.get("E", 128), kw.get("KU", 8), kw.get("H", 2048), kw.get("FE", 768), kw.get("T", 64)
+        E, KU, H, FE = kw.get("E", 128), kw.get("KU", 8), kw.get("H", 2048), kw.get("FE", 768)
         gate = q4_k_weights(rng, E * FE, H)
         up = q4_k_weights(rng, E * FE, H)
         down = q4_k_weights(rng, E * H, FE)
-        x = to_bf16_bits(normal_f32(rng, (T, H)))
-        logits = normal_f32(rng, (T, E))
-        return {"fmt": "q4_k", "E": E, "KU": KU, "H": H, "FE": FE, "T": T, "gate": gate, "up": up, "down": down,
-                "x_bf16": x, "logits": logits, "gating": 1, "norm": True, "act": "silu", "fused": False}
+        return {"fmt": "q4_k", "E": E, "KU": KU, "H": H, "FE": FE, "gate": gate, "up": up, "down": down,
+                "gating": 1, "norm": True, "act": "silu", "fused": False}
     raise ValueError(index)
+
+
+def _inputs(index, rng, w, kw):
+    """The activations (and router logits) of workload `index`, drawn after its weights."""
+    if index == 0:
+        return {"x": normal_f32(rng, (kw.get("m", 1), w["k"]))}
+    if index in (1, 2):
+        m = kw.get("m", 1 if index == 1 else 512)
+        return {"x_bf16": to_bf16_bits(normal_f32(rng, (m, w["k"])))}
+    T = kw.get("T", 256 if index == 3 else 64)
+    x = to_bf16_bits(normal_f32(rng, (T, w["H"])))
+    return {"T": T, "x_bf16": x, "logits": normal_f32(rng, (T, w["E"]))}
+
+
+def workload(index, cache=None, **kw):
+    """Inputs of one workload as host numpy arrays (see the module docstring). cache: a dict owned by the caller that
+    keeps the weights of a workload (keyed by index and shape) with the generator's state after drawing them, so a
+    second call with another token count (m / T) reuses them and draws the same inputs as a fresh call would."""
+    shape = tuple(sorted((k, v) for k, v in kw.items() if k not in ("m", "T")))
+    key = (index, shape)
+    if cache is not None and key in cache:
+        w, state = cache[key]
+        rng = np.random.default_rng()
+        rng.bit_generator.state = state
+    else:
+        rng = rng_for(index)
+        w = _weights(index, rng, kw)
+        if cache is not None:
+            cache[key] = (w, rng.bit_generator.state)
+    d = dict(w)
+    d.update(_inputs(index, rng, w, kw))
+    return d

@@ -127,17 +127,49 @@ def test_argument_validation_without_a_device(lib):
     assert lib.qmm_tile_mxfp4(fake, n, 32, 64, fake, fake, n) == st["QMM_ERR_NULL"]
     assert lib.qmm_dequant(4, fake, fake, 48, 64, fake, n) == st["QMM_ERR_SHAPE"]
     assert lib.qmm_mv(4, 64, 4, 1, 0, fake, 0, fake, fake, fake, n) == st["QMM_ERR_FORMAT"]
-    assert lib.qmm_moe_grouped(4, 0, 1, 0, 4, 128, 48, 4, 2, fake, fake, fake, 3, fake, 8, fake, fake, n, n,
+    # grouped GEMMs, the reference's launch order (max_rows, k, n, xrows, ...) after the name fields (fmt, mode,
+    # fused, act, E, KU)
+    assert lib.qmm_moe_grouped(4, 0, 1, 0, 4, 2, 256, 128, 48, 8, fake, fake, fake, 3, fake, fake, fake, n, n,
                                n, n, fake, n) == st["QMM_ERR_SHAPE"]          # n % 32 != 0
-    assert lib.qmm_moe_grouped(4, 0, 1, 0, 4, 128, 64, 4, 2, fake, fake, fake, 3, fake, 8, fake, fake, n, n,
+    assert lib.qmm_moe_grouped(4, 0, 1, 0, 4, 2, 256, 128, 64, 8, fake, fake, fake, 3, fake, fake, fake, n, n,
                                odd, n, fake, n) == st["QMM_ERR_ALIGN"]         # biases are f32
+    assert lib.qmm_moe_grouped(4, 0, 1, 0, 4, 2, 250, 128, 64, 8, fake, fake, fake, 3, fake, fake, fake, n, n,
+                               n, n, fake, n) == st["QMM_ERR_SHAPE"]          # max_rows: whole 64-row tiles
+    assert lib.qmm_moe_grouped(0, 1, 0, 0, 4, 2, 256, 128, 64, 256, fake, fake, fake, 1, fake, fake, n, n, n,
+                               n, n, fake, n) == st["QMM_ERR_SHAPE"]          # Q4_0 experts: K % 256
+    assert lib.qmm_moe_grouped(0, 1, 0, 0, 4, 2, 256, 256, 64, 128, fake, fake, fake, 1, fake, fake, n, n, n,
+                               n, n, fake, n) == st["QMM_ERR_SHAPE"]          # down: xrows >= max_rows
     # the gate/up GEMM with MXFP8 output: MXFP4 weights only, whole 32-column blocks, both outputs
-    assert lib.qmm_moe_grouped_mxfp8(1, 1, 0, 4, 256, 64, 4, 2, fake, fake, fake, fake, 8, fake, n, n, n, n, n,
+    assert lib.qmm_moe_grouped_mxfp8(1, 1, 0, 4, 2, 256, 256, 64, 8, fake, fake, fake, fake, fake, n, n, n, n, n,
                                      fake, fake, n) == st["QMM_ERR_FORMAT"]
-    assert lib.qmm_moe_grouped_mxfp8(4, 1, 0, 4, 128, 48, 4, 2, fake, fake, fake, fake, 8, fake, fake, n, n, n, n,
+    assert lib.qmm_moe_grouped_mxfp8(4, 1, 0, 4, 2, 256, 128, 48, 8, fake, fake, fake, fake, fake, fake, n, n, n, n,
                                      fake, fake, n) == st["QMM_ERR_SHAPE"]
-    assert lib.qmm_moe_grouped_mxfp8(4, 1, 0, 4, 128, 64, 4, 2, fake, fake, fake, fake, 8, fake, fake, n, n, n, n,
+    assert lib.qmm_moe_grouped_mxfp8(4, 1, 0, 4, 2, 256, 128, 64, 8, fake, fake, fake, fake, fake, fake, n, n, n, n,
                                      fake, n, n) == st["QMM_ERR_NULL"]
+    # the MXFP4 dense GEMM: split / tiled planes only, K % 64, the weights' scale planes, whole 32-row tiled blocks
+    assert lib.qmm_gemm_mxfp4(2, 0, 64, 256, 64, fake, fake, fake, fake, n, n, fake, 0, n) == st["QMM_ERR_FORMAT"]
+    assert lib.qmm_gemm_mxfp4(3, 0, 64, 96, 64, fake, fake, fake, fake, n, n, fake, 0, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_gemm_mxfp4(3, 0, 64, 256, 64, fake, fake, fake, n, n, n, fake, 0, n) == st["QMM_ERR_NULL"]
+    assert lib.qmm_gemm_mxfp4(3, 2, 64, 256, 64, fake, fake, fake, fake, fake, n, fake, 0, n) == st["QMM_ERR_NULL"]
+    assert lib.qmm_gemm_mxfp4(4, 0, 64, 256, 48, fake, fake, fake, fake, n, n, fake, 0, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_gemm_mxfp4(3, 0, 64, 256, 64, fake, fake, fake, fake, n, n, fake, 1, n) == st["QMM_ERR_DTYPE"]
+    # int8 two-matrix matvecs and expert matvecs
+    assert lib.qmm_mv_swiglu_q8(2, 256, 16, 1, 0, fake, 4, fake, fake, fake, n) == st["QMM_ERR_FORMAT"]
+    assert lib.qmm_mv_swiglu_q8(1, 256, 16, 1, 0, fake, 2, fake, fake, fake, n) == st["QMM_ERR_DTYPE"]  # GGUF: Q8 x
+    assert lib.qmm_mv_swiglu_q8(5, 4096, 16, 1, 0, fake, 2, fake, n, fake, n) == st["QMM_ERR_NULL"]
+    assert lib.qmm_mv_swiglu_q8(5, 4096, 24, 1, 0, fake, 2, fake, fake, fake, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_mv_pair_q8(5, 4096, 16, 1, 0, fake, 2, fake, fake, fake, n, n) == st["QMM_ERR_NULL"]  # y2
+    assert lib.qmm_mv_pair_q8(1, 256, 16, 1, 0, fake, 4, fake, odd, fake, fake, n) == st["QMM_ERR_ALIGN"]
+    assert lib.qmm_moe_expert_mv_q8(2, 0, 0, 0, 256, 16, 4, 2, 4, fake, fake, fake, fake, n, n, fake, n) \
+        == st["QMM_ERR_FORMAT"]
+    assert lib.qmm_moe_expert_mv_q8(1, 0, 0, 0, 256, 16, 4, 2, 3, fake, fake, fake, fake, n, n, fake, n) \
+        == st["QMM_ERR_SHAPE"]                                                 # gu: whole tokens of KU
+    assert lib.qmm_moe_expert_mv_q8(1, 0, 0, 0, 256, 16, 4, 2, 4, fake, fake, fake, n, n, n, fake, n) \
+        == st["QMM_ERR_NULL"]                                                  # gu, not fused: the up tensor
+    assert lib.qmm_moe_expert_mv_q8(0, 1, 0, 0, 96, 16, 4, 2, 4, fake, fake, fake, n, n, n, fake, n) \
+        == st["QMM_ERR_SHAPE"]                                                 # Q4_0: K % 64
+    # the prefill GEMM on Q4_0: K % 256
+    assert lib.qmm_gemm(0, 0, 64, 128, 64, fake, 1, n, fake, n, fake, 0, n) == st["QMM_ERR_SHAPE"]
     # decode swiglu matvec: GGUF-layout weights only, both matrices; the GEMM's swiglu mode needs the up matrix
     assert lib.qmm_mv_swiglu(3, 256, 4, 1, 0, fake, 0, fake, fake, fake, n) == st["QMM_ERR_FORMAT"]
     assert lib.qmm_mv_swiglu(1, 256, 4, 1, 0, fake, 0, fake, n, fake, n) == st["QMM_ERR_NULL"]
@@ -151,7 +183,7 @@ def test_argument_validation_without_a_device(lib):
     assert lib.qmm_mv_q8(6, 256, 4, 1, 0, fake, 4, odd, fake, n) == st["QMM_ERR_ALIGN"]
     assert lib.qmm_dequant(6, fake, n, 4, 320, fake, n) == st["QMM_ERR_SHAPE"]
     assert lib.qmm_gemm(6, 0, 64, 256, 64, fake, 1, n, odd, n, fake, 0, n) == st["QMM_ERR_ALIGN"]
-    assert lib.qmm_gemm(2, 0, 64, 256, 64, fake, 1, n, fake, n, fake, 0, n) == st["QMM_ERR_FORMAT"]
+    assert lib.qmm_gemm(2, 0, 64, 256, 64, fake, 1, n, fake, n, fake, 0, n) == st["QMM_ERR_FORMAT"]   # MXFP4: own entry
     # router / shared gate / wscale / gated combine
     assert lib.qmm_moe_route(4, 2882, 32, 4, 3, 0, ctypes.c_float(1), fake, 0, fake, 0, n, n, fake, fake, fake,
                              n) == st["QMM_ERR_SHAPE"]                        # H % 4

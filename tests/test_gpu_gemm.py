@@ -108,8 +108,8 @@ def test_gemm_rejects_bad_arguments(dev):
     from qmm._lib import QmmError
     import qmm.ops as ops
     w = torch.zeros(144 * 4, dtype=torch.uint8, device=dev)
-    with pytest.raises(QmmError):
-        ops.gemm("q4_0", "store", torch.zeros((4, 256), dtype=torch.float16, device=dev), w, 4, 256)
+    with pytest.raises(QmmError):   # GGUF MXFP4 blocks: the scaled-MFMA GEMM reads split / tiled planes only
+        ops.gemm("mxfp4", "store", torch.zeros((4, 256), dtype=torch.float16, device=dev), w, 4, 256)
     with pytest.raises(QmmError):
         ops.gemm("q4_k", "store", torch.zeros((4, 128), dtype=torch.float16, device=dev), w, 4, 128)
 
