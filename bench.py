@@ -27,12 +27,15 @@ one workload, or with --no-secondary):
     hbm_copy    calibration: a 256 MiB device copy, whose counter readings scale FETCH_SIZE / WRITE_SIZE to bytes
 
 Consecutive steps read different copies of the weights (more than 300 MB in rotation), so the 256 MB MALL cannot
-serve them and the figures are HBM figures. The K timed steps are captured in one HIP graph. A GPU spin kernel is
-enqueued ahead of the timed region, so the whole graph is queued on the device before the first timed kernel starts
-and the two HIP events on the launching stream see the kernels, not the host's graph submission; value = algorithmic
-work x K / elapsed. `roofline` is the dominant kernel's: algorithmic bytes (or FLOPs) per launch over its average
-launch time, each launch of that kernel timed between its own pair of HIP events. `cpu_baseline` times the numpy oracle on this
-host's cores on the same workload (dequant and matmul separately and together).
+serve them and the figures are HBM figures. The W warm-up steps run first, repeated until 30 ms of GPU time has
+passed (the clocks leave their idle state during the host-side setup). The K timed steps are launched one by one
+behind a GPU spin kernel that outlasts the host's enqueueing (--graph: captured in one HIP graph, which adds a
+launch overhead of its own on this stack), so every step is queued on the device before the first timed kernel
+starts and the two HIP events on the launching stream see the kernels and the dispatch gaps between them, not the
+host; value = algorithmic work x K / elapsed. `roofline` is the dominant kernel's: algorithmic bytes (or
+FLOPs) per launch over its average launch time, K eager launches of that kernel alone back to back between two HIP
+events (kernel time plus the dispatch gap). `cpu_baseline` times the numpy oracle on this host's cores on the same
+workload (dequant and matmul separately and together).
 """
 import argparse
 import json
@@ -68,7 +71,8 @@ def parse():
     p.add_argument("--no-secondary", action="store_true", help="measure the headline workload only")
     p.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work (headline)")
     p.add_argument("--cpu-budget-secondary", type=float, default=3.0, help="seconds of CPU work per secondary")
-    p.add_argument("--no-graph", action="store_true", help="launch steps one by one instead of a HIP graph")
+    p.add_argument("--graph", action="store_true",
+                   help="capture the timed steps in one HIP graph instead of launching them one by one")
     return p.parse_args()
 
 
@@ -494,10 +498,34 @@ WORKLOADS = {"q4_k_gemv": _q4k_gemv, "q4_k_gemv_q8": _q4k_gemv_q8, "q4_k_gemv_q8
 
 
 # ---------------------------------------------------------------------------------------------------- timing
+RAMP_MS = 30.0   # untimed GPU work before a timed region: the warm-up steps repeated until this much has run
+
+
+def _ramp(run_once):
+    """Repeats run_once() (the warm-up steps) until RAMP_MS of GPU time has passed, so the timed region starts at the
+    clocks the workload runs at, not at the idle clocks of the host-side setup before it."""
+    import torch
+    total, n = 0.0, 0
+    while total < RAMP_MS and n < 1000:
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        run_once()
+        b.record()
+        torch.cuda.synchronize()
+        total += a.elapsed_time(b)
+        n += 1
+
+
+def _spin_for(host_s_per_step, steps):
+    """Spin cycles that outlast the host's enqueueing of `steps` steps (about 2.4 cycles a ns, twice the estimate)."""
+    return int(max(SPIN_CYCLES, 2.0 * host_s_per_step * steps * 2.4e9))
+
+
 def timed(step_fn, steps, warmup, no_graph=False):
     """ms for `steps` steps between two HIP events on the launching stream, and the wall time of that region.
-    Graph mode captures the steps in one HIP graph; a spin kernel ahead of the first event holds the stream while the
-    host submits the graph, so the events time the kernels and the gaps between them only."""
+    Graph mode captures the steps in one HIP graph; eager mode launches them one by one. Either way the warm-up steps
+    run first (repeated for RAMP_MS of GPU time), and a spin kernel ahead of the first event holds the stream while
+    the host submits, so the events time the kernels and the gaps between them only."""
     import torch
     stream = torch.cuda.current_stream()
 
@@ -507,23 +535,25 @@ def timed(step_fn, steps, warmup, no_graph=False):
 
     torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    w = max(warmup, 1)
     if no_graph:
-        run(warmup, 0)
-        torch.cuda.synchronize()
-        torch.cuda._sleep(SPIN_CYCLES)
+        h0 = time.perf_counter()
+        run(w, 0)
+        host = (time.perf_counter() - h0) / w
+        _ramp(lambda: run(w, 0))
+        torch.cuda._sleep(_spin_for(host, steps))
         wall0 = time.perf_counter()
         t0.record(stream)
-        run(steps, warmup)
+        run(steps, w)
         t1.record(stream)
     else:
         gw, gt = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
         with torch.cuda.graph(gw):
-            run(max(warmup, 1), 0)
+            run(w, 0)
         with torch.cuda.graph(gt):
-            run(steps, warmup)
+            run(steps, w)
         torch.cuda.synchronize()
-        gw.replay()
-        torch.cuda.synchronize()
+        _ramp(gw.replay)
         torch.cuda._sleep(SPIN_CYCLES)
         wall0 = time.perf_counter()
         t0.record(stream)
@@ -533,31 +563,19 @@ def timed(step_fn, steps, warmup, no_graph=False):
     return t0.elapsed_time(t1), time.perf_counter() - wall0
 
 
-def kernel_times(fn, steps, warmup):
-    """Per-launch durations (ms) of fn(warmup) .. fn(warmup + steps - 1), each launch between its own pair of HIP
-    events on the launching stream. The launches are eager and queued behind a spin kernel that outlasts the host's
-    enqueueing, so every start event is followed at once by its kernel."""
-    import torch
-    stream = torch.cuda.current_stream()
-    for i in range(warmup):
-        fn(i)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    torch.cuda.synchronize()
-    torch.cuda._sleep(max(SPIN_CYCLES, 400_000 * steps))   # about 160 us of spin per queued launch
-    for i, (a, b) in enumerate(evs):
-        a.record(stream)
-        fn(warmup + i)
-        b.record(stream)
-    torch.cuda.synchronize()
-    return [a.elapsed_time(b) for a, b in evs]
+def kernel_time(fn, steps, warmup):
+    """Average launch time (ms) of the dominant kernel: `steps` eager launches fn(warmup) .. back to back between two
+    HIP events on the launching stream, after the warm-up launches and the ramp, queued behind a spin that outlasts
+    the host's enqueueing (so the GPU runs them without idling: each launch's time is its kernel plus the dispatch
+    gap to the next). The launches are eager because a captured graph adds its own launch overhead on this stack."""
+    return timed(fn, steps, warmup, no_graph=True)[0] / steps
 
 
 def measure(wl, args, cpu_budget):
     """Times one set-up workload; returns its result fields (the headline line's, or a secondary entry's)."""
-    ms, wall = timed(wl.step, args.steps, args.warmup, args.no_graph)
+    ms, wall = timed(wl.step, args.steps, args.warmup, no_graph=not args.graph)
     per_step_s = ms / 1e3 / args.steps
-    kt = kernel_times(wl.kernel_step or wl.step, args.steps, args.warmup)
-    per_launch_s = float(np.mean(kt)) / 1e3
+    per_launch_s = kernel_time(wl.kernel_step or wl.step, args.steps, args.warmup) / 1e3
     kb = wl.gu_bytes() if hasattr(wl, "gu_bytes") else wl.alg_bytes()
     kf = wl.gu_flops() if hasattr(wl, "gu_flops") else wl.alg_flops()
     if wl.bound == "hbm":
@@ -567,7 +585,6 @@ def measure(wl, args, cpu_budget):
     roof = {"bound": wl.bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4), "traffic": traffic_from_profile(wl.traffic_name),
             "kernel": wl.traffic_name.split(".")[0], "avg_launch_us": round(per_launch_s * 1e6, 3),
-            "median_launch_us": round(float(np.median(kt)) * 1e3, 3),
             "alg_bytes_per_launch": kb, "alg_flops_per_launch": kf}
     res = {"value": round(wl.value(per_step_s), 3), "unit": wl.unit, "ms_per_step": round(ms / args.steps, 6),
            "roofline": roof, "gbs": round(wl.alg_bytes() / per_step_s / 1e9, 2),

@@ -51,6 +51,7 @@ enum qmm_dtype {
 };
 enum qmm_gemm_mode { QMM_GEMM_STORE = 0, QMM_GEMM_ACC = 1, QMM_GEMM_SWIGLU = 2 };
 enum qmm_act { QMM_ACT_SILU = 0, QMM_ACT_SWIGLU_OAI = 1 };
+enum qmm_moe_flags { QMM_MOE_Q8 = 1 /* the decode chain on Q8_1 activations (the reference's MOE_Q8) */ };
 
 /* Library version (major*10000 + minor*100 + patch) and the text of a status code. */
 int qmm_version(void);
@@ -316,6 +317,31 @@ int qmm_moe_combine(int64_t tokens, int64_t rows, int64_t H, int KU, const float
  * order). sg f32 [tokens] from qmm_moe_shared_gate; other arguments as qmm_moe_combine. */
 int qmm_moe_combine_gated(int64_t tokens, int64_t rows, int64_t H, int KU, const float *ys, const int32_t *pos,
                           const float *wts, const float *sg, float *y, qmm_stream_t stream);
+
+/* The routed experts of one MoE layer as one call: the command sequence of the reference's moe_routed
+ * (S/gen_llm.py:5324-5385) on one stream, its intermediates (the buffers of moe_alloc, S/gen_llm.py:5388-5432) in the
+ * caller's workspace of at least qmm_moe_routed_workspace_size bytes (256-byte aligned):
+ *   tokens >= 64 (prefill): qmm_moe_route / qmm_moe_topk, [qmm_moe_wscale], qmm_moe_bucket, the activation operand
+ *     (qmm_row_scale_f16 for GGUF formats, qmm_quant_mxfp8 for MXFP4 planes), the grouped gate/up GEMM
+ *     (qmm_moe_grouped / qmm_moe_grouped_mxfp8), its output's operand, the grouped down GEMM, qmm_moe_combine;
+ *   tokens < 64 (decode): route, [wscale], the gate/up and down expert matvecs (qmm_moe_expert_mv[_split], or with
+ *     flags QMM_MOE_Q8 qmm_quant_q8 + qmm_moe_expert_mv_q8 for both), qmm_moe_combine over the assignments.
+ * Results equal those of the separate calls bit for bit. Names as in those calls: fmt the gate / up format (GGUF
+ * Q4_K / Q6_K / Q4_0 / MXFP4, split MXFP4S, tiled MXFP4T for prefill), fmt_down the down tensor's (-1: fmt); x f32 /
+ * bf16 [tokens, H]; logits f32 [tokens, E], or NULL to route with w_router [E, H] (f32 / bf16); router_bias and
+ * down_scale (f32 [E]) or NULL; ws_* the split / tiled scale planes; bias_* the expert biases or NULL; y f32
+ * [tokens, H] is written, or added to (accumulate), or with sg (f32 [tokens], the shared gate) y = sg y + routed. */
+int qmm_moe_routed(int fmt, int fmt_down, int fused, int act, int gating, int norm, float scale, int flags, int E,
+                   int KU, int64_t tokens, int64_t H, int64_t FE, const void *x, int x_dtype, const float *logits,
+                   const void *w_router, int w_router_dtype, const float *router_bias, const float *down_scale,
+                   const void *w_gate, const void *ws_gate, const void *w_up, const void *ws_up, const void *w_down,
+                   const void *ws_down, const float *bias_gate, const float *bias_up, const float *bias_down,
+                   const float *sg, int accumulate, float *y, void *workspace, int64_t workspace_bytes,
+                   qmm_stream_t stream);
+/* Workspace bytes qmm_moe_routed needs (router != 0: routing from w_router, which keeps the logits there), or -1
+ * for a combination it does not run. */
+int64_t qmm_moe_routed_workspace_size(int fmt, int flags, int E, int KU, int64_t tokens, int64_t H, int64_t FE,
+                                      int router);
 
 #ifdef __cplusplus
 }

@@ -20,6 +20,7 @@ S/ = skills/loom-port-llm/starter/):
     moe_combine       g_moe_combine[_sorted] [shared_gated]   S/gen_moe.py:730-779, :1231-1280
     moe_prefill       the prefill chain of moe_routed          S/gen_llm.py:5324-5385 (t >= 64)
     moe_decode        the decode chain of moe_routed           S/gen_llm.py:5324-5385 (t < 64)
+    moe_chain         moe_routed in one library call            qmm_moe_routed, S/gen_llm.py:5324-5432
     moe_layer         shared experts + routed experts          moe_layer, S/gen_llm.py:5306-5321
     row_scale_f16     g_row_scale_f16[_tiles]                 S/gen_llm.py:1843-1915, S/gen_moe.py:503-527
     dequant           the @g_<fmt>_values helpers (bit-exact f32 values)
@@ -572,6 +573,44 @@ def moe_routed(fmt, x, logits, E, KU, H, FE, gating, norm, **kw):
     if chain is moe_prefill:
         kw.pop("q8", None)   # the prefill chain's activations are the GEMMs' (f16 rows, MXFP8)
     return chain(fmt, x, logits, E, KU, H, FE, gating, norm, **kw)
+
+
+def moe_chain_workspace(fmt, E, KU, T, H, FE, q8=False, router=False):
+    """Bytes of the workspace moe_chain (qmm_moe_routed) needs."""
+    n = _lib.load().qmm_moe_routed_workspace_size(CODE[fmt], int(bool(q8)), E, KU, T, H, FE, int(bool(router)))
+    if n < 0:
+        raise ValueError(f"qmm_moe_routed does not run {fmt} at {T} tokens (q8={q8})")
+    return n
+
+
+def moe_chain(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=None, ws_gate=None, ws_down=None,
+              ws_up=None, fused=False, act="silu", scale=1.0, bias=None, router=None, expert_bias=None,
+              down_scale=None, y=None, sg=None, fmt_down=None, q8=False, workspace=None):
+    """The routed experts of one MoE layer in one library call (qmm_moe_routed, the command sequence of moe_routed,
+    S/gen_llm.py:5324-5385): the same kernels as moe_routed's op-by-op chain, the intermediates in one workspace
+    (a uint8 device tensor of at least moe_chain_workspace bytes; allocated here when None). Arguments as
+    moe_prefill / moe_decode. Returns y f32 [T, H]."""
+    _dev(x, logits, w_gate, w_down, w_up, ws_gate, ws_down, ws_up, bias, router, down_scale, y, sg, workspace)
+    T = x.shape[0]
+    _cols(x, H)
+    if (logits is None) == (router is None):
+        raise ValueError("give the router logits or the router weight, one of them")
+    need = moe_chain_workspace(fmt, E, KU, T, H, FE, q8=q8, router=router is not None)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    elif workspace.numel() < need:
+        raise ValueError(f"the workspace holds {workspace.numel()} bytes, the chain needs {need}")
+    accumulate = y is not None and sg is None
+    if sg is not None and y is None:
+        raise ValueError("the gated combine scales the shared experts' output already in y")
+    y = _out(y, (T, H), torch.float32, x.device)
+    bg, bu, bd = expert_bias if expert_bias is not None else (None, None, None)
+    _lib.call("qmm_moe_routed", CODE[fmt], CODE[fmt_down] if fmt_down else -1, int(fused), ACT[act], gating,
+              int(bool(norm)), float(scale), int(bool(q8)), E, KU, T, H, FE, _ptr(x), _dt(x), _ptr(logits),
+              _ptr(router), _dt(router) if router is not None else 0, _ptr(bias), _ptr(down_scale), _ptr(w_gate),
+              _ptr(ws_gate), _ptr(w_up), _ptr(ws_up), _ptr(w_down), _ptr(ws_down), _ptr(bg), _ptr(bu), _ptr(bd),
+              _ptr(sg), int(accumulate), _ptr(y), _ptr(workspace), workspace.numel(), _stream())
+    return y
 
 
 def moe_layer(fmt, x, logits, E, KU, H, FE, gating, norm, shared=None, **kw):
