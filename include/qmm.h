@@ -343,6 +343,21 @@ int qmm_moe_routed(int fmt, int fmt_down, int fused, int act, int gating, int no
 int64_t qmm_moe_routed_workspace_size(int fmt, int flags, int E, int KU, int64_t tokens, int64_t H, int64_t FE,
                                       int router);
 
+/* qmm_moe_routed without a workspace argument and without any allocation: no counterpart in the reference (its
+ * command programs allocate every buffer up front); it is for callers that cannot allocate device memory -- code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc. The intermediates live in one
+ * static device array of 16 MiB per GPU (held until the process ends), enough for the decode chain of any model with
+ * H + FE <= 8192 at up to 63 tokens; a call needing more returns QMM_ERR_WORKSPACE before launching anything (use
+ * qmm_moe_routed). Calls that overlap on one GPU (two streams or host threads) share the array and race. Arguments
+ * and results as qmm_moe_routed. */
+int qmm_moe_routed_static(int fmt, int fmt_down, int fused, int act, int gating, int norm, float scale, int flags,
+                          int E, int KU, int64_t tokens, int64_t H, int64_t FE, const void *x, int x_dtype,
+                          const float *logits, const void *w_router, int w_router_dtype, const float *router_bias,
+                          const float *down_scale, const void *w_gate, const void *ws_gate, const void *w_up,
+                          const void *ws_up, const void *w_down, const void *ws_down, const float *bias_gate,
+                          const float *bias_up, const float *bias_down, const float *sg, int accumulate, float *y,
+                          qmm_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -51,6 +51,9 @@ SIGNATURES = {
                        c_vp, c_int, c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
                        c_vp, c_vp, c_int, c_vp, c_vp, c_i64, c_vp],
     "qmm_moe_routed_workspace_size": [c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_int],
+    "qmm_moe_routed_static": [c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_int, c_int, c_int, c_i64, c_i64,
+                              c_i64, c_vp, c_int, c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
+                              c_vp, c_vp, c_vp, c_vp, c_int, c_vp, c_vp],
 }
 RESTYPE = {"qmm_strerror": ctypes.c_char_p, "qmm_row_bytes": c_i64, "qmm_mxfp4t_scale_bytes": c_i64,
            "qmm_moe_routed_workspace_size": c_i64}
