@@ -272,8 +272,9 @@ class MoeWorkload:
             self.T = m or 64
             self.metric = "Q4_K MoE prefill TFLOP/s (Qwen3-30B-A3B, 128 experts, top-8)"
         self.decode = self.T < 64
+        # the Q4_K prefill chain streams the tiled layout through the narrow grouped kernel
         kern = ("expert_mv" if self.decode else "mxfp4_grouped_kernel_gu8") if index == 3 else \
-            ("expert_mv" if self.decode else "q4k_mfma_kernel_gu")
+            ("expert_mv" if self.decode else "q4k_narrow_kernel_gu")
         model = "mxfp4_moe_gpt_oss_20b" if index == 3 else "q4_k_moe_qwen3_30b_a3b"
         self.traffic_name = f"{kern}.{model}_t{self.T}"
 
@@ -301,8 +302,13 @@ class MoeWorkload:
             self.wbytes_expert = (2 * FE * H + H * FE) // 2 + (2 * FE * H + H * FE) // 32
             self.peak_key = "fp8"
         else:
-            self.fmt = "q4_k"
+            # prefill: one-time weight preparation, GGUF blocks -> the tiled Q4_K layout the grouped GEMMs stream
             self.kw = dict(w_gate=u8(d["gate"]), w_up=u8(d["up"]), w_down=u8(d["down"]), fused=False, act=d["act"])
+            self.fmt = "q4_k"
+            if not self.decode:
+                for m, rows, k in (("w_gate", E * FE, H), ("w_up", E * FE, H), ("w_down", E * H, FE)):
+                    self.kw[m] = ops.tile_q4k(self.kw[m], rows, k)
+                self.fmt = "q4_kt"
             self.wbytes_expert = (2 * FE * H + H * FE) // 256 * 144
             self.peak_key = "fp16"
         self.ops = ops
@@ -380,6 +386,8 @@ class MoeWorkload:
             return "mxfp4 x mxfp8 (E4M3, E8M0 per 32) -> f32"
         if self.fmt == "mxfp4s":
             return "mxfp4 x bf16 -> f32 (expert matvecs)"
+        if self.fmt == "q4_kt":
+            return "q4_k (tiled layout) x f16 (row-scaled) -> f32"
         return "q4_k x f16 (row-scaled) -> f32"
 
     def cpu_baseline(self, budget):
@@ -403,7 +411,7 @@ class MoeWorkload:
             return g, u, of.dequantize(gfmt, d["down"][H * e * rb_f:H * (e + 1) * rb_f], H, FE)
 
         x = synth.bf16_bits_to_f32(d["x_bf16"])
-        rnd = {"mxfp4t": ref.mxfp8_values, "q4_k": ref.f16_rows}.get(self.fmt)
+        rnd = {"mxfp4t": ref.mxfp8_values, "q4_k": ref.f16_rows, "q4_kt": ref.f16_rows}.get(self.fmt)
         res = cpu_baseline.time_moe(x, d["logits"], KU, d["gating"], d["norm"], d["act"], experts, budget_s=budget,
                                     x_round=rnd, act_round=rnd)
         return cpu_entry(res, self.alg_flops(), "TFLOP/s", 1e12,

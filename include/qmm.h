@@ -65,7 +65,7 @@ int64_t qmm_row_bytes(int fmt, int64_t k);
  * (the values @g_q4_0_values S/quant_values.loom:386-408, @g_q4_k_values S/gen_llm.py:288-326,
  *  @g_mxfp4_values S/gen_llm.py:786-841 and @g_mxfp4s_values S/gen_llm.py:844-895 produce).
  * w: weight bytes; ws: the E8M0 scale plane for QMM_MXFP4S / QMM_MXFP4T, else NULL (QMM_MXFP4T: rows % 32 == 0,
- * K % 64 == 0; QMM_Q4_KT: rows % 16 == 0, K % 512 == 0). */
+ * K % 64 == 0; QMM_Q4_KT: rows % 16 == 0, K % 256 == 0). */
 int qmm_dequant(int fmt, const void *w, const void *ws, int64_t rows, int64_t k, float *out, qmm_stream_t stream);
 
 /* Decode matrix-vector product, the g_mv_{fmt}_k{K}[_t{TG}][_r{R}] family
@@ -224,12 +224,15 @@ int qmm_moe_expert_mv_split(int mode, int fused, int act, int64_t k, int64_t n, 
  * split-plane scale planes beside their nibble planes:
  *   gu (mode 0): act[r] = act_fn(Wg[e] x[t] inv + bias[e], Wu[e] x[t] inv + bias2[e]),  t = rowmap[r]/KU
  *   dn (mode 1): ys[r]  = Wd[e] x[r] inv + bias[e]                                      (x rows sorted)
- * for every row r of every 64-row tile whose expert e = tile_info[tile, 0] >= 0; rows with rowmap[r] == -1 are
- * written as zeros, rows of unused tiles are not written. Weights as qmm_moe_expert_mv: w [E, n, k] (gu: gate;
+ * for every row r of every 64-row tile whose expert e = tile_info[tile, 0] >= 0; rows with rowmap[r] == -1 and the
+ * rows of unused tiles are not written (the combine reads only the rows pos names). Weights as qmm_moe_expert_mv: w [E, n, k] (gu: gate;
  * fused != 0: [E, 2n, k], each expert's n gate rows then its n up rows; w2 the up tensor otherwise).
  *   QMM_Q4_K:   x is the row-scaled f16 operand (x_dtype QMM_F16) from qmm_row_scale_f16 with its scales f32
  *               [x_rows, 2] in x_scales (inv = scales[row, 1]); K % 256 == 0; f16 MFMA, weights staged as
  *               fma_f16(f16(q), f16(d sc), f16(-dmin m)).
+ *   QMM_Q4_KT:  as QMM_Q4_K with the weights in the tiled layout of qmm_tile_q4k (each expert's [n, k] tiled as
+ *               part of the [E n, k] tensor: n % 16 == 0; K <= 4096), read as contiguous 1 KB streams; the same
+ *               staging, the products summed in another order (no counterpart in the reference: a load-time layout).
  *   QMM_Q6_K:   as QMM_Q4_K with Q6_K weights (staged as qmm_gemm stages them); g_moe_gdn_q6_k of the Q4_K_M
  *               expert layout (Q4_K gate / up, Q6_K down).
  *   QMM_Q4_0:   as QMM_Q4_K with Q4_0 weights, staged f16(d (q - 8)) (specialize_grouped, S/moe_q4_0.py:41-61).
@@ -262,7 +265,8 @@ int qmm_moe_grouped_mxfp8(int fmt, int fused, int act, int E, int KU, int64_t ma
 
 /* Row-scaled f16 producer, g_row_scale_f16[_tiles] (S/gen_llm.py:1843-1915, S/gen_moe.py:503-527):
  * per row e = clamp(exponent(max|x|) - 13, 0, 100), x16 = f16(x * 2^-e), scales = (2^-e, 2^e).
- * tile_info (i32 [rows/64, 2]) or NULL: rows of tiles with expert -1 are skipped. x: [rows, k] of x_dtype
+ * tile_info (i32 [rows/64, 2]) or NULL: only the first tile_info[t, 1] rows of each tile t with an expert are
+ * converted (the bucket fills tiles from the top); the other rows are skipped. x: [rows, k] of x_dtype
  * (QMM_F32 as the reference, or QMM_BF16). This is the A operand qmm_gemm takes. */
 int qmm_row_scale_f16(int64_t rows, int64_t k, const void *x, int x_dtype, float *scales, void *x16,
                       const int32_t *tile_info, qmm_stream_t stream);
@@ -286,12 +290,15 @@ int qmm_quant_mxfp8(int64_t rows, int64_t k, const void *x, int x_dtype, const i
  * E8M0 scales u8 [rows, k/32]. Bit-exact: every code and exponent is kept. */
 int qmm_repack_mxfp4(const void *w, int64_t rows, int64_t k, uint8_t *nibbles, uint8_t *scales, qmm_stream_t stream);
 
-/* One-time weight preparation for the int8-activation decode GEMV (no reference counterpart: the reference reads the
- * GGUF blocks as they are): GGUF Q4_K rows [rows, k] -> the tiled layout QMM_Q4_KT. Units of 16 rows x 512 values
- * (two super-blocks a row), ordered (row block, slice), 4608 bytes each: the 32 16-byte headers ([f16 d][f16 dmin]
- * [12 scale bytes]) of super-block sb of row r at 16 (2 r + sb), then four 1 KB code planes, plane q holding at
- * 16 l (l = 4 r + 2 sb + h) code bytes 16 (4 h + q) .. +15 of that super-block. A byte permutation (same size);
- * qmm_dequant(QMM_Q4_KT) gives the GGUF values bit for bit. rows % 16 == 0, k % 512 == 0. */
+/* One-time weight preparation for the int8-activation decode GEMV and the grouped expert GEMMs (no reference
+ * counterpart: the reference reads the GGUF blocks as they are): GGUF Q4_K rows [rows, k] -> the tiled layout
+ * QMM_Q4_KT. Each block of 16 rows keeps its bytes in its own range, cut into units of 512 values (two super-blocks
+ * a row), 4608 bytes each: the 32 16-byte headers ([f16 d][f16 dmin][12 scale bytes]) of super-block sb of row r at
+ * 16 (2 r + sb), then four 1 KB code planes, plane q holding at 16 l (l = 4 r + 2 sb + h) code bytes 16 (4 h + q)
+ * .. +15 of that super-block. When k % 512 == 256 the row block ends in a half unit of 2304 bytes (the rows' last
+ * super-blocks): the 16 headers at 16 r, then four 512-byte planes, plane q holding at 16 (2 r + h) code bytes
+ * 16 (4 h + q) .. +15. A byte permutation (same size); qmm_dequant(QMM_Q4_KT) gives the GGUF values bit for bit.
+ * rows % 16 == 0, k % 256 == 0 (the decode GEMV takes k % 512 == 0). */
 int qmm_tile_q4k(const void *w, int64_t rows, int64_t k, void *w_t, qmm_stream_t stream);
 
 /* One-time weight preparation for the grouped GEMM (no reference counterpart: the reference reads the split planes
@@ -327,7 +334,7 @@ int qmm_moe_combine_gated(int64_t tokens, int64_t rows, int64_t H, int KU, const
  *   tokens < 64 (decode): route, [wscale], the gate/up and down expert matvecs (qmm_moe_expert_mv[_split], or with
  *     flags QMM_MOE_Q8 qmm_quant_q8 + qmm_moe_expert_mv_q8 for both), qmm_moe_combine over the assignments.
  * Results equal those of the separate calls bit for bit. Names as in those calls: fmt the gate / up format (GGUF
- * Q4_K / Q6_K / Q4_0 / MXFP4, split MXFP4S, tiled MXFP4T for prefill), fmt_down the down tensor's (-1: fmt); x f32 /
+ * Q4_K / Q6_K / Q4_0 / MXFP4, split MXFP4S, tiled MXFP4T or Q4_KT for prefill), fmt_down the down tensor's (-1: fmt); x f32 /
  * bf16 [tokens, H]; logits f32 [tokens, E], or NULL to route with w_router [E, H] (f32 / bf16); router_bias and
  * down_scale (f32 [E]) or NULL; ws_* the split / tiled scale planes; bias_* the expert biases or NULL; y f32
  * [tokens, H] is written, or added to (accumulate), or with sg (f32 [tokens], the shared gate) y = sg y + routed. */

@@ -7,8 +7,8 @@
 //                       + bu[e, c]),  t = rowmap[r] / KU  (rows gathered from the token rows)
 //   dn      ys[r, c]  = inv[r] sum_k A16[r, k] Wd[e][c, k] + bd[e, c]            (rows already sorted)
 //
-// for every row r of every 64-row tile whose expert e = tile_info[tile, 0] >= 0; rows with rowmap[r] < 0 are
-// written as zeros. The optional expert biases (gpt-oss ffn_{gate,up,down}_exps.bias) are added after the row
+// for every row r of every 64-row tile whose expert e = tile_info[tile, 0] >= 0; rows with rowmap[r] < 0 are not
+// written. The optional expert biases (gpt-oss ffn_{gate,up,down}_exps.bias) are added after the row
 // inverse, before the activation (_gemm_bias_act, S/gen_moe.py:958-1007). X16 / A16 are the row-scaled f16 operands the reference's g_row_scale_f16[_tiles] produces
 // (S/gen_llm.py:1843-1915, S/gen_moe.py:503-527) and inv = their scales[row, 1]. W is dequantized to f16 in
 // registers the way the reference stages it: Q4_K w = fma_f16(f16(q), f16(d sc), f16(-dmin m)) (S/gen_gemm.py:499-530),
@@ -35,6 +35,7 @@
 // Tile order is XCD-aware: consecutive tile ids land on one XCD (dense: the M tiles of one N tile, which share
 // weight columns; grouped: the column blocks of one expert tile, which share its activation rows).
 #include "common.hpp"
+#include "deq_f16.hpp"
 
 using namespace qmm;
 
@@ -47,79 +48,12 @@ constexpr int BM = 64, KSTEP = 64;
 constexpr int kDepth = QMM_GEMM_DEPTH;   // steps of loads in flight per wave (even)
 static_assert(kDepth % 2 == 0, "the LDS double buffer follows the step parity");
 constexpr int APITCH = KSTEP + 8;   // f16 per LDS row: 144 bytes, rows 16-byte aligned, reads 2-way at most
-typedef __attribute__((ext_vector_type(2))) _Float16 h2;
 
 // kDense: Y (+)= X W^T; kSwiglu: Y = silu(X Wg^T inv) (X Wu^T inv) over dense rows (the GEMM's swiglu mode);
 // kGU / kDN: the grouped gate/up and down GEMMs over bucketed expert tiles
 enum Kind { kDense = 0, kGU = 1, kDN = 2, kSwiglu = 3 };
 // weight formats: GGUF Q4_K (144-byte super-blocks), Q6_K (210), Q4_0 (18-byte blocks of 32)
 enum WFmt { kWQ4K = 0, kWQ6K = 1, kWQ40 = 2 };
-
-__device__ __forceinline__ h2 as_h2(u32 v) { return __builtin_bit_cast(h2, v); }
-__device__ __forceinline__ u32 as_u32(h2 v) { return __builtin_bit_cast(u32, v); }
-
-// 8 f16 weights of one column in K order from two code dwords (values 0..3 and 4..7 of the run) of one nibble
-// plane: bytes become (1024 + q) f16 pairs with one v_perm each, the 1024 is removed exactly, then one rounding
-// fma with the sub-block's f16 scale and negated minimum.
-__device__ __forceinline__ f16x8 deq8_codes(u32 n0, u32 n1, h2 dsc, h2 nmn) {
-  const u32 k64 = 0x64646464u;
-  const h2 m1024 = as_h2(0xE400E400u);
-  const u32 t[4] = {__builtin_amdgcn_perm(k64, n0, 0x04010400u), __builtin_amdgcn_perm(k64, n0, 0x04030402u),
-                    __builtin_amdgcn_perm(k64, n1, 0x04010400u), __builtin_amdgcn_perm(k64, n1, 0x04030402u)};
-  u32 o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = as_u32(__builtin_elementwise_fma(as_h2(t[i]) + m1024, dsc, nmn));
-  typedef __attribute__((ext_vector_type(4))) u32 u32x4;
-  return __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]});
-}
-template <bool HI>
-__device__ __forceinline__ f16x8 deq8(u32 q0, u32 q1, h2 dsc, h2 nmn) {
-  return deq8_codes(HI ? (q0 >> 4) & 0x0F0F0F0Fu : q0 & 0x0F0F0F0Fu, HI ? (q1 >> 4) & 0x0F0F0F0Fu : q1 & 0x0F0F0F0Fu,
-                    dsc, nmn);
-}
-// Q4_0: 8 f16 weights from two code dwords: (1024 + q) - 1032 = q - 8 exactly, then one rounding f16 multiply by d
-// (f16(d (q - 8)), the reference's staging, also where -8 d would overflow f16)
-template <bool HI>
-__device__ __forceinline__ f16x8 deq8_q40(u32 q0, u32 q1, h2 d) {
-  const u32 n0 = HI ? (q0 >> 4) & 0x0F0F0F0Fu : q0 & 0x0F0F0F0Fu, n1 = HI ? (q1 >> 4) & 0x0F0F0F0Fu : q1 & 0x0F0F0F0Fu;
-  const u32 k64 = 0x64646464u;
-  const h2 m1032 = __builtin_bit_cast(h2, 0xE408E408u);
-  const u32 t[4] = {__builtin_amdgcn_perm(k64, n0, 0x04010400u), __builtin_amdgcn_perm(k64, n0, 0x04030402u),
-                    __builtin_amdgcn_perm(k64, n1, 0x04010400u), __builtin_amdgcn_perm(k64, n1, 0x04030402u)};
-  u32 o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = __builtin_bit_cast(u32, (__builtin_bit_cast(h2, t[i]) + m1032) * d);
-  typedef __attribute__((ext_vector_type(4))) u32 u32x4;
-  return __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]});
-}
-
-// Q6_K (210-byte super-blocks, only 2-byte aligned): 16-byte pieces are loaded at any even address (the HSA
-// runtime runs the GPU in unaligned access mode; the compiler emits global_load_dwordx4 for them).
-typedef uint4 uint4_a2 __attribute__((aligned(2)));
-typedef u32 u32_a2 __attribute__((aligned(2)));
-__device__ __forceinline__ uint4 ld16u(const u8 *p) { return *reinterpret_cast<const uint4_a2 *>(p); }
-__device__ __forceinline__ u32 ld4u(const u8 *p) { return *reinterpret_cast<const u32_a2 *>(p); }
-
-// f16 (d sc, -dmin m) of sub-block g from a super-block header, broadcast to both halves
-__device__ __forceinline__ void sub_scale(const uint4 &hd, int g, h2 &dsc, h2 &nmn) {
-  u32 sc, mn;
-  q4k_scale_min(hd.y, hd.z, hd.w, g, sc, mn);
-  const _Float16 a = (_Float16)(f16_to_f32(hd.x) * (float)sc);
-  const _Float16 b = (_Float16)(-(f16_to_f32(hd.x >> 16) * (float)mn));
-  dsc = h2{a, a};
-  nmn = h2{b, b};
-}
-
-__device__ __forceinline__ uint4 ld16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
-
-__device__ __forceinline__ float act_fn(int act, float g, float u) {
-  if (act == QMM_ACT_SWIGLU_OAI) {
-    const float xg = fminf(g, 7.0f);
-    const float yu = fminf(fmaxf(u, -7.0f), 7.0f);
-    return xg / (1.0f + expf(-1.702f * xg)) * (yu + 1.0f);
-  }
-  return g / (1.0f + expf(-g)) * u;
-}
 
 struct Args {
   int M, N, K;                 // dense: rows; grouped: rows of the sorted output (max_tiles * 64)
@@ -523,17 +457,16 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
             yf[o] = v;
           }
         } else {
-          float v = 0.f;
-          if (src >= 0) {
-            const float inv = rinv[lr];
-            const int64_t bo = (int64_t)expert * N + col;
-            const float b = a.bias ? a.bias[bo] : 0.f;
-            if constexpr (KIND == kGU) {
-              const float b2 = a.bias2 ? a.bias2[bo] : 0.f;
-              v = act_fn(a.act, acc[i][j][r] * inv + b, red_at(0, i, j, r) * inv + b2);
-            } else {
-              v = acc[i][j][r] * inv + b;
-            }
+          if (src < 0) continue;   // a row without an assignment is not written
+          const float inv = rinv[lr];
+          const int64_t bo = (int64_t)expert * N + col;
+          const float b = a.bias ? a.bias[bo] : 0.f;
+          float v;
+          if constexpr (KIND == kGU) {
+            const float b2 = a.bias2 ? a.bias2[bo] : 0.f;
+            v = act_fn(a.act, acc[i][j][r] * inv + b, red_at(0, i, j, r) * inv + b2);
+          } else {
+            v = acc[i][j][r] * inv + b;
           }
           yf[o] = v;
         }
@@ -583,7 +516,7 @@ int launch_fmt(int fmt, const Args &a, hipStream_t s) {
 int64_t fmt_row_bytes(int fmt, int64_t k) {
   return fmt == QMM_Q4_0 ? k / 32 * 18 : k / 256 * (fmt == QMM_Q6_K ? 210 : 144);
 }
-int fmt_align(int fmt) { return fmt == QMM_Q4_K ? 16 : fmt == QMM_Q6_K ? 4 : 2; }
+int fmt_align(int fmt) { return fmt == QMM_Q4_K || fmt == QMM_Q4_KT ? 16 : fmt == QMM_Q6_K ? 4 : 2; }
 
 }  // namespace
 
@@ -618,6 +551,16 @@ extern "C" int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, c
   return launch_fmt<kDense, false, false>(fmt, a, s);
 }
 
+int qmm_grouped_q4k_narrow(int tiled, int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E,
+                           int KU, const int32_t *tile_info, const int32_t *rowmap, const void *x,
+                           const float *x_scales, int64_t x_rows, const void *w, const void *w2, const float *bias,
+                           const float *bias2, float *y, hipStream_t s);
+bool qmm_grouped_narrow_fits(int64_t k, int64_t n);
+#ifndef QMM_NARROW_ROWS
+#define QMM_NARROW_ROWS 8
+#endif
+constexpr int64_t kNarrowRowsPerExpert = QMM_NARROW_ROWS;   // mean assignments an expert up to which it applies
+
 // The Q4_K / Q6_K / Q4_0 path of qmm_moe_grouped (grouped.hip checks the arguments shared with the MXFP4 path).
 int qmm_grouped_q4k(int fmt, int mode, int fused, int act, int64_t max_tiles, int64_t k, int64_t n, int E, int KU,
                     const int32_t *tile_info, const int32_t *rowmap, const void *x, const float *x_scales,
@@ -627,6 +570,18 @@ int qmm_grouped_q4k(int fmt, int mode, int fused, int act, int64_t max_tiles, in
   if (x_rows * k * 2 >= (1ll << 31)) return QMM_ERR_SHAPE;   // activation rows are addressed by a 32-bit buffer offset
   const int wal = fmt_align(fmt);
   if (!aligned(x, 16) || !aligned(w, wal) || (w2 && !aligned(w2, wal))) return QMM_ERR_ALIGN;
+  // The tiled layout is read by the narrow kernel only. GGUF Q4_K with few rows an expert (max_tiles = assignments /
+  // 64 + E, so 64 (max_tiles - E) bounds the assignments): the narrow kernel too, which streams each expert's
+  // weights once against 16-row groups held in LDS.
+  if (fmt == QMM_Q4_KT) {
+    if (!qmm_grouped_narrow_fits(k, n)) return QMM_ERR_SHAPE;
+    if (!aligned(y, 16)) return QMM_ERR_ALIGN;
+    return qmm_grouped_q4k_narrow(1, mode, fused, act, max_tiles, k, n, E, KU, tile_info, rowmap, x, x_scales, x_rows,
+                                  w, w2, bias, bias2, y, s);
+  }
+  if (fmt == QMM_Q4_K && qmm_grouped_narrow_fits(k, n) && aligned(y, 16) && 64 * (max_tiles - E) <= kNarrowRowsPerExpert * E)
+    return qmm_grouped_q4k_narrow(0, mode, fused, act, max_tiles, k, n, E, KU, tile_info, rowmap, x, x_scales, x_rows,
+                                  w, w2, bias, bias2, y, s);
   const int64_t RB = fmt_row_bytes(fmt, k);
   Args a{};
   a.M = (int)(max_tiles * BM); a.N = (int)n; a.K = (int)k;

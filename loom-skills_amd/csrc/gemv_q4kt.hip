@@ -351,24 +351,38 @@ int launch_u(const TArgs &a, hipStream_t s) {
   return launch_tg<1, U, STAGEQ, MODE>(a, s);
 }
 
-// One thread per 16-byte piece of the tiled matrix: pieces 0..31 of a unit are the headers of (row p / 2,
-// super-block p % 2), the others the code planes (see the layout above).
+// One thread per 16-byte piece of the tiled matrix. A row block is 16 rows x K / 256 super-blocks: F = K / 512 full
+// units of 288 pieces (pieces 0..31 the headers of (row p / 2, super-block p % 2), the others the code planes), then,
+// when K % 512 == 256, a half unit of 144 pieces (pieces 0..15 the headers of the rows' last super-blocks, then four
+// planes of 32 pieces, piece 32 q + 2 r + h holding code bytes 16 (4 h + q) of row r).
 __global__ void tile_q4k_kernel(const u8 *__restrict__ src, int64_t rows, int64_t K, u8 *__restrict__ dst) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t S = K / 512, units = rows / 16 * S;
-  if (i >= units * (kUnit / 16)) return;
-  const int64_t unit = i / (kUnit / 16);
-  const int p = (int)(i % (kUnit / 16));
-  const int64_t rb = unit / S, sl = unit % S;
-  int r, sb, off;
-  if (p < 32) {
-    r = p >> 1; sb = p & 1; off = 0;
+  const int64_t rbp = K / 256 * 144;   // pieces of a row block: 16 rows x K / 256 x 144 bytes / 16
+  if (i >= rows / 16 * rbp) return;
+  const int64_t rb = i / rbp;
+  const int p = (int)(i % rbp), F = (int)(K / 512);
+  const int sl = p / (kUnit / 16), pu = p % (kUnit / 16);
+  int r, b, off;
+  if (sl < F) {
+    if (pu < 32) {
+      r = pu >> 1; b = 2 * sl + (pu & 1); off = 0;
+    } else {
+      const int q = (pu - 32) >> 6, l = (pu - 32) & 63;
+      r = l >> 2; b = 2 * sl + ((l >> 1) & 1);
+      off = 16 + 16 * (4 * (l & 1) + q);
+    }
   } else {
-    const int q = (p - 32) >> 6, l = (p - 32) & 63;
-    r = l >> 2; sb = (l >> 1) & 1;
-    off = 16 + 16 * (4 * (l & 1) + q);
+    const int ph = p - F * (kUnit / 16);
+    if (ph < 16) {
+      r = ph; off = 0;
+    } else {
+      const int q = (ph - 16) >> 5, l = (ph - 16) & 31;
+      r = l >> 1;
+      off = 16 + 16 * (4 * (l & 1) + q);
+    }
+    b = 2 * F;
   }
-  const u8 *blk = src + (16 * rb + r) * (K / 256 * 144) + (2 * sl + sb) * 144 + off;
+  const u8 *blk = src + (16 * rb + r) * (K / 256 * 144) + (int64_t)b * 144 + off;
   *reinterpret_cast<v4u *>(dst + 16 * i) = *reinterpret_cast<const v4u *>(blk);
 }
 
@@ -380,9 +394,11 @@ __global__ void dequant_q4kt_kernel(const u8 *__restrict__ w, int64_t rows, int6
   if (gi >= rows * G) return;
   const int64_t row = gi / G;
   const int g = (int)(gi % G), b = g >> 3, s = g & 7;
-  const int i = (int)(row & 15), sb = b & 1;
-  const u8 *unit = w + ((row >> 4) * (K / 512) + (b >> 1)) * kUnit;
-  const u32 *hd = reinterpret_cast<const u32 *>(unit + 16 * (2 * i + sb));
+  const int i = (int)(row & 15), sb = b & 1, F = (int)(K / 512);
+  const u8 *rbase = w + (row >> 4) * (K / 256 * 144 * 16);
+  const bool tail = b >= 2 * F;   // the half unit of K % 512 == 256
+  const u8 *unit = rbase + (int64_t)(tail ? F : b >> 1) * kUnit;
+  const u32 *hd = reinterpret_cast<const u32 *>(unit + (tail ? 16 * i : 16 * (2 * i + sb)));
   u32 sc, mn;
   q4k_scale_min(hd[1], hd[2], hd[3], s, sc, mn);
   const float scale = f16_to_f32(hd[0]) * (float)sc;
@@ -392,7 +408,9 @@ __global__ void dequant_q4kt_kernel(const u8 *__restrict__ w, int64_t rows, int6
 #pragma unroll
   for (int l = 0; l < 32; ++l) {
     const int c = 32 * (s >> 1) + l;   // code byte of the super-block
-    const u8 v = unit[512 + 1024 * ((c >> 4) & 3) + 16 * (4 * i + 2 * sb + (c >> 6)) + (c & 15)];
+    const int q = (c >> 4) & 3, h = c >> 6;
+    const u8 v = tail ? unit[256 + 512 * q + 16 * (2 * i + h) + (c & 15)]
+                      : unit[512 + 1024 * q + 16 * (4 * i + 2 * sb + h) + (c & 15)];
     o[l] = __fsub_rn(__fmul_rn(scale, (float)((v >> shift) & 15u)), minimum);
   }
 }
@@ -431,7 +449,7 @@ int qmm_mv_q4kt_q8(int mode, int64_t k, int64_t n, int64_t tokens, int accumulat
 
 
 int qmm_dequant_q4kt(const void *w, int64_t rows, int64_t k, float *out, hipStream_t s) {
-  if (rows % 16 || k % 512) return QMM_ERR_SHAPE;
+  if (rows % 16 || k % 256) return QMM_ERR_SHAPE;
   if (!aligned(w, 4)) return QMM_ERR_ALIGN;
   const int64_t groups = rows * (k / 32);
   dequant_q4kt_kernel<<<(unsigned)((groups + 255) / 256), 256, 0, s>>>(static_cast<const u8 *>(w), rows, k, out);
@@ -440,9 +458,9 @@ int qmm_dequant_q4kt(const void *w, int64_t rows, int64_t k, float *out, hipStre
 
 extern "C" int qmm_tile_q4k(const void *w, int64_t rows, int64_t k, void *w_t, qmm_stream_t stream) {
   if (!w || !w_t) return QMM_ERR_NULL;
-  if (rows <= 0 || rows % 16 || k <= 0 || k % 512 || k > (1 << 20)) return QMM_ERR_SHAPE;
+  if (rows <= 0 || rows % 16 || k <= 0 || k % 256 || k > (1 << 20)) return QMM_ERR_SHAPE;
   if (!aligned(w, 16) || !aligned(w_t, 16)) return QMM_ERR_ALIGN;
-  const int64_t pieces = rows / 16 * (k / 512) * (kUnit / 16);
+  const int64_t pieces = rows * (k / 256) * 9;   // 16-byte pieces: 144 bytes a super-block
   tile_q4k_kernel<<<(unsigned)((pieces + 255) / 256), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
       static_cast<const u8 *>(w), rows, k, static_cast<u8 *>(w_t));
   return launch_status();

@@ -7,8 +7,8 @@
 //                    t = rowmap[r] / KU
 //   dn   ys[r, c]  = sum_k A8[r, k] Wd[e][c, k] + bd[e, c]                             (rows already sorted)
 //
-// for every row r of every 64-row tile with expert e = tile_info[tile, 0] >= 0 (rows with rowmap[r] < 0 are written
-// as zeros); the expert biases are optional (gpt-oss, S/gen_moe.py:958-1007). W is MXFP4 in split planes: nibbles [E, rows, K/2] ("pairs": byte j holds elements 2j, 2j+1) and
+// for every row r of every 64-row tile with expert e = tile_info[tile, 0] >= 0 (rows with rowmap[r] < 0 are not
+// written; the MXFP8 output of the fused gate/up writes them as codes 0, scale 0); the expert biases are optional (gpt-oss, S/gen_moe.py:958-1007). W is MXFP4 in split planes: nibbles [E, rows, K/2] ("pairs": byte j holds elements 2j, 2j+1) and
 // E8M0 scales [E, rows, K/32]. X8 / A8 are MXFP8 activations from qmm_quant_mxfp8: E4M3 codes [rows, K] with one
 // E8M0 scale per 32 values along K. fp32 accumulation.
 //
@@ -479,11 +479,10 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int lr = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-      float v = 0.f;
-      if (src_row[lr] >= 0) {
-        if constexpr (GU) v = act_fn(a.act, acc[i][0][r] + bg, acc[i][1][r] + bu);
-        else v = acc[i][0][r] + bg;
-      }
+      if (src_row[lr] < 0) continue;   // a row without an assignment is not written
+      float v;
+      if constexpr (GU) v = act_fn(a.act, acc[i][0][r] + bg, acc[i][1][r] + bu);
+      else v = acc[i][0][r] + bg;
       __builtin_nontemporal_store(v, a.y + (int64_t)(m0 + lr) * N + col);
     }
 }

@@ -77,13 +77,15 @@ int check_chain(int fmt, int fmt_down, int flags, int E, int KU, int64_t T, int6
   if (flags & ~QMM_MOE_Q8) return QMM_ERR_RANGE;
   if (T <= 0 || T > 65536 || H <= 0 || FE <= 0 || H > (1 << 20) || FE > (1 << 20)) return QMM_ERR_SHAPE;
   const bool prefill = T >= kMinPrefillTokens;
-  if (prefill) {
-    if (gguf_blocks(fmt) && gguf_blocks(fmt_down)) return QMM_OK;
+  if (prefill) {   // the tiled Q4_K layout: the grouped GEMMs read it (prefill only, like the MXFP4 tiled planes)
+    const bool g = gguf_blocks(fmt) || fmt == QMM_Q4_KT, d = gguf_blocks(fmt_down) || fmt_down == QMM_Q4_KT;
+    if (g && d) return QMM_OK;
     if (mx_planes(fmt) && fmt_down == fmt) return QMM_OK;
     return QMM_ERR_FORMAT;
   }
   if (flags & QMM_MOE_Q8) return gguf_blocks(fmt) && gguf_blocks(fmt_down) ? QMM_OK : QMM_ERR_FORMAT;
-  if (fmt == QMM_MXFP4T || fmt_down == QMM_MXFP4T) return QMM_ERR_FORMAT;   // the matvecs read split planes
+  if (fmt == QMM_MXFP4T || fmt_down == QMM_MXFP4T || fmt == QMM_Q4_KT || fmt_down == QMM_Q4_KT)
+    return QMM_ERR_FORMAT;   // the expert matvecs read GGUF blocks / split planes
   if ((fmt == QMM_MXFP4S) != (fmt_down == QMM_MXFP4S)) return QMM_ERR_FORMAT;
   return QMM_OK;
 }

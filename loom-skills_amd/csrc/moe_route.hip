@@ -365,7 +365,7 @@ __global__ __launch_bounds__(256) void row_scale_kernel(int64_t rows, int64_t k,
                                                         const int32_t *__restrict__ tile_info,
                                                         const int32_t *__restrict__ info) {
   const int64_t r = blockIdx.x;
-  if (tile_info && tile_info[2 * (r / kTile)] < 0) return;
+  if (tile_info && (tile_info[2 * (r / kTile)] < 0 || r % kTile >= tile_info[2 * (r / kTile) + 1])) return;
   if (pad_row(info, r, k, scales, x16)) return;
   __shared__ float wmax[4];
   float m = 0.f;
@@ -412,7 +412,7 @@ __global__ __launch_bounds__(256) void row_scale_vec_kernel(int64_t rows, int64_
                                                             const int32_t *__restrict__ tile_info,
                                                             const int32_t *__restrict__ info) {
   const int64_t r = blockIdx.x;
-  if (tile_info && tile_info[2 * (r / kTile)] < 0) return;
+  if (tile_info && (tile_info[2 * (r / kTile)] < 0 || r % kTile >= tile_info[2 * (r / kTile) + 1])) return;
   if (pad_row(info, r, k, scales, x16)) return;
   __shared__ float wmax[4];
   const int64_t nch = k / 8, base = r * nch;

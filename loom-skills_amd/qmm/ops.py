@@ -422,7 +422,8 @@ def repack_mxfp4(w, rows, k):
 
 def tile_q4k(w, rows, k):
     """GGUF Q4_K rows (uint8, rows * k / 256 * 144 bytes) -> the tiled layout (format "q4_kt") the int8-activation
-    decode GEMV streams contiguously. rows % 16 == 0, k % 512 == 0; a byte permutation of the same size."""
+    decode GEMV and the grouped expert GEMMs stream contiguously. rows % 16 == 0, k % 256 == 0 (the GEMV takes
+    k % 512 == 0); a byte permutation of the same size. Expert tensors [E, n, k] tile as E * n rows (n % 16 == 0)."""
     _dev(w)
     w_t = torch.empty(rows * row_bytes("q4_k", k), dtype=torch.uint8, device=w.device)
     _lib.call("qmm_tile_q4k", _ptr(w), rows, k, _ptr(w_t), _stream())
@@ -467,7 +468,8 @@ def moe_prefill(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up
                 down_scale=None, y=None, sg=None, fmt_down=None):
     """The reference's prefill MoE chain (moe_routed with t >= 64, S/gen_llm.py:5324-5385): route, bucket into
     64-row expert tiles, grouped gate/up GEMM with the activation, grouped down GEMM, combine.
-    q4_k: activations row-scaled to f16 (g_row_scale_f16[_tiles]); mxfp4s / mxfp4t: quantized to MXFP8.
+    q4_k / q4_kt (tiled, tile_q4k) / q6_k / q4_0: activations row-scaled to f16 (g_row_scale_f16[_tiles]); mxfp4s /
+    mxfp4t: quantized to MXFP8.
     x bf16 / f32 [T, H]; logits f32 [T, E], or None with router (the weight f32 / bf16 [E, H]); expert_bias
     (bg [E, FE], bu [E, FE], bd [E, H]) or None; down_scale f32 [E] or None; y: None (y = routed output), or the
     shared experts' output the routed output is added to (scaled first by sg, the shared gate, when given);
@@ -481,7 +483,7 @@ def moe_prefill(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up
     ids, wts, logits = _route(x, logits, KU, gating, norm, scale, bias, router, down_scale)
     bg, bu, bd = expert_bias if expert_bias is not None else (None, None, None)
     tile_info, rowmap, pos = moe_bucket(ids, E)
-    if fmt in ("q4_k", "q6_k", "q4_0"):
+    if fmt in ("q4_k", "q4_kt", "q6_k", "q4_0"):
         x16, xs = row_scale_f16(x)
         a = moe_grouped(fmt, "gu", tile_info, rowmap, x16, w_gate, FE, H, E, KU, w2=w_up, x_scales=xs,
                         fused=fused, act=act, bias=bg, bias2=bu)

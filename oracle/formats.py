@@ -183,18 +183,21 @@ def dequant_mxfp4t(nib_t, sc_t, rows, k):
 
 
 def q4_k_to_tiled(raw, rows, k):
-    """GGUF Q4_K rows -> the lane-ordered tiled layout of the decode GEMV, written from the layout's definition:
-    units of 16 rows x 512 values (two super-blocks a row), ordered (row block, slice), 4608 bytes each: the 32
-    16-byte headers ([f16 d][f16 dmin][12 scale bytes]) of super-block sb of row r at 16 (2 r + sb), then four
-    1 KB code planes, plane q holding at 16 l (l = 4 r + 2 sb + h) code bytes 16 (4 h + q) .. +16 of that super-block.
-    rows % 16 == 0, k % 512 == 0."""
-    assert rows % 16 == 0 and k % 512 == 0, (rows, k)
+    """GGUF Q4_K rows -> the lane-ordered tiled layout of the decode GEMV and the grouped expert GEMMs, written from
+    the layout's definition. Each block of 16 rows keeps its 16 x k / 256 super-blocks in its own byte range, cut
+    into units of 512 values (two super-blocks a row), 4608 bytes each: the 32 16-byte headers ([f16 d][f16 dmin]
+    [12 scale bytes]) of super-block sb of row r at 16 (2 r + sb), then four 1 KB code planes, plane q holding at
+    16 l (l = 4 r + 2 sb + h) code bytes 16 (4 h + q) .. +16 of that super-block. When k % 512 == 256 the row
+    block ends in a half unit of 2304 bytes (its last super-block of each row): the 16 headers at 16 r, then four
+    512-byte planes, plane q holding at 16 (2 r + h) code bytes 16 (4 h + q) .. +16. rows % 16 == 0, k % 256 == 0."""
+    assert rows % 16 == 0 and k % 256 == 0, (rows, k)
     b = _blocks(raw, "q4_k").reshape(rows, k // 256, 144)
-    S = k // 512
+    F, half = k // 512, (k // 256) % 2
+    rbb = 16 * (k // 256) * 144
     out = np.empty(rows * k // 256 * 144, np.uint8)
     for rb in range(rows // 16):
-        for sl in range(S):
-            u = (rb * S + sl) * 4608
+        for sl in range(F):
+            u = rb * rbb + sl * 4608
             for r in range(16):
                 for sb in range(2):
                     blk = b[16 * rb + r, 2 * sl + sb]
@@ -205,18 +208,37 @@ def q4_k_to_tiled(raw, rows, k):
                             o = u + 512 + 1024 * q + 16 * lane
                             c = 16 + 16 * (4 * h + q)
                             out[o: o + 16] = blk[c: c + 16]
+        if half:
+            u = rb * rbb + F * 4608
+            for r in range(16):
+                blk = b[16 * rb + r, 2 * F]
+                out[u + 16 * r: u + 16 * r + 16] = blk[0:16]
+                for h in range(2):
+                    for q in range(4):
+                        o = u + 256 + 512 * q + 16 * (2 * r + h)
+                        c = 16 + 16 * (4 * h + q)
+                        out[o: o + 16] = blk[c: c + 16]
     return out
 
 
 def q4_kt_to_gguf(raw_t, rows, k):
     """Inverse of q4_k_to_tiled (vectorized: an independent construction by index arithmetic)."""
-    S = k // 512
-    t = np.asarray(raw_t).view(np.uint8).reshape(rows // 16, S, 4608)
-    hdr = t[:, :, :512].reshape(rows // 16, S, 16, 2, 16)                   # [rb, sl, r, sb, 16]
-    codes = t[:, :, 512:].reshape(rows // 16, S, 4, 16, 2, 2, 16)           # [rb, sl, q, r, sb, h, 16]
-    codes = codes.transpose(0, 1, 3, 4, 5, 2, 6).reshape(rows // 16, S, 16, 2, 128)   # [rb, sl, r, sb, (h q 16)]
+    F, half = k // 512, (k // 256) % 2
+    rbb = 16 * (k // 256) * 144
+    t = np.asarray(raw_t).view(np.uint8).reshape(rows // 16, rbb)
+    full = t[:, :F * 4608].reshape(rows // 16, F, 4608)
+    hdr = full[:, :, :512].reshape(rows // 16, F, 16, 2, 16)                  # [rb, sl, r, sb, 16]
+    codes = full[:, :, 512:].reshape(rows // 16, F, 4, 16, 2, 2, 16)          # [rb, sl, q, r, sb, h, 16]
+    codes = codes.transpose(0, 1, 3, 4, 5, 2, 6).reshape(rows // 16, F, 16, 2, 128)   # [rb, sl, r, sb, (h q 16)]
     blk = np.concatenate([hdr, codes], axis=-1)                               # [rb, sl, r, sb, 144]
-    return np.ascontiguousarray(blk.transpose(0, 2, 1, 3, 4)).reshape(-1)    # rows in order, super-blocks in order
+    blk = blk.transpose(0, 2, 1, 3, 4).reshape(rows // 16, 16, 2 * F, 144)    # [rb, r, super-block, 144]
+    if half:
+        tail = t[:, F * 4608:]
+        th = tail[:, :256].reshape(rows // 16, 16, 1, 16)                     # [rb, r, -, 16]
+        tc = tail[:, 256:].reshape(rows // 16, 4, 16, 2, 16)                  # [rb, q, r, h, 16]
+        tc = tc.transpose(0, 2, 3, 1, 4).reshape(rows // 16, 16, 1, 128)      # [rb, r, -, (h q 16)]
+        blk = np.concatenate([blk, np.concatenate([th, tc], axis=-1)], axis=2)
+    return np.ascontiguousarray(blk).reshape(-1)    # rows in order, super-blocks in order
 
 
 def q6_k_fields(raw):

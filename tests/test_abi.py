@@ -115,14 +115,15 @@ def test_argument_validation_without_a_device(lib):
     assert lib.qmm_repack_mxfp4(fake, 4, 48, fake, fake, n) == st["QMM_ERR_SHAPE"]
     # MFMA-tiled planes: whole 32-row blocks and 64-value chunks; no GEMV or decode matvec reads them
     assert lib.qmm_tile_mxfp4(fake, fake, 48, 64, fake, fake, n) == st["QMM_ERR_SHAPE"]
-    # tiled Q4_K: whole 16-row blocks and 512-value slices; at most 4 slices a wave of at most 8 waves
+    # tiled Q4_K: whole 16-row blocks and super-blocks (the GEMV: 512-value slices, at most 4 a wave of at most 8
+    # waves); the grouped GEMMs read it up to K = 4096
     assert lib.qmm_tile_q4k(fake, 24, 512, fake, n) == st["QMM_ERR_SHAPE"]
-    assert lib.qmm_tile_q4k(fake, 16, 768, fake, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_tile_q4k(fake, 16, 640, fake, n) == st["QMM_ERR_SHAPE"]
     assert lib.qmm_tile_q4k(fake, 16, 512, n, n) == st["QMM_ERR_NULL"]
     assert lib.qmm_mv_q8(5, 4096, 24, 1, 0, fake, 2, fake, fake, n) == st["QMM_ERR_SHAPE"]     # n % 16
     assert lib.qmm_mv_q8(5, 768, 16, 1, 0, fake, 2, fake, fake, n) == st["QMM_ERR_SHAPE"]      # K % 512
     assert lib.qmm_mv_q8(5, 512 * 37, 16, 1, 0, fake, 2, fake, fake, n) == st["QMM_ERR_SHAPE"]  # 37 slices
-    assert lib.qmm_dequant(5, fake, n, 16, 768, fake, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_dequant(5, fake, n, 16, 640, fake, n) == st["QMM_ERR_SHAPE"]
     assert lib.qmm_tile_mxfp4(fake, fake, 32, 96, fake, fake, n) == st["QMM_ERR_SHAPE"]
     assert lib.qmm_tile_mxfp4(fake, n, 32, 64, fake, fake, n) == st["QMM_ERR_NULL"]
     assert lib.qmm_dequant(4, fake, fake, 48, 64, fake, n) == st["QMM_ERR_SHAPE"]

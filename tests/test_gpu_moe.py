@@ -57,7 +57,7 @@ class Experts:
 
     def device(self, split, tiled=False):
         """kwargs of ops.moe_prefill / moe_decode; split: MXFP4 as split planes (repacked on the device); tiled:
-        then tiled for the grouped GEMM (format mxfp4t)."""
+        then tiled for the grouped GEMM (format mxfp4t), or Q4_K tiled (format q4_kt)."""
         ops = _ops()
         dv = lambda a: dev_u8(a, self.dev)
         if self.fmt == "q4_k" or not split:
@@ -65,6 +65,12 @@ class Experts:
             kw = dict(w_gate=dv(self.gu if self.fused else self.g), w_down=dv(self.d))
             if not self.fused:
                 kw["w_up"] = dv(self.u)
+            if fmt == "q4_k" and tiled:   # the tiled layout, each tensor tiled as [E n, k]
+                E, H, FE = self.E, self.H, self.FE
+                rows = {"w_gate": E * FE * (2 if self.fused else 1), "w_up": E * FE, "w_down": E * H}
+                for m in list(kw):
+                    kw[m] = ops.tile_q4k(kw[m], rows[m], FE if m == "w_down" else H)
+                fmt = "q4_kt"
             return fmt, kw
         E, H, FE = self.E, self.H, self.FE
         if self.fused:
@@ -179,7 +185,8 @@ def test_moe_prefill_small_shapes_heavy_expert(dev, fmt, fused, act, tiled):
 
 def test_grouped_gemm_alone_hand_made_tiles(dev):
     """dn mode on a hand-made tile table (make_kernel_tests.py:3423-3500): tiles of 64, 37, 0 (expert -1) and 5
-    rows on experts 0, E/2, -1, E-1; row groups scaled by 0.05, 1 and 20; dead rows must come out as zeros."""
+    rows on experts 0, E/2, -1, E-1; row groups scaled by 0.05, 1 and 20; dead rows and unused tiles must be left
+    as they were (a NaN sentinel)."""
     import torch
     from qmm import synth
     ops = _ops()
@@ -195,17 +202,19 @@ def test_grouped_gemm_alone_hand_made_tiles(dev):
     a = rng.standard_normal((n_tiles * 64, FE)).astype(np.float32)
     a *= np.repeat([0.05, 1.0, 20.0, 1.0], 64)[:, None].astype(np.float32)
     a16, sc = ops.row_scale_f16(dev_f32(a, dev))
+    y0 = torch.full((n_tiles * 64, H), float("nan"), dtype=torch.float32, device=dev)
     ys = host(ops.moe_grouped("q4_k", "dn", torch.from_numpy(tile_info).to(dev), torch.from_numpy(rowmap).to(dev),
-                              a16, dev_u8(wd, dev), H, FE, E, 1, x_scales=sc))
+                              a16, dev_u8(wd, dev), H, FE, E, 1, x_scales=sc, y=y0))
     ar = ref.f16_rows(a)
     for t, (e, rows) in enumerate(tiles):
         blk = ys[64 * t: 64 * t + 64]
         if e < 0:
-            continue                            # unused tiles are not written
+            assert np.all(np.isnan(blk)), f"unused tile {t} was written"
+            continue
         Wd = of.dequant_q4_k(wd[e * H * (FE // 256 * 144):(e + 1) * H * (FE // 256 * 144)], H, FE)
         want = ar[64 * t: 64 * t + rows] @ Wd.T
         assert_close_rel_l2(blk[:rows], want, 1e-3, f"tile {t}")
-        assert np.all(blk[rows:] == 0), f"dead rows of tile {t} are not zero"
+        assert np.all(np.isnan(blk[rows:])), f"dead rows of tile {t} were written"
 
 
 def test_quant_mxfp8_matches_oracle(dev):
@@ -272,8 +281,8 @@ def test_tile_mxfp4_bit_exact(dev):
                                             (100, 8, 512, 320, True)])
 def test_grouped_gate_up_mxfp8_output_equals_quantized_act(dev, T, E, H, FE, tiled):
     """The gate/up GEMM with the MXFP8 quantization fused into its epilogue writes exactly the codes and scales
-    quant_mxfp8 makes of the f32 activation the plain gate/up GEMM writes (every row of every live tile, dead rows
-    as zeros)."""
+    quant_mxfp8 makes of the f32 activation the plain gate/up GEMM writes (every live row; the fused epilogue
+    writes dead rows of live tiles as zeros)."""
     import torch
     from qmm import synth
     ops = _ops()
@@ -294,8 +303,9 @@ def test_grouped_gate_up_mxfp8_output_equals_quantized_act(dev, T, E, H, FE, til
     torch.cuda.synchronize()
     used = np.repeat(host(ti)[:, 0] >= 0, 64)
     dead = used & (host(rm) < 0)
-    np.testing.assert_array_equal(host(c)[used], host(ec)[used])
-    np.testing.assert_array_equal(host(s)[used], host(es)[used])
+    live = used & ~dead   # the plain GEMM leaves dead rows unwritten; the fused one writes them as zeros
+    np.testing.assert_array_equal(host(c)[live], host(ec)[live])
+    np.testing.assert_array_equal(host(s)[live], host(es)[live])
     assert np.all(host(c)[dead] == 0) and np.all(host(s)[dead] == 0)
     assert np.any(host(c)[used & ~dead] != 0)
 

@@ -147,7 +147,7 @@ def test_tile_q4k_bit_exact(dev):
     import torch
     ops = _ops()
     rng = np.random.default_rng(61)
-    for n, k in ((32, 4096), (48, 1536)):
+    for n, k in ((32, 4096), (48, 1536), (32, 768), (16, 256)):   # 768, 256: a trailing half unit
         w = _weights("q4_k", rng, n, k)
         wt = ops.tile_q4k(dev_u8(w, dev), n, k)
         np.testing.assert_array_equal(host(wt), of.q4_k_to_tiled(w, n, k))

@@ -415,22 +415,29 @@ def test_mxfp4t_lane_half_swap_negative_control():
 
 
 # ------------------------------------------------------------------------------------------- Q4_K tiled layout
-def test_q4_kt_byte_addresses_follow_the_layout_definition():
+@pytest.mark.parametrize("k", [1536, 1280, 256])
+def test_q4_kt_byte_addresses_follow_the_layout_definition(k):
     """Every byte of every GGUF Q4_K block lands where the tiled layout puts it, computed as a flat offset: for row
-    r, super-block b and byte j of its 144, unit u = (r // 16) * (K / 512) + b // 2, sb = b % 2, i = r % 16;
-    header byte j < 16 -> 4608 u + 16 (2 i + sb) + j; code byte c = j - 16 -> 4608 u + 512 + 1024 ((c // 16) % 4)
-    + 16 (4 i + 2 sb + c // 64) + c % 16."""
+    r, super-block b and byte j of its 144, row block base B = (r // 16) 16 (K / 256) 144, i = r % 16; in a full
+    unit (b < 2 (K // 512)): u = b // 2, sb = b % 2, header byte j < 16 -> B + 4608 u + 16 (2 i + sb) + j, code
+    byte c = j - 16 -> B + 4608 u + 512 + 1024 ((c // 16) % 4) + 16 (4 i + 2 sb + c // 64) + c % 16; in the half
+    unit of K % 512 == 256 (the last super-block): header -> B + 4608 F + 16 i + j, code -> B + 4608 F + 256
+    + 512 ((c // 16) % 4) + 16 (2 i + c // 64) + c % 16 (F = K // 512)."""
     from qmm import synth
     rng = np.random.default_rng(21)
-    rows, k = 32, 1536
+    rows = 32
     raw = synth.q4_k_weights(rng, rows, k).reshape(rows, k // 256, 144)
     t = of.q4_k_to_tiled(raw, rows, k)
     assert t.size == raw.size
     r, b, j = np.meshgrid(np.arange(rows), np.arange(k // 256), np.arange(144), indexing="ij")
-    u = (r // 16) * (k // 512) + b // 2
-    sb, i, c = b % 2, r % 16, j - 16
-    off = np.where(j < 16, 4608 * u + 16 * (2 * i + sb) + j,
-                   4608 * u + 512 + 1024 * ((c // 16) % 4) + 16 * (4 * i + 2 * sb + c // 64) + c % 16)
+    F = k // 512
+    B = (r // 16) * 16 * (k // 256) * 144
+    u, sb, i, c = b // 2, b % 2, r % 16, j - 16
+    full = np.where(j < 16, B + 4608 * u + 16 * (2 * i + sb) + j,
+                    B + 4608 * u + 512 + 1024 * ((c // 16) % 4) + 16 * (4 * i + 2 * sb + c // 64) + c % 16)
+    tail = np.where(j < 16, B + 4608 * F + 16 * i + j,
+                    B + 4608 * F + 256 + 512 * ((c // 16) % 4) + 16 * (2 * i + c // 64) + c % 16)
+    off = np.where(b < 2 * F, full, tail)
     assert np.array_equal(np.sort(off.ravel()), np.arange(raw.size))    # a permutation
     assert np.array_equal(t[off], raw)
 
@@ -438,7 +445,7 @@ def test_q4_kt_byte_addresses_follow_the_layout_definition():
 def test_q4_kt_round_trip_and_values():
     from qmm import synth
     rng = np.random.default_rng(22)
-    for rows, k in ((16, 512), (48, 4096)):
+    for rows, k in ((16, 512), (48, 4096), (32, 768), (16, 256)):
         raw = synth.q4_k_weights(rng, rows, k)
         t = of.q4_k_to_tiled(raw, rows, k)
         assert np.array_equal(of.q4_kt_to_gguf(t, rows, k), np.asarray(raw).reshape(-1))
