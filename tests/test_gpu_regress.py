@@ -26,6 +26,7 @@ def test_split_grouped_gemms_k4096_then_k8192_in_one_process(dev):
     rng = np.random.default_rng(90)
     ids = torch.from_numpy(np.array([[0], [1]] * (T // 2), np.int32)).to(dev)
     ti, rm, _ = ops.moe_bucket(ids, E)
+    live = host(rm) >= 0   # rows without an assignment are not written by the grouped GEMMs
     for K in (4096, 8192):
         x = rng.standard_normal((T, K)).astype(np.float32)
         x8, xs = ops.quant_mxfp8(torch.from_numpy(x).to(dev))
@@ -38,13 +39,13 @@ def test_split_grouped_gemms_k4096_then_k8192_in_one_process(dev):
         dt, dst = ops.tile_mxfp4(dnn, dns, E * small, K)
         a_s = ops.moe_grouped("mxfp4s", "gu", ti, rm, x8, gn, small, K, E, KU, ws=gs, x_scales=xs, fused=True)
         a_t = ops.moe_grouped("mxfp4t", "gu", ti, rm, x8, gt, small, K, E, KU, ws=gst, x_scales=xs, fused=True)
-        assert_bits_equal(host(a_s), host(a_t), f"gu K={K}")
+        assert_bits_equal(host(a_s)[live], host(a_t)[live], f"gu K={K}")
         rows = ti.shape[0] * 64
         xd = rng.standard_normal((rows, K)).astype(np.float32)
         d8, ds8 = ops.quant_mxfp8(torch.from_numpy(xd).to(dev))
         y_s = ops.moe_grouped("mxfp4s", "dn", ti, rm, d8, dnn, small, K, E, KU, ws=dns, x_scales=ds8)
         y_t = ops.moe_grouped("mxfp4t", "dn", ti, rm, d8, dt, small, K, E, KU, ws=dst, x_scales=ds8)
-        assert_bits_equal(host(y_s), host(y_t), f"dn K={K}")
+        assert_bits_equal(host(y_s)[live], host(y_t)[live], f"dn K={K}")
         # and the oracle on one expert's rows: the first live tile row of expert 0
         W = of.dequant_mxfp4(gu[:small * of.row_bytes("mxfp4", K)], small, K)
         r0 = int(host(rm)[0])
