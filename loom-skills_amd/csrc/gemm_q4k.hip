@@ -520,6 +520,10 @@ int fmt_align(int fmt) { return fmt == QMM_Q4_K || fmt == QMM_Q4_KT ? 16 : fmt =
 
 }  // namespace
 
+// the dense Q4_K GEMM (gemm_dense.hip): store / acc modes
+int qmm_gemm_q4k_dense(int acc, int64_t rows, int64_t k, int64_t n, const void *x, const float *scales, const void *w,
+                       void *y, int y_bf16, hipStream_t s);
+
 extern "C" int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, const void *x, int x_dtype,
                         const float *scales, const void *w, const void *w2, void *y, int y_dtype,
                         qmm_stream_t stream) {
@@ -544,6 +548,7 @@ extern "C" int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, c
     a.tiles_total = a.tiles_m * (int)((n + 63) / 64);
     return bf ? launch_fmt<kSwiglu, false, true>(fmt, a, s) : launch_fmt<kSwiglu, false, false>(fmt, a, s);
   }
+  if (fmt == QMM_Q4_K) return qmm_gemm_q4k_dense(acc, rows, k, n, x, scales, w, y, bf, s);
   a.tiles_total = a.tiles_m * (int)((n + 127) / 128);
   if (acc && bf) return launch_fmt<kDense, true, true>(fmt, a, s);
   if (acc) return launch_fmt<kDense, true, false>(fmt, a, s);

@@ -49,6 +49,32 @@ def test_gemm_f32_out(dev, M, N, K):
     _check(y, want, f"gemm {M}x{N}x{K}")
 
 
+def test_q4_k_staging_one_hot_rows(dev):
+    """With one-hot f16 rows (the identity) and no row scale, y[r, c] is the f16-staged weight W16[c, r] exactly
+    (fp32 accumulation of a single product). The staging must be the reference's fma_f16(f16(q), f16(d sc),
+    f16(-dmin m)) with one rounding (S/gen_gemm.py:499-530), restated here in float64 and rounded once to f16; a
+    staging with two roundings (f16(q d sc), then + f16(-dmin m)) differs on this data (the negative control)."""
+    import torch
+    import qmm.ops as ops
+    from qmm import synth
+    N, K = 256, 1024
+    rng = np.random.default_rng(77)
+    w = synth.q4_k_weights(rng, N, K)
+    d, dmin, sc, m, q = of.q4_k_fields(w)
+    dsc = (d[:, None] * sc.astype(np.float32)).astype(np.float16).astype(np.float64)
+    nmn = (-(dmin[:, None] * m.astype(np.float32))).astype(np.float16).astype(np.float64)
+    one = (q.astype(np.float64) * dsc[:, :, None] + nmn[:, :, None]).astype(np.float16)
+    want = one.astype(np.float32).reshape(N, K).T + np.float32(0.0)   # y[r, c] = W16[c, r]; -0 accumulates to +0
+    eye = torch.eye(K, dtype=torch.float16, device=dev)
+    got = host(ops.gemm("q4_k", "store", eye, dev_u8(w, dev), N, K))
+    bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
+    assert bad.size == 0, f"{bad.size} staged values differ, first at {bad[:5]}: {got.ravel()[bad[:5]]} vs " \
+                          f"{want.ravel()[bad[:5]]}"
+    two = ((q.astype(np.float64) * dsc[:, :, None]).astype(np.float16).astype(np.float64)
+           + nmn[:, :, None]).astype(np.float16)
+    assert not np.array_equal(two, one), "the negative control does not separate one rounding from two"
+
+
 def test_gemm_bf16_out_workload_shape(dev):
     """The Q4_K prefill workload: bf16 x [512, 4096], W [4096, 4096], bf16 out. The fp32 accumulation meets the
     rel-L2 bar (f32 store); the bf16 store is exactly that result rounded to nearest even, so its distance to the
