@@ -206,7 +206,7 @@ class GemmWorkload:
 
     def __init__(self, m):
         self.m, self.n, self.k = m or 512, 4096, 4096
-        self.traffic_name = f"q4k_mfma_kernel_dense.q4_k_gemm_m{self.m}_n4096_k4096"
+        self.traffic_name = f"q4k_dense_kernel.q4_k_gemm_m{self.m}_n4096_k4096"
 
     def setup(self, dev):
         import torch
@@ -237,6 +237,18 @@ class GemmWorkload:
 
     def alg_flops(self):
         return 2 * self.m * self.n * self.k
+
+    def library_setup(self, dev):
+        """Context, not a baseline of this path: the same GEMM shape with plain f16 weights through torch.matmul
+        (hipBLASLt), two weight copies in turn."""
+        import torch
+        g = torch.Generator(device=dev).manual_seed(0)
+        self.lib_b = [torch.randn((self.n, self.k), generator=g, device=dev, dtype=torch.float16) for _ in range(2)]
+        self.lib_y = torch.empty((self.m, self.n), dtype=torch.float16, device=dev)
+
+    def library_step(self, i):
+        import torch
+        torch.matmul(self.x16, self.lib_b[i % 2].t(), out=self.lib_y)
 
     def value(self, sec):
         return self.alg_flops() / sec / 1e12
@@ -601,9 +613,21 @@ def measure(wl, args, cpu_budget):
         # the scaled MFMA runs E4M3 x E2M1 at the FP8 rate; the MXFP4 figure is the fraction of the FP4 peak
         res["chain_frac_fp4_peak"] = round(res["tflops"] / MFMA_PEAK_TFLOPS["fp4"], 4)
         res["chain_frac_fp8_rate"] = round(res["tflops"] / MFMA_PEAK_TFLOPS["fp8"], 4)
+    if hasattr(wl, "library_step"):
+        wl.library_setup(torch_device())
+        lib_s = kernel_time(wl.library_step, args.steps, args.warmup) / 1e3
+        lib_tf = wl.alg_flops() / lib_s / 1e12
+        res["library_f16_gemm"] = {"what": "torch.matmul of the same shape, f16 x f16 (hipBLASLt), no dequantization",
+                                   "us": round(lib_s * 1e6, 3), "tflops": round(lib_tf, 3),
+                                   "frac": round(lib_tf / MFMA_PEAK_TFLOPS["fp16"], 4)}
     if cpu_budget:
         res["cpu_baseline"] = wl.cpu_baseline(cpu_budget)
     return res
+
+
+def torch_device():
+    import torch
+    return torch.device("cuda:0")
 
 
 def secondary_entry(name, m, wl, res):
@@ -614,6 +638,8 @@ def secondary_entry(name, m, wl, res):
            "roofline": {k: r[k] for k in ("bound", "achieved", "unit", "frac", "traffic", "kernel", "avg_launch_us")}}
     if "chain_frac_fp4_peak" in res:
         out["chain_frac_fp4_peak"] = res["chain_frac_fp4_peak"]
+    if "library_f16_gemm" in res:
+        out["library_f16_gemm"] = res["library_f16_gemm"]
     if "cpu_baseline" in res:
         c = res["cpu_baseline"]
         out["cpu"] = {k: c[k] for k in ("value", "unit", "cores", "dequant_ms", "matmul_ms", "total_ms") if k in c}

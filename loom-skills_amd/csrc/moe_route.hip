@@ -385,10 +385,8 @@ __global__ __launch_bounds__(256) void row_scale_kernel(int64_t rows, int64_t k,
   }
 }
 
-// The same with 16-byte accesses: thread c of the row handles 8 consecutive values, holding up to kRsChunks such
-// chunks in registers between the row maximum and the conversion (rows of up to 256 x 8 x kRsChunks values; the
-// host takes the scalar kernel above for wider, misaligned or k % 8 != 0 rows).
-constexpr int kRsChunks = 4;
+// 16-byte accesses for the wave-per-row kernel below
+constexpr int kRsMaxChunks = 16;   // 8-value chunks a lane: rows of up to 64 x 8 x 16 = 8192 values
 typedef __attribute__((ext_vector_type(4))) u32 v4u;
 
 template <bool BF>
@@ -406,21 +404,37 @@ __device__ __forceinline__ void load8(const void *x, int64_t i8, float (&v)[8]) 
   }
 }
 
-template <bool BF>
-__global__ __launch_bounds__(256) void row_scale_vec_kernel(int64_t rows, int64_t k, const void *__restrict__ x,
-                                                            float *__restrict__ scales, _Float16 *__restrict__ x16,
-                                                            const int32_t *__restrict__ tile_info,
-                                                            const int32_t *__restrict__ info) {
-  const int64_t r = blockIdx.x;
+// One wave per row (four rows a workgroup): lane l handles the 8-value chunks l, l + 64, ... (NCH of them at most,
+// held in registers between the row maximum and the conversion); the maximum is a wave butterfly, so the row needs no
+// workgroup barrier or LDS. Rows up to 64 x 8 x NCH values; the host takes the scalar kernel above for wider,
+// misaligned or k % 8 != 0 rows.
+template <bool BF, int NCH>
+__global__ __launch_bounds__(256) void row_scale_wave_kernel(int64_t rows, int64_t k, const void *__restrict__ x,
+                                                             float *__restrict__ scales, _Float16 *__restrict__ x16,
+                                                             const int32_t *__restrict__ tile_info,
+                                                             const int32_t *__restrict__ info) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
   if (tile_info && (tile_info[2 * (r / kTile)] < 0 || r % kTile >= tile_info[2 * (r / kTile) + 1])) return;
-  if (pad_row(info, r, k, scales, x16)) return;
-  __shared__ float wmax[4];
   const int64_t nch = k / 8, base = r * nch;
-  float v[kRsChunks][8];
+  if (info && info[4 * r + 2] == 0) {   // a padding row of the epoch: zero values, scale and inverse 0
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int64_t c = lane + 64 * i;
+      if (c < nch) reinterpret_cast<v4u *>(x16)[base + c] = v4u{0u, 0u, 0u, 0u};
+    }
+    if (lane == 0) {
+      scales[2 * r] = 0.f;
+      scales[2 * r + 1] = 0.f;
+    }
+    return;
+  }
+  float v[NCH][8];
   float m = 0.f;
 #pragma unroll
-  for (int i = 0; i < kRsChunks; ++i) {
-    const int64_t c = threadIdx.x + 256 * i;
+  for (int i = 0; i < NCH; ++i) {
+    const int64_t c = lane + 64 * i;
     if (c < nch) {
       load8<BF>(x, base + c, v[i]);
 #pragma unroll
@@ -429,15 +443,12 @@ __global__ __launch_bounds__(256) void row_scale_vec_kernel(int64_t rows, int64_
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
-  __syncthreads();
-  m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
   const int biased = (int)((f32_as_u32(m) >> 23) & 255u);
   const int e = min(max(biased - 127 - 13, 0), 100);
   const float sc = u32_as_f32((u32)(127 - e) << 23), inv = u32_as_f32((u32)(127 + e) << 23);
 #pragma unroll
-  for (int i = 0; i < kRsChunks; ++i) {
-    const int64_t c = threadIdx.x + 256 * i;
+  for (int i = 0; i < NCH; ++i) {
+    const int64_t c = lane + 64 * i;
     if (c < nch) {
       u32 o[4];
 #pragma unroll
@@ -447,7 +458,7 @@ __global__ __launch_bounds__(256) void row_scale_vec_kernel(int64_t rows, int64_
       reinterpret_cast<v4u *>(x16)[base + c] = v4u{o[0], o[1], o[2], o[3]};
     }
   }
-  if (threadIdx.x == 0) {
+  if (lane == 0) {
     scales[2 * r] = sc;
     scales[2 * r + 1] = inv;
   }
@@ -638,11 +649,19 @@ static int row_scale(int64_t rows, int64_t k, const void *x, int x_dtype, float 
   if (rows <= 0 || k <= 0 || rows > (1ll << 24)) return QMM_ERR_SHAPE;
   if (tile_info && rows % kTile) return QMM_ERR_SHAPE;
   _Float16 *o = static_cast<_Float16 *>(x16);
-  if (k % 8 == 0 && k <= 8 * 256 * kRsChunks && aligned(x, 16) && aligned(x16, 16)) {
-    if (x_dtype == QMM_BF16)
-      row_scale_vec_kernel<true><<<(unsigned)rows, 256, 0, s>>>(rows, k, x, scales, o, tile_info, info);
-    else
-      row_scale_vec_kernel<false><<<(unsigned)rows, 256, 0, s>>>(rows, k, x, scales, o, tile_info, info);
+  if (k % 8 == 0 && k <= 8 * 64 * kRsMaxChunks && aligned(x, 16) && aligned(x16, 16)) {
+    const unsigned grid = (unsigned)((rows + 3) / 4);
+    const int64_t per = (k / 8 + 63) / 64;   // chunks a lane
+    const bool bf = x_dtype == QMM_BF16;
+#define QMM_RS(N)                                                                                                   \
+  (bf ? (row_scale_wave_kernel<true, N><<<grid, 256, 0, s>>>(rows, k, x, scales, o, tile_info, info), 0)          \
+      : (row_scale_wave_kernel<false, N><<<grid, 256, 0, s>>>(rows, k, x, scales, o, tile_info, info), 0))
+    if (per <= 1) QMM_RS(1);
+    else if (per <= 2) QMM_RS(2);
+    else if (per <= 4) QMM_RS(4);
+    else if (per <= 8) QMM_RS(8);
+    else QMM_RS(16);
+#undef QMM_RS
   } else {
     row_scale_kernel<<<(unsigned)rows, 256, 0, s>>>(rows, k, x, x_dtype == QMM_BF16, scales, o, tile_info, info);
   }
