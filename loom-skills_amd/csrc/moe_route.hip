@@ -21,60 +21,80 @@ constexpr int kTile = 64;
 constexpr float kNormFloor = 6.103515625e-05f;
 
 // ------------------------------------------------------------------------------------------------- top-k
-// One wave per token; lane l holds experts l, l+64, l+128, l+192. The selection is a ranking: the wave writes its
-// selection scores to LDS and every lane counts, for each of its experts, how many experts beat it (higher score,
-// ties to the lower id -- the reference's workgroup max then min-index, S/gen_moe.py:219-235); an expert of rank
-// r < KU is pick r. The score is the logit (+ bias) for gating 1 and 3 and for gating 2 without a bias: those
+// One wave per token; lane l holds experts l, l + 64, ... (NS = ceil(E / 64) slots). The selection is a ranking: the
+// wave writes each expert's selection key to LDS and every lane counts, for each of its experts, how many experts
+// beat it; an expert of rank r < KU is pick r. A key orders (score, expert) as the reference's workgroup max then
+// min-index does (S/gen_moe.py:219-235): the score's bits mapped to an order-preserving u32 (after -0 -> +0, so equal
+// scores tie) in the high word and 0xFFFFFFFF - expert in the low word, so "higher score, ties to the lower id" is one
+// unsigned 64-bit compare. The score is the logit (+ bias) for gating 1 and 3 and for gating 2 without a bias: those
 // selections are monotone in the logit, so choosing on the exact f32 logit reproduces the float64 oracle's choice.
-__device__ __forceinline__ bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+__device__ __forceinline__ uint64_t select_key(float v, int e) {
+  const u32 u = f32_as_u32(v + 0.f);
+  const u32 o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)o << 32) | (uint64_t)(0xFFFFFFFFu - (u32)e);
+}
 
 constexpr int kTopkMaxE = 256;
 
+template <int NS>
 __global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ logits, int64_t tokens, int E, int KU,
                                                    int gating, int norm, float scale, const float *__restrict__ bias,
                                                    const int32_t *__restrict__ info, int32_t *__restrict__ ids,
                                                    float *__restrict__ wts) {
-  __shared__ __align__(16) float score[4][kTopkMaxE];
+  __shared__ __align__(16) uint64_t keys[4][64 * NS];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int64_t t = (int64_t)blockIdx.x * 4 + wv;
   if (t >= tokens) return;               // a whole wave: nothing below synchronizes the workgroup
   if (info && info[4 * t + 2] == 0) return;   // a padding token of the epoch (_live): no ids, no weights
   const float *lg = logits + t * E;
-  float l[4], sel[4];
-  bool in[4];
+  float l[NS], bv[NS];
+  bool in[NS];
   const float NEG = -3.0e38f;
+  // every logit and bias load is issued before any is used (a lane past E reloads expert E - 1 and ignores it)
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < NS; ++i) {
     const int e = lane + 64 * i;
     in[i] = e < E;
-    l[i] = in[i] ? lg[e] : NEG;
-    const float b = (in[i] && bias) ? bias[e] : 0.f;
+    l[i] = lg[in[i] ? e : E - 1];
+    bv[i] = bias ? bias[in[i] ? e : E - 1] : 0.f;
+  }
+  uint64_t key[NS];
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    const int e = lane + 64 * i;
+    l[i] = in[i] ? l[i] : NEG;
+    const float b = in[i] ? bv[i] : 0.f;
     if (gating == 3) l[i] = in[i] ? l[i] + b : NEG;   // the router bias is part of the logit (gating 3)
     float sv = l[i];
     if (gating == 2 && bias) sv = in[i] ? 1.f / (1.f + expf(-l[i])) + b : NEG;
-    sel[i] = in[i] ? sv : NEG;
-    score[wv][e] = sel[i];                // experts past E hold -3e38 and lose every comparison
+    key[i] = in[i] ? select_key(sv, e) : 0ull;   // experts past E rank below every real one
+    keys[wv][e] = key[i];
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  int rank[4] = {0, 0, 0, 0};
-  const int E4 = (E + 3) & ~3;
-  for (int e2 = 0; e2 < E4; e2 += 4) {
-    const f32x4 q = *reinterpret_cast<const f32x4 *>(&score[wv][e2]);
+  int rank[NS];
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj)
+  for (int i = 0; i < NS; ++i) rank[i] = 0;
+  // every slot of the table is ranked against (those past E hold key 0 and beat nothing): a static trip count, so
+  // the LDS reads are issued ahead of their use
+#pragma unroll 16
+  for (int e2 = 0; e2 < 64 * NS; e2 += 2) {
+    typedef __attribute__((ext_vector_type(2))) uint64_t u64x2;
+    const u64x2 q = *reinterpret_cast<const u64x2 *>(&keys[wv][e2]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) rank[i] += better(q[jj], e2 + jj, sel[i], lane + 64 * i) ? 1 : 0;
+    for (int i = 0; i < NS; ++i) rank[i] += (q.x > key[i] ? 1 : 0) + (q.y > key[i] ? 1 : 0);
   }
   // the weights: probabilities over all experts (gating 1), sigmoids (gating 2) or a softmax over the picks (3)
-  float lmax = fmaxf(fmaxf(l[0], l[1]), fmaxf(l[2], l[3]));
+  float lmax = l[0];
+#pragma unroll
+  for (int i = 1; i < NS; ++i) lmax = fmaxf(lmax, l[i]);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) lmax = fmaxf(lmax, __shfl_xor(lmax, off, 64));
-  float w[4], ws = 0.f;
-  bool pick[4];
+  float w[NS], ws = 0.f;
+  bool pick[NS];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < NS; ++i) {
     pick[i] = in[i] && rank[i] < KU;
     const float ex = in[i] ? expf(l[i] - lmax) : 0.f;
     w[i] = gating == 2 ? 1.f / (1.f + expf(-l[i])) : ex;
@@ -83,17 +103,27 @@ __global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ log
   float den = wave_sum(ws);                // gating 1: the softmax denominator; 3: the picks' sum; 2: the sum
   float sum = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < NS; ++i) {
     if (gating != 2) w[i] = w[i] / den;
     sum += pick[i] ? w[i] : 0.f;
   }
   const float nden = norm ? fmaxf(gating == 2 ? den : wave_sum(sum), kNormFloor) : 1.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < NS; ++i)
     if (pick[i]) {
       ids[t * KU + rank[i]] = lane + 64 * i;
       wts[t * KU + rank[i]] = (norm ? w[i] / nden : w[i]) * scale;
     }
+}
+
+// the top-k instantiation for E experts (slots a lane: ceil(E / 64))
+static void launch_topk(const float *logits, int64_t tokens, int E, int KU, int gating, int norm, float scale,
+                        const float *bias, const int32_t *info, int32_t *ids, float *wts, hipStream_t s) {
+  const unsigned g = (unsigned)((tokens + 3) / 4);
+  if (E <= 64) topk_kernel<1><<<g, 256, 0, s>>>(logits, tokens, E, KU, gating, norm, scale, bias, info, ids, wts);
+  else if (E <= 128) topk_kernel<2><<<g, 256, 0, s>>>(logits, tokens, E, KU, gating, norm, scale, bias, info, ids, wts);
+  else if (E <= 192) topk_kernel<3><<<g, 256, 0, s>>>(logits, tokens, E, KU, gating, norm, scale, bias, info, ids, wts);
+  else topk_kernel<4><<<g, 256, 0, s>>>(logits, tokens, E, KU, gating, norm, scale, bias, info, ids, wts);
 }
 
 // ------------------------------------------------------------------------------------------------ router
@@ -430,16 +460,20 @@ __global__ __launch_bounds__(256) void row_scale_wave_kernel(int64_t rows, int64
     }
     return;
   }
+  // every chunk load is issued before any is used (a lane past the row reloads its last chunk and ignores it), so
+  // the row costs one memory latency, not one per chunk
   float v[NCH][8];
-  float m = 0.f;
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
     const int64_t c = lane + 64 * i;
-    if (c < nch) {
-      load8<BF>(x, base + c, v[i]);
+    load8<BF>(x, base + (c < nch ? c : nch - 1), v[i]);
+  }
+  float m = 0.f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[i][j]));
-    }
+  for (int i = 0; i < NCH; ++i) {
+    const bool in = lane + 64 * i < nch;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = fmaxf(m, in ? fabsf(v[i][j]) : 0.f);
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
@@ -550,8 +584,7 @@ int qmm_moe_topk(const float *logits, int64_t tokens, int E, int KU, int gating,
   if (gating < 1 || gating > 3 || (gating == 1 && bias)) return QMM_ERR_RANGE;
   if (tokens <= 0 || tokens > (1ll << 24)) return QMM_ERR_SHAPE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  topk_kernel<<<(unsigned)((tokens + 3) / 4), 256, 0, s>>>(logits, tokens, E, KU, gating, norm, scale, bias, nullptr,
-                                                            ids, wts);
+  launch_topk(logits, tokens, E, KU, gating, norm, scale, bias, nullptr, ids, wts, s);
   return launch_status();
 }
 
@@ -583,8 +616,7 @@ int qmm_moe_route(int64_t tokens, int64_t H, int E, int KU, int gating, int norm
   if (tokens <= 0 || tokens > (1ll << 24)) return QMM_ERR_SHAPE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (int st = router(tokens, H, E, x, x_dtype, w, w_dtype, 0, logits, s)) return st;
-  topk_kernel<<<(unsigned)((tokens + 3) / 4), 256, 0, s>>>(logits, tokens, E, KU, gating, norm, scale, bias, info,
-                                                            ids, wts);
+  launch_topk(logits, tokens, E, KU, gating, norm, scale, bias, info, ids, wts, s);
   return launch_status();
 }
 
