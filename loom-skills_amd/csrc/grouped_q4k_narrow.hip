@@ -384,7 +384,7 @@ int launch_depth(const NArgs &a, bool tiled, hipStream_t s) {
 }  // namespace
 
 #ifndef QMM_NARROW_WAVES_GU
-#define QMM_NARROW_WAVES_GU 4
+#define QMM_NARROW_WAVES_GU 8
 #endif
 #ifndef QMM_NARROW_WAVES_DN
 #define QMM_NARROW_WAVES_DN 4
