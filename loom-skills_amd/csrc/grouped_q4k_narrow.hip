@@ -129,6 +129,10 @@ __device__ __forceinline__ void unit_scales(const uint4 &hd, u32 hmask, h2 (&dsc
   }
 }
 
+// s_waitcnt immediate that waits until at most n vector memory loads are outstanding (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14; expcnt and lgkmcnt left at their maxima)
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
 template <int KIND, int NW, int DEPTH, bool TILED>
 __global__ __launch_bounds__(64 * NW) void q4k_narrow_kernel(NArgs a) {
   static_assert(DEPTH % 2 == 0, "a step's parity is static inside the unrolled step loop");
@@ -153,8 +157,8 @@ __global__ __launch_bounds__(64 * NW) void q4k_narrow_kernel(NArgs a) {
       tile = b / a.col_blocks / 4;
     }
   }
-  const int expert0 = a.tile_info[2 * tile];
-  if (expert0 < 0 || kGroupRows * rg >= a.tile_info[2 * tile + 1]) return;   // uniform over the workgroup
+  const int expert0 = a.tile_info[2 * tile], tile_rows = a.tile_info[2 * tile + 1];
+  if (expert0 < 0 || kGroupRows * rg >= tile_rows) return;   // uniform over the workgroup
   const int expert = expert0 >= a.E ? a.E - 1 : expert0;
   const int r0 = tile * kTileRows + kGroupRows * rg;
 
@@ -195,48 +199,65 @@ __global__ __launch_bounds__(64 * NW) void q4k_narrow_kernel(NArgs a) {
   const int cf = 512 + 16 * (4 * lc + q), chh = 256 + 512 * (q >> 1) + 16 * (2 * lc + (q & 1));
   const int hf = 16 * (2 * lc + (q >> 1)), hh = 16 * lc;
   uint4 cring[DEPTH][2], hring[DEPTH][2], hnext[2];
-  if constexpr (TILED) {   // unit 0 (or the half unit when K == 256): header, then codes, as the loop issues them
+  constexpr int kPrefetchLoads = TILED ? 10 : 4 * DEPTH;   // the vector loads prefetch() issues
+  auto prefetch = [&]() __attribute__((always_inline)) {
+    if constexpr (TILED) {   // unit 0 (or the half unit when K == 256): header, then codes, as the loop issues them
 #pragma unroll
-    for (int g = 0; g < 2; ++g) hnext[g] = ld16(wrow[g] + (F > 0 ? hf : hh));
+      for (int g = 0; g < 2; ++g) hnext[g] = ld16(wrow[g] + (F > 0 ? hf : hh));
 #pragma unroll
-    for (int su = 0; su < 4; ++su) {
-      const int lo = F > 0 ? cf : chh;
+      for (int su = 0; su < 4; ++su) {
+        const int lo = F > 0 ? cf : chh;
 #pragma unroll
-      for (int g = 0; g < 2; ++g) cring[su][g] = ld16(wrow[g] + lo + 1024 * (F > 0 || su < 2 ? su : 0));
+        for (int g = 0; g < 2; ++g) cring[su][g] = ld16(wrow[g] + lo + 1024 * (F > 0 || su < 2 ? su : 0));
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < DEPTH; ++u) ld_step(u, cring[u], hring[u]);
     }
-  } else {
-#pragma unroll
-    for (int u = 0; u < DEPTH; ++u) ld_step(u, cring[u], hring[u]);
-  }
+  };
 
-  // ---- the row group's activation rows into LDS (rows without an assignment: zeros, not read)
-  if (tid < kGroupRows) {
-    const int rm = a.rowmap[r0 + tid];
-    int src = -1;
-    if (rm >= 0) src = KIND == kNGU ? rm / a.KU : r0 + tid;
-    if (src >= a.x_rows) src = -1;
-    src_row[tid] = src;
-    rinv[tid] = (a.scales && src >= 0) ? a.scales[2 * src + 1] : 1.f;
-  }
-  __syncthreads();
+  // ---- the row group's activation rows into LDS (rows without an assignment: zeros, not read), then the weight
+  // prefetch. gu: row i of the group is assignment rowmap[r0 + i], of token rowmap[r0 + i] / KU; dn: the sorted row
+  // r0 + i itself, staged without waiting for the row map when 16 rg + i < tile_rows (the bucket fills a tile's rows
+  // from the top); the row map decides which rows are stored (src_row >= 0). The staging loads go out before the
+  // weight prefetch: a load's wait counts every load issued before it, so staged after the prefetch they would
+  // wait for the weights' HBM latency.
+  auto dn_row = [&](int i) { return kGroupRows * rg + i < tile_rows && r0 + i < a.x_rows ? r0 + i : -1; };
+  // every thread reads its own staging row's entries (no barrier, no divergent branch whose join would wait for
+  // the loads): the row map, the row (gu: the token, which needs the row map first), its inverse scale
+  const int rm_own = a.rowmap[r0 + (tid & 15)];
+  int srow;
+  if constexpr (KIND == kNGU) srow = rm_own >= 0 && rm_own / a.KU < a.x_rows ? rm_own / a.KU : -1;
+  else srow = dn_row(tid & 15);
+  const float inv_load = a.scales ? a.scales[2 * (srow >= 0 ? srow : 0) + 1] : 1.f;
   {
-    // 16-byte chunks of the panel, row fastest: thread t stages chunks t, t + NT, ... (K / 128 of them, an even
-    // count). The loads go through a buffer resource over the activation rows; a row without an assignment gets an
-    // offset past its end, where the hardware returns zeros without a memory access, so the loop has no branch.
+    // 16-byte chunks of the panel, row fastest: thread t stages chunks t, t + NT, ... (16 K / 8 / NT of them).
+    // The loads go through a buffer resource over the activation rows; a row past them (or, for gu, without an
+    // assignment) gets an offset past their end, where the hardware returns zeros without a memory access, so the
+    // loop has no branch.
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<_Float16 *>(a.x16), (short)0, (int)((int64_t)a.x_rows * K * 2), 0x00020000);
-    const int src = src_row[tid & 15];
-    const u32 rbase = src >= 0 ? (u32)src * (u32)K * 2u : 0x80000000u;
-    const int per = K / 128;
-#pragma unroll 4
-    for (int i = 0; i < per; i += 2) {
-      const int c0s = i * NT + tid, c1s = c0s + NT;   // chunk c: row c % 16 (= tid % 16), k8 = c / 16
-      const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)(src >= 0 ? rbase + 16u * (u32)(c0s >> 4) : rbase), 0, 0);
-      const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)(src >= 0 ? rbase + 16u * (u32)(c1s >> 4) : rbase), 0, 0);
-      xs[c0s] = make_uint4(v0.x, v0.y, v0.z, v0.w);
-      xs[c1s] = make_uint4(v1.x, v1.y, v1.z, v1.w);
+    const u32 rbase = srow >= 0 ? (u32)srow * (u32)K * 2u : 0x80000000u;
+    const int per = K / 8 * kGroupRows / NT;
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    // straight into LDS (buffer_load ... lds: no registers, no store instructions); the wave's 64 lanes fill 64
+    // consecutive chunks, so the LDS destination is one wave-uniform address a load
+#pragma unroll 8
+    for (int i = 0; i < per; ++i) {
+      const int c = i * NT + tid;   // chunk c: row c % 16 (= tid % 16), k8 c / 16
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          xrs, (__attribute__((address_space(3))) void *)&xs[i * NT + 64 * wave_u], 16,
+          (int)(srow >= 0 ? rbase + 16u * (u32)(c >> 4) : rbase), 0, 0, 0);
     }
   }
+  __builtin_amdgcn_sched_barrier(0);   // the weight prefetch goes out after the staging loads
+  prefetch();
+  if (tid < kGroupRows) {   // the rows the epilogue stores, with their inverse scales
+    src_row[tid] = rm_own >= 0 ? srow : -1;
+    rinv[tid] = srow >= 0 ? inv_load : 1.f;
+  }
+  // the staging loads are complete when at most the prefetch's loads are outstanding (vmcnt counts in issue order)
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(kPrefetchLoads));
   __syncthreads();
 
   f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
