@@ -18,6 +18,11 @@ namespace {
 
 constexpr int kWavesPerBlock = 4;
 constexpr int kRW = 4;
+// Output rows a wave of the expert matvecs: four weight rows in flight a wave, i.e. two gate / up row pairs for
+// gate/up (measured: MXFP4 gpt-oss-20b T = 1 gate/up 11.5 -> 10.4 us, Q4_K Qwen3-30B-A3B 10.6 -> 8.5 us; the down
+// matvec is slower with two rows and with eight)
+template <bool GU>
+constexpr int expert_rw() { return GU ? 2 : 4; }
 
 template <int RW, int TG>
 __device__ __forceinline__ void reduce_all(float (&acc)[RW][TG]) {
@@ -222,8 +227,9 @@ int launch_expert(int64_t k, int64_t n, int E, int KU, int64_t assignments, cons
                   int64_t x_row_bytes, const void *w, const void *ws, const void *w2, const void *ws2, int64_t rb,
                   int64_t srb, int64_t ebytes, int64_t esbytes, const float *bias, const float *bias2, int act,
                   float *y, hipStream_t s, int accumulate = 0) {
-  const dim3 grid((unsigned)assignments, (unsigned)((n + kWavesPerBlock * kRW - 1) / (kWavesPerBlock * kRW)));
-  expert_mv_kernel<P, kRW, GU><<<grid, 256, 0, s>>>(
+  constexpr int RW = expert_rw<GU>();
+  const dim3 grid((unsigned)assignments, (unsigned)((n + kWavesPerBlock * RW - 1) / (kWavesPerBlock * RW)));
+  expert_mv_kernel<P, RW, GU><<<grid, 256, 0, s>>>(
       n, assignments, KU, E, k, ids, static_cast<const u8 *>(x), x_row_bytes, static_cast<const u8 *>(w),
       static_cast<const u8 *>(ws), static_cast<const u8 *>(w2), static_cast<const u8 *>(ws2), rb, srb, ebytes, esbytes,
       bias, bias2, act, accumulate, y);
