@@ -157,6 +157,18 @@ int qmm_gemm_mxfp4(int fmt, int mode, int64_t rows, int64_t k, int64_t n, const 
 int qmm_moe_topk(const float *logits, int64_t tokens, int E, int KU, int gating, int norm, float scale,
                  const float *bias, int32_t *ids, float *wts, qmm_stream_t stream);
 
+/* qmm_moe_topk together with the activation operand of the grouped gate/up GEMM, for the token rows x (bf16
+ * [tokens, H], H <= 4096): the reference's prefill chain issues the route (g_moe_route, S/gen_moe.py:116-500) and
+ * the operand (g_row_scale_f16, S/gen_llm.py:1843-1915, for GGUF experts; the MXFP8 quantization for MXFP4 experts)
+ * as separate kernels (S/gen_llm.py:5373-5376); both are per token, so one wave per token does both here (no
+ * counterpart as one kernel in the reference). ids / wts as qmm_moe_topk; op_dtype QMM_F16: xo f16 [tokens, H] and
+ * xo_scales f32 [tokens, 2] as qmm_row_scale_f16 (H % 8 == 0); QMM_MXFP8: xo E4M3 codes u8 [tokens, H] and
+ * xo_scales E8M0 u8 [tokens, H / 32] as qmm_quant_mxfp8 (H % 32 == 0). Every output equals the separate calls'
+ * bit for bit. */
+int qmm_moe_topk_operand(const float *logits, int64_t tokens, int E, int KU, int gating, int norm, float scale,
+                         const float *bias, int32_t *ids, float *wts, int64_t H, const void *x, int x_dtype,
+                         int op_dtype, void *xo, void *xo_scales, qmm_stream_t stream);
+
 /* The router with its matvec, g_moe_route / g_moe_route_tr / g_moe_route_tr_live (S/gen_moe.py:116-500; launch
  * S/gen_llm.py:5373, :5380): logits f32 [tokens, E] = x W^T (fp32 accumulation; x f32 or bf16 [tokens, H], W the
  * router weight ffn_gate_inp f32 or bf16 [E, H], H % 4 == 0), then qmm_moe_topk on them. logits is the caller's

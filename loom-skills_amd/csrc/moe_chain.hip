@@ -2,7 +2,8 @@
 // emits (S/gen_llm.py:5324-5385) run on one stream with a caller-passed workspace for its intermediates (the buffers
 // moe_alloc allocates, S/gen_llm.py:5388-5432):
 //
-//   prefill (tokens >= 64): route (router matvec + top-k, or top-k of given logits), [wscale], bucket into 64-row
+//   prefill (tokens >= 64): route (router matvec + top-k, or top-k of given logits; with given logits and bf16 rows
+//     the top-k launch also writes the activation operand), [wscale], bucket into 64-row
 //     expert tiles, the activation operand (GGUF formats: row-scaled f16; MXFP4: MXFP8), grouped gate/up GEMM with the
 //     activation, its output's operand, grouped down GEMM, combine of the sorted rows;
 //   decode (tokens < 64): route, [wscale], gate/up expert matvecs, down expert matvecs (f32 / bf16 activations, or
@@ -120,9 +121,13 @@ extern "C" int qmm_moe_routed(int fmt, int fmt_down, int fused, int act, int gat
   float *wts = static_cast<float *>(at(p.wts));
   const int64_t T = tokens;
 
-  // ---- route
+  // ---- route; a prefill batch with given logits and bf16 rows also gets the gate/up operand in the same launch
   int st;
-  if (logits)
+  const bool operand = p.prefill && logits && x_dtype == QMM_BF16 && H <= 4096 && H % (p.mx ? 32 : 8) == 0;
+  if (operand)
+    st = qmm_moe_topk_operand(logits, T, E, KU, gating, norm, scale, router_bias, ids, wts, H, x, x_dtype,
+                              p.mx ? QMM_MXFP8 : QMM_F16, at(p.xa), at(p.xs), stream);
+  else if (logits)
     st = qmm_moe_topk(logits, T, E, KU, gating, norm, scale, router_bias, ids, wts, stream);
   else
     st = qmm_moe_route(T, H, E, KU, gating, norm, scale, x, x_dtype, w_router, w_router_dtype, router_bias, nullptr,
@@ -168,7 +173,7 @@ extern "C" int qmm_moe_routed(int fmt, int fmt_down, int fused, int act, int gat
   if (p.mx) {
     uint8_t *x8 = static_cast<uint8_t *>(at(p.xa)), *xs8 = static_cast<uint8_t *>(at(p.xs));
     uint8_t *a8 = static_cast<uint8_t *>(at(p.act)), *as8 = static_cast<uint8_t *>(at(p.as));
-    if ((st = qmm_quant_mxfp8(T, H, x, x_dtype, nullptr, x8, xs8, stream))) return st;
+    if (!operand && (st = qmm_quant_mxfp8(T, H, x, x_dtype, nullptr, x8, xs8, stream))) return st;
     if ((st = qmm_moe_grouped_mxfp8(fmt, fused, act, E, KU, p.max_rows, H, FE, T, ti, rm, x8, xs8, w_gate, ws_gate,
                                     w_up, ws_up, bias_gate, bias_up, a8, as8, stream)))
       return st;
@@ -178,7 +183,7 @@ extern "C" int qmm_moe_routed(int fmt, int fmt_down, int fused, int act, int gat
     void *x16 = at(p.xa), *a16 = at(p.a2);
     float *xsc = static_cast<float *>(at(p.xs)), *asc = static_cast<float *>(at(p.as));
     float *a = static_cast<float *>(at(p.act));
-    if ((st = qmm_row_scale_f16(T, H, x, x_dtype, xsc, x16, nullptr, stream))) return st;
+    if (!operand && (st = qmm_row_scale_f16(T, H, x, x_dtype, xsc, x16, nullptr, stream))) return st;
     if ((st = qmm_moe_grouped(fmt, 0, fused, act, E, KU, p.max_rows, H, FE, T, ti, rm, x16, QMM_F16, xsc, w_gate,
                               nullptr, w_up, nullptr, bias_gate, bias_up, a, stream)))
       return st;

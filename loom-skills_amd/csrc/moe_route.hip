@@ -19,6 +19,7 @@ namespace {
 
 constexpr int kTile = 64;
 constexpr float kNormFloor = 6.103515625e-05f;
+typedef __attribute__((ext_vector_type(4))) u32 v4u;
 
 // ------------------------------------------------------------------------------------------------- top-k
 // One wave per token; lane l holds experts l, l + 64, ... (NS = ceil(E / 64) slots). The selection is a ranking: the
@@ -36,17 +37,12 @@ __device__ __forceinline__ uint64_t select_key(float v, int e) {
 
 constexpr int kTopkMaxE = 256;
 
+// The selection and weights of token t by one wave; keys: the wave's table of 64 NS selection keys in LDS.
 template <int NS>
-__global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ logits, int64_t tokens, int E, int KU,
-                                                   int gating, int norm, float scale, const float *__restrict__ bias,
-                                                   const int32_t *__restrict__ info, int32_t *__restrict__ ids,
-                                                   float *__restrict__ wts) {
-  __shared__ __align__(16) uint64_t keys[4][64 * NS];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int64_t t = (int64_t)blockIdx.x * 4 + wv;
-  if (t >= tokens) return;               // a whole wave: nothing below synchronizes the workgroup
-  if (info && info[4 * t + 2] == 0) return;   // a padding token of the epoch (_live): no ids, no weights
-  const float *lg = logits + t * E;
+__device__ __forceinline__ void topk_token(const float *__restrict__ lg, int64_t t, int E, int KU, int gating,
+                                           int norm, float scale, const float *__restrict__ bias, uint64_t *keys,
+                                           int32_t *__restrict__ ids, float *__restrict__ wts) {
+  const int lane = threadIdx.x & 63;
   float l[NS], bv[NS];
   bool in[NS];
   const float NEG = -3.0e38f;
@@ -68,7 +64,7 @@ __global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ log
     float sv = l[i];
     if (gating == 2 && bias) sv = in[i] ? 1.f / (1.f + expf(-l[i])) + b : NEG;
     key[i] = in[i] ? select_key(sv, e) : 0ull;   // experts past E rank below every real one
-    keys[wv][e] = key[i];
+    keys[e] = key[i];
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -81,7 +77,7 @@ __global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ log
 #pragma unroll 16
   for (int e2 = 0; e2 < 64 * NS; e2 += 2) {
     typedef __attribute__((ext_vector_type(2))) uint64_t u64x2;
-    const u64x2 q = *reinterpret_cast<const u64x2 *>(&keys[wv][e2]);
+    const u64x2 q = *reinterpret_cast<const u64x2 *>(&keys[e2]);
 #pragma unroll
     for (int i = 0; i < NS; ++i) rank[i] += (q.x > key[i] ? 1 : 0) + (q.y > key[i] ? 1 : 0);
   }
@@ -114,6 +110,108 @@ __global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ log
       ids[t * KU + rank[i]] = lane + 64 * i;
       wts[t * KU + rank[i]] = (norm ? w[i] / nden : w[i]) * scale;
     }
+}
+
+template <int NS>
+__global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ logits, int64_t tokens, int E, int KU,
+                                                   int gating, int norm, float scale, const float *__restrict__ bias,
+                                                   const int32_t *__restrict__ info, int32_t *__restrict__ ids,
+                                                   float *__restrict__ wts) {
+  __shared__ __align__(16) uint64_t keys[4][64 * NS];
+  const int wv = threadIdx.x >> 6;
+  const int64_t t = (int64_t)blockIdx.x * 4 + wv;
+  if (t >= tokens) return;               // a whole wave: nothing below synchronizes the workgroup
+  if (info && info[4 * t + 2] == 0) return;   // a padding token of the epoch (_live): no ids, no weights
+  topk_token<NS>(logits + t * E, t, E, KU, gating, norm, scale, bias, keys[wv], ids, wts);
+}
+
+// ------------------------------------------------------------------------------ top-k + activation operand
+// The prefill chain's first two steps, routing and the grouped gate/up GEMM's activation operand, are both per token
+// and independent: one wave per token does both, its row's loads issued before the selection so their latency
+// hides behind it. OP kOpF16: the row-scaled f16 row and its (2^-e, 2^e) as qmm_row_scale_f16 computes them; kOpMx8:
+// the E4M3 codes and E8M0 scales as qmm_quant_mxfp8 computes them. x: bf16 rows [tokens, H]; NP: 16-byte pieces
+// (8 values) a lane, H <= 512 NP.
+enum TopkOp { kOpF16 = 1, kOpMx8 = 2 };
+
+template <int NS, int OP, int NP>
+__global__ __launch_bounds__(256) void topk_operand_kernel(const float *__restrict__ logits, int64_t tokens, int E,
+                                                           int KU, int gating, int norm, float scale,
+                                                           const float *__restrict__ bias, int32_t *__restrict__ ids,
+                                                           float *__restrict__ wts, int64_t H,
+                                                           const u16 *__restrict__ x, void *__restrict__ xo,
+                                                           void *__restrict__ xs) {
+  __shared__ __align__(16) uint64_t keys[4][64 * NS];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t t = (int64_t)blockIdx.x * 4 + wv;
+  if (t >= tokens) return;
+  const int np = (int)(H / 8);           // pieces of the row
+  const v4u *xr = reinterpret_cast<const v4u *>(x + t * H);
+  v4u raw[NP];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int p = lane + 64 * i;
+    raw[i] = xr[p < np ? p : np - 1];
+  }
+  topk_token<NS>(logits + t * E, t, E, KU, gating, norm, scale, bias, keys[wv], ids, wts);
+  float v[NP][8];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const u32 d[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { v[i][2 * j] = bf16_to_f32(d[j] & 0xFFFFu); v[i][2 * j + 1] = bf16_to_f32(d[j] >> 16); }
+  }
+  if constexpr (OP == kOpF16) {
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const bool in = lane + 64 * i < np;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) m = fmaxf(m, in ? fabsf(v[i][j]) : 0.f);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    const int biased = (int)((f32_as_u32(m) >> 23) & 255u);
+    const int e = min(max(biased - 127 - 13, 0), 100);
+    const float sc = u32_as_f32((u32)(127 - e) << 23), inv = u32_as_f32((u32)(127 + e) << 23);
+    v4u *o = reinterpret_cast<v4u *>(static_cast<_Float16 *>(xo) + t * H);
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int p = lane + 64 * i;
+      if (p < np) {
+        u32 w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          w[j] = (u32)__builtin_bit_cast(u16, (_Float16)(v[i][2 * j] * sc)) |
+                 ((u32)__builtin_bit_cast(u16, (_Float16)(v[i][2 * j + 1] * sc)) << 16);
+        o[p] = v4u{w[0], w[1], w[2], w[3]};
+      }
+    }
+    if (lane == 0) reinterpret_cast<float2 *>(xs)[t] = make_float2(sc, inv);
+  } else {
+    // a 32-value block is four consecutive lanes' pieces (np % 4 == 0, so a block never straddles the row's end)
+    typedef __attribute__((ext_vector_type(2))) u32 v2u;
+    u8 *codes = static_cast<u8 *>(xo) + t * H;
+    u8 *scales = static_cast<u8 *>(xs) + t * (H / 32);
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int p = lane + 64 * i;
+      float amax = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[i][j]));
+      amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+      amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+      const int sx = mxfp8_exponent(amax);
+      if (p < np) {
+        int w0 = 0, w1 = 0;
+        w0 = e4m3_pack2<false>(v[i][0], v[i][1], sx, w0);
+        w0 = e4m3_pack2<true>(v[i][2], v[i][3], sx, w0);
+        w1 = e4m3_pack2<false>(v[i][4], v[i][5], sx, w1);
+        w1 = e4m3_pack2<true>(v[i][6], v[i][7], sx, w1);
+        reinterpret_cast<v2u *>(codes)[p] = v2u{(u32)w0, (u32)w1};
+        if ((lane & 3) == 0) scales[p / 4] = (u8)(sx + 127);
+      }
+    }
+  }
 }
 
 // the top-k instantiation for E experts (slots a lane: ceil(E / 64))
@@ -576,6 +674,38 @@ __global__ __launch_bounds__(256) void repack_mxfp4_kernel(int64_t groups, const
 }  // namespace
 
 extern "C" {
+
+int qmm_moe_topk_operand(const float *logits, int64_t tokens, int E, int KU, int gating, int norm, float scale,
+                         const float *bias, int32_t *ids, float *wts, int64_t H, const void *x, int x_dtype,
+                         int op_dtype, void *xo, void *xo_scales, qmm_stream_t stream) {
+  if (!logits || !ids || !wts || !x || !xo || !xo_scales) return QMM_ERR_NULL;
+  if (E <= 0 || E > 256 || KU <= 0 || KU > 8 || KU > E) return QMM_ERR_RANGE;
+  if (gating < 1 || gating > 3 || (gating == 1 && bias)) return QMM_ERR_RANGE;
+  if (tokens <= 0 || tokens > (1ll << 24)) return QMM_ERR_SHAPE;
+  if (x_dtype != QMM_BF16 || (op_dtype != QMM_F16 && op_dtype != QMM_MXFP8)) return QMM_ERR_DTYPE;
+  if (H <= 0 || H > 4096 || H % (op_dtype == QMM_F16 ? 8 : 32)) return QMM_ERR_SHAPE;
+  if (!aligned(x, 16) || !aligned(xo, op_dtype == QMM_F16 ? 16 : 8) || !aligned(xo_scales, 8)) return QMM_ERR_ALIGN;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const unsigned g = (unsigned)((tokens + 3) / 4);
+  const int NS = (E + 63) / 64;
+  const u16 *xb = static_cast<const u16 *>(x);
+  auto go = [&](auto kern) {
+    kern<<<g, 256, 0, s>>>(logits, tokens, E, KU, gating, norm, scale, bias, ids, wts, H, xb, xo, xo_scales);
+    return launch_status();
+  };
+#define QMM_TOPK_OP(NSV)                                                                                            \
+  if (NS == NSV) {                                                                                                  \
+    if (op_dtype == QMM_F16)                                                                                        \
+      return H <= 2048 ? go(topk_operand_kernel<NSV, kOpF16, 4>) : go(topk_operand_kernel<NSV, kOpF16, 8>);       \
+    return H <= 2048 ? go(topk_operand_kernel<NSV, kOpMx8, 4>) : go(topk_operand_kernel<NSV, kOpMx8, 8>);         \
+  }
+  QMM_TOPK_OP(1)
+  QMM_TOPK_OP(2)
+  QMM_TOPK_OP(3)
+  QMM_TOPK_OP(4)
+#undef QMM_TOPK_OP
+  return QMM_ERR_RANGE;
+}
 
 int qmm_moe_topk(const float *logits, int64_t tokens, int E, int KU, int gating, int norm, float scale,
                  const float *bias, int32_t *ids, float *wts, qmm_stream_t stream) {

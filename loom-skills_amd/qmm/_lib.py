@@ -20,6 +20,8 @@ SIGNATURES = {
     "qmm_mv_q8": [c_int, c_i64, c_i64, c_i64, c_int, c_vp, c_int, c_vp, c_vp, c_vp],
     "qmm_gemm": [c_int, c_int, c_i64, c_i64, c_i64, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_int, c_vp],
     "qmm_moe_topk": [c_vp, c_i64, c_int, c_int, c_int, c_int, c_float, c_vp, c_vp, c_vp, c_vp],
+    "qmm_moe_topk_operand": [c_vp, c_i64, c_int, c_int, c_int, c_int, c_float, c_vp, c_vp, c_vp, c_i64, c_vp, c_int,
+                             c_int, c_vp, c_vp, c_vp],
     "qmm_moe_bucket": [c_i64, c_int, c_int, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
     "qmm_moe_expert_mv": [c_int, c_int, c_int, c_int, c_i64, c_i64, c_int, c_int, c_i64, c_vp, c_vp, c_int, c_vp,
                           c_vp, c_vp, c_vp, c_vp, c_vp],

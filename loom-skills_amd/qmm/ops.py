@@ -243,6 +243,28 @@ def moe_topk(logits, KU, gating, norm, scale=1.0, bias=None):
     return ids, wts
 
 
+def moe_topk_operand(logits, KU, gating, norm, x, op, scale=1.0, bias=None):
+    """moe_topk together with the grouped gate/up GEMM's activation operand of the bf16 token rows x [T, H] in one
+    launch (qmm_moe_topk_operand): op "f16" -> (ids, wts, x16, scales) with x16, scales as row_scale_f16(x);
+    "mxfp8" -> (ids, wts, codes, scales) as quant_mxfp8(x). H <= 4096."""
+    _dev(logits, x, bias)
+    T, E = logits.shape
+    H = x.shape[1]
+    dev = logits.device
+    ids = torch.empty((T, KU), dtype=torch.int32, device=dev)
+    wts = torch.empty((T, KU), dtype=torch.float32, device=dev)
+    if op == "f16":
+        xo = torch.empty((T, H), dtype=torch.float16, device=dev)
+        xs = torch.empty((T, 2), dtype=torch.float32, device=dev)
+    else:
+        xo = torch.empty((T, H), dtype=torch.uint8, device=dev)
+        xs = torch.empty((T, H // MX_BLOCK), dtype=torch.uint8, device=dev)
+    _lib.call("qmm_moe_topk_operand", _ptr(logits), T, E, KU, gating, int(bool(norm)), float(scale), _ptr(bias),
+              _ptr(ids), _ptr(wts), H, _ptr(x), _dt(x), DTYPE["f16" if op == "f16" else "mxfp8"], _ptr(xo), _ptr(xs),
+              _stream())
+    return ids, wts, xo, xs
+
+
 def moe_route(x, w_router, KU, gating, norm, scale=1.0, bias=None, info=None, logits=None):
     """(ids, wts, logits f32 [T, E]) from the hidden rows x f32 / bf16 [T, H] and the router weight f32 / bf16
     [E, H]: logits = x W^T, then moe_topk. With info (i32 [T, 4]) padding tokens (info[t, 2] == 0) get no ids."""
@@ -480,18 +502,28 @@ def moe_prefill(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up
             repack_mxfp4(w_down, E * H, FE)
         if w_up is not None:
             w_up, ws_up = repack_mxfp4(w_up, E * FE, H)
-    ids, wts, logits = _route(x, logits, KU, gating, norm, scale, bias, router, down_scale)
+    gguf = fmt in ("q4_k", "q4_kt", "q6_k", "q4_0")
+    xop = None
+    if logits is not None and router is None and x.dtype == torch.bfloat16 and H <= 4096 and \
+            (gguf or H % MX_BLOCK == 0):
+        # routing and the gate/up operand in one launch (the same bits as the separate calls)
+        ids, wts, xop, xos = moe_topk_operand(logits, KU, gating, norm, x, "f16" if gguf else "mxfp8", scale=scale,
+                                              bias=bias)
+        if down_scale is not None:
+            moe_wscale(ids, wts, down_scale)
+    else:
+        ids, wts, logits = _route(x, logits, KU, gating, norm, scale, bias, router, down_scale)
     bg, bu, bd = expert_bias if expert_bias is not None else (None, None, None)
     tile_info, rowmap, pos = moe_bucket(ids, E)
-    if fmt in ("q4_k", "q4_kt", "q6_k", "q4_0"):
-        x16, xs = row_scale_f16(x)
+    if gguf:
+        x16, xs = (xop, xos) if xop is not None else row_scale_f16(x)
         a = moe_grouped(fmt, "gu", tile_info, rowmap, x16, w_gate, FE, H, E, KU, w2=w_up, x_scales=xs,
                         fused=fused, act=act, bias=bg, bias2=bu)
         a16, as_ = row_scale_f16(a, tile_info=tile_info)
         ys = moe_grouped(fmt_down or fmt, "dn", tile_info, rowmap, a16, w_down, H, FE, E, KU, x_scales=as_, bias=bd)
     elif fmt in ("mxfp4s", "mxfp4t"):
         # the gate/up GEMM writes its activation as MXFP8 directly (the down GEMM's A operand)
-        x8, xs = quant_mxfp8(x)
+        x8, xs = (xop, xos) if xop is not None else quant_mxfp8(x)
         a8, as8 = moe_grouped_mxfp8(fmt, tile_info, rowmap, x8, w_gate, FE, H, E, KU, w2=w_up, ws=ws_gate,
                                     ws2=ws_up, x_scales=xs, fused=fused, act=act, bias=bg, bias2=bu)
         a = None

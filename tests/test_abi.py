@@ -101,6 +101,18 @@ def test_argument_validation_without_a_device(lib):
     assert lib.qmm_moe_topk(fake, 4, 32, 9, 1, 1, ctypes.c_float(1), n, fake, fake, n) == st["QMM_ERR_RANGE"]
     assert lib.qmm_moe_topk(fake, 4, 32, 4, 4, 1, ctypes.c_float(1), n, fake, fake, n) == st["QMM_ERR_RANGE"]
     assert lib.qmm_moe_topk(fake, 4, 32, 4, 1, 1, ctypes.c_float(1), fake, fake, fake, n) == st["QMM_ERR_RANGE"]
+    # top-k + operand: bf16 rows only, f16 / MXFP8 operands, rows up to 4096 values (MXFP8: whole 32-blocks)
+    f1 = ctypes.c_float(1)
+    assert lib.qmm_moe_topk_operand(fake, 4, 32, 4, 1, 1, f1, n, fake, fake, 2048, fake, 0, 1, fake, fake,
+                                    n) == st["QMM_ERR_DTYPE"]
+    assert lib.qmm_moe_topk_operand(fake, 4, 32, 4, 1, 1, f1, n, fake, fake, 2048, fake, 2, 2, fake, fake,
+                                    n) == st["QMM_ERR_DTYPE"]
+    assert lib.qmm_moe_topk_operand(fake, 4, 32, 4, 1, 1, f1, n, fake, fake, 8192, fake, 2, 1, fake, fake,
+                                    n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_moe_topk_operand(fake, 4, 32, 4, 1, 1, f1, n, fake, fake, 2056, fake, 2, 3, fake, fake,
+                                    n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_moe_topk_operand(fake, 4, 32, 4, 1, 1, f1, n, fake, fake, 2048, fake, 2, 1, fake, n,
+                                    n) == st["QMM_ERR_NULL"]
     # bucket: too few tiles for the worst case T*KU/64 + E
     assert lib.qmm_moe_bucket(256, 4, 32, 47, n, fake, fake, fake, fake, n) == st["QMM_ERR_SHAPE"]
     assert lib.qmm_moe_bucket(256, 4, 300, 500, n, fake, fake, fake, fake, n) == st["QMM_ERR_RANGE"]

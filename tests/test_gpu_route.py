@@ -58,6 +58,37 @@ def test_bucket_canonical(dev, T, E, KU):
     np.testing.assert_array_equal(host(pos), epos)
 
 
+@pytest.mark.parametrize("op", ["f16", "mxfp8"])
+@pytest.mark.parametrize("T,E,KU,gating,norm,H,bias", [(64, 128, 8, 1, True, 2048, False),
+                                                       (256, 32, 4, 3, False, 2880, False),
+                                                       (67, 256, 8, 2, True, 4096, True),
+                                                       (130, 160, 6, 3, False, 1024, True),
+                                                       (5, 60, 6, 1, False, 2048, False)])
+def test_topk_operand_equals_separate_calls(dev, op, T, E, KU, gating, norm, H, bias):
+    """qmm_moe_topk_operand: ids and weights bit for bit those of moe_topk, the operand bit for bit row_scale_f16 /
+    quant_mxfp8 of the same rows (row magnitudes 2^-30 .. 2^30, so row scales and E8M0 exponents over a wide range
+    occur; zero rows too); 1 to 4 key slots a lane, rows up to 4096 values."""
+    import torch
+    from qmm import synth
+    ops = _ops()
+    if op == "f16" and H % 8 or op == "mxfp8" and H % 32:
+        pytest.skip("row length")
+    rng = np.random.default_rng(T * 31 + E + H)
+    xf = rng.standard_normal((T, H)).astype(np.float32) * np.exp2(rng.integers(-30, 31, (T, 1))).astype(np.float32)
+    xf[T // 2] = 0.0
+    x = dev_bf16(synth.to_bf16_bits(xf), dev)
+    lg = dev_f32(rng.standard_normal((T, E)).astype(np.float32), dev)
+    b = dev_f32(rng.standard_normal(E).astype(np.float32) * 0.5, dev) if bias else None
+    ids, wts, xo, xs = ops.moe_topk_operand(lg, KU, gating, norm, x, op, scale=1.5, bias=b)
+    ids0, wts0 = ops.moe_topk(lg, KU, gating, norm, scale=1.5, bias=b)
+    xo0, xs0 = ops.row_scale_f16(x) if op == "f16" else ops.quant_mxfp8(x)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(ids), host(ids0))
+    assert_bits_equal(host(wts), host(wts0), "weights")
+    np.testing.assert_array_equal(host(xo).view(np.uint8), host(xo0).view(np.uint8))
+    np.testing.assert_array_equal(host(xs).view(np.uint8), host(xs0).view(np.uint8))
+
+
 def test_bucket_repeat_runs_identical(dev):
     import torch
     rng = np.random.default_rng(4)
