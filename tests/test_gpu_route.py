@@ -40,7 +40,8 @@ def test_topk_ties_go_to_the_lower_id(dev):
     assert host(ids)[0].tolist() == [0, 1, 2, 3]
 
 
-@pytest.mark.parametrize("T,E,KU", [(64, 128, 8), (256, 32, 4), (3, 16, 2), (1000, 64, 8), (70, 256, 8)])
+@pytest.mark.parametrize("T,E,KU", [(64, 128, 8), (256, 32, 4), (3, 16, 2), (1000, 64, 8), (70, 256, 8), (4096, 32, 4),
+                                    (4095, 64, 4), (20000, 256, 8)])
 def test_bucket_canonical(dev, T, E, KU):
     rng = np.random.default_rng(T + E)
     ids = rng.integers(0, E, (T, KU)).astype(np.int32)
