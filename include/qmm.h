@@ -337,6 +337,19 @@ int qmm_moe_combine(int64_t tokens, int64_t rows, int64_t H, int KU, const float
 int qmm_moe_combine_gated(int64_t tokens, int64_t rows, int64_t H, int KU, const float *ys, const int32_t *pos,
                           const float *wts, const float *sg, float *y, qmm_stream_t stream);
 
+/* The decode chain's down expert matvecs and combine in one launch: g_moe_dn_{fmt}_k{FE}_r{R} (S/gen_moe.py:535-727,
+ * launch :564) followed by g_moe_combine (S/gen_moe.py:730-762), the reference's last two decode commands
+ * (S/gen_llm.py:5381-5385), fused; the ys buffer between them is not written.
+ *   y[t, c] = fma(wts[t,KU-1], ys[t*KU+KU-1, c], ... fma(wts[t,0], ys[t*KU, c], y0)),
+ *   ys[a] = Wd[e] x[a] + bias[e] (e = clamp(ids[a], 0, E - 1)),  y0 = sg ? sg[t] y[t, c] : accumulate ? y[t, c] : 0
+ * equal bit for bit to qmm_moe_expert_mv[_split](mode 1) then qmm_moe_combine[_gated] (pos NULL). fmt as
+ * qmm_moe_expert_mv plus QMM_MXFP4S (ws its scale planes [E, n, k/32]; ignored otherwise); w [E, n, k]; x [tokens*KU,
+ * k] f32 / bf16 (the gate/up output); ids i32 / wts f32 [tokens, KU]; bias f32 [E, n] or NULL; sg f32 [tokens] or
+ * NULL; y f32 [tokens, n]. tokens <= 65535. */
+int qmm_moe_expert_mv_combine(int fmt, int64_t k, int64_t n, int E, int KU, int64_t tokens, const int32_t *ids,
+                              const float *wts, const void *x, int x_dtype, const void *w, const void *ws,
+                              const float *bias, int accumulate, const float *sg, float *y, qmm_stream_t stream);
+
 /* The routed experts of one MoE layer as one call: the command sequence of the reference's moe_routed
  * (S/gen_llm.py:5324-5385) on one stream, its intermediates (the buffers of moe_alloc, S/gen_llm.py:5388-5432) in the
  * caller's workspace of at least qmm_moe_routed_workspace_size bytes (256-byte aligned):

@@ -2,6 +2,7 @@
 //   qmm_mv             y[t, r] (+)= sum_k x[t, k] W[r, k]        g_mv_{fmt}_k{K}[_t{TG}][_r{R}], S/gen_llm.py:1159-1378
 //   qmm_moe_expert_mv  gu: act[a] = act(Wg[e] x[a/KU], Wu[e] x[a/KU]); dn: ys[a] = Wd[e] x[a]
 //                                                                 g_moe_gu_* / g_moe_dn_*, S/gen_moe.py:535-727
+//   qmm_moe_expert_mv_combine  the dn matvecs and the combine in one launch     + g_moe_combine, S/gen_moe.py:730-762
 //
 // Launch shape (wave64): a workgroup is 4 waves, each wave owns RW consecutive weight rows. A wave walks the row
 // in passes of 64 items (rowdot.hpp), keeps the lane's activation fragments of its TG tokens in registers for all
@@ -150,6 +151,74 @@ __global__ __launch_bounds__(256) void expert_mv_kernel(int64_t n, int64_t assig
   }
 }
 
+// The decode chain's down matvecs and combine in one launch: workgroup (row block, token t) runs one wave per
+// routed slot j of t, all over the same RW rows. Each wave does expert_mv_kernel's per-lane arithmetic and
+// butterfly for its assignment t*KU + j (so its row sums are the separate call's ys, bit for bit); one lane a
+// row then folds the KU sums with the combine's fma chain in slot order.
+template <class P, int RW>
+__global__ __launch_bounds__(512) void expert_mv_combine_kernel(int64_t n, int KU, int E, int64_t k,
+                                                                const int32_t *__restrict__ ids,
+                                                                const float *__restrict__ wts,
+                                                                const u8 *__restrict__ x, int64_t x_row_bytes,
+                                                                const u8 *__restrict__ w, const u8 *__restrict__ ws,
+                                                                int64_t rb, int64_t srb, int64_t ebytes,
+                                                                int64_t esbytes, const float *__restrict__ bias,
+                                                                int accumulate, const float *__restrict__ sg,
+                                                                float *__restrict__ y) {
+  __shared__ float part[8][RW];
+  __shared__ float slot_w[8];
+  const int lane = threadIdx.x & 63;
+  const int j = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: ids / wts / expert in SGPRs
+  const int64_t t = blockIdx.y;
+  const int64_t row0 = (int64_t)blockIdx.x * RW;
+  const int64_t a = t * KU + j;
+  int e = ids[a];
+  e = e < 0 ? 0 : (e >= E ? E - 1 : e);
+  const float wj = wts[a];
+  // the combine's starting value, loaded ahead of the weights (lane r: row row0 + r)
+  float y0 = 0.f;
+  if (accumulate && j == 0 && lane < RW && row0 + lane < n) {
+    y0 = y[t * n + row0 + lane];
+    if (sg) y0 = y0 * sg[t];
+  }
+  const u8 *xr = x + a * x_row_bytes;
+  const u8 *we = w + e * ebytes, *wse = ws + e * esbytes;
+  const int nitems = P::items(k);
+  float ag[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) ag[r] = 0.f;
+  for (int it0 = 0; it0 < nitems; it0 += 64) {
+    const int item = it0 + lane;
+    const bool live = item < nitems;
+    typename P::X xs;
+    P::load_x(xr, item, live, xs);
+    typename P::W wg[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+      P::load_w(we + (row0 + r) * rb, wse + (row0 + r) * srb, item, live && (row0 + r) < n, wg[r]);
+#pragma unroll
+    for (int r = 0; r < RW; ++r) ag[r] += P::dot(wg[r], xs, item);
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r) ag[r] = wave_sum(ag[r]);
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int64_t row = row0 + r;
+    if (lane == r) {
+      float g = ag[r];
+      if (bias && row < n) g += bias[e * n + row];
+      part[j][r] = g;
+    }
+  }
+  if (lane == 0) slot_w[j] = wj;
+  __syncthreads();
+  if (threadIdx.x < RW && row0 + threadIdx.x < n) {
+    float acc = y0;
+    for (int i = 0; i < KU; ++i) acc = __builtin_fmaf(slot_w[i], part[i][threadIdx.x], acc);
+    y[t * n + row0 + threadIdx.x] = acc;
+  }
+}
+
 template <class P, int TG>
 int launch_mv(int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int64_t x_row_bytes,
               const void *w, const void *ws, int64_t rb, int64_t srb, float *y, hipStream_t s) {
@@ -261,6 +330,34 @@ int dispatch_expert(bool gu, bool bf, int64_t k, int64_t n, int E, int KU, int64
   return bf ? launch_expert<P<true>, false>(k, n, E, KU, assignments, ids, x, xb, w, ws, w2, ws2, rb, srb, ebytes, esbytes, bias, bias2, act, y, s)
             : launch_expert<P<false>, false>(k, n, E, KU, assignments, ids, x, xb, w, ws, w2, ws2, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
 }
+
+template <template <bool> class P, int RW>
+int launch_expert_combine_rw(bool bf, int64_t k, int64_t n, int E, int KU, int64_t tokens, const int32_t *ids,
+                             const float *wts, const void *x, const void *w, const void *ws, int64_t rb, int64_t srb,
+                             const float *bias, int accumulate, const float *sg, float *y, hipStream_t s) {
+  const dim3 grid((unsigned)((n + RW - 1) / RW), (unsigned)tokens);
+  const int64_t xb = k * (bf ? 2 : 4);
+  const u8 *xp = static_cast<const u8 *>(x), *wp = static_cast<const u8 *>(w), *wsp = static_cast<const u8 *>(ws);
+  if (bf)
+    expert_mv_combine_kernel<P<true>, RW><<<grid, 64 * KU, 0, s>>>(n, KU, E, k, ids, wts, xp, xb, wp, wsp, rb, srb,
+                                                                   rb * n, srb * n, bias, accumulate, sg, y);
+  else
+    expert_mv_combine_kernel<P<false>, RW><<<grid, 64 * KU, 0, s>>>(n, KU, E, k, ids, wts, xp, xb, wp, wsp, rb, srb,
+                                                                    rb * n, srb * n, bias, accumulate, sg, y);
+  return launch_status();
+}
+
+// Rows a wave: four, or eight where one pass over a row keeps at most half the wave's lanes busy (Q4_K FE = 768:
+// 12 items a row), so each lane has twice the weight loads in flight (measured: Qwen3-30B-A3B Q4_K decode chain at
+// one token 26.3 -> 24.8 us, at eight 149.8 -> 140.3 us; gpt-oss-20b MXFP4, 90 items a row, is slower with eight).
+template <template <bool> class P>
+int launch_expert_combine(bool bf, int64_t k, int64_t n, int E, int KU, int64_t tokens, const int32_t *ids,
+                          const float *wts, const void *x, const void *w, const void *ws, int64_t rb, int64_t srb,
+                          const float *bias, int accumulate, const float *sg, float *y, hipStream_t s) {
+  if (P<false>::items(k) <= 32)
+    return launch_expert_combine_rw<P, 8>(bf, k, n, E, KU, tokens, ids, wts, x, w, ws, rb, srb, bias, accumulate, sg, y, s);
+  return launch_expert_combine_rw<P, 4>(bf, k, n, E, KU, tokens, ids, wts, x, w, ws, rb, srb, bias, accumulate, sg, y, s);
+}
 }  // namespace
 
 // ws / ws2: for QMM_MXFP4S the scale planes come through `w2`-style pairing: w = nibble plane, bias slots unchanged.
@@ -341,4 +438,30 @@ extern "C" int qmm_moe_expert_mv_split(int mode, int fused, int act, int64_t k, 
                                        const float *bias, const float *bias2, float *y, qmm_stream_t stream) {
   return expert_mv_impl(QMM_MXFP4S, mode, fused, act, k, n, E, KU, assignments, ids, x, x_dtype, w, ws, w2, ws2,
                         bias, bias2, y, stream);
+}
+
+extern "C" int qmm_moe_expert_mv_combine(int fmt, int64_t k, int64_t n, int E, int KU, int64_t tokens,
+                                         const int32_t *ids, const float *wts, const void *x, int x_dtype,
+                                         const void *w, const void *ws, const float *bias, int accumulate,
+                                         const float *sg, float *y, qmm_stream_t stream) {
+  if (!valid_fmt(fmt)) return QMM_ERR_FORMAT;
+  if (E <= 0 || E > 1024 || KU <= 0 || KU > 8) return QMM_ERR_RANGE;
+  if (!ids || !wts || !x || !y) return QMM_ERR_NULL;
+  if (n <= 0 || tokens <= 0 || tokens > 65535 || row_bytes(fmt, k) == 0) return QMM_ERR_SHAPE;
+  if (n > (1ll << 30)) return QMM_ERR_SHAPE;
+  if (x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
+  if (int st = check_weights(fmt, k, w, ws)) return st;
+  if (!aligned(x, 16) || !aligned(y, 4)) return QMM_ERR_ALIGN;
+  if (sg) accumulate = 1;   // the gated combine: y = sg[t] y[t] + sum_j ...
+  const int64_t rb = row_bytes(fmt, k), srb = fmt == QMM_MXFP4S ? k / 32 : 0;
+  const void *wsp = fmt == QMM_MXFP4S ? ws : w;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool bf = x_dtype == QMM_BF16;
+  switch (fmt) {
+    case QMM_Q4_K: return launch_expert_combine<Q4K>(bf, k, n, E, KU, tokens, ids, wts, x, w, wsp, rb, srb, bias, accumulate, sg, y, s);
+    case QMM_Q4_0: return launch_expert_combine<Q40>(bf, k, n, E, KU, tokens, ids, wts, x, w, wsp, rb, srb, bias, accumulate, sg, y, s);
+    case QMM_MXFP4: return launch_expert_combine<MXG>(bf, k, n, E, KU, tokens, ids, wts, x, w, wsp, rb, srb, bias, accumulate, sg, y, s);
+    case QMM_Q6_K: return launch_expert_combine<Q6K>(bf, k, n, E, KU, tokens, ids, wts, x, w, wsp, rb, srb, bias, accumulate, sg, y, s);
+    default: return launch_expert_combine<MXS>(bf, k, n, E, KU, tokens, ids, wts, x, w, wsp, rb, srb, bias, accumulate, sg, y, s);
+  }
 }

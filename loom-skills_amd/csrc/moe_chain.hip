@@ -148,22 +148,20 @@ extern "C" int qmm_moe_routed(int fmt, int fmt_down, int fused, int act, int gat
       if ((st = qmm_quant_q8(p.A, FE, a, QMM_F32, aq, stream))) return st;
       st = qmm_moe_expert_mv_q8(fmt_down, 1, 0, act, FE, H, E, KU, p.A, ids, aq, w_down, nullptr, bias_down, nullptr,
                                 ys, stream);
-    } else if (fmt == QMM_MXFP4S) {
-      if ((st = qmm_moe_expert_mv_split(0, fused, act, H, FE, E, KU, p.A, ids, x, x_dtype, w_gate, ws_gate, w_up,
-                                        ws_up, bias_gate, bias_up, a, stream)))
-        return st;
-      st = qmm_moe_expert_mv_split(1, 0, act, FE, H, E, KU, p.A, ids, a, QMM_F32, w_down, ws_down, nullptr, nullptr,
-                                   bias_down, nullptr, ys, stream);
-    } else {
-      if ((st = qmm_moe_expert_mv(fmt, 0, fused, act, H, FE, E, KU, p.A, ids, x, x_dtype, w_gate, w_up, bias_gate,
-                                  bias_up, a, stream)))
-        return st;
-      st = qmm_moe_expert_mv(fmt_down, 1, 0, act, FE, H, E, KU, p.A, ids, a, QMM_F32, w_down, nullptr, bias_down,
-                             nullptr, ys, stream);
+      if (st) return st;
+      return sg ? qmm_moe_combine_gated(T, p.A, H, KU, ys, nullptr, wts, sg, y, stream)
+                : qmm_moe_combine(T, p.A, H, KU, ys, nullptr, wts, accumulate, y, stream);
     }
+    if (fmt == QMM_MXFP4S)
+      st = qmm_moe_expert_mv_split(0, fused, act, H, FE, E, KU, p.A, ids, x, x_dtype, w_gate, ws_gate, w_up, ws_up,
+                                   bias_gate, bias_up, a, stream);
+    else
+      st = qmm_moe_expert_mv(fmt, 0, fused, act, H, FE, E, KU, p.A, ids, x, x_dtype, w_gate, w_up, bias_gate,
+                             bias_up, a, stream);
     if (st) return st;
-    return sg ? qmm_moe_combine_gated(T, p.A, H, KU, ys, nullptr, wts, sg, y, stream)
-              : qmm_moe_combine(T, p.A, H, KU, ys, nullptr, wts, accumulate, y, stream);
+    // the down matvecs and the combine in one launch (the ys rows are not written)
+    return qmm_moe_expert_mv_combine(fmt_down, FE, H, E, KU, T, ids, wts, a, QMM_F32, w_down, ws_down, bias_down,
+                                     accumulate, sg, y, stream);
   }
 
   // ---- prefill: bucket, grouped GEMMs, combine of the sorted rows

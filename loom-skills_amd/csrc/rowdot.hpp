@@ -137,7 +137,7 @@ struct Q4K {
   static constexpr int kValues = 64;
   using X = typename std::conditional<BF16X, XB<8>, XF<8>>::type;
   struct W { u32 h[4], q[8]; };
-  static __device__ __forceinline__ int items(int64_t k) { return (int)(k / 256) * 4; }
+  static __host__ __device__ __forceinline__ int items(int64_t k) { return (int)(k / 256) * 4; }
   static __device__ __forceinline__ void load_x(const void *xrow, int item, bool live, X &x) {
     const int64_t off = (int64_t)(item >> 2) * 256 + 64 * (item & 3);
     if constexpr (BF16X) xb_load<8>(static_cast<const u16 *>(xrow) + off, live, x);
@@ -181,7 +181,7 @@ struct Q40 {
   using XH = typename std::conditional<BF16X, XB<4>, XF<4>>::type;
   struct X { XH blk[2]; };
   struct W { u32 v[9]; };
-  static __device__ __forceinline__ int items(int64_t k) { return (int)(k / 64); }
+  static __host__ __device__ __forceinline__ int items(int64_t k) { return (int)(k / 64); }
   static __device__ __forceinline__ void load_x(const void *xrow, int item, bool live, X &x) {
     const int64_t off = (int64_t)item * 64;
 #pragma unroll
@@ -228,7 +228,7 @@ struct MXFP4 {
   struct XFm { float lo[16], hi[16]; };
   using X = typename std::conditional<BF16X, XBm, XFm>::type;
   struct W { u32 q[4]; u32 e; };
-  static __device__ __forceinline__ int items(int64_t k) { return (int)(k / 32); }
+  static __host__ __device__ __forceinline__ int items(int64_t k) { return (int)(k / 32); }
   static __device__ __forceinline__ void load_x(const void *xrow, int item, bool live, X &x) {
     const int64_t off = (int64_t)item * 32;
     if constexpr (BF16X) {
@@ -353,7 +353,7 @@ struct Q6K {
     float s16[4];   // sums of the four 16-value runs
   };
   using W = Q6W;
-  static __device__ __forceinline__ int items(int64_t k) { return (int)(k / 256) * 4; }
+  static __host__ __device__ __forceinline__ int items(int64_t k) { return (int)(k / 256) * 4; }
   static __device__ __forceinline__ void load_x(const void *xrow, int item, bool live, X &x) {
     const int64_t off = (int64_t)item * 64;
     if constexpr (BF16X) {

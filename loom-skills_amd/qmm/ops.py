@@ -16,6 +16,7 @@ S/ = skills/loom-port-llm/starter/):
     moe_bucket        g_moe_bucket                            S/gen_moe.py:829-955
     moe_expert_mv     g_moe_gu_* / g_moe_dn_*                 S/gen_moe.py:535-727
     moe_expert_mv_q8  g_moe_gu_*_q8_* / g_moe_dn_*_q8_*       S/gen_moe.py:535-727 (MOE_Q8, S/gen_llm.py:5290-5303)
+    moe_expert_mv_combine  g_moe_dn_* + g_moe_combine in one    S/gen_moe.py:535-762 (the decode chain's last two)
     moe_grouped       g_moe_ggu_* / g_moe_gdn_*               S/gen_moe.py:1126-1228
     moe_combine       g_moe_combine[_sorted] [shared_gated]   S/gen_moe.py:730-779, :1231-1280
     moe_prefill       the prefill chain of moe_routed          S/gen_llm.py:5324-5385 (t >= 64)
@@ -407,6 +408,26 @@ def moe_combine(ys, wts, pos=None, y=None, accumulate=False, sg=None):
     return y
 
 
+def moe_expert_mv_combine(fmt, ids, wts, x, w, n, k, E, ws=None, bias=None, y=None, accumulate=False, sg=None):
+    """The decode chain's down matvecs and combine in one launch: y[t] (+)= sum_j wts[t, j] (Wd[e] x[t*KU + j] +
+    bias[e]), e = ids[t, j], equal bit for bit to moe_expert_mv(fmt, 'dn', ...) then moe_combine(...). x f32 / bf16
+    [T*KU, k]; ids i32 / wts f32 [T, KU]; with sg (f32 [T]) y holds the shared experts' output and becomes
+    sg[t] y[t] + sum_j ... Returns y f32 [T, n]."""
+    _dev(ids, wts, x, w, ws, bias, y, sg)
+    if fmt == "mxfp4t":
+        raise ValueError("the decode expert matvecs read split planes (mxfp4s); mxfp4t is the grouped GEMM's layout")
+    T, KU = wts.shape
+    _cols(x, k)
+    if x.shape[0] != T * KU:
+        raise ValueError(f"x has {x.shape[0]} rows, the down matvecs read {T * KU}")
+    if sg is not None and y is None:
+        raise ValueError("the gated combine scales the shared experts' output already in y")
+    y = _out(y, (T, n), torch.float32, x.device)
+    _lib.call("qmm_moe_expert_mv_combine", CODE[fmt], k, n, E, KU, T, _ptr(ids), _ptr(wts), _ptr(x), _dt(x), _ptr(w),
+              _ptr(ws), _ptr(bias), int(bool(accumulate)), _ptr(sg), _ptr(y), _stream())
+    return y
+
+
 def row_scale_f16(x, tile_info=None, x16=None, scales=None, info=None):
     """(x16 f16 [rows, k], scales f32 [rows, 2]) with the per-row power-of-two scale; x f32 or bf16 [rows, k].
     info (i32 [rows, 4], g_row_scale_f16_live): rows with info[row, 2] == 0 are padding, scale 0 and zero values."""
@@ -568,9 +589,10 @@ def moe_decode(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=
         return y, {"ids": ids, "wts": wts, "logits": logits, "act": a, "ys": ys}
     a = moe_expert_mv(fmt, "gu", ids, x, w_gate, FE, H, E, KU, w2=w_up, ws=ws_gate, ws2=ws_up, fused=fused, act=act,
                       bias=bg, bias2=bu)
-    ys = moe_expert_mv(fmt_down or fmt, "dn", ids, a, w_down, H, FE, E, KU, ws=ws_down, bias=bd)
-    y = moe_combine(ys, wts, y=y, accumulate=y is not None, sg=sg)
-    return y, {"ids": ids, "wts": wts, "logits": logits, "act": a, "ys": ys}
+    # the down matvecs and the combine in one launch (equal bit for bit to moe_expert_mv 'dn' then moe_combine)
+    y = moe_expert_mv_combine(fd, ids, wts, a, w_down, H, FE, E, ws=ws_down, bias=bd, y=y, accumulate=y is not None,
+                              sg=sg)
+    return y, {"ids": ids, "wts": wts, "logits": logits, "act": a}
 
 
 # ---------------------------------------------------------------------------------------------------- dispatch

@@ -122,6 +122,21 @@ def test_argument_validation_without_a_device(lib):
         == st["QMM_ERR_RANGE"]
     assert lib.qmm_moe_expert_mv(3, 0, 0, 0, 64, 8, 4, 2, 4, fake, fake, 0, fake, fake, n, n, fake, n) \
         == st["QMM_ERR_FORMAT"]
+    # fused down matvecs + combine: tiled layouts, KU above 8, null weights, split planes without scales, K, dtype
+    assert lib.qmm_moe_expert_mv_combine(4, 256, 8, 4, 2, 1, fake, fake, fake, 0, fake, fake, n, 0, n, fake, n) \
+        == st["QMM_ERR_FORMAT"]
+    assert lib.qmm_moe_expert_mv_combine(1, 256, 8, 4, 9, 1, fake, fake, fake, 0, fake, n, n, 0, n, fake, n) \
+        == st["QMM_ERR_RANGE"]
+    assert lib.qmm_moe_expert_mv_combine(1, 256, 8, 4, 2, 1, fake, n, fake, 0, fake, n, n, 0, n, fake, n) \
+        == st["QMM_ERR_NULL"]
+    assert lib.qmm_moe_expert_mv_combine(3, 64, 8, 4, 2, 1, fake, fake, fake, 0, fake, n, n, 0, n, fake, n) \
+        == st["QMM_ERR_NULL"]
+    assert lib.qmm_moe_expert_mv_combine(1, 100, 8, 4, 2, 1, fake, fake, fake, 0, fake, n, n, 0, n, fake, n) \
+        == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_moe_expert_mv_combine(1, 256, 8, 4, 2, 70000, fake, fake, fake, 0, fake, n, n, 0, n, fake, n) \
+        == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_moe_expert_mv_combine(1, 256, 8, 4, 2, 1, fake, fake, fake, 1, fake, n, n, 0, n, fake, n) \
+        == st["QMM_ERR_DTYPE"]
     # quantizer / repack shapes
     assert lib.qmm_quant_mxfp8(4, 48, fake, 0, n, fake, fake, n) == st["QMM_ERR_SHAPE"]
     assert lib.qmm_repack_mxfp4(fake, 4, 48, fake, fake, n) == st["QMM_ERR_SHAPE"]

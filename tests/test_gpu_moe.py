@@ -15,7 +15,7 @@ both chains are checked through batch invariance: the rows of a slice equal thos
 import numpy as np
 import pytest
 
-from helpers import assert_close_rel_l2, dev_bf16, dev_f32, dev_u8, host
+from helpers import assert_bits_equal, assert_close_rel_l2, dev_bf16, dev_f32, dev_u8, host
 from oracle import formats as of
 from oracle import ref
 
@@ -337,3 +337,45 @@ def test_moe_prefill_chain_graph_replays_equal_eager(dev, fmt):
         np.testing.assert_array_equal(host(y).view(np.uint32), want.view(np.uint32), err_msg=f"replay {i}")
         ops.quant_mxfp8(x)   # eager work between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("fmt,T,E,KU,H,FE,xdt,mode,bias", [
+    ("mxfp4s", 1, 32, 4, 2880, 2880, "f32", "store", False),
+    ("mxfp4s", 5, 32, 4, 2880, 2880, "f32", "acc", True),
+    ("q4_k", 1, 128, 8, 2048, 768, "f32", "store", False),
+    ("q4_k", 63, 16, 8, 512, 256, "bf16", "gated", True),
+    ("q4_k", 2, 8, 4, 258, 4096, "bf16", "acc", True),      # 64 items a row: four rows a wave
+    ("q6_k", 3, 8, 2, 520, 512, "f32", "store", False),
+    ("q4_0", 7, 16, 6, 256, 320, "f32", "acc", False),
+    ("mxfp4", 2, 8, 3, 130, 160, "bf16", "gated", False),
+])
+def test_expert_mv_combine_equals_separate_calls(dev, fmt, T, E, KU, H, FE, xdt, mode, bias):
+    """The fused down matvecs + combine equal qmm_moe_expert_mv(dn) then qmm_moe_combine[_gated], bit for bit,
+    including rows past the last full row block (H % 4 != 0), out-of-range ids (clamped) and every y mode."""
+    import torch
+    from qmm import synth
+    ops = _ops()
+    rng = np.random.default_rng(T * 131 + E)
+    gfmt = "mxfp4" if fmt == "mxfp4s" else fmt
+    raw = dev_u8(synth.weights(gfmt, rng, E * H, FE), dev)
+    w, ws = (ops.repack_mxfp4(raw, E * H, FE) if fmt == "mxfp4s" else (raw, None))
+    ids = rng.integers(0, E, (T, KU)).astype(np.int32)
+    ids[0, 0] = E + 3            # clamped to E - 1
+    if KU > 1:
+        ids[-1, KU - 1] = -2     # clamped to 0
+    wts = rng.random((T, KU)).astype(np.float32)
+    a = rng.standard_normal((T * KU, FE)).astype(np.float32)
+    x = dev_f32(a, dev) if xdt == "f32" else dev_bf16(synth.to_bf16_bits(a), dev)
+    b = dev_f32(rng.standard_normal((E, H)).astype(np.float32), dev) if bias else None
+    y0 = rng.standard_normal((T, H)).astype(np.float32)
+    sg = dev_f32(rng.random(T).astype(np.float32), dev) if mode == "gated" else None
+    idt, wt = torch.from_numpy(ids).to(dev), dev_f32(wts, dev)
+    ys = ops.moe_expert_mv(fmt, "dn", idt.reshape(-1), x, w, H, FE, E, KU, ws=ws, bias=b)
+    want = dev_f32(y0, dev) if mode != "store" else None
+    want = ops.moe_combine(ys, wt, y=want, accumulate=mode == "acc", sg=sg)
+    for rep in range(2):         # a second call on the same output buffer (no state carried between calls)
+        got = dev_f32(y0, dev) if mode != "store" else torch.full((T, H), float("nan"), device=dev)
+        got = ops.moe_expert_mv_combine(fmt, idt, wt, x, w, H, FE, E, ws=ws, bias=b, y=got,
+                                        accumulate=mode == "acc", sg=sg)
+        torch.cuda.synchronize()
+        assert_bits_equal(host(got), host(want), f"{fmt} T={T} KU={KU} {mode} call {rep}")
