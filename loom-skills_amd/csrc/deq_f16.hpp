@@ -32,6 +32,23 @@ __device__ __forceinline__ f16x8 deq8(u32 q0, u32 q1, h2 dsc, h2 nmn) {
   return deq8_codes(HI ? (q0 >> 4) & 0x0F0F0F0Fu : q0 & 0x0F0F0F0Fu, HI ? (q1 >> 4) & 0x0F0F0F0Fu : q1 & 0x0F0F0F0Fu,
                     dsc, nmn);
 }
+// The same 8 weights with the codes converted by the FP8 converter: a code byte 0000qqqq read as OCP E4M3 is
+// q 2^-9 exactly, so v_cvt_scalef32_pk_f16_fp8 with scale 512 gives two f16 codes an instruction (where the
+// (1024 + q) route takes a v_perm and an add); then the same one rounding fma.
+template <bool HI>
+__device__ __forceinline__ f16x8 deq8_e4m3(u32 q0, u32 q1, h2 dsc, h2 nmn) {
+  const u32 n0 = HI ? (q0 >> 4) & 0x0F0F0F0Fu : q0 & 0x0F0F0F0Fu;
+  const u32 n1 = HI ? (q1 >> 4) & 0x0F0F0F0Fu : q1 & 0x0F0F0F0Fu;
+  const h2 c[4] = {__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(n0, 512.0f, false),
+                   __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(n0, 512.0f, true),
+                   __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(n1, 512.0f, false),
+                   __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(n1, 512.0f, true)};
+  u32 o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = as_u32(__builtin_elementwise_fma(c[i], dsc, nmn));
+  typedef __attribute__((ext_vector_type(4))) u32 u32x4;
+  return __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]});
+}
 // Q4_0: 8 f16 weights from two code dwords: (1024 + q) - 1032 = q - 8 exactly, then one rounding f16 multiply by d
 // (f16(d (q - 8)), the reference's staging, also where -8 d would overflow f16)
 template <bool HI>

@@ -53,22 +53,6 @@ struct DArgs {
 
 typedef __attribute__((ext_vector_type(4))) u32 u32x4;
 
-// 8 staged f16 weights of one column from two code dwords (low or high nibbles): 0000qqqq as E4M3 is q 2^-9, the
-// conversion's scale 512 makes it q; then one rounding fma with the sub-block's (d sc, -dmin m)
-template <bool HI>
-__device__ __forceinline__ f16x8 deq8_e4m3(u32 q0, u32 q1, h2 dsc, h2 nmn) {
-  const u32 n0 = HI ? (q0 >> 4) & 0x0F0F0F0Fu : q0 & 0x0F0F0F0Fu;
-  const u32 n1 = HI ? (q1 >> 4) & 0x0F0F0F0Fu : q1 & 0x0F0F0F0Fu;
-  const h2 c[4] = {__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(n0, 512.0f, false),
-                   __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(n0, 512.0f, true),
-                   __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(n1, 512.0f, false),
-                   __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(n1, 512.0f, true)};
-  u32 o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = as_u32(__builtin_elementwise_fma(c[i], dsc, nmn));
-  return __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]});
-}
-
 // the eight (f16(d sc_g), f16(-dmin m_g)) pairs of a super-block header, g = 0..7, as (dsc | nmn << 16)
 __device__ __forceinline__ void header_pairs(const uint4 &hd, u32 (&out)[8]) {
   const u32 sc_lo = hd.y & 0x3F3F3F3Fu, mn_lo = hd.z & 0x3F3F3F3Fu;

@@ -474,6 +474,9 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
   }
   const float bg = a.bias ? a.bias[(int64_t)expert * N + col] : 0.f;
   const float bu = (GU && a.bias2) ? a.bias2[(int64_t)expert * N + col] : 0.f;
+  // the bias loads complete here, once: otherwise every store below, each behind its own row branch, waits for
+  // them with vmcnt(0), which also waits for the stores before it
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll

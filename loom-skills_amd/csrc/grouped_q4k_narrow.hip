@@ -62,6 +62,7 @@ struct NArgs {
   const int32_t *tile_info, *rowmap;
   const float *bias, *bias2;   // [E, N] or NULL
   int KU, E, act;
+  u32 ku_magic;                // ceil(2^32 / KU) for KU > 1: token = umulhi(assignment, ku_magic)
   float *y;                    // [max_tiles * 64, N]
   int tiles, col_blocks;       // tiles of the table; workgroups across N per row group
   int rg_outer;                // grid order: row groups outermost (few rows an expert) or beside their tile
@@ -105,7 +106,8 @@ __device__ __forceinline__ void group_step(const uint4 (&cq)[2], const h2 (&dsc)
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
         const u32 w0 = half ? cq[g].z : cq[g].x, w1 = half ? cq[g].w : cq[g].y;
-        const f16x8 aw = nib ? deq8<true>(w0, w1, dsc[g][1], nmn[g][1]) : deq8<false>(w0, w1, dsc[g][0], nmn[g][0]);
+        const f16x8 aw = nib ? deq8_e4m3<true>(w0, w1, dsc[g][1], nmn[g][1])
+                             : deq8_e4m3<false>(w0, w1, dsc[g][0], nmn[g][0]);
         acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw, bx, acc[g], 0, 0, 0);
       }
     }
@@ -158,7 +160,7 @@ __global__ __launch_bounds__(64 * NW) void q4k_narrow_kernel(NArgs a) {
     }
   }
   const int expert0 = a.tile_info[2 * tile], tile_rows = a.tile_info[2 * tile + 1];
-  if (expert0 < 0 || kGroupRows * rg >= tile_rows) return;   // uniform over the workgroup
+  if ((expert0 < 0) | (kGroupRows * rg >= tile_rows)) return;   // uniform over the workgroup; one load for both
   const int expert = expert0 >= a.E ? a.E - 1 : expert0;
   const int r0 = tile * kTileRows + kGroupRows * rg;
 
@@ -199,7 +201,6 @@ __global__ __launch_bounds__(64 * NW) void q4k_narrow_kernel(NArgs a) {
   const int cf = 512 + 16 * (4 * lc + q), chh = 256 + 512 * (q >> 1) + 16 * (2 * lc + (q & 1));
   const int hf = 16 * (2 * lc + (q >> 1)), hh = 16 * lc;
   uint4 cring[DEPTH][2], hring[DEPTH][2], hnext[2];
-  constexpr int kPrefetchLoads = TILED ? 10 : 4 * DEPTH;   // the vector loads prefetch() issues
   auto prefetch = [&]() __attribute__((always_inline)) {
     if constexpr (TILED) {   // unit 0 (or the half unit when K == 256): header, then codes, as the loop issues them
 #pragma unroll
@@ -216,20 +217,43 @@ __global__ __launch_bounds__(64 * NW) void q4k_narrow_kernel(NArgs a) {
     }
   };
 
-  // ---- the row group's activation rows into LDS (rows without an assignment: zeros, not read), then the weight
-  // prefetch. gu: row i of the group is assignment rowmap[r0 + i], of token rowmap[r0 + i] / KU; dn: the sorted row
-  // r0 + i itself, staged without waiting for the row map when 16 rg + i < tile_rows (the bucket fills a tile's rows
-  // from the top); the row map decides which rows are stored (src_row >= 0). The staging loads go out before the
-  // weight prefetch: a load's wait counts every load issued before it, so staged after the prefetch they would
-  // wait for the weights' HBM latency.
+  // ---- the weight prefetch first (it needs only the expert), then the row group's rows and inverse scales as
+  // scalar loads (uniform addresses: they do not enter the vector load counter, so reading them does not wait for
+  // the weights), then the activation rows into LDS (rows without an assignment: zeros, not read). gu: row i of the
+  // group is assignment rowmap[r0 + i], of token rowmap[r0 + i] / KU; dn: the sorted row r0 + i itself when
+  // 16 rg + i < tile_rows (the bucket fills a tile's rows from the top); the row map decides which rows are stored.
+  prefetch();
+  __builtin_amdgcn_sched_barrier(0);
   auto dn_row = [&](int i) { return kGroupRows * rg + i < tile_rows && r0 + i < a.x_rows ? r0 + i : -1; };
-  // every thread reads its own staging row's entries (no barrier, no divergent branch whose join would wait for
-  // the loads): the row map, the row (gu: the token, which needs the row map first), its inverse scale
-  const int rm_own = a.rowmap[r0 + (tid & 15)];
-  int srow;
-  if constexpr (KIND == kNGU) srow = rm_own >= 0 && rm_own / a.KU < a.x_rows ? rm_own / a.KU : -1;
-  else srow = dn_row(tid & 15);
-  const float inv_load = a.scales ? a.scales[2 * (srow >= 0 ? srow : 0) + 1] : 1.f;
+  const int own = tid & 15;   // the row this thread stages
+  int rmv[kGroupRows], srv[kGroupRows];
+  float invv[kGroupRows];
+#pragma unroll
+  for (int i = 0; i < kGroupRows; ++i) rmv[i] = a.rowmap[r0 + i];   // all issued before any is used
+#pragma unroll
+  for (int i = 0; i < kGroupRows; ++i) {
+    if constexpr (KIND == kNGU) {
+      const int tok = a.KU == 1 ? rmv[i] : (int)__umulhi((u32)rmv[i], a.ku_magic);
+      srv[i] = (rmv[i] >= 0) & (tok < a.x_rows) ? tok : -1;
+    } else {
+      srv[i] = dn_row(i);
+    }
+  }
+  if (a.scales) {
+#pragma unroll
+    for (int i = 0; i < kGroupRows; ++i) invv[i] = a.scales[2 * (srv[i] >= 0 ? srv[i] : 0) + 1];
+  } else {
+#pragma unroll
+    for (int i = 0; i < kGroupRows; ++i) invv[i] = 1.f;
+  }
+  int rm_own = rmv[0], srow = srv[0];
+  float inv_own = invv[0];
+#pragma unroll
+  for (int i = 1; i < kGroupRows; ++i) {
+    rm_own = own == i ? rmv[i] : rm_own;
+    srow = own == i ? srv[i] : srow;
+    inv_own = own == i ? invv[i] : inv_own;
+  }
   {
     // 16-byte chunks of the panel, row fastest: thread t stages chunks t, t + NT, ... (16 K / 8 / NT of them).
     // The loads go through a buffer resource over the activation rows; a row past them (or, for gu, without an
@@ -250,14 +274,12 @@ __global__ __launch_bounds__(64 * NW) void q4k_narrow_kernel(NArgs a) {
           (int)(srow >= 0 ? rbase + 16u * (u32)(c >> 4) : rbase), 0, 0, 0);
     }
   }
-  __builtin_amdgcn_sched_barrier(0);   // the weight prefetch goes out after the staging loads
-  prefetch();
   if (tid < kGroupRows) {   // the rows the epilogue stores, with their inverse scales
     src_row[tid] = rm_own >= 0 ? srow : -1;
-    rinv[tid] = srow >= 0 ? inv_load : 1.f;
+    rinv[tid] = srow >= 0 ? inv_own : 1.f;
   }
-  // the staging loads are complete when at most the prefetch's loads are outstanding (vmcnt counts in issue order)
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(kPrefetchLoads));
+  // the weight prefetch and the staging loads (the first unit needs both)
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   __syncthreads();
 
   f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
@@ -351,10 +373,10 @@ __global__ __launch_bounds__(64 * NW) void q4k_narrow_kernel(NArgs a) {
 
   // ---- epilogue: lane (lc, q) holds output columns 4 q .. 4 q + 3 of its group for row r0 + lc
   const int src = src_row[lc];
-  if (src < 0) return;
   const float inv = rinv[lc];
   float *yrow = a.y + (int64_t)(r0 + lc) * N;
   if constexpr (KIND == kNGU) {
+    if (src < 0) return;
     const int f = c0 + 4 * q;
     if (f >= N) return;
     f32x4 o;
@@ -366,14 +388,21 @@ __global__ __launch_bounds__(64 * NW) void q4k_narrow_kernel(NArgs a) {
     }
     *reinterpret_cast<f32x4 *>(yrow + f) = o;
   } else {
+    if (src >= 0) {
+      // both groups' outputs (and their bias loads) before any store, so no store waits for another
+      f32x4 o[2];
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      const int f = c0 + 16 * g + 4 * q;
-      if (f >= N) continue;
-      f32x4 o;
+      for (int g = 0; g < 2; ++g) {
+        const int f = c0 + 16 * g + 4 * q, fb = f < N ? f : 0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = acc[g][i] * inv + (a.bias ? a.bias[(int64_t)expert * N + f + i] : 0.f);
-      *reinterpret_cast<f32x4 *>(yrow + f) = o;
+        for (int i = 0; i < 4; ++i) o[g][i] = acc[g][i] * inv + (a.bias ? a.bias[(int64_t)expert * N + fb + i] : 0.f);
+      }
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const int f = c0 + 16 * g + 4 * q;
+        if (f >= N) continue;
+        *reinterpret_cast<f32x4 *>(yrow + f) = o[g];
+      }
     }
   }
 }
@@ -422,6 +451,7 @@ int qmm_grouped_q4k_narrow(int tiled, int mode, int fused, int act, int64_t max_
   a.N = (int)n; a.K = (int)k;
   a.x16 = static_cast<const _Float16 *>(x); a.scales = x_scales; a.x_rows = (int)x_rows;
   a.tile_info = tile_info; a.rowmap = rowmap; a.KU = KU; a.E = E; a.act = act; a.y = y;
+  a.ku_magic = KU > 1 ? (u32)((0x100000000ull + (unsigned long long)KU - 1) / (unsigned long long)KU) : 0u;   // exact below 2^24
   a.bias = bias; a.bias2 = mode == 0 ? bias2 : nullptr;
   a.w = static_cast<const u8 *>(w);
   a.tiles = (int)max_tiles;
