@@ -349,7 +349,9 @@ class MoeWorkload:
         torch.cuda.synchronize()
         self.experts_hit = int(torch.unique(mid["ids"]).numel())
         self.mid = mid
-        # inputs of the dominant kernel (the gate/up GEMM or expert matvec) for its own timing
+        # inputs of the dominant kernel (the gate/up GEMM or expert matvec) for its own timing; the decode chain
+        # routes inside its gate/up matvecs where ops.moe_decode does
+        self.route_gu = self.decode and self.E <= ops.ROUTE_GU_MAX_E and self.T * self.KU <= ops.ROUTE_GU_MAX_A
         if self.decode:
             self.gu_y = torch.empty_like(mid["act"])
         elif self.fmt == "mxfp4t":
@@ -368,7 +370,11 @@ class MoeWorkload:
 
     def kernel_step(self, i):
         kw = self.kws[i % self.copies]
-        if self.decode:   # the gate/up expert matvecs of the decode chain
+        if self.decode and self.route_gu:   # the decode chain's gate/up expert matvecs, routing their own tokens
+            self.ops.moe_topk_expert_mv(self.fmt, self.logits, self.KU, self.d["gating"], self.d["norm"], self.x,
+                                        kw["w_gate"], self.FE, self.H, self.E, w2=kw.get("w_up"), ws=kw.get("ws_gate"),
+                                        fused=kw["fused"], act=kw["act"], y=self.gu_y)
+        elif self.decode:   # the gate/up expert matvecs of the decode chain
             self.ops.moe_expert_mv(self.fmt, "gu", self.mid["ids"], self.x, kw["w_gate"], self.FE, self.H, self.E,
                                    self.KU, w2=kw.get("w_up"), ws=kw.get("ws_gate"), fused=kw["fused"],
                                    act=kw["act"], y=self.gu_y)

@@ -337,6 +337,18 @@ int qmm_moe_combine(int64_t tokens, int64_t rows, int64_t H, int KU, const float
 int qmm_moe_combine_gated(int64_t tokens, int64_t rows, int64_t H, int KU, const float *ys, const int32_t *pos,
                           const float *wts, const float *sg, float *y, qmm_stream_t stream);
 
+/* The decode chain's routing and gate/up expert matvecs in one launch: g_moe_route (S/gen_moe.py:116-500) over given
+ * logits followed by g_moe_gu_{fmt}[_fused]_k{H}_r{R} (S/gen_moe.py:535-727, launch :564), the reference's first
+ * decode commands (S/gen_llm.py:5373-5381), fused. The routing arguments as qmm_moe_topk (ids / wts are written as
+ * it writes them), then the gate/up matvec's as qmm_moe_expert_mv_split with mode 0 (fmt any qmm_moe_expert_mv
+ * format or QMM_MXFP4S with its scale planes ws / ws2; w2 / ws2 ignored when fused): act[a] for the tokens * KU
+ * assignments, each workgroup ranking its token's logits itself. Equal bit for bit to qmm_moe_topk then
+ * qmm_moe_expert_mv[_split](mode 0). */
+int qmm_moe_topk_expert_mv(const float *logits, int64_t tokens, int E, int KU, int gating, int norm, float scale,
+                           const float *router_bias, int32_t *ids, float *wts, int fmt, int fused, int act, int64_t k,
+                           int64_t n, const void *x, int x_dtype, const void *w, const void *ws, const void *w2,
+                           const void *ws2, const float *bias, const float *bias2, float *y, qmm_stream_t stream);
+
 /* The decode chain's down expert matvecs and combine in one launch: g_moe_dn_{fmt}_k{FE}_r{R} (S/gen_moe.py:535-727,
  * launch :564) followed by g_moe_combine (S/gen_moe.py:730-762), the reference's last two decode commands
  * (S/gen_llm.py:5381-5385), fused; the ys buffer between them is not written.

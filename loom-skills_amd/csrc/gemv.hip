@@ -12,6 +12,7 @@
 #include <type_traits>
 
 #include "rowdot.hpp"
+#include "topk.hpp"
 
 using namespace qmm;
 
@@ -87,8 +88,19 @@ __device__ __forceinline__ float act_fn(int act, float g, float u) {
   return g / (1.0f + expf(-g)) * u;
 }
 
+// The routing of the gate/up matvec that selects its own experts (NS > 0): every wave ranks its token's logits
+// (topk_select, the routing kernels' arithmetic) and takes pick a % KU; row block 0's first wave writes ids / wts.
+struct RouteArgs {
+  const float *logits;   // [tokens, E]
+  int gating, norm;
+  float scale;
+  const float *bias;     // router bias [E] or NULL
+  int32_t *ids;          // out: [tokens, KU]
+  float *wts;            // out: [tokens, KU]
+};
+
 // One assignment per workgroup row (blockIdx.x), RW output rows per wave.
-template <class P, int RW, bool GU>
+template <class P, int RW, bool GU, int NS = 0>
 __global__ __launch_bounds__(256) void expert_mv_kernel(int64_t n, int64_t assignments, int KU, int E, int64_t k,
                                                         const int32_t *__restrict__ ids, const u8 *__restrict__ x,
                                                         int64_t x_row_bytes, const u8 *__restrict__ w,
@@ -96,13 +108,35 @@ __global__ __launch_bounds__(256) void expert_mv_kernel(int64_t n, int64_t assig
                                                         const u8 *__restrict__ ws2, int64_t rb, int64_t srb,
                                                         int64_t ebytes, int64_t esbytes, const float *__restrict__ bias,
                                                         const float *__restrict__ bias2, int act, int accumulate,
-                                                        float *__restrict__ y) {
+                                                        float *__restrict__ y, RouteArgs route = {}) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t a = blockIdx.x;
   const int64_t row0 = ((int64_t)blockIdx.y * kWavesPerBlock + wave) * RW;
-  if (row0 >= n || a >= assignments) return;
-  int e = ids ? ids[a] : 0;                // no ids: one expert (the dense swiglu matvec)
+  if constexpr (NS > 0) {
+    if (a >= assignments) return;
+  } else {
+    if (row0 >= n || a >= assignments) return;
+  }
+  int e;
+  if constexpr (NS > 0) {
+    __shared__ __align__(16) uint64_t keys[kWavesPerBlock][64 * NS];
+    int rank[NS];
+    float wo[NS];
+    bool pick[NS];
+    const int64_t t = a / KU;
+    topk_select<NS>(route.logits + t * E, E, KU, route.gating, route.norm, route.scale, route.bias, keys[wave], rank,
+                    wo, pick);
+    float wt;
+    topk_pick<NS>(rank, wo, pick, (int)(a % KU), e, wt);
+    if (blockIdx.y == 0 && wave == 0 && lane == 0) {
+      route.ids[a] = e;
+      route.wts[a] = wt;
+    }
+    if (row0 >= n) return;
+  } else {
+    e = ids ? ids[a] : 0;                    // no ids: one expert (the dense swiglu matvec)
+  }
   e = e < 0 ? 0 : (e >= E ? E - 1 : e);   // ids are clamped into range as the reference does (S/gen_moe.py:592-596)
   const u8 *xr = x + (GU ? a / KU : a) * x_row_bytes;
   const u8 *we = w + e * ebytes, *wse = ws + e * esbytes;
@@ -305,6 +339,39 @@ int launch_expert(int64_t k, int64_t n, int E, int KU, int64_t assignments, cons
   return launch_status();
 }
 
+// The gate/up expert matvecs routing their own tokens (NS = ceil(E / 64) key slots a lane).
+template <class P, int NS>
+int launch_expert_route(int64_t k, int64_t n, int E, int KU, int64_t assignments, const RouteArgs &r, const void *x,
+                        int64_t x_row_bytes, const void *w, const void *ws, const void *w2, const void *ws2,
+                        int64_t rb, int64_t srb, int64_t ebytes, int64_t esbytes, const float *bias,
+                        const float *bias2, int act, float *y, hipStream_t s) {
+  constexpr int RW = expert_rw<true>();
+  const dim3 grid((unsigned)assignments, (unsigned)((n + kWavesPerBlock * RW - 1) / (kWavesPerBlock * RW)));
+  expert_mv_kernel<P, RW, true, NS><<<grid, 256, 0, s>>>(
+      n, assignments, KU, E, k, nullptr, static_cast<const u8 *>(x), x_row_bytes, static_cast<const u8 *>(w),
+      static_cast<const u8 *>(ws), static_cast<const u8 *>(w2), static_cast<const u8 *>(ws2), rb, srb, ebytes, esbytes,
+      bias, bias2, act, 0, y, r);
+  return launch_status();
+}
+
+template <template <bool> class P>
+int dispatch_route(bool bf, int64_t k, int64_t n, int E, int KU, int64_t assignments, const RouteArgs &r,
+                   const void *x, const void *w, const void *ws, const void *w2, const void *ws2, int64_t rb,
+                   int64_t srb, int64_t ebytes, int64_t esbytes, const float *bias, const float *bias2, int act,
+                   float *y, hipStream_t s) {
+  const int64_t xb = k * (bf ? 2 : 4);
+#define QMM_ROUTE(NS)                                                                                                \
+  (bf ? launch_expert_route<P<true>, NS>(k, n, E, KU, assignments, r, x, xb, w, ws, w2, ws2, rb, srb, ebytes,        \
+                                         esbytes, bias, bias2, act, y, s)                                             \
+      : launch_expert_route<P<false>, NS>(k, n, E, KU, assignments, r, x, xb, w, ws, w2, ws2, rb, srb, ebytes,       \
+                                          esbytes, bias, bias2, act, y, s))
+  if (E <= 64) return QMM_ROUTE(1);
+  if (E <= 128) return QMM_ROUTE(2);
+  if (E <= 192) return QMM_ROUTE(3);
+  return QMM_ROUTE(4);
+#undef QMM_ROUTE
+}
+
 // The dense swiglu matvec: the gate/up expert kernel with one expert (no ids) and one token a row of x.
 template <template <bool> class P>
 int launch_swiglu(bool bf, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, const void *w,
@@ -438,6 +505,46 @@ extern "C" int qmm_moe_expert_mv_split(int mode, int fused, int act, int64_t k, 
                                        const float *bias, const float *bias2, float *y, qmm_stream_t stream) {
   return expert_mv_impl(QMM_MXFP4S, mode, fused, act, k, n, E, KU, assignments, ids, x, x_dtype, w, ws, w2, ws2,
                         bias, bias2, y, stream);
+}
+
+extern "C" int qmm_moe_topk_expert_mv(const float *logits, int64_t tokens, int E, int KU, int gating, int norm,
+                                      float scale, const float *router_bias, int32_t *ids, float *wts, int fmt,
+                                      int fused, int act, int64_t k, int64_t n, const void *x, int x_dtype,
+                                      const void *w, const void *ws, const void *w2, const void *ws2,
+                                      const float *bias, const float *bias2, float *y, qmm_stream_t stream) {
+  // the routing's checks (qmm_moe_topk), then the gate/up matvec's (qmm_moe_expert_mv[_split], mode 0)
+  if (!logits || !ids || !wts) return QMM_ERR_NULL;
+  if (E <= 0 || E > 256 || KU <= 0 || KU > 8 || KU > E) return QMM_ERR_RANGE;
+  if (gating < 1 || gating > 3 || (gating == 1 && router_bias)) return QMM_ERR_RANGE;
+  if (tokens <= 0 || tokens * KU > (1 << 24)) return QMM_ERR_SHAPE;
+  if (!valid_fmt(fmt)) return QMM_ERR_FORMAT;
+  if (act != QMM_ACT_SILU && act != QMM_ACT_SWIGLU_OAI) return QMM_ERR_RANGE;
+  if (!x || !y) return QMM_ERR_NULL;
+  if (n <= 0 || row_bytes(fmt, k) == 0) return QMM_ERR_SHAPE;
+  if (x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
+  if (int st = check_weights(fmt, k, w, ws)) return st;
+  if (!fused && check_weights(fmt, k, w2, ws2) != QMM_OK) return check_weights(fmt, k, w2, ws2);
+  if (!aligned(x, 16) || !aligned(y, 4)) return QMM_ERR_ALIGN;
+  const int64_t rb = row_bytes(fmt, k), srb = fmt == QMM_MXFP4S ? k / 32 : 0;
+  const int64_t ebytes = rb * n * (fused ? 2 : 1), esbytes = srb * n * (fused ? 2 : 1);
+  const void *wu = w2, *wsu = ws2;
+  if (fused) {   // one [E, 2n, k] tensor: expert e's n gate rows, then its n up rows (S/gen_moe.py:538)
+    wu = static_cast<const u8 *>(w) + rb * n;
+    wsu = fmt == QMM_MXFP4S ? static_cast<const u8 *>(ws) + srb * n : nullptr;
+  }
+  if (!wsu) wsu = wu;
+  const void *wsg = fmt == QMM_MXFP4S ? ws : w;
+  const RouteArgs r{logits, gating, norm, scale, router_bias, ids, wts};
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool bf = x_dtype == QMM_BF16;
+  const int64_t A = tokens * KU;
+  switch (fmt) {
+    case QMM_Q4_K: return dispatch_route<Q4K>(bf, k, n, E, KU, A, r, x, w, wsg, wu, wsu, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
+    case QMM_Q4_0: return dispatch_route<Q40>(bf, k, n, E, KU, A, r, x, w, wsg, wu, wsu, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
+    case QMM_MXFP4: return dispatch_route<MXG>(bf, k, n, E, KU, A, r, x, w, wsg, wu, wsu, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
+    case QMM_Q6_K: return dispatch_route<Q6K>(bf, k, n, E, KU, A, r, x, w, wsg, wu, wsu, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
+    default: return dispatch_route<MXS>(bf, k, n, E, KU, A, r, x, w, wsg, wu, wsu, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
+  }
 }
 
 extern "C" int qmm_moe_expert_mv_combine(int fmt, int64_t k, int64_t n, int E, int KU, int64_t tokens,

@@ -124,7 +124,19 @@ extern "C" int qmm_moe_routed(int fmt, int fmt_down, int fused, int act, int gat
   // ---- route; a prefill batch with given logits and bf16 rows also gets the gate/up operand in the same launch
   int st;
   const bool operand = p.prefill && logits && x_dtype == QMM_BF16 && H <= 4096 && H % (p.mx ? 32 : 8) == 0;
-  if (operand)
+  // decode with given logits on f32 / bf16 activations, one key slot a lane and few assignments: the routing runs
+  // inside the gate/up matvecs (every workgroup ranks its token itself: gpt-oss-20b at one token 25.0 -> 23.9 us;
+  // slower with 128 experts or eight tokens)
+  const bool route_gu = !p.prefill && !p.q8 && logits && E <= 64 && p.A <= 8;
+  if (route_gu)
+    st = fmt == QMM_MXFP4S
+             ? qmm_moe_topk_expert_mv(logits, T, E, KU, gating, norm, scale, router_bias, ids, wts, fmt, fused, act, H,
+                                      FE, x, x_dtype, w_gate, ws_gate, w_up, ws_up, bias_gate, bias_up,
+                                      static_cast<float *>(at(p.act)), stream)
+             : qmm_moe_topk_expert_mv(logits, T, E, KU, gating, norm, scale, router_bias, ids, wts, fmt, fused, act, H,
+                                      FE, x, x_dtype, w_gate, nullptr, w_up, nullptr, bias_gate, bias_up,
+                                      static_cast<float *>(at(p.act)), stream);
+  else if (operand)
     st = qmm_moe_topk_operand(logits, T, E, KU, gating, norm, scale, router_bias, ids, wts, H, x, x_dtype,
                               p.mx ? QMM_MXFP8 : QMM_F16, at(p.xa), at(p.xs), stream);
   else if (logits)
@@ -152,7 +164,9 @@ extern "C" int qmm_moe_routed(int fmt, int fmt_down, int fused, int act, int gat
       return sg ? qmm_moe_combine_gated(T, p.A, H, KU, ys, nullptr, wts, sg, y, stream)
                 : qmm_moe_combine(T, p.A, H, KU, ys, nullptr, wts, accumulate, y, stream);
     }
-    if (fmt == QMM_MXFP4S)
+    if (route_gu)
+      st = QMM_OK;   // the gate/up matvecs ran with the routing
+    else if (fmt == QMM_MXFP4S)
       st = qmm_moe_expert_mv_split(0, fused, act, H, FE, E, KU, p.A, ids, x, x_dtype, w_gate, ws_gate, w_up, ws_up,
                                    bias_gate, bias_up, a, stream);
     else

@@ -16,6 +16,7 @@ S/ = skills/loom-port-llm/starter/):
     moe_bucket        g_moe_bucket                            S/gen_moe.py:829-955
     moe_expert_mv     g_moe_gu_* / g_moe_dn_*                 S/gen_moe.py:535-727
     moe_expert_mv_q8  g_moe_gu_*_q8_* / g_moe_dn_*_q8_*       S/gen_moe.py:535-727 (MOE_Q8, S/gen_llm.py:5290-5303)
+    moe_topk_expert_mv     g_moe_route + g_moe_gu_* in one       S/gen_moe.py:116-727 (the decode chain's first two)
     moe_expert_mv_combine  g_moe_dn_* + g_moe_combine in one    S/gen_moe.py:535-762 (the decode chain's last two)
     moe_grouped       g_moe_ggu_* / g_moe_gdn_*               S/gen_moe.py:1126-1228
     moe_combine       g_moe_combine[_sorted] [shared_gated]   S/gen_moe.py:730-779, :1231-1280
@@ -408,6 +409,29 @@ def moe_combine(ys, wts, pos=None, y=None, accumulate=False, sg=None):
     return y
 
 
+def moe_topk_expert_mv(fmt, logits, KU, gating, norm, x, w, n, k, E, w2=None, ws=None, ws2=None, fused=False,
+                       act="silu", bias=None, bias2=None, scale=1.0, router_bias=None, y=None):
+    """The decode chain's routing and gate/up expert matvecs in one launch: (ids, wts, act) equal bit for bit to
+    moe_topk(logits, KU, gating, norm, scale, router_bias) then moe_expert_mv(fmt, 'gu', ids, x, w, n, k, E, KU, ...).
+    logits f32 [T, E]; x f32 / bf16 [T, k]; act f32 [T*KU, n]."""
+    _dev(logits, x, w, w2, ws, ws2, bias, bias2, router_bias, y)
+    if fmt == "mxfp4t":
+        raise ValueError("the decode expert matvecs read split planes (mxfp4s); mxfp4t is the grouped GEMM's layout")
+    T, E_ = logits.shape
+    if E_ != E:
+        raise ValueError(f"logits have {E_} experts, E is {E}")
+    _cols(x, k)
+    if x.shape[0] != T:
+        raise ValueError(f"x has {x.shape[0]} rows, the logits {T}")
+    ids = torch.empty((T, KU), dtype=torch.int32, device=x.device)
+    wts = torch.empty((T, KU), dtype=torch.float32, device=x.device)
+    y = _out(y, (T * KU, n), torch.float32, x.device)
+    _lib.call("qmm_moe_topk_expert_mv", _ptr(logits), T, E, KU, gating, int(bool(norm)), float(scale),
+              _ptr(router_bias), _ptr(ids), _ptr(wts), CODE[fmt], int(fused), ACT[act], k, n, _ptr(x), _dt(x), _ptr(w),
+              _ptr(ws), _ptr(w2), _ptr(ws2), _ptr(bias), _ptr(bias2), _ptr(y), _stream())
+    return ids, wts, y
+
+
 def moe_expert_mv_combine(fmt, ids, wts, x, w, n, k, E, ws=None, bias=None, y=None, accumulate=False, sg=None):
     """The decode chain's down matvecs and combine in one launch: y[t] (+)= sum_j wts[t, j] (Wd[e] x[t*KU + j] +
     bias[e]), e = ids[t, j], equal bit for bit to moe_expert_mv(fmt, 'dn', ...) then moe_combine(...). x f32 / bf16
@@ -560,6 +584,10 @@ def moe_prefill(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up
 
 
 Q8_FORMATS = ("q4_0", "q4_k", "q6_k")   # formats with integer-code expert matvecs (gen_llm ICODES)
+# The decode chain routes inside its gate/up matvecs (every workgroup ranks its token's logits itself) where that is
+# cheaper than a routing launch: one key slot a lane and few assignments (gpt-oss-20b at one token: 25.0 -> 23.9 us;
+# Qwen3-30B-A3B at one token, 128 experts, 24.8 -> 25.5 us, and either at eight tokens +14 to +26 us)
+ROUTE_GU_MAX_E, ROUTE_GU_MAX_A = 64, 8
 
 
 def moe_decode(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=None, ws_gate=None, ws_down=None,
@@ -578,8 +606,18 @@ def moe_decode(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=
         q8 = fmt in Q8_FORMATS and fd in Q8_FORMATS and expert_bias is None
     if q8 and (fmt not in Q8_FORMATS or fd not in Q8_FORMATS):
         raise ValueError(f"the int8 expert matvecs take {Q8_FORMATS} (gate/up {fmt}, down {fd})")
-    ids, wts, logits = _route(x, logits, KU, gating, norm, scale, bias, router, down_scale)
     bg, bu, bd = expert_bias if expert_bias is not None else (None, None, None)
+    if not q8 and logits is not None and router is None and E <= ROUTE_GU_MAX_E and x.shape[0] * KU <= ROUTE_GU_MAX_A:
+        # routing and the gate/up matvecs in one launch (equal bit for bit to moe_topk then moe_expert_mv 'gu')
+        ids, wts, a = moe_topk_expert_mv(fmt, logits, KU, gating, norm, x, w_gate, FE, H, E, w2=w_up, ws=ws_gate,
+                                         ws2=ws_up, fused=fused, act=act, bias=bg, bias2=bu, scale=scale,
+                                         router_bias=bias)
+        if down_scale is not None:
+            moe_wscale(ids, wts, down_scale)
+        y = moe_expert_mv_combine(fd, ids, wts, a, w_down, H, FE, E, ws=ws_down, bias=bd, y=y, accumulate=y is not None,
+                                  sg=sg)
+        return y, {"ids": ids, "wts": wts, "logits": logits, "act": a}
+    ids, wts, logits = _route(x, logits, KU, gating, norm, scale, bias, router, down_scale)
     if q8:
         xq = quant_q8(x)
         a = moe_expert_mv_q8(fmt, "gu", ids, xq, w_gate, FE, H, E, KU, w2=w_up, fused=fused, act=act, bias=bg,

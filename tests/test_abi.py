@@ -122,6 +122,17 @@ def test_argument_validation_without_a_device(lib):
         == st["QMM_ERR_RANGE"]
     assert lib.qmm_moe_expert_mv(3, 0, 0, 0, 64, 8, 4, 2, 4, fake, fake, 0, fake, fake, n, n, fake, n) \
         == st["QMM_ERR_FORMAT"]
+    # routing + gate/up matvecs: E past 256, the gating-1 bias, a tiled layout, K, dtype
+    assert lib.qmm_moe_topk_expert_mv(fake, 1, 300, 4, 1, 1, f1, n, fake, fake, 1, 0, 0, 256, 8, fake, 2, fake, n, fake,
+                                      n, n, n, fake, n) == st["QMM_ERR_RANGE"]
+    assert lib.qmm_moe_topk_expert_mv(fake, 1, 32, 4, 1, 1, f1, fake, fake, fake, 1, 0, 0, 256, 8, fake, 2, fake, n,
+                                      fake, n, n, n, fake, n) == st["QMM_ERR_RANGE"]
+    assert lib.qmm_moe_topk_expert_mv(fake, 1, 32, 4, 1, 1, f1, n, fake, fake, 5, 0, 0, 256, 8, fake, 2, fake, n, fake,
+                                      n, n, n, fake, n) == st["QMM_ERR_FORMAT"]
+    assert lib.qmm_moe_topk_expert_mv(fake, 1, 32, 4, 1, 1, f1, n, fake, fake, 1, 0, 0, 100, 8, fake, 2, fake, n, fake,
+                                      n, n, n, fake, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_moe_topk_expert_mv(fake, 1, 32, 4, 1, 1, f1, n, fake, fake, 1, 0, 0, 256, 8, fake, 1, fake, n, fake,
+                                      n, n, n, fake, n) == st["QMM_ERR_DTYPE"]
     # fused down matvecs + combine: tiled layouts, KU above 8, null weights, split planes without scales, K, dtype
     assert lib.qmm_moe_expert_mv_combine(4, 256, 8, 4, 2, 1, fake, fake, fake, 0, fake, fake, n, 0, n, fake, n) \
         == st["QMM_ERR_FORMAT"]

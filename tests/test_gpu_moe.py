@@ -379,3 +379,45 @@ def test_expert_mv_combine_equals_separate_calls(dev, fmt, T, E, KU, H, FE, xdt,
                                         accumulate=mode == "acc", sg=sg)
         torch.cuda.synchronize()
         assert_bits_equal(host(got), host(want), f"{fmt} T={T} KU={KU} {mode} call {rep}")
+
+
+@pytest.mark.parametrize("fmt,T,E,KU,H,FE,gating,norm,fused,act,rbias,ebias,xdt", [
+    ("mxfp4s", 1, 32, 4, 2880, 256, 3, False, True, "swiglu_oai", True, True, "bf16"),    # gpt-oss-20b routing
+    ("q4_k", 1, 128, 8, 2048, 64, 1, True, False, "silu", False, False, "bf16"),           # Qwen3-30B-A3B routing
+    ("q4_k", 5, 256, 8, 512, 256, 2, True, False, "silu", True, False, "f32"),
+    ("q6_k", 3, 160, 6, 256, 512, 1, False, True, "silu", False, True, "f32"),
+    ("q4_0", 63, 60, 4, 256, 128, 3, True, False, "swiglu_oai", False, False, "bf16"),
+    ("mxfp4", 2, 8, 2, 160, 96, 2, False, True, "silu", False, False, "bf16"),
+])
+def test_topk_expert_mv_equals_separate_calls(dev, fmt, T, E, KU, H, FE, gating, norm, fused, act, rbias, ebias, xdt):
+    """The gate/up expert matvecs that rank their own token's logits give the routing kernel's ids and weights and
+    the separate matvecs' activations, bit for bit (every E up to four key slots a lane, all gatings)."""
+    import torch
+    from qmm import synth
+    ops = _ops()
+    rng = np.random.default_rng(T * 17 + E)
+    gfmt = "mxfp4" if fmt == "mxfp4s" else fmt
+    rows = E * FE * (2 if fused else 1)
+    raw = dev_u8(synth.weights(gfmt, rng, rows, H), dev)
+    raw2 = None if fused else dev_u8(synth.weights(gfmt, rng, E * FE, H), dev)
+    ws = ws2 = None
+    if fmt == "mxfp4s":
+        w, ws = ops.repack_mxfp4(raw, rows, H)
+        w2, ws2 = ops.repack_mxfp4(raw2, E * FE, H) if raw2 is not None else (None, None)
+    else:
+        w, w2 = raw, raw2
+    logits = dev_f32(rng.standard_normal((T, E)).astype(np.float32), dev)
+    xv = rng.standard_normal((T, H)).astype(np.float32)
+    x = dev_f32(xv, dev) if xdt == "f32" else dev_bf16(synth.to_bf16_bits(xv), dev)
+    rb = dev_f32(rng.standard_normal(E).astype(np.float32), dev) if rbias else None
+    bg = dev_f32(rng.standard_normal((E, FE)).astype(np.float32), dev) if ebias else None
+    bu = dev_f32(rng.standard_normal((E, FE)).astype(np.float32), dev) if ebias else None
+    ids_w, wts_w = ops.moe_topk(logits, KU, gating, norm, scale=0.75, bias=rb)
+    a_w = ops.moe_expert_mv(fmt, "gu", ids_w.reshape(-1), x, w, FE, H, E, KU, w2=w2, ws=ws, ws2=ws2, fused=fused,
+                            act=act, bias=bg, bias2=bu)
+    ids, wts, a = ops.moe_topk_expert_mv(fmt, logits, KU, gating, norm, x, w, FE, H, E, w2=w2, ws=ws, ws2=ws2,
+                                         fused=fused, act=act, bias=bg, bias2=bu, scale=0.75, router_bias=rb)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(ids), host(ids_w))
+    assert_bits_equal(host(wts), host(wts_w), "weights")
+    assert_bits_equal(host(a), host(a_w), f"{fmt} act")
