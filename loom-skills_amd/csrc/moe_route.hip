@@ -36,8 +36,7 @@ __global__ __launch_bounds__(256) void topk_kernel(const float *__restrict__ log
 
 // ------------------------------------------------------------------------------ top-k + activation operand
 // The prefill chain's first two steps, routing and the grouped gate/up GEMM's activation operand, are both per token
-// and independent: one wave per token does both, its row's loads issued before the selection so their latency
-// hides behind it. OP kOpF16: the row-scaled f16 row and its (2^-e, 2^e) as qmm_row_scale_f16 computes them; kOpMx8:
+// and independent: one launch does both, a wave ranking each token while another writes its operand. OP kOpF16: the row-scaled f16 row and its (2^-e, 2^e) as qmm_row_scale_f16 computes them; kOpMx8:
 // the E4M3 codes and E8M0 scales as qmm_quant_mxfp8 computes them. x: bf16 rows [tokens, H]; NP: 16-byte pieces
 // (8 values) a lane, H <= 512 NP.
 enum TopkOp { kOpF16 = 1, kOpMx8 = 2 };
@@ -49,10 +48,15 @@ __global__ __launch_bounds__(256) void topk_operand_kernel(const float *__restri
                                                            float *__restrict__ wts, int64_t H,
                                                            const u16 *__restrict__ x, void *__restrict__ xo,
                                                            void *__restrict__ xs) {
-  __shared__ __align__(16) uint64_t keys[4][64 * NS];
+  __shared__ __align__(16) uint64_t keys[2][64 * NS];
+  // two tokens a workgroup: waves 0 / 1 rank tokens 2 b / 2 b + 1, waves 2 / 3 write their operands meanwhile
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int64_t t = (int64_t)blockIdx.x * 4 + wv;
+  const int64_t t = (int64_t)blockIdx.x * 2 + (wv & 1);
   if (t >= tokens) return;
+  if (wv < 2) {
+    topk_token<NS>(logits + t * E, t, E, KU, gating, norm, scale, bias, keys[wv], ids, wts);
+    return;
+  }
   const int np = (int)(H / 8);           // pieces of the row
   const v4u *xr = reinterpret_cast<const v4u *>(x + t * H);
   v4u raw[NP];
@@ -61,7 +65,6 @@ __global__ __launch_bounds__(256) void topk_operand_kernel(const float *__restri
     const int p = lane + 64 * i;
     raw[i] = xr[p < np ? p : np - 1];
   }
-  topk_token<NS>(logits + t * E, t, E, KU, gating, norm, scale, bias, keys[wv], ids, wts);
   float v[NP][8];
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
@@ -595,7 +598,7 @@ int qmm_moe_topk_operand(const float *logits, int64_t tokens, int E, int KU, int
   if (H <= 0 || H > 4096 || H % (op_dtype == QMM_F16 ? 8 : 32)) return QMM_ERR_SHAPE;
   if (!aligned(x, 16) || !aligned(xo, op_dtype == QMM_F16 ? 16 : 8) || !aligned(xo_scales, 8)) return QMM_ERR_ALIGN;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const unsigned g = (unsigned)((tokens + 3) / 4);
+  const unsigned g = (unsigned)((tokens + 1) / 2);
   const int NS = (E + 63) / 64;
   const u16 *xb = static_cast<const u16 *>(x);
   auto go = [&](auto kern) {
