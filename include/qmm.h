@@ -369,7 +369,9 @@ int qmm_moe_expert_mv_combine(int fmt, int64_t k, int64_t n, int E, int KU, int6
  *     (qmm_row_scale_f16 for GGUF formats, qmm_quant_mxfp8 for MXFP4 planes), the grouped gate/up GEMM
  *     (qmm_moe_grouped / qmm_moe_grouped_mxfp8), its output's operand, the grouped down GEMM, qmm_moe_combine;
  *   tokens < 64 (decode): route, [wscale], the gate/up and down expert matvecs (qmm_moe_expert_mv[_split], or with
- *     flags QMM_MOE_Q8 qmm_quant_q8 + qmm_moe_expert_mv_q8 for both), qmm_moe_combine over the assignments.
+ *     flags QMM_MOE_Q8 qmm_quant_q8 + qmm_moe_expert_mv_q8 for both), qmm_moe_combine over the assignments; on f32 /
+ *     bf16 activations the down matvecs and the combine run as qmm_moe_expert_mv_combine, and with given logits,
+ *     E <= 64 and tokens * KU <= 8 the routing and the gate/up matvecs as qmm_moe_topk_expert_mv.
  * Results equal those of the separate calls bit for bit. Names as in those calls: fmt the gate / up format (GGUF
  * Q4_K / Q6_K / Q4_0 / MXFP4, split MXFP4S, tiled MXFP4T or Q4_KT for prefill), fmt_down the down tensor's (-1: fmt); x f32 /
  * bf16 [tokens, H]; logits f32 [tokens, E], or NULL to route with w_router [E, H] (f32 / bf16); router_bias and
