@@ -348,6 +348,7 @@ def test_moe_prefill_chain_graph_replays_equal_eager(dev, fmt):
     ("q6_k", 3, 8, 2, 520, 512, "f32", "store", False),
     ("q4_0", 7, 16, 6, 256, 320, "f32", "acc", False),
     ("mxfp4", 2, 8, 3, 130, 160, "bf16", "gated", False),
+    ("q4_k", 9, 4, 1, 64, 256, "f32", "acc", True),         # one slot: a one-wave workgroup
 ])
 def test_expert_mv_combine_equals_separate_calls(dev, fmt, T, E, KU, H, FE, xdt, mode, bias):
     """The fused down matvecs + combine equal qmm_moe_expert_mv(dn) then qmm_moe_combine[_gated], bit for bit,
@@ -388,6 +389,8 @@ def test_expert_mv_combine_equals_separate_calls(dev, fmt, T, E, KU, H, FE, xdt,
     ("q6_k", 3, 160, 6, 256, 512, 1, False, True, "silu", False, True, "f32"),
     ("q4_0", 63, 60, 4, 256, 128, 3, True, False, "swiglu_oai", False, False, "bf16"),
     ("mxfp4", 2, 8, 2, 160, 96, 2, False, True, "silu", False, False, "bf16"),
+    ("q4_0", 4, 4, 4, 128, 64, 1, True, False, "silu", False, False, "bf16"),              # every expert picked
+    ("mxfp4s", 1, 1, 1, 64, 32, 3, False, True, "swiglu_oai", False, False, "f32"),       # one expert
 ])
 def test_topk_expert_mv_equals_separate_calls(dev, fmt, T, E, KU, H, FE, gating, norm, fused, act, rbias, ebias, xdt):
     """The gate/up expert matvecs that rank their own token's logits give the routing kernel's ids and weights and
