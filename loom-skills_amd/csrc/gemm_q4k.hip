@@ -361,7 +361,7 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
               bf[j] = gl ? deq8_q40<true>(q0, q1, dsc[j]) : deq8_q40<false>(q0, q1, dsc[j]);
             } else {
               const u32 q0 = s2 ? cring[u][j].z : cring[u][j].x, q1 = s2 ? cring[u][j].w : cring[u][j].y;
-              bf[j] = gl ? deq8<true>(q0, q1, dsc[j], nmn[j]) : deq8<false>(q0, q1, dsc[j], nmn[j]);
+              bf[j] = gl ? deq8_e4m3<true>(q0, q1, dsc[j], nmn[j]) : deq8_e4m3<false>(q0, q1, dsc[j], nmn[j]);
             }
           }
           const int ak = Q40 ? 32 * h + 16 * gl + 8 * s2 : 32 * gl + 16 * h + 8 * s2;   // the lane's K position
