@@ -283,6 +283,13 @@ int qmm_moe_grouped_mxfp8(int fmt, int fused, int act, int E, int KU, int64_t ma
 int qmm_row_scale_f16(int64_t rows, int64_t k, const void *x, int x_dtype, float *scales, void *x16,
                       const int32_t *tile_info, qmm_stream_t stream);
 
+/* qmm_row_scale_f16 over listed rows only: for i < n, row rows[i] (skipped when < 0) of x [.., k] is scaled and
+ * written where qmm_row_scale_f16 writes it (x16 / scales at that row). With the bucket's pos as the list these are
+ * the rows g_row_scale_f16_tiles (S/gen_moe.py:503-527) scales, by a grid over the assignments instead of over every
+ * tile row. k % 8 == 0, k <= 8192, x and x16 16-byte aligned. */
+int qmm_row_scale_f16_rows(int64_t n, const int32_t *rows, int64_t k, const void *x, int x_dtype, float *scales,
+                           void *x16, qmm_stream_t stream);
+
 /* g_row_scale_f16_live (S/gen_llm.py:1915-1937): qmm_row_scale_f16 over an epoch's rows, where a padding row
  * (info i32 [rows, 4] with info[row, 2] == 0) gets scale and inverse 0 and zero f16 values without its x row being
  * read. qmm_gemm skips a 64-row tile whose rows all have scale 0 (GEMM_SKIP_PADDING, S/gen_gemm.py:2188-2220). */

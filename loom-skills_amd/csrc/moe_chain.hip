@@ -199,7 +199,10 @@ extern "C" int qmm_moe_routed(int fmt, int fmt_down, int fused, int act, int gat
     if ((st = qmm_moe_grouped(fmt, 0, fused, act, E, KU, p.max_rows, H, FE, T, ti, rm, x16, QMM_F16, xsc, w_gate,
                               nullptr, w_up, nullptr, bias_gate, bias_up, a, stream)))
       return st;
-    if ((st = qmm_row_scale_f16(p.max_rows, FE, a, QMM_F32, asc, a16, ti, stream))) return st;
+    // the down GEMM's operand over the assignments' rows (the rows the tile-wise producer covers)
+    if ((st = FE % 8 == 0 && FE <= 8192 ? qmm_row_scale_f16_rows(p.A, pos, FE, a, QMM_F32, asc, a16, stream)
+                                         : qmm_row_scale_f16(p.max_rows, FE, a, QMM_F32, asc, a16, ti, stream)))
+      return st;
     st = qmm_moe_grouped(fmt_down, 1, 0, act, E, KU, p.max_rows, FE, H, p.max_rows, ti, rm, a16, QMM_F16, asc,
                          w_down, nullptr, nullptr, nullptr, bias_down, nullptr, ys, stream);
   }

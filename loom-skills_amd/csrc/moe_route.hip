@@ -9,6 +9,7 @@
 //   qmm_moe_combine    y[t] (+)= sum_k w[t,k] ys[row(t,k)]           g_moe_combine[_sorted], S/gen_moe.py:730-762, :1231-1280
 //   qmm_moe_combine_gated  y[t] = sg[t] y[t] + sum_k ...             shared_gated combine, S/gen_moe.py:765-779
 //   qmm_row_scale_f16  per-row power-of-two scale + f16 copy         g_row_scale_f16[_tiles], S/gen_llm.py:1843-1915
+//   qmm_row_scale_f16_rows  the same over listed rows (the bucket's pos): the rows g_row_scale_f16_tiles covers
 //   qmm_quant_mxfp8    E4M3 + E8M0-per-32 operand of the scaled MFMA
 //   qmm_repack_mxfp4   GGUF 17-byte MXFP4 blocks -> split planes
 #include "common.hpp"
@@ -452,10 +453,13 @@ template <bool BF, int NCH>
 __global__ __launch_bounds__(256) void row_scale_wave_kernel(int64_t rows, int64_t k, const void *__restrict__ x,
                                                              float *__restrict__ scales, _Float16 *__restrict__ x16,
                                                              const int32_t *__restrict__ tile_info,
-                                                             const int32_t *__restrict__ info) {
+                                                             const int32_t *__restrict__ info,
+                                                             const int32_t *__restrict__ ridx = nullptr) {
   const int lane = threadIdx.x & 63;
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= rows) return;
+  const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (i >= rows) return;
+  const int64_t r = ridx ? ridx[i] : i;   // ridx: the listed rows only (rows = entries of the list)
+  if (r < 0) return;
   if (tile_info && (tile_info[2 * (r / kTile)] < 0 || r % kTile >= tile_info[2 * (r / kTile) + 1])) return;
   const int64_t nch = k / 8, base = r * nch;
   if (info && info[4 * r + 2] == 0) {   // a padding row of the epoch: zero values, scale and inverse 0
@@ -717,19 +721,21 @@ int qmm_moe_combine_gated(int64_t tokens, int64_t rows, int64_t H, int KU, const
 }
 
 static int row_scale(int64_t rows, int64_t k, const void *x, int x_dtype, float *scales, void *x16,
-                     const int32_t *tile_info, const int32_t *info, hipStream_t s) {
+                     const int32_t *tile_info, const int32_t *info, hipStream_t s, const int32_t *ridx = nullptr) {
   if (!x || !scales || !x16) return QMM_ERR_NULL;
   if (x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
   if (rows <= 0 || k <= 0 || rows > (1ll << 24)) return QMM_ERR_SHAPE;
   if (tile_info && rows % kTile) return QMM_ERR_SHAPE;
   _Float16 *o = static_cast<_Float16 *>(x16);
-  if (k % 8 == 0 && k <= 8 * 64 * kRsMaxChunks && aligned(x, 16) && aligned(x16, 16)) {
+  const bool wave_path = k % 8 == 0 && k <= 8 * 64 * kRsMaxChunks && aligned(x, 16) && aligned(x16, 16);
+  if (ridx && !wave_path) return k % 8 || k > 8 * 64 * kRsMaxChunks ? QMM_ERR_SHAPE : QMM_ERR_ALIGN;
+  if (wave_path) {
     const unsigned grid = (unsigned)((rows + 3) / 4);
     const int64_t per = (k / 8 + 63) / 64;   // chunks a lane
     const bool bf = x_dtype == QMM_BF16;
 #define QMM_RS(N)                                                                                                   \
-  (bf ? (row_scale_wave_kernel<true, N><<<grid, 256, 0, s>>>(rows, k, x, scales, o, tile_info, info), 0)          \
-      : (row_scale_wave_kernel<false, N><<<grid, 256, 0, s>>>(rows, k, x, scales, o, tile_info, info), 0))
+  (bf ? (row_scale_wave_kernel<true, N><<<grid, 256, 0, s>>>(rows, k, x, scales, o, tile_info, info, ridx), 0)    \
+      : (row_scale_wave_kernel<false, N><<<grid, 256, 0, s>>>(rows, k, x, scales, o, tile_info, info, ridx), 0))
     if (per <= 1) QMM_RS(1);
     else if (per <= 2) QMM_RS(2);
     else if (per <= 4) QMM_RS(4);
@@ -745,6 +751,12 @@ static int row_scale(int64_t rows, int64_t k, const void *x, int x_dtype, float 
 int qmm_row_scale_f16(int64_t rows, int64_t k, const void *x, int x_dtype, float *scales, void *x16,
                       const int32_t *tile_info, qmm_stream_t stream) {
   return row_scale(rows, k, x, x_dtype, scales, x16, tile_info, nullptr, reinterpret_cast<hipStream_t>(stream));
+}
+
+int qmm_row_scale_f16_rows(int64_t n, const int32_t *rows, int64_t k, const void *x, int x_dtype, float *scales,
+                           void *x16, qmm_stream_t stream) {
+  if (!rows) return QMM_ERR_NULL;
+  return row_scale(n, k, x, x_dtype, scales, x16, nullptr, nullptr, reinterpret_cast<hipStream_t>(stream), rows);
 }
 
 int qmm_row_scale_f16_live(int64_t rows, const int32_t *info, int64_t k, const void *x, int x_dtype, float *scales,

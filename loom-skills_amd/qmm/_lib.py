@@ -42,6 +42,7 @@ SIGNATURES = {
     "qmm_moe_wscale": [c_i64, c_int, c_int, c_vp, c_vp, c_vp, c_vp],
     "qmm_moe_combine_gated": [c_i64, c_i64, c_i64, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
     "qmm_row_scale_f16": [c_i64, c_i64, c_vp, c_int, c_vp, c_vp, c_vp, c_vp],
+    "qmm_row_scale_f16_rows": [c_i64, c_vp, c_i64, c_vp, c_int, c_vp, c_vp, c_vp],
     "qmm_row_scale_f16_live": [c_i64, c_vp, c_i64, c_vp, c_int, c_vp, c_vp, c_vp],
     "qmm_quant_mxfp8": [c_i64, c_i64, c_vp, c_int, c_vp, c_vp, c_vp, c_vp],
     "qmm_repack_mxfp4": [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp],

@@ -468,6 +468,18 @@ def row_scale_f16(x, tile_info=None, x16=None, scales=None, info=None):
     return x16, scales
 
 
+def row_scale_f16_rows(x, rows, x16=None, scales=None):
+    """row_scale_f16 over the listed rows only (rows i32, -1 entries skipped): (x16, scales) of x's shape, the
+    listed rows written as row_scale_f16 writes them, the others left as they were."""
+    _dev(x, rows, x16, scales)
+    n, k = x.shape
+    x16 = torch.empty((n, k), dtype=torch.float16, device=x.device) if x16 is None else x16
+    scales = torch.empty((n, 2), dtype=torch.float32, device=x.device) if scales is None else scales
+    _lib.call("qmm_row_scale_f16_rows", rows.numel(), _ptr(rows), k, _ptr(x), _dt(x), _ptr(scales), _ptr(x16),
+              _stream())
+    return x16, scales
+
+
 def quant_mxfp8(x, tile_info=None, codes=None, scales=None):
     """(E4M3 codes u8 [rows, k], E8M0 scales u8 [rows, k/64]) of x f32 / bf16 [rows, k]."""
     _dev(x, tile_info, codes, scales)
@@ -564,7 +576,8 @@ def moe_prefill(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up
         x16, xs = (xop, xos) if xop is not None else row_scale_f16(x)
         a = moe_grouped(fmt, "gu", tile_info, rowmap, x16, w_gate, FE, H, E, KU, w2=w_up, x_scales=xs,
                         fused=fused, act=act, bias=bg, bias2=bu)
-        a16, as_ = row_scale_f16(a, tile_info=tile_info)
+        # the down GEMM's operand over the assignments' rows (the rows the tile-wise producer covers)
+        a16, as_ = row_scale_f16_rows(a, pos) if FE % 8 == 0 and FE <= 8192 else row_scale_f16(a, tile_info=tile_info)
         ys = moe_grouped(fmt_down or fmt, "dn", tile_info, rowmap, a16, w_down, H, FE, E, KU, x_scales=as_, bias=bd)
     elif fmt in ("mxfp4s", "mxfp4t"):
         # the gate/up GEMM writes its activation as MXFP8 directly (the down GEMM's A operand)

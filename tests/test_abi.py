@@ -122,6 +122,9 @@ def test_argument_validation_without_a_device(lib):
         == st["QMM_ERR_RANGE"]
     assert lib.qmm_moe_expert_mv(3, 0, 0, 0, 64, 8, 4, 2, 4, fake, fake, 0, fake, fake, n, n, fake, n) \
         == st["QMM_ERR_FORMAT"]
+    # listed-rows row scale: no list, K not a multiple of 8
+    assert lib.qmm_row_scale_f16_rows(4, n, 256, fake, 0, fake, fake, n) == st["QMM_ERR_NULL"]
+    assert lib.qmm_row_scale_f16_rows(4, fake, 100, fake, 0, fake, fake, n) == st["QMM_ERR_SHAPE"]
     # routing + gate/up matvecs: E past 256, the gating-1 bias, a tiled layout, K, dtype
     assert lib.qmm_moe_topk_expert_mv(fake, 1, 300, 4, 1, 1, f1, n, fake, fake, 1, 0, 0, 256, 8, fake, 2, fake, n, fake,
                                       n, n, n, fake, n) == st["QMM_ERR_RANGE"]

@@ -166,3 +166,22 @@ def test_row_scale_f16(dev):
     np.testing.assert_array_equal(host(sc)[:, 1], 2.0 ** e)
     want = (x.astype(np.float64) * 2.0 ** -e[:, None]).astype(np.float16)
     assert_bits_equal(host(x16).astype(np.float32), want.astype(np.float32), "x16")
+
+
+def test_row_scale_rows_equals_tile_rows(dev):
+    """The listed-rows producer writes the bucket's live rows exactly as the tile-wise one does."""
+    import torch
+    ops = _ops()
+    rng = np.random.default_rng(11)
+    T, E, KU, k = 64, 128, 8, 768
+    ids, _ = ops.moe_topk(dev_f32(rng.standard_normal((T, E)).astype(np.float32), dev), KU, 1, True)
+    ti, rm, pos = ops.moe_bucket(ids, E)
+    rows = ti.shape[0] * 64
+    a = dev_f32((rng.standard_normal((rows, k)) * np.exp2(rng.integers(-20, 20, (rows, 1)))).astype(np.float32), dev)
+    want16, wants = ops.row_scale_f16(a, tile_info=ti)
+    got16, gots = ops.row_scale_f16_rows(a, pos)
+    torch.cuda.synchronize()
+    live = host(rm) >= 0
+    assert live.sum() == T * KU
+    np.testing.assert_array_equal(host(got16.view(torch.int16))[live], host(want16.view(torch.int16))[live])
+    np.testing.assert_array_equal(host(gots)[live].view(np.uint32), host(wants)[live].view(np.uint32))
