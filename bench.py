@@ -206,6 +206,9 @@ class GemvWorkload:
                          f"{res['runs']} full {self.fmt} GEMVs (N={n}, K={self.k}, M={self.m}): numpy oracle, "
                          f"dequant fused in 256-row chunks + f32 matmul on {res['threads']} threads")
 
+    def tokens(self):
+        return self.m
+
     def config(self):
         return {"workload": self.name, "format": self.fmt, "layout": "tiled (q4_kt)" if self.tiled else "gguf",
                 "N": self.n, "K": self.k, "M": self.m,
@@ -281,6 +284,9 @@ class GemmWorkload:
                          f"{res['runs']} full GEMMs (M={self.m}, N={self.n}, K={self.k}): numpy oracle, dequant "
                          f"fused in 256-row chunks + f32 matmul on {res['threads']} threads")
 
+    def tokens(self):
+        return self.m
+
     def config(self):
         return {"workload": self.name, "format": "q4_k", "M": self.m, "N": self.n, "K": self.k, "x_dtype": "bf16",
                 "y_dtype": "bf16", "weight_copies_rotated": self.copies, "rotated_bytes": self.copies * self.wbytes}
@@ -288,7 +294,7 @@ class GemmWorkload:
 
 class MoeWorkload:
     """The routed-expert chain (ops.moe_routed: the decode chain for T < 64, the prefill chain from 64 tokens); one
-    step = the whole chain over one batch of T tokens, on one of two copies of the expert weights in turn."""
+    step = the whole chain over one batch of T tokens, on one of several copies of the expert weights in turn."""
     unit = "TFLOP/s"
 
     def __init__(self, name, index, m):
@@ -343,12 +349,20 @@ class MoeWorkload:
         # a second copy of every expert tensor, alternated from step to step: one layer's experts (441 MB MXFP4,
         # 340 MB Q4_K) are close to the 256 MB MALL, and a kernel timed on the same copy again would partly be
         # served from it
-        self.kws = [self.kw, {k: (v.clone() if hasattr(v, "clone") else v) for k, v in self.kw.items()}]
-        self.copies = 2
+        self.kws = [self.kw]
+        self.copies = 1
         y, mid = self.run_chain()
         torch.cuda.synchronize()
         self.experts_hit = int(torch.unique(mid["ids"]).numel())
         self.mid = mid
+        # copies of every expert tensor, taken in turn from step to step, so that more than 300 MB of expert weights
+        # pass between two reads of one copy and the 256 MB MALL cannot serve them: one layer's experts (441 MB MXFP4,
+        # 340 MB Q4_K) at prefill, 6 copies of the 4 x 13.2 MB the MXFP4 decode chain reads at one token
+        touched = self.experts_hit * self.wbytes_expert
+        self.copies = max(2, -(-ROTATE_BYTES // touched))
+        while len(self.kws) < self.copies:
+            self.kws.append({k: (v.clone() if hasattr(v, "clone") else v) for k, v in self.kw.items()})
+        self.rotated_bytes = self.copies * touched
         # inputs of the dominant kernel (the gate/up GEMM or expert matvec) for its own timing; the decode chain
         # routes inside its gate/up matvecs where ops.moe_decode does
         self.route_gu = self.decode and self.E <= ops.ROUTE_GU_MAX_E and self.T * self.KU <= ops.ROUTE_GU_MAX_A
@@ -455,7 +469,11 @@ class MoeWorkload:
     def config(self):
         return {"workload": self.name, "format": self.fmt, "chain": "decode" if self.decode else "prefill",
                 "E": self.E, "top_k": self.KU, "H": self.H, "FE": self.FE, "T": self.T, "gating": self.d["gating"],
-                "act": self.d["act"], "experts_hit": self.experts_hit, "weight_copies_rotated": self.copies}
+                "act": self.d["act"], "experts_hit": self.experts_hit, "weight_copies_rotated": self.copies,
+                "rotated_expert_bytes": self.rotated_bytes}
+
+    def tokens(self):
+        return self.T
 
 
 class CopyWorkload:
@@ -541,11 +559,14 @@ WORKLOADS = {"q4_k_gemv": _q4k_gemv, "q4_k_gemv_q8": _q4k_gemv_q8, "q4_k_gemv_q8
 
 # ---------------------------------------------------------------------------------------------------- timing
 RAMP_MS = 30.0   # untimed GPU work before a timed region: the warm-up steps repeated until this much has run
+PRE_MS = 3.0     # warm-up steps queued right ahead of the first timed step (behind the spin), in GPU time
+MAX_SPIN_CYCLES = 1_000_000_000
 
 
 def _ramp(run_once):
     """Repeats run_once() (the warm-up steps) until RAMP_MS of GPU time has passed, so the timed region starts at the
-    clocks the workload runs at, not at the idle clocks of the host-side setup before it."""
+    clocks the workload runs at, not at the idle clocks of the host-side setup before it. Returns the GPU ms of one
+    run_once()."""
     import torch
     total, n = 0.0, 0
     while total < RAMP_MS and n < 1000:
@@ -556,18 +577,21 @@ def _ramp(run_once):
         torch.cuda.synchronize()
         total += a.elapsed_time(b)
         n += 1
+    return total / n
 
 
 def _spin_for(host_s_per_step, steps):
     """Spin cycles that outlast the host's enqueueing of `steps` steps (about 2.4 cycles a ns, twice the estimate)."""
-    return int(max(SPIN_CYCLES, 2.0 * host_s_per_step * steps * 2.4e9))
+    return int(min(max(SPIN_CYCLES, 2.0 * host_s_per_step * steps * 2.4e9), MAX_SPIN_CYCLES))
 
 
 def timed(step_fn, steps, warmup, no_graph=False):
     """ms for `steps` steps between two HIP events on the launching stream, and the wall time of that region.
     Graph mode captures the steps in one HIP graph; eager mode launches them one by one. Either way the warm-up steps
-    run first (repeated for RAMP_MS of GPU time), and a spin kernel ahead of the first event holds the stream while
-    the host submits, so the events time the kernels and the gaps between them only."""
+    run first (repeated for RAMP_MS of GPU time), then a spin kernel holds the stream while the host submits PRE_MS
+    of warm-up steps and the timed steps behind it, so the events time the kernels and the gaps between them only,
+    and the GPU has run the workload at full load right up to the first timed step (a spin alone, one wave, would
+    let the clocks fall before it)."""
     import torch
     stream = torch.cuda.current_stream()
 
@@ -579,11 +603,17 @@ def timed(step_fn, steps, warmup, no_graph=False):
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     w = max(warmup, 1)
     if no_graph:
+        # the host's enqueue time a step, from a second warm-up pass (the first carries one-time costs: code object
+        # loads, first calls)
+        run(w, 0)
+        torch.cuda.synchronize()
         h0 = time.perf_counter()
         run(w, 0)
         host = (time.perf_counter() - h0) / w
-        _ramp(lambda: run(w, 0))
-        torch.cuda._sleep(_spin_for(host, steps))
+        gpu_ms = _ramp(lambda: run(w, 0)) / w
+        pre = int(min(max(w, PRE_MS / max(gpu_ms, 1e-4)), 5000))
+        torch.cuda._sleep(_spin_for(host, steps + pre))
+        run(pre, 0)
         wall0 = time.perf_counter()
         t0.record(stream)
         run(steps, w)
@@ -595,8 +625,10 @@ def timed(step_fn, steps, warmup, no_graph=False):
         with torch.cuda.graph(gt):
             run(steps, w)
         torch.cuda.synchronize()
-        _ramp(gw.replay)
+        gpu_ms = _ramp(gw.replay)
         torch.cuda._sleep(SPIN_CYCLES)
+        for _ in range(int(min(max(1, PRE_MS / max(gpu_ms, 1e-4)), 200))):
+            gw.replay()
         wall0 = time.perf_counter()
         t0.record(stream)
         gt.replay()
@@ -631,6 +663,8 @@ def measure(wl, args, cpu_budget):
     res = {"value": round(wl.value(per_step_s), 3), "unit": wl.unit, "ms_per_step": round(ms / args.steps, 6),
            "roofline": roof, "gbs": round(wl.alg_bytes() / per_step_s / 1e9, 2),
            "tflops": round(wl.alg_flops() / per_step_s / 1e12, 3), "wall_s_timed_region": round(wall, 4)}
+    if hasattr(wl, "tokens"):   # tokens through the step (decode rows, prefill rows, MoE tokens) a second
+        res["tokens_per_s"] = round(wl.tokens() / per_step_s, 1)
     if getattr(wl, "peak_key", None) == "fp8":
         # the scaled MFMA runs E4M3 x E2M1 at the FP8 rate; the MXFP4 figure is the fraction of the FP4 peak
         res["chain_frac_fp4_peak"] = round(res["tflops"] / MFMA_PEAK_TFLOPS["fp4"], 4)
@@ -657,6 +691,7 @@ def secondary_entry(name, m, wl, res):
     r = res["roofline"]
     out = {"workload": name, "m": m, "value": res["value"], "unit": res["unit"],
            "us_per_step": round(res["ms_per_step"] * 1e3, 3), "gbs": res["gbs"], "tflops": res["tflops"],
+           "tokens_per_s": res.get("tokens_per_s"),
            "roofline": {k: r[k] for k in ("bound", "achieved", "unit", "frac", "traffic", "kernel", "avg_launch_us")}}
     if "chain_frac_fp4_peak" in res:
         out["chain_frac_fp4_peak"] = res["chain_frac_fp4_peak"]

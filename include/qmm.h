@@ -399,8 +399,9 @@ int64_t qmm_moe_routed_workspace_size(int fmt, int flags, int E, int KU, int64_t
 /* qmm_moe_routed without a workspace argument and without any allocation: no counterpart in the reference (its
  * command programs allocate every buffer up front); it is for callers that cannot allocate device memory -- code
  * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc. The intermediates live in one
- * static device array of 16 MiB per GPU (held until the process ends), enough for the decode chain of any model with
- * H + FE <= 8192 at up to 63 tokens; a call needing more returns QMM_ERR_WORKSPACE before launching anything (use
+ * static device array of 16 MiB per GPU (held until the process ends), enough for the decode chain of a model with
+ * H + FE <= 8192 and top-8 routing on given logits at up to 63 tokens on f32 / bf16 activations, and up to 48 tokens
+ * with QMM_MOE_Q8 (its Q8_1 buffers take the rest); a call needing more returns QMM_ERR_WORKSPACE before launching anything (use
  * qmm_moe_routed). Calls that overlap on one GPU (two streams or host threads) share the array and race. Arguments
  * and results as qmm_moe_routed. */
 int qmm_moe_routed_static(int fmt, int fmt_down, int fused, int act, int gating, int norm, float scale, int flags,

@@ -537,6 +537,7 @@ extern "C" int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, c
   const int wal = fmt_align(fmt);
   if (!aligned(x, 16) || !aligned(w, wal) || !aligned(y, 4) || (w2 && !aligned(w2, wal))) return QMM_ERR_ALIGN;
   if (rows * k * 2 >= (1ll << 31)) return QMM_ERR_SHAPE;   // activation rows are addressed by a 32-bit buffer offset
+  if (n * fmt_row_bytes(fmt, k) >= (1ll << 31)) return QMM_ERR_SHAPE;   // so are the weight rows (buffer size, offsets)
   Args a{};
   a.M = (int)rows; a.N = (int)n; a.K = (int)k;
   a.x16 = static_cast<const _Float16 *>(x); a.scales = scales; a.x_rows = (int)rows;

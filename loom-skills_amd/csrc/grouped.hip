@@ -39,6 +39,8 @@ extern "C" int qmm_moe_grouped(int fmt, int mode, int fused, int act, int E, int
   if (mode != 0 && mode != 1) return QMM_ERR_RANGE;
   if (int st = check_grouped(act, E, KU, max_rows, k, n, x_rows, tile_info, rowmap, x, w)) return st;
   if (!y) return QMM_ERR_NULL;
+  // an unfused gate/up needs its up matrix on every kernel path (the narrow and 64-row Q4_K kernels, MXFP4)
+  if (mode == 0 && !fused && !w2) return QMM_ERR_NULL;
   if (mode == 1 && x_rows < max_rows) return QMM_ERR_SHAPE;   // the down GEMM reads its sorted rows in place
   if (!aligned(y, 4) || !aligned(bias, 4) || !aligned(bias2, 4)) return QMM_ERR_ALIGN;
   const int64_t max_tiles = max_rows / 64;
@@ -62,6 +64,7 @@ extern "C" int qmm_moe_grouped_mxfp8(int fmt, int fused, int act, int E, int KU,
   if (fmt != QMM_MXFP4S && fmt != QMM_MXFP4T) return QMM_ERR_FORMAT;
   if (int st = check_grouped(act, E, KU, max_rows, k, n, x_rows, tile_info, rowmap, x, w)) return st;
   if (!codes || !scales) return QMM_ERR_NULL;
+  if (!fused && (!w2 || !ws2)) return QMM_ERR_NULL;
   if (n % 32) return QMM_ERR_SHAPE;
   if (!aligned(bias, 4) || !aligned(bias2, 4)) return QMM_ERR_ALIGN;
   return qmm_grouped_mxfp4(fmt == QMM_MXFP4T, 0, fused, act, max_rows / 64, k, n, E, KU, tile_info, rowmap, x,

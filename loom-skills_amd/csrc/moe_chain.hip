@@ -110,6 +110,7 @@ extern "C" int qmm_moe_routed(int fmt, int fmt_down, int fused, int act, int gat
   if (fmt_down < 0) fmt_down = fmt;
   if (int st = check_chain(fmt, fmt_down, flags, E, KU, tokens, H, FE)) return st;
   if (!x || !y || !w_gate || !w_down || (!logits && !w_router)) return QMM_ERR_NULL;
+  if (!fused && !w_up) return QMM_ERR_NULL;   // an unfused gate/up reads its up matrix in every chain
   if (x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
   const Plan p = moe_plan(fmt, flags, E, KU, tokens, H, FE, logits == nullptr);
   if (!workspace) return QMM_ERR_NULL;

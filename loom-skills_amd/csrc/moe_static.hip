@@ -11,7 +11,9 @@
 using namespace qmm;
 
 namespace {
-constexpr int64_t kScratchBytes = int64_t(16) << 20;   // the decode chain of any model up to H + FE = 8192 at 63 tokens
+// 16 MiB: the decode chain of a model with H + FE <= 8192 and top-8 routing on given logits at up to 63 tokens on
+// f32 / bf16 activations, and up to 48 tokens on the Q8_1 path (QMM_MOE_Q8 adds the quantized input and gate/up rows)
+constexpr int64_t kScratchBytes = int64_t(16) << 20;
 constexpr int kMaxDevices = 64;
 }  // namespace
 

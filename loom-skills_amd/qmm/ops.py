@@ -34,6 +34,8 @@ fastest), the last two one-time weight preparations.
 Every function validates its arguments on the host (the C ABI returns a status that becomes ``QmmError``) and
 launches asynchronously on torch's current stream. Weights are uint8 tensors holding the raw GGUF block bytes.
 """
+import weakref
+
 import torch
 
 from . import _lib
@@ -499,6 +501,25 @@ def repack_mxfp4(w, rows, k):
     return nib, sc
 
 
+_SPLIT_PLANES = {}
+
+
+def split_planes(w, rows, k):
+    """The split planes (nibbles, scales) of GGUF MXFP4 weights w [rows, k], made by repack_mxfp4 once per weight
+    tensor and kept while that tensor lives: the load-time preparation the reference's mxfp4s tensors get
+    (S/formats.py:12-15), which the prefill GEMMs read. A tensor written in place since (its version counter moved)
+    or asked for with another shape is repacked again."""
+    key, tag = id(w), (w.data_ptr(), w._version, rows, k)
+    hit = _SPLIT_PLANES.get(key)
+    if hit is not None and hit[0] == tag:
+        return hit[1]
+    planes = repack_mxfp4(w, rows, k)
+    if hit is None:   # the entry goes when the tensor does, before its id can name another object
+        weakref.finalize(w, _SPLIT_PLANES.pop, key, None)
+    _SPLIT_PLANES[key] = (tag, planes)
+    return planes
+
+
 def tile_q4k(w, rows, k):
     """GGUF Q4_K rows (uint8, rows * k / 256 * 144 bytes) -> the tiled layout (format "q4_kt") the int8-activation
     decode GEMV and the grouped expert GEMMs stream contiguously. rows % 16 == 0, k % 256 == 0 (the GEMV takes
@@ -554,11 +575,11 @@ def moe_prefill(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up
     shared experts' output the routed output is added to (scaled first by sg, the shared gate, when given);
     fmt_down: the down tensor's format when it differs (q4_k gate / up with q6_k down, the Q4_K_M expert layout).
     Returns (y f32 [T, H], intermediates dict)."""
-    if fmt == "mxfp4":   # GGUF blocks: split planes for the scaled MFMA (one-time weight preparation, done per call)
-        fmt, (w_gate, ws_gate), (w_down, ws_down) = "mxfp4s", repack_mxfp4(w_gate, E * FE * (2 if fused else 1), H), \
-            repack_mxfp4(w_down, E * H, FE)
+    if fmt == "mxfp4":   # GGUF blocks: split planes for the scaled MFMA (repacked once per weight tensor)
+        fmt, (w_gate, ws_gate), (w_down, ws_down) = "mxfp4s", split_planes(w_gate, E * FE * (2 if fused else 1), H), \
+            split_planes(w_down, E * H, FE)
         if w_up is not None:
-            w_up, ws_up = repack_mxfp4(w_up, E * FE, H)
+            w_up, ws_up = split_planes(w_up, E * FE, H)
     gguf = fmt in ("q4_k", "q4_kt", "q6_k", "q4_0")
     xop = None
     if logits is not None and router is None and x.dtype == torch.bfloat16 and H <= 4096 and \
@@ -597,6 +618,14 @@ def moe_prefill(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up
 
 
 Q8_FORMATS = ("q4_0", "q4_k", "q6_k")   # formats with integer-code expert matvecs (gen_llm ICODES)
+
+
+def _moe_q8(q8, fmt, fmt_down, expert_bias):
+    """Whether a decode chain takes int8 activations: "auto" as the reference decides it (MOE_Q8 on by default,
+    moe_iq S/gen_llm.py:5296-5303: integer codes in both formats, no expert biases), else the caller's choice."""
+    if q8 == "auto":
+        return fmt in Q8_FORMATS and fmt_down in Q8_FORMATS and expert_bias is None
+    return bool(q8)
 # The decode chain routes inside its gate/up matvecs (every workgroup ranks its token's logits itself) where that is
 # cheaper than a routing launch: one key slot a lane and few assignments (gpt-oss-20b at one token: 25.0 -> 23.9 us;
 # Qwen3-30B-A3B at one token, 128 experts, 24.8 -> 25.5 us, and either at eight tokens +14 to +26 us)
@@ -605,18 +634,18 @@ ROUTE_GU_MAX_E, ROUTE_GU_MAX_A = 64, 8
 
 def moe_decode(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=None, ws_gate=None, ws_down=None,
                ws_up=None, fused=False, act="silu", scale=1.0, bias=None, router=None, expert_bias=None,
-               down_scale=None, y=None, sg=None, fmt_down=None, q8=False):
+               down_scale=None, y=None, sg=None, fmt_down=None, q8="auto"):
     """The reference's decode MoE chain (moe_routed with t < 64): route, per-assignment expert matvecs
     (g_moe_gu_* then g_moe_dn_*), combine in assignment order. Arguments as moe_prefill; fmt_down: the down
     tensor's format when it differs (Q4_K_M files: Q4_K gate / up, Q6_K down, S/gen_llm.py:5336-5340).
     q8: the int8-activation chain (the reference's MOE_Q8 default, S/gen_llm.py:5290-5303, :5381-5383): x is
     quantized to Q8_1 once, the gate/up matvecs contract integer codes, their output is quantized again (g_quant_q8)
-    for the down matvecs; formats q4_0 / q4_k / q6_k. "auto" takes it where the reference does: both formats have
-    integer codes and the experts have no biases (gen_llm.moe_iq).
+    for the down matvecs; formats q4_0 / q4_k / q6_k. "auto" (the default) takes it where the reference does: both
+    formats have integer codes and the experts have no biases (gen_llm.moe_iq, S/gen_llm.py:5296-5303); False keeps
+    the f32 / bf16 activations (the reference's MOE_Q8=0).
     Returns (y f32 [T, H], intermediates dict)."""
     fd = fmt_down or fmt
-    if q8 == "auto":
-        q8 = fmt in Q8_FORMATS and fd in Q8_FORMATS and expert_bias is None
+    q8 = _moe_q8(q8, fmt, fd, expert_bias)
     if q8 and (fmt not in Q8_FORMATS or fd not in Q8_FORMATS):
         raise ValueError(f"the int8 expert matvecs take {Q8_FORMATS} (gate/up {fmt}, down {fd})")
     bg, bu, bd = expert_bias if expert_bias is not None else (None, None, None)
@@ -650,22 +679,33 @@ def moe_decode(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=
 GEMM_MIN_TOKENS = 64   # %gemm: epochs of 64+ tokens take the GEMM / grouped chain (S/gen_llm.py:6107-6126)
 
 
-def linear(fmt, x, w, n, k, y=None, mode="store", ws=None, w2=None, ws2=None):
+# formats whose decode matvecs contract integer weight codes with Q8_1 activations (IQ_FMTS, S/gen_llm.py:514-519)
+LINEAR_Q8_FORMATS = ("q4_0", "q4_k", "q4_kt", "q6_k")
+
+
+def linear(fmt, x, w, n, k, y=None, mode="store", ws=None, w2=None, ws2=None, q8=True):
     """Projection y (+)= x W^T, or swiglu y = silu(x W^T) (x W2^T), with the reference's per-epoch choice (linear,
     S/gen_llm.py:4568-4625): the prefill GEMM for 64+ tokens (GGUF q4_k / q6_k / q4_0 on the f16 MFMA, the activation
     row-scaled to f16 first; MXFP4 on the scaled MFMA, the activation quantized to MXFP8 first -- GGUF mxfp4 blocks
-    are repacked to split planes for it), else the decode GEMV. y is f32."""
+    go through split_planes, repacked once per weight tensor), else the decode GEMV. The decode GEMV of a format with
+    integer codes (q4_0, q4_k, q4_kt, q6_k) takes Q8_1 activations, as the reference does by default (ACT_Q8,
+    iq = ACT_Q8 and fmt in IQ_FMTS and K / 32 <= 1024, S/gen_llm.py:514-519, :4590); q8=False keeps f32 / bf16
+    activations (ACT_Q8=0). y is f32."""
     if mode not in ("store", "acc", "swiglu"):
         raise ValueError(f"linear mode {mode}")
     if mode == "swiglu" and w2 is None:
         raise ValueError("swiglu needs the up matrix w2")
     if x.shape[0] >= GEMM_MIN_TOKENS:
-        if fmt == "mxfp4":   # GGUF blocks -> split planes (a one-time weight preparation a model does at load)
-            (w, ws), (w2, ws2) = repack_mxfp4(w, n, k), (repack_mxfp4(w2, n, k) if w2 is not None else (None, None))
+        if fmt == "mxfp4":   # GGUF blocks -> split planes (kept per weight tensor after the first call)
+            (w, ws), (w2, ws2) = split_planes(w, n, k), (split_planes(w2, n, k) if w2 is not None else (None, None))
             fmt = "mxfp4s"
-        if fmt in ("q4_k", "q6_k", "q4_0", "mxfp4s", "mxfp4t"):
+        if fmt in ("q4_k", "q4_kt", "q6_k", "q4_0", "mxfp4s", "mxfp4t"):
             return gemm(fmt, mode, x, w, n, k, w2=w2, y=y, ws=ws, ws2=ws2)
         raise ValueError(f"no prefill GEMM reads {fmt} weights")
+    if q8 and fmt in LINEAR_Q8_FORMATS and k // 32 <= 1024:
+        if mode == "swiglu":
+            return mv_swiglu_q8(fmt, w, w2, x, n, k, y=y)
+        return mv_q8(fmt, w, x, n, k, y=y, accumulate=mode == "acc")
     if mode == "swiglu":
         return mv_swiglu(fmt, w, w2, x, n, k, y=y)
     return mv(fmt, w, x, n, k, y=y, accumulate=mode == "acc", ws=ws)
@@ -673,7 +713,8 @@ def linear(fmt, x, w, n, k, y=None, mode="store", ws=None, w2=None, ws2=None):
 
 def moe_routed(fmt, x, logits, E, KU, H, FE, gating, norm, **kw):
     """The routed experts of one MoE layer (moe_routed, S/gen_llm.py:5324-5385): the grouped prefill chain for 64+
-    tokens, the per-assignment decode chain below. Returns (y f32 [T, H], intermediates dict)."""
+    tokens, the per-assignment decode chain below (on int8 activations where the reference takes them, q8="auto";
+    q8=False keeps f32 / bf16). Returns (y f32 [T, H], intermediates dict)."""
     chain = moe_prefill if x.shape[0] >= GEMM_MIN_TOKENS else moe_decode
     if fmt == "mxfp4s" and "w_gate" in kw and kw.get("ws_gate") is None:
         raise ValueError("mxfp4s weights need their scale planes")
@@ -692,13 +733,14 @@ def moe_chain_workspace(fmt, E, KU, T, H, FE, q8=False, router=False):
 
 def moe_chain(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=None, ws_gate=None, ws_down=None,
               ws_up=None, fused=False, act="silu", scale=1.0, bias=None, router=None, expert_bias=None,
-              down_scale=None, y=None, sg=None, fmt_down=None, q8=False, workspace=None):
+              down_scale=None, y=None, sg=None, fmt_down=None, q8="auto", workspace=None):
     """The routed experts of one MoE layer in one library call (qmm_moe_routed, the command sequence of moe_routed,
     S/gen_llm.py:5324-5385): the same kernels as moe_routed's op-by-op chain, the intermediates in one workspace
     (a uint8 device tensor of at least moe_chain_workspace bytes; allocated here when None). Arguments as
     moe_prefill / moe_decode. Returns y f32 [T, H]."""
     _dev(x, logits, w_gate, w_down, w_up, ws_gate, ws_down, ws_up, bias, router, down_scale, y, sg, workspace)
     T = x.shape[0]
+    q8 = T < GEMM_MIN_TOKENS and _moe_q8(q8, fmt, fmt_down or fmt, expert_bias)
     _cols(x, H)
     if (logits is None) == (router is None):
         raise ValueError("give the router logits or the router weight, one of them")
@@ -728,8 +770,9 @@ def moe_layer(fmt, x, logits, E, KU, H, FE, gating, norm, shared=None, **kw):
     if shared is None:
         return moe_routed(fmt, x, logits, E, KU, H, FE, gating, norm, **kw)
     FS, sf = shared["FS"], shared["fmt"]
-    f = linear(sf, x, shared["w_gate"], FS, H, mode="swiglu", w2=shared["w_up"])
-    y = linear(shared.get("fmt_down", sf), f, shared["w_down"], H, FS)
+    q8 = kw.get("q8", "auto") is not False   # the shared experts' matvecs follow the routed chain's activations
+    f = linear(sf, x, shared["w_gate"], FS, H, mode="swiglu", w2=shared["w_up"], q8=q8)
+    y = linear(shared.get("fmt_down", sf), f, shared["w_down"], H, FS, q8=q8)
     sg = moe_shared_gate(x, shared["gate"]) if shared.get("gate") is not None else None
     y, mid = moe_routed(fmt, x, logits, E, KU, H, FE, gating, norm, y=y, sg=sg, **kw)
     mid.update(shared_act=f, sg=sg)

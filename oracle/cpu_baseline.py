@@ -40,14 +40,10 @@ def _blas_limit(n):
         return contextlib.nullcontext()
 
 
-def _median_runs(fn, budget_s, min_runs=2, max_runs=50):
-    """fn() once as a warm-up, then repeatedly for about budget_s seconds; (median seconds, runs). A budget under
-    two seconds (a secondary workload's share) takes one warm-up-free run when one call already exceeds it."""
-    t0 = time.perf_counter()
+def _median_runs(fn, budget_s, min_runs=5, max_runs=50):
+    """fn() once as a warm-up, then at least min_runs times and on for about budget_s seconds; (median seconds,
+    runs)."""
     fn()
-    first = time.perf_counter() - t0
-    if budget_s < 2.0 and first >= budget_s:
-        return first, 1
     times = []
     t_end = time.perf_counter() + budget_s
     while len(times) < min_runs or (time.perf_counter() < t_end and len(times) < max_runs):

@@ -236,6 +236,31 @@ def test_argument_validation_without_a_device(lib):
     assert lib.qmm_moe_shared_gate(4, 2048, fake, 0, n, 0, fake, n) == st["QMM_ERR_NULL"]
     assert lib.qmm_moe_wscale(4, 9, 32, fake, fake, fake, n) == st["QMM_ERR_RANGE"]
     assert lib.qmm_moe_combine_gated(4, 16, 8, 4, fake, n, fake, n, fake, n) == st["QMM_ERR_NULL"]
+    # an unfused gate/up without its up matrix, on every kernel path: the tiled layout and GGUF Q4_K with few rows an
+    # expert (the narrow kernel), GGUF Q4_K with many (the 64-row tile), and the whole chain
+    for fmt, max_rows in ((5, 256), (1, 256), (1, 64 * 40)):
+        assert lib.qmm_moe_grouped(fmt, 0, 0, 0, 4, 2, max_rows, 2048, 768, 64, fake, fake, fake, 1, fake, fake, n,
+                                   n, n, n, n, fake, n) == st["QMM_ERR_NULL"], (fmt, max_rows)
+    assert lib.qmm_moe_grouped_mxfp8(4, 0, 0, 4, 2, 256, 128, 64, 8, fake, fake, fake, fake, fake, fake, n, n, n, n,
+                                     fake, fake, n) == st["QMM_ERR_NULL"]
+    for T in (4, 64):   # decode and prefill chains
+        assert lib.qmm_moe_routed(1, -1, 0, 0, 1, 1, f1, 0, 128, 8, T, 2048, 768, fake, 2, fake, n, 0, n, n, fake, n,
+                                  n, n, fake, n, n, n, n, n, 0, fake, fake, 1 << 30, n) == st["QMM_ERR_NULL"], T
+    # the prefill GEMM's weight rows are addressed by 32-bit buffer offsets: 2 GiB of weights at most
+    assert lib.qmm_gemm(1, 0, 64, 1 << 20, 1 << 14, fake, 1, n, fake, n, fake, 0, n) == st["QMM_ERR_SHAPE"]
+
+
+def test_static_chain_scratch_bounds(lib):
+    """qmm_moe_routed_static's 16 MiB array holds the decode chain of an H + FE <= 8192, top-8 model on given logits
+    at up to 63 tokens on f32 / bf16 activations and up to 48 on the Q8_1 path (the bounds its header states), and
+    the bound is tight where the header says the Q8_1 buffers take the rest."""
+    lim = 16 << 20
+    size = lib.qmm_moe_routed_workspace_size
+    for H in range(256, 8192, 256):
+        assert 0 < size(1, 0, 256, 8, 63, H, 8192 - H, 0) <= lim, H
+        assert 0 < size(1, 1, 256, 8, 48, H, 8192 - H, 0) <= lim, H
+    assert size(1, 1, 128, 8, 55, 4096, 4096, 0) > lim
+    assert size(1, 0, 128, 8, 64, 4096, 4096, 0) > lim   # 64 tokens: the prefill chain
 
 
 def test_python_surface_refuses_host_tensors():

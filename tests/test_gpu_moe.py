@@ -101,6 +101,8 @@ def _run_chain(dev, fmt, E, KU, H, FE, T, gating, norm, act, fused, prefill, see
     logits = rng.standard_normal((T, E)).astype(np.float32) if live_logits is None else live_logits
     wfmt, kw = ex.device(split=prefill, tiled=tiled)
     chain = _ops().moe_prefill if prefill else _ops().moe_decode
+    if not prefill:
+        kw["q8"] = False   # the decode chain on bf16 activations (the f32 oracle below); int8: test_gpu_q8_matvecs.py
     y, mid = chain(wfmt, dev_bf16(xb, dev), dev_f32(logits, dev), E, KU, H, FE, gating, norm, fused=fused, act=act,
                    **kw)
     torch.cuda.synchronize()

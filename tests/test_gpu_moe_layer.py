@@ -234,6 +234,7 @@ def test_moe_layer_with_gated_shared_experts(dev, T):
     x = synth.bf16_bits_to_f32(xb)
     logits = rng.standard_normal((T, E)).astype(np.float32)
     fmt, kw = ex.device(split=True)
+    kw["q8"] = False   # decode on bf16 activations, the float oracle below (int8 decode: test_gpu_q8_matvecs.py)
     from helpers import dev_u8
     shared = dict(fmt="q4_k", w_gate=dev_u8(wsg, dev), w_up=dev_u8(wsu, dev), w_down=dev_u8(wsd, dev), FS=FS,
                   gate=dev_f32(gw, dev))
