@@ -29,13 +29,15 @@ one workload, or with --no-secondary):
 Consecutive steps read different copies of the weights (more than 300 MB in rotation), so the 256 MB MALL cannot
 serve them and the figures are HBM figures. The W warm-up steps run first, repeated until 30 ms of GPU time has
 passed (the clocks leave their idle state during the host-side setup). The K timed steps are launched one by one
-behind a GPU spin kernel that outlasts the host's enqueueing (--graph: captured in one HIP graph, which adds a
-launch overhead of its own on this stack), so every step is queued on the device before the first timed kernel
-starts and the two HIP events on the launching stream see the kernels and the dispatch gaps between them, not the
-host; value = algorithmic work x K / elapsed. `roofline` is the dominant kernel's: algorithmic bytes (or
-FLOPs) per launch over its average launch time, K eager launches of that kernel alone back to back between two HIP
-events (kernel time plus the dispatch gap). `cpu_baseline` times the numpy oracle on this host's cores on the same
-workload (dequant and matmul separately and together).
+behind a GPU spin kernel that outlasts the host's enqueueing and 3 ms of warm-up steps queued behind it (--graph:
+captured in one HIP graph, which adds a launch overhead of its own on this stack), so every step is queued on the
+device before the first timed kernel starts, the GPU has run the workload right up to it, and the two HIP events on
+the launching stream see the kernels and the dispatch gaps between them, not the host. The region of K steps is
+timed 5 times and its median taken; value = algorithmic work x K / that median. `roofline` is the dominant
+kernel's: algorithmic bytes (or FLOPs) per launch over its average launch time, K eager launches of that kernel
+alone back to back between two HIP events (kernel time plus the dispatch gap; the step's own timing where a step is
+one launch of it). `cpu_baseline` times the numpy oracle on this host's cores on the same workload (dequant and
+matmul separately and together), at least 5 runs.
 """
 import argparse
 import json
@@ -161,6 +163,10 @@ class GemvWorkload:
             self.ops.mv_q8(self.kfmt, w, self.x, self.n, self.k, y=self.y)
         else:
             self.ops.mv(self.fmt, w, self.x, self.n, self.k, y=self.y)
+
+    @property
+    def kernel_is_step(self):
+        return not self.split
 
     def kernel_step(self, i):
         if not self.split:
@@ -585,8 +591,12 @@ def _spin_for(host_s_per_step, steps):
     return int(min(max(SPIN_CYCLES, 2.0 * host_s_per_step * steps * 2.4e9), MAX_SPIN_CYCLES))
 
 
-def timed(step_fn, steps, warmup, no_graph=False):
-    """ms for `steps` steps between two HIP events on the launching stream, and the wall time of that region.
+REPEATS = 5   # timed regions of K steps each; their median is reported (a region of 20 short steps varies by 5-10 %)
+
+
+def timed(step_fn, steps, warmup, no_graph=False, repeats=REPEATS):
+    """ms for `steps` steps between two HIP events on the launching stream (the median over `repeats` such regions),
+    and the wall time of all of them.
     Graph mode captures the steps in one HIP graph; eager mode launches them one by one. Either way the warm-up steps
     run first (repeated for RAMP_MS of GPU time), then a spin kernel holds the stream while the host submits PRE_MS
     of warm-up steps and the timed steps behind it, so the events time the kernels and the gaps between them only,
@@ -600,8 +610,8 @@ def timed(step_fn, steps, warmup, no_graph=False):
             step_fn(start + i)
 
     torch.cuda.synchronize()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     w = max(warmup, 1)
+    times, wall = [], 0.0
     if no_graph:
         # the host's enqueue time a step, from a second warm-up pass (the first carries one-time costs: code object
         # loads, first calls)
@@ -612,12 +622,6 @@ def timed(step_fn, steps, warmup, no_graph=False):
         host = (time.perf_counter() - h0) / w
         gpu_ms = _ramp(lambda: run(w, 0)) / w
         pre = int(min(max(w, PRE_MS / max(gpu_ms, 1e-4)), 5000))
-        torch.cuda._sleep(_spin_for(host, steps + pre))
-        run(pre, 0)
-        wall0 = time.perf_counter()
-        t0.record(stream)
-        run(steps, w)
-        t1.record(stream)
     else:
         gw, gt = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
         with torch.cuda.graph(gw):
@@ -626,15 +630,27 @@ def timed(step_fn, steps, warmup, no_graph=False):
             run(steps, w)
         torch.cuda.synchronize()
         gpu_ms = _ramp(gw.replay)
-        torch.cuda._sleep(SPIN_CYCLES)
-        for _ in range(int(min(max(1, PRE_MS / max(gpu_ms, 1e-4)), 200))):
-            gw.replay()
-        wall0 = time.perf_counter()
-        t0.record(stream)
-        gt.replay()
-        t1.record(stream)
-    torch.cuda.synchronize()
-    return t0.elapsed_time(t1), time.perf_counter() - wall0
+    for _ in range(repeats):
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        if no_graph:
+            torch.cuda._sleep(_spin_for(host, steps + pre))
+            run(pre, 0)
+            wall0 = time.perf_counter()
+            t0.record(stream)
+            run(steps, w)
+            t1.record(stream)
+        else:
+            torch.cuda._sleep(SPIN_CYCLES)
+            for _ in range(int(min(max(1, PRE_MS / max(gpu_ms, 1e-4)), 200))):
+                gw.replay()
+            wall0 = time.perf_counter()
+            t0.record(stream)
+            gt.replay()
+            t1.record(stream)
+        torch.cuda.synchronize()
+        wall += time.perf_counter() - wall0
+        times.append(t0.elapsed_time(t1))
+    return float(np.median(times)), wall
 
 
 def kernel_time(fn, steps, warmup):
@@ -649,7 +665,10 @@ def measure(wl, args, cpu_budget):
     """Times one set-up workload; returns its result fields (the headline line's, or a secondary entry's)."""
     ms, wall = timed(wl.step, args.steps, args.warmup, no_graph=not args.graph)
     per_step_s = ms / 1e3 / args.steps
-    per_launch_s = kernel_time(wl.kernel_step or wl.step, args.steps, args.warmup) / 1e3
+    if getattr(wl, "kernel_is_step", False) and not args.graph:
+        per_launch_s = per_step_s   # the step is one launch of the dominant kernel: the same measurement
+    else:
+        per_launch_s = kernel_time(wl.kernel_step or wl.step, args.steps, args.warmup) / 1e3
     kb = wl.kernel_bytes() if hasattr(wl, "kernel_bytes") else wl.alg_bytes()
     kf = wl.kernel_flops() if hasattr(wl, "kernel_flops") else wl.alg_flops()
     if wl.bound == "hbm":
@@ -662,7 +681,8 @@ def measure(wl, args, cpu_budget):
             "alg_bytes_per_launch": kb, "alg_flops_per_launch": kf}
     res = {"value": round(wl.value(per_step_s), 3), "unit": wl.unit, "ms_per_step": round(ms / args.steps, 6),
            "roofline": roof, "gbs": round(wl.alg_bytes() / per_step_s / 1e9, 2),
-           "tflops": round(wl.alg_flops() / per_step_s / 1e12, 3), "wall_s_timed_region": round(wall, 4)}
+           "tflops": round(wl.alg_flops() / per_step_s / 1e12, 3), "wall_s_timed_region": round(wall, 4),
+           "timed_regions": REPEATS}
     if hasattr(wl, "tokens"):   # tokens through the step (decode rows, prefill rows, MoE tokens) a second
         res["tokens_per_s"] = round(wl.tokens() / per_step_s, 1)
     if getattr(wl, "peak_key", None) == "fp8":

@@ -187,8 +187,7 @@ def test_moe_prefill_q4_k_gate_up_q6_k_down(dev):
     xb = synth.to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32))
     logits = rng.standard_normal((T, E)).astype(np.float32)
     y, mid = ops.moe_prefill("q4_k", dev_bf16(xb, dev), dev_f32(logits, dev), E, KU, H, FE, 1, True,
-                             w_gate=dev_u8(wg, dev), w_up=dev_u8(wu, dev), w_down=dev_u8(wd, dev), fmt_down="q6_k",
-                            q8=False)
+                             w_gate=dev_u8(wg, dev), w_up=dev_u8(wu, dev), w_down=dev_u8(wd, dev), fmt_down="q6_k")
     torch.cuda.synchronize()
     eids, ewts = ref.route(logits, KU, 1, True)
     np.testing.assert_array_equal(host(mid["ids"]), eids)
