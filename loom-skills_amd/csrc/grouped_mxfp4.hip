@@ -593,6 +593,7 @@ int qmm_grouped_mxfp4(int tiled, int mode, int fused, int act, int64_t max_tiles
   const bool out8 = y8 != nullptr;   // gu with the activation quantized to MXFP8 in the epilogue
   if (out8 && (mode != 0 || n % 32 || !ys8)) return mode != 0 ? QMM_ERR_RANGE : (ys8 ? QMM_ERR_SHAPE : QMM_ERR_NULL);
   if (out8 && !aligned(y8, 16)) return QMM_ERR_ALIGN;
+  if (mode == 0 && !fused && (!w2 || !ws2)) return QMM_ERR_NULL;
   MArgs a{};
   a.N = (int)n; a.K = (int)k;
   a.x8 = static_cast<const u8 *>(x); a.xs = static_cast<const u8 *>(x_scales); a.x_rows = (int)x_rows;

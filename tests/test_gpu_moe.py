@@ -219,6 +219,56 @@ def test_grouped_gemm_alone_hand_made_tiles(dev):
         assert np.all(np.isnan(blk[rows:])), f"dead rows of tile {t} were written"
 
 
+@pytest.mark.parametrize("mode,fused", [("dn", False), ("gu", True), ("gu", False)])
+def test_grouped_mxfp4_tiled_hand_made_table(dev, mode, fused):
+    """The MXFP4 grouped GEMMs on the MFMA-tiled planes over a hand-made tile table: three tiles of one expert (the
+    last of 10 rows), two of another (the last of 5 rows), unused tiles. Every live row against the float64 oracle
+    on the MXFP8 activation; dead rows and unused tiles keep their NaN sentinel (FE = 320: a gate/up column block
+    of 64 live columns of 128)."""
+    import torch
+    from qmm import synth
+    ops = _ops()
+    rng = np.random.default_rng(23 + fused)
+    E, H, FE, KU = 2, 512, 320, 1
+    tiles = [(0, 64), (0, 64), (0, 10), (1, 64), (1, 5), (-1, 0), (-1, 0)]
+    n_tiles = len(tiles)
+    ex = Experts(dev, "mxfp4", rng, E, H, FE, fused)
+    _, kw = ex.device(split=True, tiled=True)
+    tile_info = np.array(tiles, np.int32)
+    rowmap = np.full(n_tiles * 64, -1, np.int32)
+    x_rows = n_tiles * 64
+    for t, (e, rows) in enumerate(tiles):
+        rowmap[64 * t: 64 * t + rows] = np.arange(rows) + 64 * t
+    k = H if mode == "gu" else FE
+    n = FE if mode == "gu" else H
+    xv = rng.standard_normal((x_rows, k)).astype(np.float32) * np.repeat(
+        rng.choice([0.05, 1.0, 20.0], n_tiles), 64)[:, None].astype(np.float32)
+    x8, xs = ops.quant_mxfp8(dev_f32(xv, dev))
+    xr = ref.mxfp8_values(xv)
+    y0 = torch.full((x_rows, n), float("nan"), dtype=torch.float32, device=dev)
+    ti, rm = torch.from_numpy(tile_info).to(dev), torch.from_numpy(rowmap).to(dev)
+    if mode == "gu":
+        y = host(ops.moe_grouped("mxfp4t", "gu", ti, rm, x8, kw["w_gate"], FE, H, E, KU, w2=kw.get("w_up"),
+                                 ws=kw["ws_gate"], ws2=kw.get("ws_up"), x_scales=xs, fused=fused, act="swiglu_oai",
+                                 y=y0))
+    else:
+        y = host(ops.moe_grouped("mxfp4t", "dn", ti, rm, x8, kw["w_down"], H, FE, E, KU, ws=kw["ws_down"],
+                                 x_scales=xs, y=y0))
+    for t, (e, rows) in enumerate(tiles):
+        blk = y[64 * t: 64 * t + 64]
+        if e < 0:
+            assert np.all(np.isnan(blk)), f"unused tile {t} was written"
+            continue
+        a = xr[64 * t: 64 * t + rows].astype(np.float64)
+        if mode == "gu":
+            wg, wu = ex.gate_up(e)
+            want = ref.swiglu_oai(a @ wg.T.astype(np.float64), a @ wu.T.astype(np.float64))
+        else:
+            want = a @ ex.down(e).T.astype(np.float64)
+        assert_close_rel_l2(blk[:rows], want, 1e-3, f"{mode} tile {t}")
+        assert np.all(np.isnan(blk[rows:])), f"dead rows of tile {t} were written"
+
+
 def test_quant_mxfp8_matches_oracle(dev):
     rng = np.random.default_rng(2)
     x = (rng.standard_normal((64, 2880)) * np.exp(rng.uniform(-8, 8, (64, 1)))).astype(np.float32)
@@ -229,10 +279,12 @@ def test_quant_mxfp8_matches_oracle(dev):
     assert np.all(ref.e4m3_decode(c) == ref.e4m3_decode(ec))
 
 
-@pytest.mark.parametrize("T,E,H,FE", [(256, 32, 2880, 2880), (100, 8, 512, 320)])
+@pytest.mark.parametrize("T,E,H,FE", [(256, 32, 2880, 2880), (100, 8, 512, 320), (1024, 32, 2880, 2880),
+                                      (600, 8, 512, 320)])
 def test_grouped_mxfp4_tiled_equals_split_bit_for_bit(dev, T, E, H, FE):
     """The MFMA-tiled planes feed the scaled MFMA the same operands in the same K order as the split planes, so
-    both grouped GEMMs (fused gate_up with swiglu_oai, and down) give identical bits on every live row."""
+    both grouped GEMMs (fused gate_up with swiglu_oai, and down) give identical bits on every live row; also with
+    two or more tiles an expert (T = 1024 at the gpt-oss-20b shape, T = 600 with 8 experts, top-2)."""
     import torch
     from qmm import synth
     ops = _ops()
@@ -280,7 +332,8 @@ def test_tile_mxfp4_bit_exact(dev):
 
 
 @pytest.mark.parametrize("T,E,H,FE,tiled", [(256, 32, 2880, 2880, True), (256, 32, 2880, 2880, False),
-                                            (100, 8, 512, 320, True)])
+                                            (100, 8, 512, 320, True), (1024, 32, 2880, 2880, True),
+                                            (600, 8, 512, 320, True)])
 def test_grouped_gate_up_mxfp8_output_equals_quantized_act(dev, T, E, H, FE, tiled):
     """The gate/up GEMM with the MXFP8 quantization fused into its epilogue writes exactly the codes and scales
     quant_mxfp8 makes of the f32 activation the plain gate/up GEMM writes (every live row; the fused epilogue
