@@ -42,6 +42,13 @@ enum qmm_status {
  * QMM_Q6_K: GGUF Q6_K (210 bytes per 256 values; ffn_down of the Q4_K_M files), read in place from a 4-byte aligned
  *           tensor (its super-blocks start on even addresses). */
 enum qmm_format { QMM_Q4_0 = 0, QMM_Q4_K = 1, QMM_MXFP4 = 2, QMM_MXFP4S = 3, QMM_MXFP4T = 4, QMM_Q4_KT = 5, QMM_Q6_K = 6 };
+/* A gate/up pair whose up matrix has another format than the gate matrix (the reference's "GATE+UP" formats, e.g. a
+ * Q4_K_M layer with a Q4_K gate and a Q6_K up: g_gemm_{fmt}_{fmt2}_swiglu S/gen_gemm.py:535-547, g_moe_ggu_{fg}_{fu}
+ * S/gen_moe.py:1126-1141, g_moe_gu_{fg}_{fu} S/gen_moe.py:535-552): pass QMM_GATE_UP(gate format, up format) as the
+ * `fmt` of a call that computes silu(gate) * up (qmm_mv_swiglu, qmm_gemm in QMM_GEMM_SWIGLU mode, qmm_moe_expert_mv
+ * and qmm_moe_grouped in mode 0, qmm_moe_routed). The high byte holds the up format + 1; a plain format (high byte 0)
+ * is both matrices' format. */
+#define QMM_GATE_UP(gate, up) ((gate) | (((up) + 1) << 8))
 enum qmm_dtype {
   QMM_F32 = 0,
   QMM_F16 = 1,
@@ -79,8 +86,9 @@ int qmm_mv(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const 
 
 /* Decode swiglu matvec, g_mv_{fmt}_k{K}_swiglu[_t{TG}] (S/gen_llm.py:1159-1197; launch args (n, tokens, accumulate,
  * x, w, w2, y)): y[t, r] = (accumulate ? y[t, r] : 0) + silu(sum_k x[t, k] W[r, k]) * (sum_k x[t, k] W2[r, k]),
- * silu(g) = g / (1 + e^-g), fp32 accumulation. fmt QMM_Q4_0 / QMM_Q4_K / QMM_MXFP4 (the reference has no swiglu
- * matvec on split planes); w (gate) and w2 (up) [n, k]; x f32 / bf16 [tokens, k]; y f32 [tokens, n]. */
+ * silu(g) = g / (1 + e^-g), fp32 accumulation. fmt QMM_Q4_0 / QMM_Q4_K / QMM_Q6_K / QMM_MXFP4 (the reference has no
+ * swiglu matvec on split planes), or QMM_GATE_UP(gate, up) of two of them; w (gate) and w2 (up) [n, k]; x f32 / bf16
+ * [tokens, k]; y f32 [tokens, n]. */
 int qmm_mv_swiglu(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
                   const void *w, const void *w2, float *y, qmm_stream_t stream);
 
@@ -131,7 +139,9 @@ int qmm_mv_pair_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate
  * QMM_Q6_K, S/gen_gemm.py:369-444) fma_f16(f16(q), f16(d sc), f16(-32 d sc)) with q the unsigned 6-bit code; Q4_0
  * (fmt QMM_Q4_0, the reference's native Q4_0 staging S/moe_q4_0.py:11-38, S/gen_gemm.py:40-45) f16(q - 8) * d with
  * one f16 rounding, i.e. f16(d (q - 8)) for every finite d. MXFP4 weights go through qmm_gemm_mxfp4.
- * QMM_GEMM_SWIGLU: w is the gate matrix and w2 the up matrix (both [n, k]); silu(g) = g / (1 + e^-g).
+ * QMM_GEMM_SWIGLU: w is the gate matrix and w2 the up matrix (both [n, k]); silu(g) = g / (1 + e^-g); with
+ * fmt = QMM_GATE_UP(gate, up) (Q4_K, Q6_K, Q4_0) the two matrices are in their own formats, g_gemm_{fmt}_{fmt2}_swiglu
+ * (S/gen_gemm.py:535-547, :696-700).
  * Skip-padding (the reference's default GEMM_SKIP_PADDING): with scales, a 64-row tile whose rows all have
  * scales[row, 0] == 0 (padding rows of qmm_row_scale_f16_live) does no work and its y rows are not written. */
 int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, const void *x, int x_dtype, const float *scales,
@@ -203,7 +213,8 @@ int qmm_moe_bucket(int64_t tokens, int KU, int E, int64_t max_tiles, const int32
  * n: output width (FE for gu, H for dn); k: input width. w: expert tensor [E, n, k] (gu: gate; fused != 0: one
  * [E, 2n, k] tensor, each expert's n gate rows then its n up rows, w2 ignored); w2: up tensor [E, n, k] for gu.
  * bias: for gu f32 [E, n] gate bias and bias2 up bias; for dn bias [E, n]; NULL = none. x: [rows, k] of x_dtype
- * (gu: rows = assignments/KU tokens; dn: rows = assignments). y: f32 [assignments, n]. */
+ * (gu: rows = assignments/KU tokens; dn: rows = assignments). y: f32 [assignments, n]. gu with two tensors may take
+ * fmt = QMM_GATE_UP(gate, up) of GGUF formats (g_moe_gu_{fg}_{fu}, S/gen_moe.py:535-552, :643-649). */
 int qmm_moe_expert_mv(int fmt, int mode, int fused, int act, int64_t k, int64_t n, int E, int KU,
                       int64_t assignments, const int32_t *ids, const void *x, int x_dtype, const void *w,
                       const void *w2, const float *bias, const float *bias2, float *y, qmm_stream_t stream);
@@ -248,6 +259,8 @@ int qmm_moe_expert_mv_split(int mode, int fused, int act, int64_t k, int64_t n, 
  *   QMM_Q6_K:   as QMM_Q4_K with Q6_K weights (staged as qmm_gemm stages them); g_moe_gdn_q6_k of the Q4_K_M
  *               expert layout (Q4_K gate / up, Q6_K down).
  *   QMM_Q4_0:   as QMM_Q4_K with Q4_0 weights, staged f16(d (q - 8)) (specialize_grouped, S/moe_q4_0.py:41-61).
+ *   QMM_GATE_UP(gate, up) of QMM_Q4_K / QMM_Q6_K / QMM_Q4_0: gu with two tensors, each in its own format
+ *               (g_moe_ggu_{fg}_{fu}, S/gen_moe.py:1126-1141).
  *   QMM_MXFP4S: weights in split planes, ws / ws2 the E8M0 planes [E, rows, k/32]; x is MXFP8 (x_dtype
  *               QMM_MXFP8) from qmm_quant_mxfp8: E4M3 codes u8 [x_rows, k] with x_scales u8 [x_rows, k/32];
  *               K % 64 == 0; scaled f8f6f4 MFMA, inv = 1.
@@ -380,7 +393,8 @@ int qmm_moe_expert_mv_combine(int fmt, int64_t k, int64_t n, int E, int KU, int6
  *     bf16 activations the down matvecs and the combine run as qmm_moe_expert_mv_combine, and with given logits,
  *     E <= 64 and tokens * KU <= 8 the routing and the gate/up matvecs as qmm_moe_topk_expert_mv.
  * Results equal those of the separate calls bit for bit. Names as in those calls: fmt the gate / up format (GGUF
- * Q4_K / Q6_K / Q4_0 / MXFP4, split MXFP4S, tiled MXFP4T or Q4_KT for prefill), fmt_down the down tensor's (-1: fmt); x f32 /
+ * Q4_K / Q6_K / Q4_0 / MXFP4, split MXFP4S, tiled MXFP4T or Q4_KT for prefill; or QMM_GATE_UP(gate, up) of GGUF
+ * formats with two tensors, without QMM_MOE_Q8), fmt_down the down tensor's (-1: fmt, a pair's gate format); x f32 /
  * bf16 [tokens, H]; logits f32 [tokens, E], or NULL to route with w_router [E, H] (f32 / bf16); router_bias and
  * down_scale (f32 [E]) or NULL; ws_* the split / tiled scale planes; bias_* the expert biases or NULL; y f32
  * [tokens, H] is written, or added to (accumulate), or with sg (f32 [tokens], the shared gate) y = sg y + routed. */

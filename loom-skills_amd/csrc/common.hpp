@@ -95,6 +95,17 @@ inline int raise_dyn_lds(const void *fn, int bytes, std::atomic<unsigned> &done)
   return QMM_OK;
 }
 
+// QMM_GATE_UP(gate, up): the gate matrix's format and the up matrix's (the gate's when the call names one format)
+inline int fmt_gate(int fmt) { return fmt < 0 ? fmt : fmt & 0xFF; }
+inline int fmt_up(int fmt) {
+  if (fmt < 0) return fmt;
+  const int u = (fmt >> 8) & 0xFF;
+  return u ? u - 1 : (fmt & 0xFF);
+}
+inline bool fmt_mixed(int fmt) { return fmt >= 0 && fmt_gate(fmt) != fmt_up(fmt); }
+// a format code is one format or a gate/up pair, nothing more
+inline bool fmt_code_ok(int fmt) { return fmt >= 0 && (fmt >> 16) == 0; }
+
 inline int64_t block_values(int fmt) {
   switch (fmt) {
     case QMM_Q4_0: return 32;

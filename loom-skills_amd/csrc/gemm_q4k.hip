@@ -34,6 +34,8 @@
 //
 // Tile order is XCD-aware: consecutive tile ids land on one XCD (dense: the M tiles of one N tile, which share
 // weight columns; grouped: the column blocks of one expert tile, which share its activation rows).
+#include <type_traits>
+
 #include "common.hpp"
 #include "deq_f16.hpp"
 
@@ -62,6 +64,7 @@ struct Args {
   int x_rows;                  // rows of x16 (gu)
   const u8 *w, *w2;            // dense: W; grouped: expert tensors (gu: gate, up; fused: w only)
   int64_t ebytes;              // bytes of one expert's matrix (grouped)
+  int64_t ebytes2;             // gu, two tensors: bytes of one expert's up matrix (its own format's rows)
   int64_t up_off;              // gu: byte offset of the up matrix from the gate matrix of an expert (fused)
   const int32_t *tile_info, *rowmap;
   const float *bias, *bias2;   // grouped: per-expert output biases [E, N] (gu: gate, up; dn: bias only) or NULL
@@ -75,20 +78,24 @@ struct Args {
 // pairs per column with one 8-byte LDS read instead of loading and decoding the super-block header again.
 constexpr int kStagedMaxK = 6144;
 
-template <int KIND, bool ACC, bool BF16OUT, int DEPTH, bool STAGED, int WF, int KS>
+// WF2: the up matrix's format when it differs from the gate's (kGU / kSwiglu of a QMM_GATE_UP pair): the up waves
+// load and dequantize in their own format, with their own row stride, the gate waves in WF.
+template <int KIND, bool ACC, bool BF16OUT, int DEPTH, bool STAGED, int WF, int KS, int WF2 = WF>
 __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
   constexpr int NT = 128 * KS;   // threads: 2 column halves (or matrices) x KS K-parts
-  constexpr bool Q6 = WF == kWQ6K, Q40 = WF == kWQ40;
+  constexpr bool MIXED = WF2 != WF;
   static_assert(!(WF != kWQ4K && STAGED), "Q6_K / Q4_0 scales are read with the codes");
   constexpr bool kTwoW = KIND == kGU || KIND == kSwiglu;        // two weight matrices (gate, up): wave pairs
+  static_assert(!MIXED || (kTwoW && !STAGED), "a second format is the up matrix's of gate/up, scales read with codes");
   constexpr bool kDenseRows = KIND == kDense || KIND == kSwiglu;  // rows m0 .. m0 + 63 of x, tiles row-major
   constexpr int BN = kTwoW ? 64 : 128;
   extern __shared__ __align__(16) u32 scl[];   // STAGED: [128 columns][K / 32 + 2] (dsc | nmn << 16)
   __shared__ __align__(16) _Float16 As[2][KS][BM][APITCH];   // [buffer][K-part][row][k]
   __shared__ int src_row[BM];
   __shared__ float rinv[BM];   // the row's inverse activation scale (1 without scales)
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int sel = wave & 1, kh = wave >> 1;   // sel: N-half (dense, dn) or matrix (gu: 0 gate, 1 up); kh: K-part
+  const bool upw = MIXED && sel == 1;         // a wave of the up matrix in its own format
   const int M = a.M, N = a.N, K = a.K;
 
   int m0, n0, expert = 0;
@@ -138,7 +145,8 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
   // zeros of dead rows) -- expert tiles of prefill batches are often less than half full
   const bool upper = __syncthreads_or(tid >= 32 && my_src >= 0) != 0;
 
-  const int64_t RB = Q40 ? (int64_t)K / 32 * 18 : (int64_t)K / 256 * (Q6 ? 210 : 144);
+  auto rowb = [&](int f) { return f == kWQ40 ? (int64_t)K / 32 * 18 : (int64_t)K / 256 * (f == kWQ6K ? 210 : 144); };
+  const int64_t RB = upw ? rowb(WF2) : rowb(WF);   // bytes per weight row of the wave's matrix
   const int S = K / KSTEP, S0 = S / KS;
 
   // ---- A staging map: chunk c = i * NT + tid of 16 bytes; K-part, row, 16-byte column. Loads are unconditional
@@ -173,7 +181,7 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
   else if constexpr (KIND == kSwiglu) wbase = sel ? a.w2 : a.w;
   else if constexpr (KIND == kGU) {
     const u8 *g = a.w + (int64_t)expert * a.ebytes;
-    wbase = sel ? (a.w2 ? a.w2 + (int64_t)expert * a.ebytes : g + a.up_off) : g;
+    wbase = sel ? (a.w2 ? a.w2 + (int64_t)expert * a.ebytes2 : g + a.up_off) : g;
   } else {
     wbase = a.w + (int64_t)expert * a.ebytes;
   }
@@ -231,7 +239,7 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
         else if constexpr (KIND == kSwiglu) mb = msel ? a.w2 : a.w;
         else if constexpr (KIND == kGU) {
           const u8 *g = a.w + (int64_t)expert * a.ebytes;
-          mb = msel ? (a.w2 ? a.w2 + (int64_t)expert * a.ebytes : g + a.up_off) : g;
+          mb = msel ? (a.w2 ? a.w2 + (int64_t)expert * a.ebytes2 : g + a.up_off) : g;
         } else {
           mb = a.w + (int64_t)expert * a.ebytes;
         }
@@ -271,18 +279,24 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) aring[slot][i] = a_load(i, st);
   };
-  auto load_b = [&](int slot, int st) {
+  auto load_b_f = [&](auto fc, int slot, int st) __attribute__((always_inline)) {
+    constexpr int F = decltype(fc)::value;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      if constexpr (Q6) {
+      if constexpr (F == kWQ6K) {
         b_q6(j, st, cring[slot][j], q6b[slot][j], q6h[slot][j], q6s[slot][j], q6d[slot][j]);
-      } else if constexpr (Q40) {
+      } else if constexpr (F == kWQ40) {
         b_q40(j, st, cring[slot][j], q6d[slot][j]);
       } else {
         cring[slot][j] = b_code(j, st);
         if constexpr (!STAGED) hring[slot][j] = b_head(j, st);
       }
     }
+  };
+  auto load_b = [&](int slot, int st) __attribute__((always_inline)) {
+    if constexpr (!MIXED) load_b_f(std::integral_constant<int, WF>{}, slot, st);
+    else if (upw) load_b_f(std::integral_constant<int, WF2>{}, slot, st);
+    else load_b_f(std::integral_constant<int, WF>{}, slot, st);
   };
   // The prologue issues its loads in the loop's own order (a step issues the weights of step s + DEPTH, then the
   // activations of step s + 1 + DEPTH). Vector loads complete in issue order for s_waitcnt, and the compiler places
@@ -318,64 +332,70 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) sp[j] = *reinterpret_cast<const u32x2 *>(&scl[(sel * 64 + 32 * j + lc) * SBP + 2 * gstep]);
       }
-#pragma unroll
-      for (int gl = 0; gl < 2; ++gl) {
-        h2 dsc[2], nmn[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          if constexpr (Q40) {
-            const _Float16 d16 = __builtin_bit_cast(_Float16, (u16)q6d[u][j]);
-            dsc[j] = h2{d16, d16};
-            nmn[j] = h2{0, 0};
-          } else if constexpr (Q6) {
-            // f16 (d sc, -32 d sc) of the lane's 16-value run: d sc is exact in f32 (S/gen_gemm.py:435-444)
-            const float sv = f16_to_f32(q6d[u][j]) * (float)(signed char)((q6s[u][j] >> (8 * (2 * gl + h))) & 0xFFu);
-            const _Float16 a16 = (_Float16)sv, b16 = (_Float16)(-32.f * sv);
-            dsc[j] = h2{a16, a16};
-            nmn[j] = h2{b16, b16};
-          } else if constexpr (STAGED) {
-            const u32 v = gl ? sp[j].y : sp[j].x;
-            dsc[j] = as_h2((v & 0xFFFFu) * 0x10001u);
-            nmn[j] = as_h2((v >> 16) * 0x10001u);
-          } else {
-            sub_scale(hring[u][j], 2 * page + gl, dsc[j], nmn[j]);
-          }
-          if (s >= S0) dsc[j] = nmn[j] = h2{0, 0};   // a padding step: zero weights
-        }
-#pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          f16x8 bf[2], af[2];
-#pragma unroll
+      auto math = [&](auto fc) __attribute__((always_inline)) {
+        constexpr int F = decltype(fc)::value;
+  #pragma unroll
+        for (int gl = 0; gl < 2; ++gl) {
+          h2 dsc[2], nmn[2];
+  #pragma unroll
           for (int j = 0; j < 2; ++j) {
-            if constexpr (Q6) {
-              // codes ((ql >> 4 jh) & 15) | (((qh >> (4 jh + 2 gl)) & 3) << 4), four to a dword
-              const uint4 &ql = gl ? q6b[u][j] : cring[u][j];
-              const u32 l0 = s2 ? ql.z : ql.x, l1 = s2 ? ql.w : ql.y;
-              const u32 h0 = s2 ? q6h[u][j].z : q6h[u][j].x, h1 = s2 ? q6h[u][j].w : q6h[u][j].y;
-              const u32 ls = 4u * (u32)(page & 1), hs = ls + 2u * (u32)gl;
-              const u32 c0 = ((l0 >> ls) & 0x0F0F0F0Fu) | (((h0 >> hs) & 0x03030303u) << 4);
-              const u32 c1 = ((l1 >> ls) & 0x0F0F0F0Fu) | (((h1 >> hs) & 0x03030303u) << 4);
-              bf[j] = deq8_codes(c0, c1, dsc[j], nmn[j]);
-            } else if constexpr (Q40) {
-              const u32 q0 = s2 ? cring[u][j].z : cring[u][j].x, q1 = s2 ? cring[u][j].w : cring[u][j].y;
-              bf[j] = gl ? deq8_q40<true>(q0, q1, dsc[j]) : deq8_q40<false>(q0, q1, dsc[j]);
+            if constexpr (F == kWQ40) {
+              const _Float16 d16 = __builtin_bit_cast(_Float16, (u16)q6d[u][j]);
+              dsc[j] = h2{d16, d16};
+              nmn[j] = h2{0, 0};
+            } else if constexpr (F == kWQ6K) {
+              // f16 (d sc, -32 d sc) of the lane's 16-value run: d sc is exact in f32 (S/gen_gemm.py:435-444)
+              const float sv = f16_to_f32(q6d[u][j]) * (float)(signed char)((q6s[u][j] >> (8 * (2 * gl + h))) & 0xFFu);
+              const _Float16 a16 = (_Float16)sv, b16 = (_Float16)(-32.f * sv);
+              dsc[j] = h2{a16, a16};
+              nmn[j] = h2{b16, b16};
+            } else if constexpr (STAGED) {
+              const u32 v = gl ? sp[j].y : sp[j].x;
+              dsc[j] = as_h2((v & 0xFFFFu) * 0x10001u);
+              nmn[j] = as_h2((v >> 16) * 0x10001u);
             } else {
-              const u32 q0 = s2 ? cring[u][j].z : cring[u][j].x, q1 = s2 ? cring[u][j].w : cring[u][j].y;
-              bf[j] = gl ? deq8_e4m3<true>(q0, q1, dsc[j], nmn[j]) : deq8_e4m3<false>(q0, q1, dsc[j], nmn[j]);
+              sub_scale(hring[u][j], 2 * page + gl, dsc[j], nmn[j]);
+            }
+            if (s >= S0) dsc[j] = nmn[j] = h2{0, 0};   // a padding step: zero weights
+          }
+  #pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) {
+            f16x8 bf[2], af[2];
+  #pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              if constexpr (F == kWQ6K) {
+                // codes ((ql >> 4 jh) & 15) | (((qh >> (4 jh + 2 gl)) & 3) << 4), four to a dword
+                const uint4 &ql = gl ? q6b[u][j] : cring[u][j];
+                const u32 l0 = s2 ? ql.z : ql.x, l1 = s2 ? ql.w : ql.y;
+                const u32 h0 = s2 ? q6h[u][j].z : q6h[u][j].x, h1 = s2 ? q6h[u][j].w : q6h[u][j].y;
+                const u32 ls = 4u * (u32)(page & 1), hs = ls + 2u * (u32)gl;
+                const u32 c0 = ((l0 >> ls) & 0x0F0F0F0Fu) | (((h0 >> hs) & 0x03030303u) << 4);
+                const u32 c1 = ((l1 >> ls) & 0x0F0F0F0Fu) | (((h1 >> hs) & 0x03030303u) << 4);
+                bf[j] = deq8_codes(c0, c1, dsc[j], nmn[j]);
+              } else if constexpr (F == kWQ40) {
+                const u32 q0 = s2 ? cring[u][j].z : cring[u][j].x, q1 = s2 ? cring[u][j].w : cring[u][j].y;
+                bf[j] = gl ? deq8_q40<true>(q0, q1, dsc[j]) : deq8_q40<false>(q0, q1, dsc[j]);
+              } else {
+                const u32 q0 = s2 ? cring[u][j].z : cring[u][j].x, q1 = s2 ? cring[u][j].w : cring[u][j].y;
+                bf[j] = gl ? deq8_e4m3<true>(q0, q1, dsc[j], nmn[j]) : deq8_e4m3<false>(q0, q1, dsc[j], nmn[j]);
+              }
+            }
+            const int ak = F == kWQ40 ? 32 * h + 16 * gl + 8 * s2 : 32 * gl + 16 * h + 8 * s2;   // the lane's K position
+            af[0] = *reinterpret_cast<const f16x8 *>(&As[buf][kh][lc][ak]);
+  #pragma unroll
+            for (int j = 0; j < 2; ++j) acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[0], bf[j], acc[0][j], 0, 0, 0);
+            if (upper) {
+              af[1] = *reinterpret_cast<const f16x8 *>(&As[buf][kh][32 + lc][ak]);
+  #pragma unroll
+              for (int j = 0; j < 2; ++j)
+                acc[1][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[1], bf[j], acc[1][j], 0, 0, 0);
             }
           }
-          const int ak = Q40 ? 32 * h + 16 * gl + 8 * s2 : 32 * gl + 16 * h + 8 * s2;   // the lane's K position
-          af[0] = *reinterpret_cast<const f16x8 *>(&As[buf][kh][lc][ak]);
-#pragma unroll
-          for (int j = 0; j < 2; ++j) acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[0], bf[j], acc[0][j], 0, 0, 0);
-          if (upper) {
-            af[1] = *reinterpret_cast<const f16x8 *>(&As[buf][kh][32 + lc][ak]);
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-              acc[1][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[1], bf[j], acc[1][j], 0, 0, 0);
-          }
         }
-      }
+      };
+      if constexpr (!MIXED) math(std::integral_constant<int, WF>{});
+      else if (upw) math(std::integral_constant<int, WF2>{});
+      else math(std::integral_constant<int, WF>{});
       load_b(u, s + DEPTH);
       const int nx = (u + 1) % DEPTH;
 #pragma unroll
@@ -511,6 +531,32 @@ int launch_fmt(int fmt, const Args &a, hipStream_t s) {
   return launch<KIND, ACC, BF16OUT, kWQ4K>(a, s);
 }
 
+// A gate/up pair in two formats (kSwiglu dense rows, kGU expert tiles): gate format WG, up format WU. Two K-parts
+// (one wave a SIMD): the register rings of both formats would spill at two waves a SIMD.
+template <int KIND, bool BF16OUT, int WG, int WU>
+int launch_pair(const Args &a, hipStream_t s) {
+  constexpr bool kDenseRows = KIND == kSwiglu;
+  constexpr int KS = 2;
+  const dim3 grid((unsigned)(kDenseRows ? 8 * ((a.tiles_total + 7) / 8) : 8 * a.n_blocks * ((a.tiles_m + 7) / 8)));
+  q4k_mfma_kernel<KIND, false, BF16OUT, kDepth, false, WG, KS, WU><<<grid, 128 * KS, 0, s>>>(a);
+  return launch_status();
+}
+int wfmt_of(int fmt) { return fmt == QMM_Q6_K ? kWQ6K : fmt == QMM_Q4_0 ? kWQ40 : kWQ4K; }
+template <int KIND, bool BF16OUT, int WG>
+int launch_pair_up(int wu, const Args &a, hipStream_t s) {
+  if (wu == kWQ6K) return launch_pair<KIND, BF16OUT, WG, kWQ6K>(a, s);
+  if (wu == kWQ40) return launch_pair<KIND, BF16OUT, WG, kWQ40>(a, s);
+  return launch_pair<KIND, BF16OUT, WG, kWQ4K>(a, s);
+}
+template <int KIND, bool BF16OUT>
+int launch_mixed(int fg, int fu, const Args &a, hipStream_t s) {
+  const int wg = wfmt_of(fg), wu = wfmt_of(fu);
+  if (wg == kWQ6K) return launch_pair_up<KIND, BF16OUT, kWQ6K>(wu, a, s);
+  if (wg == kWQ40) return launch_pair_up<KIND, BF16OUT, kWQ40>(wu, a, s);
+  return launch_pair_up<KIND, BF16OUT, kWQ4K>(wu, a, s);
+}
+bool gguf_gemm_fmt(int f) { return f == QMM_Q4_K || f == QMM_Q6_K || f == QMM_Q4_0; }
+
 // bytes per row of K values, and the weight alignment the loads need (Q4_K: 16; Q6_K: 4, super-blocks realigned from
 // even addresses; Q4_0: 2, 16-byte code runs read from even addresses)
 int64_t fmt_row_bytes(int fmt, int64_t k) {
@@ -527,6 +573,11 @@ int qmm_gemm_q4k_dense(int acc, int64_t rows, int64_t k, int64_t n, const void *
 extern "C" int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, const void *x, int x_dtype,
                         const float *scales, const void *w, const void *w2, void *y, int y_dtype,
                         qmm_stream_t stream) {
+  if (!fmt_code_ok(fmt)) return QMM_ERR_FORMAT;
+  const int fu = fmt_up(fmt);   // QMM_GATE_UP(gate, up): the up matrix of the swiglu mode in its own format
+  const bool mixed = fmt_mixed(fmt);
+  fmt = fmt_gate(fmt);
+  if (mixed && (mode != QMM_GEMM_SWIGLU || !gguf_gemm_fmt(fu))) return QMM_ERR_FORMAT;
   if (fmt != QMM_Q4_K && fmt != QMM_Q6_K && fmt != QMM_Q4_0) return QMM_ERR_FORMAT;   // MXFP4: qmm_gemm_mxfp4
   if (mode != QMM_GEMM_STORE && mode != QMM_GEMM_ACC && mode != QMM_GEMM_SWIGLU) return QMM_ERR_RANGE;
   if (!x || !w || !y || (mode == QMM_GEMM_SWIGLU && !w2)) return QMM_ERR_NULL;
@@ -535,9 +586,11 @@ extern "C" int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, c
   if (rows <= 0 || n <= 0 || k <= 0 || k % 256) return QMM_ERR_SHAPE;
   if (rows > (1 << 24) || n > (1 << 24) || k > (1 << 20)) return QMM_ERR_SHAPE;
   const int wal = fmt_align(fmt);
-  if (!aligned(x, 16) || !aligned(w, wal) || !aligned(y, 4) || (w2 && !aligned(w2, wal))) return QMM_ERR_ALIGN;
+  if (!aligned(x, 16) || !aligned(w, wal) || !aligned(y, 4) || (w2 && !aligned(w2, fmt_align(fu))))
+    return QMM_ERR_ALIGN;
   if (rows * k * 2 >= (1ll << 31)) return QMM_ERR_SHAPE;   // activation rows are addressed by a 32-bit buffer offset
-  if (n * fmt_row_bytes(fmt, k) >= (1ll << 31)) return QMM_ERR_SHAPE;   // so are the weight rows (buffer size, offsets)
+  if (n * fmt_row_bytes(fmt, k) >= (1ll << 31) || n * fmt_row_bytes(fu, k) >= (1ll << 31))
+    return QMM_ERR_SHAPE;   // so are the weight rows (buffer size, offsets)
   Args a{};
   a.M = (int)rows; a.N = (int)n; a.K = (int)k;
   a.x16 = static_cast<const _Float16 *>(x); a.scales = scales; a.x_rows = (int)rows;
@@ -547,6 +600,7 @@ extern "C" int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, c
   const bool acc = mode == QMM_GEMM_ACC, bf = y_dtype == QMM_BF16;
   if (mode == QMM_GEMM_SWIGLU) {   // 64 output columns a workgroup: its wave pairs take the gate and the up matrix
     a.tiles_total = a.tiles_m * (int)((n + 63) / 64);
+    if (mixed) return bf ? launch_mixed<kSwiglu, true>(fmt, fu, a, s) : launch_mixed<kSwiglu, false>(fmt, fu, a, s);
     return bf ? launch_fmt<kSwiglu, false, true>(fmt, a, s) : launch_fmt<kSwiglu, false, false>(fmt, a, s);
   }
   if (fmt == QMM_Q4_K) return qmm_gemm_q4k_dense(acc, rows, k, n, x, scales, w, y, bf, s);
@@ -574,6 +628,26 @@ int qmm_grouped_q4k(int fmt, int mode, int fused, int act, int64_t max_tiles, in
                     hipStream_t s) {
   if (k % 256) return QMM_ERR_SHAPE;
   if (x_rows * k * 2 >= (1ll << 31)) return QMM_ERR_SHAPE;   // activation rows are addressed by a 32-bit buffer offset
+  if (fmt_mixed(fmt)) {
+    // QMM_GATE_UP(gate, up), gate/up of two tensors in GGUF blocks: the 64-row tile kernel, the up waves in the up
+    // format (g_moe_ggu_{fg}_{fu}, S/gen_moe.py:1126-1141)
+    const int fg = fmt_gate(fmt), fu = fmt_up(fmt);
+    if (mode != 0 || fused || !gguf_gemm_fmt(fg) || !gguf_gemm_fmt(fu)) return QMM_ERR_FORMAT;
+    if (!aligned(x, 16) || !aligned(w, fmt_align(fg)) || !aligned(w2, fmt_align(fu))) return QMM_ERR_ALIGN;
+    Args a{};
+    a.M = (int)(max_tiles * BM); a.N = (int)n; a.K = (int)k;
+    a.x16 = static_cast<const _Float16 *>(x); a.scales = x_scales; a.x_rows = (int)x_rows;
+    a.tile_info = tile_info; a.rowmap = rowmap; a.KU = KU; a.E = E; a.act = act; a.y = y;
+    a.bias = bias; a.bias2 = bias2;
+    a.w = static_cast<const u8 *>(w); a.w2 = static_cast<const u8 *>(w2);
+    a.ebytes = fmt_row_bytes(fg, k) * n;
+    a.ebytes2 = fmt_row_bytes(fu, k) * n;
+    a.up_off = 0;
+    a.n_blocks = (int)((n + 63) / 64);
+    a.tiles_m = (int)max_tiles;
+    a.tiles_total = (int)max_tiles * a.n_blocks;
+    return launch_mixed<kGU, false>(fg, fu, a, s);
+  }
   const int wal = fmt_align(fmt);
   if (!aligned(x, 16) || !aligned(w, wal) || (w2 && !aligned(w2, wal))) return QMM_ERR_ALIGN;
   // The tiled layout is read by the narrow kernel only. GGUF Q4_K with few rows an expert (max_tiles = assignments /
@@ -598,6 +672,7 @@ int qmm_grouped_q4k(int fmt, int mode, int fused, int act, int64_t max_tiles, in
   if (mode == 0) {
     if (!fused && !w2) return QMM_ERR_NULL;
     a.ebytes = RB * n * (fused ? 2 : 1);
+    a.ebytes2 = RB * n;
     a.up_off = fused ? RB * n : 0;
     a.w2 = fused ? nullptr : static_cast<const u8 *>(w2);
     a.n_blocks = (int)((n + 63) / 64);

@@ -185,6 +185,71 @@ __global__ __launch_bounds__(256) void expert_mv_kernel(int64_t n, int64_t assig
   }
 }
 
+// The gate/up expert matvecs with gate and up in different formats (the reference's "GATE+UP" expert tensors,
+// g_moe_gu_{fg}_{fu}_k{K}_r{R}, S/gen_moe.py:535-552; with no ids one expert: the dense swiglu matvec): the gate
+// rows are walked in the gate format's items and the up rows in the up format's, each with the one-format kernel's
+// per-lane arithmetic and butterfly, then act_fn(g + bg, u + bu) as there.
+template <class PG, class PU, int RW>
+__global__ __launch_bounds__(256) void expert_mv_mixed_kernel(int64_t n, int64_t assignments, int KU, int E, int64_t k,
+                                                              const int32_t *__restrict__ ids, const u8 *__restrict__ x,
+                                                              int64_t x_row_bytes, const u8 *__restrict__ w,
+                                                              const u8 *__restrict__ w2, int64_t rbg, int64_t rbu,
+                                                              const float *__restrict__ bias,
+                                                              const float *__restrict__ bias2, int act, int accumulate,
+                                                              float *__restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t a = blockIdx.x;
+  const int64_t row0 = ((int64_t)blockIdx.y * kWavesPerBlock + wave) * RW;
+  if (row0 >= n || a >= assignments) return;
+  int e = ids ? ids[a] : 0;
+  e = e < 0 ? 0 : (e >= E ? E - 1 : e);
+  const u8 *xr = x + (a / KU) * x_row_bytes;
+  const u8 *we = w + e * (rbg * n), *w2e = w2 + e * (rbu * n);
+  float ag[RW], au[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) ag[r] = au[r] = 0.f;
+  const int ng = PG::items(k), nu = PU::items(k);
+  for (int it0 = 0; it0 < ng; it0 += 64) {
+    const int item = it0 + lane;
+    const bool live = item < ng;
+    typename PG::X xs;
+    PG::load_x(xr, item, live, xs);
+    typename PG::W wg[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) PG::load_w(we + (row0 + r) * rbg, we, item, live && (row0 + r) < n, wg[r]);
+#pragma unroll
+    for (int r = 0; r < RW; ++r) ag[r] += PG::dot(wg[r], xs, item);
+  }
+  for (int it0 = 0; it0 < nu; it0 += 64) {
+    const int item = it0 + lane;
+    const bool live = item < nu;
+    typename PU::X xs;
+    PU::load_x(xr, item, live, xs);
+    typename PU::W wu[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) PU::load_w(w2e + (row0 + r) * rbu, w2e, item, live && (row0 + r) < n, wu[r]);
+#pragma unroll
+    for (int r = 0; r < RW; ++r) au[r] += PU::dot(wu[r], xs, item);
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    ag[r] = wave_sum(ag[r]);
+    au[r] = wave_sum(au[r]);
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int64_t row = row0 + r;
+    if (lane == r && row < n) {
+      float g = ag[r], u = au[r];
+      if (bias) g += bias[e * n + row];
+      if (bias2) u += bias2[e * n + row];
+      const float v = act_fn(act, g, u);
+      y[a * n + row] = accumulate ? y[a * n + row] + v : v;
+    }
+  }
+}
+
 // The decode chain's down matvecs and combine in one launch: workgroup (row block, token t) runs one wave per
 // routed slot j of t, all over the same RW rows. Each wave does expert_mv_kernel's per-lane arithmetic and
 // butterfly for its assignment t*KU + j (so its row sums are the separate call's ys, bit for bit); one lane a
@@ -398,6 +463,48 @@ int dispatch_expert(bool gu, bool bf, int64_t k, int64_t n, int E, int KU, int64
             : launch_expert<P<false>, false>(k, n, E, KU, assignments, ids, x, xb, w, ws, w2, ws2, rb, srb, ebytes, esbytes, bias, bias2, act, y, s);
 }
 
+template <class PG, class PU>
+int launch_mixed(int64_t k, int64_t n, int E, int KU, int64_t assignments, const int32_t *ids, const void *x,
+                 int64_t x_row_bytes, const void *w, const void *w2, int64_t rbg, int64_t rbu, const float *bias,
+                 const float *bias2, int act, int accumulate, float *y, hipStream_t s) {
+  constexpr int RW = expert_rw<true>();
+  const dim3 grid((unsigned)assignments, (unsigned)((n + kWavesPerBlock * RW - 1) / (kWavesPerBlock * RW)));
+  expert_mv_mixed_kernel<PG, PU, RW><<<grid, 256, 0, s>>>(
+      n, assignments, KU, E, k, ids, static_cast<const u8 *>(x), x_row_bytes, static_cast<const u8 *>(w),
+      static_cast<const u8 *>(w2), rbg, rbu, bias, bias2, act, accumulate, y);
+  return launch_status();
+}
+
+// gate format PG, then the up format from its code (GGUF blocks: Q4_0, Q4_K, Q6_K, MXFP4)
+template <template <bool> class PG, bool B>
+int dispatch_mixed_up(int fu, int64_t k, int64_t n, int E, int KU, int64_t assignments, const int32_t *ids,
+                      const void *x, const void *w, const void *w2, int64_t rbg, int64_t rbu, const float *bias,
+                      const float *bias2, int act, int accumulate, float *y, hipStream_t s) {
+  const int64_t xb = k * (B ? 2 : 4);
+  switch (fu) {
+    case QMM_Q4_K: return launch_mixed<PG<B>, Q4K<B>>(k, n, E, KU, assignments, ids, x, xb, w, w2, rbg, rbu, bias, bias2, act, accumulate, y, s);
+    case QMM_Q6_K: return launch_mixed<PG<B>, Q6K<B>>(k, n, E, KU, assignments, ids, x, xb, w, w2, rbg, rbu, bias, bias2, act, accumulate, y, s);
+    case QMM_Q4_0: return launch_mixed<PG<B>, Q40<B>>(k, n, E, KU, assignments, ids, x, xb, w, w2, rbg, rbu, bias, bias2, act, accumulate, y, s);
+    default: return launch_mixed<PG<B>, MXG<B>>(k, n, E, KU, assignments, ids, x, xb, w, w2, rbg, rbu, bias, bias2, act, accumulate, y, s);
+  }
+}
+
+template <bool B>
+int dispatch_mixed(int fg, int fu, int64_t k, int64_t n, int E, int KU, int64_t assignments, const int32_t *ids,
+                   const void *x, const void *w, const void *w2, const float *bias, const float *bias2, int act,
+                   int accumulate, float *y, hipStream_t s) {
+  const int64_t rbg = row_bytes(fg, k), rbu = row_bytes(fu, k);
+  switch (fg) {
+    case QMM_Q4_K: return dispatch_mixed_up<Q4K, B>(fu, k, n, E, KU, assignments, ids, x, w, w2, rbg, rbu, bias, bias2, act, accumulate, y, s);
+    case QMM_Q6_K: return dispatch_mixed_up<Q6K, B>(fu, k, n, E, KU, assignments, ids, x, w, w2, rbg, rbu, bias, bias2, act, accumulate, y, s);
+    case QMM_Q4_0: return dispatch_mixed_up<Q40, B>(fu, k, n, E, KU, assignments, ids, x, w, w2, rbg, rbu, bias, bias2, act, accumulate, y, s);
+    default: return dispatch_mixed_up<MXG, B>(fu, k, n, E, KU, assignments, ids, x, w, w2, rbg, rbu, bias, bias2, act, accumulate, y, s);
+  }
+}
+
+// the formats a mixed gate/up pair takes: GGUF blocks (each matrix read in place)
+bool mixed_fmt_ok(int f) { return f == QMM_Q4_0 || f == QMM_Q4_K || f == QMM_Q6_K || f == QMM_MXFP4; }
+
 template <template <bool> class P, int RW>
 int launch_expert_combine_rw(bool bf, int64_t k, int64_t n, int E, int KU, int64_t tokens, const int32_t *ids,
                              const float *wts, const void *x, const void *w, const void *ws, int64_t rb, int64_t srb,
@@ -438,6 +545,26 @@ static int expert_mv_impl(int fmt, int mode, int fused, int act, int64_t k, int6
                           int64_t assignments, const int32_t *ids, const void *x, int x_dtype, const void *w,
                           const void *ws, const void *w2, const void *ws2, const float *bias, const float *bias2,
                           float *y, qmm_stream_t stream) {
+  if (fmt_code_ok(fmt) && fmt_mixed(fmt)) {
+    // QMM_GATE_UP(gate, up): gate/up only (the down matvec has one matrix), two tensors (a fused gate_up tensor has
+    // one format)
+    const int fg = fmt_gate(fmt), fu = fmt_up(fmt);
+    if (!mixed_fmt_ok(fg) || !mixed_fmt_ok(fu) || mode != 0 || fused) return QMM_ERR_FORMAT;
+    if (act != QMM_ACT_SILU && act != QMM_ACT_SWIGLU_OAI) return QMM_ERR_RANGE;
+    if (E <= 0 || E > 1024 || KU <= 0 || KU > 8) return QMM_ERR_RANGE;
+    if (!ids || !x || !y || !w || !w2) return QMM_ERR_NULL;
+    if (n <= 0 || assignments <= 0 || assignments > (1 << 24) || assignments % KU || row_bytes(fg, k) == 0 ||
+        row_bytes(fu, k) == 0)
+      return QMM_ERR_SHAPE;
+    if (x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
+    if (int st = check_weights(fg, k, w, nullptr)) return st;
+    if (int st = check_weights(fu, k, w2, nullptr)) return st;
+    if (!aligned(x, 16) || !aligned(y, 4)) return QMM_ERR_ALIGN;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    return x_dtype == QMM_BF16
+               ? dispatch_mixed<true>(fg, fu, k, n, E, KU, assignments, ids, x, w, w2, bias, bias2, act, 0, y, s)
+               : dispatch_mixed<false>(fg, fu, k, n, E, KU, assignments, ids, x, w, w2, bias, bias2, act, 0, y, s);
+  }
   if (!valid_fmt(fmt)) return QMM_ERR_FORMAT;
   if (mode != 0 && mode != 1) return QMM_ERR_RANGE;
   if (act != QMM_ACT_SILU && act != QMM_ACT_SWIGLU_OAI) return QMM_ERR_RANGE;
@@ -473,6 +600,23 @@ static int expert_mv_impl(int fmt, int mode, int fused, int act, int64_t k, int6
 
 extern "C" int qmm_mv_swiglu(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x,
                              int x_dtype, const void *w, const void *w2, float *y, qmm_stream_t stream) {
+  if (fmt_code_ok(fmt) && fmt_mixed(fmt)) {   // QMM_GATE_UP(gate, up): the gate and up matrices in their own formats
+    const int fg = fmt_gate(fmt), fu = fmt_up(fmt);
+    if (!mixed_fmt_ok(fg) || !mixed_fmt_ok(fu)) return QMM_ERR_FORMAT;
+    if (!x || !w || !w2 || !y) return QMM_ERR_NULL;
+    if (n <= 0 || tokens <= 0 || tokens > (1 << 24) || row_bytes(fg, k) == 0 || row_bytes(fu, k) == 0)
+      return QMM_ERR_SHAPE;
+    if (x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
+    if (int st = check_weights(fg, k, w, nullptr)) return st;
+    if (int st = check_weights(fu, k, w2, nullptr)) return st;
+    if (!aligned(x, 16) || !aligned(y, 4)) return QMM_ERR_ALIGN;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    return x_dtype == QMM_BF16
+               ? dispatch_mixed<true>(fg, fu, k, n, 1, 1, tokens, nullptr, x, w, w2, nullptr, nullptr, QMM_ACT_SILU,
+                                      accumulate, y, s)
+               : dispatch_mixed<false>(fg, fu, k, n, 1, 1, tokens, nullptr, x, w, w2, nullptr, nullptr, QMM_ACT_SILU,
+                                       accumulate, y, s);
+  }
   if (fmt != QMM_Q4_0 && fmt != QMM_Q4_K && fmt != QMM_MXFP4 && fmt != QMM_Q6_K) return QMM_ERR_FORMAT;
   if (!x || !w || !w2 || !y) return QMM_ERR_NULL;
   if (n <= 0 || tokens <= 0 || tokens > (1 << 24) || row_bytes(fmt, k) == 0) return QMM_ERR_SHAPE;

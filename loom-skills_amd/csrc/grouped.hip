@@ -33,9 +33,12 @@ extern "C" int qmm_moe_grouped(int fmt, int mode, int fused, int act, int E, int
                                const void *w2, const void *ws2, const float *bias, const float *bias2, float *y,
                                qmm_stream_t stream) {
   using namespace qmm;
-  if (fmt != QMM_Q4_K && fmt != QMM_Q4_KT && fmt != QMM_Q6_K && fmt != QMM_Q4_0 && fmt != QMM_MXFP4S &&
-      fmt != QMM_MXFP4T)
+  if (!fmt_code_ok(fmt)) return QMM_ERR_FORMAT;
+  const bool mixed = fmt_mixed(fmt);   // QMM_GATE_UP(gate, up): GGUF gate / up tensors in two formats
+  const int fg = fmt_gate(fmt);
+  if (fg != QMM_Q4_K && fg != QMM_Q4_KT && fg != QMM_Q6_K && fg != QMM_Q4_0 && fg != QMM_MXFP4S && fg != QMM_MXFP4T)
     return QMM_ERR_FORMAT;
+  if (mixed && (mode != 0 || fused)) return QMM_ERR_FORMAT;   // one up tensor in its own format, gate/up only
   if (mode != 0 && mode != 1) return QMM_ERR_RANGE;
   if (int st = check_grouped(act, E, KU, max_rows, k, n, x_rows, tile_info, rowmap, x, w)) return st;
   if (!y) return QMM_ERR_NULL;
@@ -45,7 +48,7 @@ extern "C" int qmm_moe_grouped(int fmt, int mode, int fused, int act, int E, int
   if (!aligned(y, 4) || !aligned(bias, 4) || !aligned(bias2, 4)) return QMM_ERR_ALIGN;
   const int64_t max_tiles = max_rows / 64;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (fmt == QMM_Q4_K || fmt == QMM_Q4_KT || fmt == QMM_Q6_K || fmt == QMM_Q4_0) {
+  if (mixed || fmt == QMM_Q4_K || fmt == QMM_Q4_KT || fmt == QMM_Q6_K || fmt == QMM_Q4_0) {
     if (x_dtype != QMM_F16) return QMM_ERR_DTYPE;
     return qmm_grouped_q4k(fmt, mode, fused, act, max_tiles, k, n, E, KU, tile_info, rowmap, x,
                            static_cast<const float *>(x_scales), x_rows, w, w2, bias, bias2, y, s);

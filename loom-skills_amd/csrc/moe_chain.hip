@@ -34,6 +34,7 @@ struct Plan {
 };
 
 Plan moe_plan(int fmt, int flags, int E, int KU, int64_t T, int64_t H, int64_t FE, bool router) {
+  fmt = fmt_gate(fmt);   // a QMM_GATE_UP pair plans as its gate format (GGUF blocks either way)
   Plan p{};
   p.prefill = T >= kMinPrefillTokens;
   p.q8 = !p.prefill && (flags & QMM_MOE_Q8);
@@ -75,6 +76,13 @@ Plan moe_plan(int fmt, int flags, int E, int KU, int64_t T, int64_t H, int64_t F
 
 int check_chain(int fmt, int fmt_down, int flags, int E, int KU, int64_t T, int64_t H, int64_t FE) {
   if (E <= 0 || E > 256 || KU <= 0 || KU > 8 || KU > E) return QMM_ERR_RANGE;
+  if (!fmt_code_ok(fmt) || fmt_mixed(fmt_down)) return QMM_ERR_FORMAT;
+  if (fmt_mixed(fmt)) {
+    // QMM_GATE_UP(gate, up): GGUF gate / up tensors in two formats (two tensors), f32 / bf16 decode activations (the
+    // reference's int8 expert matvecs take one format, S/gen_moe.py:545)
+    if (!gguf_blocks(fmt_gate(fmt)) || !gguf_blocks(fmt_up(fmt)) || (flags & QMM_MOE_Q8)) return QMM_ERR_FORMAT;
+    fmt = fmt_gate(fmt);
+  }
   if (flags & ~QMM_MOE_Q8) return QMM_ERR_RANGE;
   if (T <= 0 || T > 65536 || H <= 0 || FE <= 0 || H > (1 << 20) || FE > (1 << 20)) return QMM_ERR_SHAPE;
   const bool prefill = T >= kMinPrefillTokens;
@@ -95,7 +103,7 @@ int check_chain(int fmt, int fmt_down, int flags, int E, int KU, int64_t T, int6
 
 extern "C" int64_t qmm_moe_routed_workspace_size(int fmt, int flags, int E, int KU, int64_t tokens, int64_t H,
                                                  int64_t FE, int router) {
-  if (check_chain(fmt, fmt, flags, E, KU, tokens, H, FE) != QMM_OK) return -1;
+  if (check_chain(fmt, fmt_gate(fmt), flags, E, KU, tokens, H, FE) != QMM_OK) return -1;
   return moe_plan(fmt, flags, E, KU, tokens, H, FE, router != 0).total;
 }
 
@@ -107,10 +115,11 @@ extern "C" int qmm_moe_routed(int fmt, int fmt_down, int fused, int act, int gat
                               const void *ws_down, const float *bias_gate, const float *bias_up,
                               const float *bias_down, const float *sg, int accumulate, float *y, void *workspace,
                               int64_t workspace_bytes, qmm_stream_t stream) {
-  if (fmt_down < 0) fmt_down = fmt;
+  if (fmt_down < 0) fmt_down = fmt_gate(fmt);
   if (int st = check_chain(fmt, fmt_down, flags, E, KU, tokens, H, FE)) return st;
   if (!x || !y || !w_gate || !w_down || (!logits && !w_router)) return QMM_ERR_NULL;
   if (!fused && !w_up) return QMM_ERR_NULL;   // an unfused gate/up reads its up matrix in every chain
+  if (fused && fmt_mixed(fmt)) return QMM_ERR_FORMAT;   // one fused gate_up tensor has one format
   if (x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
   const Plan p = moe_plan(fmt, flags, E, KU, tokens, H, FE, logits == nullptr);
   if (!workspace) return QMM_ERR_NULL;
@@ -128,7 +137,7 @@ extern "C" int qmm_moe_routed(int fmt, int fmt_down, int fused, int act, int gat
   // decode with given logits on f32 / bf16 activations, one key slot a lane and few assignments: the routing runs
   // inside the gate/up matvecs (every workgroup ranks its token itself: gpt-oss-20b at one token 25.0 -> 23.9 us;
   // slower with 128 experts or eight tokens)
-  const bool route_gu = !p.prefill && !p.q8 && logits && E <= 64 && p.A <= 8;
+  const bool route_gu = !p.prefill && !p.q8 && logits && E <= 64 && p.A <= 8 && !fmt_mixed(fmt);
   if (route_gu)
     st = fmt == QMM_MXFP4S
              ? qmm_moe_topk_expert_mv(logits, T, E, KU, gating, norm, scale, router_bias, ids, wts, fmt, fused, act, H,

@@ -11,7 +11,23 @@ SB = {"q4_0": 32, "q4_k": 256, "mxfp4": 32, "mxfp4s": 32, "mxfp4t": 32, "q4_kt":
 SPLIT = frozenset({"mxfp4s", "mxfp4t"})                         # weight plane + scale plane (two operands)
 SCALE_DIV = {"mxfp4s": 16}                                      # nibble-plane bytes per scale-plane byte
 
-CODE = {"q4_0": 0, "q4_k": 1, "mxfp4": 2, "mxfp4s": 3, "mxfp4t": 4, "q4_kt": 5, "q6_k": 6}   # enum qmm_format
+class _Codes(dict):
+    """enum qmm_format; a key "gate+up" (the reference's GATE+UP notation for gate and up matrices in two formats,
+    S/gen_moe.py:535-552) gives QMM_GATE_UP(gate, up) = gate | (up + 1) << 8."""
+
+    def __missing__(self, key):
+        if isinstance(key, str) and key.count("+") == 1:
+            g, u = key.split("+")
+            return self[g] | ((self[u] + 1) << 8)
+        raise KeyError(key)
+
+
+CODE = _Codes({"q4_0": 0, "q4_k": 1, "mxfp4": 2, "mxfp4s": 3, "mxfp4t": 4, "q4_kt": 5, "q6_k": 6})   # enum qmm_format
+
+
+def gate_format(fmt):
+    """The gate matrix's format of a "gate+up" pair (the format itself otherwise)."""
+    return fmt.split("+")[0]
 DTYPE = {"f32": 0, "f16": 1, "bf16": 2, "mxfp8": 3, "q8": 4}    # enum qmm_dtype
 MX_BLOCK = 32                                                   # values per E8M0 scale of an MXFP8 operand
 GEMM_MODE = {"store": 0, "acc": 1, "swiglu": 2}                 # enum qmm_gemm_mode

@@ -7,7 +7,7 @@ computes the same kernel, with the arguments in the reference's order:
 
     g_mv_{fmt}_k{K}[_swiglu|_pair][_t{TG}][_q8][_r{R}]  [n, tokens]  (n, tokens, accumulate, x, w [, w2|ws], y [, y2])
                                                                       S/gen_llm.py:1187-1197, mv_name :5098-5111
-    g_gemm_{fmt}_{store|acc|swiglu}[_m128|_m256]        [rows, n]    (rows, k, n, x16, scales, w [, w2|ws], y)
+    g_gemm_{fmt}[_{fmt2}]_{store|acc|swiglu}[_m128|_m256] [rows, n]  (rows, k, n, x16, scales, w [, w2|ws], y)
                                                                       S/gen_gemm.py:549-556, S/gen_llm.py:4568-4625
     g_gemm_mxfp4s_{store|swiglu}_f8_m256[_rdna4]        [rows, n]    (rows, k, n, x8, scales, w, ws [, w2, w2s], y)
                                                                       S/gen_mxfp4s.py:50-101
@@ -15,9 +15,9 @@ computes the same kernel, with the arguments in the reference's order:
                                                                       S/gen_moe.py:170-174, :410
     g_moe_bucket                                        [tokens]     (tokens, max_tiles, info, ids, tile_info, rowmap,
                                                                       pos)  S/gen_moe.py:833-837
-    g_moe_{gu|dn}_{fmt}[_fused][_q8]_k{K}_r{R}          [n, T*KU]    (n, tokens, ids, x, w [, w2] [, biases], y)
+    g_moe_{gu|dn}_{fmt}[_{fmt2}][_fused][_q8]_k{K}_r{R} [n, T*KU]    (n, tokens, ids, x, w [, w2] [, biases], y)
                                                                       S/gen_moe.py:535-564
-    g_moe_g{gu|dn}_{fmt}[_fused]_k{K}                   [max_rows, n] (max_rows, k, n, xrows, tile_info, rowmap, x16,
+    g_moe_g{gu|dn}_{fmt}[_{fmt2}][_fused]_k{K}          [max_rows, n] (max_rows, k, n, xrows, tile_info, rowmap, x16,
                                                                       scales, w [, w2] [, biases], y)
                                                                       S/gen_moe.py:1147-1148, S/gen_llm.py:5376-5378
     g_moe_combine / g_moe_combine_sorted                [tokens]     (tokens, [rows,] ys, [pos,] wts, [sg,] y)
@@ -34,7 +34,9 @@ expert activation, the router / probability biases, whether a layer has shared e
 sees: the reference's row-scaled f16 activations (x16 + scales) are the A operand of the GGUF-block GEMMs as there;
 the MXFP4 GEMMs take MXFP8 activations (E4M3 codes + one E8M0 scale per 32 values, ``ops.quant_mxfp8``) and the
 ``g_moe_g{gu|dn}_mxfp4*`` launches convert the reference's x16 rows to it; GGUF MXFP4 (17-byte block) weights given
-to a grouped or dense prefill GEMM are repacked to split planes per call (the fast form is repacked at load).
+to a grouped or dense prefill GEMM are repacked to split planes once per weight tensor (``ops.split_planes``).
+Kernels whose gate and up matrices differ in format (``g_gemm_{fmt}_{fmt2}_swiglu``, ``g_moe_gu_{fg}_{fu}_*``,
+``g_moe_ggu_{fg}_{fu}_*``) call the same entry points with ``QMM_GATE_UP(gate, up)`` as the format.
 Unknown names raise ``KeyError``; argument-count and grid mismatches raise ``ValueError``.
 """
 import re
@@ -46,17 +48,20 @@ from . import ops
 from .formats import ACT, CODE, DTYPE, GEMM_MODE
 
 _FMT = r"q4_0|q4_k|q6_k|mxfp4s|mxfp4"
+_FMT2 = r"q4_0|q4_k|q6_k|mxfp4"   # the up matrix's format of a gate/up kernel whose gate and up formats differ
 
 PATTERNS = [
     ("mv", re.compile(rf"g_mv_(?P<fmt>{_FMT})_k(?P<k>\d+)(?:_(?P<variant>swiglu|pair))?(?:_t(?P<tg>\d+))?"
                       rf"(?P<q8>_q8)?(?:_r(?P<r>\d+))?")),
     ("gemm_f8", re.compile(r"g_gemm_mxfp4s_(?P<mode>store|swiglu)_f8_m256(?:_rdna4)?")),
-    ("gemm", re.compile(rf"g_gemm_(?P<fmt>{_FMT})_(?P<mode>store|acc|swiglu)(?:_(?P<tile>m128|m256))?")),
+    ("gemm", re.compile(rf"g_gemm_(?P<fmt>{_FMT})(?:_(?P<fmt2>{_FMT2}))?_(?P<mode>store|acc|swiglu)"
+                        rf"(?:_(?P<tile>m128|m256))?")),
     ("route", re.compile(r"g_moe_route(?P<tr>_tr)?(?P<live>_live)?")),
     ("bucket", re.compile(r"g_moe_bucket")),
-    ("expert", re.compile(rf"g_moe_(?P<mode>gu|dn)_(?P<fmt>{_FMT})(?P<fused>_fused)?(?P<q8>_q8)?_k(?P<k>\d+)"
-                          rf"_r(?P<r>\d+)")),
-    ("grouped", re.compile(rf"g_moe_g(?P<mode>gu|dn)_(?P<fmt>{_FMT})(?P<fused>_fused)?_k(?P<k>\d+)")),
+    ("expert", re.compile(rf"g_moe_(?P<mode>gu|dn)_(?P<fmt>{_FMT})(?:_(?P<fmt2>{_FMT2}))?(?P<fused>_fused)?"
+                          rf"(?P<q8>_q8)?_k(?P<k>\d+)_r(?P<r>\d+)")),
+    ("grouped", re.compile(rf"g_moe_g(?P<mode>gu|dn)_(?P<fmt>{_FMT})(?:_(?P<fmt2>{_FMT2}))?(?P<fused>_fused)?"
+                           rf"_k(?P<k>\d+)")),
     ("combine", re.compile(r"g_moe_combine(?P<sorted>_sorted)?")),
     ("wscale", re.compile(r"g_moe_wscale")),
     ("shared_gate", re.compile(r"g_moe_shared_gate_(?P<ty>f32|bf16|f16)")),
@@ -77,12 +82,22 @@ ENTRY = {
 
 
 def parse(name):
-    """(family, fields) of a reference kernel name; KeyError when no family matches."""
+    """(family, fields) of a reference kernel name; KeyError when no family matches. A second format (fmt2, the
+    reference's "GATE+UP" kernels: gate and up matrices in different formats) belongs to the gate/up kernels only."""
     for family, pat in PATTERNS:
         m = pat.fullmatch(name)
         if m:
-            return family, {k: v for k, v in m.groupdict().items() if v is not None}
+            f = {k: v for k, v in m.groupdict().items() if v is not None}
+            if "fmt2" in f and (f.get("mode") not in ("swiglu", "gu") or "fused" in f or "q8" in f):
+                raise KeyError(f"{name!r}: a second weight format names the up matrix of a two-tensor gate/up kernel "
+                               f"(S/gen_gemm.py:535-547, S/gen_moe.py:535-552, :1126-1141)")
+            return family, f
     raise KeyError(f"no libqmm kernel computes {name!r}")
+
+
+def _fcode(f):
+    """The format code of a parsed name: one format, or QMM_GATE_UP(gate, up) for a gate/up pair."""
+    return CODE[f"{f['fmt']}+{f['fmt2']}"] if "fmt2" in f else CODE[f["fmt"]]
 
 
 def entry_point(name, cfg=None):
@@ -207,15 +222,15 @@ class Launcher:
         if fmt.startswith("mxfp4"):
             if fmt == "mxfp4s":
                 (w, ws), (w2, ws2) = (a[5], a[6]), (None, None)
-            else:   # GGUF blocks -> split planes
-                w, ws = ops.repack_mxfp4(a[5], n, k)
-                w2, ws2 = ops.repack_mxfp4(a[6], n, k) if mode == "swiglu" else (None, None)
+            else:   # GGUF blocks -> split planes (once per weight tensor)
+                w, ws = ops.split_planes(a[5], n, k)
+                w2, ws2 = ops.split_planes(a[6], n, k) if mode == "swiglu" else (None, None)
             x8, xs8 = ops.quant_mxfp8(_rows_f32(x16, scales))
             _lib.call("qmm_gemm_mxfp4", CODE["mxfp4s"], GEMM_MODE[mode], rows, k, n, _p(x8), _p(xs8), _p(w), _p(ws),
                       _p(w2), _p(ws2), _p(y), ops._dt(y), _s())
             return
         w, w2 = (a[5], a[6]) if mode == "swiglu" else (a[5], None)
-        _lib.call("qmm_gemm", CODE[fmt], GEMM_MODE[mode], rows, k, n, _p(x16), ops._dt(x16), _p(scales), _p(w),
+        _lib.call("qmm_gemm", _fcode(f), GEMM_MODE[mode], rows, k, n, _p(x16), ops._dt(x16), _p(scales), _p(w),
                   _p(w2), _p(y), ops._dt(y), _s())
 
     def _gemm_f8(self, name, f, grid, a):
@@ -273,7 +288,7 @@ class Launcher:
         elif fmt == "mxfp4s":
             raise KeyError(f"{name!r}: split-plane expert weights come with their scale planes (ops.moe_expert_mv)")
         else:
-            _lib.call("qmm_moe_expert_mv", CODE[fmt], m, int(fused), act, k, n, E, KU, ta, _p(ids), _p(x),
+            _lib.call("qmm_moe_expert_mv", _fcode(f), m, int(fused), act, k, n, E, KU, ta, _p(ids), _p(x),
                       ops._dt(x), _p(w), _p(None if fused else w2), _p(bg), _p(bu), _p(y), _s())
 
     def _grouped(self, name, f, grid, a):
@@ -299,15 +314,15 @@ class Launcher:
             rows_needed = xrows
             x8, xs8 = ops.quant_mxfp8(_rows_f32(x16[:rows_needed], scales[:rows_needed]))
             ws = ws2 = None
-            if fmt == "mxfp4":   # GGUF blocks -> split planes
-                w, ws = ops.repack_mxfp4(w, w.numel() // (k // 32 * 17), k)
+            if fmt == "mxfp4":   # GGUF blocks -> split planes (once per weight tensor)
+                w, ws = ops.split_planes(w, w.numel() // (k // 32 * 17), k)
                 if w2 is not None and not fused:
-                    w2, ws2 = ops.repack_mxfp4(w2, w2.numel() // (k // 32 * 17), k)
+                    w2, ws2 = ops.split_planes(w2, w2.numel() // (k // 32 * 17), k)
             _lib.call("qmm_moe_grouped", CODE["mxfp4s"], m, int(fused), act, E, KU, max_rows, k, n, xrows,
                       _p(tile_info), _p(rowmap), _p(x8), DTYPE["mxfp8"], _p(xs8), _p(w), _p(ws),
                       _p(None if fused else w2), _p(ws2), _p(bg), _p(bu), _p(y), _s())
             return
-        _lib.call("qmm_moe_grouped", CODE[fmt], m, int(fused), act, E, KU, max_rows, k, n, xrows, _p(tile_info),
+        _lib.call("qmm_moe_grouped", _fcode(f), m, int(fused), act, E, KU, max_rows, k, n, xrows, _p(tile_info),
                   _p(rowmap), _p(x16), ops._dt(x16), _p(scales), _p(w), None, _p(None if fused else w2), None,
                   _p(bg), _p(bu), _p(y), _s())
 

@@ -39,7 +39,7 @@ import weakref
 import torch
 
 from . import _lib
-from .formats import ACT, CODE, DTYPE, GEMM_MODE, MX_BLOCK, SPLIT, row_bytes
+from .formats import ACT, CODE, DTYPE, GEMM_MODE, MX_BLOCK, SPLIT, gate_format, row_bytes
 
 TILE = 64
 
@@ -580,7 +580,7 @@ def moe_prefill(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up
             split_planes(w_down, E * H, FE)
         if w_up is not None:
             w_up, ws_up = split_planes(w_up, E * FE, H)
-    gguf = fmt in ("q4_k", "q4_kt", "q6_k", "q4_0")
+    gguf = gate_format(fmt) in ("q4_k", "q4_kt", "q6_k", "q4_0")   # a "gate+up" pair: GGUF gate / up in two formats
     xop = None
     if logits is not None and router is None and x.dtype == torch.bfloat16 and H <= 4096 and \
             (gguf or H % MX_BLOCK == 0):
@@ -599,7 +599,8 @@ def moe_prefill(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up
                         fused=fused, act=act, bias=bg, bias2=bu)
         # the down GEMM's operand over the assignments' rows (the rows the tile-wise producer covers)
         a16, as_ = row_scale_f16_rows(a, pos) if FE % 8 == 0 and FE <= 8192 else row_scale_f16(a, tile_info=tile_info)
-        ys = moe_grouped(fmt_down or fmt, "dn", tile_info, rowmap, a16, w_down, H, FE, E, KU, x_scales=as_, bias=bd)
+        ys = moe_grouped(fmt_down or gate_format(fmt), "dn", tile_info, rowmap, a16, w_down, H, FE, E, KU,
+                         x_scales=as_, bias=bd)
     elif fmt in ("mxfp4s", "mxfp4t"):
         # the gate/up GEMM writes its activation as MXFP8 directly (the down GEMM's A operand)
         x8, xs = (xop, xos) if xop is not None else quant_mxfp8(x)
@@ -644,12 +645,13 @@ def moe_decode(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=
     formats have integer codes and the experts have no biases (gen_llm.moe_iq, S/gen_llm.py:5296-5303); False keeps
     the f32 / bf16 activations (the reference's MOE_Q8=0).
     Returns (y f32 [T, H], intermediates dict)."""
-    fd = fmt_down or fmt
+    fd = fmt_down or gate_format(fmt)
     q8 = _moe_q8(q8, fmt, fd, expert_bias)
     if q8 and (fmt not in Q8_FORMATS or fd not in Q8_FORMATS):
         raise ValueError(f"the int8 expert matvecs take {Q8_FORMATS} (gate/up {fmt}, down {fd})")
     bg, bu, bd = expert_bias if expert_bias is not None else (None, None, None)
-    if not q8 and logits is not None and router is None and E <= ROUTE_GU_MAX_E and x.shape[0] * KU <= ROUTE_GU_MAX_A:
+    if not q8 and logits is not None and router is None and E <= ROUTE_GU_MAX_E and x.shape[0] * KU <= ROUTE_GU_MAX_A \
+            and "+" not in fmt:
         # routing and the gate/up matvecs in one launch (equal bit for bit to moe_topk then moe_expert_mv 'gu')
         ids, wts, a = moe_topk_expert_mv(fmt, logits, KU, gating, norm, x, w_gate, FE, H, E, w2=w_up, ws=ws_gate,
                                          ws2=ws_up, fused=fused, act=act, bias=bg, bias2=bu, scale=scale,

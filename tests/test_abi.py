@@ -250,6 +250,44 @@ def test_argument_validation_without_a_device(lib):
     assert lib.qmm_gemm(1, 0, 64, 1 << 20, 1 << 14, fake, 1, n, fake, n, fake, 0, n) == st["QMM_ERR_SHAPE"]
 
 
+def test_gate_up_format_pairs(lib):
+    """QMM_GATE_UP(gate, up) as the header defines it, the Python code for "gate+up", and the entry points' checks:
+    a pair is the format of a gate/up call only (swiglu GEMM, gate/up expert matvecs and grouped GEMM, two tensors,
+    f32 / bf16 decode activations in the chain)."""
+    from qmm.formats import CODE
+    text = open(HEADER).read()
+    assert "#define QMM_GATE_UP(gate, up) ((gate) | (((up) + 1) << 8))" in text
+    assert CODE["q4_k+q6_k"] == 1 | (7 << 8) and CODE["q6_k+q4_k"] == 6 | (2 << 8)
+    st = header_enum("qmm_status")
+    fake, n, f1 = ctypes.c_void_p(0x1000), None, ctypes.c_float(1)
+    pair = CODE["q4_k+q6_k"]
+    # the GEMM: swiglu only; formats of the f16 MFMA kernels only
+    assert lib.qmm_gemm(pair, 0, 64, 256, 64, fake, 1, n, fake, n, fake, 0, n) == st["QMM_ERR_FORMAT"]
+    assert lib.qmm_gemm(CODE["q4_k+mxfp4"], 2, 64, 256, 64, fake, 1, n, fake, fake, fake, 0, n) == st["QMM_ERR_FORMAT"]
+    assert lib.qmm_gemm(pair, 2, 64, 256, 64, fake, 1, n, fake, n, fake, 0, n) == st["QMM_ERR_NULL"]
+    # the grouped GEMM: gate/up of two tensors
+    assert lib.qmm_moe_grouped(pair, 1, 0, 0, 4, 2, 256, 256, 64, 256, fake, fake, fake, 1, fake, fake, n, n, n,
+                               n, n, fake, n) == st["QMM_ERR_FORMAT"]
+    assert lib.qmm_moe_grouped(pair, 0, 1, 0, 4, 2, 256, 256, 64, 8, fake, fake, fake, 1, fake, fake, n, fake, n,
+                               n, n, fake, n) == st["QMM_ERR_FORMAT"]
+    # the expert matvecs: gate/up of two tensors; the fused routing launch and the down + combine take one format
+    assert lib.qmm_moe_expert_mv(pair, 1, 0, 0, 256, 8, 4, 2, 4, fake, fake, 0, fake, fake, n, n, fake, n) \
+        == st["QMM_ERR_FORMAT"]
+    assert lib.qmm_moe_expert_mv(pair, 0, 1, 0, 256, 8, 4, 2, 4, fake, fake, 0, fake, fake, n, n, fake, n) \
+        == st["QMM_ERR_FORMAT"]
+    assert lib.qmm_moe_expert_mv(pair, 0, 0, 0, 256, 8, 4, 2, 4, fake, fake, 0, fake, n, n, n, fake, n) \
+        == st["QMM_ERR_NULL"]
+    assert lib.qmm_moe_topk_expert_mv(fake, 1, 32, 4, 1, 1, f1, n, fake, fake, pair, 0, 0, 256, 8, fake, 2, fake, n,
+                                      fake, n, n, n, fake, n) == st["QMM_ERR_FORMAT"]
+    assert lib.qmm_mv_swiglu(CODE["q4_k+mxfp4s"], 256, 4, 1, 0, fake, 0, fake, fake, fake, n) == st["QMM_ERR_FORMAT"]
+    # the chain: f32 / bf16 decode activations, two tensors; the workspace of a pair is its gate format's
+    size = lib.qmm_moe_routed_workspace_size
+    assert size(pair, 0, 128, 8, 4, 2048, 768, 0) == size(1, 0, 128, 8, 4, 2048, 768, 0) > 0
+    assert size(pair, 1, 128, 8, 4, 2048, 768, 0) == -1
+    assert lib.qmm_moe_routed(pair, -1, 1, 0, 1, 1, f1, 0, 128, 8, 4, 2048, 768, fake, 2, fake, n, 0, n, n, fake, n,
+                              fake, n, fake, n, n, n, n, n, 0, fake, fake, 1 << 30, n) == st["QMM_ERR_FORMAT"]
+
+
 def test_static_chain_scratch_bounds(lib):
     """qmm_moe_routed_static's 16 MiB array holds the decode chain of an H + FE <= 8192, top-8 model on given logits
     at up to 63 tokens on f32 / bf16 activations and up to 48 on the Q8_1 path (the bounds its header states), and

@@ -144,6 +144,26 @@ def test_unknown_names_are_refused(name):
         launch.entry_point(name)
 
 
+def test_gate_up_kernels_in_two_formats_map_to_the_gate_up_entry_points(lib):
+    """The reference's "GATE+UP" kernels of a layer whose gate and up tensors differ in format (a Q4_K_M layer with
+    a Q4_K gate and a Q6_K up, S/gen_llm.py:5335-5336): g_gemm_{fmt}_{fmt2}_swiglu (S/gen_gemm.py:535-547),
+    g_moe_ggu_{fg}_{fu}_k{H} (S/gen_moe.py:1126-1141) and g_moe_gu_{fg}_{fu}_k{H}_r{R} (S/gen_moe.py:535-552) call the
+    gate/up entry points with QMM_GATE_UP(gate, up); a second format anywhere else is refused."""
+    from qmm import launch
+    from qmm.formats import CODE
+    names = {"g_gemm_q4_k_q6_k_swiglu": "qmm_gemm", "g_gemm_q6_k_q4_k_swiglu_m256": "qmm_gemm",
+             "g_moe_ggu_q4_k_q6_k_k2048": "qmm_moe_grouped", "g_moe_gu_q4_k_q6_k_k2048_r2": "qmm_moe_expert_mv",
+             "g_moe_gu_q4_0_mxfp4_k2880_r2": "qmm_moe_expert_mv"}
+    for name, ep in names.items():
+        assert launch.entry_point(name) == ep and hasattr(lib, ep), name
+        fam, f = launch.parse(name)
+        assert launch._fcode(f) == CODE[f["fmt"]] | ((CODE[f["fmt2"]] + 1) << 8), name
+    for bad in ("g_gemm_q4_k_q6_k_store", "g_moe_dn_q4_k_q6_k_k768_r4", "g_moe_gdn_q4_k_q6_k_k768",
+                "g_moe_gu_q4_k_q6_k_q8_k2048_r2", "g_moe_ggu_q4_k_q6_k_fused_k2048"):
+        with pytest.raises(KeyError):
+            launch.entry_point(bad)
+
+
 def test_malformed_launches_fail_before_any_device_call():
     """Argument counts and grids are checked against the reference's launch lists first (ints stand in for
     buffers: a check that came later would fail on them with another error)."""
