@@ -17,6 +17,8 @@ one workload, or with --no-secondary):
     q4_k_gemv   the Q4_K GEMV on the f16-activation path (x bf16 staged as f16, v_dot2_f32_f16)
     q4_k_gemv_q8p the int8 GEMV on its reference boundary: x is the planar Q8_1 buffer qmm_quant_q8 makes
     q4_0_gemv   Q4_0 decode GEMV, W [4096, 4096], x f32 [1, 4096], y f32
+    q4_0_gemv_q8 the same GEMV on the int8-activation path, the weights repacked once into the tiled layout
+                (qmm_tile_q40) the Q4_K int8 kernel streams
     q4_k_gemm   Q4_K prefill GEMM, x bf16 [512, 4096] (row scale to f16, then the MFMA GEMM), W [4096, 4096],
                 y bf16 [512, 4096] (Qwen3-8B attn o_proj)
     mxfp4_moe   MXFP4 MoE at the gpt-oss-20b shape (32 experts, top-4, H = FE = 2880), T tokens (--m): T < 64 the
@@ -58,6 +60,7 @@ SPIN_CYCLES = 4_000_000   # the spin ahead of a timed graph: about 2 ms, longer 
 
 # (workload, M or T) measured after the headline by the default run
 SECONDARY = [("q4_k_gemv_q8", 4), ("q4_k_gemv_q8", 8), ("q4_k_swiglu_q8", 1), ("q4_k_gemv", 1), ("q4_0_gemv", 1),
+             ("q4_0_gemv_q8", 1),
              ("q4_k_gemm", 512), ("mxfp4_moe", 1), ("mxfp4_moe", 256), ("mxfp4_moe", 1024), ("mxfp4_moe", 4096),
              ("q4_k_moe", 64)]
 
@@ -119,7 +122,8 @@ class GemvWorkload:
         self.name, self.index, self.fmt, self.n, self.k, self.m = name, index, fmt, n, k, m
         self.x_dtype, self.traffic_name, self.q8, self.tiled = x_dtype, traffic_name, q8, tiled
         self.swiglu = swiglu
-        self.kfmt = "q4_kt" if tiled else fmt   # the weights the kernel reads (tiled: repacked once at load)
+        # the weights the kernel reads (tiled: repacked once at load)
+        self.kfmt = {"q4_k": "q4_kt", "q4_0": "q4_0t"}[fmt] if tiled else fmt
 
     def setup(self, dev):
         import torch
@@ -136,8 +140,9 @@ class GemvWorkload:
         if self.swiglu:   # the up matrix: the gate matrix's code bytes in reverse order (same distributions)
             self.raw_up = np.ascontiguousarray(self.raw.reshape(-1, 144)[::-1]).reshape(-1)
             w0 = torch.cat([w0, torch.from_numpy(self.raw_up).to(dev)])
-        if self.tiled:   # one-time weight preparation: GGUF Q4_K blocks -> the lane-ordered tiled layout
-            parts = [ops.tile_q4k(p, self.n, self.k) for p in w0.chunk(2 if self.swiglu else 1)]
+        if self.tiled:   # one-time weight preparation: GGUF blocks -> the lane-ordered tiled layout
+            tile = ops.tile_q4k if self.fmt == "q4_k" else ops.tile_q40
+            parts = [tile(p, self.n, self.k) for p in w0.chunk(2 if self.swiglu else 1)]
             w0 = torch.cat(parts) if len(parts) > 1 else parts[0]
         self.wbytes = w0.numel()
         copies = max(2, -(-ROTATE_BYTES // self.wbytes))
@@ -216,7 +221,7 @@ class GemvWorkload:
         return self.m
 
     def config(self):
-        return {"workload": self.name, "format": self.fmt, "layout": "tiled (q4_kt)" if self.tiled else "gguf",
+        return {"workload": self.name, "format": self.fmt, "layout": f"tiled ({self.kfmt})" if self.tiled else "gguf",
                 "N": self.n, "K": self.k, "M": self.m,
                 "x_dtype": "q8_1 planar" if self.q8 == "planar" else self.x_dtype,
                 "activations": "q8_1" if self.q8 else self.x_dtype, "y_dtype": "f32",
@@ -557,8 +562,14 @@ def _q40_gemv(m):
                         f"mv_kernel_q4_0.q4_0_gemv_n4096_k4096_m{m or 1}")
 
 
+def _q40_gemv_q8(m):
+    return GemvWorkload("q4_0_gemv_q8", 0, "q4_0", 4096, 4096, m or 1, "f32",
+                        f"mv_q4kt_q8_kernel.q4_0_gemv_q8_n4096_k4096_m{m or 1}", q8=True, tiled=True)
+
+
 WORKLOADS = {"q4_k_gemv": _q4k_gemv, "q4_k_gemv_q8": _q4k_gemv_q8, "q4_k_gemv_q8_gguf": _q4k_gemv_q8_gguf,
              "q4_k_gemv_q8p": _q4k_gemv_q8p, "q4_k_swiglu_q8": _q4k_swiglu_q8, "q4_0_gemv": _q40_gemv,
+             "q4_0_gemv_q8": _q40_gemv_q8,
              "q4_k_gemm": GemmWorkload, "mxfp4_moe": lambda m: MoeWorkload("mxfp4_moe", 3, m),
              "q4_k_moe": lambda m: MoeWorkload("q4_k_moe", 4, m), "hbm_copy": CopyWorkload}
 

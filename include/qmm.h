@@ -40,8 +40,11 @@ enum qmm_status {
 /* QMM_MXFP4T: MXFP4 in MFMA-tiled planes (qmm_tile_mxfp4), the grouped GEMM's fast weight layout.
  * QMM_Q4_KT: Q4_K in the lane-ordered tiled layout (qmm_tile_q4k), the int8-activation decode GEMV's fast layout.
  * QMM_Q6_K: GGUF Q6_K (210 bytes per 256 values; ffn_down of the Q4_K_M files), read in place from a 4-byte aligned
- *           tensor (its super-blocks start on even addresses). */
-enum qmm_format { QMM_Q4_0 = 0, QMM_Q4_K = 1, QMM_MXFP4 = 2, QMM_MXFP4S = 3, QMM_MXFP4T = 4, QMM_Q4_KT = 5, QMM_Q6_K = 6 };
+ *           tensor (its super-blocks start on even addresses).
+ * QMM_Q4_0T: Q4_0 in the lane-ordered tiled layout (qmm_tile_q40), the int8-activation decode GEMV's fast layout. */
+enum qmm_format {
+  QMM_Q4_0 = 0, QMM_Q4_K = 1, QMM_MXFP4 = 2, QMM_MXFP4S = 3, QMM_MXFP4T = 4, QMM_Q4_KT = 5, QMM_Q6_K = 6, QMM_Q4_0T = 7
+};
 /* A gate/up pair whose up matrix has another format than the gate matrix (the reference's "GATE+UP" formats, e.g. a
  * Q4_K_M layer with a Q4_K gate and a Q6_K up: g_gemm_{fmt}_{fmt2}_swiglu S/gen_gemm.py:535-547, g_moe_ggu_{fg}_{fu}
  * S/gen_moe.py:1126-1141, g_moe_gu_{fg}_{fu} S/gen_moe.py:535-552): pass QMM_GATE_UP(gate format, up format) as the
@@ -72,7 +75,7 @@ int64_t qmm_row_bytes(int fmt, int64_t k);
  * (the values @g_q4_0_values S/quant_values.loom:386-408, @g_q4_k_values S/gen_llm.py:288-326,
  *  @g_mxfp4_values S/gen_llm.py:786-841 and @g_mxfp4s_values S/gen_llm.py:844-895 produce).
  * w: weight bytes; ws: the E8M0 scale plane for QMM_MXFP4S / QMM_MXFP4T, else NULL (QMM_MXFP4T: rows % 32 == 0,
- * K % 64 == 0; QMM_Q4_KT: rows % 16 == 0, K % 256 == 0). */
+ * K % 64 == 0; QMM_Q4_KT: rows % 16 == 0, K % 256 == 0; QMM_Q4_0T: rows % 16 == 0, K % 512 == 0). */
 int qmm_dequant(int fmt, const void *w, const void *ws, int64_t rows, int64_t k, float *out, qmm_stream_t stream);
 
 /* Decode matrix-vector product, the g_mv_{fmt}_k{K}[_t{TG}][_r{R}] family
@@ -107,7 +110,9 @@ int qmm_quant_q8(int64_t rows, int64_t k, const void *x, int x_dtype, void *xq, 
  * [tokens, n]. A multi-token call equals one-token calls bit for bit.
  * fmt QMM_Q4_KT: the weights in the tiled layout of qmm_tile_q4k (n % 16 == 0, K % 512 == 0, K / 512 a multiple of
  * at most 4 of a count of at most 8 waves); x planar Q8_1 or f32 / bf16 rows for every such K. For K = 4096 the
- * results equal the QMM_Q4_K call's bit for bit. */
+ * results equal the QMM_Q4_K call's bit for bit. fmt QMM_Q4_0T: the Q4_0 weights in the tiled layout of qmm_tile_q40,
+ * the same shapes and activations as QMM_Q4_KT, per block (d da) (di - 8 xs) with di the dot of the codes q: the
+ * QMM_Q4_0 call's sum, in the tiled kernel's summation order. */
 int qmm_mv_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
               const void *w, float *y, qmm_stream_t stream);
 
@@ -120,7 +125,8 @@ int qmm_mv_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, con
  * with g = x W^T and u = x W2^T computed as qmm_mv_q8 computes one matrix (per 32-value group an exact int32 dot of
  * codes, f32 fixups, the same reductions), so each is bit for bit the one-matrix kernel's of the same layout and K
  * (for GGUF Q4_K at K = 4096 / 8192 that is the tiled layout's, since the one-matrix GGUF call takes its K-sliced
- * kernel there). fmt QMM_Q4_KT: W and W2 in the tiled layout of qmm_tile_q4k, x planar Q8_1 or f32 / bf16 rows
+ * kernel there). fmt QMM_Q4_KT / QMM_Q4_0T: W and W2 in the tiled layout of qmm_tile_q4k / qmm_tile_q40, x planar
+ * Q8_1 or f32 / bf16 rows
  * (quantized in the kernel exactly as qmm_quant_q8 does); QMM_Q4_K / QMM_Q4_0 / QMM_Q6_K (GGUF): x planar Q8_1.
  * W, W2: [n, k]; y, y2: f32 [tokens, n]. A multi-token call equals one-token calls bit for bit. */
 int qmm_mv_swiglu_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
@@ -332,6 +338,14 @@ int qmm_repack_mxfp4(const void *w, int64_t rows, int64_t k, uint8_t *nibbles, u
  * 16 (4 h + q) .. +15. A byte permutation (same size); qmm_dequant(QMM_Q4_KT) gives the GGUF values bit for bit.
  * rows % 16 == 0, k % 256 == 0 (the decode GEMV takes k % 512 == 0). */
 int qmm_tile_q4k(const void *w, int64_t rows, int64_t k, void *w_t, qmm_stream_t stream);
+
+/* The same preparation for GGUF Q4_0 rows (no reference counterpart: the reference's @g_q4_0 matvecs read the 18-byte
+ * blocks in place, S/gen_llm.py:536-552) -> QMM_Q4_0T, units of 16 rows x 512 values, 4608 bytes: at 16 (2 r + sb)
+ * the eight f16 d of blocks 8 sb .. 8 sb + 7 of row r, then four 1 KB code planes, plane q holding at 16 l
+ * (l = 4 r + 2 sb + h) bytes 16 (4 h + q) .. +15 of the 128 code bytes of those eight blocks, whose byte 32 p + i
+ * holds code i of block 2 p in its low nibble and code i of block 2 p + 1 in its high nibble. A permutation of codes
+ * and scales (same size); qmm_dequant(QMM_Q4_0T) gives the GGUF values bit for bit. rows % 16 == 0, k % 512 == 0. */
+int qmm_tile_q40(const void *w, int64_t rows, int64_t k, void *w_t, qmm_stream_t stream);
 
 /* One-time weight preparation for the grouped GEMM (no reference counterpart: the reference reads the split planes
  * of S/formats.py:12-15 as they are): split planes (nibbles [rows, k/2], scales [rows, k/32]) -> MFMA-tiled planes.

@@ -115,6 +115,7 @@ inline int64_t block_values(int fmt) {
     case QMM_MXFP4T: return 32;
     case QMM_Q4_KT: return 256;
     case QMM_Q6_K: return 256;
+    case QMM_Q4_0T: return 512;
     default: return 0;
   }
 }
@@ -127,6 +128,7 @@ inline int64_t block_bytes(int fmt) {
     case QMM_MXFP4T: return 16;
     case QMM_Q4_KT: return 144;
     case QMM_Q6_K: return 210;
+    case QMM_Q4_0T: return 288;
     default: return 0;
   }
 }

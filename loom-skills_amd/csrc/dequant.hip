@@ -8,12 +8,14 @@
 //   MXFP4S w = E2M1(code) * 2^(e - 127)               S/st_tensors.py:26-33 (code 8 -> -0)
 //   MXFP4T the same values from MFMA-tiled planes (grouped_mxfp4.hip)
 //   Q4_KT  the Q4_K values from the tiled GEMV layout (gemv_q4kt.hip)
+//   Q4_0T  the Q4_0 values from the tiled GEMV layout (gemv_q4kt.hip)
 #include "common.hpp"
 
 using namespace qmm;
 
 int qmm_dequant_mxfp4t(const void *w, const void *ws, int64_t rows, int64_t k, float *out, hipStream_t s);
 int qmm_dequant_q4kt(const void *w, int64_t rows, int64_t k, float *out, hipStream_t s);
+int qmm_dequant_q40t(const void *w, int64_t rows, int64_t k, float *out, hipStream_t s);
 
 namespace {
 
@@ -130,11 +132,12 @@ const char *qmm_strerror(int status) {
 int64_t qmm_row_bytes(int fmt, int64_t k) { return row_bytes(fmt, k); }
 
 int qmm_dequant(int fmt, const void *w, const void *ws, int64_t rows, int64_t k, float *out, qmm_stream_t stream) {
-  if (fmt < QMM_Q4_0 || fmt > QMM_Q6_K) return QMM_ERR_FORMAT;
+  if (fmt < QMM_Q4_0 || fmt > QMM_Q4_0T) return QMM_ERR_FORMAT;
   if (!w || !out || ((fmt == QMM_MXFP4S || fmt == QMM_MXFP4T) && !ws)) return QMM_ERR_NULL;
   if (rows <= 0 || row_bytes(fmt, k) == 0) return QMM_ERR_SHAPE;
   if (fmt == QMM_MXFP4T) return qmm_dequant_mxfp4t(w, ws, rows, k, out, reinterpret_cast<hipStream_t>(stream));
   if (fmt == QMM_Q4_KT) return qmm_dequant_q4kt(w, rows, k, out, reinterpret_cast<hipStream_t>(stream));
+  if (fmt == QMM_Q4_0T) return qmm_dequant_q40t(w, rows, k, out, reinterpret_cast<hipStream_t>(stream));
   if (fmt == QMM_Q4_K && !aligned(w, 4)) return QMM_ERR_ALIGN;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int64_t groups = rows * (k / 32);

@@ -16,6 +16,14 @@
 // codes. The row's four lanes meet in a butterfly, the waves in LDS in a fixed order; for K = 4096 the arithmetic
 // and its order are those of the GGUF-layout kernel, so both give the same bits.
 //
+// Q4_0 in the same units (QMM_Q4_0T, qmm_tile_q40): 512 values of a Q4_0 row are 16 blocks of 18 bytes, the bytes of
+// two Q4_K super-blocks, so a unit keeps the Q4_K unit's shape. Header slot 16 (2 r + sb) holds the eight f16 d of
+// blocks 8 sb .. 8 sb + 7 of the unit's row r; the 128 code bytes of those eight blocks are laid out as a Q4_K
+// super-block's (page p = bytes 32 p .. 32 p + 31: low nibbles the 32 codes of block 2 p in value order, high nibbles
+// those of block 2 p + 1) and cut into the same four planes. A lane then takes blocks 4 h .. 4 h + 3 of its span and
+// adds, per block, (d da) (di - 8 xs): di the exact dot of the codes with the activation codes, xs their sum, i.e. the
+// integer dot of codes q - 8 the reference's Q4_0 int8 matvec forms (@g_q4_0_icodes, S/gen_llm.py:536-552).
+//
 // Two-matrix variants stream a second matrix W2 of the same shape in the same waves, with the same per-lane arithmetic
 // and reductions for each: swiglu y = silu(x W^T) (x W2^T) (g_mv_q4_k_k{K}_swiglu[_t{TG}]_q8, S/gen_llm.py:1159-1197)
 // and pair y = x W^T, y2 = x W2^T (g_mv_q4_k_k{K}_pair[_t{TG}]_q8, S/gen_llm.py:1166-1176), each row of a pair
@@ -33,6 +41,7 @@ typedef __attribute__((ext_vector_type(2))) u32 v2u;
 
 constexpr int kUnit = 4608, kMaxWaves = 8;
 enum Mode { kPlain = 0, kSwiglu = 1, kPair = 2 };
+enum TFmt { kTQ4K = 0, kTQ40 = 1 };   // the tiled layouts: Q4_K (qmm_tile_q4k), Q4_0 (qmm_tile_q40)
 
 __device__ __forceinline__ int sdot4(u32 a, u32 b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
@@ -80,7 +89,7 @@ __device__ __forceinline__ void q8_group(const float (&v)[8], u32 &c0, u32 &c1, 
   sum = (float)s;
 }
 
-template <int TG, int U, bool STAGEQ, int MODE>
+template <int TG, int U, bool STAGEQ, int MODE, int WF>
 __global__ __launch_bounds__(kMaxWaves * 64) void mv_q4kt_q8_kernel(int64_t n, int64_t tokens, int64_t K,
                                                                    int accumulate, const void *__restrict__ x, int bf,
                                                                    const u8 *__restrict__ w, const u8 *__restrict__ w2,
@@ -218,13 +227,21 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mv_q4kt_q8_kernel(int64_t n, i
     for (int m = 0; m < NM; ++m) {
 #pragma unroll
       for (int i2 = 0; i2 < 16; ++i2) { lo[m][i2] = q[m][i2] & 0x0F0F0F0Fu; hi[m][i2] = (q[m][i2] >> 4) & 0x0F0F0F0Fu; }
-      const float d = f16_to_f32(hd[m].x), dmin = f16_to_f32(hd[m].x >> 16);
+      if constexpr (WF == kTQ40) {   // the d of blocks 4 h .. 4 h + 3 of the span: dwords 2 h, 2 h + 1
+        const u32 w0 = h ? hd[m].z : hd[m].x, w1 = h ? hd[m].w : hd[m].y;
+        sc[m][0] = f16_to_f32(w0); sc[m][1] = f16_to_f32(w0 >> 16);
+        sc[m][2] = f16_to_f32(w1); sc[m][3] = f16_to_f32(w1 >> 16);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        u32 s_, m_;
-        q4k_scale_min(hd[m].y, hd[m].z, hd[m].w, 4 * h + g, s_, m_);
-        sc[m][g] = d * (float)s_;
-        mn[m][g] = dmin * (float)m_;
+        for (int g = 0; g < 4; ++g) mn[m][g] = 0.f;
+      } else {
+        const float d = f16_to_f32(hd[m].x), dmin = f16_to_f32(hd[m].x >> 16);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          u32 s_, m_;
+          q4k_scale_min(hd[m].y, hd[m].z, hd[m].w, 4 * h + g, s_, m_);
+          sc[m][g] = d * (float)s_;
+          mn[m][g] = dmin * (float)m_;
+        }
       }
     }
     auto token = [&](int t, const u32 (&xa)[4][8], const float (&md)[4], const float (&ms)[4])
@@ -240,8 +257,15 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mv_q4kt_q8_kernel(int64_t n, i
             ia = sdot4(lo[m][8 * pg + i2], xa[2 * pg][i2], ia);
             ib = sdot4(hi[m][8 * pg + i2], xa[2 * pg + 1][i2], ib);
           }
-          p += ((float)ia * sc[m][2 * pg] - ms[2 * pg] * mn[m][2 * pg]) * md[2 * pg];
-          p += ((float)ib * sc[m][2 * pg + 1] - ms[2 * pg + 1] * mn[m][2 * pg + 1]) * md[2 * pg + 1];
+          if constexpr (WF == kTQ40) {   // codes q - 8: the code sum is an exact integer
+            ia -= 8 * (int)ms[2 * pg];
+            ib -= 8 * (int)ms[2 * pg + 1];
+            p += (sc[m][2 * pg] * md[2 * pg]) * (float)ia;
+            p += (sc[m][2 * pg + 1] * md[2 * pg + 1]) * (float)ib;
+          } else {
+            p += ((float)ia * sc[m][2 * pg] - ms[2 * pg] * mn[m][2 * pg]) * md[2 * pg];
+            p += ((float)ib * sc[m][2 * pg + 1] - ms[2 * pg + 1] * mn[m][2 * pg + 1]) * md[2 * pg + 1];
+          }
         }
         part[m][t] = u == 0 ? p : part[m][t] + p;
       }
@@ -324,12 +348,19 @@ struct TArgs {
   const void *w, *w2;
   float *y, *y2;
   int nw;
+  int wf;   // TFmt
 };
 
 template <int TG, int U, bool STAGEQ, int MODE>
 int launch_tg(const TArgs &a, hipStream_t s) {
   const dim3 grid((unsigned)(a.n / 16), (unsigned)((a.tokens + TG - 1) / TG));
-  mv_q4kt_q8_kernel<TG, U, STAGEQ, MODE><<<grid, a.nw * 64, 0, s>>>(
+  if (a.wf == kTQ40) {
+    mv_q4kt_q8_kernel<TG, U, STAGEQ, MODE, kTQ40><<<grid, a.nw * 64, 0, s>>>(
+        a.n, a.tokens, a.k, a.accumulate, a.x, a.bf, static_cast<const u8 *>(a.w), static_cast<const u8 *>(a.w2), a.y,
+        a.y2);
+    return launch_status();
+  }
+  mv_q4kt_q8_kernel<TG, U, STAGEQ, MODE, kTQ4K><<<grid, a.nw * 64, 0, s>>>(
       a.n, a.tokens, a.k, a.accumulate, a.x, a.bf, static_cast<const u8 *>(a.w), static_cast<const u8 *>(a.w2), a.y,
       a.y2);
   return launch_status();
@@ -416,6 +447,61 @@ __global__ void dequant_q4kt_kernel(const u8 *__restrict__ w, int64_t rows, int6
 }
 
 
+// Q4_0 -> QMM_Q4_0T, one thread per 16-byte piece of the tiled matrix: unit (row block, slice) pieces 0..31 the
+// header slots (row p / 2, span p % 2: its eight d), then four planes of 64 pieces, piece 32 + 64 q + l (l = 4 r + 2 sb
+// + h) holding bytes 16 (4 h + q) .. + 15 of row r's span sb: byte 32 P + i of a span is code i of block 2 P in its
+// low nibble and code i of block 2 P + 1 in its high nibble (code i of a block: byte i & 15, low nibble for i < 16).
+__global__ void tile_q40_kernel(const u8 *__restrict__ src, int64_t rows, int64_t K, u8 *__restrict__ dst) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t rbp = K / 512 * (kUnit / 16);   // pieces of a row block
+  if (i >= rows / 16 * rbp) return;
+  const int64_t rb = i / rbp;
+  const int p = (int)(i % rbp), u = p / (kUnit / 16), pu = p % (kUnit / 16);
+  const int64_t RB = K / 32 * 18;
+  u32 o[4];
+  if (pu < 32) {
+    const int r = pu >> 1, sb = pu & 1;
+    const u8 *row = src + (16 * rb + r) * RB + (int64_t)(16 * u + 8 * sb) * 18;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      o[j] = (u32)row[36 * j] | ((u32)row[36 * j + 1] << 8) | ((u32)row[36 * j + 18] << 16) | ((u32)row[36 * j + 19] << 24);
+  } else {
+    const int q = (pu - 32) >> 6, l = (pu - 32) & 63, r = l >> 2, sb = (l >> 1) & 1, h = l & 1;
+    const u8 *row = src + (16 * rb + r) * RB + (int64_t)(16 * u + 8 * sb) * 18;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = 0u;
+#pragma unroll
+    for (int b = 0; b < 16; ++b) {
+      const int c = 16 * (4 * h + q) + b, P = c >> 5, ci = c & 31;   // span byte c: page P, code index ci
+      const u8 *b0 = row + (2 * P) * 18 + 2, *b1 = row + (2 * P + 1) * 18 + 2;
+      const u32 lo = ci < 16 ? b0[ci] & 15u : (u32)b0[ci - 16] >> 4;
+      const u32 hi = ci < 16 ? b1[ci] & 15u : (u32)b1[ci - 16] >> 4;
+      o[b >> 2] |= (lo | (hi << 4)) << (8 * (b & 3));
+    }
+  }
+  *reinterpret_cast<v4u *>(dst + 16 * i) = v4u{o[0], o[1], o[2], o[3]};
+}
+
+// f32 values of a QMM_Q4_0T matrix, one thread per block: d (q - 8) as the value helper (S/quant_values.loom:386-408)
+__global__ void dequant_q40t_kernel(const u8 *__restrict__ w, int64_t rows, int64_t K, float *__restrict__ out) {
+  const int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t G = K / 32;
+  if (gi >= rows * G) return;
+  const int64_t row = gi / G;
+  const int b = (int)(gi % G), u = b >> 4, sb = (b >> 3) & 1, j = b & 7, r = (int)(row & 15);
+  const u8 *unit = w + ((row >> 4) * (K / 512) + u) * kUnit;
+  const u16 dbits = *reinterpret_cast<const u16 *>(unit + 16 * (2 * r + sb) + 2 * j);
+  const float d = f16_to_f32(dbits);
+  float *o = out + gi * 32;
+#pragma unroll
+  for (int v = 0; v < 32; ++v) {
+    const int c = 32 * (j >> 1) + v, h = c >> 6, q = (c >> 4) & 3;
+    const u8 byte = unit[512 + 1024 * q + 16 * (4 * r + 2 * sb + h) + (c & 15)];
+    const int code = (j & 1) ? byte >> 4 : byte & 15;
+    o[v] = __fmul_rn(d, (float)(code - 8));
+  }
+}
+
 template <int MODE>
 int launch_mode(TArgs &a, int x_dtype, hipStream_t s) {
   if (a.n % 16 || a.k % 512 || a.n / 16 > 2147483647ll || a.tokens > 65535) return QMM_ERR_SHAPE;   // grid.y <= 65535
@@ -439,9 +525,9 @@ int launch_mode(TArgs &a, int x_dtype, hipStream_t s) {
 // The tiled-layout path of qmm_mv_q8 (fmt QMM_Q4_KT): rows % 16 == 0, K % 512 == 0, K = 512 U NW with U <= 4
 // slices a wave and NW <= 8 waves. mode 0: y = x W^T; 1 (swiglu): y = silu(x W^T) (x W2^T); 2 (pair): y = x W^T and
 // y2 = x W2^T.
-int qmm_mv_q4kt_q8(int mode, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
-                   const void *w, const void *w2, float *y, float *y2, hipStream_t s) {
-  TArgs a{n, tokens, k, accumulate, x, 0, w, w2, y, y2, 0};
+int qmm_mv_q4kt_q8(int fmt, int mode, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x,
+                   int x_dtype, const void *w, const void *w2, float *y, float *y2, hipStream_t s) {
+  TArgs a{n, tokens, k, accumulate, x, 0, w, w2, y, y2, 0, fmt == QMM_Q4_0T ? kTQ40 : kTQ4K};
   if (mode == kSwiglu) return launch_mode<kSwiglu>(a, x_dtype, s);
   if (mode == kPair) return launch_mode<kPair>(a, x_dtype, s);
   return launch_mode<kPlain>(a, x_dtype, s);
@@ -453,6 +539,24 @@ int qmm_dequant_q4kt(const void *w, int64_t rows, int64_t k, float *out, hipStre
   if (!aligned(w, 4)) return QMM_ERR_ALIGN;
   const int64_t groups = rows * (k / 32);
   dequant_q4kt_kernel<<<(unsigned)((groups + 255) / 256), 256, 0, s>>>(static_cast<const u8 *>(w), rows, k, out);
+  return launch_status();
+}
+
+int qmm_dequant_q40t(const void *w, int64_t rows, int64_t k, float *out, hipStream_t s) {
+  if (rows % 16 || k % 512) return QMM_ERR_SHAPE;
+  if (!aligned(w, 4)) return QMM_ERR_ALIGN;
+  const int64_t blocks = rows * (k / 32);
+  dequant_q40t_kernel<<<(unsigned)((blocks + 255) / 256), 256, 0, s>>>(static_cast<const u8 *>(w), rows, k, out);
+  return launch_status();
+}
+
+extern "C" int qmm_tile_q40(const void *w, int64_t rows, int64_t k, void *w_t, qmm_stream_t stream) {
+  if (!w || !w_t) return QMM_ERR_NULL;
+  if (rows <= 0 || rows % 16 || k <= 0 || k % 512 || k > (1 << 20)) return QMM_ERR_SHAPE;
+  if (!aligned(w_t, 16)) return QMM_ERR_ALIGN;
+  const int64_t pieces = rows / 16 * (k / 512) * (kUnit / 16);
+  tile_q40_kernel<<<(unsigned)((pieces + 255) / 256), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      static_cast<const u8 *>(w), rows, k, static_cast<u8 *>(w_t));
   return launch_status();
 }
 

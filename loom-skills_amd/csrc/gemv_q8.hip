@@ -559,8 +559,8 @@ extern "C" int qmm_quant_q8(int64_t rows, int64_t k, const void *x, int x_dtype,
   return launch_status();
 }
 
-int qmm_mv_q4kt_q8(int mode, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
-                   const void *w, const void *w2, float *y, float *y2, hipStream_t s);
+int qmm_mv_q4kt_q8(int fmt, int mode, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x,
+                   int x_dtype, const void *w, const void *w2, float *y, float *y2, hipStream_t s);
 
 namespace {
 // the generic (GGUF-layout, planar Q8_1) matvec of one format in one mode
@@ -586,10 +586,11 @@ int generic_fmt(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, c
   return launch_generic<Q408, MODE>(k, n, tokens, accumulate, x, w, w2, rb, y, y2, s);
 }
 
-// checks shared by the int8 matvec entry points: formats with integer codes (GGUF Q4_K / Q4_0 / Q6_K and tiled Q4_K)
+// checks shared by the int8 matvec entry points: formats with integer codes (GGUF Q4_K / Q4_0 / Q6_K, tiled Q4_K / Q4_0)
 int check_q8(int fmt, int64_t k, int64_t n, int64_t tokens, const void *x, int x_dtype, const void *w, const float *y) {
   if (!x || !w || !y) return QMM_ERR_NULL;
-  if (fmt != QMM_Q4_K && fmt != QMM_Q4_0 && fmt != QMM_Q4_KT && fmt != QMM_Q6_K) return QMM_ERR_FORMAT;
+  if (fmt != QMM_Q4_K && fmt != QMM_Q4_0 && fmt != QMM_Q4_KT && fmt != QMM_Q6_K && fmt != QMM_Q4_0T)
+    return QMM_ERR_FORMAT;
   if (x_dtype != QMM_Q8 && x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
   if (k <= 0 || n <= 0 || tokens <= 0 || n > (1ll << 30) || tokens > (1ll << 24) || k > (1ll << 20))
     return QMM_ERR_SHAPE;
@@ -604,7 +605,8 @@ extern "C" int qmm_mv_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accu
                          const void *w, float *y, qmm_stream_t stream) {
   if (int st = check_q8(fmt, k, n, tokens, x, x_dtype, w, y)) return st;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (fmt == QMM_Q4_KT) return qmm_mv_q4kt_q8(kPlain, k, n, tokens, accumulate, x, x_dtype, w, nullptr, y, nullptr, s);
+  if (fmt == QMM_Q4_KT || fmt == QMM_Q4_0T)
+    return qmm_mv_q4kt_q8(fmt, kPlain, k, n, tokens, accumulate, x, x_dtype, w, nullptr, y, nullptr, s);
   const bool fast = fmt == QMM_Q4_K && (k == 4096 || k == 8192) && tokens <= 65535ll * 2;
   if (x_dtype != QMM_Q8) {
     // f32 / bf16 rows are quantized while staged; only the fast path stages (others take planar Q8 from
@@ -620,7 +622,7 @@ extern "C" int qmm_mv_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accu
   return generic_fmt<kPlain>(fmt, k, n, tokens, accumulate, x, w, nullptr, y, nullptr, s);
 }
 
-// The two-matrix int8 matvecs (mode kSwiglu / kPair): the tiled Q4_K kernel takes planar Q8_1 or f32 / bf16 rows, the
+// The two-matrix int8 matvecs (mode kSwiglu / kPair): the tiled kernel takes planar Q8_1 or f32 / bf16 rows, the
 // GGUF layouts planar Q8_1.
 static int mv2_q8(int mode, int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
                   const void *w, const void *w2, float *y, float *y2, qmm_stream_t stream) {
@@ -628,7 +630,8 @@ static int mv2_q8(int mode, int fmt, int64_t k, int64_t n, int64_t tokens, int a
   if (!w2 || (mode == kPair && !y2)) return QMM_ERR_NULL;
   if (!aligned(w2, fmt == QMM_Q6_K ? 4 : 16) || (y2 && !aligned(y2, 4))) return QMM_ERR_ALIGN;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (fmt == QMM_Q4_KT) return qmm_mv_q4kt_q8(mode, k, n, tokens, accumulate, x, x_dtype, w, w2, y, y2, s);
+  if (fmt == QMM_Q4_KT || fmt == QMM_Q4_0T)
+    return qmm_mv_q4kt_q8(fmt, mode, k, n, tokens, accumulate, x, x_dtype, w, w2, y, y2, s);
   if (x_dtype != QMM_Q8) return QMM_ERR_DTYPE;   // GGUF layouts: the planar Q8_1 buffer of qmm_quant_q8
   return mode == kSwiglu ? generic_fmt<kSwiglu>(fmt, k, n, tokens, accumulate, x, w, w2, y, nullptr, s)
                          : generic_fmt<kPair>(fmt, k, n, tokens, accumulate, x, w, w2, y, y2, s);

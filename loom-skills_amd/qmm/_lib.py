@@ -48,6 +48,7 @@ SIGNATURES = {
     "qmm_repack_mxfp4": [c_vp, c_i64, c_i64, c_vp, c_vp, c_vp],
     "qmm_tile_mxfp4": [c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp],
     "qmm_tile_q4k": [c_vp, c_i64, c_i64, c_vp, c_vp],
+    "qmm_tile_q40": [c_vp, c_i64, c_i64, c_vp, c_vp],
     "qmm_mxfp4t_scale_bytes": [c_i64, c_i64],
     "qmm_moe_combine": [c_i64, c_i64, c_i64, c_int, c_vp, c_vp, c_vp, c_int, c_vp, c_vp],
     "qmm_moe_topk_expert_mv": [c_vp, c_i64, c_int, c_int, c_int, c_int, c_float, c_vp, c_vp, c_vp, c_int, c_int, c_int,

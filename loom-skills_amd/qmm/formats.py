@@ -5,9 +5,12 @@ for the formats this library decodes. The integer codes are this library's own (
 """
 
 # mxfp4t: MXFP4 in MFMA-tiled planes (this library's load-time layout for the grouped GEMM, qmm_tile_mxfp4)
-# q4_kt: Q4_K in the lane-ordered tiled layout of the int8-activation decode GEMV (qmm_tile_q4k)
-FMT = {"q4_0": 18, "q4_k": 144, "mxfp4": 17, "mxfp4s": 16, "mxfp4t": 16, "q4_kt": 144, "q6_k": 210}   # bytes per block
-SB = {"q4_0": 32, "q4_k": 256, "mxfp4": 32, "mxfp4s": 32, "mxfp4t": 32, "q4_kt": 256, "q6_k": 256}    # values per block
+# q4_kt / q4_0t: Q4_K / Q4_0 in the lane-ordered tiled layout of the int8-activation decode GEMV (qmm_tile_q4k /
+# qmm_tile_q40; a q4_0t "block" is one row's 512 values of a tile unit)
+FMT = {"q4_0": 18, "q4_k": 144, "mxfp4": 17, "mxfp4s": 16, "mxfp4t": 16, "q4_kt": 144, "q6_k": 210,
+       "q4_0t": 288}   # bytes per block
+SB = {"q4_0": 32, "q4_k": 256, "mxfp4": 32, "mxfp4s": 32, "mxfp4t": 32, "q4_kt": 256, "q6_k": 256,
+      "q4_0t": 512}    # values per block
 SPLIT = frozenset({"mxfp4s", "mxfp4t"})                         # weight plane + scale plane (two operands)
 SCALE_DIV = {"mxfp4s": 16}                                      # nibble-plane bytes per scale-plane byte
 
@@ -22,7 +25,8 @@ class _Codes(dict):
         raise KeyError(key)
 
 
-CODE = _Codes({"q4_0": 0, "q4_k": 1, "mxfp4": 2, "mxfp4s": 3, "mxfp4t": 4, "q4_kt": 5, "q6_k": 6})   # enum qmm_format
+CODE = _Codes({"q4_0": 0, "q4_k": 1, "mxfp4": 2, "mxfp4s": 3, "mxfp4t": 4, "q4_kt": 5, "q6_k": 6,
+               "q4_0t": 7})   # enum qmm_format
 
 
 def gate_format(fmt):

@@ -135,13 +135,16 @@ def quant_q8(x, xq=None):
 def mv_q8(fmt, w, x, n, k, tokens=None, y=None, accumulate=False):
     """The int8-activation decode matvec (g_mv_{fmt}_k{K}[_t{TG}]_q8, S/gen_llm.py:1288-1301): x is the planar Q8_1
     buffer of `tokens` rows (uint8, from quant_q8), or f32 / bf16 rows [tokens, k], which the Q4_K K = 4096 / 8192
-    and (up to two tokens) tiled-layout q4_kt kernels quantize themselves and any other call quantizes through
+    and (up to two tokens) tiled-layout q4_kt / q4_0t kernels quantize themselves and any other call quantizes through
     quant_q8 first (identical results)."""
     _dev(w, x, y)
     x, xd, tokens = _q8_input(fmt, x, k, tokens, staged_tokens=2)
     y = _out(y, (tokens, n), torch.float32, w.device, accumulate)
     _lib.call("qmm_mv_q8", CODE[fmt], k, n, tokens, int(bool(accumulate)), _ptr(x), xd, _ptr(w), _ptr(y), _stream())
     return y
+
+
+TILED_Q8 = ("q4_kt", "q4_0t")   # the tiled layouts of the int8 matvec, which quantize f32 / bf16 rows themselves
 
 
 def _q8_input(fmt, x, k, tokens, staged_tokens):
@@ -159,17 +162,17 @@ def _q8_input(fmt, x, k, tokens, staged_tokens):
     _cols(x, k)
     # the kernels that quantize f32 / bf16 rows themselves do so in every workgroup; from three tokens on a separate
     # quant_q8 pass is cheaper for the tiled layout (same bits either way)
-    if (fmt == "q4_k" and k in (4096, 8192) and staged_tokens >= 2) or (fmt == "q4_kt" and tokens <= staged_tokens):
+    if (fmt == "q4_k" and k in (4096, 8192) and staged_tokens >= 2) or (fmt in TILED_Q8 and tokens <= staged_tokens):
         return x, _dt(x), tokens
     return quant_q8(x), DTYPE["q8"], tokens
 
 
 def mv_swiglu_q8(fmt, w, w2, x, n, k, tokens=None, y=None, accumulate=False):
     """The int8 swiglu matvec y (+)= silu(x W^T) (x W2^T) (g_mv_{fmt}_k{K}_swiglu[_t{TG}]_q8): gate W and up W2
-    [n, k]; x a planar Q8_1 buffer (with tokens) or f32 / bf16 rows (quantized as quant_q8 does). fmt q4_kt (tiled
-    layout) or GGUF q4_k / q4_0 / q6_k. Returns y f32 [tokens, n]."""
+    [n, k]; x a planar Q8_1 buffer (with tokens) or f32 / bf16 rows (quantized as quant_q8 does). fmt q4_kt / q4_0t
+    (tiled layouts) or GGUF q4_k / q4_0 / q6_k. Returns y f32 [tokens, n]."""
     _dev(w, w2, x, y)
-    x, xd, tokens = _q8_input(fmt, x, k, tokens, staged_tokens=2 if fmt == "q4_kt" else 0)
+    x, xd, tokens = _q8_input(fmt, x, k, tokens, staged_tokens=2 if fmt in TILED_Q8 else 0)
     y = _out(y, (tokens, n), torch.float32, w.device, accumulate)
     _lib.call("qmm_mv_swiglu_q8", CODE[fmt], k, n, tokens, int(bool(accumulate)), _ptr(x), xd, _ptr(w), _ptr(w2),
               _ptr(y), _stream())
@@ -180,7 +183,7 @@ def mv_pair_q8(fmt, w, w2, x, n, k, tokens=None, y=None, y2=None, accumulate=Fal
     """Two int8 matvecs of one input in one launch (g_mv_{fmt}_k{K}_pair[_t{TG}]_q8): y (+)= x W^T, y2 (+)= x W2^T,
     each equal bit for bit to the one-matrix kernel's of the same layout. Returns (y, y2) f32 [tokens, n]."""
     _dev(w, w2, x, y, y2)
-    x, xd, tokens = _q8_input(fmt, x, k, tokens, staged_tokens=2 if fmt == "q4_kt" else 0)
+    x, xd, tokens = _q8_input(fmt, x, k, tokens, staged_tokens=2 if fmt in TILED_Q8 else 0)
     y = _out(y, (tokens, n), torch.float32, w.device, accumulate)
     y2 = _out(y2, (tokens, n), torch.float32, w.device, accumulate)
     _lib.call("qmm_mv_pair_q8", CODE[fmt], k, n, tokens, int(bool(accumulate)), _ptr(x), xd, _ptr(w), _ptr(w2),
@@ -530,6 +533,15 @@ def tile_q4k(w, rows, k):
     return w_t
 
 
+def tile_q40(w, rows, k):
+    """GGUF Q4_0 rows (uint8, rows * k / 32 * 18 bytes) -> the tiled layout (format "q4_0t") the int8-activation
+    decode GEMV streams contiguously, in the units of tile_q4k. rows % 16 == 0, k % 512 == 0; the same size."""
+    _dev(w)
+    w_t = torch.empty(rows * row_bytes("q4_0", k), dtype=torch.uint8, device=w.device)
+    _lib.call("qmm_tile_q40", _ptr(w), rows, k, _ptr(w_t), _stream())
+    return w_t
+
+
 def tile_mxfp4(nib, sc, rows, k):
     """Split planes (nibbles u8 [rows, k/2], scales u8 [rows, k/32]) -> MFMA-tiled planes (nib_t u8 [rows*k/2],
     sc_t u8 [qmm_mxfp4t_scale_bytes]) for the grouped GEMM (format "mxfp4t"). rows % 32 == 0, k % 64 == 0; a
@@ -682,7 +694,7 @@ GEMM_MIN_TOKENS = 64   # %gemm: epochs of 64+ tokens take the GEMM / grouped cha
 
 
 # formats whose decode matvecs contract integer weight codes with Q8_1 activations (IQ_FMTS, S/gen_llm.py:514-519)
-LINEAR_Q8_FORMATS = ("q4_0", "q4_k", "q4_kt", "q6_k")
+LINEAR_Q8_FORMATS = ("q4_0", "q4_k", "q4_kt", "q6_k", "q4_0t")
 
 
 def linear(fmt, x, w, n, k, y=None, mode="store", ws=None, w2=None, ws2=None, q8=True):
@@ -690,7 +702,7 @@ def linear(fmt, x, w, n, k, y=None, mode="store", ws=None, w2=None, ws2=None, q8
     S/gen_llm.py:4568-4625): the prefill GEMM for 64+ tokens (GGUF q4_k / q6_k / q4_0 on the f16 MFMA, the activation
     row-scaled to f16 first; MXFP4 on the scaled MFMA, the activation quantized to MXFP8 first -- GGUF mxfp4 blocks
     go through split_planes, repacked once per weight tensor), else the decode GEMV. The decode GEMV of a format with
-    integer codes (q4_0, q4_k, q4_kt, q6_k) takes Q8_1 activations, as the reference does by default (ACT_Q8,
+    integer codes (q4_0, q4_k, q4_kt, q6_k, q4_0t) takes Q8_1 activations, as the reference does by default (ACT_Q8,
     iq = ACT_Q8 and fmt in IQ_FMTS and K / 32 <= 1024, S/gen_llm.py:514-519, :4590); q8=False keeps f32 / bf16
     activations (ACT_Q8=0). y is f32."""
     if mode not in ("store", "acc", "swiglu"):

@@ -241,6 +241,53 @@ def q4_kt_to_gguf(raw_t, rows, k):
     return np.ascontiguousarray(blk).reshape(-1)    # rows in order, super-blocks in order
 
 
+def q4_0_to_tiled(raw, rows, k):
+    """GGUF Q4_0 rows -> the tiled layout of the decode GEMV (qmm_tile_q40), written from the layout's definition:
+    per block of 16 rows, units of 512 values, 4608 bytes each; at 16 (2 r + sb) the eight f16 d of blocks 8 sb ..
+    8 sb + 7 of the unit's row r (a 256-value span), then four 1 KB code planes, plane q holding at 16 l
+    (l = 4 r + 2 sb + h) bytes 16 (4 h + q) .. +16 of the span's 128 code bytes. Span byte 32 p + i holds code i of
+    block 2 p in its low nibble and code i of block 2 p + 1 in its high nibble (code i of a block: qs[i] & 15 for
+    i < 16, qs[i - 16] >> 4 otherwise). rows % 16 == 0, k % 512 == 0."""
+    assert rows % 16 == 0 and k % 512 == 0, (rows, k)
+    b = _blocks(raw, "q4_0").reshape(rows, k // 32, 18)
+    out = np.empty(rows * k // 32 * 18, np.uint8)
+    for rb in range(rows // 16):
+        for u in range(k // 512):
+            base = (rb * (k // 512) + u) * 4608
+            for r in range(16):
+                for sb in range(2):
+                    blks = b[16 * rb + r, 16 * u + 8 * sb: 16 * u + 8 * sb + 8]     # [8, 18]
+                    out[base + 16 * (2 * r + sb): base + 16 * (2 * r + sb) + 16] = blks[:, 0:2].reshape(-1)
+                    codes = [[int(bk[2 + i] & 15) if i < 16 else int(bk[2 + i - 16] >> 4) for i in range(32)]
+                             for bk in blks]
+                    span = bytes(codes[2 * (c // 32)][c % 32] | (codes[2 * (c // 32) + 1][c % 32] << 4)
+                                 for c in range(128))
+                    for h in range(2):
+                        for q in range(4):
+                            o = base + 512 + 1024 * q + 16 * (4 * r + 2 * sb + h)
+                            out[o: o + 16] = np.frombuffer(span[16 * (4 * h + q): 16 * (4 * h + q) + 16], np.uint8)
+    return out
+
+
+def q4_0t_to_gguf(raw_t, rows, k):
+    """Inverse of q4_0_to_tiled (vectorized: an independent construction by index arithmetic)."""
+    U = k // 512
+    t = np.asarray(raw_t).view(np.uint8).reshape(rows // 16, U, 4608)
+    d = t[:, :, :512].reshape(rows // 16, U, 16, 2, 8, 2)                     # [rb, u, r, sb, block, 2 bytes]
+    span = t[:, :, 512:].reshape(rows // 16, U, 4, 16, 2, 2, 16)              # [rb, u, q, r, sb, h, 16]
+    span = span.transpose(0, 1, 3, 4, 5, 2, 6).reshape(rows // 16, U, 16, 2, 4, 32)   # [rb, u, r, sb, page, i]
+    lo, hi = span & 15, span >> 4                                             # codes i of blocks 2 p, 2 p + 1
+    codes = np.stack([lo, hi], axis=5).reshape(rows // 16, U, 16, 2, 8, 32)   # [rb, u, r, sb, block, i]
+    qs = codes[..., :16] | (codes[..., 16:] << 4)
+    blk = np.concatenate([d, qs.astype(np.uint8)], axis=-1)                   # [rb, u, r, sb, block, 18]
+    return np.ascontiguousarray(blk.transpose(0, 2, 1, 3, 4, 5)).reshape(-1)
+
+
+def dequant_q4_0t(raw_t, rows, k):
+    """Q4_0 in the tiled GEMV layout: the values of the GGUF blocks it permutes."""
+    return dequant_q4_0(q4_0t_to_gguf(raw_t, rows, k), rows, k)
+
+
 def q6_k_fields(raw):
     """(d f32 [nb], sc i32 [nb, 16], q i32 [nb, 256]) of Q6_K super-blocks: ql = bytes 0..127, qh = 128..191, int8
     scales = 192..207, f16 d = 208..209. Value c = 128 half + 32 j + l (group g = 4 half + j) has the 6-bit code
@@ -286,4 +333,6 @@ def dequantize(fmt, raw, rows, k, scales=None):
         return dequant_q4_kt(raw, rows, k)
     if fmt == "q6_k":
         return dequant_q6_k(raw, rows, k)
+    if fmt == "q4_0t":
+        return dequant_q4_0t(raw, rows, k)
     raise ValueError(fmt)

@@ -451,3 +451,60 @@ def test_q4_kt_round_trip_and_values():
         assert np.array_equal(of.q4_kt_to_gguf(t, rows, k), np.asarray(raw).reshape(-1))
         want = of.dequant_q4_k(raw, rows, k)
         assert np.array_equal(of.dequant_q4_kt(t, rows, k).view(np.uint32), want.view(np.uint32))
+
+
+# ------------------------------------------------------------------------------------------- Q4_0 tiled layout
+def _q4_0_signed(rng, rows, k):
+    """Q4_0 blocks with scales of both signs (synth draws positive ones)."""
+    from qmm import synth
+    raw = synth.q4_0_weights(rng, rows, k).reshape(-1, 18).copy()
+    raw[::3, 1] |= 0x80
+    return raw.reshape(-1)
+
+
+@pytest.mark.parametrize("rows,k", [(16, 512), (32, 1024)])
+def test_q4_0t_addresses_follow_the_layout_definition(rows, k):
+    """Every scale byte and every code nibble of every GGUF Q4_0 block lands where the tiled layout puts it, as a flat
+    offset: row r, block b, code i (value 32 b + i); rb = r // 16, s = r % 16, unit u = b // 16, span sb = (b // 8)
+    % 2, j = b % 8, unit base B = 4608 (rb (K / 512) + u); d byte e -> B + 16 (2 s + sb) + 2 j + e; span byte
+    c = 32 (j // 2) + i -> B + 512 + 1024 ((c // 16) % 4) + 16 (4 s + 2 sb + c // 64) + c % 16, low nibble for even j."""
+    rng = np.random.default_rng(31)
+    raw = _q4_0_signed(rng, rows, k)
+    t = of.q4_0_to_tiled(raw, rows, k)
+    assert t.size == raw.size
+    blk = raw.reshape(rows, k // 32, 18)
+    r, b, i = np.meshgrid(np.arange(rows), np.arange(k // 32), np.arange(32), indexing="ij")
+    s, u, sb, j = r % 16, b // 16, (b // 8) % 2, b % 8
+    B = 4608 * ((r // 16) * (k // 512) + u)
+    c = 32 * (j // 2) + i
+    off = B + 512 + 1024 * ((c // 16) % 4) + 16 * (4 * s + 2 * sb + c // 64) + c % 16
+    nib = np.where(j % 2 == 0, t[off] & 15, t[off] >> 4)
+    code = np.where(i < 16, blk[r, b, 2 + i % 16] & 15, blk[r, b, 2 + i % 16] >> 4)
+    assert np.array_equal(nib, code)
+    for e in range(2):
+        doff = B[..., 0] + 16 * (2 * s[..., 0] + sb[..., 0]) + 2 * j[..., 0] + e
+        assert np.array_equal(t[doff], blk[:, :, e])
+    # the code planes are a permutation of nibbles: every plane byte is named exactly twice, once per nibble
+    cnt = np.bincount((2 * off + j % 2).ravel(), minlength=2 * t.size).reshape(-1, 4608, 2)
+    assert (cnt[:, 512:] == 1).all() and (cnt[:, :512] == 0).all()
+
+
+def test_q4_0t_round_trip_and_values():
+    rng = np.random.default_rng(32)
+    for rows, k in ((16, 512), (48, 2048), (32, 1536)):
+        raw = _q4_0_signed(rng, rows, k)
+        t = of.q4_0_to_tiled(raw, rows, k)
+        assert np.array_equal(of.q4_0t_to_gguf(t, rows, k), raw)
+        want = of.dequant_q4_0(raw, rows, k)
+        assert np.array_equal(of.dequant_q4_0t(t, rows, k).view(np.uint32), want.view(np.uint32))
+
+
+def test_q4_0t_span_page_swap_negative_control():
+    """Swapping the two nibbles of every code byte (blocks 2 p <-> 2 p + 1 of a page) must change the values."""
+    rng = np.random.default_rng(33)
+    rows, k = 16, 512
+    raw = _q4_0_signed(rng, rows, k)
+    t = of.q4_0_to_tiled(raw, rows, k)
+    bad = t.copy().reshape(-1, 4608)
+    bad[:, 512:] = (bad[:, 512:] >> 4) | (bad[:, 512:] << 4)
+    assert not np.array_equal(of.dequant_q4_0t(bad.reshape(-1), rows, k), of.dequant_q4_0(raw, rows, k))
