@@ -22,7 +22,7 @@ one workload, or with --no-secondary):
     q4_k_gemm   Q4_K prefill GEMM, x bf16 [512, 4096] (row scale to f16, then the MFMA GEMM), W [4096, 4096],
                 y bf16 [512, 4096] (Qwen3-8B attn o_proj)
     mxfp4_moe   MXFP4 MoE at the gpt-oss-20b shape (32 experts, top-4, H = FE = 2880), T tokens (--m): T < 64 the
-                decode chain (top-k, gate/up and down expert matvecs on split planes, combine), else the prefill chain
+                decode chain (top-k, gate/up and down expert matvecs, combine), else the prefill chain
                 (top-k, bucket, MXFP8 quantize, grouped gate_up on the scaled MFMA + swiglu_oai with the MXFP8
                 quantization of its output fused, grouped down, combine). Secondary at T = 1, 256, 1024 and 4096.
     q4_k_moe    Q4_K MoE prefill chain at the Qwen3-30B-A3B shape (128 experts, top-8, H = 2048, FE = 768), T = 64
@@ -318,7 +318,7 @@ class MoeWorkload:
             self.metric = "Q4_K MoE prefill TFLOP/s (Qwen3-30B-A3B, 128 experts, top-8)"
         self.decode = self.T < 64
         # the Q4_K prefill chain streams the tiled layout through the narrow grouped kernel
-        kern = ("expert_mv" if self.decode else "mxfp4_grouped_kernel_gu8") if index == 3 else \
+        kern = ("mxt_expert_kernel" if self.decode else "mxfp4_grouped_kernel_gu8") if index == 3 else \
             ("expert_mv" if self.decode else "q4k_narrow_kernel_gu")
         model = "mxfp4_moe_gpt_oss_20b" if index == 3 else "q4_k_moe_qwen3_30b_a3b"
         self.traffic_name = f"{kern}.{model}_t{self.T}"
@@ -334,15 +334,13 @@ class MoeWorkload:
         self.logits = torch.from_numpy(d["logits"]).to(dev)
         E, H, FE = self.E, self.H, self.FE
         if d["fmt"] == "mxfp4":
-            # one-time weight preparation: GGUF blocks -> split planes (decode) -> MFMA-tiled planes (prefill)
+            # one-time weight preparation: GGUF blocks -> split planes -> MFMA-tiled planes, the one copy the decode
+            # expert matvecs and the prefill grouped GEMMs both read
             gn, gs = ops.repack_mxfp4(u8(d["gate_up"]), E * 2 * FE, H)
             dn, ds = ops.repack_mxfp4(u8(d["down"]), E * H, FE)
-            if self.decode:
-                self.fmt = "mxfp4s"
-            else:
-                gn, gs = ops.tile_mxfp4(gn, gs, E * 2 * FE, H)
-                dn, ds = ops.tile_mxfp4(dn, ds, E * H, FE)
-                self.fmt = "mxfp4t"
+            gn, gs = ops.tile_mxfp4(gn, gs, E * 2 * FE, H)
+            dn, ds = ops.tile_mxfp4(dn, ds, E * H, FE)
+            self.fmt = "mxfp4t"
             self.kw = dict(w_gate=gn, ws_gate=gs, w_down=dn, ws_down=ds, fused=True, act=d["act"])
             self.wbytes_expert = (2 * FE * H + H * FE) // 2 + (2 * FE * H + H * FE) // 32
             self.peak_key = "fp8"
@@ -379,7 +377,7 @@ class MoeWorkload:
         self.route_gu = self.decode and self.E <= ops.ROUTE_GU_MAX_E and self.T * self.KU <= ops.ROUTE_GU_MAX_A
         if self.decode:
             self.gu_y = torch.empty_like(mid["act"])
-        elif self.fmt == "mxfp4t":
+        elif self.fmt == "mxfp4t":   # prefill
             self.gu_x, self.gu_xs = ops.quant_mxfp8(self.x)
             self.gu_y = (torch.empty_like(mid["act8"]), torch.empty_like(mid["act_scales"]))
         else:
@@ -403,7 +401,7 @@ class MoeWorkload:
             self.ops.moe_expert_mv(self.fmt, "gu", self.mid["ids"], self.x, kw["w_gate"], self.FE, self.H, self.E,
                                    self.KU, w2=kw.get("w_up"), ws=kw.get("ws_gate"), fused=kw["fused"],
                                    act=kw["act"], y=self.gu_y)
-        elif self.fmt == "mxfp4t":   # the gate/up GEMM with its activation written as MXFP8 (the chain's kernel)
+        elif self.fmt == "mxfp4t":   # prefill: the gate/up GEMM with its activation written as MXFP8 (the chain's kernel)
             self.ops.moe_grouped_mxfp8(self.fmt, self.mid["tile_info"], self.mid["rowmap"], self.gu_x, kw["w_gate"],
                                        self.FE, self.H, self.E, self.KU, ws=kw.get("ws_gate"), x_scales=self.gu_xs,
                                        fused=kw["fused"], act=kw["act"], codes=self.gu_y[0], scales=self.gu_y[1])
@@ -430,7 +428,7 @@ class MoeWorkload:
         MXFP4 grouped GEMM, f32 otherwise)"""
         T, H, A = self.T, self.H, self.T * self.KU
         wgu = self.experts_hit * (self.wbytes_expert * 2 // 3)
-        if self.fmt == "mxfp4t":
+        if self.fmt == "mxfp4t" and not self.decode:
             return wgu + T * H + T * H // 32 + A * self.FE * 33 // 32
         return wgu + T * H * 2 + A * self.FE * 4
 
@@ -441,10 +439,10 @@ class MoeWorkload:
         return self.alg_flops() / sec / 1e12
 
     def dtype(self):
+        if self.fmt == "mxfp4t" and self.decode:
+            return "mxfp4 (MFMA-tiled planes) x bf16 -> f32 (expert matvecs)"
         if self.fmt == "mxfp4t":
             return "mxfp4 x mxfp8 (E4M3, E8M0 per 32) -> f32"
-        if self.fmt == "mxfp4s":
-            return "mxfp4 x bf16 -> f32 (expert matvecs)"
         if self.fmt == "q4_kt":
             return "q4_k (tiled layout) x f16 (row-scaled) -> f32"
         return "q4_k x f16 (row-scaled) -> f32"

@@ -246,6 +246,19 @@ int qmm_moe_expert_mv_split(int mode, int fused, int act, int64_t k, int64_t n, 
                             const void *w2, const void *ws2, const float *bias, const float *bias2, float *y,
                             qmm_stream_t stream);
 
+/* qmm_moe_expert_mv for MXFP4 in MFMA-tiled planes (QMM_MXFP4T from qmm_tile_mxfp4, each expert tensor tiled as
+ * [E rows, k]), the planes the grouped prefill GEMM reads, so one weight copy serves decode and prefill (no reference
+ * counterpart for the layout; the products are g_moe_gu_* / g_moe_dn_* on mxfp4s, S/gen_moe.py:535-727): w / w2 the
+ * tile planes, ws / ws2 their scale groups; fused as qmm_moe_expert_mv_split (expert e's n gate rows then its n up
+ * rows in one tiled tensor). n % 32 == 0, k % 64 == 0, assignments <= 65535. Per 32-value block the split-plane
+ * kernel's arithmetic (fp4 x activation pairs in f32, times the E8M0 scale); the blocks are summed in another order
+ * (the rel-L2 bar against the oracle holds, not bit equality with the split-plane call). A multi-token call equals
+ * one-token calls bit for bit. */
+int qmm_moe_expert_mv_tiled(int mode, int fused, int act, int64_t k, int64_t n, int E, int KU, int64_t assignments,
+                            const int32_t *ids, const void *x, int x_dtype, const void *w, const void *ws,
+                            const void *w2, const void *ws2, const float *bias, const float *bias2, float *y,
+                            qmm_stream_t stream);
+
 /* Grouped expert GEMM over bucketed rows, g_moe_ggu_{fmt}[_fused]_k{H} / g_moe_gdn_{fmt}_k{FE}
  * (S/gen_moe.py:1126-1228). The name fields (fmt, mode gu / dn, fused, the activation, E and KU, which the reference
  * compiles into the kernel) come first, then the launch arguments in the reference's order
@@ -375,9 +388,9 @@ int qmm_moe_combine_gated(int64_t tokens, int64_t rows, int64_t H, int KU, const
  * logits followed by g_moe_gu_{fmt}[_fused]_k{H}_r{R} (S/gen_moe.py:535-727, launch :564), the reference's first
  * decode commands (S/gen_llm.py:5373-5381), fused. The routing arguments as qmm_moe_topk (ids / wts are written as
  * it writes them), then the gate/up matvec's as qmm_moe_expert_mv_split with mode 0 (fmt any qmm_moe_expert_mv
- * format or QMM_MXFP4S with its scale planes ws / ws2; w2 / ws2 ignored when fused): act[a] for the tokens * KU
- * assignments, each workgroup ranking its token's logits itself. Equal bit for bit to qmm_moe_topk then
- * qmm_moe_expert_mv[_split](mode 0). */
+ * format, QMM_MXFP4S with its scale planes ws / ws2, or QMM_MXFP4T with its tiled planes; w2 / ws2 ignored when
+ * fused): act[a] for the tokens * KU assignments, each workgroup ranking its token's logits itself. Equal bit for bit
+ * to qmm_moe_topk then qmm_moe_expert_mv[_split|_tiled](mode 0). */
 int qmm_moe_topk_expert_mv(const float *logits, int64_t tokens, int E, int KU, int gating, int norm, float scale,
                            const float *router_bias, int32_t *ids, float *wts, int fmt, int fused, int act, int64_t k,
                            int64_t n, const void *x, int x_dtype, const void *w, const void *ws, const void *w2,
@@ -389,7 +402,8 @@ int qmm_moe_topk_expert_mv(const float *logits, int64_t tokens, int E, int KU, i
  *   y[t, c] = fma(wts[t,KU-1], ys[t*KU+KU-1, c], ... fma(wts[t,0], ys[t*KU, c], y0)),
  *   ys[a] = Wd[e] x[a] + bias[e] (e = clamp(ids[a], 0, E - 1)),  y0 = sg ? sg[t] y[t, c] : accumulate ? y[t, c] : 0
  * equal bit for bit to qmm_moe_expert_mv[_split](mode 1) then qmm_moe_combine[_gated] (pos NULL). fmt as
- * qmm_moe_expert_mv plus QMM_MXFP4S (ws its scale planes [E, n, k/32]; ignored otherwise); w [E, n, k]; x [tokens*KU,
+ * qmm_moe_expert_mv plus QMM_MXFP4S (ws its scale planes [E, n, k/32]; ignored otherwise) and QMM_MXFP4T (tiled
+ * planes, ws their scale groups; then each ys row is qmm_moe_expert_mv_tiled's); w [E, n, k]; x [tokens*KU,
  * k] f32 / bf16 (the gate/up output); ids i32 / wts f32 [tokens, KU]; bias f32 [E, n] or NULL; sg f32 [tokens] or
  * NULL; y f32 [tokens, n]. tokens <= 65535. */
 int qmm_moe_expert_mv_combine(int fmt, int64_t k, int64_t n, int E, int KU, int64_t tokens, const int32_t *ids,
@@ -402,12 +416,12 @@ int qmm_moe_expert_mv_combine(int fmt, int64_t k, int64_t n, int E, int KU, int6
  *   tokens >= 64 (prefill): qmm_moe_route / qmm_moe_topk, [qmm_moe_wscale], qmm_moe_bucket, the activation operand
  *     (qmm_row_scale_f16 for GGUF formats, qmm_quant_mxfp8 for MXFP4 planes), the grouped gate/up GEMM
  *     (qmm_moe_grouped / qmm_moe_grouped_mxfp8), its output's operand, the grouped down GEMM, qmm_moe_combine;
- *   tokens < 64 (decode): route, [wscale], the gate/up and down expert matvecs (qmm_moe_expert_mv[_split], or with
+ *   tokens < 64 (decode): route, [wscale], the gate/up and down expert matvecs (qmm_moe_expert_mv[_split|_tiled], or with
  *     flags QMM_MOE_Q8 qmm_quant_q8 + qmm_moe_expert_mv_q8 for both), qmm_moe_combine over the assignments; on f32 /
  *     bf16 activations the down matvecs and the combine run as qmm_moe_expert_mv_combine, and with given logits,
  *     E <= 64 and tokens * KU <= 8 the routing and the gate/up matvecs as qmm_moe_topk_expert_mv.
  * Results equal those of the separate calls bit for bit. Names as in those calls: fmt the gate / up format (GGUF
- * Q4_K / Q6_K / Q4_0 / MXFP4, split MXFP4S, tiled MXFP4T or Q4_KT for prefill; or QMM_GATE_UP(gate, up) of GGUF
+ * Q4_K / Q6_K / Q4_0 / MXFP4, split MXFP4S, tiled MXFP4T, or Q4_KT for prefill; or QMM_GATE_UP(gate, up) of GGUF
  * formats with two tensors, without QMM_MOE_Q8), fmt_down the down tensor's (-1: fmt, a pair's gate format); x f32 /
  * bf16 [tokens, H]; logits f32 [tokens, E], or NULL to route with w_router [E, H] (f32 / bf16); router_bias and
  * down_scale (f32 [E]) or NULL; ws_* the split / tiled scale planes; bias_* the expert biases or NULL; y f32

@@ -68,6 +68,17 @@ __device__ __forceinline__ int e4m3_pack2(float a, float b, int sx, int w) {
   return __builtin_amdgcn_cvt_pk_fp8_f32(ldexpf(a, -sx), ldexpf(b, -sx), w, HI);
 }
 
+// The expert activations (S/gen_moe.py:27-46): silu(g) u = g / (1 + e^-g) u, and gpt-oss's swiglu_oai
+// min(g, 7) sigmoid(1.702 min(g, 7)) (clamp(u, -7, 7) + 1).
+__device__ __forceinline__ float act_fn(int act, float g, float u) {
+  if (act == QMM_ACT_SWIGLU_OAI) {
+    const float xg = fminf(g, 7.0f);
+    const float yu = fminf(fmaxf(u, -7.0f), 7.0f);
+    return xg / (1.0f + expf(-1.702f * xg)) * (yu + 1.0f);
+  }
+  return g / (1.0f + expf(-g)) * u;
+}
+
 // ----------------------------------------------------------------------------------------- wave reductions
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -84,13 +84,4 @@ __device__ __forceinline__ void sub_scale(const uint4 &hd, int g, h2 &dsc, h2 &n
 
 __device__ __forceinline__ uint4 ld16(const void *p) { return *reinterpret_cast<const uint4 *>(p); }
 
-__device__ __forceinline__ float act_fn(int act, float g, float u) {
-  if (act == QMM_ACT_SWIGLU_OAI) {
-    const float xg = fminf(g, 7.0f);
-    const float yu = fminf(fmaxf(u, -7.0f), 7.0f);
-    return xg / (1.0f + expf(-1.702f * xg)) * (yu + 1.0f);
-  }
-  return g / (1.0f + expf(-g)) * u;
-}
-
 }  // namespace qmm

@@ -79,26 +79,6 @@ __global__ __launch_bounds__(256) void mv_kernel(int64_t n, int64_t tokens, int6
     }
 }
 
-__device__ __forceinline__ float act_fn(int act, float g, float u) {
-  if (act == QMM_ACT_SWIGLU_OAI) {
-    const float xg = fminf(g, 7.0f);
-    const float yu = fminf(fmaxf(u, -7.0f), 7.0f);
-    return xg / (1.0f + expf(-1.702f * xg)) * (yu + 1.0f);
-  }
-  return g / (1.0f + expf(-g)) * u;
-}
-
-// The routing of the gate/up matvec that selects its own experts (NS > 0): every wave ranks its token's logits
-// (topk_select, the routing kernels' arithmetic) and takes pick a % KU; row block 0's first wave writes ids / wts.
-struct RouteArgs {
-  const float *logits;   // [tokens, E]
-  int gating, norm;
-  float scale;
-  const float *bias;     // router bias [E] or NULL
-  int32_t *ids;          // out: [tokens, KU]
-  float *wts;            // out: [tokens, KU]
-};
-
 // One assignment per workgroup row (blockIdx.x), RW output rows per wave.
 template <class P, int RW, bool GU, int NS = 0>
 __global__ __launch_bounds__(256) void expert_mv_kernel(int64_t n, int64_t assignments, int KU, int E, int64_t k,
@@ -362,6 +342,12 @@ int check_weights(int fmt, int64_t k, const void *w, const void *ws) {
 
 int qmm_mv_q4k_fast(int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, const void *w, float *y,
                     hipStream_t s);
+int qmm_topk_expert_mv_tiled(const RouteArgs &r, int E, int KU, int64_t tokens, int fused, int act, int64_t k,
+                             int64_t n, const void *x, int x_dtype, const void *w, const void *ws, const void *w2,
+                             const void *ws2, const float *bias, const float *bias2, float *y, hipStream_t s);
+int qmm_expert_mv_combine_tiled(int64_t k, int64_t n, int E, int KU, int64_t tokens, const int32_t *ids,
+                                const float *wts, const void *x, int x_dtype, const void *w, const void *ws,
+                                const float *bias, int accumulate, const float *sg, float *y, hipStream_t s);
 
 extern "C" int qmm_mv(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
                       const void *w, const void *ws, float *y, qmm_stream_t stream) {
@@ -661,8 +647,12 @@ extern "C" int qmm_moe_topk_expert_mv(const float *logits, int64_t tokens, int E
   if (E <= 0 || E > 256 || KU <= 0 || KU > 8 || KU > E) return QMM_ERR_RANGE;
   if (gating < 1 || gating > 3 || (gating == 1 && router_bias)) return QMM_ERR_RANGE;
   if (tokens <= 0 || tokens * KU > (1 << 24)) return QMM_ERR_SHAPE;
-  if (!valid_fmt(fmt)) return QMM_ERR_FORMAT;
   if (act != QMM_ACT_SILU && act != QMM_ACT_SWIGLU_OAI) return QMM_ERR_RANGE;
+  if (fmt == QMM_MXFP4T)   // the MFMA-tiled planes: expert_mv_tiled.hip
+    return qmm_topk_expert_mv_tiled(RouteArgs{logits, gating, norm, scale, router_bias, ids, wts}, E, KU, tokens,
+                                    fused, act, k, n, x, x_dtype, w, ws, w2, ws2, bias, bias2, y,
+                                    reinterpret_cast<hipStream_t>(stream));
+  if (!valid_fmt(fmt)) return QMM_ERR_FORMAT;
   if (!x || !y) return QMM_ERR_NULL;
   if (n <= 0 || row_bytes(fmt, k) == 0) return QMM_ERR_SHAPE;
   if (x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
@@ -695,10 +685,13 @@ extern "C" int qmm_moe_expert_mv_combine(int fmt, int64_t k, int64_t n, int E, i
                                          const int32_t *ids, const float *wts, const void *x, int x_dtype,
                                          const void *w, const void *ws, const float *bias, int accumulate,
                                          const float *sg, float *y, qmm_stream_t stream) {
-  if (!valid_fmt(fmt)) return QMM_ERR_FORMAT;
+  if (!valid_fmt(fmt) && fmt != QMM_MXFP4T) return QMM_ERR_FORMAT;
   if (E <= 0 || E > 1024 || KU <= 0 || KU > 8) return QMM_ERR_RANGE;
   if (!ids || !wts || !x || !y) return QMM_ERR_NULL;
   if (n <= 0 || tokens <= 0 || tokens > 65535 || row_bytes(fmt, k) == 0) return QMM_ERR_SHAPE;
+  if (fmt == QMM_MXFP4T)   // the MFMA-tiled planes: expert_mv_tiled.hip
+    return qmm_expert_mv_combine_tiled(k, n, E, KU, tokens, ids, wts, x, x_dtype, w, ws, bias, sg ? 1 : accumulate, sg,
+                                       y, reinterpret_cast<hipStream_t>(stream));
   if (n > (1ll << 30)) return QMM_ERR_SHAPE;
   if (x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
   if (int st = check_weights(fmt, k, w, ws)) return st;

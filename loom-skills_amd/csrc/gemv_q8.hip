@@ -220,15 +220,6 @@ enum Mode { kPlain = 0, kSwiglu = 1, kPair = 2 };
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
-__device__ __forceinline__ float act_fn(int act, float g, float u) {
-  if (act == QMM_ACT_SWIGLU_OAI) {
-    const float xg = fminf(g, 7.0f);
-    const float yu = fminf(fmaxf(u, -7.0f), 7.0f);
-    return xg / (1.0f + expf(-1.702f * xg)) * (yu + 1.0f);
-  }
-  return silu_mul(g, u);
-}
-
 // RW rows per wave (4 for one matrix, 2 when two stream), TG tokens per workgroup sharing every weight load
 template <class P, int TG, int MODE, int RW>
 __global__ __launch_bounds__(256) void mv_q8_kernel(int64_t n, int64_t tokens, int64_t k, int accumulate,

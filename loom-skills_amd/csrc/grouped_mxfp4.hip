@@ -3,7 +3,7 @@
 // g_gemm_mxfp4s_{store|swiglu}_f8_m256 (S/gen_mxfp4s.py:50-101, the gfx12 fp8 WMMA counterpart), which is the same
 // kernel over dense 64-row tiles of one weight matrix (qmm_gemm_mxfp4):
 //
-//   gu   act[r, c] = act_fn(sum_k X8[t, k] Wg[e][c, k] + bg[e, c], sum_k X8[t, k] Wu[e][c, k] + bu[e, c]),
+//   gu   act[r, c] = act_fast(sum_k X8[t, k] Wg[e][c, k] + bg[e, c], sum_k X8[t, k] Wu[e][c, k] + bu[e, c]),
 //                    t = rowmap[r] / KU
 //   dn   ys[r, c]  = sum_k A8[r, k] Wd[e][c, k] + bd[e, c]                             (rows already sorted)
 //
@@ -101,7 +101,7 @@ struct MArgs {
 // expf per value are a measurable tail. The outputs are MXFP8-quantized next (3 mantissa bits).
 __device__ __forceinline__ float sigmoid_fast(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
-__device__ __forceinline__ float act_fn(int act, float g, float u) {
+__device__ __forceinline__ float act_fast(int act, float g, float u) {
   if (act == QMM_ACT_SWIGLU_OAI) {
     const float xg = fminf(g, 7.0f);
     const float yu = fminf(fmaxf(u, -7.0f), 7.0f);
@@ -424,7 +424,7 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
       for (int r = 0; r < 16; ++r) {
         const int lr = 8 * (r >> 2) + 4 * h + (r & 3);
         Of[lr * OPITCH + 32 * wave + lc] =
-            src_row[32 * i + lr] >= 0 ? act_fn(a.act, acc[i][0][r] + bg, acc[i][1][r] + bu) : 0.f;
+            src_row[32 * i + lr] >= 0 ? act_fast(a.act, acc[i][0][r] + bg, acc[i][1][r] + bu) : 0.f;
       }
       __syncthreads();
       const f32x4 *src = reinterpret_cast<const f32x4 *>(Of + qrow * OPITCH + 32 * blk + 16 * part);
@@ -458,7 +458,7 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
         const int row = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
         if (row >= a.M) continue;
         float v;
-        if constexpr (GU) v = act_fn(QMM_ACT_SILU, acc[i][0][r], acc[i][1][r]);
+        if constexpr (GU) v = act_fast(QMM_ACT_SILU, acc[i][0][r], acc[i][1][r]);
         else v = acc[i][0][r];
         const int64_t o = (int64_t)row * N + col;
         if constexpr (OUT == kOutF32 || OUT == kOutF32Acc) {
@@ -484,7 +484,7 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
       const int lr = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
       if (src_row[lr] < 0) continue;   // a row without an assignment is not written
       float v;
-      if constexpr (GU) v = act_fn(a.act, acc[i][0][r] + bg, acc[i][1][r] + bu);
+      if constexpr (GU) v = act_fast(a.act, acc[i][0][r] + bg, acc[i][1][r] + bu);
       else v = acc[i][0][r] + bg;
       __builtin_nontemporal_store(v, a.y + (int64_t)(m0 + lr) * N + col);
     }

@@ -93,9 +93,9 @@ int check_chain(int fmt, int fmt_down, int flags, int E, int KU, int64_t T, int6
     return QMM_ERR_FORMAT;
   }
   if (flags & QMM_MOE_Q8) return gguf_blocks(fmt) && gguf_blocks(fmt_down) ? QMM_OK : QMM_ERR_FORMAT;
-  if (fmt == QMM_MXFP4T || fmt_down == QMM_MXFP4T || fmt == QMM_Q4_KT || fmt_down == QMM_Q4_KT)
-    return QMM_ERR_FORMAT;   // the expert matvecs read GGUF blocks / split planes
-  if ((fmt == QMM_MXFP4S) != (fmt_down == QMM_MXFP4S)) return QMM_ERR_FORMAT;
+  if (fmt == QMM_Q4_KT || fmt_down == QMM_Q4_KT) return QMM_ERR_FORMAT;   // the expert matvecs read GGUF blocks
+  if ((fmt == QMM_MXFP4S) != (fmt_down == QMM_MXFP4S) || (fmt == QMM_MXFP4T) != (fmt_down == QMM_MXFP4T))
+    return QMM_ERR_FORMAT;
   return QMM_OK;
 }
 
@@ -139,7 +139,7 @@ extern "C" int qmm_moe_routed(int fmt, int fmt_down, int fused, int act, int gat
   // slower with 128 experts or eight tokens)
   const bool route_gu = !p.prefill && !p.q8 && logits && E <= 64 && p.A <= 8 && !fmt_mixed(fmt);
   if (route_gu)
-    st = fmt == QMM_MXFP4S
+    st = mx_planes(fmt)
              ? qmm_moe_topk_expert_mv(logits, T, E, KU, gating, norm, scale, router_bias, ids, wts, fmt, fused, act, H,
                                       FE, x, x_dtype, w_gate, ws_gate, w_up, ws_up, bias_gate, bias_up,
                                       static_cast<float *>(at(p.act)), stream)
@@ -178,6 +178,9 @@ extern "C" int qmm_moe_routed(int fmt, int fmt_down, int fused, int act, int gat
       st = QMM_OK;   // the gate/up matvecs ran with the routing
     else if (fmt == QMM_MXFP4S)
       st = qmm_moe_expert_mv_split(0, fused, act, H, FE, E, KU, p.A, ids, x, x_dtype, w_gate, ws_gate, w_up, ws_up,
+                                   bias_gate, bias_up, a, stream);
+    else if (fmt == QMM_MXFP4T)
+      st = qmm_moe_expert_mv_tiled(0, fused, act, H, FE, E, KU, p.A, ids, x, x_dtype, w_gate, ws_gate, w_up, ws_up,
                                    bias_gate, bias_up, a, stream);
     else
       st = qmm_moe_expert_mv(fmt, 0, fused, act, H, FE, E, KU, p.A, ids, x, x_dtype, w_gate, w_up, bias_gate,

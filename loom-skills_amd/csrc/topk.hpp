@@ -129,5 +129,15 @@ __device__ __forceinline__ void topk_pick(const int (&rank)[NS], const float (&w
   weight = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), src));
 }
 
+// The routing of a gate/up matvec that selects its own experts: every wave ranks its token's logits (topk_select, the
+// routing kernels' arithmetic) and takes pick a % KU; one wave of the assignment's first workgroup writes ids / wts.
+struct RouteArgs {
+  const float *logits;   // [tokens, E]
+  int gating, norm;
+  float scale;
+  const float *bias;     // router bias [E] or NULL
+  int32_t *ids;          // out: [tokens, KU]
+  float *wts;            // out: [tokens, KU]
+};
 
 }  // namespace qmm

@@ -27,6 +27,8 @@ SIGNATURES = {
                           c_vp, c_vp, c_vp, c_vp, c_vp],
     "qmm_moe_expert_mv_split": [c_int, c_int, c_int, c_i64, c_i64, c_int, c_int, c_i64, c_vp, c_vp, c_int, c_vp,
                                 c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
+    "qmm_moe_expert_mv_tiled": [c_int, c_int, c_int, c_i64, c_i64, c_int, c_int, c_i64, c_vp, c_vp, c_int, c_vp,
+                                c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
     "qmm_moe_grouped": [c_int, c_int, c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_int,
                         c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
     "qmm_moe_grouped_mxfp8": [c_int, c_int, c_int, c_int, c_int, c_i64, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp,

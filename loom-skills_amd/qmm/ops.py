@@ -324,16 +324,16 @@ def moe_bucket(ids, E, n_tiles=None, info=None):
 
 def moe_expert_mv(fmt, mode, ids, x, w, n, k, E, KU, w2=None, ws=None, ws2=None, fused=False, act="silu",
                   bias=None, bias2=None, y=None):
-    """Decode expert matvecs: mode 'gu' act[a] = act(Wg[e] x[a/KU], Wu[e] x[a/KU]) or 'dn' ys[a] = Wd[e] x[a]."""
+    """Decode expert matvecs: mode 'gu' act[a] = act(Wg[e] x[a/KU], Wu[e] x[a/KU]) or 'dn' ys[a] = Wd[e] x[a].
+    MXFP4 as split planes (mxfp4s) or as the grouped GEMM's MFMA-tiled planes (mxfp4t: one weight copy for decode and
+    prefill); ws / ws2 the scale planes."""
     _dev(ids, x, w, w2, ws, ws2, bias, bias2, y)
-    if fmt == "mxfp4t":
-        raise ValueError("the decode expert matvecs read split planes (mxfp4s); mxfp4t is the grouped GEMM's layout")
     A = ids.numel()
     _cols(x, k)
     y = _out(y, (A, n), torch.float32, x.device)
     m = {"gu": 0, "dn": 1}[mode]
     if fmt in SPLIT:
-        _lib.call("qmm_moe_expert_mv_split", m, int(fused), ACT[act], k, n, E, KU, A, _ptr(ids), _ptr(x), _dt(x),
+        _lib.call("qmm_moe_expert_mv_split" if fmt == "mxfp4s" else "qmm_moe_expert_mv_tiled", m, int(fused), ACT[act], k, n, E, KU, A, _ptr(ids), _ptr(x), _dt(x),
                   _ptr(w), _ptr(ws), _ptr(w2), _ptr(ws2), _ptr(bias), _ptr(bias2), _ptr(y), _stream())
     else:
         _lib.call("qmm_moe_expert_mv", CODE[fmt], m, int(fused), ACT[act], k, n, E, KU, A, _ptr(ids), _ptr(x), _dt(x),
@@ -420,8 +420,6 @@ def moe_topk_expert_mv(fmt, logits, KU, gating, norm, x, w, n, k, E, w2=None, ws
     moe_topk(logits, KU, gating, norm, scale, router_bias) then moe_expert_mv(fmt, 'gu', ids, x, w, n, k, E, KU, ...).
     logits f32 [T, E]; x f32 / bf16 [T, k]; act f32 [T*KU, n]."""
     _dev(logits, x, w, w2, ws, ws2, bias, bias2, router_bias, y)
-    if fmt == "mxfp4t":
-        raise ValueError("the decode expert matvecs read split planes (mxfp4s); mxfp4t is the grouped GEMM's layout")
     T, E_ = logits.shape
     if E_ != E:
         raise ValueError(f"logits have {E_} experts, E is {E}")
@@ -443,8 +441,6 @@ def moe_expert_mv_combine(fmt, ids, wts, x, w, n, k, E, ws=None, bias=None, y=No
     [T*KU, k]; ids i32 / wts f32 [T, KU]; with sg (f32 [T]) y holds the shared experts' output and becomes
     sg[t] y[t] + sum_j ... Returns y f32 [T, n]."""
     _dev(ids, wts, x, w, ws, bias, y, sg)
-    if fmt == "mxfp4t":
-        raise ValueError("the decode expert matvecs read split planes (mxfp4s); mxfp4t is the grouped GEMM's layout")
     T, KU = wts.shape
     _cols(x, k)
     if x.shape[0] != T * KU:

@@ -136,9 +136,31 @@ def test_argument_validation_without_a_device(lib):
                                       n, n, n, fake, n) == st["QMM_ERR_SHAPE"]
     assert lib.qmm_moe_topk_expert_mv(fake, 1, 32, 4, 1, 1, f1, n, fake, fake, 1, 0, 0, 256, 8, fake, 1, fake, n, fake,
                                       n, n, n, fake, n) == st["QMM_ERR_DTYPE"]
-    # fused down matvecs + combine: tiled layouts, KU above 8, null weights, split planes without scales, K, dtype
-    assert lib.qmm_moe_expert_mv_combine(4, 256, 8, 4, 2, 1, fake, fake, fake, 0, fake, fake, n, 0, n, fake, n) \
+    # fused down matvecs + combine: tiled Q4_K, MXFP4 tiles of whole 32-row blocks and 64-value chunks with their
+    # scale groups, KU above 8, null weights, split planes without scales, K, dtype
+    assert lib.qmm_moe_expert_mv_combine(5, 256, 32, 4, 2, 1, fake, fake, fake, 0, fake, fake, n, 0, n, fake, n) \
         == st["QMM_ERR_FORMAT"]
+    assert lib.qmm_moe_expert_mv_combine(4, 256, 8, 4, 2, 1, fake, fake, fake, 0, fake, fake, n, 0, n, fake, n) \
+        == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_moe_expert_mv_combine(4, 96, 32, 4, 2, 1, fake, fake, fake, 0, fake, fake, n, 0, n, fake, n) \
+        == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_moe_expert_mv_combine(4, 256, 32, 4, 2, 1, fake, fake, fake, 0, fake, n, n, 0, n, fake, n) \
+        == st["QMM_ERR_NULL"]
+    # decode expert matvecs on tiled MXFP4 planes: mode, whole row blocks / chunks, scale planes, unfused up, assignments
+    assert lib.qmm_moe_expert_mv_tiled(2, 1, 0, 256, 32, 4, 2, 2, fake, fake, 0, fake, fake, n, n, n, n, fake,
+                                       n) == st["QMM_ERR_RANGE"]
+    assert lib.qmm_moe_expert_mv_tiled(0, 1, 0, 256, 48, 4, 2, 2, fake, fake, 0, fake, fake, n, n, n, n, fake,
+                                       n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_moe_expert_mv_tiled(0, 1, 0, 160, 32, 4, 2, 2, fake, fake, 0, fake, fake, n, n, n, n, fake,
+                                       n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_moe_expert_mv_tiled(1, 0, 0, 256, 32, 4, 2, 2, fake, fake, 0, fake, n, n, n, n, n, fake,
+                                       n) == st["QMM_ERR_NULL"]
+    assert lib.qmm_moe_expert_mv_tiled(0, 0, 0, 256, 32, 4, 2, 2, fake, fake, 0, fake, fake, n, n, n, n, fake,
+                                       n) == st["QMM_ERR_NULL"]
+    assert lib.qmm_moe_expert_mv_tiled(0, 1, 0, 256, 32, 4, 2, 3, fake, fake, 0, fake, fake, n, n, n, n, fake,
+                                       n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_moe_expert_mv_tiled(0, 1, 0, 256, 32, 4, 2, 2, fake, fake, 1, fake, fake, n, n, n, n, fake,
+                                       n) == st["QMM_ERR_DTYPE"]
     assert lib.qmm_moe_expert_mv_combine(1, 256, 8, 4, 9, 1, fake, fake, fake, 0, fake, n, n, 0, n, fake, n) \
         == st["QMM_ERR_RANGE"]
     assert lib.qmm_moe_expert_mv_combine(1, 256, 8, 4, 2, 1, fake, n, fake, 0, fake, n, n, 0, n, fake, n) \

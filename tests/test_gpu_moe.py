@@ -99,7 +99,7 @@ def _run_chain(dev, fmt, E, KU, H, FE, T, gating, norm, act, fused, prefill, see
     ex = Experts(dev, fmt, rng, E, H, FE, fused)
     xb = synth.to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32))
     logits = rng.standard_normal((T, E)).astype(np.float32) if live_logits is None else live_logits
-    wfmt, kw = ex.device(split=prefill, tiled=tiled)
+    wfmt, kw = ex.device(split=prefill or tiled, tiled=tiled)
     chain = _ops().moe_prefill if prefill else _ops().moe_decode
     if not prefill:
         kw["q8"] = False   # the decode chain on bf16 activations (the f32 oracle below); int8: test_gpu_q8_matvecs.py
@@ -129,14 +129,49 @@ def test_q4_k_moe_qwen3_30b_a3b_shape(dev, prefill):
 
 
 @pytest.mark.parametrize("T,prefill,tiled", [(256, True, False), (256, True, True), (1024, True, True),
-                                             (1, False, False)])
+                                             (1, False, False), (1, False, True), (5, False, True)])
 def test_mxfp4_moe_gpt_oss_20b_shape(dev, T, prefill, tiled):
     """32 experts, top-4 with softmax over the picked logits (gating 3), H = FE = 2880, fused gate_up,
     swiglu_oai; prefill quantizes activations to MXFP8 for the scaled MFMA (weights as split planes or MFMA-tiled
-    planes), decode multiplies bf16 directly."""
+    planes), decode multiplies bf16 directly (GGUF blocks, or the prefill's MFMA-tiled planes: one weight copy)."""
     y, want, _ = _run_chain(dev, "mxfp4", 32, 4, 2880, 2880, T, 3, False, "swiglu_oai", True, prefill,
                             seed=20261203 + T, tiled=tiled)
     assert_close_rel_l2(y, want, 1e-3, f"mxfp4 moe T={T} tiled={tiled}")
+
+
+@pytest.mark.parametrize("shift,bound", [(0, 0.11), (6, 0.05)])
+def test_mxfp4_chain_mxfp8_cost_against_f16_activations(dev, shift, bound):
+    """What the MXFP8 operands of the scaled MFMA cost against an f16-activation grouped GEMM (the reference's
+    g_gemm_mxfp4s_* on row-scaled f16, S/gen_gemm.py:40): the MXFP4 prefill chain at the gpt-oss-20b shape, T = 256,
+    against the oracle with the hidden rows and the expert activations rounded by the f16 row scale. E4M3 keeps 3
+    mantissa bits, 2.7 % rel-L2 a rounding on these rows, and the chain rounds twice. With the workload's synthetic
+    weights (E8M0 2^-8 .. 2^0, weight RMS 1.1) the gate / up outputs are ~60 and swiglu_oai clamps at 7, which
+    amplifies the hidden rows' rounding: 0.100 rel-L2 in the oracle (bound 0.11). With the exponents lowered by 6
+    (weight RMS 0.018, activations ~1, the scale of a trained layer) it is 0.042 (bound 0.05). The f16 path is within
+    2e-4 of the unrounded products in both cases. The chain itself equals the MXFP8 oracle within 1e-3
+    (test_mxfp4_moe_gpt_oss_20b_shape)."""
+    import torch
+    from qmm import synth
+    E, KU, H, FE, T = 32, 4, 2880, 2880, 256
+    rng = np.random.default_rng(20261301 + shift)
+    ex = Experts(dev, "mxfp4", rng, E, H, FE, True)
+    for name in ("gu", "d"):
+        blk = getattr(ex, name).reshape(-1, 17).copy()
+        blk[:, 0] -= shift
+        setattr(ex, name, blk.reshape(-1))
+    xb = synth.to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32))
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    wfmt, kw = ex.device(split=True, tiled=True)
+    y, mid = _ops().moe_prefill(wfmt, dev_bf16(xb, dev), dev_f32(logits, dev), E, KU, H, FE, 3, False, fused=True,
+                                act="swiglu_oai", **kw)
+    torch.cuda.synchronize()
+    eids, ewts = ref.route(logits, KU, 3, False)
+    np.testing.assert_array_equal(host(mid["ids"]), eids)
+    want, _ = ref.moe(synth.bf16_bits_to_f32(xb), eids, ewts, ex.gate_up, ex.down, act="swiglu_oai",
+                      x_round=ref.f16_rows, act_round=ref.f16_rows)
+    gap = ref.rel_l2(host(y), want)
+    print(f"MXFP8 chain vs f16-activation oracle, exponent shift {shift}: rel-L2 {gap:.4f}")
+    assert gap <= bound, (gap, bound)
 
 
 @pytest.mark.parametrize("fmt,E,KU,H,FE,gating,norm,act,fused,tiled", [
@@ -404,6 +439,10 @@ def test_moe_prefill_chain_graph_replays_equal_eager(dev, fmt):
     ("q4_0", 7, 16, 6, 256, 320, "f32", "acc", False),
     ("mxfp4", 2, 8, 3, 130, 160, "bf16", "gated", False),
     ("q4_k", 9, 4, 1, 64, 256, "f32", "acc", True),         # one slot: a one-wave workgroup
+    ("mxfp4t", 1, 32, 4, 2880, 2880, "f32", "store", False),  # tiled planes: four waves a slot
+    ("mxfp4t", 5, 32, 4, 2880, 2880, "bf16", "acc", True),
+    ("mxfp4t", 3, 8, 3, 96, 192, "f32", "gated", True),       # one scale group: one wave a slot
+    ("mxfp4t", 2, 16, 8, 64, 2880, "f32", "acc", False),      # two waves a slot, six groups each: two batches
 ])
 def test_expert_mv_combine_equals_separate_calls(dev, fmt, T, E, KU, H, FE, xdt, mode, bias):
     """The fused down matvecs + combine equal qmm_moe_expert_mv(dn) then qmm_moe_combine[_gated], bit for bit,
@@ -412,9 +451,11 @@ def test_expert_mv_combine_equals_separate_calls(dev, fmt, T, E, KU, H, FE, xdt,
     from qmm import synth
     ops = _ops()
     rng = np.random.default_rng(T * 131 + E)
-    gfmt = "mxfp4" if fmt == "mxfp4s" else fmt
+    gfmt = "mxfp4" if fmt in ("mxfp4s", "mxfp4t") else fmt
     raw = dev_u8(synth.weights(gfmt, rng, E * H, FE), dev)
-    w, ws = (ops.repack_mxfp4(raw, E * H, FE) if fmt == "mxfp4s" else (raw, None))
+    w, ws = (ops.repack_mxfp4(raw, E * H, FE) if fmt in ("mxfp4s", "mxfp4t") else (raw, None))
+    if fmt == "mxfp4t":
+        w, ws = ops.tile_mxfp4(w, ws, E * H, FE)
     ids = rng.integers(0, E, (T, KU)).astype(np.int32)
     ids[0, 0] = E + 3            # clamped to E - 1
     if KU > 1:
@@ -446,6 +487,9 @@ def test_expert_mv_combine_equals_separate_calls(dev, fmt, T, E, KU, H, FE, xdt,
     ("mxfp4", 2, 8, 2, 160, 96, 2, False, True, "silu", False, False, "bf16"),
     ("q4_0", 4, 4, 4, 128, 64, 1, True, False, "silu", False, False, "bf16"),              # every expert picked
     ("mxfp4s", 1, 1, 1, 64, 32, 3, False, True, "swiglu_oai", False, False, "f32"),       # one expert
+    ("mxfp4t", 1, 32, 4, 2880, 2880, 3, False, True, "swiglu_oai", True, True, "bf16"),   # tiled planes
+    ("mxfp4t", 2, 8, 2, 192, 96, 2, False, False, "silu", False, True, "f32"),            # tiled, two tensors
+    ("mxfp4t", 3, 130, 4, 64, 64, 2, True, True, "silu", True, False, "bf16"),            # three key slots
 ])
 def test_topk_expert_mv_equals_separate_calls(dev, fmt, T, E, KU, H, FE, gating, norm, fused, act, rbias, ebias, xdt):
     """The gate/up expert matvecs that rank their own token's logits give the routing kernel's ids and weights and
@@ -454,14 +498,18 @@ def test_topk_expert_mv_equals_separate_calls(dev, fmt, T, E, KU, H, FE, gating,
     from qmm import synth
     ops = _ops()
     rng = np.random.default_rng(T * 17 + E)
-    gfmt = "mxfp4" if fmt == "mxfp4s" else fmt
+    gfmt = "mxfp4" if fmt in ("mxfp4s", "mxfp4t") else fmt
     rows = E * FE * (2 if fused else 1)
     raw = dev_u8(synth.weights(gfmt, rng, rows, H), dev)
     raw2 = None if fused else dev_u8(synth.weights(gfmt, rng, E * FE, H), dev)
     ws = ws2 = None
-    if fmt == "mxfp4s":
+    if fmt in ("mxfp4s", "mxfp4t"):
         w, ws = ops.repack_mxfp4(raw, rows, H)
         w2, ws2 = ops.repack_mxfp4(raw2, E * FE, H) if raw2 is not None else (None, None)
+        if fmt == "mxfp4t":
+            w, ws = ops.tile_mxfp4(w, ws, rows, H)
+            if w2 is not None:
+                w2, ws2 = ops.tile_mxfp4(w2, ws2, E * FE, H)
     else:
         w, w2 = raw, raw2
     logits = dev_f32(rng.standard_normal((T, E)).astype(np.float32), dev)
@@ -479,3 +527,24 @@ def test_topk_expert_mv_equals_separate_calls(dev, fmt, T, E, KU, H, FE, gating,
     np.testing.assert_array_equal(host(ids), host(ids_w))
     assert_bits_equal(host(wts), host(wts_w), "weights")
     assert_bits_equal(host(a), host(a_w), f"{fmt} act")
+
+
+def test_mxfp4t_decode_multi_token_equals_single_tokens(dev):
+    """The decode chain on MFMA-tiled planes (routing inside the gate/up launch, down + combine in one launch): each
+    token of a five-token call equals the call on that token alone, bit for bit."""
+    import torch
+    from qmm import synth
+    E, KU, H, FE, T = 32, 4, 2880, 2880, 5
+    rng = np.random.default_rng(20261311)
+    ex = Experts(dev, "mxfp4", rng, E, H, FE, True)
+    wfmt, kw = ex.device(split=True, tiled=True)
+    xb = synth.to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32))
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    x, lg = dev_bf16(xb, dev), dev_f32(logits, dev)
+    run = lambda xx, ll: _ops().moe_decode(wfmt, xx, ll, E, KU, H, FE, 3, False, fused=True, act="swiglu_oai",
+                                           q8=False, **kw)[0]
+    y = host(run(x, lg))
+    for t in range(T):
+        yt = host(run(x[t:t + 1].contiguous(), lg[t:t + 1].contiguous()))
+        torch.cuda.synchronize()
+        assert_bits_equal(yt[0], y[t], f"token {t}")

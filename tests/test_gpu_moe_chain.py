@@ -3,7 +3,7 @@ moe_routed, S/gen_llm.py:5324-5385, with moe_alloc's intermediates in a caller-p
 the same kernels as the op-by-op chains (ops.moe_prefill / moe_decode), which are checked against the oracle in
 test_gpu_moe.py and test_gpu_q8_matvecs.py, so its output must equal theirs bit for bit. Cases: the Qwen3-30B-A3B
 shape (Q4_K; prefill at T = 64, decode at T = 4 with f32 and int8 activations, a Q6_K down tensor), the gpt-oss-20b
-shape (MXFP4: tiled planes at T = 256, split planes at T = 1, swiglu_oai, expert biases, down scales), routing from
+shape (MXFP4: tiled planes at T = 256, split or tiled planes at T = 1 and 3, swiglu_oai, expert biases, down scales), routing from
 the router weight, a shared-expert gate, and a workspace one byte short.
 """
 import numpy as np
@@ -43,10 +43,10 @@ def test_chain_equals_op_chain_qwen3_30b_a3b(dev, T, q8, fmt_down, use_router):
     assert_bits_equal(host(y), host(y_ops), f"chain T={T} q8={q8}")
 
 
-@pytest.mark.parametrize("T", [1, 256])
-def test_chain_equals_op_chain_gpt_oss_20b(dev, T):
-    """MXFP4 experts (split planes for decode, MFMA-tiled planes for prefill), swiglu_oai, expert biases, per-expert
-    down scales, gating 3."""
+@pytest.mark.parametrize("T,tiled", [(1, False), (1, True), (3, True), (256, True)])
+def test_chain_equals_op_chain_gpt_oss_20b(dev, T, tiled):
+    """MXFP4 experts (split planes or MFMA-tiled planes for decode, tiled planes for prefill), swiglu_oai, expert
+    biases, per-expert down scales, gating 3."""
     import torch
     import qmm.ops as ops
     from qmm import synth
@@ -56,7 +56,7 @@ def test_chain_equals_op_chain_gpt_oss_20b(dev, T):
     gn, gs = ops.repack_mxfp4(dev_u8(gu, dev), E * 2 * FE, H)
     dnn, ds = ops.repack_mxfp4(dev_u8(dn, dev), E * H, FE)
     fmt = "mxfp4s"
-    if T >= 64:
+    if tiled:
         gn, gs = ops.tile_mxfp4(gn, gs, E * 2 * FE, H)
         dnn, ds = ops.tile_mxfp4(dnn, ds, E * H, FE)
         fmt = "mxfp4t"
