@@ -145,6 +145,9 @@ int qmm_mv_pair_q8(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate
  * QMM_Q6_K, S/gen_gemm.py:369-444) fma_f16(f16(q), f16(d sc), f16(-32 d sc)) with q the unsigned 6-bit code; Q4_0
  * (fmt QMM_Q4_0, the reference's native Q4_0 staging S/moe_q4_0.py:11-38, S/gen_gemm.py:40-45) f16(q - 8) * d with
  * one f16 rounding, i.e. f16(d (q - 8)) for every finite d. MXFP4 weights go through qmm_gemm_mxfp4.
+ * fmt QMM_Q4_KT: Q4_K in the tiled layout of qmm_tile_q4k (the int8 decode GEMV's; n % 16 == 0, K % 512 == 0), the
+ * results equal the QMM_Q4_K call's on the GGUF blocks bit for bit, so one weight copy serves decode and prefill (the
+ * reference's single weight view, S/gen_llm.py:5364-5371).
  * QMM_GEMM_SWIGLU: w is the gate matrix and w2 the up matrix (both [n, k]); silu(g) = g / (1 + e^-g); with
  * fmt = QMM_GATE_UP(gate, up) (Q4_K, Q6_K, Q4_0) the two matrices are in their own formats, g_gemm_{fmt}_{fmt2}_swiglu
  * (S/gen_gemm.py:535-547, :696-700).
@@ -273,8 +276,10 @@ int qmm_moe_expert_mv_tiled(int mode, int fused, int act, int64_t k, int64_t n, 
  *               [x_rows, 2] in x_scales (inv = scales[row, 1]); K % 256 == 0; f16 MFMA, weights staged as
  *               fma_f16(f16(q), f16(d sc), f16(-dmin m)).
  *   QMM_Q4_KT:  as QMM_Q4_K with the weights in the tiled layout of qmm_tile_q4k (each expert's [n, k] tiled as
- *               part of the [E n, k] tensor: n % 16 == 0; K <= 4096), read as contiguous 1 KB streams; the same
- *               staging, the products summed in another order (no counterpart in the reference: a load-time layout).
+ *               part of the [E n, k] tensor: n % 16 == 0): for K <= 4096 read by the narrow kernel as contiguous
+ *               1 KB streams at every row count (the same staging, the products summed in another order), beyond
+ *               that (K % 512 == 0) by the 64-row tile kernel at its tiled addresses, whose results then equal the
+ *               QMM_Q4_K call's bit for bit (no counterpart in the reference: a load-time layout).
  *   QMM_Q6_K:   as QMM_Q4_K with Q6_K weights (staged as qmm_gemm stages them); g_moe_gdn_q6_k of the Q4_K_M
  *               expert layout (Q4_K gate / up, Q6_K down).
  *   QMM_Q4_0:   as QMM_Q4_K with Q4_0 weights, staged f16(d (q - 8)) (specialize_grouped, S/moe_q4_0.py:41-61).

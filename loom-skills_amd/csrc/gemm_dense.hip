@@ -28,6 +28,14 @@
 // 16 h .. 16 h + 15 of a page; K16 step (gl, s2) of the page holds its values 16 h + 8 s2 .. + 7 of sub-block
 // 2 page + gl, i.e. K positions 64 page + 32 gl + 16 h + 8 s2 .. + 7, where the activation fragment is read too.
 // Tiles are dealt XCD-aware: the eight M tiles of an N tile run on one XCD and share its weight columns in L2.
+//
+// Weights in the tiled layout QMM_Q4_KT (qmm_tile_q4k, the decode GEMV's; K % 512 == 0, N % 16 == 0): the lane reads
+// the same 16 code bytes and header, at their tiled addresses. Column c's block of 16 rows starts at (c / 16) 16 RB
+// (RB = K / 256 * 144 bytes a row); super-block sb of its row r = c % 16 is half sb % 2 of unit sb / 2 (4608 bytes):
+// header at 16 (2 r + sb % 2), and code bytes 16 (4 h' + q) .. + 15 in plane q at 512 + 1024 q + 16 (4 r + 2 (sb % 2)
+// + h'). Page p's bytes 16 h .. + 15 are chunk 2 p + h: plane 2 (p % 2) + h, h' = p / 2. So the per-column part of an
+// address is (c / 16) 16 RB + 512 + 1024 h + 64 r (codes) or + 32 r (header), and the rest, (sb / 2) 4608 +
+// 2048 (p % 2) + 32 (sb % 2) + 16 (p / 2) (codes) or (sb / 2) 4608 + 16 (sb % 2) (header), is the same for every lane.
 #include "common.hpp"
 #include "deq_f16.hpp"
 
@@ -71,7 +79,7 @@ __device__ __forceinline__ void header_pairs(const uint4 &hd, u32 (&out)[8]) {
   }
 }
 
-template <bool ACC, bool BF16OUT>
+template <bool ACC, bool BF16OUT, bool TL>
 __global__ __launch_bounds__(kWaves * 64, 1) void q4k_dense_kernel(DArgs a) {
   __shared__ __align__(16) u8 abuf[kWaves][2][kAbuf];   // also the K-part reduction area at the end
   __shared__ __align__(16) u32 stab[kWaves][2][kSlot];
@@ -128,14 +136,21 @@ __global__ __launch_bounds__(kWaves * 64, 1) void q4k_dense_kernel(DArgs a) {
   u32 wv[4], whv[2];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int c = n0 + 32 * j + lc;
-    wv[j] = (u32)(c < N ? c : N - 1) * RB + 16u + 16u * (u32)h;
+    int c = n0 + 32 * j + lc;
+    c = c < N ? c : N - 1;
+    wv[j] = TL ? (u32)(c >> 4) * 16u * RB + 512u + 1024u * (u32)h + 64u * (u32)(c & 15)
+               : (u32)c * RB + 16u + 16u * (u32)h;
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int c = n0 + 64 * j + lane;
-    whv[j] = (u32)(c < N ? c : N - 1) * RB;
+    int c = n0 + 64 * j + lane;
+    c = c < N ? c : N - 1;
+    whv[j] = TL ? (u32)(c >> 4) * 16u * RB + 32u * (u32)(c & 15) : (u32)c * RB;
   }
+  // the lane-independent parts of a super-block's code page and header addresses
+  auto code_at = [&](int sb, int p) { return TL ? (sb >> 1) * 4608 + 2048 * (p & 1) + 32 * (sb & 1) + 16 * (p >> 1)
+                                                : sb * 144 + 32 * p; };
+  auto head_at = [&](int sb) { return TL ? (sb >> 1) * 4608 + 16 * (sb & 1) : sb * 144; };
   auto a_load = [&](u32x4 (&r)[8], int step) __attribute__((always_inline)) {   // step of the wave's range
     int s = sb_lo * 4 + step;
     s = s < 4 * (sbl + 1) ? s : 4 * sbl + 3;
@@ -156,8 +171,8 @@ __global__ __launch_bounds__(kWaves * 64, 1) void q4k_dense_kernel(DArgs a) {
     for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
       for (int p = 0; p < 4; ++p)
-        r[2 * hf + jj][p] = __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)wv[2 * hf + jj], sb * 144 + 32 * p, 0);
-    hd[hf] = __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)whv[hf], sb * 144, 0);
+        r[2 * hf + jj][p] = __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)wv[2 * hf + jj], code_at(sb, p), 0);
+    hd[hf] = __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)whv[hf], head_at(sb), 0);
   };
   typedef __attribute__((ext_vector_type(2))) u32 u32x2;
   // the scale pairs of header half hf (columns 64 hf + lane) into scale slot `slot`, page pages of it
@@ -401,25 +416,27 @@ __global__ __launch_bounds__(kWaves * 64, 1) void q4k_dense_kernel(DArgs a) {
 }
 
 template <bool ACC, bool BF16OUT>
-int launch_dense(const DArgs &a, hipStream_t s) {
+int launch_dense(const DArgs &a, bool tiled, hipStream_t s) {
   const dim3 grid((unsigned)(8 * ((a.tiles_total + 7) / 8)));
-  q4k_dense_kernel<ACC, BF16OUT><<<grid, kWaves * 64, 0, s>>>(a);
+  if (tiled) q4k_dense_kernel<ACC, BF16OUT, true><<<grid, kWaves * 64, 0, s>>>(a);
+  else q4k_dense_kernel<ACC, BF16OUT, false><<<grid, kWaves * 64, 0, s>>>(a);
   return launch_status();
 }
 
 }  // namespace
 
-// The Q4_K store / acc path of qmm_gemm (gemm_q4k.hip validates the arguments): GGUF Q4_K weights, f16 rows.
-int qmm_gemm_q4k_dense(int acc, int64_t rows, int64_t k, int64_t n, const void *x, const float *scales, const void *w,
-                       void *y, int y_bf16, hipStream_t s) {
+// The Q4_K store / acc path of qmm_gemm (gemm_q4k.hip validates the arguments): GGUF Q4_K weights or (tiled) the
+// QMM_Q4_KT layout, f16 rows.
+int qmm_gemm_q4k_dense(int acc, int tiled, int64_t rows, int64_t k, int64_t n, const void *x, const float *scales,
+                       const void *w, void *y, int y_bf16, hipStream_t s) {
   DArgs a{};
   a.M = (int)rows; a.N = (int)n; a.K = (int)k;
   a.x16 = static_cast<const _Float16 *>(x); a.scales = scales;
   a.w = static_cast<const u8 *>(w); a.y = y;
   a.tiles_m = (int)((rows + kBM - 1) / kBM);
   a.tiles_total = a.tiles_m * (int)((n + kBN - 1) / kBN);
-  if (acc && y_bf16) return launch_dense<true, true>(a, s);
-  if (acc) return launch_dense<true, false>(a, s);
-  if (y_bf16) return launch_dense<false, true>(a, s);
-  return launch_dense<false, false>(a, s);
+  if (acc && y_bf16) return launch_dense<true, true>(a, tiled, s);
+  if (acc) return launch_dense<true, false>(a, tiled, s);
+  if (y_bf16) return launch_dense<false, true>(a, tiled, s);
+  return launch_dense<false, false>(a, tiled, s);
 }

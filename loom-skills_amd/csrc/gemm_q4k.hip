@@ -80,13 +80,18 @@ constexpr int kStagedMaxK = 6144;
 
 // WF2: the up matrix's format when it differs from the gate's (kGU / kSwiglu of a QMM_GATE_UP pair): the up waves
 // load and dequantize in their own format, with their own row stride, the gate waves in WF.
-template <int KIND, bool ACC, bool BF16OUT, int DEPTH, bool STAGED, int WF, int KS, int WF2 = WF>
+// TL: Q4_K weights in the tiled layout QMM_Q4_KT (K % 512 == 0, N % 16 == 0): the lane reads the same code bytes and
+// headers at their tiled addresses (column c's 16-row block at (c / 16) 16 RB; super-block sb of its row r = c % 16
+// is half sb % 2 of unit sb / 2 of 4608 bytes: header at 16 (2 r + sb % 2), page p's bytes 16 h .. + 15 in plane
+// 2 (p % 2) + h at 512 + 1024 (2 (p % 2) + h) + 16 (4 r + 2 (sb % 2) + p / 2)), so the results are the GGUF call's.
+template <int KIND, bool ACC, bool BF16OUT, int DEPTH, bool STAGED, int WF, int KS, int WF2 = WF, bool TL = false>
 __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
   constexpr int NT = 128 * KS;   // threads: 2 column halves (or matrices) x KS K-parts
   constexpr bool MIXED = WF2 != WF;
   static_assert(!(WF != kWQ4K && STAGED), "Q6_K / Q4_0 scales are read with the codes");
   constexpr bool kTwoW = KIND == kGU || KIND == kSwiglu;        // two weight matrices (gate, up): wave pairs
   static_assert(!MIXED || (kTwoW && !STAGED), "a second format is the up matrix's of gate/up, scales read with codes");
+  static_assert(!TL || (WF == kWQ4K && !MIXED), "the tiled layout holds Q4_K");
   constexpr bool kDenseRows = KIND == kDense || KIND == kSwiglu;  // rows m0 .. m0 + 63 of x, tiles row-major
   constexpr int BN = kTwoW ? 64 : 128;
   extern __shared__ __align__(16) u32 scl[];   // STAGED: [128 columns][K / 32 + 2] (dsc | nmn << 16)
@@ -185,15 +190,22 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
   } else {
     wbase = a.w + (int64_t)expert * a.ebytes;
   }
-  const u8 *wcol[2];
+  const u8 *wcol[2];   // GGUF: the column's row; tiled: its 16-row block
+  int tco[2], tho[2];  // tiled: the column's code and header offsets in a unit
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     int c = n0 + (kTwoW ? 0 : sel * 64) + 32 * j + lc;
     c = c < N ? c : N - 1;
-    wcol[j] = wbase + (int64_t)c * RB;
+    wcol[j] = TL ? wbase + (int64_t)(c >> 4) * 16 * RB : wbase + (int64_t)c * RB;
+    tco[j] = 512 + 1024 * h + 64 * (c & 15);
+    tho[j] = 32 * (c & 15);
   }
   auto b_code = [&](int j, int s) -> uint4 {
     const int gs = kh * S0 + (s < S0 ? s : S0 - 1);
+    if constexpr (TL) {
+      const int sb = gs >> 2, p = gs & 3;
+      return ld16(wcol[j] + tco[j] + (int64_t)(sb >> 1) * 4608 + 2048 * (p & 1) + 32 * (sb & 1) + 16 * (p >> 1));
+    }
     return ld16(wcol[j] + (int64_t)(gs >> 2) * 144 + 16 + 32 * (gs & 3) + 16 * h);
   };
   // Q6_K page gs & 3 = (half, jh): groups j = 2 jh (ql bytes 64 half + l) and 2 jh + 1 (64 half + 32 + l), both with
@@ -216,7 +228,9 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
     dd = *reinterpret_cast<const u16 *>(blk);
   };
   auto b_head = [&](int j, int s) -> uint4 {
-    return ld16(wcol[j] + (int64_t)((kh * S0 + (s < S0 ? s : S0 - 1)) >> 2) * 144);
+    const int sb = (kh * S0 + (s < S0 ? s : S0 - 1)) >> 2;
+    if constexpr (TL) return ld16(wcol[j] + tho[j] + (int64_t)(sb >> 1) * 4608 + 16 * (sb & 1));
+    return ld16(wcol[j] + (int64_t)sb * 144);
   };
   // sub-blocks per column, and the staged table's row pitch in dwords: two more than K / 32 (a multiple of 8), so
   // the 32 columns a wave reads at once start two banks apart instead of all in one bank
@@ -245,7 +259,8 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
         }
         int c = n0 + (kTwoW ? cl - 64 * msel : cl);
         c = c < N ? c : N - 1;
-        hd[q] = ld16(mb + (int64_t)c * RB + (int64_t)b * 144);
+        hd[q] = TL ? ld16(mb + (int64_t)(c >> 4) * 16 * RB + 32 * (c & 15) + (int64_t)(b >> 1) * 4608 + 16 * (b & 1))
+                   : ld16(mb + (int64_t)c * RB + (int64_t)b * 144);
       }
 #pragma unroll
       for (int q = 0; q < kHdrBatch; ++q) {
@@ -497,7 +512,7 @@ __global__ __launch_bounds__(128 * KS, 1) void q4k_mfma_kernel(Args a) {
 // has two waves a SIMD, so one wave's dequantization overlaps the other's MFMAs (the grid of a 512-row GEMM is one
 // workgroup a CU). The grouped GEMMs keep two K-parts (their expert tiles are many and their K short), and so does
 // Q6_K.
-template <int KIND, bool ACC, bool BF16OUT, int WF = kWQ4K>
+template <int KIND, bool ACC, bool BF16OUT, int WF = kWQ4K, bool TL = false>
 int launch(const Args &a, hipStream_t s) {
   constexpr bool kDenseRows = KIND == kDense || KIND == kSwiglu;
   constexpr int KS = kDenseRows && WF != kWQ6K ? 4 : 2;   // Q6_K's wider rings would spill at two waves a SIMD
@@ -512,13 +527,14 @@ int launch(const Args &a, hipStream_t s) {
     const size_t dyn = (size_t)128 * (a.K / 32 + 2) * 4;
     if (dyn > 32768) {   // beyond the default dynamic LDS limit: raised to the largest table this kernel stages
       static std::atomic<unsigned> raised{0};
-      if (int st = raise_dyn_lds(reinterpret_cast<const void *>(&q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, true, kWQ4K, KS>),
-                                 (int)((size_t)128 * (kMaxK / 32 + 2) * 4), raised))
+      if (int st = raise_dyn_lds(
+              reinterpret_cast<const void *>(&q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, true, kWQ4K, KS, kWQ4K, TL>),
+              (int)((size_t)128 * (kMaxK / 32 + 2) * 4), raised))
         return st;
     }
-    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, true, kWQ4K, KS><<<grid, 128 * KS, dyn, s>>>(a);
+    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, true, kWQ4K, KS, kWQ4K, TL><<<grid, 128 * KS, dyn, s>>>(a);
   } else {
-    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, false, kWQ4K, KS><<<grid, 128 * KS, 0, s>>>(a);
+    q4k_mfma_kernel<KIND, ACC, BF16OUT, kDepth, false, kWQ4K, KS, kWQ4K, TL><<<grid, 128 * KS, 0, s>>>(a);
   }
   return launch_status();
 }
@@ -528,6 +544,7 @@ template <int KIND, bool ACC, bool BF16OUT>
 int launch_fmt(int fmt, const Args &a, hipStream_t s) {
   if (fmt == QMM_Q6_K) return launch<KIND, ACC, BF16OUT, kWQ6K>(a, s);
   if (fmt == QMM_Q4_0) return launch<KIND, ACC, BF16OUT, kWQ40>(a, s);
+  if (fmt == QMM_Q4_KT) return launch<KIND, ACC, BF16OUT, kWQ4K, true>(a, s);
   return launch<KIND, ACC, BF16OUT, kWQ4K>(a, s);
 }
 
@@ -566,9 +583,9 @@ int fmt_align(int fmt) { return fmt == QMM_Q4_K || fmt == QMM_Q4_KT ? 16 : fmt =
 
 }  // namespace
 
-// the dense Q4_K GEMM (gemm_dense.hip): store / acc modes
-int qmm_gemm_q4k_dense(int acc, int64_t rows, int64_t k, int64_t n, const void *x, const float *scales, const void *w,
-                       void *y, int y_bf16, hipStream_t s);
+// the dense Q4_K GEMM (gemm_dense.hip): store / acc modes, GGUF or tiled weights
+int qmm_gemm_q4k_dense(int acc, int tiled, int64_t rows, int64_t k, int64_t n, const void *x, const float *scales,
+                       const void *w, void *y, int y_bf16, hipStream_t s);
 
 extern "C" int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, const void *x, int x_dtype,
                         const float *scales, const void *w, const void *w2, void *y, int y_dtype,
@@ -577,14 +594,16 @@ extern "C" int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, c
   const int fu = fmt_up(fmt);   // QMM_GATE_UP(gate, up): the up matrix of the swiglu mode in its own format
   const bool mixed = fmt_mixed(fmt);
   fmt = fmt_gate(fmt);
-  if (mixed && (mode != QMM_GEMM_SWIGLU || !gguf_gemm_fmt(fu))) return QMM_ERR_FORMAT;
-  if (fmt != QMM_Q4_K && fmt != QMM_Q6_K && fmt != QMM_Q4_0) return QMM_ERR_FORMAT;   // MXFP4: qmm_gemm_mxfp4
+  if (mixed && (mode != QMM_GEMM_SWIGLU || !gguf_gemm_fmt(fmt) || !gguf_gemm_fmt(fu))) return QMM_ERR_FORMAT;
+  const bool tiled = fmt == QMM_Q4_KT;   // the decode GEMV's tiled Q4_K: one weight copy for decode and prefill
+  if (!gguf_gemm_fmt(fmt) && !tiled) return QMM_ERR_FORMAT;   // MXFP4: qmm_gemm_mxfp4
   if (mode != QMM_GEMM_STORE && mode != QMM_GEMM_ACC && mode != QMM_GEMM_SWIGLU) return QMM_ERR_RANGE;
   if (!x || !w || !y || (mode == QMM_GEMM_SWIGLU && !w2)) return QMM_ERR_NULL;
   if (x_dtype != QMM_F16) return QMM_ERR_DTYPE;   // bf16 / f32 rows go through qmm_row_scale_f16 first
   if (y_dtype != QMM_F32 && y_dtype != QMM_BF16) return QMM_ERR_DTYPE;
   if (rows <= 0 || n <= 0 || k <= 0 || k % 256) return QMM_ERR_SHAPE;
   if (rows > (1 << 24) || n > (1 << 24) || k > (1 << 20)) return QMM_ERR_SHAPE;
+  if (tiled && (n % 16 || k % 512)) return QMM_ERR_SHAPE;   // whole 16-row blocks of whole 512-value units
   const int wal = fmt_align(fmt);
   if (!aligned(x, 16) || !aligned(w, wal) || !aligned(y, 4) || (w2 && !aligned(w2, fmt_align(fu))))
     return QMM_ERR_ALIGN;
@@ -603,7 +622,7 @@ extern "C" int qmm_gemm(int fmt, int mode, int64_t rows, int64_t k, int64_t n, c
     if (mixed) return bf ? launch_mixed<kSwiglu, true>(fmt, fu, a, s) : launch_mixed<kSwiglu, false>(fmt, fu, a, s);
     return bf ? launch_fmt<kSwiglu, false, true>(fmt, a, s) : launch_fmt<kSwiglu, false, false>(fmt, a, s);
   }
-  if (fmt == QMM_Q4_K) return qmm_gemm_q4k_dense(acc, rows, k, n, x, scales, w, y, bf, s);
+  if (fmt == QMM_Q4_K || tiled) return qmm_gemm_q4k_dense(acc, tiled, rows, k, n, x, scales, w, y, bf, s);
   a.tiles_total = a.tiles_m * (int)((n + 127) / 128);
   if (acc && bf) return launch_fmt<kDense, true, true>(fmt, a, s);
   if (acc) return launch_fmt<kDense, true, false>(fmt, a, s);
@@ -650,16 +669,19 @@ int qmm_grouped_q4k(int fmt, int mode, int fused, int act, int64_t max_tiles, in
   }
   const int wal = fmt_align(fmt);
   if (!aligned(x, 16) || !aligned(w, wal) || (w2 && !aligned(w2, wal))) return QMM_ERR_ALIGN;
-  // The tiled layout is read by the narrow kernel only. GGUF Q4_K with few rows an expert (max_tiles = assignments /
-  // 64 + E, so 64 (max_tiles - E) bounds the assignments): the narrow kernel too, which streams each expert's
-  // weights once against 16-row groups held in LDS.
-  if (fmt == QMM_Q4_KT) {
-    if (!qmm_grouped_narrow_fits(k, n)) return QMM_ERR_SHAPE;
+  // The tiled layout: the narrow kernel wherever it fits (at every batch size, so a token's output does not depend
+  // on the batch), else (K beyond the narrow kernel's LDS rows) the 64-row tile kernel, which reads it in whole units
+  // (K % 512 == 0, n % 16 == 0). GGUF Q4_K with few rows an expert (max_tiles = assignments / 64 + E, so
+  // 64 (max_tiles - E) bounds the assignments): the narrow kernel too, which streams each expert's weights once
+  // against 16-row groups held in LDS.
+  const bool narrow = qmm_grouped_narrow_fits(k, n);
+  if (fmt == QMM_Q4_KT && (narrow || k % 512 || n % 16)) {
+    if (!narrow) return QMM_ERR_SHAPE;
     if (!aligned(y, 16)) return QMM_ERR_ALIGN;
     return qmm_grouped_q4k_narrow(1, mode, fused, act, max_tiles, k, n, E, KU, tile_info, rowmap, x, x_scales, x_rows,
                                   w, w2, bias, bias2, y, s);
   }
-  if (fmt == QMM_Q4_K && qmm_grouped_narrow_fits(k, n) && aligned(y, 16) && 64 * (max_tiles - E) <= kNarrowRowsPerExpert * E)
+  if (fmt == QMM_Q4_K && narrow && aligned(y, 16) && 64 * (max_tiles - E) <= kNarrowRowsPerExpert * E)
     return qmm_grouped_q4k_narrow(0, mode, fused, act, max_tiles, k, n, E, KU, tile_info, rowmap, x, x_scales, x_rows,
                                   w, w2, bias, bias2, y, s);
   const int64_t RB = fmt_row_bytes(fmt, k);

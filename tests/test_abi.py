@@ -187,6 +187,10 @@ def test_argument_validation_without_a_device(lib):
     assert lib.qmm_mv_q8(5, 768, 16, 1, 0, fake, 2, fake, fake, n) == st["QMM_ERR_SHAPE"]      # K % 512
     assert lib.qmm_mv_q8(5, 512 * 37, 16, 1, 0, fake, 2, fake, fake, n) == st["QMM_ERR_SHAPE"]  # 37 slices
     assert lib.qmm_dequant(5, fake, n, 16, 640, fake, n) == st["QMM_ERR_SHAPE"]
+    # the prefill GEMM on tiled Q4_K: whole 16-row blocks and 512-value units; no QMM_GATE_UP pair with a tiled gate
+    assert lib.qmm_gemm(5, 0, 64, 4096, 24, fake, 1, n, fake, n, fake, 0, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_gemm(5, 0, 64, 768, 32, fake, 1, n, fake, n, fake, 0, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_gemm(5 | (7 << 8), 2, 64, 4096, 32, fake, 1, n, fake, fake, fake, 0, n) == st["QMM_ERR_FORMAT"]
     # tiled Q4_0: whole 16-row blocks and 512-value units only
     assert lib.qmm_tile_q40(fake, 24, 512, fake, n) == st["QMM_ERR_SHAPE"]
     assert lib.qmm_tile_q40(fake, 16, 768, fake, n) == st["QMM_ERR_SHAPE"]

@@ -196,3 +196,42 @@ def test_gemm_skip_padding(dev):
     assert_close_rel_l2(yh[live], want[live], 1e-3, "live rows")
     assert np.all(yh[64:128] == 7.0), "the padding-only tile was written"
     assert np.all(yh[192 + 40:] == 0.0), "padding rows of a live tile are not zero"
+
+
+# --------------------------------------------------------------------------- one Q4_K weight copy: the tiled layout
+@pytest.mark.parametrize("M,N,K,mode,out", [
+    (512, 4096, 4096, "store", "bf16"),    # Qwen3-8B o_proj, the workload's shape
+    (70, 208, 1536, "acc", "f32"),         # partial row / column tiles, three units a row
+    (130, 384, 512, "store", "f32"),       # one unit: waves without super-blocks
+    (64, 256, 12288, "store", "f32"),      # K beyond the staged scale table
+])
+def test_gemm_tiled_layout_equals_gguf(dev, M, N, K, mode, out):
+    """The prefill GEMM on the decode GEMV's tiled layout (qmm_tile_q4k) equals the GGUF-layout call bit for bit: a
+    model keeps one Q4_K copy for decode and prefill (the reference's single weight view, S/gen_llm.py:5364-5371)."""
+    import torch
+    import qmm.ops as ops
+    wt, xt, want, _, _ = _case(dev, M, N, K, seed=M * 7 + K)
+    tiled = ops.tile_q4k(wt, N, K)
+    od = torch.bfloat16 if out == "bf16" else torch.float32
+    y0 = None if mode == "store" else dev_f32(np.random.default_rng(3).standard_normal((M, N)).astype(np.float32), dev)
+    yg = ops.gemm("q4_k", mode, xt, wt, N, K, out_dtype=od, y=None if y0 is None else y0.clone())
+    yt = ops.gemm("q4_kt", mode, xt, tiled, N, K, out_dtype=od, y=None if y0 is None else y0.clone())
+    torch.cuda.synchronize()
+    assert torch.equal(yg.view(torch.int16) if out == "bf16" else yg.view(torch.int32),
+                       yt.view(torch.int16) if out == "bf16" else yt.view(torch.int32)), f"{M}x{N}x{K} {mode}"
+    if mode == "store" and out == "f32":
+        _check(host(yt), want, f"tiled gemm {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 12288, 4096), (70, 208, 1024)])
+def test_gemm_swiglu_tiled_layout_equals_gguf(dev, M, N, K):
+    """silu(X Wg^T) (X Wu^T) on tiled gate / up weights equals the GGUF-layout call bit for bit."""
+    import torch
+    import qmm.ops as ops
+    from qmm import synth
+    wg, xt, _, _, _ = _case(dev, M, N, K, seed=M + 11)
+    wu = dev_u8(synth.q4_k_weights(np.random.default_rng(M + 12), N, K), dev)
+    yg = ops.gemm("q4_k", "swiglu", xt, wg, N, K, w2=wu)
+    yt = ops.gemm("q4_kt", "swiglu", xt, ops.tile_q4k(wg, N, K), N, K, w2=ops.tile_q4k(wu, N, K))
+    torch.cuda.synchronize()
+    assert torch.equal(yg.view(torch.int32), yt.view(torch.int32)), f"swiglu {M}x{N}x{K}"

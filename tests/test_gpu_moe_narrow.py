@@ -155,3 +155,36 @@ def test_tiled_many_rows_equal_batches(dev):
     ti = host(mid["tile_info"])
     assert ti[:, 1].max() > 32, "no tile with three row groups"
     np.testing.assert_array_equal(host(big)[lo:lo + T].view(np.uint32), host(small).view(np.uint32))
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_tiled_grouped_gate_up_beyond_narrow_k_equals_gguf(dev, fused):
+    """Gate/up of K = 5120 (beyond the narrow kernel's LDS rows) on the tiled layout takes the 64-row tile kernel at
+    the tiled addresses, as the GGUF blocks do: the two grouped GEMMs are equal bit for bit, and the tiled chain
+    matches the oracle within rel-L2 1e-3."""
+    import torch
+    from qmm import synth
+    ops = _ops()
+    E_, KU_, H_, FE_, T_ = 8, 2, 5120, 512, 96
+    rng = np.random.default_rng(20261260 + fused)
+    ex = Experts(dev, "q4_k", rng, E_, H_, FE_, fused)
+    xb = synth.to_bf16_bits(rng.standard_normal((T_, H_)).astype(np.float32))
+    logits = rng.standard_normal((T_, E_)).astype(np.float32)
+    x, lg = dev_bf16(xb, dev), dev_f32(logits, dev)
+    gfmt, gkw = ex.device(split=True, tiled=False)
+    tfmt, tkw = ex.device(split=True, tiled=True)
+    _, mid = ops.moe_prefill(gfmt, x, lg, E_, KU_, H_, FE_, 1, True, fused=fused, act="silu", **gkw)
+    x16, xs = ops.row_scale_f16(x)
+    outs = []
+    rows = mid["tile_info"].shape[0] * 64
+    for fmt, kw in ((gfmt, gkw), (tfmt, tkw)):   # rows without an assignment keep the NaN sentinel in both
+        yy = torch.full((rows, FE_), float("nan"), device=dev)
+        outs.append(host(ops.moe_grouped(fmt, "gu", mid["tile_info"], mid["rowmap"], x16, kw["w_gate"], FE_, H_, E_,
+                                         KU_, w2=kw.get("w_up"), x_scales=xs, fused=fused, act="silu", y=yy)))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(outs[1].view(np.uint32), outs[0].view(np.uint32))
+    y, _ = ops.moe_prefill(tfmt, x, lg, E_, KU_, H_, FE_, 1, True, fused=fused, act="silu", **tkw)
+    eids, ewts = ref.route(logits, KU_, 1, True)
+    want, _ = ref.moe(synth.bf16_bits_to_f32(xb), eids, ewts, ex.gate_up, ex.down, act="silu", x_round=ref.f16_rows,
+                      act_round=ref.f16_rows)
+    assert_close_rel_l2(host(y), want, 1e-3, f"tiled chain, K = 5120, fused={fused}")
