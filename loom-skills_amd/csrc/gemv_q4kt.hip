@@ -96,7 +96,10 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mv_q4kt_q8_kernel(int64_t n, i
                                                                    float *__restrict__ y, float *__restrict__ y2) {
   constexpr int SLICE = 512 * U, NG = SLICE / 32;   // values / Q8 groups of a wave
   constexpr int NM = MODE == kPlain ? 1 : 2;        // weight matrices streamed
-  __shared__ __align__(16) u32 xc[kMaxWaves][TG][SLICE / 4];
+  // the codes of a token's slice, four dwords of padding after every 32 (pidx): the four lane classes (super-block
+  // half sb, h) read fragments 32 dwords apart, which would sit in the same LDS banks
+  __shared__ __align__(16) u32 xc[kMaxWaves][TG][SLICE / 4 + SLICE / 32];
+  auto pidx = [](int d) { return d + 4 * (d >> 5); };
   __shared__ __align__(16) float xm[kMaxWaves][TG][NG][2];
   __shared__ float red[kMaxWaves][NM][16][TG];
 
@@ -151,12 +154,12 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mv_q4kt_q8_kernel(int64_t n, i
         u32 c0, c1;
         float d16, sum;
         q8_group(xv[t][j], c0, c1, d16, sum);
-        xc[wave][t][2 * c] = c0;
-        xc[wave][t][2 * c + 1] = c1;
+        xc[wave][t][pidx(2 * c)] = c0;
+        xc[wave][t][pidx(2 * c) + 1] = c1;
         if ((c & 3) == 0) { xm[wave][t][c >> 2][0] = d16; xm[wave][t][c >> 2][1] = sum; }
       } else {
-        xc[wave][t][2 * c] = qv[t][j].x;
-        xc[wave][t][2 * c + 1] = qv[t][j].y;
+        xc[wave][t][pidx(2 * c)] = qv[t][j].x;
+        xc[wave][t][pidx(2 * c) + 1] = qv[t][j].y;
       }
     }
     if constexpr (!STAGEQ) {
@@ -173,8 +176,8 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mv_q4kt_q8_kernel(int64_t n, i
     const int g0 = 16 * u + 8 * sb + 4 * h;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const v4u p0 = *reinterpret_cast<const v4u *>(&xc[wave][t][8 * (g0 + g)]);
-      const v4u p1 = *reinterpret_cast<const v4u *>(&xc[wave][t][8 * (g0 + g) + 4]);
+      const v4u p0 = *reinterpret_cast<const v4u *>(&xc[wave][t][pidx(8 * (g0 + g))]);
+      const v4u p1 = *reinterpret_cast<const v4u *>(&xc[wave][t][pidx(8 * (g0 + g)) + 4]);
       xa[g][0] = p0.x; xa[g][1] = p0.y; xa[g][2] = p0.z; xa[g][3] = p0.w;
       xa[g][4] = p1.x; xa[g][5] = p1.y; xa[g][6] = p1.z; xa[g][7] = p1.w;
       md[g] = xm[wave][t][g0 + g][0];
