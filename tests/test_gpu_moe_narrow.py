@@ -8,12 +8,16 @@ weights, with the f16 row rounding of the prefill path applied to the hidden row
 (make_kernel_tests.py:3194-3196); the MoE output must match within rel-L2 1e-3. Cases: the workload shape with a
 fused gate_up tensor, swiglu_oai and the gpt-oss expert biases (S/gen_moe.py:958-1007); an expert holding all 64
 tokens of the batch (four 16-row groups of one tile) and one holding 20 (two groups, the second partly dead); and the
-grouped GEMMs alone on sentinel-filled outputs, whose rows without an assignment must stay untouched.
+grouped GEMMs alone on sentinel-filled outputs, whose rows without an assignment must stay untouched. Small shapes
+cover one and two experts a token, gate/up K of 256 (tiled: a half unit only), 768 and 1280, down K of 256 and 1280,
+and a down GEMM of 48 output columns called directly; the tiled layout beyond the narrow kernel's K (5120) goes to
+the 64-row tile kernel, whose results equal the GGUF layout's bit for bit.
 """
 import numpy as np
 import pytest
 
-from helpers import assert_close_rel_l2, dev_bf16, dev_f32, host
+from helpers import assert_close_rel_l2, dev_bf16, dev_f32, dev_u8, host
+from oracle import formats as of
 from oracle import ref
 from test_gpu_moe import Experts
 
@@ -188,3 +192,56 @@ def test_tiled_grouped_gate_up_beyond_narrow_k_equals_gguf(dev, fused):
     want, _ = ref.moe(synth.bf16_bits_to_f32(xb), eids, ewts, ex.gate_up, ex.down, act="silu", x_round=ref.f16_rows,
                       act_round=ref.f16_rows)
     assert_close_rel_l2(host(y), want, 1e-3, f"tiled chain, K = 5120, fused={fused}")
+
+
+@LAYOUTS
+@pytest.mark.parametrize("KU_,H_,FE_,fused", [(1, 256, 1280, False), (2, 1280, 256, True), (2, 768, 512, False)])
+def test_narrow_small_shapes(dev, tiled, KU_, H_, FE_, fused):
+    """The narrow kernels at the shapes the workload does not reach: one and two experts a token (KU = 1, 2), gate/up
+    K of 256 (tiled: a half unit only), 768 and 1280 (GGUF: step loops whose K / 128 is not a multiple of four), and
+    down K of 256 and 1280; a few rows an expert (16 tokens over 8 experts) keep both layouts on the narrow kernels."""
+    from qmm import synth
+    E_, T_ = 8, 16
+    rng = np.random.default_rng(20261280 + KU_ + H_)
+    ex = Experts(dev, "q4_k", rng, E_, H_, FE_, fused)
+    xb = synth.to_bf16_bits(rng.standard_normal((T_, H_)).astype(np.float32))
+    logits = rng.standard_normal((T_, E_)).astype(np.float32)
+    wfmt, kw = ex.device(split=True, tiled=tiled)
+    y, mid = _ops().moe_prefill(wfmt, dev_bf16(xb, dev), dev_f32(logits, dev), E_, KU_, H_, FE_, 1, True,
+                                fused=fused, act="silu", **kw)
+    eids, ewts = ref.route(logits, KU_, 1, True)
+    np.testing.assert_array_equal(host(mid["ids"]), eids)
+    want, _ = ref.moe(synth.bf16_bits_to_f32(xb), eids, ewts, ex.gate_up, ex.down, act="silu", x_round=ref.f16_rows,
+                      act_round=ref.f16_rows)
+    assert_close_rel_l2(host(y), want, 1e-3, f"narrow KU={KU_} H={H_} FE={FE_} fused={fused}")
+
+
+@LAYOUTS
+def test_narrow_down_gemm_alone_n48(dev, tiled):
+    """A down GEMM called directly with n = 48 output columns (a second 16-column group clamped into the first block's
+    columns) on a NaN-filled output: live rows equal the oracle's, dead rows stay NaN."""
+    import torch
+    from qmm import synth
+    ops = _ops()
+    E_, KU_, H_, FE_, T_ = 8, 2, 48, 512, 24
+    rng = np.random.default_rng(20261290)
+    d = synth.q4_k_weights(rng, E_ * H_, FE_)   # the down tensor [E, 48, 512]
+    wd = ops.tile_q4k(dev_u8(d, dev), E_ * H_, FE_) if tiled else dev_u8(d, dev)
+    ids, _ = ops.moe_topk(dev_f32(rng.standard_normal((T_, E_)).astype(np.float32), dev), KU_, 1, True)
+    ti, rm, _ = ops.moe_bucket(ids, E_)
+    rows = ti.shape[0] * 64
+    a = dev_f32(rng.standard_normal((rows, FE_)).astype(np.float32), dev)
+    a16, as_ = ops.row_scale_f16(a, tile_info=ti)
+    ys = torch.full((rows, H_), float("nan"), dtype=torch.float32, device=dev)
+    ops.moe_grouped("q4_kt" if tiled else "q4_k", "dn", ti, rm, a16, wd, H_, FE_, E_, KU_, x_scales=as_, y=ys)
+    torch.cuda.synchronize()
+    rmh, idh, ysh, ah = host(rm), host(ids).reshape(-1), host(ys), host(a)
+    live = rmh >= 0
+    assert np.all(np.isnan(ysh[~live])), "rows without an assignment were written"
+    rb = of.row_bytes("q4_k", FE_)
+    want = np.zeros((rows, H_))
+    for e in np.unique(idh):
+        r = np.flatnonzero(live & (idh[np.maximum(rmh, 0)] == e))
+        We = of.dequantize("q4_k", d[e * H_ * rb:(e + 1) * H_ * rb], H_, FE_)
+        want[r] = ref.f16_rows(ah[r]) @ We.T.astype(np.float64)
+    assert_close_rel_l2(ysh[live], want[live], 1e-3, "down rows, n = 48")
