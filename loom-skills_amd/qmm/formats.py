@@ -3,6 +3,7 @@
 Mirrors the reference's format table (skills/loom-port-llm/starter/formats.py:5-19, FMT / SB / SPLIT / SCALE_DIV)
 for the formats this library decodes. The integer codes are this library's own (include/qmm.h, enum qmm_format).
 """
+import os
 
 # mxfp4t: MXFP4 in MFMA-tiled planes (this library's load-time layout for the grouped GEMM, qmm_tile_mxfp4)
 # q4_kt / q4_0t: Q4_K / Q4_0 in the lane-ordered tiled layout of the int8-activation decode GEMV (qmm_tile_q4k /
@@ -52,3 +53,19 @@ def scale_row_bytes(fmt, k):
     if fmt == "mxfp4t":
         return (k // 64 + 3) // 4 * 8
     return row_bytes(fmt, k) // SCALE_DIV[fmt] if fmt in SPLIT else 0
+
+
+def _opt_in(name):
+    return os.environ.get(name, "0").strip().lower() not in ("", "0", "false", "no", "off")
+
+
+# The formats whose decode takes int8 (Q8_1) activations by default: the reference's formats.ICODES (S/formats.py:20-30)
+# restricted to the formats here. Q4_K and Q6_K always; Q4_0 only with Q4_0_Q8=1, the reference's own opt-in switch
+# (llama.cpp's vec_dot_q4_0_q8_1 arithmetic); the tiled layouts follow their format, except that the tiled Q4_0 layout
+# has no other decode kernel than the int8 one.
+ICODES = frozenset({"q4_k", "q6_k"} | ({"q4_0"} if _opt_in("Q4_0_Q8") else set()))
+
+
+def decode_q8(fmt):
+    """Whether the decode matvecs of weight format `fmt` take int8 activations by default (see ICODES)."""
+    return fmt in ICODES or fmt == "q4_kt" or fmt == "q4_0t"

@@ -39,7 +39,7 @@ import weakref
 import torch
 
 from . import _lib
-from .formats import ACT, CODE, DTYPE, GEMM_MODE, MX_BLOCK, SPLIT, gate_format, row_bytes
+from .formats import ACT, CODE, DTYPE, GEMM_MODE, ICODES, MX_BLOCK, SPLIT, decode_q8, gate_format, row_bytes
 
 TILE = 64
 
@@ -626,14 +626,15 @@ def moe_prefill(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up
     return y, mid
 
 
-Q8_FORMATS = ("q4_0", "q4_k", "q6_k")   # formats with integer-code expert matvecs (gen_llm ICODES)
+Q8_FORMATS = ("q4_0", "q4_k", "q6_k")   # formats with integer-code expert matvecs (the kernels exist)
 
 
 def _moe_q8(q8, fmt, fmt_down, expert_bias):
     """Whether a decode chain takes int8 activations: "auto" as the reference decides it (MOE_Q8 on by default,
-    moe_iq S/gen_llm.py:5296-5303: integer codes in both formats, no expert biases), else the caller's choice."""
+    moe_iq S/gen_llm.py:5296-5303: both formats in its default int8 set ICODES -- Q4_K, Q6_K; Q4_0 with Q4_0_Q8=1 --
+    and no expert biases), else the caller's choice (q8=True for any of Q8_FORMATS)."""
     if q8 == "auto":
-        return fmt in Q8_FORMATS and fmt_down in Q8_FORMATS and expert_bias is None
+        return fmt in ICODES and fmt_down in ICODES and expert_bias is None
     return bool(q8)
 # The decode chain routes inside its gate/up matvecs (every workgroup ranks its token's logits itself) where that is
 # cheaper than a routing launch: one key slot a lane and few assignments (gpt-oss-20b at one token: 25.0 -> 23.9 us;
@@ -689,17 +690,18 @@ def moe_decode(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=
 GEMM_MIN_TOKENS = 64   # %gemm: epochs of 64+ tokens take the GEMM / grouped chain (S/gen_llm.py:6107-6126)
 
 
-# formats whose decode matvecs contract integer weight codes with Q8_1 activations (IQ_FMTS, S/gen_llm.py:514-519)
+# formats with int8-activation decode matvecs (their kernels exist); linear takes them by default for decode_q8(fmt)
 LINEAR_Q8_FORMATS = ("q4_0", "q4_k", "q4_kt", "q6_k", "q4_0t")
 
 
-def linear(fmt, x, w, n, k, y=None, mode="store", ws=None, w2=None, ws2=None, q8=True):
+def linear(fmt, x, w, n, k, y=None, mode="store", ws=None, w2=None, ws2=None, q8="auto"):
     """Projection y (+)= x W^T, or swiglu y = silu(x W^T) (x W2^T), with the reference's per-epoch choice (linear,
     S/gen_llm.py:4568-4625): the prefill GEMM for 64+ tokens (GGUF q4_k / q6_k / q4_0 on the f16 MFMA, the activation
     row-scaled to f16 first; MXFP4 on the scaled MFMA, the activation quantized to MXFP8 first -- GGUF mxfp4 blocks
-    go through split_planes, repacked once per weight tensor), else the decode GEMV. The decode GEMV of a format with
-    integer codes (q4_0, q4_k, q4_kt, q6_k, q4_0t) takes Q8_1 activations, as the reference does by default (ACT_Q8,
-    iq = ACT_Q8 and fmt in IQ_FMTS and K / 32 <= 1024, S/gen_llm.py:514-519, :4590); q8=False keeps f32 / bf16
+    go through split_planes, repacked once per weight tensor), else the decode GEMV. The decode GEMV takes Q8_1
+    activations where the reference does by default (ACT_Q8, iq = ACT_Q8 and fmt in IQ_FMTS and K / 32 <= 1024,
+    S/gen_llm.py:514-519, :4590): Q4_K and Q6_K (and the tiled q4_kt), Q4_0 with the reference's Q4_0_Q8=1 switch,
+    and the tiled q4_0t always (formats.decode_q8); q8=True also takes it for q4_0; q8=False keeps f32 / bf16
     activations (ACT_Q8=0). y is f32."""
     if mode not in ("store", "acc", "swiglu"):
         raise ValueError(f"linear mode {mode}")
@@ -712,7 +714,8 @@ def linear(fmt, x, w, n, k, y=None, mode="store", ws=None, w2=None, ws2=None, q8
         if fmt in ("q4_k", "q4_kt", "q6_k", "q4_0", "mxfp4s", "mxfp4t"):
             return gemm(fmt, mode, x, w, n, k, w2=w2, y=y, ws=ws, ws2=ws2)
         raise ValueError(f"no prefill GEMM reads {fmt} weights")
-    if q8 and fmt in LINEAR_Q8_FORMATS and k // 32 <= 1024:
+    iq = decode_q8(fmt) if q8 == "auto" else bool(q8) and fmt in LINEAR_Q8_FORMATS
+    if iq and k // 32 <= 1024:
         if mode == "swiglu":
             return mv_swiglu_q8(fmt, w, w2, x, n, k, y=y)
         return mv_q8(fmt, w, x, n, k, y=y, accumulate=mode == "acc")
@@ -780,7 +783,7 @@ def moe_layer(fmt, x, logits, E, KU, H, FE, gating, norm, shared=None, **kw):
     if shared is None:
         return moe_routed(fmt, x, logits, E, KU, H, FE, gating, norm, **kw)
     FS, sf = shared["FS"], shared["fmt"]
-    q8 = kw.get("q8", "auto") is not False   # the shared experts' matvecs follow the routed chain's activations
+    q8 = kw.get("q8", "auto")   # the shared experts' matvecs follow the routed chain's choice of activations
     f = linear(sf, x, shared["w_gate"], FS, H, mode="swiglu", w2=shared["w_up"], q8=q8)
     y = linear(shared.get("fmt_down", sf), f, shared["w_down"], H, FS, q8=q8)
     sg = moe_shared_gate(x, shared["gate"]) if shared.get("gate") is not None else None

@@ -341,3 +341,24 @@ def test_python_surface_refuses_host_tensors():
     from qmm import ops
     with pytest.raises(ValueError):
         ops.mv("q4_k", torch.zeros(144, dtype=torch.uint8), torch.zeros((1, 256)), 1, 256)
+
+
+def test_decode_int8_defaults_follow_the_reference():
+    """The decode matvecs take int8 activations by default for the reference's ICODES formats (Q4_K, Q6_K; Q4_0 only
+    with its Q4_0_Q8=1 switch, S/formats.py:20-30), the tiled layouts with their format, the tiled Q4_0 always."""
+    import importlib
+    import os
+    from qmm import formats
+    assert formats.decode_q8("q4_k") and formats.decode_q8("q6_k") and formats.decode_q8("q4_kt")
+    assert formats.decode_q8("q4_0t")
+    assert not formats.decode_q8("mxfp4") and not formats.decode_q8("mxfp4s")
+    old = os.environ.pop("Q4_0_Q8", None)
+    try:
+        assert not importlib.reload(formats).decode_q8("q4_0")
+        os.environ["Q4_0_Q8"] = "1"
+        assert importlib.reload(formats).decode_q8("q4_0")
+    finally:
+        os.environ.pop("Q4_0_Q8", None)
+        if old is not None:
+            os.environ["Q4_0_Q8"] = old
+        importlib.reload(formats)
