@@ -28,10 +28,12 @@
 // plane holds per (rb, group of four chunks) 256 bytes, lane l's four scale bytes at 4 l, so one dword load per
 // lane brings the scales of four chunks.
 //
-// Tiling: a workgroup of four waves owns one 64-row expert tile; each wave computes 64 rows x 64 weight columns
-// (2 x 2 MFMA blocks) over all of K. gu: wave w owns output columns 32 w .. 32 w + 31 of a 128-column block, its
-// two column blocks being those columns of the gate and of the up matrix, so the activation is applied in
-// registers. dn: wave w owns the 32 columns 32 w .. 32 w + 31 of a 128-column block. Workgroup b runs on XCD b % 8;
+// Tiling: a workgroup of four waves owns one 64-row expert tile; each wave computes its 64 rows x CB output column
+// blocks of 32 over all of K. gu: wave w owns output columns 32 CB w .. 32 CB (w + 1) - 1 of a 128 CB-column block,
+// its weight blocks being those columns of the gate and of the up matrix (2 CB x 2 MFMA blocks), so the activation
+// is applied in registers. dn: the same columns of the one matrix (CB x 2 MFMA blocks). CB = 2 (tiled planes, many
+// rows an expert) halves the activation bytes a weight byte meets; CB = 1 keeps more workgroups on the weight
+// stream when the experts hold few rows. Workgroup b runs on XCD b % 8;
 // the live tiles (those with an expert) are cut into eight contiguous ranges, one per XCD, and each XCD walks its
 // range tile-fastest: the workgroups resident together on an XCD are then the tiles of one or a few experts on the
 // same column blocks, so an expert's weights come from HBM once and its other tiles read them from that XCD's L2.
@@ -70,6 +72,7 @@ namespace {
 #ifndef QMM_MX_WAVES
 #define QMM_MX_WAVES 3            // minimum waves per SIMD the register allocation must allow (3 workgroups per CU)
 #endif
+
 constexpr int BM = 64, KC = 64;
 
 enum Kind { kGU = 1, kDN = 2, kGU8 = 3 };   // kGU8: gu with its output quantized to MXFP8
@@ -153,18 +156,22 @@ __device__ __forceinline__ void copy_to_lds(u8 *dst, const u8 *src, int64_t n, i
   }
 }
 
-template <int KIND, int LAYOUT, int DEPTH, int kSub, int OUT>
-__global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs a) {
+template <int KIND, int LAYOUT, int DEPTH, int kSub, int OUT, int CB, int WAVES>
+__global__ __launch_bounds__(256, WAVES) void mxfp4_grouped_kernel(MArgs a) {
   constexpr bool DENSE = OUT != kOutGrouped;
   static_assert(!(DENSE && KIND == kGU8), "the MXFP8 epilogue writes the grouped activation");
+  static_assert(CB == 1 || LAYOUT == kTiled, "several column blocks a wave on the tiled planes only");
   constexpr int APITCH = kSub * KC + 16;     // activation bytes per LDS row (16-byte aligned rows)
-  constexpr int BN = 128;                   // output columns per workgroup
   constexpr bool GU = KIND != kDN;
-  constexpr int NJ = GU ? 2 : 1;             // 32-column weight blocks per wave (gu: gate and up)
+  // CB output column blocks of 32 per wave; its 32-column weight blocks: gu the CB gate blocks, then the same CB
+  // blocks of the up matrix; dn the CB blocks
+  constexpr int NJ = GU ? 2 * CB : CB;
+  constexpr int WC = 32 * CB;                // output columns per wave
+  constexpr int BN = 4 * WC;                 // output columns per workgroup
   // the activation double buffer; kGU8 reuses it after the loop for its f32 output, 32 rows at a time
   constexpr int OPITCH = BN + 4;   // floats per output row: the 4-float skew spreads a column's rows over the banks
-  __shared__ __align__(16) u8 smem[2 * BM * APITCH];
-  static_assert(32 * OPITCH * 4 <= sizeof(smem), "epilogue staging");
+  constexpr int kStage = 2 * BM * APITCH, kOut = KIND == kGU8 ? 32 * OPITCH * 4 : 0;
+  __shared__ __align__(16) u8 smem[kStage > kOut ? kStage : kOut];
   auto As = reinterpret_cast<u8 (*)[BM][APITCH]>(smem);
   __shared__ int src_row[BM];
   __shared__ int live_end;
@@ -215,16 +222,20 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
 
   // ---- weights: this lane's two columns (gu: one column of the gate and of the up matrix) and K half
   const int h = lane >> 5, lc = lane & 31;
-  const int col = n0 + 32 * wave + lc;       // the lane's output column
-  const u8 *nbj[NJ], *sbj[NJ];
-  if constexpr (GU) {
+  const int col = n0 + WC * wave + lc;       // the lane's output column (dn: of its first block)
+  const u8 *nbj[NJ], *sbj[NJ];   // the matrix of weight block j
+  {
     const u8 *gn = a.wn + (int64_t)expert * a.nib_ebytes, *gs = a.wsc + (int64_t)expert * a.sc_ebytes;
-    nbj[0] = gn; sbj[0] = gs;
-    if (a.wn2) { nbj[1] = a.wn2 + (int64_t)expert * a.nib_ebytes; sbj[1] = a.wsc2 + (int64_t)expert * a.sc_ebytes; }
-    else { nbj[1] = gn + a.up_nib_off; sbj[1] = gs + a.up_sc_off; }
-  } else {
-    nbj[0] = a.wn + (int64_t)expert * a.nib_ebytes;
-    sbj[0] = a.wsc + (int64_t)expert * a.sc_ebytes;
+    const u8 *un = gn, *us = gs;
+    if constexpr (GU) {
+      if (a.wn2) { un = a.wn2 + (int64_t)expert * a.nib_ebytes; us = a.wsc2 + (int64_t)expert * a.sc_ebytes; }
+      else { un = gn + a.up_nib_off; us = gs + a.up_sc_off; }
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      nbj[j] = j < CB ? gn : un;
+      sbj[j] = j < CB ? gs : us;
+    }
   }
   // the lane's weight stream: split -- its column's row at K half h; tiled -- lane slot of the wave's row block
   // (waves past the last column read the last block and store nothing)
@@ -232,10 +243,10 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
   const u8 *wcs[NJ];
   int wrow[NJ];   // kSplit: the lane's weight columns as rows of Wsc (gu: the gate block, then the up block)
   if constexpr (LAYOUT == kTiled) {
-    int rb = (n0 >> 5) + wave;
-    rb = rb < (N >> 5) ? rb : (N >> 5) - 1;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
+      int rb = (n0 >> 5) + CB * wave + j % CB;
+      rb = rb < (N >> 5) ? rb : (N >> 5) - 1;
       wcn[j] = nbj[j] + (int64_t)rb * C * 1024 + 16 * lane;
       wcs[j] = sbj[j] + (int64_t)rb * C4 * 256 + 4 * lane;
       wrow[j] = 0;
@@ -409,42 +420,54 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
   if constexpr (KIND == kGU8) {
     // The activation quantized to MXFP8 as qmm_quant_mxfp8 quantizes it. Per 32-row half of the tile, the f32
     // activations go to LDS (the activation buffers are free after the loop's last barrier); then threads 2 b and
-    // 2 b + 1 own 32-value block b (row b / 4, columns 32 (b % 4) .. +31), 16 values each: their maximum is one lane
+    // 2 b + 1 own 32-value block b of a row (BN / 32 blocks a row), 16 values each: their maximum is one lane
     // exchange, and each thread's 16 E4M3 codes leave as one 16-byte store. Dead rows quantize zeros: codes 0, scale
     // byte 0.
     float *Of = reinterpret_cast<float *>(smem);
-    const int64_t bo = (int64_t)expert * N + (col < N ? col : N - 1);
-    const float bg = a.bias ? a.bias[bo] : 0.f, bu = a.bias2 ? a.bias2[bo] : 0.f;
+    float bg[CB], bu[CB];
+#pragma unroll
+    for (int cc = 0; cc < CB; ++cc) {
+      const int64_t bo = (int64_t)expert * N + (col + 32 * cc < N ? col + 32 * cc : N - 1);
+      bg[cc] = a.bias ? a.bias[bo] : 0.f;
+      bu[cc] = a.bias2 ? a.bias2[bo] : 0.f;
+    }
     const int cols = N - n0 < BN ? N - n0 : BN;   // a multiple of 32
-    const int qrow = tid >> 3, blk = (tid >> 1) & 3, part = tid & 1;
+    constexpr int QT = BN / 16, QR = 256 / QT;    // threads per row, rows per round
+    const int blk = (tid % QT) >> 1, part = tid & 1;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       if (i) __syncthreads();   // the first half's reads are done before the second half overwrites them
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int lr = 8 * (r >> 2) + 4 * h + (r & 3);
-        Of[lr * OPITCH + 32 * wave + lc] =
-            src_row[32 * i + lr] >= 0 ? act_fast(a.act, acc[i][0][r] + bg, acc[i][1][r] + bu) : 0.f;
-      }
+      for (int cc = 0; cc < CB; ++cc)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int lr = 8 * (r >> 2) + 4 * h + (r & 3);
+          Of[lr * OPITCH + WC * wave + 32 * cc + lc] =
+              src_row[32 * i + lr] >= 0 ? act_fast(a.act, acc[i][cc][r] + bg[cc], acc[i][CB + cc][r] + bu[cc]) : 0.f;
+        }
       __syncthreads();
-      const f32x4 *src = reinterpret_cast<const f32x4 *>(Of + qrow * OPITCH + 32 * blk + 16 * part);
-      f32x4 v[4];
-      float m = 0.f;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        v[q] = src[q];
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(v[q][0]), fabsf(v[q][1])), fmaxf(fabsf(v[q][2]), fabsf(v[q][3]))));
-      }
-      m = fmaxf(m, xshfl<1>(m));
-      const int sx = mxfp8_exponent(m);
-      v4u code;
+      for (int q0 = 0; q0 < 32; q0 += QR) {
+        const int qrow = q0 + tid / QT;
+        const f32x4 *src = reinterpret_cast<const f32x4 *>(Of + qrow * OPITCH + 32 * blk + 16 * part);
+        f32x4 v[4];
+        float m = 0.f;
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        code[q] = (u32)e4m3_pack2<true>(v[q][2], v[q][3], sx, e4m3_pack2<false>(v[q][0], v[q][1], sx, 0));
-      const int64_t orow = m0 + 32 * i + qrow;
-      if (32 * blk < cols) {
-        __builtin_nontemporal_store(code, reinterpret_cast<v4u *>(a.y8 + orow * N + n0 + 32 * blk + 16 * part));
-        if (!part) a.ys8[orow * (N / 32) + n0 / 32 + blk] = (u8)(sx + 127);
+        for (int q = 0; q < 4; ++q) {
+          v[q] = src[q];
+          m = fmaxf(m, fmaxf(fmaxf(fabsf(v[q][0]), fabsf(v[q][1])), fmaxf(fabsf(v[q][2]), fabsf(v[q][3]))));
+        }
+        m = fmaxf(m, xshfl<1>(m));
+        const int sx = mxfp8_exponent(m);
+        v4u code;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          code[q] = (u32)e4m3_pack2<true>(v[q][2], v[q][3], sx, e4m3_pack2<false>(v[q][0], v[q][1], sx, 0));
+        const int64_t orow = m0 + 32 * i + qrow;
+        if (32 * blk < cols) {
+          __builtin_nontemporal_store(code, reinterpret_cast<v4u *>(a.y8 + orow * N + n0 + 32 * blk + 16 * part));
+          if (!part) a.ys8[orow * (N / 32) + n0 / 32 + blk] = (u8)(sx + 127);
+        }
       }
     }
     return;
@@ -452,66 +475,95 @@ __global__ __launch_bounds__(256, QMM_MX_WAVES) void mxfp4_grouped_kernel(MArgs 
   if (col >= N) return;
   if constexpr (DENSE) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int cc = 0; cc < CB; ++cc) {
+      const int cj = col + 32 * cc;
+      if (cj >= N) continue;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (row >= a.M) continue;
-        float v;
-        if constexpr (GU) v = act_fast(QMM_ACT_SILU, acc[i][0][r], acc[i][1][r]);
-        else v = acc[i][0][r];
-        const int64_t o = (int64_t)row * N + col;
-        if constexpr (OUT == kOutF32 || OUT == kOutF32Acc) {
-          if constexpr (OUT == kOutF32Acc) v += a.y[o];
-          a.y[o] = v;
-        } else {
-          u16 *yb = reinterpret_cast<u16 *>(a.y);
-          if constexpr (OUT == kOutBF16Acc) v += bf16_to_f32(yb[o]);
-          yb[o] = (u16)f32_to_bf16_rne(v);
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = m0 + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+          if (row >= a.M) continue;
+          float v;
+          if constexpr (GU) v = act_fast(QMM_ACT_SILU, acc[i][cc][r], acc[i][CB + cc][r]);
+          else v = acc[i][cc][r];
+          const int64_t o = (int64_t)row * N + cj;
+          if constexpr (OUT == kOutF32 || OUT == kOutF32Acc) {
+            if constexpr (OUT == kOutF32Acc) v += a.y[o];
+            a.y[o] = v;
+          } else {
+            u16 *yb = reinterpret_cast<u16 *>(a.y);
+            if constexpr (OUT == kOutBF16Acc) v += bf16_to_f32(yb[o]);
+            yb[o] = (u16)f32_to_bf16_rne(v);
+          }
         }
-      }
+    }
     return;
   }
-  const float bg = a.bias ? a.bias[(int64_t)expert * N + col] : 0.f;
-  const float bu = (GU && a.bias2) ? a.bias2[(int64_t)expert * N + col] : 0.f;
+  float bg[CB], bu[CB];
+#pragma unroll
+  for (int cc = 0; cc < CB; ++cc) {
+    const int64_t bo = (int64_t)expert * N + (col + 32 * cc < N ? col + 32 * cc : N - 1);
+    bg[cc] = a.bias ? a.bias[bo] : 0.f;
+    bu[cc] = (GU && a.bias2) ? a.bias2[bo] : 0.f;
+  }
   // the bias loads complete here, once: otherwise every store below, each behind its own row branch, waits for
   // them with vmcnt(0), which also waits for the stores before it
   __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int cc = 0; cc < CB; ++cc) {
+    const int cj = col + 32 * cc;
+    if (cj >= N) continue;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int lr = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-      if (src_row[lr] < 0) continue;   // a row without an assignment is not written
-      float v;
-      if constexpr (GU) v = act_fast(a.act, acc[i][0][r] + bg, acc[i][1][r] + bu);
-      else v = acc[i][0][r] + bg;
-      __builtin_nontemporal_store(v, a.y + (int64_t)(m0 + lr) * N + col);
-    }
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int lr = 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (src_row[lr] < 0) continue;   // a row without an assignment is not written
+        float v;
+        if constexpr (GU) v = act_fast(a.act, acc[i][cc][r] + bg[cc], acc[i][CB + cc][r] + bu[cc]);
+        else v = acc[i][cc][r] + bg[cc];
+        __builtin_nontemporal_store(v, a.y + (int64_t)(m0 + lr) * N + cj);
+      }
+  }
 }
 
 constexpr int kMaxK = 12288;   // the workgroup stages (64 + 256) x K / 32 scale bytes in LDS
 
-template <int KIND, int LAYOUT, int OUT = kOutGrouped>
-int launch(const MArgs &a, hipStream_t s) {
+// CB output column blocks of 32 per wave (CB > 1: tiled planes): 128 CB output columns a workgroup. The register
+// allocation allows three workgroups a CU while the accumulators take at most two weight blocks a wave, else two.
+template <int KIND, int LAYOUT, int OUT = kOutGrouped, int CB = 1>
+int launch(const MArgs &a0, hipStream_t s) {
+  MArgs a = a0;
+  a.n_blocks = (a.N + 128 * CB - 1) / (128 * CB);
+  constexpr int NJ = KIND == kDN ? CB : 2 * CB;
+  constexpr int kWaves = NJ <= 2 ? QMM_MX_WAVES : 2;
   constexpr int kDepth = KIND == kDN ? QMM_MX_DEPTH_DN : QMM_MX_DEPTH_GU;
-  constexpr int kSub = KIND == kDN ? QMM_MX_SUB_DN : QMM_MX_SUB_GU;
+  // several weight blocks a wave shorten the super-steps to keep the bytes per barrier
+  constexpr int kSub0 = (KIND == kDN ? QMM_MX_SUB_DN : QMM_MX_SUB_GU) / CB;
+  constexpr int kSub = kSub0 > 0 ? kSub0 : 1;
   constexpr int kRows = BM + (LAYOUT == kSplit ? (KIND != kDN ? 256 : 128) : 0);   // scale rows staged in LDS
   const dim3 grid((unsigned)(8 * a.n_blocks * ((a.max_tiles + 7) / 8)));
   const size_t dyn = (size_t)kRows * (a.K / 32);
+  const void *fn = reinterpret_cast<const void *>(&mxfp4_grouped_kernel<KIND, LAYOUT, kDepth, kSub, OUT, CB, kWaves>);
   if constexpr ((size_t)kRows * (kMaxK / 32) > 32768) {
     // beyond the default dynamic LDS limit: raised once per device to the largest K this kernel takes, so the order
     // of calls with different K does not matter
     if (dyn > 32768) {
       static std::atomic<unsigned> raised{0};
-      if (int st = raise_dyn_lds(reinterpret_cast<const void *>(&mxfp4_grouped_kernel<KIND, LAYOUT, kDepth, kSub, OUT>),
-                                 kRows * (kMaxK / 32), raised))
-        return st;
+      if (int st = raise_dyn_lds(fn, kRows * (kMaxK / 32), raised)) return st;
     }
   }
-  mxfp4_grouped_kernel<KIND, LAYOUT, kDepth, kSub, OUT><<<grid, 256, dyn, s>>>(a);
+  mxfp4_grouped_kernel<KIND, LAYOUT, kDepth, kSub, OUT, CB, kWaves><<<grid, 256, dyn, s>>>(a);
   return launch_status();
 }
+
+// Column blocks a wave of the grouped GEMMs on tiled planes: two once the table holds, on average, at least
+// kWideRows rows an expert (the down GEMM; kWideRowsGU for the gate/up GEMM, whose two-block waves run two
+// workgroups a CU instead of three). max_tiles - E tiles hold the assignments: the bucket sizes max_tiles as
+// A / 64 + E. Below that the one-block kernels keep more workgroups in flight on the weight stream.
+constexpr int kWideRows = 64, kWideRowsGU = 256;
+inline bool wide_tiles(int64_t max_tiles, int E, int rows) { return (max_tiles - E) * BM >= (int64_t)rows * E; }
 
 // MFMA-tiled planes from split planes (a byte permutation): one thread per 16-byte lane slot of a 1 KB tile, and
 // per (row block, chunk group) the 64 lanes' four scale bytes. Chunks past K in the last group get scale 0.
@@ -600,8 +652,8 @@ int qmm_grouped_mxfp4(int tiled, int mode, int fused, int act, int64_t max_tiles
   a.wn = static_cast<const u8 *>(w); a.wsc = static_cast<const u8 *>(ws);
   a.tile_info = tile_info; a.rowmap = rowmap; a.KU = KU; a.E = E; a.act = act; a.y = y; a.y8 = y8; a.ys8 = ys8;
   a.bias = bias; a.bias2 = mode == 0 ? bias2 : nullptr;
-  a.n_blocks = (int)((n + 127) / 128);
   a.max_tiles = (int)max_tiles;
+  const bool wide = tiled && wide_tiles(max_tiles, E, mode == 0 ? kWideRowsGU : kWideRows);
   const int64_t nrow = k / 2;                                        // nibble bytes per row (both layouts)
   const int64_t srow = tiled ? qmm_mxfp4t_scale_bytes(32, k) / 32 : k / 32;   // scale bytes per row
   if (mode == 0) {
@@ -612,11 +664,13 @@ int qmm_grouped_mxfp4(int tiled, int mode, int fused, int act, int64_t max_tiles
     a.up_sc_off = fused ? srow * n : 0;
     a.wn2 = fused ? nullptr : static_cast<const u8 *>(w2);
     a.wsc2 = fused ? nullptr : static_cast<const u8 *>(ws2);
+    if (wide) return out8 ? launch<kGU8, kTiled, kOutGrouped, 2>(a, s) : launch<kGU, kTiled, kOutGrouped, 2>(a, s);
     if (out8) return tiled ? launch<kGU8, kTiled>(a, s) : launch<kGU8, kSplit>(a, s);
     return tiled ? launch<kGU, kTiled>(a, s) : launch<kGU, kSplit>(a, s);
   }
   a.nib_ebytes = nrow * n;
   a.sc_ebytes = srow * n;
+  if (wide) return launch<kDN, kTiled, kOutGrouped, 2>(a, s);
   return tiled ? launch<kDN, kTiled>(a, s) : launch<kDN, kSplit>(a, s);
 }
 
@@ -642,7 +696,6 @@ extern "C" int qmm_gemm_mxfp4(int fmt, int mode, int64_t rows, int64_t k, int64_
   a.wn = static_cast<const u8 *>(w); a.wsc = static_cast<const u8 *>(ws);
   a.wn2 = static_cast<const u8 *>(w2); a.wsc2 = static_cast<const u8 *>(ws2);
   a.E = 1; a.KU = 1; a.act = QMM_ACT_SILU; a.y = static_cast<float *>(y);
-  a.n_blocks = (int)((n + 127) / 128);
   a.max_tiles = (int)((rows + BM - 1) / BM);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool bf = y_dtype == QMM_BF16;

@@ -320,6 +320,169 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(int64_t tokens, 
   }
 }
 
+// Many assignments (from 8192): the same rows from three launches of many workgroups. Workgroup g owns the assignments
+// [g C, g C + C) (the last one also the remainder, C = kBucketChunk >= kMaxE). (1) count: per expert the live
+// assignments of the range, parked in pos[g C + e] (the range's own slice of pos, which only its scatter writes
+// later), and rowmap cleared. (2) scan, one workgroup: tiles per expert, the tile table, and per (g, e) the first
+// row of expert e's assignments of range g, base[e] * 64 + the counts of the ranges before g, parked back in the
+// same slot. (3) scatter: range g reads its row offsets, then ranks its assignments in ascending a exactly as the
+// one-workgroup kernel does. Rows are therefore the one-workgroup kernel's, bit for bit.
+constexpr int kBucketChunk = 1024;
+static_assert(kBucketChunk >= kMaxE, "a range parks one count per expert in its own slice of pos");
+constexpr int64_t kBucketSplit = 8 * kBucketChunk;   // assignments from which the three launches are faster
+
+__device__ __forceinline__ void bucket_range(int64_t A, int G, int g, int64_t &a0, int64_t &a1) {
+  a0 = (int64_t)g * kBucketChunk;
+  a1 = g == G - 1 ? A : a0 + kBucketChunk;
+}
+
+__global__ __launch_bounds__(kBucketThreads) void bucket_count_kernel(int64_t tokens, int KU, int E, int64_t max_tiles,
+                                                                      const int32_t *__restrict__ info,
+                                                                      const int32_t *__restrict__ ids,
+                                                                      int32_t *__restrict__ rowmap,
+                                                                      int32_t *__restrict__ pos) {
+  __shared__ int count[kMaxE];
+  const int tid = threadIdx.x, G = gridDim.x, g = blockIdx.x;
+  const int64_t A = tokens * KU;
+  int64_t a0, a1;
+  bucket_range(A, G, g, a0, a1);
+  for (int e = tid; e < kMaxE; e += kBucketThreads) count[e] = 0;
+  // this range's share of the row map cleared (every row; the scatter writes the live ones)
+  const int64_t R = max_tiles * kTile, r0 = R * g / G, r1 = R * (g + 1) / G;
+  for (int64_t r = r0 + tid; r < r1; r += kBucketThreads) rowmap[r] = -1;
+  __syncthreads();
+  for (int64_t a = a0 + tid; a < a1; a += kBucketThreads) {
+    if (info && info[(a / KU) * 4 + 2] == 0) continue;
+    int e = ids[a];
+    e = e < 0 ? 0 : (e >= E ? E - 1 : e);
+    atomicAdd(&count[e], 1);
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += kBucketThreads) pos[a0 + e] = count[e];
+}
+
+__global__ __launch_bounds__(kBucketThreads) void bucket_scan_kernel(int64_t tokens, int KU, int E, int64_t max_tiles,
+                                                                     int G, int32_t *__restrict__ tile_info,
+                                                                     int32_t *__restrict__ pos) {
+  __shared__ int total[kMaxE];
+  __shared__ int base[kMaxE];
+  __shared__ int total_tiles;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t A = tokens * KU;
+  // per expert: the counts of the ranges become running offsets inside the expert (a thread per expert)
+  for (int e = tid; e < kMaxE; e += kBucketThreads) {
+    int run = 0;
+    if (e < E)
+      for (int g = 0; g < G; ++g) {
+        int64_t a0, a1;
+        bucket_range(A, G, g, a0, a1);
+        const int c = pos[a0 + e];
+        pos[a0 + e] = run;
+        run += c;
+      }
+    total[e] = run;
+  }
+  __syncthreads();
+  if (wave == 0) {   // exclusive scan of tiles per expert over <= 256 experts, 4 per lane
+    int tl[4], sum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = lane * 4 + i;
+      tl[i] = e < E ? (total[e] + kTile - 1) / kTile : 0;
+      sum += tl[i];
+    }
+    int incl = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int o = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += o;
+    }
+    int b = incl - sum;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      base[lane * 4 + i] = b;
+      b += tl[i];
+    }
+    if (lane == 63) total_tiles = incl;
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += kBucketThreads) {
+    const int tiles = (total[e] + kTile - 1) / kTile;
+    for (int j = 0; j < tiles; ++j) {
+      tile_info[2 * (base[e] + j)] = e;
+      tile_info[2 * (base[e] + j) + 1] = min(kTile, total[e] - kTile * j);
+    }
+  }
+  for (int64_t i = total_tiles + tid; i < max_tiles; i += kBucketThreads) {
+    tile_info[2 * i] = -1;
+    tile_info[2 * i + 1] = 0;
+  }
+  // the first row of each (range, expert): the expert's first tile row plus the running offset
+  for (int64_t i = tid; i < (int64_t)G * E; i += kBucketThreads) {
+    const int g = (int)(i / E), e = (int)(i % E);
+    int64_t a0, a1;
+    bucket_range(A, G, g, a0, a1);
+    pos[a0 + e] += base[e] * kTile;
+  }
+}
+
+__global__ __launch_bounds__(kBucketThreads) void bucket_scatter_kernel(int64_t tokens, int KU, int E,
+                                                                        const int32_t *__restrict__ info,
+                                                                        const int32_t *__restrict__ ids,
+                                                                        int32_t *__restrict__ rowmap,
+                                                                        int32_t *__restrict__ pos) {
+  __shared__ int first[kMaxE];
+  __shared__ int wcount[kBucketWaves][kMaxE];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, G = gridDim.x, g = blockIdx.x;
+  const int64_t A = tokens * KU;
+  int64_t a0, a1;
+  bucket_range(A, G, g, a0, a1);
+  for (int e = tid; e < E; e += kBucketThreads) first[e] = pos[a0 + e];
+  for (int i = tid; i < kBucketWaves * kMaxE; i += kBucketThreads) (&wcount[0][0])[i] = 0;
+  __syncthreads();   // the offsets are read before this range's pos entries are written
+  for (int64_t c0 = a0; c0 < a1; c0 += kBucketThreads) {
+    const int64_t a = c0 + tid;
+    bool live = a < a1;
+    int e = 0;
+    if (live) {
+      live = !(info && info[(a / KU) * 4 + 2] == 0);
+      e = ids[a];
+      e = e < 0 ? 0 : (e >= E ? E - 1 : e);
+    }
+    uint64_t peers = __ballot(live);
+#pragma unroll
+    for (int bit = 0; bit < 8; ++bit) {
+      const uint64_t ones = __ballot(live && ((e >> bit) & 1));
+      peers &= ((e >> bit) & 1) ? ones : ~ones;
+    }
+    const int rank_w = __popcll(peers & ((1ull << lane) - 1ull));
+    if (live && rank_w == 0) wcount[wave][e] = __popcll(peers);
+    __syncthreads();
+    for (int ex = tid; ex < E; ex += kBucketThreads) {   // per expert: exclusive offsets over waves
+      int run = first[ex];
+      for (int w = 0; w < kBucketWaves; ++w) {
+        const int c = wcount[w][ex];
+        wcount[w][ex] = run;
+        run += c;
+      }
+      first[ex] = run;
+    }
+    __syncthreads();
+    if (a < a1) {
+      if (live) {
+        const int row = wcount[wave][e] + rank_w;
+        rowmap[row] = (int32_t)a;
+        pos[a] = row;
+      } else {
+        pos[a] = -1;
+      }
+    }
+    __syncthreads();
+    for (int i = tid; i < kBucketWaves * kMaxE; i += kBucketThreads) (&wcount[0][0])[i] = 0;
+    __syncthreads();
+  }
+}
+
 // ----------------------------------------------------------------------------------------------- combine
 // One workgroup per token, 256-channel blocks; the fma chain runs in k order (S/gen_moe.py:1231-1280).
 __global__ __launch_bounds__(256) void combine_kernel(int64_t tokens, int64_t rows, int64_t H, int KU,
@@ -690,7 +853,15 @@ int qmm_moe_bucket(int64_t tokens, int KU, int E, int64_t max_tiles, const int32
   if (tokens <= 0 || tokens > 65536) return QMM_ERR_SHAPE;
   if (max_tiles < tokens * KU / kTile + E || max_tiles > (1 << 24)) return QMM_ERR_SHAPE;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  bucket_kernel<<<1, kBucketThreads, 0, s>>>(tokens, KU, E, max_tiles, info, ids, tile_info, rowmap, pos);
+  const int64_t A = tokens * KU;
+  if (A < kBucketSplit) {   // three launches cost about 15 us; the one-workgroup kernel about 2 us per 1024
+    bucket_kernel<<<1, kBucketThreads, 0, s>>>(tokens, KU, E, max_tiles, info, ids, tile_info, rowmap, pos);
+    return launch_status();
+  }
+  const int G = (int)(A / kBucketChunk);   // ranges of kBucketChunk assignments, the last with the remainder
+  bucket_count_kernel<<<G, kBucketThreads, 0, s>>>(tokens, KU, E, max_tiles, info, ids, rowmap, pos);
+  bucket_scan_kernel<<<1, kBucketThreads, 0, s>>>(tokens, KU, E, max_tiles, G, tile_info, pos);
+  bucket_scatter_kernel<<<G, kBucketThreads, 0, s>>>(tokens, KU, E, info, ids, rowmap, pos);
   return launch_status();
 }
 

@@ -315,11 +315,12 @@ def test_quant_mxfp8_matches_oracle(dev):
 
 
 @pytest.mark.parametrize("T,E,H,FE", [(256, 32, 2880, 2880), (100, 8, 512, 320), (1024, 32, 2880, 2880),
-                                      (600, 8, 512, 320)])
+                                      (600, 8, 512, 320), (4096, 32, 2880, 2880), (2048, 8, 512, 320)])
 def test_grouped_mxfp4_tiled_equals_split_bit_for_bit(dev, T, E, H, FE):
     """The MFMA-tiled planes feed the scaled MFMA the same operands in the same K order as the split planes, so
     both grouped GEMMs (fused gate_up with swiglu_oai, and down) give identical bits on every live row; also with
-    two or more tiles an expert (T = 1024 at the gpt-oss-20b shape, T = 600 with 8 experts, top-2)."""
+    two or more tiles an expert (T = 1024 and 4096 at the gpt-oss-20b shape, T = 600 and 2048 with 8 experts,
+    top-2)."""
     import torch
     from qmm import synth
     ops = _ops()
@@ -368,7 +369,8 @@ def test_tile_mxfp4_bit_exact(dev):
 
 @pytest.mark.parametrize("T,E,H,FE,tiled", [(256, 32, 2880, 2880, True), (256, 32, 2880, 2880, False),
                                             (100, 8, 512, 320, True), (1024, 32, 2880, 2880, True),
-                                            (600, 8, 512, 320, True)])
+                                            (600, 8, 512, 320, True), (4096, 32, 2880, 2880, True),
+                                            (2048, 8, 512, 320, True)])
 def test_grouped_gate_up_mxfp8_output_equals_quantized_act(dev, T, E, H, FE, tiled):
     """The gate/up GEMM with the MXFP8 quantization fused into its epilogue writes exactly the codes and scales
     quant_mxfp8 makes of the f32 activation the plain gate/up GEMM writes (every live row; the fused epilogue

@@ -41,8 +41,10 @@ def test_topk_ties_go_to_the_lower_id(dev):
 
 
 @pytest.mark.parametrize("T,E,KU", [(64, 128, 8), (256, 32, 4), (3, 16, 2), (1000, 64, 8), (70, 256, 8), (4096, 32, 4),
-                                    (4095, 64, 4), (20000, 256, 8)])
+                                    (4095, 64, 4), (20000, 256, 8), (2048, 32, 4), (8191, 16, 1), (9300, 256, 1)])
 def test_bucket_canonical(dev, T, E, KU):
+    """From 8192 assignments on, the bucket runs as count / scan / scatter launches over ranges of 1024 (the last
+    with the remainder): 2048 x 4 is the first such case, 8191 x 1 the last one-workgroup case."""
     rng = np.random.default_rng(T + E)
     ids = rng.integers(0, E, (T, KU)).astype(np.int32)
     if T > 3:
@@ -88,6 +90,24 @@ def test_topk_operand_equals_separate_calls(dev, op, T, E, KU, gating, norm, H, 
     assert_bits_equal(host(wts), host(wts0), "weights")
     np.testing.assert_array_equal(host(xo).view(np.uint8), host(xo0).view(np.uint8))
     np.testing.assert_array_equal(host(xs).view(np.uint8), host(xs0).view(np.uint8))
+
+
+def test_bucket_dead_range_and_one_expert(dev):
+    """Ranges of the many-workgroup bucket whose tokens are all padding (info[t, 2] == 0) and ranges that hold a
+    single expert: rows, tiles and pos still equal the oracle's."""
+    import torch
+    rng = np.random.default_rng(8)
+    T, E, KU = 12000, 8, 1
+    ids = rng.integers(0, E, (T, KU)).astype(np.int32)
+    ids[5600:7900, 0] = 3
+    info = np.ones((T, 4), np.int32)
+    info[1000:4500, 2] = 0
+    mt = ref.max_tiles(T, KU, E)
+    ti, rm, pos = _ops().moe_bucket(torch.from_numpy(ids).to(dev), E, mt, info=torch.from_numpy(info).to(dev))
+    eti, erm, epos = ref.bucket(ids, E, mt, live=info[:, 2])
+    np.testing.assert_array_equal(host(ti), eti)
+    np.testing.assert_array_equal(host(rm), erm)
+    np.testing.assert_array_equal(host(pos), epos)
 
 
 def test_bucket_repeat_runs_identical(dev):
