@@ -241,6 +241,25 @@ int qmm_moe_expert_mv_q8(int fmt, int mode, int fused, int act, int64_t k, int64
                          int64_t assignments, const int32_t *ids, const void *x, const void *w, const void *w2,
                          const float *bias, const float *bias2, float *y, qmm_stream_t stream);
 
+/* The reference's opt-in int8 decode of MXFP4 split planes (MXFP4S_Q8, S/formats.py:26-28): the int8 matvecs of
+ * qmm_mv_q8 / qmm_mv_swiglu_q8 / qmm_mv_pair_q8 (mode 0 / 1 / 2; g_mv_mxfp4s_k{K}[_swiglu|_pair][_t{TG}]_q8,
+ * S/gen_llm.py:1159-1197, :1288-1301) and of qmm_moe_expert_mv_q8 for mxfp4s weights, whose scale planes have no
+ * place in those signatures. Per 32-value block: signed codes c = 2 x the E2M1 values (0 1 2 3 4 6 8 12 and
+ * negatives) and d = 2^(e - 128) from the E8M0 byte (@g_mxfp4s_icodes, S/gen_mxfp4s.py:1113-1160), the exact integer
+ * dot sum c q with the Q8_1 codes, then (d da) di (iq_dot, S/gen_llm.py:1047-1049). w / w2: nibble planes [n, k/2]
+ * (byte j: values 2j low, 2j+1 high); ws / ws2: E8M0 planes [n, k/32]; k % 64 == 0. x: the planar Q8_1 buffer of
+ * qmm_quant_q8 (x_dtype QMM_Q8). y (and y2, pair): f32 [tokens, n]. */
+int qmm_mv_mxfp4s_q8(int mode, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
+                     const void *w, const void *ws, const void *w2, const void *ws2, float *y, float *y2,
+                     qmm_stream_t stream);
+/* The decode expert matvecs of qmm_moe_expert_mv_q8 on mxfp4s experts: w / ws the [E, n, k] planes (fused gate_up:
+ * [E, 2n, k] planes, expert e's n gate rows then its n up rows, in both planes), w2 / ws2 the up planes when not
+ * fused. */
+int qmm_moe_expert_mv_mxfp4s_q8(int mode, int fused, int act, int64_t k, int64_t n, int E, int KU,
+                                int64_t assignments, const int32_t *ids, const void *x, const void *w, const void *ws,
+                                const void *w2, const void *ws2, const float *bias, const float *bias2, float *y,
+                                qmm_stream_t stream);
+
 /* qmm_moe_expert_mv for MXFP4 split planes (the reference's mxfp4s expert tensors, S/gen_llm.py:844-895):
  * w / w2 are nibble planes [E, rows, k/2] and ws / ws2 their E8M0 scale planes [E, rows, k/32]; with fused != 0
  * w and ws hold each expert's n gate rows then its n up rows and w2 / ws2 are ignored. */

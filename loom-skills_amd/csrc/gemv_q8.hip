@@ -120,6 +120,7 @@ __device__ __forceinline__ void xq_load(const u8 *codes, const float *meta, int6
 
 // Q4_K: item = 4 * block + page j; groups 8 block + 2 j (low nibbles) and + 1 (high nibbles)
 struct Q4K8 {
+  static constexpr bool kSplit = false;
   struct W { v4u h, q0, q1; };
   static __device__ __forceinline__ int items(int64_t k) { return (int)(k / 256) * 4; }
   static __device__ __forceinline__ int64_t group(int item) { return (int64_t)(item >> 2) * 8 + 2 * (item & 3); }
@@ -152,6 +153,7 @@ struct Q4K8 {
 
 // Q4_0: item = pair of blocks p (36 bytes at 36 p, 4-byte aligned when K % 64 == 0); groups 2 p and 2 p + 1
 struct Q408 {
+  static constexpr bool kSplit = false;
   struct W { u32 v[9]; };
   static __device__ __forceinline__ int items(int64_t k) { return (int)(k / 64); }
   static __device__ __forceinline__ int64_t group(int item) { return 2 * (int64_t)item; }
@@ -184,6 +186,7 @@ struct Q408 {
 // taken unsigned and 32 times the activation code sum of each 16-value run removed, the same integer as the
 // reference's signed codes q - 32 (iq_dot, S/gen_llm.py:1036-1044): per group (ilo s0 + ihi s1) da, s = d sc.
 struct Q6K8 {
+  static constexpr bool kSplit = false;
   using W = Q6W;
   static __device__ __forceinline__ int items(int64_t k) { return (int)(k / 256) * 4; }
   static __device__ __forceinline__ int64_t group(int item) { return 2 * (int64_t)item; }
@@ -215,6 +218,61 @@ struct Q6K8 {
   }
 };
 
+// MXFP4 split planes, the reference's opt-in int8 decode (MXFP4S_Q8, S/formats.py:26-28; @g_mxfp4s_icodes,
+// S/gen_mxfp4s.py:1113-1160): a 32-value block's signed codes c = 2 x its E2M1 values (0 1 2 3 4 6 8 12 and their
+// negatives; -0 is 0) and d = 2^(e - 128) from its E8M0 byte e (the codes carry the factor 2), so d c is the weight
+// exactly. The group's integer dot di = sum c q is exact (eight v_dot4 steps) and adds (d da) di, as the reference's
+// one-scale formats do (iq_dot, S/gen_llm.py:1047-1049). Item = blocks 2 p and 2 p + 1 of a row: 32 nibble bytes at
+// 32 p of the nibble plane, two E8M0 bytes at 2 p of the scale plane.
+__device__ __forceinline__ u32 e2m1x4_codes(u32 nb) {   // four E2M1 codes, one in each byte's low nibble
+  const u32 sel = nb & 0x07070707u;
+  const u32 pos = __builtin_amdgcn_perm(0x0C080604u, 0x03020100u, sel);   // bytes 0 1 2 3 4 6 8 12
+  const u32 neg = __builtin_amdgcn_perm(0xF4F8FAFCu, 0xFDFEFF00u, sel);   // bytes 0 -1 -2 -3 -4 -6 -8 -12
+  const u32 m = ((nb >> 3) & 0x01010101u) * 0xFFu;                        // 0xFF in the bytes with the sign bit
+  return (neg & m) | (pos & ~m);
+}
+
+__device__ __forceinline__ float e8m0_half(u32 e) {   // 2^(e - 128), exact (a subnormal for e < 2)
+  return u32_as_f32(e < 2 ? 0x00200000u << e : (e - 1) << 23);
+}
+
+// the exact integer dot of one block's 16 nibble bytes (byte j: values 2 j low, 2 j + 1 high) with 32 codes
+__device__ __forceinline__ int e2m1_block_dot(v4u nib, const u32 (&xq)[8]) {
+  const u32 b[4] = {nib.x, nib.y, nib.z, nib.w};
+  int acc = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const u32 lo = e2m1x4_codes(b[i] & 0x0F0F0F0Fu), hi = e2m1x4_codes((b[i] >> 4) & 0x0F0F0F0Fu);
+    acc = sdot4(__builtin_amdgcn_perm(hi, lo, 0x05010400u), xq[2 * i], acc);       // values 8 i .. 8 i + 3
+    acc = sdot4(__builtin_amdgcn_perm(hi, lo, 0x07030602u), xq[2 * i + 1], acc);   // values 8 i + 4 .. 8 i + 7
+  }
+  return acc;
+}
+
+struct MX4S8 {
+  static constexpr bool kSplit = true;
+  struct W { v4u a, b; u32 e; };
+  static __device__ __forceinline__ int items(int64_t k) { return (int)(k / 64); }
+  static __device__ __forceinline__ int64_t group(int item) { return 2 * (int64_t)item; }
+  static __device__ __forceinline__ void load_w(const u8 *row, const u8 *srow, int item, bool live, W &w) {
+    const v4u z{0u, 0u, 0u, 0u};
+    w.a = live ? *reinterpret_cast<const v4u *>(row + 32 * (int64_t)item) : z;
+    w.b = live ? *reinterpret_cast<const v4u *>(row + 32 * (int64_t)item + 16) : z;
+    w.e = live ? (u32) * reinterpret_cast<const u16 *>(srow + 2 * (int64_t)item) : 0u;
+  }
+  static __device__ __forceinline__ float dot(const W &w, const XQ &x, int) {
+    const int ia = e2m1_block_dot(w.a, x.a), ib = e2m1_block_dot(w.b, x.b);
+    return (e8m0_half(w.e & 255u) * x.da) * (float)ia + (e8m0_half(w.e >> 8) * x.db) * (float)ib;
+  }
+};
+
+// a row's weights of item `item`; split planes also read the row's scale plane srow
+template <class P>
+__device__ __forceinline__ void load_row(const u8 *row, const u8 *srow, int item, bool live, typename P::W &w) {
+  if constexpr (P::kSplit) P::load_w(row, srow, item, live, w);
+  else P::load_w(row, item, live, w);
+}
+
 constexpr int kWaves = 4;
 enum Mode { kPlain = 0, kSwiglu = 1, kPair = 2 };
 
@@ -225,6 +283,7 @@ template <class P, int TG, int MODE, int RW>
 __global__ __launch_bounds__(256) void mv_q8_kernel(int64_t n, int64_t tokens, int64_t k, int accumulate,
                                                     const u8 *__restrict__ codes, const float *__restrict__ meta,
                                                     const u8 *__restrict__ w, const u8 *__restrict__ w2, int64_t rb,
+                                                    const u8 *__restrict__ ws, const u8 *__restrict__ ws2, int64_t sb,
                                                     float *__restrict__ y, float *__restrict__ y2) {
   constexpr int NM = MODE == kPlain ? 1 : 2;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -253,7 +312,9 @@ __global__ __launch_bounds__(256) void mv_q8_kernel(int64_t n, int64_t tokens, i
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
-      for (int r = 0; r < RW; ++r) P::load_w((m ? w2 : w) + (row0 + r) * rb, item, live && (row0 + r) < n, wv[m][r]);
+      for (int r = 0; r < RW; ++r)
+        load_row<P>((m ? w2 : w) + (row0 + r) * rb, (m ? ws2 : ws) + (row0 + r) * sb, item, live && (row0 + r) < n,
+                    wv[m][r]);
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
@@ -295,7 +356,8 @@ __global__ __launch_bounds__(256) void expert_mv_q8_kernel(int64_t n, int64_t as
                                                            const int32_t *__restrict__ ids, const u8 *__restrict__ codes,
                                                            const float *__restrict__ meta, const u8 *__restrict__ w,
                                                            const u8 *__restrict__ w2, int64_t rb, int64_t ebytes,
-                                                           const float *__restrict__ bias,
+                                                           const u8 *__restrict__ ws, const u8 *__restrict__ ws2,
+                                                           int64_t sb, int64_t sebytes, const float *__restrict__ bias,
                                                            const float *__restrict__ bias2, int act,
                                                            float *__restrict__ y) {
   constexpr int RW = 4, NM = GU ? 2 : 1;
@@ -309,9 +371,13 @@ __global__ __launch_bounds__(256) void expert_mv_q8_kernel(int64_t n, int64_t as
   const int64_t G = k / 32;
   const u8 *xc = codes + xr * k;
   const float *xm = meta + 2 * xr * G;
-  const u8 *we[NM];
+  const u8 *we[NM], *se[NM];
   we[0] = w + e * ebytes;
-  if constexpr (GU) we[NM - 1] = w2 + e * ebytes;
+  se[0] = ws + e * sebytes;   // split planes: the expert's scale rows (unused otherwise)
+  if constexpr (GU) {
+    we[NM - 1] = w2 + e * ebytes;
+    se[NM - 1] = ws2 + e * sebytes;
+  }
   const int nitems = P::items(k);
   float acc[NM][RW];
 #pragma unroll
@@ -327,7 +393,8 @@ __global__ __launch_bounds__(256) void expert_mv_q8_kernel(int64_t n, int64_t as
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
-      for (int r = 0; r < RW; ++r) P::load_w(we[m] + (row0 + r) * rb, item, live && (row0 + r) < n, wv[m][r]);
+      for (int r = 0; r < RW; ++r)
+        load_row<P>(we[m] + (row0 + r) * rb, se[m] + (row0 + r) * sb, item, live && (row0 + r) < n, wv[m][r]);
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
@@ -557,14 +624,16 @@ namespace {
 // the generic (GGUF-layout, planar Q8_1) matvec of one format in one mode
 template <class P, int MODE>
 int launch_generic(int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, const void *w, const void *w2,
-                   int64_t rb, float *y, float *y2, hipStream_t s) {
+                   int64_t rb, float *y, float *y2, hipStream_t s, const void *ws = nullptr,
+                   const void *ws2 = nullptr) {
   constexpr int TG = 2, RW = MODE == kPlain ? 4 : 2;
   const u8 *codes = static_cast<const u8 *>(x);
   const float *meta = reinterpret_cast<const float *>(codes + tokens * k);
   const dim3 grid((unsigned)((tokens + TG - 1) / TG), (unsigned)((n + kWaves * RW - 1) / (kWaves * RW)));
   if (grid.x > 2147483647u || grid.y > 65535u) return QMM_ERR_SHAPE;
   mv_q8_kernel<P, TG, MODE, RW><<<grid, 256, 0, s>>>(n, tokens, k, accumulate, codes, meta, static_cast<const u8 *>(w),
-                                                    static_cast<const u8 *>(w2), rb, y, y2);
+                                                    static_cast<const u8 *>(w2), rb, static_cast<const u8 *>(ws),
+                                                    static_cast<const u8 *>(ws2), k / 32, y, y2);
   return launch_status();
 }
 
@@ -642,7 +711,9 @@ namespace {
 template <class P>
 int launch_expert_q8(bool gu, int64_t k, int64_t n, int E, int KU, int64_t assignments, const int32_t *ids,
                      const void *x, const void *w, const void *w2, int64_t rb, int64_t ebytes, const float *bias,
-                     const float *bias2, int act, float *y, hipStream_t s) {
+                     const float *bias2, int act, float *y, hipStream_t s, const void *ws = nullptr,
+                     const void *ws2 = nullptr, int64_t sebytes = 0) {
+  const u8 *s1 = static_cast<const u8 *>(ws), *s2 = static_cast<const u8 *>(ws2);
   const int64_t x_rows = gu ? assignments / KU : assignments;
   const u8 *codes = static_cast<const u8 *>(x);
   const float *meta = reinterpret_cast<const float *>(codes + x_rows * k);
@@ -651,11 +722,11 @@ int launch_expert_q8(bool gu, int64_t k, int64_t n, int E, int KU, int64_t assig
   if (gu)
     expert_mv_q8_kernel<P, true><<<grid, 256, 0, s>>>(n, assignments, KU, E, k, ids, codes, meta,
                                                       static_cast<const u8 *>(w), static_cast<const u8 *>(w2), rb,
-                                                      ebytes, bias, bias2, act, y);
+                                                      ebytes, s1, s2, k / 32, sebytes, bias, bias2, act, y);
   else
     expert_mv_q8_kernel<P, false><<<grid, 256, 0, s>>>(n, assignments, KU, E, k, ids, codes, meta,
-                                                       static_cast<const u8 *>(w), nullptr, rb, ebytes, bias, nullptr,
-                                                       act, y);
+                                                       static_cast<const u8 *>(w), nullptr, rb, ebytes, s1, nullptr,
+                                                       k / 32, sebytes, bias, nullptr, act, y);
   return launch_status();
 }
 }  // namespace
@@ -687,4 +758,52 @@ extern "C" int qmm_moe_expert_mv_q8(int fmt, int mode, int fused, int act, int64
   if (fmt == QMM_Q6_K)
     return launch_expert_q8<Q6K8>(gu, k, n, E, KU, assignments, ids, x, w, wu, rb, ebytes, bias, bias2, act, y, s);
   return launch_expert_q8<Q408>(gu, k, n, E, KU, assignments, ids, x, w, wu, rb, ebytes, bias, bias2, act, y, s);
+}
+
+// The opt-in int8 decode of MXFP4 split planes (MXFP4S_Q8, S/formats.py:26-28): g_mv_mxfp4s_k{K}[_swiglu|_pair]
+// [_t{TG}]_q8 (S/gen_llm.py:1288-1301 with @g_mxfp4s_icodes, S/gen_mxfp4s.py:1113-1160) and the MOE_Q8 expert
+// matvecs of mxfp4s experts (S/gen_moe.py:535-727), over the generic item walk (MX4S8).
+extern "C" int qmm_mv_mxfp4s_q8(int mode, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x,
+                                int x_dtype, const void *w, const void *ws, const void *w2, const void *ws2, float *y,
+                                float *y2, qmm_stream_t stream) {
+  if (mode != kPlain && mode != kSwiglu && mode != kPair) return QMM_ERR_RANGE;
+  if (!x || !w || !ws || !y) return QMM_ERR_NULL;
+  if (mode != kPlain && (!w2 || !ws2)) return QMM_ERR_NULL;
+  if (mode == kPair && !y2) return QMM_ERR_NULL;
+  if (x_dtype != QMM_Q8) return QMM_ERR_DTYPE;   // the planar Q8_1 buffer of qmm_quant_q8
+  if (k <= 0 || n <= 0 || tokens <= 0 || k % 64 || n > (1ll << 30) || tokens > (1ll << 24) || k > (1ll << 20))
+    return QMM_ERR_SHAPE;
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(ws, 2) || (w2 && !aligned(w2, 16)) || (ws2 && !aligned(ws2, 2)) ||
+      !aligned(y, 4) || (y2 && !aligned(y2, 4)))
+    return QMM_ERR_ALIGN;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t rb = k / 2;
+  if (mode == kSwiglu) return launch_generic<MX4S8, kSwiglu>(k, n, tokens, accumulate, x, w, w2, rb, y, nullptr, s, ws, ws2);
+  if (mode == kPair) return launch_generic<MX4S8, kPair>(k, n, tokens, accumulate, x, w, w2, rb, y, y2, s, ws, ws2);
+  return launch_generic<MX4S8, kPlain>(k, n, tokens, accumulate, x, w, nullptr, rb, y, nullptr, s, ws, nullptr);
+}
+
+extern "C" int qmm_moe_expert_mv_mxfp4s_q8(int mode, int fused, int act, int64_t k, int64_t n, int E, int KU,
+                                           int64_t assignments, const int32_t *ids, const void *x, const void *w,
+                                           const void *ws, const void *w2, const void *ws2, const float *bias,
+                                           const float *bias2, float *y, qmm_stream_t stream) {
+  if (mode != 0 && mode != 1) return QMM_ERR_RANGE;
+  if (act != QMM_ACT_SILU && act != QMM_ACT_SWIGLU_OAI) return QMM_ERR_RANGE;
+  if (E <= 0 || E > 1024 || KU <= 0 || KU > 8) return QMM_ERR_RANGE;
+  if (!ids || !x || !w || !ws || !y) return QMM_ERR_NULL;
+  const bool gu = mode == 0;
+  if (gu && !fused && (!w2 || !ws2)) return QMM_ERR_NULL;
+  if (k <= 0 || k % 64 || n <= 0 || assignments <= 0 || assignments > (1 << 24) || n > (1 << 24) || k > (1 << 20))
+    return QMM_ERR_SHAPE;
+  if (gu && assignments % KU) return QMM_ERR_SHAPE;
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(ws, 2) || (w2 && !aligned(w2, 16)) || (ws2 && !aligned(ws2, 2)) ||
+      !aligned(y, 4) || !aligned(bias, 4) || !aligned(bias2, 4))
+    return QMM_ERR_ALIGN;
+  // a fused [E, 2n, k] gate_up tensor (both planes): expert e's n gate rows, then its n up rows
+  const int64_t rb = k / 2, sb = k / 32;
+  const int64_t ebytes = rb * n * (gu && fused ? 2 : 1), sebytes = sb * n * (gu && fused ? 2 : 1);
+  const void *wu = gu && fused ? static_cast<const void *>(static_cast<const u8 *>(w) + rb * n) : w2;
+  const void *wsu = gu && fused ? static_cast<const void *>(static_cast<const u8 *>(ws) + sb * n) : ws2;
+  return launch_expert_q8<MX4S8>(gu, k, n, E, KU, assignments, ids, x, w, wu, rb, ebytes, bias, bias2, act, y,
+                                 reinterpret_cast<hipStream_t>(stream), ws, wsu, sebytes);
 }

@@ -36,6 +36,9 @@ SIGNATURES = {
     "qmm_gemm_mxfp4": [c_int, c_int, c_i64, c_i64, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_vp],
     "qmm_mv_swiglu_q8": [c_int, c_i64, c_i64, c_i64, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_vp],
     "qmm_mv_pair_q8": [c_int, c_i64, c_i64, c_i64, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp],
+    "qmm_mv_mxfp4s_q8": [c_int, c_i64, c_i64, c_i64, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
+    "qmm_moe_expert_mv_mxfp4s_q8": [c_int, c_int, c_int, c_i64, c_i64, c_int, c_int, c_i64, c_vp, c_vp, c_vp, c_vp,
+                                    c_vp, c_vp, c_vp, c_vp, c_vp, c_vp],
     "qmm_moe_expert_mv_q8": [c_int, c_int, c_int, c_int, c_i64, c_i64, c_int, c_int, c_i64, c_vp, c_vp, c_vp, c_vp,
                              c_vp, c_vp, c_vp, c_vp],
     "qmm_moe_route": [c_i64, c_i64, c_int, c_int, c_int, c_int, c_float, c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_vp,

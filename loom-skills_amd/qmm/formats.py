@@ -60,10 +60,11 @@ def _opt_in(name):
 
 
 # The formats whose decode takes int8 (Q8_1) activations by default: the reference's formats.ICODES (S/formats.py:20-30)
-# restricted to the formats here. Q4_K and Q6_K always; Q4_0 only with Q4_0_Q8=1, the reference's own opt-in switch
-# (llama.cpp's vec_dot_q4_0_q8_1 arithmetic); the tiled layouts follow their format, except that the tiled Q4_0 layout
-# has no other decode kernel than the int8 one.
-ICODES = frozenset({"q4_k", "q6_k"} | ({"q4_0"} if _opt_in("Q4_0_Q8") else set()))
+# restricted to the formats here. Q4_K and Q6_K always; Q4_0 only with Q4_0_Q8=1 and MXFP4 split planes only with
+# MXFP4S_Q8=1, the reference's own opt-in switches (llama.cpp's vec_dot_q4_0_q8_1 arithmetic; @g_mxfp4s_icodes); the
+# tiled layouts follow their format, except that the tiled Q4_0 layout has no other decode kernel than the int8 one.
+ICODES = frozenset({"q4_k", "q6_k"} | ({"q4_0"} if _opt_in("Q4_0_Q8") else set())
+                   | ({"mxfp4s"} if _opt_in("MXFP4S_Q8") else set()))
 
 
 def decode_q8(fmt):

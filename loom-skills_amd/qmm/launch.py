@@ -195,7 +195,13 @@ class Launcher:
         if q8:
             kf = "q4_kt" if fmt == "q4_k" and self.cfg.tiled_q4k else fmt
             xd = _dt(x)
-            if variant == "swiglu":
+            if fmt == "mxfp4s":   # (w, ws): the opt-in int8 matvec of split planes (MXFP4S_Q8, S/formats.py:26-28)
+                if variant or w2 is None:
+                    raise KeyError(f"{name!r}: split-plane matvecs take (w, ws) and have no swiglu / pair form "
+                                   "(S/gen_llm.py:1183-1184)")
+                _lib.call("qmm_mv_mxfp4s_q8", 0, k, n, tokens, acc, _p(x), xd, _p(w), _p(w2), None, None, _p(y), None,
+                          _s())
+            elif variant == "swiglu":
                 _lib.call("qmm_mv_swiglu_q8", CODE[kf], k, n, tokens, acc, _p(x), xd, _p(w), _p(w2), _p(y), _s())
             elif variant == "pair":
                 _lib.call("qmm_mv_pair_q8", CODE[kf], k, n, tokens, acc, _p(x), xd, _p(w), _p(w2), _p(y), _p(y2), _s())
@@ -282,11 +288,12 @@ class Launcher:
             bg, bu = (a[5] if len(a) == 7 else None), None
         y = a[-1]
         m, act = (0 if gu else 1), ACT[self.cfg.act]
+        if fmt == "mxfp4s":
+            raise KeyError(f"{name!r}: split-plane expert weights come with their scale planes (ops.moe_expert_mv, "
+                           "ops.moe_expert_mv_q8)")
         if q8:
             _lib.call("qmm_moe_expert_mv_q8", CODE[fmt], m, int(fused), act, k, n, E, KU, ta, _p(ids), _p(x), _p(w),
                       _p(None if fused else w2), _p(bg), _p(bu), _p(y), _s())
-        elif fmt == "mxfp4s":
-            raise KeyError(f"{name!r}: split-plane expert weights come with their scale planes (ops.moe_expert_mv)")
         else:
             _lib.call("qmm_moe_expert_mv", _fcode(f), m, int(fused), act, k, n, E, KU, ta, _p(ids), _p(x),
                       ops._dt(x), _p(w), _p(None if fused else w2), _p(bg), _p(bu), _p(y), _s())

@@ -132,16 +132,28 @@ def quant_q8(x, xq=None):
     return xq
 
 
-def mv_q8(fmt, w, x, n, k, tokens=None, y=None, accumulate=False):
+def mv_q8(fmt, w, x, n, k, tokens=None, y=None, accumulate=False, ws=None):
     """The int8-activation decode matvec (g_mv_{fmt}_k{K}[_t{TG}]_q8, S/gen_llm.py:1288-1301): x is the planar Q8_1
     buffer of `tokens` rows (uint8, from quant_q8), or f32 / bf16 rows [tokens, k], which the Q4_K K = 4096 / 8192
     and (up to two tokens) tiled-layout q4_kt / q4_0t kernels quantize themselves and any other call quantizes through
-    quant_q8 first (identical results)."""
-    _dev(w, x, y)
+    quant_q8 first (identical results). mxfp4s (the reference's opt-in MXFP4S_Q8): w the nibble plane, ws the E8M0
+    plane."""
+    _dev(w, ws, x, y)
     x, xd, tokens = _q8_input(fmt, x, k, tokens, staged_tokens=2)
     y = _out(y, (tokens, n), torch.float32, w.device, accumulate)
+    if fmt == "mxfp4s":
+        _split_q8(0, k, n, tokens, accumulate, x, xd, w, ws, None, None, y, None)
+        return y
     _lib.call("qmm_mv_q8", CODE[fmt], k, n, tokens, int(bool(accumulate)), _ptr(x), xd, _ptr(w), _ptr(y), _stream())
     return y
+
+
+def _split_q8(mode, k, n, tokens, accumulate, x, xd, w, ws, w2, ws2, y, y2):
+    """qmm_mv_mxfp4s_q8: the int8 matvecs of MXFP4 split planes (mode 0 plain, 1 swiglu, 2 pair)."""
+    if ws is None or (mode and ws2 is None):
+        raise ValueError("mxfp4s weights need their E8M0 scale planes (ws / ws2)")
+    _lib.call("qmm_mv_mxfp4s_q8", mode, k, n, tokens, int(bool(accumulate)), _ptr(x), xd, _ptr(w), _ptr(ws), _ptr(w2),
+              _ptr(ws2), _ptr(y), _ptr(y2), _stream())
 
 
 TILED_Q8 = ("q4_kt", "q4_0t")   # the tiled layouts of the int8 matvec, which quantize f32 / bf16 rows themselves
@@ -167,25 +179,32 @@ def _q8_input(fmt, x, k, tokens, staged_tokens):
     return quant_q8(x), DTYPE["q8"], tokens
 
 
-def mv_swiglu_q8(fmt, w, w2, x, n, k, tokens=None, y=None, accumulate=False):
+def mv_swiglu_q8(fmt, w, w2, x, n, k, tokens=None, y=None, accumulate=False, ws=None, ws2=None):
     """The int8 swiglu matvec y (+)= silu(x W^T) (x W2^T) (g_mv_{fmt}_k{K}_swiglu[_t{TG}]_q8): gate W and up W2
     [n, k]; x a planar Q8_1 buffer (with tokens) or f32 / bf16 rows (quantized as quant_q8 does). fmt q4_kt / q4_0t
-    (tiled layouts) or GGUF q4_k / q4_0 / q6_k. Returns y f32 [tokens, n]."""
-    _dev(w, w2, x, y)
+    (tiled layouts), GGUF q4_k / q4_0 / q6_k, or mxfp4s with ws / ws2 the scale planes. Returns y f32 [tokens, n]."""
+    _dev(w, w2, ws, ws2, x, y)
     x, xd, tokens = _q8_input(fmt, x, k, tokens, staged_tokens=2 if fmt in TILED_Q8 else 0)
     y = _out(y, (tokens, n), torch.float32, w.device, accumulate)
+    if fmt == "mxfp4s":
+        _split_q8(1, k, n, tokens, accumulate, x, xd, w, ws, w2, ws2, y, None)
+        return y
     _lib.call("qmm_mv_swiglu_q8", CODE[fmt], k, n, tokens, int(bool(accumulate)), _ptr(x), xd, _ptr(w), _ptr(w2),
               _ptr(y), _stream())
     return y
 
 
-def mv_pair_q8(fmt, w, w2, x, n, k, tokens=None, y=None, y2=None, accumulate=False):
+def mv_pair_q8(fmt, w, w2, x, n, k, tokens=None, y=None, y2=None, accumulate=False, ws=None, ws2=None):
     """Two int8 matvecs of one input in one launch (g_mv_{fmt}_k{K}_pair[_t{TG}]_q8): y (+)= x W^T, y2 (+)= x W2^T,
-    each equal bit for bit to the one-matrix kernel's of the same layout. Returns (y, y2) f32 [tokens, n]."""
-    _dev(w, w2, x, y, y2)
+    each equal bit for bit to the one-matrix kernel's of the same layout (mxfp4s: ws / ws2 the scale planes).
+    Returns (y, y2) f32 [tokens, n]."""
+    _dev(w, w2, ws, ws2, x, y, y2)
     x, xd, tokens = _q8_input(fmt, x, k, tokens, staged_tokens=2 if fmt in TILED_Q8 else 0)
     y = _out(y, (tokens, n), torch.float32, w.device, accumulate)
     y2 = _out(y2, (tokens, n), torch.float32, w.device, accumulate)
+    if fmt == "mxfp4s":
+        _split_q8(2, k, n, tokens, accumulate, x, xd, w, ws, w2, ws2, y, y2)
+        return y, y2
     _lib.call("qmm_mv_pair_q8", CODE[fmt], k, n, tokens, int(bool(accumulate)), _ptr(x), xd, _ptr(w), _ptr(w2),
               _ptr(y), _ptr(y2), _stream())
     return y, y2
@@ -342,11 +361,12 @@ def moe_expert_mv(fmt, mode, ids, x, w, n, k, E, KU, w2=None, ws=None, ws2=None,
 
 
 def moe_expert_mv_q8(fmt, mode, ids, x, w, n, k, E, KU, w2=None, fused=False, act="silu", bias=None, bias2=None,
-                     y=None, x_rows=None):
+                     y=None, x_rows=None, ws=None, ws2=None):
     """Decode expert matvecs on Q8_1 activations (g_moe_gu_{fmt}[_fused]_q8_k{H}_r{R} / g_moe_dn_{fmt}_q8_k{FE}_r{R}):
     x is the planar Q8_1 buffer of x_rows rows (gu: the tokens, dn: the assignments), or f32 / bf16 rows quantized
-    here first (quant_q8). fmt q4_k / q4_0 / q6_k. Returns y f32 [assignments, n]."""
-    _dev(ids, x, w, w2, bias, bias2, y)
+    here first (quant_q8). fmt q4_k / q4_0 / q6_k, or mxfp4s (the reference's opt-in MXFP4S_Q8) with ws / ws2 the
+    scale planes. Returns y f32 [assignments, n]."""
+    _dev(ids, x, w, w2, ws, ws2, bias, bias2, y)
     A = ids.numel()
     rows = A // KU if mode == "gu" else A
     if x.dtype != torch.uint8:
@@ -358,6 +378,13 @@ def moe_expert_mv_q8(fmt, mode, ids, x, w, n, k, E, KU, w2=None, fused=False, ac
         raise ValueError(f"the planar Q8_1 buffer holds {x.numel()} bytes, {rows} rows of K {k} need "
                          f"{q8_bytes(rows, k)}")
     y = _out(y, (A, n), torch.float32, x.device)
+    if fmt == "mxfp4s":
+        if ws is None or (mode == "gu" and not fused and ws2 is None):
+            raise ValueError("mxfp4s experts need their E8M0 scale planes (ws / ws2)")
+        _lib.call("qmm_moe_expert_mv_mxfp4s_q8", {"gu": 0, "dn": 1}[mode], int(fused), ACT[act], k, n, E, KU, A,
+                  _ptr(ids), _ptr(x), _ptr(w), _ptr(ws), _ptr(w2), _ptr(ws2), _ptr(bias), _ptr(bias2), _ptr(y),
+                  _stream())
+        return y
     _lib.call("qmm_moe_expert_mv_q8", CODE[fmt], {"gu": 0, "dn": 1}[mode], int(fused), ACT[act], k, n, E, KU, A,
               _ptr(ids), _ptr(x), _ptr(w), _ptr(w2), _ptr(bias), _ptr(bias2), _ptr(y), _stream())
     return y
@@ -626,7 +653,7 @@ def moe_prefill(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up
     return y, mid
 
 
-Q8_FORMATS = ("q4_0", "q4_k", "q6_k")   # formats with integer-code expert matvecs (the kernels exist)
+Q8_FORMATS = ("q4_0", "q4_k", "q6_k", "mxfp4s")   # formats with integer-code expert matvecs (the kernels exist)
 
 
 def _moe_q8(q8, fmt, fmt_down, expert_bias):
@@ -650,9 +677,9 @@ def moe_decode(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=
     tensor's format when it differs (Q4_K_M files: Q4_K gate / up, Q6_K down, S/gen_llm.py:5336-5340).
     q8: the int8-activation chain (the reference's MOE_Q8 default, S/gen_llm.py:5290-5303, :5381-5383): x is
     quantized to Q8_1 once, the gate/up matvecs contract integer codes, their output is quantized again (g_quant_q8)
-    for the down matvecs; formats q4_0 / q4_k / q6_k. "auto" (the default) takes it where the reference does: both
-    formats have integer codes and the experts have no biases (gen_llm.moe_iq, S/gen_llm.py:5296-5303); False keeps
-    the f32 / bf16 activations (the reference's MOE_Q8=0).
+    for the down matvecs; formats q4_0 / q4_k / q6_k / mxfp4s. "auto" (the default) takes it where the reference
+    does: both formats in its int8 set (formats.ICODES) and the experts without biases (gen_llm.moe_iq,
+    S/gen_llm.py:5296-5303); False keeps the f32 / bf16 activations (the reference's MOE_Q8=0).
     Returns (y f32 [T, H], intermediates dict)."""
     fd = fmt_down or gate_format(fmt)
     q8 = _moe_q8(q8, fmt, fd, expert_bias)
@@ -674,8 +701,8 @@ def moe_decode(fmt, x, logits, E, KU, H, FE, gating, norm, w_gate, w_down, w_up=
     if q8:
         xq = quant_q8(x)
         a = moe_expert_mv_q8(fmt, "gu", ids, xq, w_gate, FE, H, E, KU, w2=w_up, fused=fused, act=act, bias=bg,
-                             bias2=bu)
-        ys = moe_expert_mv_q8(fd, "dn", ids, quant_q8(a), w_down, H, FE, E, KU, bias=bd)
+                             bias2=bu, ws=ws_gate, ws2=ws_up)
+        ys = moe_expert_mv_q8(fd, "dn", ids, quant_q8(a), w_down, H, FE, E, KU, bias=bd, ws=ws_down)
         y = moe_combine(ys, wts, y=y, accumulate=y is not None, sg=sg)
         return y, {"ids": ids, "wts": wts, "logits": logits, "act": a, "ys": ys}
     a = moe_expert_mv(fmt, "gu", ids, x, w_gate, FE, H, E, KU, w2=w_up, ws=ws_gate, ws2=ws_up, fused=fused, act=act,
@@ -691,7 +718,7 @@ GEMM_MIN_TOKENS = 64   # %gemm: epochs of 64+ tokens take the GEMM / grouped cha
 
 
 # formats with int8-activation decode matvecs (their kernels exist); linear takes them by default for decode_q8(fmt)
-LINEAR_Q8_FORMATS = ("q4_0", "q4_k", "q4_kt", "q6_k", "q4_0t")
+LINEAR_Q8_FORMATS = ("q4_0", "q4_k", "q4_kt", "q6_k", "q4_0t", "mxfp4s")
 
 
 def linear(fmt, x, w, n, k, y=None, mode="store", ws=None, w2=None, ws2=None, q8="auto"):
@@ -701,8 +728,8 @@ def linear(fmt, x, w, n, k, y=None, mode="store", ws=None, w2=None, ws2=None, q8
     go through split_planes, repacked once per weight tensor), else the decode GEMV. The decode GEMV takes Q8_1
     activations where the reference does by default (ACT_Q8, iq = ACT_Q8 and fmt in IQ_FMTS and K / 32 <= 1024,
     S/gen_llm.py:514-519, :4590): Q4_K and Q6_K (and the tiled q4_kt), Q4_0 with the reference's Q4_0_Q8=1 switch,
-    and the tiled q4_0t always (formats.decode_q8); q8=True also takes it for q4_0; q8=False keeps f32 / bf16
-    activations (ACT_Q8=0). y is f32."""
+    MXFP4 split planes with MXFP4S_Q8=1, and the tiled q4_0t always (formats.decode_q8); q8=True also takes it for
+    q4_0 and mxfp4s; q8=False keeps f32 / bf16 activations (ACT_Q8=0). y is f32."""
     if mode not in ("store", "acc", "swiglu"):
         raise ValueError(f"linear mode {mode}")
     if mode == "swiglu" and w2 is None:
@@ -717,8 +744,8 @@ def linear(fmt, x, w, n, k, y=None, mode="store", ws=None, w2=None, ws2=None, q8
     iq = decode_q8(fmt) if q8 == "auto" else bool(q8) and fmt in LINEAR_Q8_FORMATS
     if iq and k // 32 <= 1024:
         if mode == "swiglu":
-            return mv_swiglu_q8(fmt, w, w2, x, n, k, y=y)
-        return mv_q8(fmt, w, x, n, k, y=y, accumulate=mode == "acc")
+            return mv_swiglu_q8(fmt, w, w2, x, n, k, y=y, ws=ws, ws2=ws2)
+        return mv_q8(fmt, w, x, n, k, y=y, accumulate=mode == "acc", ws=ws)
     if mode == "swiglu":
         return mv_swiglu(fmt, w, w2, x, n, k, y=y)
     return mv(fmt, w, x, n, k, y=y, accumulate=mode == "acc", ws=ws)

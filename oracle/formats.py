@@ -131,6 +131,16 @@ def dequant_mxfp4s(nibbles, scales, rows, k):
     return (v.reshape(rows, -1, 32) * s[:, :, None]).reshape(rows, k).astype(np.float32)
 
 
+def mxfp4s_icodes(nibbles16, e):
+    """@g_mxfp4s_icodes (S/gen_mxfp4s.py:1113-1160), the weight side of the reference's opt-in int8 decode of MXFP4
+    split planes (MXFP4S_Q8): a 32-value block's 16 nibble bytes (pairs order: value 2j is the low nibble of byte j,
+    2j+1 the high nibble) give signed codes kvalues_mxfp4 (twice the E2M1 values; code 8 is 0), and its E8M0 byte e
+    the block scale 2^(e - 128) (the codes carry the factor 2). Returns (codes int8 [32], d f32)."""
+    b = np.asarray(nibbles16, np.uint8).reshape(16)
+    codes = np.stack([KVALUES_MXFP4[b & 15], KVALUES_MXFP4[b >> 4]], axis=-1).reshape(32)
+    return codes, e8m0_half_scale(np.uint8(e))[()]
+
+
 def mxfp4_to_split(raw, rows, k):
     """GGUF MXFP4 blocks -> (nibbles [rows, K/2] pairs order, scales [rows, K/32]): the same codes and exponents in
     the split-plane layout (S/formats.py:12-15). Values are preserved except that code 8 reads as -0 in the split

@@ -245,6 +245,21 @@ def test_argument_validation_without_a_device(lib):
         == st["QMM_ERR_NULL"]                                                  # gu, not fused: the up tensor
     assert lib.qmm_moe_expert_mv_q8(0, 1, 0, 0, 96, 16, 4, 2, 4, fake, fake, fake, n, n, n, fake, n) \
         == st["QMM_ERR_SHAPE"]                                                 # Q4_0: K % 64
+    # the opt-in int8 matvecs of MXFP4 split planes: modes 0..2, the scale planes, planar Q8_1 input, K % 64
+    mq = lib.qmm_mv_mxfp4s_q8
+    assert mq(3, 256, 16, 1, 0, fake, 4, fake, fake, n, n, fake, n, n) == st["QMM_ERR_RANGE"]
+    assert mq(0, 256, 16, 1, 0, fake, 4, fake, n, n, n, fake, n, n) == st["QMM_ERR_NULL"]      # ws
+    assert mq(1, 256, 16, 1, 0, fake, 4, fake, fake, fake, n, fake, n, n) == st["QMM_ERR_NULL"]  # ws2
+    assert mq(2, 256, 16, 1, 0, fake, 4, fake, fake, fake, fake, fake, n, n) == st["QMM_ERR_NULL"]   # y2
+    assert mq(0, 256, 16, 1, 0, fake, 0, fake, fake, n, n, fake, n, n) == st["QMM_ERR_DTYPE"]
+    assert mq(0, 96, 16, 1, 0, fake, 4, fake, fake, n, n, fake, n, n) == st["QMM_ERR_SHAPE"]
+    assert mq(0, 256, 16, 1, 0, fake, 4, odd, fake, n, n, fake, n, n) == st["QMM_ERR_ALIGN"]
+    me = lib.qmm_moe_expert_mv_mxfp4s_q8
+    assert me(2, 0, 0, 256, 16, 4, 2, 4, fake, fake, fake, fake, n, n, n, n, fake, n) == st["QMM_ERR_RANGE"]
+    assert me(0, 1, 0, 256, 16, 4, 2, 4, fake, fake, fake, n, n, n, n, n, fake, n) == st["QMM_ERR_NULL"]   # ws
+    assert me(0, 0, 0, 256, 16, 4, 2, 4, fake, fake, fake, fake, fake, n, n, n, fake, n) == st["QMM_ERR_NULL"]
+    assert me(1, 0, 0, 96, 16, 4, 2, 4, fake, fake, fake, fake, n, n, n, n, fake, n) == st["QMM_ERR_SHAPE"]
+    assert me(0, 1, 0, 256, 16, 4, 2, 3, fake, fake, fake, fake, n, n, n, n, fake, n) == st["QMM_ERR_SHAPE"]
     # the prefill GEMM on Q4_0: K % 256
     assert lib.qmm_gemm(0, 0, 64, 128, 64, fake, 1, n, fake, n, fake, 0, n) == st["QMM_ERR_SHAPE"]
     # decode swiglu matvec: GGUF-layout weights only, both matrices; the GEMM's swiglu mode needs the up matrix
@@ -344,21 +359,25 @@ def test_python_surface_refuses_host_tensors():
 
 
 def test_decode_int8_defaults_follow_the_reference():
-    """The decode matvecs take int8 activations by default for the reference's ICODES formats (Q4_K, Q6_K; Q4_0 only
-    with its Q4_0_Q8=1 switch, S/formats.py:20-30), the tiled layouts with their format, the tiled Q4_0 always."""
+    """The decode matvecs take int8 activations by default for the reference's ICODES formats (Q4_K, Q6_K; Q4_0 and
+    MXFP4 split planes only with their Q4_0_Q8=1 / MXFP4S_Q8=1 switches, S/formats.py:20-30), the tiled layouts with
+    their format, the tiled Q4_0 always."""
     import importlib
     import os
     from qmm import formats
     assert formats.decode_q8("q4_k") and formats.decode_q8("q6_k") and formats.decode_q8("q4_kt")
     assert formats.decode_q8("q4_0t")
-    assert not formats.decode_q8("mxfp4") and not formats.decode_q8("mxfp4s")
-    old = os.environ.pop("Q4_0_Q8", None)
-    try:
-        assert not importlib.reload(formats).decode_q8("q4_0")
-        os.environ["Q4_0_Q8"] = "1"
-        assert importlib.reload(formats).decode_q8("q4_0")
-    finally:
-        os.environ.pop("Q4_0_Q8", None)
-        if old is not None:
-            os.environ["Q4_0_Q8"] = old
-        importlib.reload(formats)
+    for fmt, switch in (("q4_0", "Q4_0_Q8"), ("mxfp4s", "MXFP4S_Q8")):   # the reference's opt-in switches
+        old = os.environ.pop(switch, None)
+        try:
+            assert not importlib.reload(formats).decode_q8(fmt)
+            os.environ[switch] = "1"
+            assert importlib.reload(formats).decode_q8(fmt)
+            os.environ[switch] = "off"
+            assert not importlib.reload(formats).decode_q8(fmt)
+        finally:
+            os.environ.pop(switch, None)
+            if old is not None:
+                os.environ[switch] = old
+            importlib.reload(formats)
+    assert not formats.decode_q8("mxfp4")

@@ -327,6 +327,28 @@ def mxfp4_ggml_scalar(raw):
     return out
 
 
+def test_mxfp4s_icodes_times_scale_is_the_weight_exactly():
+    """The int8 weight codes of the opt-in MXFP4S_Q8 decode (of.mxfp4s_icodes) against the split-plane dequantization:
+    codes x d equals the decoded value exactly for every nibble byte (all 16 x 16 low / high pairs, so every code in
+    both halves) and every E8M0 byte whose values stay finite in f32 (0 .. 250, both subnormal scale bytes included);
+    d itself is 2^(e - 128) for all 256 bytes. Negative control: the low / high nibbles swapped (the "split16" order of
+    GGUF blocks) breaks the equality."""
+    nib = np.arange(256, dtype=np.uint8)
+    for e in range(256):
+        assert of.mxfp4s_icodes(nib[:16], e)[1] == np.float32(np.ldexp(1.0, e - 128)), e
+    for e in range(251):
+        for b0 in range(0, 256, 16):
+            blk = nib[b0:b0 + 16]
+            codes, d = of.mxfp4s_icodes(blk, e)
+            got = codes.astype(np.float64) * np.float64(d)
+            want = of.dequant_mxfp4s(blk, np.array([e], np.uint8), 1, 32).reshape(32).astype(np.float64)
+            assert np.array_equal(got, want), (e, b0)
+    blk = nib[16:32]
+    codes, d = of.mxfp4s_icodes(blk, 127)
+    swapped = np.concatenate([codes[0::2], codes[1::2]]).astype(np.float64) * np.float64(d)
+    assert not np.array_equal(swapped, of.dequant_mxfp4s(blk, np.array([127], np.uint8), 1, 32).reshape(32))
+
+
 def test_mxfp4_gguf_matches_scalar_ggml_decoder_all_exponents():
     rng = np.random.default_rng(9)
     raw = np.empty((254 * 2, 17), np.uint8)
