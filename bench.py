@@ -16,7 +16,8 @@ one workload, or with --no-secondary):
     q4_k_gemv_q8_gguf the int8 GEMV reading the GGUF Q4_K blocks as they are
     q4_k_gemv   the Q4_K GEMV on the f16-activation path (x bf16 staged as f16, v_dot2_f32_f16)
     q4_k_gemv_q8p the int8 GEMV on its reference boundary: x is the planar Q8_1 buffer qmm_quant_q8 makes
-    q4_0_gemv   Q4_0 decode GEMV, W [4096, 4096], x f32 [1, 4096], y f32
+    q4_0_gemv   Q4_0 decode GEMV, W [4096, 4096], x f32 [1, 4096], y f32 (the weights repacked once into the tiled
+                layout; f32 activations, the reference's default Q4_0 decode)
     q4_0_gemv_q8 the same GEMV on the int8-activation path, the weights repacked once into the tiled layout
                 (qmm_tile_q40) the Q4_K int8 kernel streams
     q4_k_gemm   Q4_K prefill GEMM, x bf16 [512, 4096] (row scale to f16, then the MFMA GEMM), W [4096, 4096],
@@ -167,7 +168,7 @@ class GemvWorkload:
         elif self.q8:
             self.ops.mv_q8(self.kfmt, w, self.x, self.n, self.k, y=self.y)
         else:
-            self.ops.mv(self.fmt, w, self.x, self.n, self.k, y=self.y)
+            self.ops.mv(self.kfmt, w, self.x, self.n, self.k, y=self.y)
 
     @property
     def kernel_is_step(self):
@@ -557,7 +558,7 @@ def _q4k_gemv_q8p(m):
 
 def _q40_gemv(m):
     return GemvWorkload("q4_0_gemv", 0, "q4_0", 4096, 4096, m or 1, "f32",
-                        f"mv_kernel_q4_0.q4_0_gemv_n4096_k4096_m{m or 1}")
+                        f"mv_q40t_f32_kernel.q4_0_gemv_n4096_k4096_m{m or 1}", tiled=True)
 
 
 def _q40_gemv_q8(m):

@@ -349,8 +349,18 @@ int qmm_expert_mv_combine_tiled(int64_t k, int64_t n, int E, int KU, int64_t tok
                                 const float *wts, const void *x, int x_dtype, const void *w, const void *ws,
                                 const float *bias, int accumulate, const float *sg, float *y, hipStream_t s);
 
+int qmm_mv_q40t_f32(int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype, const void *w,
+                    float *y, hipStream_t s);
+
 extern "C" int qmm_mv(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
                       const void *w, const void *ws, float *y, qmm_stream_t stream) {
+  if (fmt == QMM_Q4_0T) {   // the tiled Q4_0 units of qmm_tile_q40 (gemv_q4kt.hip)
+    if (!x || !w || !y) return QMM_ERR_NULL;
+    if (x_dtype != QMM_F32 && x_dtype != QMM_BF16) return QMM_ERR_DTYPE;
+    if (n <= 0 || tokens <= 0 || k <= 0 || n > (1ll << 30) || k > (1ll << 20)) return QMM_ERR_SHAPE;
+    if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 4)) return QMM_ERR_ALIGN;
+    return qmm_mv_q40t_f32(k, n, tokens, accumulate, x, x_dtype, w, y, reinterpret_cast<hipStream_t>(stream));
+  }
   if (!valid_fmt(fmt)) return QMM_ERR_FORMAT;
   if (!x || !y) return QMM_ERR_NULL;
   if (n <= 0 || tokens <= 0 || row_bytes(fmt, k) == 0) return QMM_ERR_SHAPE;

@@ -343,6 +343,130 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mv_q4kt_q8_kernel(int64_t n, i
 }
 
 // the launch arguments of one call (the weights and outputs of the second matrix for swiglu / pair)
+// ------------------------------------------------------------------------- Q4_0 tiled, f32 / bf16 activations
+// The reference's default Q4_0 decode (its int8 path covers Q4_0 only with Q4_0_Q8=1, S/formats.py:20-30): the matvec
+// g_mv_q4_0_k{K}[_t{TG}] on f32 activations (S/gen_llm.py:1187-1197 with @g_q4_0_values, S/quant_values.loom:386-408)
+// over the tiled units (QMM_Q4_0T), with the int8 kernel's launch shape and lane map. Each wave stages its K slice of
+// every token in LDS as f32 with the sum of each 32-value block (four lanes' chunks, summed in a fixed tree); a lane
+// then contracts its four blocks (4 h .. 4 h + 3 of span sb of row r) with them, s = sum q x over the block's codes
+// 0..15 as f32 (one fma chain in value order), and adds d (s - 8 sum x): sum d (q - 8) x up to f32 rounding. The row's
+// four lanes meet in a butterfly, the waves in LDS in a fixed order, so a multi-token call equals one-token calls.
+template <int TG, int U, bool BF>
+__global__ __launch_bounds__(kMaxWaves * 64) void mv_q40t_f32_kernel(int64_t n, int64_t tokens, int64_t K,
+                                                                     int accumulate, const void *__restrict__ x,
+                                                                     const u8 *__restrict__ w, float *__restrict__ y) {
+  constexpr int SLICE = 512 * U, NB = SLICE / 32;
+  __shared__ __align__(16) float xs[kMaxWaves][TG][SLICE];
+  __shared__ float xsum[kMaxWaves][TG][NB];
+  __shared__ float red[kMaxWaves][16][TG];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NW = (int)(blockDim.x >> 6);
+  const int64_t t0 = (int64_t)blockIdx.y * TG;
+  const int64_t rb = blockIdx.x;
+  const int r = lane >> 2, sb = (lane >> 1) & 1, h = lane & 1;
+  const int64_t k0 = (int64_t)wave * SLICE;
+
+  // ---- the wave's activations (chunk c = lane + 64 j: 8 values), then its U units (a header and four planes each)
+  float xv[TG][U][8];
+#pragma unroll
+  for (int t = 0; t < TG; ++t) {
+    const int64_t tok = t0 + t < tokens ? t0 + t : tokens - 1;
+#pragma unroll
+    for (int j = 0; j < U; ++j) load8(x, BF, tok * K + k0 + 8 * (lane + 64 * j), xv[t][j]);
+  }
+  v4u wd[U][5];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const v4u *up = reinterpret_cast<const v4u *>(w + (rb * (K / 512) + (int64_t)wave * U + u) * kUnit);
+    wd[u][0] = up[lane >> 1];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) wd[u][1 + q] = up[32 + 64 * q + lane];
+  }
+#pragma unroll
+  for (int t = 0; t < TG; ++t)
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const int c = lane + 64 * j;
+      float4 *dst = reinterpret_cast<float4 *>(&xs[wave][t][8 * c]);
+      dst[0] = make_float4(xv[t][j][0], xv[t][j][1], xv[t][j][2], xv[t][j][3]);
+      dst[1] = make_float4(xv[t][j][4], xv[t][j][5], xv[t][j][6], xv[t][j][7]);
+      float bs = xv[t][j][0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) bs += xv[t][j][i];
+      bs += xshfl<1>(bs);
+      bs += xshfl<2>(bs);
+      if ((c & 3) == 0) xsum[wave][t][c >> 2] = bs;
+    }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // ---- math: block 4 h + blk of the span is page 2 h + blk / 2 (low nibbles for even blk, high for odd), its codes
+  //      16 half .. 16 half + 15 in plane 2 (blk / 2) + half
+  float part[TG];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const v4u hd = wd[u][0];
+    const u32 w0 = h ? hd.z : hd.x, w1 = h ? hd.w : hd.y;
+    const float d[4] = {f16_to_f32(w0), f16_to_f32(w0 >> 16), f16_to_f32(w1), f16_to_f32(w1 >> 16)};
+#pragma unroll
+    for (int t = 0; t < TG; ++t) {
+      float p = 0.f;
+#pragma unroll
+      for (int blk = 0; blk < 4; ++blk) {
+        const int base = 512 * u + 32 * (8 * sb + 4 * h + blk);   // the block's first value in the slice
+        float sq = 0.f;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const v4u pl = wd[u][1 + 2 * (blk >> 1) + half];
+          const u32 dw[4] = {pl.x, pl.y, pl.z, pl.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const u32 cq = (blk & 1 ? dw[i] >> 4 : dw[i]) & 0x0F0F0F0Fu;
+            const float4 xq = *reinterpret_cast<const float4 *>(&xs[wave][t][base + 16 * half + 4 * i]);
+            sq = __builtin_fmaf((float)((cq >> 0) & 255u), xq.x, sq);
+            sq = __builtin_fmaf((float)((cq >> 8) & 255u), xq.y, sq);
+            sq = __builtin_fmaf((float)((cq >> 16) & 255u), xq.z, sq);
+            sq = __builtin_fmaf((float)((cq >> 24) & 255u), xq.w, sq);
+          }
+        }
+        p += d[blk] * (sq - 8.f * xsum[wave][t][16 * u + 8 * sb + 4 * h + blk]);
+      }
+      part[t] = u == 0 ? p : part[t] + p;
+    }
+  }
+  // ---- the row's four lanes (h, then sb), then the waves in order
+#pragma unroll
+  for (int t = 0; t < TG; ++t) {
+    float v = part[t];
+    v += xshfl<1>(v);
+    v += xshfl<2>(v);
+    if ((lane & 3) == 0) red[wave][r][t] = v;
+  }
+  __syncthreads();
+  if (tid < 16 * TG) {
+    const int rr = tid / TG, t = tid % TG;
+    float tot = red[0][rr][t];
+    for (int wv = 1; wv < NW; ++wv) tot += red[wv][rr][t];
+    const int64_t row = 16 * rb + rr, tok = t0 + t;
+    if (row < n && tok < tokens) {
+      float *py = y + tok * n + row;
+      *py = accumulate ? *py + tot : tot;
+    }
+  }
+}
+
+template <int TG, int U>
+int launch_q40t_f32(int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, bool bf, const void *w,
+                    float *y, int nw, hipStream_t s) {
+  const dim3 grid((unsigned)(n / 16), (unsigned)((tokens + TG - 1) / TG));
+  if (bf)
+    mv_q40t_f32_kernel<TG, U, true><<<grid, nw * 64, 0, s>>>(n, tokens, k, accumulate, x, static_cast<const u8 *>(w), y);
+  else
+    mv_q40t_f32_kernel<TG, U, false><<<grid, nw * 64, 0, s>>>(n, tokens, k, accumulate, x, static_cast<const u8 *>(w),
+                                                              y);
+  return launch_status();
+}
+
 struct TArgs {
   int64_t n, tokens, k;
   int accumulate;
@@ -536,6 +660,23 @@ int qmm_mv_q4kt_q8(int fmt, int mode, int64_t k, int64_t n, int64_t tokens, int 
   return launch_mode<kPlain>(a, x_dtype, s);
 }
 
+
+// The f32 / bf16-activation matvec of the tiled Q4_0 layout (the qmm_mv path of QMM_Q4_0T): rows % 16 == 0,
+// K = 512 U NW with U <= 3 slices a wave (the staged slices fit a workgroup's LDS) and NW <= 8 waves; a workgroup a
+// (row block, token).
+int qmm_mv_q40t_f32(int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype, const void *w,
+                    float *y, hipStream_t s) {
+  if (n % 16 || k % 512 || n / 16 > 2147483647ll || tokens > 65535) return QMM_ERR_SHAPE;
+  const int64_t slices = k / 512;
+  int U = 1;
+  while (U <= 3 && (slices % U || slices / U > kMaxWaves)) ++U;
+  if (U > 3) return QMM_ERR_SHAPE;
+  const int nw = (int)(slices / U);
+  const bool bf = x_dtype == QMM_BF16;
+  if (U == 1) return launch_q40t_f32<1, 1>(k, n, tokens, accumulate, x, bf, w, y, nw, s);
+  return U == 2 ? launch_q40t_f32<1, 2>(k, n, tokens, accumulate, x, bf, w, y, nw, s)
+                : launch_q40t_f32<1, 3>(k, n, tokens, accumulate, x, bf, w, y, nw, s);
+}
 
 int qmm_dequant_q4kt(const void *w, int64_t rows, int64_t k, float *out, hipStream_t s) {
   if (rows % 16 || k % 256) return QMM_ERR_SHAPE;

@@ -199,7 +199,11 @@ def test_argument_validation_without_a_device(lib):
     assert lib.qmm_mv_q8(7, 768, 16, 1, 0, fake, 2, fake, fake, n) == st["QMM_ERR_SHAPE"]      # K % 512
     assert lib.qmm_dequant(7, fake, n, 16, 768, fake, n) == st["QMM_ERR_SHAPE"]
     assert lib.qmm_row_bytes(7, 4096) == 4096 // 32 * 18 and lib.qmm_row_bytes(7, 768) == 0
-    assert lib.qmm_mv(7, 4096, 16, 1, 0, fake, 0, fake, n, fake, n) == st["QMM_ERR_FORMAT"]    # the int8 matvec only
+    # the tiled Q4_0 f32-activation matvec: 16-row blocks, K % 512, x f32 / bf16
+    assert lib.qmm_mv(7, 4096, 24, 1, 0, fake, 0, fake, n, fake, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_mv(7, 4000, 16, 1, 0, fake, 0, fake, n, fake, n) == st["QMM_ERR_SHAPE"]
+    assert lib.qmm_mv(7, 4096, 16, 1, 0, fake, 4, fake, n, fake, n) == st["QMM_ERR_DTYPE"]
+    assert lib.qmm_mv(7, 4096, 16, 1, 0, fake, 0, n, n, fake, n) == st["QMM_ERR_NULL"]
     assert lib.qmm_tile_mxfp4(fake, fake, 32, 96, fake, fake, n) == st["QMM_ERR_SHAPE"]
     assert lib.qmm_tile_mxfp4(fake, n, 32, 64, fake, fake, n) == st["QMM_ERR_NULL"]
     assert lib.qmm_dequant(4, fake, fake, 48, 64, fake, n) == st["QMM_ERR_SHAPE"]

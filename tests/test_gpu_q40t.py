@@ -1,6 +1,7 @@
 """GPU parity of Q4_0 in the tiled GEMV layout (qmm_tile_q40, format q4_0t): the int8-activation decode matvecs
 g_mv_q4_0_k{K}[_t{TG}]_q8 and their swiglu / pair forms (S/gen_llm.py:1159-1197, :1288-1301; the Q4_0 int8 dot
-@g_q4_0_icodes, S/gen_llm.py:536-552) read from the tiled units the Q4_K kernel streams.
+@g_q4_0_icodes, S/gen_llm.py:536-552) read from the tiled units the Q4_K kernel streams, and the f32 / bf16-activation
+matvec g_mv_q4_0_k{K}[_t{TG}] (the reference's default Q4_0 decode; @g_q4_0_values) on the same units.
 
 Bars: the tiled bytes equal the oracle's construction byte for byte and dequantize to the GGUF values bit for bit;
 the matvec matches the float64 oracle on the Q8_1 activations and the exactly dequantized weights within rel-L2 1e-3
@@ -103,3 +104,44 @@ def test_linear_decode_reads_q40t(dev):
     xt, xv = _x(rng, 2, k, "f32", dev)
     got = host(ops.linear("q4_0t", xt, wt, n, k))
     assert_close_rel_l2(got, ref.gemv(ref.q8_1(xv), of.dequant_q4_0(w, n, k)), 1e-3, "linear q4_0t")
+
+
+@pytest.mark.parametrize("n,k,m,dtype", [
+    (4096, 4096, 1, "f32"),    # the Q4_0 GEMV workload (4096 x 4096, f32 x)
+    (16, 512, 1, "bf16"),      # one wave, one unit
+    (48, 1536, 3, "f32"),      # three waves
+    (64, 8192, 2, "bf16"),     # two units a wave
+    (32, 12288, 2, "f32"),     # three units a wave
+])
+def test_mv_f32_q40t_matches_oracle(dev, n, k, m, dtype):
+    """The f32-activation matvec on the tiled units against the float64 oracle (f32 x, exactly dequantized weights,
+    rel-L2 <= 1e-3, make_kernel_tests.py:246-281); a multi-token call equals one-token calls bit for bit; against
+    the GGUF-layout f32 kernel (the same products, another summation order) far below the bar; accumulate adds."""
+    import qmm.ops as ops
+    rng = np.random.default_rng(n + k + m + 17)
+    w = _w(rng, n, k)
+    wg = dev_u8(w, dev)
+    wt = ops.tile_q40(wg, n, k)
+    xt, xv = _x(rng, m, k, dtype, dev)
+    y = host(ops.mv("q4_0t", wt, xt, n, k))
+    assert_close_rel_l2(y, ref.gemv(xv, of.dequant_q4_0(w, n, k)), 1e-3, f"q4_0t mv n={n} k={k} m={m}")
+    for t in range(m):
+        assert_bits_equal(host(ops.mv("q4_0t", wt, xt[t:t + 1].contiguous(), n, k))[0], y[t], f"token {t}")
+    assert_close_rel_l2(y, host(ops.mv("q4_0", wg, xt, n, k)).astype(np.float64), 1e-5, "vs the GGUF-layout kernel")
+    y0 = rng.standard_normal((m, n)).astype(np.float32)
+    yt = dev_f32(y0, dev)
+    ops.mv("q4_0t", wt, xt, n, k, y=yt, accumulate=True)
+    assert_close_rel_l2(host(yt), y0 + y, 1e-6, "accumulate")
+
+
+def test_linear_f32_path_reads_q40t(dev):
+    """ops.linear on q4_0t weights with q8=False (the reference's ACT_Q8=0 / default Q4_0 arithmetic) takes the
+    f32-activation matvec."""
+    import qmm.ops as ops
+    rng = np.random.default_rng(96)
+    n, k = 256, 2048
+    w = _w(rng, n, k)
+    wt = ops.tile_q40(dev_u8(w, dev), n, k)
+    xt, xv = _x(rng, 2, k, "f32", dev)
+    got = host(ops.linear("q4_0t", xt, wt, n, k, q8=False))
+    assert_close_rel_l2(got, ref.gemv(xv, of.dequant_q4_0(w, n, k)), 1e-3, "linear q4_0t f32")
