@@ -83,7 +83,9 @@ int qmm_dequant(int fmt, const void *w, const void *ws, int64_t rows, int64_t k,
  *   y[t, r] = (accumulate ? y[t, r] : 0) + sum_k x[t, k] * W[r, k]   for t < tokens, r < n, fp32 accumulation.
  * x: [tokens, k] of x_dtype (QMM_F32 as the reference, or QMM_BF16); w: n rows of qmm_row_bytes(fmt, k) bytes;
  * ws: scale plane for QMM_MXFP4S else NULL; y: f32 [tokens, n]. Every token is computed with the same arithmetic
- * whatever `tokens` is, so a multi-token call equals one-token calls bit for bit. */
+ * whatever `tokens` is, so a multi-token call equals one-token calls bit for bit. fmt QMM_Q4_0T: the Q4_0 weights in
+ * the tiled layout of qmm_tile_q40 (n % 16 == 0, K = 512 U NW with U <= 3, NW <= 8), per block d (sum q x - 8 sum x)
+ * in f32 (the reference's f32 Q4_0 decode up to f32 rounding). */
 int qmm_mv(int fmt, int64_t k, int64_t n, int64_t tokens, int accumulate, const void *x, int x_dtype,
            const void *w, const void *ws, float *y, qmm_stream_t stream);
 
