@@ -663,6 +663,9 @@ def timed(step_fn, steps, warmup, no_graph=False, repeats=REPEATS):
     return float(np.median(times)), wall
 
 
+KERNEL_LAUNCHES = 200   # launches of the dominant kernel a timed region for roofline.avg_launch_us
+
+
 def kernel_time(fn, steps, warmup):
     """Average launch time (ms) of the dominant kernel: `steps` eager launches fn(warmup) .. back to back between two
     HIP events on the launching stream, after the warm-up launches and the ramp, queued behind a spin that outlasts
@@ -678,7 +681,9 @@ def measure(wl, args, cpu_budget):
     if getattr(wl, "kernel_is_step", False) and not args.graph:
         per_launch_s = per_step_s   # the step is one launch of the dominant kernel: the same measurement
     else:
-        per_launch_s = kernel_time(wl.kernel_step or wl.step, args.steps, args.warmup) / 1e3
+        # at least KERNEL_LAUNCHES launches a region, whatever --steps is: a short burst of a long kernel reads a few
+        # per cent slow (the first launches after the host-side setup), and the profiles trace 200 launches
+        per_launch_s = kernel_time(wl.kernel_step or wl.step, max(args.steps, KERNEL_LAUNCHES), args.warmup) / 1e3
     kb = wl.kernel_bytes() if hasattr(wl, "kernel_bytes") else wl.alg_bytes()
     kf = wl.kernel_flops() if hasattr(wl, "kernel_flops") else wl.alg_flops()
     if wl.bound == "hbm":
@@ -701,7 +706,7 @@ def measure(wl, args, cpu_budget):
         res["chain_frac_fp8_rate"] = round(res["tflops"] / MFMA_PEAK_TFLOPS["fp8"], 4)
     if hasattr(wl, "library_step"):
         wl.library_setup(torch_device())
-        lib_s = kernel_time(wl.library_step, args.steps, args.warmup) / 1e3
+        lib_s = kernel_time(wl.library_step, max(args.steps, KERNEL_LAUNCHES), args.warmup) / 1e3
         lib_tf = wl.alg_flops() / lib_s / 1e12
         res["library_f16_gemm"] = {"what": "torch.matmul of the same shape, f16 x f16 (hipBLASLt), no dequantization",
                                    "us": round(lib_s * 1e6, 3), "tflops": round(lib_tf, 3),
