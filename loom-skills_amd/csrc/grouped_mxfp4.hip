@@ -269,25 +269,32 @@ __global__ __launch_bounds__(256, WAVES) void mxfp4_grouped_kernel(MArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  // Rings DEPTH super-steps deep; kTiled also carries the scale dword of the super-step's chunk group (kSub divides
-  // four, so the kSub chunks of a super-step share one).
+  // Rings DEPTH super-steps deep. kTiled also streams the weight blocks' scale dwords, one per group of four chunks
+  // (kSub divides four): with four chunks a super-step, one a ring slot; with fewer (SPG = 4 / kSub super-steps a
+  // dword), each dword is loaded once, SPG super-steps ahead of its group, into one of two group slots, and the loop
+  // runs 2 SPG super-steps an iteration so that every slot index is a constant (one dword load per weight block and
+  // super-step was a sixth of the bytes the workgroup moves through its vector memory path, and measurably slower).
+  constexpr int SPG = LAYOUT == kTiled && kSub < 4 ? 4 / kSub : 0;
+  constexpr int U = SPG ? 2 * SPG : DEPTH;   // super-steps per loop iteration
+  static_assert(U % DEPTH == 0, "an iteration holds whole turns of the rings");
   v4u aring[DEPTH][kSub], bring[DEPTH][kSub][NJ];
-  u32 sring[DEPTH][NJ];
+  u32 sring[SPG ? 2 : DEPTH][NJ];
+  auto load_s = [&](int slot, int g) __attribute__((always_inline)) {
+    g = g < C4 ? g : C4 - 1;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) sring[slot][j] = *reinterpret_cast<const u32 *>(wcs[j] + (int64_t)g * 256);
+  };
   auto load_b = [&](int slot, int st) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int i = 0; i < kSub; ++i)
         bring[slot][i][j] = *reinterpret_cast<const v4u *>(wcn[j] + (int64_t)clampc(kSub * st + i) * CSTRIDE);
-    if constexpr (LAYOUT == kTiled) {
-      int g = (kSub * st) >> 2;
-      g = g < C4 ? g : C4 - 1;
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) sring[slot][j] = *reinterpret_cast<const u32 *>(wcs[j] + (int64_t)g * 256);
-    }
+    if constexpr (LAYOUT == kTiled && !SPG) load_s(slot, st);
   };
   // the weight stream: the first super-step (the others follow the activation staging, below)
   load_b(0, 0);
+  if constexpr (SPG) load_s(0, 0);
 
   int my_src = -1;
   if (tid < BM) {
@@ -335,11 +342,23 @@ __global__ __launch_bounds__(256, WAVES) void mxfp4_grouped_kernel(MArgs a) {
   // every weight load of the previous super-step waited on before the activations are staged).
   load_a(0, 0);
   if constexpr (DEPTH > 1) load_a(1, 1);
-  batched_copy<16>(reinterpret_cast<u16 *>(Asc), (int64_t)BM * (SK / 2), tid, [&](int64_t i) {
-    const int r = (int)(i / (SK / 2)), q = (int)(i % (SK / 2));
-    const int sr = src_row[r] >= 0 ? src_row[r] : 0;
-    return reinterpret_cast<const u16 *>(a.xs + (int64_t)sr * SK)[q];
-  });
+  {
+    // the rows' scales: four threads a row (BM x 4 = 256), each every fourth 2-byte piece of its row (K / 32 is
+    // even), eight loads in flight before their stores; no division per piece (a 64-bit one took about 130
+    // instructions a piece, some 2000 a thread in every workgroup's prologue)
+    static_assert(BM * 4 == 256, "four threads a scale row");
+    const int r = tid >> 2, q0 = tid & 3, n2 = SK / 2;
+    const u16 *sp = reinterpret_cast<const u16 *>(a.xs + (int64_t)(src_row[r] >= 0 ? src_row[r] : 0) * SK);
+    u16 *dp = reinterpret_cast<u16 *>(Asc + r * SK);
+    for (int b = q0; b < n2; b += 32) {
+      u16 v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = sp[b + 4 * q < n2 ? b + 4 * q : n2 - 1];
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (b + 4 * q < n2) dp[b + 4 * q] = v[q];
+    }
+  }
   if constexpr (LAYOUT == kSplit) {
     const int cols = N - n0 < BN ? N - n0 : BN;   // columns past N are never stored
 #pragma unroll
@@ -358,15 +377,20 @@ __global__ __launch_bounds__(256, WAVES) void mxfp4_grouped_kernel(MArgs a) {
 
   // The super-step count is rounded up to a multiple of DEPTH. A padding chunk (c >= C) runs with both E8M0 scales
   // 0: its products are at most 448 * 6 * 2^-254, far below the smallest f32 subnormal, so they add exactly zero.
-  // The loop body thus has no data-dependent branch; each super-step is instantiated with its ring slot as a
-  // constant (integral_constant), so the rings stay in registers.
+  // Each super-step is instantiated with its ring slots as constants (integral_constant), so the rings stay in
+  // registers; the super-steps past the last chunk that rounding the count up to U adds skip their MFMAs (a uniform
+  // branch) but keep their loads and barrier, so the waits are the same in every iteration.
+  const int S = (C + kSub - 1) / kSub;
+  const int SP = (S + U - 1) / U * U;
   auto step = [&](auto uc, int s0) __attribute__((always_inline)) {
     constexpr int u = decltype(uc)::value;
+    constexpr int ub = u % DEPTH;              // ring slot
     constexpr int nx = (u + 1) % DEPTH;
+    constexpr int us = SPG ? u / SPG : ub;     // scale slot
     const int st = s0 + u;
     const int buf = st & 1;
 #pragma unroll
-    for (int i = 0; i < kSub; ++i) {
+    for (int i = 0; i < kSub && st < S; ++i) {
       const int c = kSub * st + i;
       const bool live = c < C;
       const int sc_off = 2 * clampc(c) + h;   // the lane's E8M0 byte of this chunk in a scale row
@@ -380,9 +404,9 @@ __global__ __launch_bounds__(256, WAVES) void mxfp4_grouped_kernel(MArgs a) {
       int sb[NJ];
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        const v4u bv = bring[u][i][j];
+        const v4u bv = bring[ub][i][j];
         bf[j] = i32x8{(int)bv.x, (int)bv.y, (int)bv.z, (int)bv.w, 0, 0, 0, 0};
-        if constexpr (LAYOUT == kTiled) sb[j] = live ? (int)((sring[u][j] >> (8 * (c & 3))) & 255u) : 0;
+        if constexpr (LAYOUT == kTiled) sb[j] = live ? (int)((sring[us][j] >> (8 * (c & 3))) & 255u) : 0;
         else sb[j] = live ? Wsc[wrow[j] * SK + sc_off] : 0;
       }
       {
@@ -409,13 +433,12 @@ __global__ __launch_bounds__(256, WAVES) void mxfp4_grouped_kernel(MArgs a) {
     // in flight across it.
     stage(nx, buf ^ 1);
     load_a(nx, st + 1 + DEPTH);
-    load_b(u, st + DEPTH);
+    load_b(ub, st + DEPTH);
+    if constexpr (SPG && u % SPG == 0) load_s((us + 1) % 2, st / SPG + 1);   // the next group's dwords
     __syncthreads();
   };
-  const int S = (C + kSub - 1) / kSub;
-  const int SP = (S + DEPTH - 1) / DEPTH * DEPTH;
-  for (int s0 = 0; s0 < SP; s0 += DEPTH)
-    for_steps(step, s0, std::make_integer_sequence<int, DEPTH>{});
+  for (int s0 = 0; s0 < SP; s0 += U)
+    for_steps(step, s0, std::make_integer_sequence<int, U>{});
 
   if constexpr (KIND == kGU8) {
     // The activation quantized to MXFP8 as qmm_quant_mxfp8 quantizes it. Per 32-row half of the tile, the f32
