@@ -31,9 +31,10 @@
 // Tiling: a workgroup of four waves owns one 64-row expert tile; each wave computes its 64 rows x CB output column
 // blocks of 32 over all of K. gu: wave w owns output columns 32 CB w .. 32 CB (w + 1) - 1 of a 128 CB-column block,
 // its weight blocks being those columns of the gate and of the up matrix (2 CB x 2 MFMA blocks), so the activation
-// is applied in registers. dn: the same columns of the one matrix (CB x 2 MFMA blocks). CB = 2 (tiled planes, many
-// rows an expert) halves the activation bytes a weight byte meets; CB = 1 keeps more workgroups on the weight
-// stream when the experts hold few rows. Workgroup b runs on XCD b % 8;
+// is applied in registers. dn: the same columns of the one matrix (CB x 2 MFMA blocks). Wide tiles (tiled planes,
+// many rows an expert: gu CB = 2, dn CB = 4, four weight blocks a wave either way) halve or quarter the activation
+// bytes a weight byte meets; CB = 1 keeps more workgroups on the weight stream when the experts hold few rows.
+// Workgroup b runs on XCD b % 8;
 // the live tiles (those with an expert) are cut into eight contiguous ranges, one per XCD, and each XCD walks its
 // range tile-fastest: the workgroups resident together on an XCD are then the tiles of one or a few experts on the
 // same column blocks, so an expert's weights come from HBM once and its other tiles read them from that XCD's L2.
@@ -581,10 +582,11 @@ int launch(const MArgs &a0, hipStream_t s) {
   return launch_status();
 }
 
-// Column blocks a wave of the grouped GEMMs on tiled planes: two once the table holds, on average, at least
-// kWideRows rows an expert (the down GEMM; kWideRowsGU for the gate/up GEMM, whose two-block waves run two
-// workgroups a CU instead of three). max_tiles - E tiles hold the assignments: the bucket sizes max_tiles as
-// A / 64 + E. Below that the one-block kernels keep more workgroups in flight on the weight stream.
+// Column blocks a wave of the grouped GEMMs on tiled planes: four weight blocks a wave (gate/up two column blocks of
+// each matrix, down four of its one; two workgroups a CU instead of three) once the table holds, on average, at
+// least kWideRows rows an expert (the down GEMM; kWideRowsGU the gate/up GEMM). max_tiles - E tiles hold the
+// assignments: the bucket sizes max_tiles as A / 64 + E. Below that the one-block kernels keep more workgroups in
+// flight on the weight stream. (Down at gpt-oss-20b: four blocks 60 / 184 µs at T = 1024 / 4096, two 67 / 191.)
 constexpr int kWideRows = 64, kWideRowsGU = 256;
 inline bool wide_tiles(int64_t max_tiles, int E, int rows) { return (max_tiles - E) * BM >= (int64_t)rows * E; }
 
@@ -693,7 +695,7 @@ int qmm_grouped_mxfp4(int tiled, int mode, int fused, int act, int64_t max_tiles
   }
   a.nib_ebytes = nrow * n;
   a.sc_ebytes = srow * n;
-  if (wide) return launch<kDN, kTiled, kOutGrouped, 2>(a, s);
+  if (wide) return launch<kDN, kTiled, kOutGrouped, 4>(a, s);
   return tiled ? launch<kDN, kTiled>(a, s) : launch<kDN, kSplit>(a, s);
 }
 
