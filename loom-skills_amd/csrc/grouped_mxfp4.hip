@@ -586,8 +586,9 @@ int launch(const MArgs &a0, hipStream_t s) {
 // each matrix, down four of its one; two workgroups a CU instead of three) once the table holds, on average, at
 // least kWideRows rows an expert (the down GEMM; kWideRowsGU the gate/up GEMM). max_tiles - E tiles hold the
 // assignments: the bucket sizes max_tiles as A / 64 + E. Below that the one-block kernels keep more workgroups in
-// flight on the weight stream. (Down at gpt-oss-20b: four blocks 60 / 184 µs at T = 1024 / 4096, two 67 / 191.)
-constexpr int kWideRows = 64, kWideRowsGU = 256;
+// flight on the weight stream. (gpt-oss-20b at T = 1024, 128 rows an expert: gate/up 111 µs wide, 117 with one
+// block; down with four blocks 60 / 184 µs at T = 1024 / 4096, with two 67 / 191.)
+constexpr int kWideRows = 64, kWideRowsGU = 128;
 inline bool wide_tiles(int64_t max_tiles, int E, int rows) { return (max_tiles - E) * BM >= (int64_t)rows * E; }
 
 // MFMA-tiled planes from split planes (a byte permutation): one thread per 16-byte lane slot of a 1 KB tile, and
