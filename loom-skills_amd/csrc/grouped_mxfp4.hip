@@ -36,8 +36,9 @@
 // bytes a weight byte meets; CB = 1 keeps more workgroups on the weight stream when the experts hold few rows.
 // Workgroup b runs on XCD b % 8;
 // the live tiles (those with an expert) are cut into eight contiguous ranges, one per XCD, and each XCD walks its
-// range tile-fastest: the workgroups resident together on an XCD are then the tiles of one or a few experts on the
-// same column blocks, so an expert's weights come from HBM once and its other tiles read them from that XCD's L2.
+// range in groups of twelve tiles, tile-fastest: the workgroups resident together on an XCD are then the tiles of one
+// or two experts on a few column blocks, so an expert's weights come from HBM about once and its other tiles read
+// them from that XCD's L2, and a group's activation rows are read by all column blocks while still in L2.
 //
 // Steps. The E8M0 scales of the tile's 64 activation rows (and, for kSplit, of its 128 + 128 or 128 weight columns),
 // K / 32 bytes each, are staged in LDS once; per-step byte loads of split-plane scales through the vector memory
@@ -75,6 +76,7 @@ namespace {
 #endif
 
 constexpr int BM = 64, KC = 64;
+constexpr int kTileGroup = 12;   // tiles of a range walked together over the column blocks
 
 enum Kind { kGU = 1, kDN = 2, kGU8 = 3 };   // kGU8: gu with its output quantized to MXFP8
 enum Layout { kSplit = 0, kTiled = 1 };
@@ -183,7 +185,7 @@ __global__ __launch_bounds__(256, WAVES) void mxfp4_grouped_kernel(MArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
   // ---- which tile and column block: the live tiles [0, L) (L = 1 + the last tile with an expert) in eight
-  //      contiguous ranges, range x on XCD x, walked tile-fastest
+  //      contiguous ranges, range x on XCD x, walked in groups of kTileGroup tiles (below)
   int L = a.max_tiles;   // dense: every 64-row tile of x
   if constexpr (!DENSE) {
     if (tid == 0) live_end = 0;
@@ -201,9 +203,22 @@ __global__ __launch_bounds__(256, WAVES) void mxfp4_grouped_kernel(MArgs a) {
   const int t_begin = (int)(((int64_t)xcd * L) >> 3), t_end = (int)(((int64_t)(xcd + 1) * L) >> 3);
   const int cnt = t_end - t_begin;
   if (cnt <= 0 || xi >= cnt * a.n_blocks) return;
-  const int tile = t_begin + xi % cnt;
+  // the range in groups of kTileGroup tiles, each group walked tile-fastest over every column block before the next:
+  // a group's activation rows (12 x 64 rows) are then read by its column blocks while they are still in the XCD's
+  // L2, where one sweep of all the range's tiles per column block lets the weight stream evict them in between
+  // (gpt-oss-20b at T = 4096, HBM reads a launch: gate/up 878 -> 727 MB, down 454 -> 386 MB; times within 2 %)
+  int tile, cbk;
+  if (cnt > kTileGroup) {
+    const int per = kTileGroup * a.n_blocks, g = xi / per, r = xi - g * per, gt0 = g * kTileGroup;
+    const int gn = cnt - gt0 < kTileGroup ? cnt - gt0 : kTileGroup;
+    tile = t_begin + gt0 + r % gn;
+    cbk = r / gn;
+  } else {
+    tile = t_begin + xi % cnt;
+    cbk = xi / cnt;
+  }
   const int N = a.N, K = a.K, C = K / KC;
-  const int n0 = (xi / cnt) * BN, m0 = tile * BM;
+  const int n0 = cbk * BN, m0 = tile * BM;
   // the tile's expert and row map are loaded together; the weight stream starts as soon as the expert is known,
   // before the row map, the activation rows and their scales (every workgroup starts at once, so each dependent
   // round trip before the first weight load is time the HBM idles)
