@@ -503,7 +503,8 @@ int launch_u(const TArgs &a, hipStream_t s) {
   constexpr int TGMAX = MODE == kPlain ? TG1 : (TG1 > 1 ? TG1 / 2 : 1);
   constexpr int T8 = TGMAX >= 8 ? 8 : 1, T4 = TGMAX >= 4 ? 4 : 1, T2 = TGMAX >= 2 ? 2 : 1;
   const int64_t tokens = a.tokens;
-  if (tokens >= 5 && T8 == 8) return launch_tg<T8, U, STAGEQ, MODE>(a, s);
+  // the output stage takes one thread an output (16 rows x TG tokens): eight tokens need two waves (K >= 1024)
+  if (tokens >= 5 && T8 == 8 && a.nw >= 2) return launch_tg<T8, U, STAGEQ, MODE>(a, s);
   if (tokens >= 3 && T4 == 4) return launch_tg<T4, U, STAGEQ, MODE>(a, s);
   if (tokens >= 2 && T2 == 2) return launch_tg<T2, U, STAGEQ, MODE>(a, s);
   return launch_tg<1, U, STAGEQ, MODE>(a, s);

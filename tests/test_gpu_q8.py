@@ -176,6 +176,7 @@ def test_mv_q8_tiled_equals_gguf_layout_at_k4096(dev, m):
 
 @pytest.mark.parametrize("n,k,m,dtype", [
     (16, 512, 1, "bf16"),      # one wave, one slice
+    (32, 512, 8, "bf16"),      # one wave, eight tokens: more outputs a workgroup (16 x 8) than threads
     (48, 1536, 3, "f32"),      # three waves
     (32, 5120, 2, "bf16"),     # two slices a wave, five waves
     (64, 8192, 5, "bf16"),     # two slices a wave, eight waves
