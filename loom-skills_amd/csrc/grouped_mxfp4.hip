@@ -42,9 +42,9 @@
 //
 // Steps. The E8M0 scales of the tile's 64 activation rows (and, for kSplit, of its 128 + 128 or 128 weight columns),
 // K / 32 bytes each, are staged in LDS once; per-step byte loads of split-plane scales through the vector memory
-// path cost more than the weight stream (kTiled streams its scales as dwords instead). A super-step covers kSub
-// 64-value chunks: the tile's activation codes for it are staged in LDS (double-buffered, one barrier per
-// super-step) and the weights stream straight into registers one super-step ahead.
+// path cost more than the weight stream (kTiled streams its scales as one dword per four chunks instead). A
+// super-step covers kSub 64-value chunks: the tile's activation codes for it are staged in LDS (double-buffered, one
+// barrier per super-step) and the weights stream straight into registers DEPTH super-steps ahead.
 #include <type_traits>
 
 #include "bfly.hpp"
