@@ -205,6 +205,34 @@ def test_moe_prefill_large_batch_rows_match_small_batch(dev, fmt, E, KU, H, FE, 
     np.testing.assert_array_equal(b[lo:hi].view(np.uint32), s.view(np.uint32))
 
 
+def test_mxfp4_tile_groups_cover_every_row(dev):
+    """The tiled MXFP4 grouped GEMMs walk each XCD's tiles in groups of twelve over the column blocks once a range
+    holds more than twelve tiles. 4096 tokens, 8 experts, top-2 (136 tiles: 17 a range, a full group and a partial
+    one of 5): every row of the chain equals bit for bit the same token's row of a 256-token chain (2 tiles a range,
+    no grouping), over all sixteen slices, so every (tile, column block) of both GEMMs was computed once."""
+    import torch
+    from qmm import synth
+    ops = _ops()
+    rng = np.random.default_rng(4096 + 8)
+    E, KU, H, FE, T = 8, 2, 512, 320, 4096
+    ex = Experts(dev, "mxfp4", rng, E, H, FE, True)
+    wfmt, kw = ex.device(split=True, tiled=True)
+    xb = dev_bf16(synth.to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32)), dev)
+    logits = dev_f32(rng.standard_normal((T, E)).astype(np.float32), dev)
+    big, mid = ops.moe_prefill(wfmt, xb, logits, E, KU, H, FE, 3, False, fused=True, act="swiglu_oai", **kw)
+    torch.cuda.synchronize()
+    ti = host(mid["tile_info"])
+    assert (ti[:, 0] >= 0).sum() > 8 * 12, "the ranges must hold more than one group of tiles"
+    b = host(big)
+    assert np.all(np.isfinite(b))
+    for lo in range(0, T, 256):
+        small, _ = ops.moe_prefill(wfmt, xb[lo:lo + 256].contiguous(), logits[lo:lo + 256].contiguous(), E, KU, H,
+                                   FE, 3, False, fused=True, act="swiglu_oai", **kw)
+        np.testing.assert_array_equal(b[lo:lo + 256].view(np.uint32), host(small).view(np.uint32),
+                                      err_msg=f"tokens {lo}..{lo + 255}")
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("fmt,fused,act,tiled", [("q4_k", True, "swiglu_oai", False), ("q4_k", False, "silu", False),
                                                  ("mxfp4", False, "silu", False), ("mxfp4", True, "swiglu_oai", False),
                                                  ("mxfp4", False, "silu", True), ("mxfp4", True, "swiglu_oai", True)])
