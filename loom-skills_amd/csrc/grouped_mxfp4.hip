@@ -239,6 +239,9 @@ __global__ __launch_bounds__(256, WAVES) void mxfp4_grouped_kernel(MArgs a) {
   // ---- weights: this lane's two columns (gu: one column of the gate and of the up matrix) and K half
   const int h = lane >> 5, lc = lane & 31;
   const int col = n0 + WC * wave + lc;       // the lane's output column (dn: of its first block)
+  // a wave whose columns all lie past N (the last column block of a matrix whose N is not a multiple of the
+  // block) keeps its loads and barriers but issues no MFMA: its outputs are never stored
+  const bool wlive = n0 + WC * wave < N;
   const u8 *nbj[NJ], *sbj[NJ];   // the matrix of weight block j
   {
     const u8 *gn = a.wn + (int64_t)expert * a.nib_ebytes, *gs = a.wsc + (int64_t)expert * a.sc_ebytes;
@@ -406,7 +409,7 @@ __global__ __launch_bounds__(256, WAVES) void mxfp4_grouped_kernel(MArgs a) {
     const int st = s0 + u;
     const int buf = st & 1;
 #pragma unroll
-    for (int i = 0; i < kSub && st < S; ++i) {
+    for (int i = 0; i < kSub && st < S && wlive; ++i) {
       const int c = kSub * st + i;
       const bool live = c < C;
       const int sc_off = 2 * clampc(c) + h;   // the lane's E8M0 byte of this chunk in a scale row
