@@ -95,3 +95,10 @@ def test_checker_catches_a_shifted_call():
                      "NULL, wu, NULL, NULL, NULL, act_sorted, stream")
     assert len(old) == len(params)
     assert any(a in params and params.index(a) != i for i, a in enumerate(old))
+
+
+def test_every_entry_point_is_documented():
+    """Every entry point the header declares has at least one call in the document."""
+    doc = open(DOC).read()
+    missing = [name for name in prototypes() if not re.search(rf"\b{name}\(", doc)]
+    assert not missing, f"entry points without a call in INTEGRATION.md: {missing}"
