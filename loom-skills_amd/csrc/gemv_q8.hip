@@ -122,7 +122,7 @@ __device__ __forceinline__ void xq_load(const u8 *codes, const float *meta, int6
 struct Q4K8 {
   static constexpr bool kSplit = false;
   struct W { v4u h, q0, q1; };
-  static __device__ __forceinline__ int items(int64_t k) { return (int)(k / 256) * 4; }
+  static __host__ __device__ __forceinline__ int items(int64_t k) { return (int)(k / 256) * 4; }
   static __device__ __forceinline__ int64_t group(int item) { return (int64_t)(item >> 2) * 8 + 2 * (item & 3); }
   static __device__ __forceinline__ void load_w(const u8 *row, int item, bool live, W &w) {
     const u8 *b = row + (int64_t)(item >> 2) * 144;
@@ -155,7 +155,7 @@ struct Q4K8 {
 struct Q408 {
   static constexpr bool kSplit = false;
   struct W { u32 v[9]; };
-  static __device__ __forceinline__ int items(int64_t k) { return (int)(k / 64); }
+  static __host__ __device__ __forceinline__ int items(int64_t k) { return (int)(k / 64); }
   static __device__ __forceinline__ int64_t group(int item) { return 2 * (int64_t)item; }
   static __device__ __forceinline__ void load_w(const u8 *row, int item, bool live, W &w) {
     const u32 *p = reinterpret_cast<const u32 *>(row + (int64_t)item * 36);
@@ -188,7 +188,7 @@ struct Q408 {
 struct Q6K8 {
   static constexpr bool kSplit = false;
   using W = Q6W;
-  static __device__ __forceinline__ int items(int64_t k) { return (int)(k / 256) * 4; }
+  static __host__ __device__ __forceinline__ int items(int64_t k) { return (int)(k / 256) * 4; }
   static __device__ __forceinline__ int64_t group(int item) { return 2 * (int64_t)item; }
   static __device__ __forceinline__ void load_w(const u8 *row, int item, bool live, W &w) {
     q6k_load(row, item, live, w);
@@ -252,7 +252,7 @@ __device__ __forceinline__ int e2m1_block_dot(v4u nib, const u32 (&xq)[8]) {
 struct MX4S8 {
   static constexpr bool kSplit = true;
   struct W { v4u a, b; u32 e; };
-  static __device__ __forceinline__ int items(int64_t k) { return (int)(k / 64); }
+  static __host__ __device__ __forceinline__ int items(int64_t k) { return (int)(k / 64); }
   static __device__ __forceinline__ int64_t group(int item) { return 2 * (int64_t)item; }
   static __device__ __forceinline__ void load_w(const u8 *row, const u8 *srow, int item, bool live, W &w) {
     const v4u z{0u, 0u, 0u, 0u};
@@ -347,11 +347,16 @@ __global__ __launch_bounds__(256) void mv_q8_kernel(int64_t n, int64_t tokens, i
   }
 }
 
-// The decode expert matvecs on Q8_1 activations: one assignment a per workgroup column (blockIdx.x), RW = 4 output
-// rows per wave; e = clamp(ids[a], 0, E - 1) (S/gen_moe.py:592-596). gu: act[a] = act_fn(Wg[e] xq[a / KU], Wu[e]
-// xq[a / KU]) (+ the expert biases before the activation); dn: ys[a] = Wd[e] xq[a] (+ bias). xq is the planar Q8_1
-// buffer of x_rows rows (gu: the tokens; dn: the assignments).
-template <class P, bool GU>
+// The decode expert matvecs on Q8_1 activations: one assignment a per workgroup column (blockIdx.x); a wave owns
+// 64 / LPR output rows, LPR lanes a row, lane (row rr, sub) taking items sub, sub + LPR, ... of its row; e =
+// clamp(ids[a], 0, E - 1) (S/gen_moe.py:592-596). gu: act[a] = act_fn(Wg[e] xq[a / KU], Wu[e] xq[a / KU]) (+ the
+// expert biases before the activation); dn: ys[a] = Wd[e] xq[a] (+ bias). xq is the planar Q8_1 buffer of x_rows
+// rows (gu: the tokens; dn: the assignments). LPR is the item count rounded up to a power of two (16 to 64), so
+// rows with fewer than 64 items (Q4_K K = 768: 12) fill the wave instead of leaving most lanes idle. A row's LPR
+// lanes meet in the butterfly of wave_sum restricted to their group (xor LPR / 2 .. 1): with one item a lane up to
+// LPR items, the lanes a full-wave butterfly would add past the group hold zeros, so every row's sum is the same
+// for every LPR.
+template <class P, bool GU, int LPR>
 __global__ __launch_bounds__(256) void expert_mv_q8_kernel(int64_t n, int64_t assignments, int KU, int E, int64_t k,
                                                            const int32_t *__restrict__ ids, const u8 *__restrict__ codes,
                                                            const float *__restrict__ meta, const u8 *__restrict__ w,
@@ -360,11 +365,14 @@ __global__ __launch_bounds__(256) void expert_mv_q8_kernel(int64_t n, int64_t as
                                                            int64_t sb, int64_t sebytes, const float *__restrict__ bias,
                                                            const float *__restrict__ bias2, int act,
                                                            float *__restrict__ y) {
-  constexpr int RW = 4, NM = GU ? 2 : 1;
+  constexpr int RPW = 64 / LPR, NM = GU ? 2 : 1;   // rows a wave, matrices streamed
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane % LPR, rr = lane / LPR;
   const int64_t a = blockIdx.x;
-  const int64_t row0 = ((int64_t)blockIdx.y * kWaves + wave) * RW;
+  const int64_t row0 = ((int64_t)blockIdx.y * kWaves + wave) * RPW;
   if (row0 >= n || a >= assignments) return;
+  const int64_t row = row0 + rr;
+  const bool rlive = row < n;
   int e = ids[a];
   e = e < 0 ? 0 : (e >= E ? E - 1 : e);
   const int64_t xr = GU ? a / KU : a;
@@ -379,45 +387,34 @@ __global__ __launch_bounds__(256) void expert_mv_q8_kernel(int64_t n, int64_t as
     se[NM - 1] = ws2 + e * sebytes;
   }
   const int nitems = P::items(k);
-  float acc[NM][RW];
+  float acc[NM];
 #pragma unroll
-  for (int m = 0; m < NM; ++m)
-#pragma unroll
-    for (int r = 0; r < RW; ++r) acc[m][r] = 0.f;
-  for (int it0 = 0; it0 < nitems; it0 += 64) {
-    const int item = it0 + lane;
+  for (int m = 0; m < NM; ++m) acc[m] = 0.f;
+  for (int it0 = 0; it0 < nitems; it0 += LPR) {
+    const int item = it0 + sub;
     const bool live = item < nitems;
     XQ xs;
     xq_load(xc, xm, P::group(item), live, xs);
-    typename P::W wv[NM][RW];
+    typename P::W wv[NM];
 #pragma unroll
-    for (int m = 0; m < NM; ++m)
+    for (int m = 0; m < NM; ++m) load_row<P>(we[m] + row * rb, se[m] + row * sb, item, live && rlive, wv[m]);
 #pragma unroll
-      for (int r = 0; r < RW; ++r)
-        load_row<P>(we[m] + (row0 + r) * rb, se[m] + (row0 + r) * sb, item, live && (row0 + r) < n, wv[m][r]);
-#pragma unroll
-    for (int m = 0; m < NM; ++m)
-#pragma unroll
-      for (int r = 0; r < RW; ++r) acc[m][r] += P::dot(wv[m][r], xs, item);
+    for (int m = 0; m < NM; ++m) acc[m] += P::dot(wv[m], xs, item);
   }
 #pragma unroll
   for (int m = 0; m < NM; ++m)
 #pragma unroll
-    for (int r = 0; r < RW; ++r) acc[m][r] = wave_sum(acc[m][r]);
-#pragma unroll
-  for (int r = 0; r < RW; ++r) {
-    const int64_t row = row0 + r;
-    if (lane == r && row < n) {
-      float g = acc[0][r];
-      if (bias) g += bias[e * n + row];
-      float v = g;
-      if constexpr (GU) {
-        float u = acc[NM - 1][r];
-        if (bias2) u += bias2[e * n + row];
-        v = act_fn(act, g, u);
-      }
-      y[a * n + row] = v;
+    for (int off = LPR / 2; off >= 1; off >>= 1) acc[m] += __shfl_xor(acc[m], off, kWave);
+  if (sub == 0 && rlive) {
+    float g = acc[0];
+    if (bias) g += bias[e * n + row];
+    float v = g;
+    if constexpr (GU) {
+      float u = acc[NM - 1];
+      if (bias2) u += bias2[e * n + row];
+      v = act_fn(act, g, u);
     }
+    y[a * n + row] = v;
   }
 }
 
@@ -717,16 +714,25 @@ int launch_expert_q8(bool gu, int64_t k, int64_t n, int E, int KU, int64_t assig
   const int64_t x_rows = gu ? assignments / KU : assignments;
   const u8 *codes = static_cast<const u8 *>(x);
   const float *meta = reinterpret_cast<const float *>(codes + x_rows * k);
-  const dim3 grid((unsigned)assignments, (unsigned)((n + kWaves * 4 - 1) / (kWaves * 4)));
+  const int items = P::items(k);
+  const int lpr = items <= 16 ? 16 : (items <= 32 ? 32 : 64);   // lanes a row: the item count's power of two
+  const int64_t rows_wg = kWaves * (64 / lpr);
+  const dim3 grid((unsigned)assignments, (unsigned)((n + rows_wg - 1) / rows_wg));
   if (grid.y > 65535u) return QMM_ERR_SHAPE;
-  if (gu)
-    expert_mv_q8_kernel<P, true><<<grid, 256, 0, s>>>(n, assignments, KU, E, k, ids, codes, meta,
-                                                      static_cast<const u8 *>(w), static_cast<const u8 *>(w2), rb,
-                                                      ebytes, s1, s2, k / 32, sebytes, bias, bias2, act, y);
-  else
-    expert_mv_q8_kernel<P, false><<<grid, 256, 0, s>>>(n, assignments, KU, E, k, ids, codes, meta,
-                                                       static_cast<const u8 *>(w), nullptr, rb, ebytes, s1, nullptr,
-                                                       k / 32, sebytes, bias, nullptr, act, y);
+  auto go = [&](auto lc) {
+    constexpr int L = decltype(lc)::value;
+    if (gu)
+      expert_mv_q8_kernel<P, true, L><<<grid, 256, 0, s>>>(n, assignments, KU, E, k, ids, codes, meta,
+                                                           static_cast<const u8 *>(w), static_cast<const u8 *>(w2),
+                                                           rb, ebytes, s1, s2, k / 32, sebytes, bias, bias2, act, y);
+    else
+      expert_mv_q8_kernel<P, false, L><<<grid, 256, 0, s>>>(n, assignments, KU, E, k, ids, codes, meta,
+                                                            static_cast<const u8 *>(w), nullptr, rb, ebytes, s1,
+                                                            nullptr, k / 32, sebytes, bias, nullptr, act, y);
+  };
+  if (lpr == 16) go(std::integral_constant<int, 16>{});
+  else if (lpr == 32) go(std::integral_constant<int, 32>{});
+  else go(std::integral_constant<int, 64>{});
   return launch_status();
 }
 }  // namespace
