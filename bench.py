@@ -316,11 +316,12 @@ class MoeWorkload:
             self.metric = METRIC
         else:
             self.T = m or 64
-            self.metric = "Q4_K MoE prefill TFLOP/s (Qwen3-30B-A3B, 128 experts, top-8)"
+            chain = "decode" if self.T < 64 else "prefill"
+            self.metric = f"Q4_K MoE {chain} TFLOP/s (Qwen3-30B-A3B, 128 experts, top-8)"
         self.decode = self.T < 64
         # the Q4_K prefill chain streams the tiled layout through the narrow grouped kernel
         kern = ("mxt_expert_kernel" if self.decode else "mxfp4_grouped_kernel_gu8") if index == 3 else \
-            ("expert_mv" if self.decode else "q4k_narrow_kernel_gu")
+            ("expert_mv_q8_kernel" if self.decode else "q4k_narrow_kernel_gu")
         model = "mxfp4_moe_gpt_oss_20b" if index == 3 else "q4_k_moe_qwen3_30b_a3b"
         self.traffic_name = f"{kern}.{model}_t{self.T}"
 
@@ -375,9 +376,16 @@ class MoeWorkload:
         self.rotated_bytes = self.copies * touched
         # inputs of the dominant kernel (the gate/up GEMM or expert matvec) for its own timing; the decode chain
         # routes inside its gate/up matvecs where ops.moe_decode does
-        self.route_gu = self.decode and self.E <= ops.ROUTE_GU_MAX_E and self.T * self.KU <= ops.ROUTE_GU_MAX_A
+        # int8 decode (the reference's MOE_Q8 default for Q4_K / Q6_K): the Q8_1 gate/up matvecs on the quantized x
+        kw0 = self.kw
+        self.q8 = self.decode and ops._moe_q8("auto", self.fmt, kw0.get("fmt_down") or ops.gate_format(self.fmt),
+                                              kw0.get("expert_bias"))
+        self.route_gu = (self.decode and not self.q8 and self.E <= ops.ROUTE_GU_MAX_E
+                         and self.T * self.KU <= ops.ROUTE_GU_MAX_A)
         if self.decode:
             self.gu_y = torch.empty_like(mid["act"])
+            if self.q8:
+                self.gu_xq = ops.quant_q8(self.x)
         elif self.fmt == "mxfp4t":   # prefill
             self.gu_x, self.gu_xs = ops.quant_mxfp8(self.x)
             self.gu_y = (torch.empty_like(mid["act8"]), torch.empty_like(mid["act_scales"]))
@@ -398,6 +406,10 @@ class MoeWorkload:
             self.ops.moe_topk_expert_mv(self.fmt, self.logits, self.KU, self.d["gating"], self.d["norm"], self.x,
                                         kw["w_gate"], self.FE, self.H, self.E, w2=kw.get("w_up"), ws=kw.get("ws_gate"),
                                         fused=kw["fused"], act=kw["act"], y=self.gu_y)
+        elif self.decode and self.q8:   # the int8 gate/up expert matvecs of the decode chain
+            self.ops.moe_expert_mv_q8(self.fmt, "gu", self.mid["ids"], self.gu_xq, kw["w_gate"], self.FE, self.H,
+                                      self.E, self.KU, w2=kw.get("w_up"), fused=kw["fused"], act=kw["act"],
+                                      y=self.gu_y)
         elif self.decode:   # the gate/up expert matvecs of the decode chain
             self.ops.moe_expert_mv(self.fmt, "gu", self.mid["ids"], self.x, kw["w_gate"], self.FE, self.H, self.E,
                                    self.KU, w2=kw.get("w_up"), ws=kw.get("ws_gate"), fused=kw["fused"],
