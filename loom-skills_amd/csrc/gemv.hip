@@ -79,8 +79,12 @@ __global__ __launch_bounds__(256) void mv_kernel(int64_t n, int64_t tokens, int6
     }
 }
 
-// One assignment per workgroup row (blockIdx.x), RW output rows per wave.
-template <class P, int RW, bool GU, int NS = 0>
+// One assignment per workgroup row (blockIdx.x), RW output rows per wave. LPR lanes a row (the row's item count
+// rounded up to a power of two, at least 64 / RW): lane (group rg, sub) takes items sub, sub + LPR, ... of rows
+// rg, rg + 64 / LPR, ... of the wave's RW, and a row's LPR lanes meet in the butterfly of wave_sum restricted to
+// their group. With one item a lane up to LPR items, the lanes a full-wave butterfly would add past the group hold
+// zeros, so the row sums are the same for every LPR.
+template <class P, int RW, bool GU, int NS = 0, int LPR = 64>
 __global__ __launch_bounds__(256) void expert_mv_kernel(int64_t n, int64_t assignments, int KU, int E, int64_t k,
                                                         const int32_t *__restrict__ ids, const u8 *__restrict__ x,
                                                         int64_t x_row_bytes, const u8 *__restrict__ w,
@@ -122,36 +126,42 @@ __global__ __launch_bounds__(256) void expert_mv_kernel(int64_t n, int64_t assig
   const u8 *we = w + e * ebytes, *wse = ws + e * esbytes;
   const u8 *w2e = w2 + e * ebytes, *ws2e = ws2 + e * esbytes;
   const int nitems = P::items(k);
-  float ag[RW], au[RW];
+  constexpr int G = 64 / LPR, RL = RW / G;   // row groups a wave, rows a lane
+  static_assert(RL >= 1 && RW % G == 0, "LPR below 64 / RW");
+  const int sub = lane % LPR, rg = lane / LPR;
+  float ag[RL], au[RL];
 #pragma unroll
-  for (int r = 0; r < RW; ++r) ag[r] = au[r] = 0.f;
-  for (int it0 = 0; it0 < nitems; it0 += 64) {
-    const int item = it0 + lane;
+  for (int r = 0; r < RL; ++r) ag[r] = au[r] = 0.f;
+  for (int it0 = 0; it0 < nitems; it0 += LPR) {
+    const int item = it0 + sub;
     const bool live = item < nitems;
     typename P::X xs;
     P::load_x(xr, item, live, xs);
-    typename P::W wg[RW], wu[GU ? RW : 1];
+    typename P::W wg[RL], wu[GU ? RL : 1];
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
-      const bool rl = live && (row0 + r) < n;
-      P::load_w(we + (row0 + r) * rb, wse + (row0 + r) * srb, item, rl, wg[r]);
-      if constexpr (GU) P::load_w(w2e + (row0 + r) * rb, ws2e + (row0 + r) * srb, item, rl, wu[r]);
+    for (int r = 0; r < RL; ++r) {
+      const int64_t row = row0 + rg + G * r;
+      const bool rl = live && row < n;
+      P::load_w(we + row * rb, wse + row * srb, item, rl, wg[r]);
+      if constexpr (GU) P::load_w(w2e + row * rb, ws2e + row * srb, item, rl, wu[r]);
     }
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
+    for (int r = 0; r < RL; ++r) {
       ag[r] += P::dot(wg[r], xs, item);
       if constexpr (GU) au[r] += P::dot(wu[r], xs, item);
     }
   }
 #pragma unroll
-  for (int r = 0; r < RW; ++r) {
-    ag[r] = wave_sum(ag[r]);
-    if constexpr (GU) au[r] = wave_sum(au[r]);
-  }
+  for (int r = 0; r < RL; ++r)
 #pragma unroll
-  for (int r = 0; r < RW; ++r) {
-    const int64_t row = row0 + r;
-    if (lane == r && row < n) {
+    for (int off = LPR / 2; off >= 1; off >>= 1) {
+      ag[r] += __shfl_xor(ag[r], off, kWave);
+      if constexpr (GU) au[r] += __shfl_xor(au[r], off, kWave);
+    }
+#pragma unroll
+  for (int r = 0; r < RL; ++r) {
+    const int64_t row = row0 + rg + G * r;
+    if (sub == 0 && row < n) {
       float g = ag[r];
       if (bias) g += bias[e * n + row];
       float v = g;
@@ -234,7 +244,7 @@ __global__ __launch_bounds__(256) void expert_mv_mixed_kernel(int64_t n, int64_t
 // routed slot j of t, all over the same RW rows. Each wave does expert_mv_kernel's per-lane arithmetic and
 // butterfly for its assignment t*KU + j (so its row sums are the separate call's ys, bit for bit); one lane a
 // row then folds the KU sums with the combine's fma chain in slot order.
-template <class P, int RW>
+template <class P, int RW, int LPR = 64>
 __global__ __launch_bounds__(512) void expert_mv_combine_kernel(int64_t n, int KU, int E, int64_t k,
                                                                 const int32_t *__restrict__ ids,
                                                                 const float *__restrict__ wts,
@@ -263,30 +273,38 @@ __global__ __launch_bounds__(512) void expert_mv_combine_kernel(int64_t n, int K
   const u8 *xr = x + a * x_row_bytes;
   const u8 *we = w + e * ebytes, *wse = ws + e * esbytes;
   const int nitems = P::items(k);
-  float ag[RW];
+  constexpr int G = 64 / LPR, RL = RW / G;   // row groups a wave, rows a lane (expert_mv_kernel's lane map)
+  static_assert(RL >= 1 && RW % G == 0, "LPR below 64 / RW");
+  const int sub = lane % LPR, rg = lane / LPR;
+  float ag[RL];
 #pragma unroll
-  for (int r = 0; r < RW; ++r) ag[r] = 0.f;
-  for (int it0 = 0; it0 < nitems; it0 += 64) {
-    const int item = it0 + lane;
+  for (int r = 0; r < RL; ++r) ag[r] = 0.f;
+  for (int it0 = 0; it0 < nitems; it0 += LPR) {
+    const int item = it0 + sub;
     const bool live = item < nitems;
     typename P::X xs;
     P::load_x(xr, item, live, xs);
-    typename P::W wg[RW];
+    typename P::W wg[RL];
 #pragma unroll
-    for (int r = 0; r < RW; ++r)
-      P::load_w(we + (row0 + r) * rb, wse + (row0 + r) * srb, item, live && (row0 + r) < n, wg[r]);
+    for (int r = 0; r < RL; ++r) {
+      const int64_t row = row0 + rg + G * r;
+      P::load_w(we + row * rb, wse + row * srb, item, live && row < n, wg[r]);
+    }
 #pragma unroll
-    for (int r = 0; r < RW; ++r) ag[r] += P::dot(wg[r], xs, item);
+    for (int r = 0; r < RL; ++r) ag[r] += P::dot(wg[r], xs, item);
   }
 #pragma unroll
-  for (int r = 0; r < RW; ++r) ag[r] = wave_sum(ag[r]);
+  for (int r = 0; r < RL; ++r)
 #pragma unroll
-  for (int r = 0; r < RW; ++r) {
-    const int64_t row = row0 + r;
-    if (lane == r) {
+    for (int off = LPR / 2; off >= 1; off >>= 1) ag[r] += __shfl_xor(ag[r], off, kWave);
+#pragma unroll
+  for (int r = 0; r < RL; ++r) {
+    const int rl = rg + G * r;   // the row's place in the workgroup's RW
+    const int64_t row = row0 + rl;
+    if (sub == 0) {
       float g = ag[r];
       if (bias && row < n) g += bias[e * n + row];
-      part[j][r] = g;
+      part[j][rl] = g;
     }
   }
   if (lane == 0) slot_w[j] = wj;
@@ -386,6 +404,22 @@ extern "C" int qmm_mv(int fmt, int64_t k, int64_t n, int64_t tokens, int accumul
 }
 
 namespace {
+// Lanes a row for the expert matvecs: the item count rounded up to a power of two, at least 64 / RW
+inline int expert_lpr(int items, int rw) {
+  int l = items <= 16 ? 16 : (items <= 32 ? 32 : 64);
+  return l < 64 / rw ? 64 / rw : l;
+}
+// the kernel instantiation for lpr; MAXL: the largest lpr the caller's rows can have (no kernel is built past it)
+template <int RW, int MAXL = 64, class F>
+int with_lpr(int lpr, F &&f) {
+  if constexpr (64 / RW <= 16) { if (lpr == 16) return f(std::integral_constant<int, 16>{}); }
+  if constexpr (MAXL == 32) return f(std::integral_constant<int, 32>{});
+  else {
+    if constexpr (64 / RW <= 32) { if (lpr == 32) return f(std::integral_constant<int, 32>{}); }
+    return f(std::integral_constant<int, 64>{});
+  }
+}
+
 template <class P, bool GU>
 int launch_expert(int64_t k, int64_t n, int E, int KU, int64_t assignments, const int32_t *ids, const void *x,
                   int64_t x_row_bytes, const void *w, const void *ws, const void *w2, const void *ws2, int64_t rb,
@@ -393,11 +427,13 @@ int launch_expert(int64_t k, int64_t n, int E, int KU, int64_t assignments, cons
                   float *y, hipStream_t s, int accumulate = 0) {
   constexpr int RW = expert_rw<GU>();
   const dim3 grid((unsigned)assignments, (unsigned)((n + kWavesPerBlock * RW - 1) / (kWavesPerBlock * RW)));
-  expert_mv_kernel<P, RW, GU><<<grid, 256, 0, s>>>(
-      n, assignments, KU, E, k, ids, static_cast<const u8 *>(x), x_row_bytes, static_cast<const u8 *>(w),
-      static_cast<const u8 *>(ws), static_cast<const u8 *>(w2), static_cast<const u8 *>(ws2), rb, srb, ebytes, esbytes,
-      bias, bias2, act, accumulate, y);
-  return launch_status();
+  return with_lpr<RW>(expert_lpr(P::items(k), RW), [&](auto lc) {
+    expert_mv_kernel<P, RW, GU, 0, decltype(lc)::value><<<grid, 256, 0, s>>>(
+        n, assignments, KU, E, k, ids, static_cast<const u8 *>(x), x_row_bytes, static_cast<const u8 *>(w),
+        static_cast<const u8 *>(ws), static_cast<const u8 *>(w2), static_cast<const u8 *>(ws2), rb, srb, ebytes,
+        esbytes, bias, bias2, act, accumulate, y);
+    return launch_status();
+  });
 }
 
 // The gate/up expert matvecs routing their own tokens (NS = ceil(E / 64) key slots a lane).
@@ -408,11 +444,13 @@ int launch_expert_route(int64_t k, int64_t n, int E, int KU, int64_t assignments
                         const float *bias2, int act, float *y, hipStream_t s) {
   constexpr int RW = expert_rw<true>();
   const dim3 grid((unsigned)assignments, (unsigned)((n + kWavesPerBlock * RW - 1) / (kWavesPerBlock * RW)));
-  expert_mv_kernel<P, RW, true, NS><<<grid, 256, 0, s>>>(
-      n, assignments, KU, E, k, nullptr, static_cast<const u8 *>(x), x_row_bytes, static_cast<const u8 *>(w),
-      static_cast<const u8 *>(ws), static_cast<const u8 *>(w2), static_cast<const u8 *>(ws2), rb, srb, ebytes, esbytes,
-      bias, bias2, act, 0, y, r);
-  return launch_status();
+  return with_lpr<RW>(expert_lpr(P::items(k), RW), [&](auto lc) {
+    expert_mv_kernel<P, RW, true, NS, decltype(lc)::value><<<grid, 256, 0, s>>>(
+        n, assignments, KU, E, k, nullptr, static_cast<const u8 *>(x), x_row_bytes, static_cast<const u8 *>(w),
+        static_cast<const u8 *>(ws), static_cast<const u8 *>(w2), static_cast<const u8 *>(ws2), rb, srb, ebytes,
+        esbytes, bias, bias2, act, 0, y, r);
+    return launch_status();
+  });
 }
 
 template <template <bool> class P>
@@ -508,13 +546,17 @@ int launch_expert_combine_rw(bool bf, int64_t k, int64_t n, int E, int KU, int64
   const dim3 grid((unsigned)((n + RW - 1) / RW), (unsigned)tokens);
   const int64_t xb = k * (bf ? 2 : 4);
   const u8 *xp = static_cast<const u8 *>(x), *wp = static_cast<const u8 *>(w), *wsp = static_cast<const u8 *>(ws);
-  if (bf)
-    expert_mv_combine_kernel<P<true>, RW><<<grid, 64 * KU, 0, s>>>(n, KU, E, k, ids, wts, xp, xb, wp, wsp, rb, srb,
-                                                                   rb * n, srb * n, bias, accumulate, sg, y);
-  else
-    expert_mv_combine_kernel<P<false>, RW><<<grid, 64 * KU, 0, s>>>(n, KU, E, k, ids, wts, xp, xb, wp, wsp, rb, srb,
-                                                                    rb * n, srb * n, bias, accumulate, sg, y);
-  return launch_status();
+  // eight rows a wave only for rows of at most 32 items (launch_expert_combine)
+  return with_lpr<RW, RW == 8 ? 32 : 64>(expert_lpr(P<false>::items(k), RW), [&](auto lc) {
+    constexpr int L = decltype(lc)::value;
+    if (bf)
+      expert_mv_combine_kernel<P<true>, RW, L><<<grid, 64 * KU, 0, s>>>(n, KU, E, k, ids, wts, xp, xb, wp, wsp, rb,
+                                                                       srb, rb * n, srb * n, bias, accumulate, sg, y);
+    else
+      expert_mv_combine_kernel<P<false>, RW, L><<<grid, 64 * KU, 0, s>>>(n, KU, E, k, ids, wts, xp, xb, wp, wsp, rb,
+                                                                        srb, rb * n, srb * n, bias, accumulate, sg, y);
+    return launch_status();
+  });
 }
 
 // Rows a wave: four, or eight where one pass over a row keeps at most half the wave's lanes busy (Q4_K FE = 768:
