@@ -279,7 +279,9 @@ enum Mode { kPlain = 0, kSwiglu = 1, kPair = 2 };
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
 // RW rows per wave (4 for one matrix, 2 when two stream), TG tokens per workgroup sharing every weight load
-template <class P, int TG, int MODE, int RW>
+// LPR lanes a row (the item count's power of two, at least 64 / RW), the butterfly restricted to the row's lanes:
+// the row sums equal the full-wave butterfly's over one row a pass (the expert matvecs' lane map)
+template <class P, int TG, int MODE, int RW, int LPR = 64>
 __global__ __launch_bounds__(256) void mv_q8_kernel(int64_t n, int64_t tokens, int64_t k, int accumulate,
                                                     const u8 *__restrict__ codes, const float *__restrict__ meta,
                                                     const u8 *__restrict__ w, const u8 *__restrict__ w2, int64_t rb,
@@ -292,15 +294,18 @@ __global__ __launch_bounds__(256) void mv_q8_kernel(int64_t n, int64_t tokens, i
   if (row0 >= n) return;
   const int nitems = P::items(k);
   const int64_t G = k / 32;
-  float acc[NM][RW][TG];
+  constexpr int GR = 64 / LPR, RL = RW / GR;   // row groups a wave, rows a lane
+  static_assert(RL >= 1 && RW % GR == 0, "LPR below 64 / RW");
+  const int sub = lane % LPR, rg = lane / LPR;
+  float acc[NM][RL][TG];
 #pragma unroll
   for (int m = 0; m < NM; ++m)
 #pragma unroll
-    for (int r = 0; r < RW; ++r)
+    for (int r = 0; r < RL; ++r)
 #pragma unroll
       for (int t = 0; t < TG; ++t) acc[m][r][t] = 0.f;
-  for (int it0 = 0; it0 < nitems; it0 += 64) {
-    const int item = it0 + lane;
+  for (int it0 = 0; it0 < nitems; it0 += LPR) {
+    const int item = it0 + sub;
     const bool live = item < nitems;
     XQ xs[TG];
 #pragma unroll
@@ -308,32 +313,35 @@ __global__ __launch_bounds__(256) void mv_q8_kernel(int64_t n, int64_t tokens, i
       const int64_t tok = t0 + t;
       xq_load(codes + tok * k, meta + 2 * tok * G, P::group(item), live && tok < tokens, xs[t]);
     }
-    typename P::W wv[NM][RW];
+    typename P::W wv[NM][RL];
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
-      for (int r = 0; r < RW; ++r)
-        load_row<P>((m ? w2 : w) + (row0 + r) * rb, (m ? ws2 : ws) + (row0 + r) * sb, item, live && (row0 + r) < n,
-                    wv[m][r]);
+      for (int r = 0; r < RL; ++r) {
+        const int64_t row = row0 + rg + GR * r;
+        load_row<P>((m ? w2 : w) + row * rb, (m ? ws2 : ws) + row * sb, item, live && row < n, wv[m][r]);
+      }
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
-      for (int r = 0; r < RW; ++r)
+      for (int r = 0; r < RL; ++r)
 #pragma unroll
         for (int t = 0; t < TG; ++t) acc[m][r][t] += P::dot(wv[m][r], xs[t], item);
   }
 #pragma unroll
   for (int m = 0; m < NM; ++m)
 #pragma unroll
-    for (int r = 0; r < RW; ++r)
+    for (int r = 0; r < RL; ++r)
 #pragma unroll
-      for (int t = 0; t < TG; ++t) acc[m][r][t] = wave_sum(acc[m][r][t]);
-  if (lane == 0) {
+      for (int t = 0; t < TG; ++t)
 #pragma unroll
-    for (int r = 0; r < RW; ++r)
+        for (int off = LPR / 2; off >= 1; off >>= 1) acc[m][r][t] += __shfl_xor(acc[m][r][t], off, kWave);
+  if (sub == 0) {
+#pragma unroll
+    for (int r = 0; r < RL; ++r)
 #pragma unroll
       for (int t = 0; t < TG; ++t) {
-        const int64_t row = row0 + r, tok = t0 + t;
+        const int64_t row = row0 + rg + GR * r, tok = t0 + t;
         if (row < n && tok < tokens) {
           float *py = y + tok * n + row;
           const float v = MODE == kSwiglu ? silu_mul(acc[0][r][t], acc[NM - 1][r][t]) : acc[0][r][t];
@@ -628,10 +636,18 @@ int launch_generic(int64_t k, int64_t n, int64_t tokens, int accumulate, const v
   const float *meta = reinterpret_cast<const float *>(codes + tokens * k);
   const dim3 grid((unsigned)((tokens + TG - 1) / TG), (unsigned)((n + kWaves * RW - 1) / (kWaves * RW)));
   if (grid.x > 2147483647u || grid.y > 65535u) return QMM_ERR_SHAPE;
-  mv_q8_kernel<P, TG, MODE, RW><<<grid, 256, 0, s>>>(n, tokens, k, accumulate, codes, meta, static_cast<const u8 *>(w),
-                                                    static_cast<const u8 *>(w2), rb, static_cast<const u8 *>(ws),
-                                                    static_cast<const u8 *>(ws2), k / 32, y, y2);
-  return launch_status();
+  const int items = P::items(k);
+  int lpr = items <= 16 ? 16 : (items <= 32 ? 32 : 64);   // lanes a row, at least 64 / RW
+  lpr = lpr < 64 / RW ? 64 / RW : lpr;
+  auto go = [&](auto lc) {
+    mv_q8_kernel<P, TG, MODE, RW, decltype(lc)::value><<<grid, 256, 0, s>>>(
+        n, tokens, k, accumulate, codes, meta, static_cast<const u8 *>(w), static_cast<const u8 *>(w2), rb,
+        static_cast<const u8 *>(ws), static_cast<const u8 *>(ws2), k / 32, y, y2);
+    return launch_status();
+  };
+  if constexpr (RW >= 4) { if (lpr == 16) return go(std::integral_constant<int, 16>{}); }
+  if (lpr == 32) return go(std::integral_constant<int, 32>{});
+  return go(std::integral_constant<int, 64>{});
 }
 
 template <int MODE>
